@@ -1,0 +1,136 @@
+/* C-ABI of the MI355X-native fused EGNN/MPNN message-passing layer.
+ *
+ * Plain C, plain pointers and sizes, no torch types.  All device pointers are
+ * HIP device memory owned by the caller; `stream` is a hipStream_t passed as
+ * void*.  Every call is asynchronous on `stream` except egnn_schedule_build,
+ * which synchronises once to report CSR validation errors.
+ *
+ * Reference interfaces replaced (SatxaFortuny/PyMolecular):
+ *   egnn_fwd            <- egnn_forward_kernel_node_parallel[grid](...)
+ *                          models/EGNN/forward_kernel.py:14-43 (launch grid
+ *                          (num_nodes,), forward_kernel.py:47-49)
+ *   egnn_bwd            <- egnn_backward_kernel_node_parallel[grid](...)
+ *                          models/EGNN/backward_kernel.py:14-50, launched by
+ *                          launch_triton, test_mem.py:7-35
+ *   egnn_schedule_build <- no reference counterpart: the reference runs one
+ *                          program per CSR row (forward_kernel.py:47,
+ *                          test_mem.py:22); this builds the degree-aware edge
+ *                          tiling, the split-row list and the source-sorted
+ *                          (CSC) permutation once per graph.
+ *
+ * Semantics (pytorch_baseline.py:18-48 with the optional biases of
+ * egnn_clean.py:22-37): CSR row i is the destination, col[e] the source j,
+ *   delta = x_i - x_j, r2 = |delta|^2
+ *   m  = SiLU(SiLU(h_i W_n1 + h_j W_n2 + r2 w_d + e W_e + b1) W_hl + b2)
+ *   phi = SiLU(m W1_mov + bx1) . w2_mov
+ *   out_msg[i] = sum_j m_ij ;  out_mov[i] = sum_j delta_ij phi_ij  (/ max(deg_i,1) if mean_agg)
+ * Weights are row-major (in, out) as in layer.py:24-33: w1_msg is the packed
+ * (2F + g + FE, H) matrix [W_n1 | W_n2 | w_d | W_e] (g = 1 EGNN, 0 MPNN: no w_d
+ * row, no phi_x, no coordinate output).  Outputs are overwritten (never
+ * accumulated into) and weight gradients go to separate buffers.
+ */
+#ifndef PYMOLECULAR_AMD_EGNN_H
+#define PYMOLECULAR_AMD_EGNN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define EGNN_OK 0
+#define EGNN_ERR_NULL 1        /* a required pointer is NULL */
+#define EGNN_ERR_DIMS 2        /* unsupported or inconsistent dimensions */
+#define EGNN_ERR_STRIDE 3      /* a row stride is too small or not a multiple of the vector width */
+#define EGNN_ERR_ALIGN 4       /* a pointer is not 16-byte aligned */
+#define EGNN_ERR_WORKSPACE 5   /* workspace or schedule buffer too small */
+#define EGNN_ERR_CSR 6         /* rowptr not monotone / not [0..E], or a col index out of [0, N) */
+#define EGNN_ERR_HIP 7         /* a HIP runtime call or kernel launch failed */
+
+/* activation / weight dtype of h, edge_feat, weights, out_msg and grads
+ * (coordinates, out_mov and grad_coord are always fp32) */
+#define EGNN_F32 0
+#define EGNN_BF16 1
+
+typedef struct EgnnDims {
+  int64_t N;           /* nodes */
+  int64_t E;           /* CSR edges */
+  int32_t F;           /* node feature width (F_NODE); multiple of 16, <= 512 */
+  int32_t FE;          /* edge feature width (F_EDGE); multiple of 8, 0..480 */
+  int32_t H;           /* phi_e hidden (HIDDEN_FEATURES): 64, 128 or 256 */
+  int32_t O;           /* message width (OUT_FEATURES): equal to H, or 32 when H = 64 */
+  int32_t M;           /* phi_x hidden (HID_FEAT_MOV_MLP): equal to O */
+  int32_t equivariant; /* 1 = EGNN (r2 input, phi_x, coordinate output), 0 = MPNN */
+  int32_t mean_agg;    /* 1: out_mov divided by max(in-degree, 1) (egnn_clean.py:11,78) */
+  int32_t dtype;       /* EGNN_F32 or EGNN_BF16 */
+} EgnnDims;
+
+/* Row strides in elements; the inner dimension is always contiguous. */
+typedef struct EgnnStrides {
+  int64_t h;           /* h and grad_h                                  */
+  int64_t coord;       /* coord and grad_coord (>= 3)                   */
+  int64_t edge;        /* edge_feat                                     */
+  int64_t msg;         /* out_msg and grad_out_msg                      */
+  int64_t mov;         /* out_mov and grad_out_mov (>= 3)               */
+} EgnnStrides;
+
+/* Version of this ABI (bumped on any signature change). */
+int32_t egnn_abi_version(void);
+
+/* Human-readable text for a status code (static storage). */
+const char* egnn_status_string(int32_t status);
+
+/* Schedule buffer bytes (device memory) for a graph of N nodes and E edges. */
+size_t egnn_schedule_bytes(int64_t N, int64_t E);
+/* Temporary device bytes needed while building the schedule. */
+size_t egnn_schedule_tmp_bytes(int64_t N, int64_t E);
+
+/* Validate the CSR (rowptr[0]=0, non-decreasing, rowptr[N]=E, 0<=col<N) and
+ * build the schedule into `sched` (egnn_schedule_bytes bytes): the per-edge
+ * row ids, the list of rows that cross a 32-edge tile or are empty, and the
+ * stable source-sorted permutation of the edges.  Bit-exact and deterministic.
+ * Synchronises `stream` once to read the validation flag. */
+int32_t egnn_schedule_build(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E,
+                            void* sched, size_t sched_bytes, void* tmp, size_t tmp_bytes,
+                            void* stream);
+
+/* Workspace bytes for egnn_fwd / egnn_bwd with these dimensions. */
+size_t egnn_fwd_workspace_bytes(const EgnnDims* dims);
+size_t egnn_bwd_workspace_bytes(const EgnnDims* dims);
+
+/* Fused forward.  b1/b2/bx1 may be NULL (no bias); edge_ids may be NULL
+ * (identity, datasets_loaders.py:11); edge_feat may be NULL when FE = 0.
+ * For MPNN (equivariant = 0) coord, w1_mov, w2_mov, bx1 and out_mov are
+ * ignored and may be NULL.  Writes out_msg (N, O) and out_mov (N, 3). */
+int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides,
+                 const void* h, const float* coord, const void* edge_feat,
+                 const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
+                 const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov,
+                 const void* b1, const void* b2, const void* bx1,
+                 void* out_msg, float* out_mov,
+                 const void* sched, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Fused backward by recomputation.  Takes the forward inputs plus the
+ * incoming gradients grad_out_msg (N, O) and grad_out_mov (N, 3), and writes
+ * grad_h (N, F), grad_coord (N, 3), grad_w1_msg (packed, like w1_msg),
+ * grad_w2_msg (H, O), grad_w1_mov (O, M), grad_w2_mov (M), and grad_b1/b2/bx1
+ * when non-NULL.  No edge-feature gradient (the reference computes none).
+ * Deterministic: fixed-order reductions only, no floating-point atomics. */
+int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides,
+                 const void* h, const float* coord, const void* edge_feat,
+                 const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
+                 const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov,
+                 const void* b1, const void* b2, const void* bx1,
+                 const void* grad_out_msg, const float* grad_out_mov,
+                 void* grad_h, float* grad_coord,
+                 void* grad_w1_msg, void* grad_w2_msg, void* grad_w1_mov, void* grad_w2_mov,
+                 void* grad_b1, void* grad_b2, void* grad_bx1,
+                 const void* sched, void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PYMOLECULAR_AMD_EGNN_H */

@@ -1,0 +1,87 @@
+"""ctypes binding of the C-ABI in ``include/egnn.h`` (``libpymolecular_egnn.so``).
+
+The library is built in-tree by ``pymolecular_amd._build`` (``__graft_entry__.build``).
+There is no fallback: if the library is missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int32, c_int64, c_size_t, c_void_p, c_char_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().with_name("libpymolecular_egnn.so")
+
+EGNN_OK = 0
+EGNN_F32 = 0
+EGNN_BF16 = 1
+
+# every symbol include/egnn.h declares
+EXPORTED = (
+    "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
+    "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_fwd", "egnn_bwd",
+)
+
+
+class EgnnDims(ctypes.Structure):
+    _fields_ = [("N", c_int64), ("E", c_int64), ("F", c_int32), ("FE", c_int32), ("H", c_int32),
+                ("O", c_int32), ("M", c_int32), ("equivariant", c_int32), ("mean_agg", c_int32),
+                ("dtype", c_int32)]
+
+
+class EgnnStrides(ctypes.Structure):
+    _fields_ = [("h", c_int64), ("coord", c_int64), ("edge", c_int64), ("msg", c_int64), ("mov", c_int64)]
+
+
+_lib = None
+
+
+class EgnnError(RuntimeError):
+    """A C-ABI call returned a non-zero status."""
+
+    def __init__(self, fn: str, status: int):
+        self.status = status
+        super().__init__(f"{fn} failed with status {status}: {status_string(status)}")
+
+
+def lib() -> ctypes.CDLL:
+    """Load the HIP library once; raise if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m pymolecular_amd._build` "
+                           "(or __graft_entry__.build()); there is no CPU fallback")
+    L = ctypes.CDLL(str(LIB_PATH))
+    P = c_void_p
+    L.egnn_abi_version.restype = c_int32
+    L.egnn_abi_version.argtypes = []
+    L.egnn_status_string.restype = c_char_p
+    L.egnn_status_string.argtypes = [c_int32]
+    L.egnn_schedule_bytes.restype = c_size_t
+    L.egnn_schedule_bytes.argtypes = [c_int64, c_int64]
+    L.egnn_schedule_tmp_bytes.restype = c_size_t
+    L.egnn_schedule_tmp_bytes.argtypes = [c_int64, c_int64]
+    L.egnn_schedule_build.restype = c_int32
+    L.egnn_schedule_build.argtypes = [P, P, c_int64, c_int64, P, c_size_t, P, c_size_t, P]
+    L.egnn_fwd_workspace_bytes.restype = c_size_t
+    L.egnn_fwd_workspace_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
+    L.egnn_bwd_workspace_bytes.restype = c_size_t
+    L.egnn_bwd_workspace_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
+    L.egnn_fwd.restype = c_int32
+    L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 17 + [c_size_t, P]
+    L.egnn_bwd.restype = c_int32
+    L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 26 + [c_size_t, P]
+    _lib = L
+    return L
+
+
+def status_string(status: int) -> str:
+    try:
+        return lib().egnn_status_string(int(status)).decode()
+    except Exception:  # pragma: no cover - only when the library itself is unusable
+        return "unknown"
+
+
+def check(fn: str, status: int) -> None:
+    if status != EGNN_OK:
+        raise EgnnError(fn, status)

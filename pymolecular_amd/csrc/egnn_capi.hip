@@ -1,0 +1,247 @@
+// C-ABI entry points of the fused EGNN/MPNN layer (declared in include/egnn.h).
+// Validates arguments, lays out the caller's workspace and enqueues the
+// kernels on the caller's stream.  No allocation, no host synchronisation
+// (except the one documented in egnn_schedule_build).
+#include "egnn_device.h"
+#include "egnn_internal.h"
+
+using namespace egnn;
+
+namespace {
+
+constexpr int32_t kAbiVersion = 1;
+
+bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
+
+int32_t hip_status(int e) { return e == (int)hipSuccess ? EGNN_OK : EGNN_ERR_HIP; }
+
+// Per-node projection  P | Q = h [W_n1 | W_n2] + [b1 | 0], stored in the
+// activation dtype with each 32-feature group in chain order.
+int32_t project_nodes(const LayerShape& s, const void* h, int64_t sh, const void* w1, const void* b1, void* PQ,
+                      hipStream_t st) {
+  GemmArgs g{};
+  g.M = s.N; g.N = 2 * s.H; g.K = s.F;
+  g.A = h; g.sam = sh; g.sak = 1; g.a_bf16 = s.bf16; g.a_ones_row = -1;
+  g.B = w1; g.sbk = s.H; g.sbn = 1; g.b_bf16 = s.bf16;
+  g.b_kjump_at = INT64_MAX; g.b_kjump = 0;
+  g.b_njump_at = s.H; g.b_njump = (int64_t)s.F * s.H - s.H;   // columns H..2H read W_n2 = rows F..2F-1
+  g.bias = b1; g.bias_bf16 = s.bf16; g.bias_len = b1 ? s.H : 0;
+  g.C = PQ; g.scm = 2 * s.H; g.scn = 1; g.c_bf16 = s.bf16;
+  g.perm_half = s.H;
+  return hip_status(launch_gemm(g, s.bf16, st));
+}
+
+int32_t check_strides(const LayerShape& s, const EgnnStrides* st, bool bwd) {
+  if (!st) return EGNN_ERR_NULL;
+  const int vec = s.bf16 ? 8 : 4;  // elements per 16 bytes
+  if (st->h < s.F) return EGNN_ERR_STRIDE;
+  if (st->msg < s.O || st->msg % 4 != 0) return EGNN_ERR_STRIDE;
+  if (s.FE > 0 && (st->edge < s.FE || st->edge % vec != 0)) return EGNN_ERR_STRIDE;
+  if (s.eq && st->coord < 3) return EGNN_ERR_STRIDE;
+  if (s.eq && st->mov < 3) return EGNN_ERR_STRIDE;
+  (void)bwd;
+  return EGNN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t egnn_abi_version(void) { return kAbiVersion; }
+
+const char* egnn_status_string(int32_t status) {
+  switch (status) {
+    case EGNN_OK: return "ok";
+    case EGNN_ERR_NULL: return "a required pointer is NULL";
+    case EGNN_ERR_DIMS: return "unsupported or inconsistent dimensions";
+    case EGNN_ERR_STRIDE: return "a row stride is too small or not a multiple of the vector width";
+    case EGNN_ERR_ALIGN: return "a pointer is not 16-byte aligned";
+    case EGNN_ERR_WORKSPACE: return "workspace or schedule buffer too small";
+    case EGNN_ERR_CSR: return "invalid CSR: rowptr not monotone from 0 to E, or col index outside [0, N)";
+    case EGNN_ERR_HIP: return "HIP runtime call or kernel launch failed";
+    default: return "unknown status";
+  }
+}
+
+size_t egnn_schedule_bytes(int64_t N, int64_t E) {
+  SchedView v;
+  return sched_layout(N, E, nullptr, &v);
+}
+
+size_t egnn_schedule_tmp_bytes(int64_t N, int64_t E) { return schedule_tmp_bytes(N, E); }
+
+int32_t egnn_schedule_build(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E, void* sched,
+                            size_t sched_bytes, void* tmp, size_t tmp_bytes, void* stream) {
+  if (!rowptr || !sched || !tmp || (E > 0 && !col)) return EGNN_ERR_NULL;
+  if (N < 1 || E < 0 || N > (int64_t)INT32_MAX - 1 || E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
+  SchedView v;
+  if (sched_layout(N, E, sched, &v) > sched_bytes) return EGNN_ERR_WORKSPACE;
+  return launch_schedule(rowptr, col, N, E, v, tmp, tmp_bytes, (hipStream_t)stream);
+}
+
+size_t egnn_fwd_workspace_bytes(const EgnnDims* dims) {
+  LayerShape s;
+  if (make_shape(dims, &s) != EGNN_OK) return 0;
+  FwdWs w;
+  return fwd_ws_layout(s, nullptr, &w);
+}
+
+size_t egnn_bwd_workspace_bytes(const EgnnDims* dims) {
+  LayerShape s;
+  if (make_shape(dims, &s) != EGNN_OK) return 0;
+  BwdWs w;
+  return bwd_ws_layout(s, nullptr, &w);
+}
+
+int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h, const float* coord,
+                 const void* edge_feat, const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
+                 const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov, const void* b1,
+                 const void* b2, const void* bx1, void* out_msg, float* out_mov, const void* sched, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  LayerShape s;
+  int32_t rc = make_shape(dims, &s);
+  if (rc != EGNN_OK) return rc;
+  if ((rc = check_strides(s, strides, false)) != EGNN_OK) return rc;
+  if (!h || !rowptr || !w1_msg || !w2_msg || !out_msg || !sched || !workspace) return EGNN_ERR_NULL;
+  if (s.E > 0 && !col) return EGNN_ERR_NULL;
+  if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
+  if (s.eq && (!coord || !w1_mov || !w2_mov || !out_mov)) return EGNN_ERR_NULL;
+  if (!aligned16(edge_feat) || !aligned16(out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
+  FwdWs w;
+  if (fwd_ws_layout(s, workspace, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
+  SchedView v;
+  sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
+  hipStream_t st = (hipStream_t)stream;
+
+  if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, st))) != EGNN_OK) return rc;
+  if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+  FwdArgs a{};
+  a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, kTileEdges);
+  a.FE = s.FE; a.NUC = s.NUC; a.mean = s.mean;
+  a.PQ = w.PQ;
+  a.coord = coord; a.sc = strides->coord;
+  a.ef = edge_feat; a.se = strides->edge;
+  a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
+  a.fr = w.fr;
+  a.out_msg = out_msg; a.smsg = strides->msg;
+  a.out_mov = out_mov; a.smov = strides->mov;
+  a.carry = w.carry;
+  a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
+  return hip_status(launch_fwd(s, a, st));
+}
+
+int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h, const float* coord,
+                 const void* edge_feat, const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
+                 const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov, const void* b1,
+                 const void* b2, const void* bx1, const void* grad_out_msg, const float* grad_out_mov, void* grad_h,
+                 float* grad_coord, void* grad_w1_msg, void* grad_w2_msg, void* grad_w1_mov, void* grad_w2_mov,
+                 void* grad_b1, void* grad_b2, void* grad_bx1, const void* sched, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  LayerShape s;
+  int32_t rc = make_shape(dims, &s);
+  if (rc != EGNN_OK) return rc;
+  if ((rc = check_strides(s, strides, true)) != EGNN_OK) return rc;
+  if (!h || !rowptr || !w1_msg || !w2_msg || !grad_out_msg || !grad_h || !grad_w1_msg || !grad_w2_msg || !sched ||
+      !workspace)
+    return EGNN_ERR_NULL;
+  if (s.E > 0 && !col) return EGNN_ERR_NULL;
+  if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
+  if (s.eq && (!coord || !w1_mov || !w2_mov || !grad_out_mov || !grad_coord || !grad_w1_mov || !grad_w2_mov))
+    return EGNN_ERR_NULL;
+  if (!aligned16(edge_feat) || !aligned16(grad_out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
+  BwdWs w;
+  if (bwd_ws_layout(s, workspace, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
+  SchedView v;
+  sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
+  hipStream_t st = (hipStream_t)stream;
+
+  if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, st))) != EGNN_OK) return rc;
+  if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+
+  BwdArgs a{};
+  a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, bwd_tile_edges(s));
+  a.FE = s.FE; a.NUC = s.NUC; a.mean = s.mean;
+  a.PQ = w.PQ;
+  a.coord = coord; a.sc = strides->coord;
+  a.ef = edge_feat; a.se = strides->edge;
+  a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
+  a.fr = w.fr;
+  a.gmsg = grad_out_msg; a.sgm = strides->msg;
+  a.gmov = grad_out_mov; a.sgx = strides->mov;
+  a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
+  if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
+
+  // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
+  float* gcoord = s.eq ? grad_coord : nullptr;
+  if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
+                                          strides->coord, st))) != EGNN_OK)
+    return rc;
+
+  // dh = dP W_n1^T + dQ W_n2^T
+  {
+    GemmArgs g{};
+    g.M = s.N; g.N = s.F; g.K = 2 * s.H;
+    g.A = w.dPQ; g.sam = 2 * s.H; g.sak = 1; g.a_bf16 = 0; g.a_ones_row = -1;
+    g.B = w1_msg; g.sbk = 1; g.sbn = s.H; g.b_bf16 = s.bf16;
+    g.b_kjump_at = s.H; g.b_kjump = (int64_t)s.F * s.H - s.H;
+    g.b_njump_at = INT64_MAX;
+    g.C = grad_h; g.scm = strides->h; g.scn = 1; g.c_bf16 = s.bf16;
+    if ((rc = hip_status(launch_gemm(g, s.bf16, st))) != EGNN_OK) return rc;
+  }
+
+  // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
+  auto splitk = [&](GemmArgs g, float* dst) -> int32_t {
+    g.ksplit = splitk_len(std::max<int64_t>(g.K, 1));
+    g.partial = w.part;
+    int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
+    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    int32_t r = hip_status(launch_gemm(g, s.bf16, st));
+    if (r != EGNN_OK) return r;
+    return hip_status(launch_sum_rows(w.part, nsplit, g.M * g.N, dst, st));
+  };
+  {
+    GemmArgs g{};
+    g.M = s.H + 1; g.N = s.O; g.K = s.E;
+    g.A = w.Dm1; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = s.H;
+    g.B = w.Dga2; g.sbk = s.O; g.sbn = 1; g.b_bf16 = s.bf16;
+    if ((rc = splitk(g, w.dWhl)) != EGNN_OK) return rc;
+  }
+  if (s.eq) {
+    GemmArgs g{};
+    g.M = s.O + 1; g.N = s.M; g.K = s.E;
+    g.A = w.Dm; g.sam = 1; g.sak = s.O; g.a_bf16 = s.bf16; g.a_ones_row = s.O;
+    g.B = w.Dgq; g.sbk = s.M; g.sbn = 1; g.b_bf16 = s.bf16;
+    if ((rc = splitk(g, w.dW1m)) != EGNN_OK) return rc;
+    GemmArgs p{};
+    p.M = s.M; p.N = 1; p.K = s.E;
+    p.A = w.Dp; p.sam = 1; p.sak = s.M; p.a_bf16 = s.bf16; p.a_ones_row = -1;
+    p.B = w.Gx + 3; p.sbk = 4; p.sbn = 0; p.b_bf16 = 0;
+    if ((rc = splitk(p, w.dw2m)) != EGNN_OK) return rc;
+    GemmArgs d{};
+    d.M = s.H; d.N = 1; d.K = s.E;
+    d.A = w.Gh; d.sam = 1; d.sak = s.H; d.a_bf16 = s.bf16; d.a_ones_row = -1;
+    d.B = w.R2; d.sbk = 1; d.sbn = 0; d.b_bf16 = 0;
+    if ((rc = splitk(d, w.dwd)) != EGNN_OK) return rc;
+  }
+  if (s.FE > 0) {
+    GemmArgs g{};
+    g.M = s.H; g.N = s.FE; g.K = s.E;
+    g.A = w.Gh; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = -1;
+    g.B = edge_feat; g.sbk = strides->edge; g.sbn = 1; g.b_bf16 = s.bf16; g.b_kidx = edge_ids;
+    if ((rc = splitk(g, w.dWe)) != EGNN_OK) return rc;
+  }
+  {
+    GemmArgs g{};
+    g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
+    g.A = h; g.sam = 1; g.sak = strides->h; g.a_bf16 = s.bf16; g.a_ones_row = s.F;
+    g.B = w.dPQ; g.sbk = 2 * s.H; g.sbn = 1; g.b_bf16 = 0;
+    if ((rc = splitk(g, w.dWn)) != EGNN_OK) return rc;
+  }
+  FinalizeArgs f{};
+  f.dWhl = w.dWhl; f.dW1m = w.dW1m; f.dw2m = w.dw2m; f.dWe = w.dWe; f.dwd = w.dwd; f.dWn = w.dWn;
+  f.gw1 = grad_w1_msg; f.gw2 = grad_w2_msg; f.gw1m = grad_w1_mov; f.gw2m = grad_w2_mov;
+  f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1;
+  return hip_status(launch_finalize(s, f, st));
+}
+
+}  // extern "C"

@@ -1,0 +1,285 @@
+// Fused forward of the EGNN/MPNN message-passing layer (gfx950).
+//
+// Follows forward_kernel.py:89-153 (gather, geometry, phi_e, phi_x, per-row
+// sums, no atomics) with a different work decomposition:
+//  * the edge stream is cut into 32-edge wave tiles (not one program per row);
+//    rows that cross a tile are finished by a fixed-order fix-up, so skewed
+//    degrees do not serialise a wave and the result is deterministic;
+//  * h_i W_n1 + b1 and h_j W_n2 come from per-node projections (P, Q) computed
+//    once per node by a GEMM, so the first phi_e layer costs two gathers and
+//    an add per edge plus one small MFMA for [r2, e] W_u;
+//  * edges sit on the MFMA N axis (lanes) and features on M/K, so the output
+//    C-blocks of each product feed the next product directly (kappa_chain);
+//  * per-row sums run out of a wave-private LDS tile, one pass per 64 columns.
+#include "egnn_device.h"
+#include "egnn_internal.h"
+
+namespace egnn {
+
+template <typename T, bool EQ>
+__device__ __forceinline__ typename ChunkOf<T>::type edge_input_chunk(const T* ef, int64_t se, int eid, int FE, int uc,
+                                                                    int g, float r2) {
+  typedef typename ChunkOf<T>::type C;
+  const int slot0 = 32 * uc + 8 * g;
+  if (slot0 + 8 <= FE) return load_chunk(ef + (int64_t)eid * se + slot0);
+  C z = zero_chunk<T>();
+  if (EQ && slot0 == FE) {
+    if constexpr (sizeof(T) == 2) {
+      bf16 hi = (bf16)r2;
+      bf16 lo = (bf16)(r2 - (float)hi);
+      z[0] = hi;
+      z[1] = lo;
+    } else {
+      z.lo[0] = r2;
+    }
+  }
+  return z;
+}
+
+template <typename T, int H, int O, int M, int NB, bool EQ>
+__global__ __launch_bounds__(256) void fwd_edge_kernel(FwdArgs a) {
+  typedef typename ChunkOf<T>::type C;
+  constexpr int TE = kTileEdges, NSUB = TE / (16 * NB), KH = H / 32, KO = O / 32, KM = M / 32;
+  constexpr int SEGW = O + (EQ ? 4 : 0), SEGP = SEGW + 4;
+  extern __shared__ float smem[];
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  float* seg = smem + wave * (TE * SEGP + TE);
+  int* segrow = (int*)(seg + TE * SEGP);
+
+  const T* PQ = (const T*)a.PQ;
+  const T* ef = (const T*)a.ef;
+  const T* FhlT = (const T*)a.fr.hlT;
+  const T* FmovT = (const T*)a.fr.movT;
+  const T* Fu = (const T*)a.fr.u;
+  const int NUC = a.NUC;
+  const int64_t E = a.E;
+  const int64_t nwt = (int64_t)gridDim.x * 4;
+
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < a.ntiles; t += nwt) {
+    const int64_t base = t * TE;
+#pragma unroll 1
+    for (int sub = 0; sub < NSUB; ++sub) {
+      int ri[NB], rj[NB], eid[NB];
+      bool valid[NB];
+      float dx[NB], dy[NB], dz[NB], r2[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int64_t e = base + sub * 16 * NB + nb * 16 + c;
+        valid[nb] = e < E;
+        const int64_t ec = valid[nb] ? e : E - 1;
+        ri[nb] = clampi(a.erow[ec], (int)a.N);
+        rj[nb] = clampi(a.col[ec], (int)a.N);
+        eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
+        dx[nb] = dy[nb] = dz[nb] = r2[nb] = 0.f;
+        if constexpr (EQ) {
+          const float* xi = a.coord + (int64_t)ri[nb] * a.sc;
+          const float* xj = a.coord + (int64_t)rj[nb] * a.sc;
+          dx[nb] = xi[0] - xj[0];
+          dy[nb] = xi[1] - xj[1];
+          dz[nb] = xi[2] - xj[2];
+          r2[nb] = dx[nb] * dx[nb] + dy[nb] * dy[nb] + dz[nb] * dz[nb];
+        }
+      }
+      // ---- stage 1: pre1 = P_i + Q_j + W_u [e, r2] ; m1 = SiLU(pre1) ----
+      C m1c[KH][NB];
+#pragma unroll
+      for (int kc = 0; kc < KH; ++kc) {
+        f32x4 lo[NB], hi[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) lo[nb] = hi[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+        for (int uc = 0; uc < NUC; ++uc) {
+          const C ua0 = load_chunk(Fu + ((int64_t)(2 * kc) * NUC + uc) * kFragElems + l * 8);
+          const C ua1 = load_chunk(Fu + ((int64_t)(2 * kc + 1) * NUC + uc) * kFragElems + l * 8);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const C u = edge_input_chunk<T, EQ>(ef, a.se, eid[nb], a.FE, uc, g, r2[nb]);
+            mma(lo[nb], ua0, u);
+            mma(hi[nb], ua1, u);
+          }
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 plo, phi_, qlo, qhi;
+          unpack_chunk(load_chunk(PQ + (int64_t)ri[nb] * 2 * H + 32 * kc + 8 * g), plo, phi_);
+          unpack_chunk(load_chunk(PQ + (int64_t)rj[nb] * 2 * H + H + 32 * kc + 8 * g), qlo, qhi);
+          f32x4 x0, x1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            x0[i] = silu_t<T>(lo[nb][i] + plo[i] + qlo[i]);
+            x1[i] = silu_t<T>(hi[nb][i] + phi_[i] + qhi[i]);
+          }
+          m1c[kc][nb] = pack_chunk<T>(x0, x1);
+        }
+      }
+      // ---- stage 2: pre2 = W_hl^T m1 + b2 ; m = SiLU(pre2) -----------------
+      C mc[KO][NB];
+#pragma unroll
+      for (int kp = 0; kp < KO; ++kp) {
+        f32x4 acc0[NB], acc1[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < KH; ++kc) {
+          const C a0 = load_chunk(FhlT + ((int64_t)(2 * kp) * KH + kc) * kFragElems + l * 8);
+          const C a1 = load_chunk(FhlT + ((int64_t)(2 * kp + 1) * KH + kc) * kFragElems + l * 8);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            mma(acc0[nb], a0, m1c[kc][nb]);
+            mma(acc1[nb], a1, m1c[kc][nb]);
+          }
+        }
+        const f32x4 b0 = load4_f32(a.fr.b2f + 32 * kp + 4 * g);
+        const f32x4 b1 = load4_f32(a.fr.b2f + 32 * kp + 16 + 4 * g);
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          f32x4 x0, x1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            x0[i] = silu_t<T>(acc0[nb][i] + b0[i]);
+            x1[i] = silu_t<T>(acc1[nb][i] + b1[i]);
+          }
+          float* srow = seg + (sub * 16 * NB + nb * 16 + c) * SEGP;
+          *reinterpret_cast<f32x4*>(srow + 32 * kp + 4 * g) = x0;
+          *reinterpret_cast<f32x4*>(srow + 32 * kp + 16 + 4 * g) = x1;
+          mc[kp][nb] = pack_chunk<T>(x0, x1);
+        }
+      }
+      // ---- stage 3: phi = SiLU(W1mov^T m + bx1) . w2mov ; delta * phi -------
+      if constexpr (EQ) {
+        float phi[NB];
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) phi[nb] = 0.f;
+#pragma unroll
+        for (int mp = 0; mp < KM; ++mp) {
+          f32x4 acc0[NB], acc1[NB];
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kc = 0; kc < KO; ++kc) {
+            const C a0 = load_chunk(FmovT + ((int64_t)(2 * mp) * KO + kc) * kFragElems + l * 8);
+            const C a1 = load_chunk(FmovT + ((int64_t)(2 * mp + 1) * KO + kc) * kFragElems + l * 8);
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              mma(acc0[nb], a0, mc[kc][nb]);
+              mma(acc1[nb], a1, mc[kc][nb]);
+            }
+          }
+          const f32x4 q0 = load4_f32(a.fr.bx1f + 32 * mp + 4 * g), q1 = load4_f32(a.fr.bx1f + 32 * mp + 16 + 4 * g);
+          const f32x4 w0 = load4_f32(a.fr.w2mf + 32 * mp + 4 * g), w1 = load4_f32(a.fr.w2mf + 32 * mp + 16 + 4 * g);
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              phi[nb] += silu_t<T>(acc0[nb][i] + q0[i]) * w0[i] + silu_t<T>(acc1[nb][i] + q1[i]) * w1[i];
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          phi[nb] += shfl_xor(phi[nb], 16);
+          phi[nb] += shfl_xor(phi[nb], 32);
+          if (g == 0) {
+            float* srow = seg + (sub * 16 * NB + nb * 16 + c) * SEGP;
+            *reinterpret_cast<f32x4*>(srow + O) = f32x4{dx[nb] * phi[nb], dy[nb] * phi[nb], dz[nb] * phi[nb], 0.f};
+          }
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        if (g == 0) segrow[sub * 16 * NB + nb * 16 + c] = valid[nb] ? ri[nb] : -1;
+    }
+    // make the wave's LDS writes visible to all of its lanes
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // ---- per-row sums of the tile (rows are contiguous edge ranges) --------
+    const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
+    const int rfirst = segrow[0];
+#pragma unroll 1
+    for (int cb = 0; cb < SEGW; cb += 64) {
+      const int colx = cb + l;
+      const bool act = colx < SEGW;
+      float acc = 0.f;
+      int r = segrow[0];
+#pragma unroll 1
+      for (int k = 0; k < nvalid; ++k) {
+        if (act) acc += seg[k * SEGP + colx];
+        const int rn = (k + 1 < nvalid) ? segrow[k + 1] : -2;
+        if (rn != r) {
+          const int rs = a.rowptr[r], re = a.rowptr[r + 1];
+          if (rs >= base && re <= base + TE) {
+            if (colx < O) {
+              ((T*)a.out_msg)[(int64_t)r * a.smsg + colx] = from_f32<T>(acc);
+            } else if (EQ && colx < O + 3) {
+              float v = acc;
+              if (a.mean) v /= (float)(re - rs);
+              a.out_mov[(int64_t)r * a.smov + (colx - O)] = v;
+            }
+          } else if (act) {
+            const int slot = (r == rfirst) ? 0 : 1;
+            a.carry[((int64_t)t * 2 + slot) * SEGW + colx] = acc;
+          }
+          acc = 0.f;
+          r = rn;
+        }
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+}
+
+// Rows that are empty or cross a tile: sum the tile partials in tile order.
+template <typename T, bool EQ>
+__global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
+  const int SEGW = O + (EQ ? 4 : 0);
+  const int l = threadIdx.x & 63;
+  const int nfix = *a.n_fix;
+  const int64_t nw = (int64_t)gridDim.x * 4;
+  for (int64_t f = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); f < nfix; f += nw) {
+    const int r = a.fix_rows[f];
+    const int rs = a.rowptr[r], re = a.rowptr[r + 1];
+    for (int colx = l; colx < SEGW; colx += 64) {
+      float acc = 0.f;
+      if (re > rs) {
+        const int64_t t0 = rs / kTileEdges, t1 = (re - 1) / kTileEdges;
+        const int slot0 = (a.erow[t0 * kTileEdges] == r) ? 0 : 1;
+        for (int64_t tt = t0; tt <= t1; ++tt) acc += a.carry[(tt * 2 + (tt == t0 ? slot0 : 0)) * SEGW + colx];
+      }
+      if (colx < O) {
+        ((T*)a.out_msg)[(int64_t)r * a.smsg + colx] = from_f32<T>(acc);
+      } else if (EQ && colx < O + 3) {
+        if (a.mean && re > rs) acc /= (float)(re - rs);
+        a.out_mov[(int64_t)r * a.smov + (colx - O)] = acc;
+      }
+    }
+  }
+}
+
+template <typename T, int H, int O, int M, int NB, bool EQ>
+static int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
+  constexpr int SEGW = O + (EQ ? 4 : 0), SEGP = SEGW + 4;
+  const size_t lds = 4 * (size_t)(kTileEdges * SEGP + kTileEdges) * sizeof(float);
+  if (a.ntiles > 0) {
+    int blocks = (int)std::min<int64_t>(cdiv(a.ntiles, 4), 256 * 2);
+    hipLaunchKernelGGL((fwd_edge_kernel<T, H, O, M, NB, EQ>), dim3(blocks), dim3(256), lds, st, a);
+  }
+  int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 2048);
+  hipLaunchKernelGGL((fwd_fixup_kernel<T, EQ>), dim3(fb), dim3(256), 0, st, a, O);
+  return (int)hipGetLastError();
+}
+
+template <typename T, bool EQ>
+static int launch_fwd_dims(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+  if (s.H == 64 && s.O == 32) return launch_fwd_t<T, 64, 32, 32, 2, EQ>(a, st);
+  if (s.H == 128) return launch_fwd_t<T, 128, 128, 128, 2, EQ>(a, st);
+  return launch_fwd_t<T, 256, 256, 256, 1, EQ>(a, st);
+}
+
+int launch_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+  if (s.bf16) return s.eq ? launch_fwd_dims<bf16, true>(s, a, st) : launch_fwd_dims<bf16, false>(s, a, st);
+  return s.eq ? launch_fwd_dims<float, true>(s, a, st) : launch_fwd_dims<float, false>(s, a, st);
+}
+
+}  // namespace egnn

@@ -1,0 +1,149 @@
+// Host-side internal interface between the C-ABI (egnn_capi.hip) and the
+// kernel translation units.  Not part of the public ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include "../../include/egnn.h"
+
+namespace egnn {
+
+constexpr int kTileEdges = 32;        // edges per forward wave tile (carry granularity)
+constexpr int kFragElems = 512;       // one A-operand fragment: 64 lanes x 8 values
+
+inline size_t align_up(size_t x, size_t a = 256) { return (x + a - 1) / a * a; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---- schedule layout (device memory, caller-owned) ------------------------
+struct SchedView {
+  int32_t* erow;      // [E]   row (destination) of every CSR edge
+  int32_t* fix_rows;  // [N]   rows that are empty or cross a 32-edge tile, ascending
+  int32_t* n_fix;     // [1]
+  int32_t* csc_ptr;   // [N+1] source-sorted offsets
+  int32_t* csc_eid;   // [E]   CSR edge positions sorted by col (stable)
+  int32_t* err;       // [1]   CSR validation flag
+};
+size_t sched_layout(int64_t N, int64_t E, void* base, SchedView* v);
+
+// ---- weight fragments ------------------------------------------------------
+// Chain-ordered A-operand fragments of the message-chain weights.  R x K
+// logical matrix -> (R/16) x (ceil(K/32)) fragments of kFragElems values.
+struct FragSet {
+  void* hlT;   // A = W_hl^T   (O x H)   pre2  = W_hl^T  m1
+  void* movT;  // A = W1mov^T  (M x O)   q     = W1mov^T m
+  void* mov;   // A = W1mov    (O x M)   g_m   = W1mov   g_q
+  void* hl;    // A = W_hl     (H x O)   g_a1  = W_hl    g_a2
+  void* u;     // A = W_u      (H x KU)  pre1 += W_u U     (KU slots: e..., r2hi, r2lo)
+  void* uT;    // A = W_u^T    (16 x H)  row 0 = w_d:  g_r = w_d . g_a1
+  float* b2f;  // [O]  fp32 copies of the small vectors
+  float* bx1f; // [M]
+  float* w2mf; // [M]
+};
+
+struct LayerShape {
+  int64_t N, E;
+  int F, FE, H, O, M, KU, NUC;   // KU = 32 * NUC (edge-input slots incl. r2 hi/lo)
+  bool eq, mean, bf16;
+  size_t esz;                    // bytes per activation element
+};
+int make_shape(const EgnnDims* d, LayerShape* s);
+
+// workspace layout
+struct FwdWs {
+  FragSet fr;
+  void* PQ;        // [N][2H] activation dtype, chain-permuted per 32 features
+  float* carry;    // [ntiles][2][O+4]
+};
+struct BwdWs {
+  FragSet fr;
+  void* PQ;        // [N][2H] activation dtype
+  void* Dm1;       // [E][H] per-edge factors of the weight gradients (activation dtype)
+  void* Dm;        // [E][O]
+  void* Dgq;       // [E][M]
+  void* Dga2;      // [E][O]
+  void* Dp;        // [E][M]
+  void* Gh;        // [E][H] dL/dpre1 per edge
+  float* Gx;       // [E][4] (dL/ddelta xyz, dL/dphi)
+  float* R2;       // [E]
+  float* dPQ;      // [N][2H] fp32
+  float* part;     // split-K partials
+  float* dWhl;     // (H+1) x O   last row = db2
+  float* dW1m;     // (O+1) x M   last row = dbx1
+  float* dw2m;     // M
+  float* dWe;      // H x FE
+  float* dwd;      // H
+  float* dWn;      // (F+1) x 2H  last row = [db1 | sum dQ]
+  int64_t part_elems;
+};
+size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
+size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
+int64_t splitk_len(int64_t K);
+
+// ---- launchers (return hipError_t as int) --------------------------------
+int launch_schedule(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E, const SchedView& v,
+                    void* tmp, size_t tmp_bytes, hipStream_t st);
+size_t schedule_tmp_bytes(int64_t N, int64_t E);
+
+int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
+                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st);
+
+// Generic MFMA GEMM: C(m,n) = sum_k A(m,k) B(k,n) [+ bias(n)], fp32 accumulate.
+struct GemmArgs {
+  int64_t M, N, K;
+  const void* A; int64_t sam, sak; int a_bf16; int64_t a_ones_row;  // row index that reads as all-ones (-1: none)
+  const void* B; int64_t sbk, sbn; int b_bf16;
+  const int32_t* b_kidx;          // non-null: B's k index goes through b_kidx[k] (edge_ids gather)
+  int64_t b_kjump_at, b_kjump;    // B offset += b_kjump for k >= b_kjump_at (two stacked blocks)
+  int64_t b_njump_at, b_njump;    // B offset += b_njump for n >= b_njump_at (two side-by-side blocks)
+  const void* bias; int bias_bf16; int64_t bias_len;   // bias(n) for n < bias_len
+  void* C; int64_t scm, scn; int c_bf16;
+  int perm_half;        // >0: column n stored at chain-permuted position within 32-column groups
+  float* partial;       // split-K partial output [split][M][N] (then C unused)
+  int64_t ksplit;       // K per split (0: no split)
+};
+int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st);
+
+struct FwdArgs {
+  int64_t N, E, ntiles;
+  int FE, NUC, mean;
+  const void* PQ;
+  const float* coord; int64_t sc;
+  const void* ef; int64_t se;
+  const int32_t* rowptr; const int32_t* col; const int32_t* eids; const int32_t* erow;
+  FragSet fr;
+  void* out_msg; int64_t smsg;
+  float* out_mov; int64_t smov;
+  float* carry;
+  const int32_t* fix_rows; const int32_t* n_fix;
+};
+int launch_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
+
+struct BwdArgs {
+  int64_t N, E, ntiles;
+  int FE, NUC, mean;
+  const void* PQ;
+  const float* coord; int64_t sc;
+  const void* ef; int64_t se;
+  const int32_t* rowptr; const int32_t* col; const int32_t* eids; const int32_t* erow;
+  FragSet fr;
+  const void* gmsg; int64_t sgm;
+  const float* gmov; int64_t sgx;
+  void* Dm1; void* Dm; void* Dgq; void* Dga2; void* Dp; void* Gh; float* Gx; float* R2;
+};
+int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
+int bwd_tile_edges(const LayerShape& s);
+
+// dPQ[n] = [sum_row Gh | sum_csc Gh] (fp32); grad_coord = sum_row Gx - sum_csc Gx
+int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
+                       const int32_t* csc_ptr, const int32_t* csc_eid, float* dPQ, float* gcoord,
+                       int64_t sgc, hipStream_t st);
+// out[l] = sum_b part[b][l] for l < L (fixed order)
+int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st);
+// scatter the fp32 weight-gradient sums into the caller's tensors
+struct FinalizeArgs {
+  const float *dWhl, *dW1m, *dw2m, *dWe, *dwd, *dWn;   // fp32 sums (see BwdWs)
+  void* gw1; void* gw2; void* gw1m; void* gw2m; void* gb1; void* gb2; void* gbx1;
+};
+int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st);
+
+}  // namespace egnn

@@ -1,0 +1,383 @@
+// Node-level kernels of the fused EGNN/MPNN layer:
+//  * weight-fragment preparation (chain-ordered A operands, fp32 vectors)
+//  * a generic MFMA GEMM used for the per-node projections
+//      P|Q = h [W_n1 | W_n2] + [b1 | 0]      (forward, hoisted out of the edge loop)
+//      dh  = dP W_n1^T + dQ W_n2^T            (backward)
+//      [dW_n1 | dW_n2 ; db1] = [h | 1]^T [dP | dQ]   (backward, split-K, fixed-order sum)
+//  * the per-node gradient reduction over CSR rows and CSC columns
+//  * fixed-order partial sums and the scatter of weight gradients
+// The hoisting uses linearity of the first phi_e layer: h_i W_n1 + h_j W_n2 is
+// computed once per node instead of once per edge (forward_kernel.py:207
+// recomputes it per edge).
+#include "egnn_device.h"
+#include "egnn_internal.h"
+
+namespace egnn {
+
+// ---------------------------------------------------------------------------
+// shapes and workspace layouts (host)
+// ---------------------------------------------------------------------------
+int make_shape(const EgnnDims* d, LayerShape* s) {
+  if (!d) return EGNN_ERR_NULL;
+  s->N = d->N; s->E = d->E; s->F = d->F; s->FE = d->FE; s->H = d->H; s->O = d->O; s->M = d->M;
+  s->eq = d->equivariant != 0; s->mean = d->mean_agg != 0; s->bf16 = d->dtype == EGNN_BF16;
+  if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
+  if (d->F < 1 || d->F > 512 || d->F % 16 != 0) return EGNN_ERR_DIMS;
+  if (d->FE < 0 || d->FE > 480 || d->FE % 8 != 0) return EGNN_ERR_DIMS;
+  bool ok = (d->H == 64 && d->O == 32 && d->M == 32) || (d->H == 128 && d->O == 128 && d->M == 128) ||
+            (d->H == 256 && d->O == 256 && d->M == 256);
+  if (!ok) return EGNN_ERR_DIMS;
+  s->NUC = s->eq ? (int)cdiv(d->FE + 2, 32) : (int)cdiv(d->FE, 32);
+  s->KU = 32 * s->NUC;
+  s->esz = s->bf16 ? 2 : 4;
+  return EGNN_OK;
+}
+
+static size_t frag_bytes(int R, int K, size_t esz) { return (size_t)(R / 16) * cdiv(K, 32) * kFragElems * esz; }
+
+static size_t frag_layout(const LayerShape& s, char* base, FragSet* f, size_t off, bool with_bwd) {
+  auto take = [&](size_t bytes) { void* p = base ? base + off : nullptr; off = align_up(off + bytes); return p; };
+  f->hlT = take(frag_bytes(s.O, s.H, s.esz));
+  f->movT = s.eq ? take(frag_bytes(s.M, s.O, s.esz)) : nullptr;
+  f->u = s.NUC ? take(frag_bytes(s.H, s.KU, s.esz)) : nullptr;
+  f->mov = (with_bwd && s.eq) ? take(frag_bytes(s.O, s.M, s.esz)) : nullptr;
+  f->hl = with_bwd ? take(frag_bytes(s.H, s.O, s.esz)) : nullptr;
+  f->uT = (with_bwd && s.eq) ? take(frag_bytes(16, s.H, s.esz)) : nullptr;
+  f->b2f = (float*)take(sizeof(float) * s.O);
+  f->bx1f = (float*)take(sizeof(float) * (s.M + 4));
+  f->w2mf = (float*)take(sizeof(float) * (s.M + 4));
+  return off;
+}
+
+size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
+  char* b = (char*)base;
+  size_t off = frag_layout(s, b, &w->fr, 0, false);
+  w->PQ = b ? b + off : nullptr; off = align_up(off + (size_t)s.N * 2 * s.H * s.esz);
+  int64_t ntiles = cdiv(s.E, kTileEdges);
+  w->carry = (float*)(b ? b + off : nullptr); off = align_up(off + (size_t)ntiles * 2 * (s.O + 4) * sizeof(float));
+  return off;
+}
+
+int64_t splitk_len(int64_t K) {
+  int64_t ks = std::max<int64_t>(256, cdiv(K, 256));
+  return cdiv(ks, 32) * 32;
+}
+
+size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
+  char* b = (char*)base;
+  size_t off = frag_layout(s, b, &w->fr, 0, true);
+  auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
+  const size_t E = (size_t)std::max<int64_t>(s.E, 1);
+  w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
+  w->Dm1 = take(E * s.H * s.esz);
+  w->Dm = take(E * s.O * s.esz);
+  w->Dgq = s.eq ? take(E * s.M * s.esz) : nullptr;
+  w->Dga2 = take(E * s.O * s.esz);
+  w->Dp = s.eq ? take(E * s.M * s.esz) : nullptr;
+  w->Gh = take(E * s.H * s.esz);
+  w->Gx = (float*)take(E * 4 * sizeof(float));
+  w->R2 = (float*)take(E * sizeof(float));
+  w->dPQ = (float*)take((size_t)s.N * 2 * s.H * sizeof(float));
+  // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
+  int64_t se = cdiv(std::max<int64_t>(s.E, 1), splitk_len(s.E)), sn = cdiv(s.N, splitk_len(s.N));
+  int64_t pe = std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
+                                  (int64_t)s.H * std::max(s.FE, 1), (int64_t)s.H});
+  w->part_elems = std::max<int64_t>(se * pe, sn * (int64_t)(s.F + 1) * 2 * s.H);
+  w->part = (float*)take((size_t)w->part_elems * sizeof(float));
+  w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
+  w->dW1m = (float*)take((size_t)(s.O + 1) * s.M * sizeof(float));
+  w->dw2m = (float*)take((size_t)s.M * sizeof(float));
+  w->dWe = (float*)take((size_t)s.H * std::max(s.FE, 1) * sizeof(float));
+  w->dwd = (float*)take((size_t)s.H * sizeof(float));
+  w->dWn = (float*)take((size_t)(s.F + 1) * 2 * s.H * sizeof(float));
+  return off;
+}
+
+// ---------------------------------------------------------------------------
+// fragment preparation
+// ---------------------------------------------------------------------------
+enum FragKind { FK_WT = 0, FK_W = 1, FK_U = 2, FK_UT = 3 };
+struct FragDesc {
+  void* dst; int R, K, nkc, kind, chain;
+  const void* src; int64_t ld;
+};
+
+template <typename T>
+__global__ void frag_build_kernel(FragDesc d, int F, int FE, int H, int eq) {
+  const int64_t total = (int64_t)(d.R / 16) * d.nkc * kFragElems;
+  const T* src = (const T*)d.src;
+  T* dst = (T*)d.dst;
+  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+    int s = (int)(idx & 7);
+    int lane = (int)((idx >> 3) & 63);
+    int64_t f = idx >> 9;
+    int kc = (int)(f % d.nkc);
+    int rb = (int)(f / d.nkc);
+    int r = rb * 16 + (lane & 15);
+    int g = lane >> 4;
+    int k = kc * 32 + (d.chain ? kappa_chain(g, s) : 8 * g + s);
+    float v = 0.0f;
+    if (r < d.R && k < d.K) {
+      switch (d.kind) {
+        case FK_WT: v = to_f32(src[(int64_t)k * d.ld + r]); break;
+        case FK_W: v = to_f32(src[(int64_t)r * d.ld + k]); break;
+        case FK_U:  // r = hidden unit h, k = edge-input slot
+          if (k < FE) v = to_f32(src[(int64_t)(2 * F + eq + k) * H + r]);
+          else if (eq && k == FE) v = to_f32(src[(int64_t)(2 * F) * H + r]);
+          else if (eq && k == FE + 1 && sizeof(T) == 2) v = to_f32(src[(int64_t)(2 * F) * H + r]);
+          break;
+        case FK_UT:  // row 0 = w_d
+          if (eq && r == 0) v = to_f32(src[(int64_t)(2 * F) * H + k]);
+          break;
+      }
+    }
+    dst[idx] = from_f32<T>(v);
+  }
+}
+
+template <typename T>
+__global__ void vec_prep_kernel(const T* b2, const T* bx1, const T* w2m, float* b2f, float* bx1f, float* w2mf, int O, int M) {
+  int t = blockIdx.x * blockDim.x + threadIdx.x;
+  if (t < O) b2f[t] = b2 ? to_f32(b2[t]) : 0.0f;
+  if (t < M + 4) {
+    bx1f[t] = (bx1 && t < M) ? to_f32(bx1[t]) : 0.0f;
+    w2mf[t] = (w2m && t < M) ? to_f32(w2m[t]) : 0.0f;
+  }
+}
+
+template <typename T>
+static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
+                     const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st) {
+  auto build = [&](void* dst, int R, int K, int kind, int chain, const void* src, int64_t ld) {
+    if (!dst) return;
+    FragDesc d{dst, R, K, (int)cdiv(K, 32), kind, chain, src, ld};
+    int64_t total = (int64_t)(R / 16) * d.nkc * kFragElems;
+    int blocks = (int)std::min<int64_t>(cdiv(total, 256), 4096);
+    hipLaunchKernelGGL(frag_build_kernel<T>, dim3(blocks), dim3(256), 0, st, d, s.F, s.FE, s.H, s.eq ? 1 : 0);
+  };
+  build(fr.hlT, s.O, s.H, FK_WT, 1, w2, s.O);        // A[o][h] = W_hl[h][o]
+  if (s.eq) build(fr.movT, s.M, s.O, FK_WT, 1, w1m, s.M);  // A[m][o] = W1mov[o][m]
+  if (s.NUC) build(fr.u, s.H, s.KU, FK_U, 0, w1, s.H);
+  if (with_bwd) {
+    if (s.eq) build(fr.mov, s.O, s.M, FK_W, 1, w1m, s.M);   // A[o][m] = W1mov[o][m]
+    build(fr.hl, s.H, s.O, FK_W, 1, w2, s.O);               // A[h][o] = W_hl[h][o]
+    if (s.eq) build(fr.uT, 16, s.H, FK_UT, 1, w1, s.H);
+  }
+  int n = std::max(s.O, s.M + 4);
+  hipLaunchKernelGGL(vec_prep_kernel<T>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const T*)b2,
+                     (const T*)(s.eq ? bx1 : nullptr), (const T*)(s.eq ? w2m : nullptr), fr.b2f, fr.bx1f, fr.w2mf,
+                     s.O, s.M);
+  return (int)hipGetLastError();
+}
+
+int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
+                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st) {
+  return s.bf16 ? prep_impl<bf16>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, st)
+                : prep_impl<float>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, st);
+}
+
+// ---------------------------------------------------------------------------
+// generic MFMA GEMM (64 x 64 tile per 4-wave block, k step 32)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float ld_elem(const void* p, int64_t off, int is_bf16) {
+  return is_bf16 ? (float)((const bf16*)p)[off] : ((const float*)p)[off];
+}
+
+// inverse of kappa_chain within a 32-column group: feature f (0..31) -> position
+__device__ __forceinline__ int chain_pos(int f) {
+  return f < 16 ? 8 * (f >> 2) + (f & 3) : 8 * ((f - 16) >> 2) + 4 + ((f - 16) & 3);
+}
+
+template <typename TC>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int BM = 64, BN = 64, BK = 32, PAD = sizeof(TC) == 2 ? 8 : 4, LDK = BK + PAD;
+  __shared__ __attribute__((aligned(16))) TC As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) TC Bs[BN * LDK];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
+  int64_t kbeg = 0, kend = g.K;
+  if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
+  f32x4 acc[2][2];
+  for (int a = 0; a < 2; ++a) for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    for (int it = 0; it < (BM * BK) / 256; ++it) {
+      int idx = tid + it * 256;
+      int mm = idx / BK, kk = idx % BK;
+      int64_t m = m0 + mm, k = k0 + kk;
+      float v = 0.0f;
+      if (m < g.M && k < kend) v = (m == g.a_ones_row) ? 1.0f : ld_elem(g.A, m * g.sam + k * g.sak, g.a_bf16);
+      As[mm * LDK + kk] = from_f32<TC>(v);
+    }
+    for (int it = 0; it < (BN * BK) / 256; ++it) {
+      int idx = tid + it * 256;
+      int nn = idx % BN, kk = idx / BN;
+      int64_t n = n0 + nn, k = k0 + kk;
+      float v = 0.0f;
+      if (n < g.N && k < kend) {
+        const int64_t kk2 = g.b_kidx ? (int64_t)clampi(g.b_kidx[k], (int)g.K) : k;
+        const int64_t off = kk2 * g.sbk + n * g.sbn + (k >= g.b_kjump_at ? g.b_kjump : 0) + (n >= g.b_njump_at ? g.b_njump : 0);
+        v = ld_elem(g.B, off, g.b_bf16);
+      }
+      Bs[nn * LDK + kk] = from_f32<TC>(v);
+    }
+    __syncthreads();
+    typedef typename ChunkOf<TC>::type Ch;
+    Ch a[2], b[2];
+    for (int i = 0; i < 2; ++i) {
+      a[i] = load_chunk(&As[(wm * 32 + i * 16 + c) * LDK + 8 * gq]);
+      b[i] = load_chunk(&Bs[(wn * 32 + i * 16 + c) * LDK + 8 * gq]);
+    }
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 2; ++j) mma(acc[i][j], a[i], b[j]);
+    __syncthreads();
+  }
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
+      for (int r = 0; r < 4; ++r) {
+        int64_t m = m0 + wm * 32 + i * 16 + 4 * gq + r;
+        int64_t n = n0 + wn * 32 + j * 16 + c;
+        if (m >= g.M || n >= g.N) continue;
+        float v = acc[i][j][r];
+        if (g.partial) {
+          g.partial[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
+          continue;
+        }
+        if (g.bias && n < g.bias_len) v += ld_elem(g.bias, n, g.bias_bf16);
+        int64_t pn = n;
+        if (g.perm_half > 0) {
+          int64_t half = n / g.perm_half, f = n % g.perm_half;
+          pn = half * g.perm_half + (f & ~31) + chain_pos((int)(f & 31));
+        }
+        int64_t off = m * g.scm + pn * g.scn;
+        if (g.c_bf16) ((bf16*)g.C)[off] = (bf16)v;
+        else ((float*)g.C)[off] = v;
+      }
+}
+
+int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st) {
+  if (g.M <= 0 || g.N <= 0) return 0;
+  unsigned gz = g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
+  dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
+  if (compute_bf16) hipLaunchKernelGGL(gemm_kernel<bf16>, grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL(gemm_kernel<float>, grid, dim3(256), 0, st, g);
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// node gradient reduction: one wave per node
+// ---------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ Gh, const float* __restrict__ Gx,
+                                                          const int32_t* __restrict__ rowptr,
+                                                          const int32_t* __restrict__ csc_ptr,
+                                                          const int32_t* __restrict__ csc_eid, float* __restrict__ dPQ,
+                                                          float* __restrict__ gcoord, int64_t sgc, int64_t N, int eq) {
+  constexpr int PER = (H + 63) / 64;
+  const int l = threadIdx.x & 63;
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  for (int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); n < N; n += nw) {
+    float ap[PER], aq[PER];
+    for (int u = 0; u < PER; ++u) { ap[u] = 0.f; aq[u] = 0.f; }
+    float ax = 0.f;
+    const int rs = rowptr[n], re = rowptr[n + 1];
+    for (int e = rs; e < re; ++e) {
+      const T* row = Gh + (int64_t)e * H;
+      for (int u = 0; u < PER; ++u) { int p = l + 64 * u; if (p < H) ap[u] += to_f32(row[p]); }
+      if (eq && l < 3) ax += Gx[(int64_t)e * 4 + l];
+    }
+    const int cs = csc_ptr[n], ce = csc_ptr[n + 1];
+    for (int k = cs; k < ce; ++k) {
+      const int e = csc_eid[k];
+      const T* row = Gh + (int64_t)e * H;
+      for (int u = 0; u < PER; ++u) { int p = l + 64 * u; if (p < H) aq[u] += to_f32(row[p]); }
+      if (eq && l < 3) ax -= Gx[(int64_t)e * 4 + l];
+    }
+    float* out = dPQ + n * 2 * H;
+    for (int u = 0; u < PER; ++u) {
+      int p = l + 64 * u;
+      if (p < H) {
+        out[p] = ap[u];
+        out[H + p] = aq[u];
+      }
+    }
+    if (eq && l < 3) gcoord[n * sgc + l] = ax;
+  }
+}
+
+int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
+                       const int32_t* csc_ptr, const int32_t* csc_eid, float* dPQ, float* gcoord, int64_t sgc,
+                       hipStream_t st) {
+  int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
+  int eq = s.eq ? 1 : 0;
+#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, dPQ, gcoord, sgc, s.N, eq)
+  if (s.bf16) {
+    if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
+  } else {
+    if (s.H == 64) NR_LAUNCH(float, 64); else if (s.H == 128) NR_LAUNCH(float, 128); else NR_LAUNCH(float, 256);
+  }
+#undef NR_LAUNCH
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// fixed-order partial sums and gradient scatter
+// ---------------------------------------------------------------------------
+__global__ void sum_rows_kernel(const float* __restrict__ part, int64_t nrows, int64_t L, float* __restrict__ out) {
+  for (int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; l < L; l += (int64_t)gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    for (int64_t b = 0; b < nrows; ++b) acc += part[b * L + l];
+    out[l] = acc;
+  }
+}
+
+int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st) {
+  if (L <= 0) return 0;
+  int blocks = (int)std::min<int64_t>(cdiv(L, 256), 2048);
+  hipLaunchKernelGGL(sum_rows_kernel, dim3(blocks), dim3(256), 0, st, part, nrows, L, out);
+  return (int)hipGetLastError();
+}
+
+template <typename T>
+__global__ void finalize_kernel(FinalizeArgs f, int F, int FE, int H, int O, int M, int eq) {
+  const int g = eq ? 1 : 0;
+  const int64_t n_w1 = (int64_t)(2 * F + g + FE) * H;
+  const int64_t n_w2 = (int64_t)H * O, n_w1m = eq ? (int64_t)O * M : 0, n_w2m = eq ? M : 0;
+  const int64_t n_b1 = f.gb1 ? H : 0, n_b2 = f.gb2 ? O : 0, n_bx1 = (f.gbx1 && eq) ? M : 0;
+  const int64_t total = n_w1 + n_w2 + n_w1m + n_w2m + n_b1 + n_b2 + n_bx1;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    int64_t u = t;
+    if (u < n_w1) {  // packed [W_n1 | W_n2 | w_d | W_e] (layer.py:24-28)
+      const int64_t row = u / H, h = u % H;
+      float v;
+      if (row < 2 * F) v = f.dWn[(row % F) * 2 * H + (row >= F ? H : 0) + h];
+      else if (eq && row == 2 * F) v = f.dwd[h];
+      else v = f.dWe[h * FE + (row - 2 * F - g)];
+      ((T*)f.gw1)[u] = from_f32<T>(v);
+      continue;
+    }
+    u -= n_w1;
+    if (u < n_w2) { ((T*)f.gw2)[u] = from_f32<T>(f.dWhl[u]); continue; }
+    u -= n_w2;
+    if (u < n_w1m) { ((T*)f.gw1m)[u] = from_f32<T>(f.dW1m[u]); continue; }
+    u -= n_w1m;
+    if (u < n_w2m) { ((T*)f.gw2m)[u] = from_f32<T>(f.dw2m[u]); continue; }
+    u -= n_w2m;
+    if (u < n_b1) { ((T*)f.gb1)[u] = from_f32<T>(f.dWn[(int64_t)F * 2 * H + u]); continue; }
+    u -= n_b1;
+    if (u < n_b2) { ((T*)f.gb2)[u] = from_f32<T>(f.dWhl[(int64_t)H * O + u]); continue; }
+    u -= n_b2;
+    if (u < n_bx1) { ((T*)f.gbx1)[u] = from_f32<T>(f.dW1m[(int64_t)O * M + u]); continue; }
+  }
+}
+
+int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st) {
+  if (s.bf16)
+    hipLaunchKernelGGL(finalize_kernel<bf16>, dim3(512), dim3(256), 0, st, f, s.F, s.FE, s.H, s.O, s.M, s.eq ? 1 : 0);
+  else
+    hipLaunchKernelGGL(finalize_kernel<float>, dim3(512), dim3(256), 0, st, f, s.F, s.FE, s.H, s.O, s.M, s.eq ? 1 : 0);
+  return (int)hipGetLastError();
+}
+
+}  // namespace egnn

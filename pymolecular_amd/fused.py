@@ -1,0 +1,265 @@
+"""Host side of the fused EGNN/MPNN layer: schedule cache, workspaces, autograd.
+
+Everything here is plumbing around the C-ABI (``include/egnn.h``): torch
+provides device memory and the current stream, the HIP library does the work.
+There is no CPU path: tensors must live on a ROCm device and the library must
+be built, otherwise the calls raise.
+
+Reference counterparts
+  * the Triton launches ``egnn_forward_kernel_node_parallel[grid](...)``
+    (models/EGNN/forward_kernel.py:14-43) and
+    ``egnn_backward_kernel_node_parallel[grid](...)`` (backward_kernel.py:14-50)
+    -> :func:`egnn_fused_forward` / :func:`egnn_fused_backward`;
+  * the reference has no ``autograd.Function`` (SURVEY of the repo: none), so
+    :class:`EGNNFusedFn` is new; it saves only its inputs and recomputes in the
+    backward, like backward_kernel.py:173-180.
+"""
+from __future__ import annotations
+
+import weakref
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _capi
+from ._capi import EgnnDims, EgnnStrides, check
+
+__all__ = ["Schedule", "get_schedule", "egnn_fused_forward", "egnn_fused_backward", "EGNNFusedFn",
+           "egnn_fused", "coo_to_csr"]
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _require_device(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a ROCm device tensor: the fused EGNN layer has no CPU path")
+
+
+@dataclass
+class Schedule:
+    """Per-graph schedule (row ids per edge, split-row list, CSC permutation)."""
+    buf: torch.Tensor
+    N: int
+    E: int
+
+
+_SCHED_CACHE: "dict[tuple, tuple[weakref.ref, weakref.ref, Schedule]]" = {}
+
+
+def get_schedule(row_ptrs: torch.Tensor, col_indices: torch.Tensor, num_nodes: int) -> Schedule:
+    """Build (or fetch from the cache) the schedule of a dst-sorted int32 CSR graph.
+
+    Keyed by the storage pointers and in-place version counters of ``row_ptrs``
+    and ``col_indices``, so an edited graph gets a new schedule.
+    """
+    _require_device(row_ptrs, "row_ptrs")
+    if row_ptrs.dtype != torch.int32 or col_indices.dtype != torch.int32:
+        raise TypeError("row_ptrs and col_indices must be int32 (datasets_loaders.py CSR contract)")
+    if row_ptrs.numel() != num_nodes + 1:
+        raise ValueError(f"row_ptrs has {row_ptrs.numel()} entries, expected num_nodes + 1 = {num_nodes + 1}")
+    row_ptrs = row_ptrs.contiguous()
+    col_indices = col_indices.contiguous()
+    N, E = int(num_nodes), int(col_indices.numel())
+    key = (row_ptrs.data_ptr(), col_indices.data_ptr(), N, E, row_ptrs._version, col_indices._version,
+           row_ptrs.device.index)
+    hit = _SCHED_CACHE.get(key)
+    if hit is not None and hit[0]() is row_ptrs and hit[1]() is col_indices:
+        return hit[2]
+    L = _capi.lib()
+    nbytes = L.egnn_schedule_bytes(N, E)
+    tbytes = L.egnn_schedule_tmp_bytes(N, E)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=row_ptrs.device)
+    tmp = torch.empty(max(tbytes, 1), dtype=torch.uint8, device=row_ptrs.device)
+    rc = L.egnn_schedule_build(row_ptrs.data_ptr(), col_indices.data_ptr() if E else None, N, E, buf.data_ptr(),
+                               nbytes, tmp.data_ptr(), tbytes, _stream(row_ptrs.device))
+    check("egnn_schedule_build", rc)
+    sched = Schedule(buf, N, E)
+    if len(_SCHED_CACHE) > 64:
+        _SCHED_CACHE.clear()
+    _SCHED_CACHE[key] = (weakref.ref(row_ptrs), weakref.ref(col_indices), sched)
+    return sched
+
+
+def coo_to_csr(row: torch.Tensor, col: torch.Tensor, num_nodes: int):
+    """COO (row = destination) -> dst-sorted int32 CSR plus the permutation.
+
+    A stable sort by destination keeps the original order of edges within a
+    row; ``edge_ids[k]`` is the COO position of CSR edge ``k`` (the indirection
+    of forward_kernel.py:19-21 / explanation.txt:113).
+    """
+    row = row.to(torch.int64)
+    order = torch.sort(row, stable=True).indices
+    counts = torch.bincount(row, minlength=num_nodes)
+    row_ptrs = torch.zeros(num_nodes + 1, dtype=torch.int64, device=row.device)
+    row_ptrs[1:] = torch.cumsum(counts, 0)
+    return (row_ptrs.to(torch.int32), col.to(torch.int64)[order].to(torch.int32).contiguous(),
+            order.to(torch.int32).contiguous())
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return _capi.EGNN_F32
+    if dt == torch.bfloat16:
+        return _capi.EGNN_BF16
+    raise TypeError(f"unsupported dtype {dt}: the fused layer runs in float32 or bfloat16")
+
+
+def _dims(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg) -> EgnnDims:
+    N, F = h.shape
+    FE = 0 if edge_feat is None else int(edge_feat.shape[1])
+    H = int(w1.shape[-1])
+    O = int(w2.shape[1])
+    M = int(w1m.shape[1]) if (equivariant and w1m is not None) else O
+    g = 1 if equivariant else 0
+    if w1.shape[0] != 2 * F + g + FE:
+        raise ValueError(f"w1_msg has {w1.shape[0]} rows, expected 2*F + {g} + F_E = {2 * F + g + FE}")
+    return EgnnDims(N=N, E=int(col.numel()), F=F, FE=FE, H=H, O=O, M=M, equivariant=g,
+                    mean_agg=1 if mean_agg else 0, dtype=_dtype_code(h.dtype))
+
+
+def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant):
+    _require_device(h, "h")
+    dt = h.dtype
+    h = h.contiguous()
+    cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
+    w1, w2, w1m, b1, b2, bx1 = cv(w1), cv(w2), cv(w1m), cv(b1), cv(b2), cv(bx1)
+    if w2m is not None:
+        w2m = w2m.reshape(-1).to(dt).contiguous()
+    if edge_feat is not None:
+        edge_feat = edge_feat.to(dt).contiguous()
+        if edge_feat.shape[1] == 0:
+            edge_feat = None
+    if equivariant:
+        coord = coord.to(torch.float32).contiguous()
+    return h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1
+
+
+def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
+                       w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
+                       equivariant: bool = True):
+    """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``."""
+    h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
+        h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
+    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg)
+    sched = get_schedule(row_ptrs, col_indices, h.shape[0])
+    dev = h.device
+    N, O = h.shape[0], dims.O
+    out_msg = torch.empty((N, O), dtype=h.dtype, device=dev)
+    out_mov = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
+    L = _capi.lib()
+    ws_bytes = L.egnn_fwd_workspace_bytes(dims)
+    if ws_bytes == 0:
+        raise ValueError(f"unsupported dimensions F={dims.F} FE={dims.FE} H={dims.H} O={dims.O} M={dims.M}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    strides = EgnnStrides(h=h.stride(0), coord=coord.stride(0) if equivariant else 4,
+                          edge=edge_feat.stride(0) if edge_feat is not None else 0, msg=out_msg.stride(0), mov=3)
+    eids = None if edge_ids is None else edge_ids.to(torch.int32).contiguous()
+    rc = L.egnn_fwd(dims, strides, _ptr(h), _ptr(coord) if equivariant else None, _ptr(edge_feat),
+                    _ptr(row_ptrs.contiguous()), _ptr(col_indices.contiguous()), _ptr(eids), _ptr(w1), _ptr(w2),
+                    _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
+                    _ptr(bx1) if equivariant else None, _ptr(out_msg), _ptr(out_mov), sched.buf.data_ptr(),
+                    ws.data_ptr(), ws_bytes, _stream(dev))
+    check("egnn_fwd", rc)
+    return out_msg, out_mov
+
+
+def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
+                        b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
+                        equivariant: bool = True):
+    """Backward by recomputation.  Returns a dict of gradients (None where absent)."""
+    w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
+    h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
+        h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
+    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg)
+    sched = get_schedule(row_ptrs, col_indices, h.shape[0])
+    dev, dt = h.device, h.dtype
+    N = h.shape[0]
+    gm = grad_out_msg.to(dt).contiguous()
+    gx = grad_out_mov.to(torch.float32).contiguous() if equivariant else None
+    grad_h = torch.empty_like(h)
+    grad_coord = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
+    g_w1 = torch.empty_like(w1)
+    g_w2 = torch.empty_like(w2)
+    g_w1m = torch.empty_like(w1m) if equivariant else None
+    g_w2m = torch.empty_like(w2m) if equivariant else None
+    g_b1 = torch.empty_like(b1) if b1 is not None else None
+    g_b2 = torch.empty_like(b2) if b2 is not None else None
+    g_bx1 = torch.empty_like(bx1) if (bx1 is not None and equivariant) else None
+    L = _capi.lib()
+    ws_bytes = L.egnn_bwd_workspace_bytes(dims)
+    if ws_bytes == 0:
+        raise ValueError(f"unsupported dimensions F={dims.F} FE={dims.FE} H={dims.H} O={dims.O} M={dims.M}")
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    strides = EgnnStrides(h=h.stride(0), coord=3, edge=edge_feat.stride(0) if edge_feat is not None else 0,
+                          msg=gm.stride(0), mov=gx.stride(0) if equivariant else 3)
+    if equivariant and coord.stride(0) != 3:
+        coord = coord[:, :3].contiguous()
+    eids = None if edge_ids is None else edge_ids.to(torch.int32).contiguous()
+    rc = L.egnn_bwd(dims, strides, _ptr(h), _ptr(coord) if equivariant else None, _ptr(edge_feat),
+                    _ptr(row_ptrs.contiguous()), _ptr(col_indices.contiguous()), _ptr(eids), _ptr(w1), _ptr(w2),
+                    _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
+                    _ptr(bx1) if equivariant else None, _ptr(gm), _ptr(gx), _ptr(grad_h), _ptr(grad_coord),
+                    _ptr(g_w1), _ptr(g_w2), _ptr(g_w1m), _ptr(g_w2m), _ptr(g_b1), _ptr(g_b2), _ptr(g_bx1),
+                    sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
+    check("egnn_bwd", rc)
+    if g_w2m is not None and w2m_shape is not None:
+        g_w2m = g_w2m.reshape(w2m_shape)
+    return dict(h=grad_h, coord=grad_coord, w1_msg=g_w1, w2_msg=g_w2, w1_mov=g_w1m, w2_mov=g_w2m, b1=g_b1,
+                b2=g_b2, bx1=g_bx1)
+
+
+class EGNNFusedFn(torch.autograd.Function):
+    """Autograd wrapper: ``(out_msg, out_mov) = EGNNFusedFn.apply(h, coord, edge_feat, row_ptrs,
+    col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, mean_agg, equivariant)``.
+
+    Saves only the inputs; the backward recomputes the messages.  No gradient
+    flows to ``edge_feat`` or the CSR (the reference computes none).
+    """
+
+    @staticmethod
+    def forward(ctx, h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
+                b1=None, b2=None, bx1=None, mean_agg=False, equivariant=True):
+        out_msg, out_mov = egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg,
+                                              w2_msg, w1_mov, w2_mov, b1, b2, bx1, mean_agg=mean_agg,
+                                              equivariant=equivariant)
+        ctx.save_for_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov,
+                              w2_mov, b1, b2, bx1)
+        ctx.mean_agg = mean_agg
+        ctx.equivariant = equivariant
+        ctx.coord_shape = None if coord is None else tuple(coord.shape)
+        if out_mov is None:
+            out_mov = torch.zeros((h.shape[0], 3), dtype=torch.float32, device=h.device)
+        return out_msg, out_mov
+
+    @staticmethod
+    def backward(ctx, g_msg, g_mov):
+        (h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1) = ctx.saved_tensors
+        if g_msg is None:
+            g_msg = torch.zeros((h.shape[0], w2.shape[1]), dtype=h.dtype, device=h.device)
+        if g_mov is None:
+            g_mov = torch.zeros((h.shape[0], 3), dtype=torch.float32, device=h.device)
+        g = egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2,
+                                bx1, g_msg, g_mov, mean_agg=ctx.mean_agg, equivariant=ctx.equivariant)
+        gc = g["coord"]
+        if gc is not None and ctx.coord_shape is not None and ctx.coord_shape[1] != 3:
+            full = torch.zeros(ctx.coord_shape, dtype=torch.float32, device=gc.device)
+            full[:, :3] = gc
+            gc = full
+        if gc is not None and coord is not None:
+            gc = gc.to(coord.dtype)
+        return (g["h"], gc, None, None, None, None, g["w1_msg"], g["w2_msg"], g["w1_mov"], g["w2_mov"], g["b1"],
+                g["b2"], g["bx1"], None, None)
+
+
+def egnn_fused(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None, w2_mov=None,
+               b1=None, b2=None, bx1=None, *, mean_agg=False, equivariant=True):
+    """Differentiable fused layer (see :class:`EGNNFusedFn`)."""
+    return EGNNFusedFn.apply(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
+                             b1, b2, bx1, mean_agg, equivariant)

@@ -1,0 +1,59 @@
+"""The C-ABI library loads and exports every symbol include/egnn.h declares (no GPU needed)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from pymolecular_amd import _capi
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "egnn.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(egnn_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_capi.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _capi.lib()
+    for name in declared_symbols():
+        assert hasattr(L, name), name
+        assert ctypes.cast(getattr(L, name), ctypes.c_void_p).value
+
+
+def test_host_only_entry_points():
+    L = _capi.lib()
+    assert L.egnn_abi_version() == 1
+    assert _capi.status_string(0) == "ok"
+    assert "CSR" in _capi.status_string(6)
+    assert L.egnn_schedule_bytes(100, 1000) > 4 * 1000
+    d = _capi.EgnnDims(N=100, E=1000, F=128, FE=16, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=1)
+    assert L.egnn_fwd_workspace_bytes(d) > 0
+    assert L.egnn_bwd_workspace_bytes(d) > L.egnn_fwd_workspace_bytes(d)
+
+
+@pytest.mark.parametrize("field,value", [("H", 96), ("FE", 12), ("F", 24), ("dtype", 7), ("O", 64)])
+def test_unsupported_dims_rejected(field, value):
+    L = _capi.lib()
+    kw = dict(N=100, E=1000, F=128, FE=16, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=0)
+    kw[field] = value
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**kw)) == 0
+
+
+def test_bad_arguments_return_status_not_crash():
+    L = _capi.lib()
+    d = _capi.EgnnDims(N=10, E=20, F=128, FE=0, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=0)
+    s = _capi.EgnnStrides(h=128, coord=3, edge=0, msg=128, mov=3)
+    # NULL inputs are reported before anything touches the device
+    rc = L.egnn_fwd(d, s, *([None] * 17), 0, None)
+    assert rc == 1
+    s_bad = _capi.EgnnStrides(h=16, coord=3, edge=0, msg=128, mov=3)
+    assert L.egnn_fwd(d, s_bad, *([None] * 17), 0, None) == 3
+    assert L.egnn_schedule_build(None, None, 10, 20, None, 0, None, 0, None) == 1
+    assert L.egnn_schedule_build(1, 1, 0, 20, 1, 0, 1, 0, None) == 2

@@ -1,0 +1,129 @@
+"""GPU parity of the fused EGNN/MPNN layer (HIP kernels through the C-ABI) against the oracle.
+
+Tolerance: normwise max|y - ref| / max|ref| <= 1e-5 (fp32), <= 2e-2 (bf16); the
+bf16 oracle runs in float64 on bf16-rounded inputs and weights.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import egnn_oracle as orc
+from pymolecular_amd import graphs
+from tests.cases import Case, random_csr
+
+pytestmark = pytest.mark.gpu
+
+TOL = {"fp32": 1e-5, "bf16": 2e-2}
+DT = {"fp32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _dev(a, dt=None):
+    if a is None:
+        return None
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t.to(dt) if dt is not None else t
+
+
+def run_fused(case, dtype, backward=True):
+    from pymolecular_amd import fused
+    dt = DT[dtype]
+    rowptr, col = _dev(case.rowptr), _dev(case.col)
+    eids = _dev(case.edge_ids)
+    h = _dev(case.h, dt)
+    coord = _dev(case.coord) if case.eq else None
+    ef = _dev(case.ef, dt)
+    p = {k: _dev(v, dt) for k, v in case.p.items()}
+    print(f"[fused] N={case.N} E={case.E} F={case.F} FE={case.FE} H={case.H} O={case.O} M={case.M} "
+          f"eq={case.eq} mean={case.mean} dtype={dtype}", flush=True)
+    out_msg, out_mov = fused.egnn_fused_forward(h, coord, ef, rowptr, col, eids, p["w1_msg"], p["w2_msg"],
+                                                p.get("w1_mov"), p.get("w2_mov"), p.get("b1"), p.get("b2"),
+                                                p.get("bx1"), mean_agg=case.mean, equivariant=case.eq)
+    res = dict(out_msg=out_msg.float().cpu().numpy(), out_mov=None if out_mov is None else out_mov.cpu().numpy())
+    if backward:
+        g = fused.egnn_fused_backward(h, coord, ef, rowptr, col, eids, p["w1_msg"], p["w2_msg"], p.get("w1_mov"),
+                                      p.get("w2_mov"), p.get("b1"), p.get("b2"), p.get("bx1"), _dev(case.gm, dt),
+                                      _dev(case.gx) if case.eq else None, mean_agg=case.mean, equivariant=case.eq)
+        res["grads"] = {k: (None if v is None else v.float().cpu().numpy()) for k, v in g.items()}
+    torch.cuda.synchronize()
+    return res
+
+
+def check_case(case, dtype, backward=True):
+    bf = dtype == "bf16"
+    tol = TOL[dtype]
+    res = run_fused(case, dtype, backward)
+    ref_msg, ref_mov = case.forward_ref(bf)
+    errs = {"out_msg": orc.normwise_rel_err(res["out_msg"], ref_msg)}
+    if case.eq:
+        errs["out_mov"] = orc.normwise_rel_err(res["out_mov"], ref_mov)
+    if backward:
+        gref = case.backward_ref(bf)
+        for k, v in gref.items():
+            if v is None or res["grads"].get(k) is None:
+                continue
+            errs["d" + k] = orc.normwise_rel_err(res["grads"][k].reshape(v.shape), v)
+    print("errors:", {k: f"{v:.2e}" for k, v in errs.items()}, flush=True)
+    bad = {k: v for k, v in errs.items() if not (v <= tol)}
+    assert not bad, f"{dtype} parity failed (tol {tol}): {bad}"
+    return errs
+
+
+def molecule_case(n_graphs, F, FE, H, O, M, seed, **kw):
+    g = graphs.molecule_batch(n_graphs, seed=seed, feat_seed=seed + 1)
+    return Case(g.rowptr, g.col, F, FE, H, O, M, seed=seed, **kw)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_molecules_h128(dtype):
+    check_case(molecule_case(6, 128, 0, 128, 128, 128, seed=11), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_molecules_h128_mean_agg(dtype):
+    check_case(molecule_case(5, 128, 0, 128, 128, 128, seed=12, mean_agg=True), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_reference_sweep_dims(dtype):
+    # F_NODE 32, F_EDGE 16, HIDDEN 64, OUT 32, HID_MOV 32 (test_mem.py:46-50)
+    rowptr, col = random_csr(300, np.full(300, 32), seed=5)
+    check_case(Case(rowptr, col, 32, 16, 64, 32, 32, seed=13, bias=False), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_skewed_rows_and_empty_rows(dtype):
+    # rows crossing many 32-edge tiles, empty rows, and a final partial tile
+    degs = np.array([0, 1, 100, 0, 3, 31, 32, 33, 0, 64, 2, 200, 5, 0, 17] * 4)
+    rowptr, col = random_csr(len(degs), degs, seed=7)
+    check_case(Case(rowptr, col, 128, 16, 128, 128, 128, seed=14), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_edge_ids_permutation(dtype):
+    rowptr, col = random_csr(120, np.arange(120) % 40, seed=9)
+    E = len(col)
+    perm = np.random.Generator(np.random.PCG64(3)).permutation(E)
+    check_case(Case(rowptr, col, 128, 32, 128, 128, 128, seed=15, edge_ids=perm), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+def test_mpnn_variant(dtype):
+    rowptr, col = random_csr(400, (np.arange(400) * 7) % 23 + 2, seed=21)
+    check_case(Case(rowptr, col, 128, 16, 128, 128, 128, seed=16, eq=False), dtype)
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+def test_hidden_256(dtype):
+    rowptr, col = random_csr(160, np.full(160, 40), seed=31)
+    check_case(Case(rowptr, col, 256, 32, 256, 256, 256, seed=17, mean_agg=True), dtype)
+
+
+def test_determinism_bitwise():
+    rowptr, col = random_csr(500, (np.arange(500) * 13) % 50, seed=41)
+    case = Case(rowptr, col, 128, 16, 128, 128, 128, seed=18)
+    a = run_fused(case, "bf16")
+    b = run_fused(case, "bf16")
+    assert np.array_equal(a["out_msg"], b["out_msg"]) and np.array_equal(a["out_mov"], b["out_mov"])
+    for k, v in a["grads"].items():
+        if v is not None:
+            assert np.array_equal(v, b["grads"][k]), k
