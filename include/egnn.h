@@ -129,6 +129,23 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides,
                  void* grad_b1, void* grad_b2, void* grad_bx1,
                  const void* sched, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- instrumentation (no reference counterpart) ---------------------------
+ * When enabled, every kernel launch made by egnn_fwd / egnn_bwd is bracketed
+ * by HIP events recorded on the caller's stream, grouped by kernel class.
+ * egnn_profile_read synchronises on those events and returns the summed
+ * device time and the launch count of one class.  Off by default; enabling
+ * clears previous records.  Not thread-safe; for benchmarks only. */
+#define EGNN_K_FWD_EDGE 0     /* fused forward edge kernel             */
+#define EGNN_K_FWD_FIXUP 1    /* forward split/empty-row fix-up         */
+#define EGNN_K_BWD_EDGE 2     /* fused backward edge kernel            */
+#define EGNN_K_NODE_GEMM 3    /* per-node projection GEMMs (P|Q, dh)   */
+#define EGNN_K_WGRAD 4        /* weight-gradient split-K GEMMs + sums  */
+#define EGNN_K_NODE_REDUCE 5  /* CSR/CSC node gradient reduction       */
+#define EGNN_K_PREP 6         /* weight-fragment preparation           */
+#define EGNN_K_COUNT 7
+int32_t egnn_profile_enable(int32_t on);
+int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches);
+
 #ifdef __cplusplus
 }
 #endif

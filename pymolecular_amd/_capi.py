@@ -19,7 +19,12 @@ EGNN_BF16 = 1
 EXPORTED = (
     "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
     "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_fwd", "egnn_bwd",
+    "egnn_profile_enable", "egnn_profile_read",
 )
+
+# kernel classes of the instrumentation hook
+K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP = range(7)
+K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep")
 
 
 class EgnnDims(ctypes.Structure):
@@ -71,8 +76,26 @@ def lib() -> ctypes.CDLL:
     L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 17 + [c_size_t, P]
     L.egnn_bwd.restype = c_int32
     L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 26 + [c_size_t, P]
+    L.egnn_profile_enable.restype = c_int32
+    L.egnn_profile_enable.argtypes = [c_int32]
+    L.egnn_profile_read.restype = c_int32
+    L.egnn_profile_read.argtypes = [c_int32, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(c_int64)]
     _lib = L
     return L
+
+
+def profile_enable(on: bool) -> None:
+    check("egnn_profile_enable", lib().egnn_profile_enable(1 if on else 0))
+
+
+def profile_read() -> dict:
+    """{kernel class name: (total ms, launches)} of the records since profile_enable(True)."""
+    out = {}
+    for k, name in enumerate(K_NAMES):
+        t, n = ctypes.c_double(0.0), c_int64(0)
+        check("egnn_profile_read", lib().egnn_profile_read(k, ctypes.byref(t), ctypes.byref(n)))
+        out[name] = (t.value, n.value)
+    return out
 
 
 def status_string(status: int) -> str:

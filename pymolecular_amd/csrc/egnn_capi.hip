@@ -3,6 +3,7 @@
 // kernels on the caller's stream.  No allocation, no host synchronisation
 // (except the one documented in egnn_schedule_build).
 #include "egnn_device.h"
+#include <vector>
 #include "egnn_internal.h"
 
 using namespace egnn;
@@ -14,6 +15,30 @@ constexpr int32_t kAbiVersion = 1;
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
 int32_t hip_status(int e) { return e == (int)hipSuccess ? EGNN_OK : EGNN_ERR_HIP; }
+
+// ---- instrumentation: HIP events around launches, grouped by kernel class ----
+struct ProfRec { int cls; hipEvent_t a, b; };
+bool g_prof_on = false;
+std::vector<ProfRec> g_prof;
+
+struct ProfScope {
+  hipStream_t st; int cls; hipEvent_t a = nullptr, b = nullptr;
+  ProfScope(int c, hipStream_t s) : st(s), cls(c) {
+    if (!g_prof_on) return;
+    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { a = b = nullptr; return; }
+    (void)hipEventRecord(a, st);
+  }
+  ~ProfScope() {
+    if (!a) return;
+    (void)hipEventRecord(b, st);
+    g_prof.push_back(ProfRec{cls, a, b});
+  }
+};
+
+void prof_clear() {
+  for (auto& r : g_prof) { (void)hipEventDestroy(r.a); (void)hipEventDestroy(r.b); }
+  g_prof.clear();
+}
 
 // Per-node projection  P | Q = h [W_n1 | W_n2] + [b1 | 0], stored in the
 // activation dtype with each 32-feature group in chain order.
@@ -113,8 +138,14 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
   hipStream_t st = (hipStream_t)stream;
 
-  if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, st))) != EGNN_OK) return rc;
-  if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+  {
+    ProfScope ps(EGNN_K_PREP, st);
+    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, st))) != EGNN_OK) return rc;
+  }
+  {
+    ProfScope ps(EGNN_K_NODE_GEMM, st);
+    if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+  }
   FwdArgs a{};
   a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, kTileEdges);
   a.FE = s.FE; a.NUC = s.NUC; a.mean = s.mean;
@@ -127,7 +158,12 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;
   a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
-  return hip_status(launch_fwd(s, a, st));
+  {
+    ProfScope ps(EGNN_K_FWD_EDGE, st);
+    if ((rc = hip_status(launch_fwd(s, a, 0, st))) != EGNN_OK) return rc;
+  }
+  ProfScope ps(EGNN_K_FWD_FIXUP, st);
+  return hip_status(launch_fwd(s, a, 1, st));
 }
 
 int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h, const float* coord,
@@ -155,8 +191,14 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
   hipStream_t st = (hipStream_t)stream;
 
-  if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, st))) != EGNN_OK) return rc;
-  if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+  {
+    ProfScope ps(EGNN_K_PREP, st);
+    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, st))) != EGNN_OK) return rc;
+  }
+  {
+    ProfScope ps(EGNN_K_NODE_GEMM, st);
+    if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+  }
 
   BwdArgs a{};
   a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, bwd_tile_edges(s));
@@ -169,13 +211,19 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.gmsg = grad_out_msg; a.sgm = strides->msg;
   a.gmov = grad_out_mov; a.sgx = strides->mov;
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
-  if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
+  {
+    ProfScope ps(EGNN_K_BWD_EDGE, st);
+    if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
+  }
 
   // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
   float* gcoord = s.eq ? grad_coord : nullptr;
-  if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
+  {
+    ProfScope ps(EGNN_K_NODE_REDUCE, st);
+    if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
                                           strides->coord, st))) != EGNN_OK)
-    return rc;
+      return rc;
+  }
 
   // dh = dP W_n1^T + dQ W_n2^T
   {
@@ -186,6 +234,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     g.b_kjump_at = s.H; g.b_kjump = (int64_t)s.F * s.H - s.H;
     g.b_njump_at = INT64_MAX;
     g.C = grad_h; g.scm = strides->h; g.scn = 1; g.c_bf16 = s.bf16;
+    ProfScope ps(EGNN_K_NODE_GEMM, st);
     if ((rc = hip_status(launch_gemm(g, s.bf16, st))) != EGNN_OK) return rc;
   }
 
@@ -194,6 +243,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     g.ksplit = splitk_len(std::max<int64_t>(g.K, 1));
     g.partial = w.part;
     int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
+    ProfScope ps(EGNN_K_WGRAD, st);
     if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
     int32_t r = hip_status(launch_gemm(g, s.bf16, st));
     if (r != EGNN_OK) return r;
@@ -241,7 +291,31 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   f.dWhl = w.dWhl; f.dW1m = w.dW1m; f.dw2m = w.dw2m; f.dWe = w.dWe; f.dwd = w.dwd; f.dWn = w.dWn;
   f.gw1 = grad_w1_msg; f.gw2 = grad_w2_msg; f.gw1m = grad_w1_mov; f.gw2m = grad_w2_mov;
   f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1;
+  ProfScope ps(EGNN_K_WGRAD, st);
   return hip_status(launch_finalize(s, f, st));
+}
+
+int32_t egnn_profile_enable(int32_t on) {
+  prof_clear();
+  g_prof_on = on != 0;
+  return EGNN_OK;
+}
+
+int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches) {
+  if (!total_ms || !launches) return EGNN_ERR_NULL;
+  double t = 0.0;
+  int64_t n = 0;
+  for (auto& r : g_prof) {
+    if (r.cls != kernel_class) continue;
+    if (hipEventSynchronize(r.b) != hipSuccess) return EGNN_ERR_HIP;
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) return EGNN_ERR_HIP;
+    t += ms;
+    ++n;
+  }
+  *total_ms = t;
+  *launches = n;
+  return EGNN_OK;
 }
 
 }  // extern "C"

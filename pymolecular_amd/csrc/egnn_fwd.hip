@@ -258,12 +258,15 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
 }
 
 template <typename T, int H, int O, int M, int NB, bool EQ>
-static int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
+static int launch_fwd_t(const FwdArgs& a, int part, hipStream_t st) {
   constexpr int SEGW = O + (EQ ? 4 : 0), SEGP = SEGW + 4;
   const size_t lds = 4 * (size_t)(kTileEdges * SEGP + kTileEdges) * sizeof(float);
-  if (a.ntiles > 0) {
-    int blocks = (int)std::min<int64_t>(cdiv(a.ntiles, 4), 256 * 2);
-    hipLaunchKernelGGL((fwd_edge_kernel<T, H, O, M, NB, EQ>), dim3(blocks), dim3(256), lds, st, a);
+  if (part == 0) {
+    if (a.ntiles > 0) {
+      int blocks = (int)std::min<int64_t>(cdiv(a.ntiles, 4), 256 * 2);
+      hipLaunchKernelGGL((fwd_edge_kernel<T, H, O, M, NB, EQ>), dim3(blocks), dim3(256), lds, st, a);
+    }
+    return (int)hipGetLastError();
   }
   int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 2048);
   hipLaunchKernelGGL((fwd_fixup_kernel<T, EQ>), dim3(fb), dim3(256), 0, st, a, O);
@@ -271,15 +274,15 @@ static int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
 }
 
 template <typename T, bool EQ>
-static int launch_fwd_dims(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
-  if (s.H == 64 && s.O == 32) return launch_fwd_t<T, 64, 32, 32, 2, EQ>(a, st);
-  if (s.H == 128) return launch_fwd_t<T, 128, 128, 128, 2, EQ>(a, st);
-  return launch_fwd_t<T, 256, 256, 256, 1, EQ>(a, st);
+static int launch_fwd_dims(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st) {
+  if (s.H == 64 && s.O == 32) return launch_fwd_t<T, 64, 32, 32, 2, EQ>(a, part, st);
+  if (s.H == 128) return launch_fwd_t<T, 128, 128, 128, 2, EQ>(a, part, st);
+  return launch_fwd_t<T, 256, 256, 256, 1, EQ>(a, part, st);
 }
 
-int launch_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
-  if (s.bf16) return s.eq ? launch_fwd_dims<bf16, true>(s, a, st) : launch_fwd_dims<bf16, false>(s, a, st);
-  return s.eq ? launch_fwd_dims<float, true>(s, a, st) : launch_fwd_dims<float, false>(s, a, st);
+int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st) {
+  if (s.bf16) return s.eq ? launch_fwd_dims<bf16, true>(s, a, part, st) : launch_fwd_dims<bf16, false>(s, a, part, st);
+  return s.eq ? launch_fwd_dims<float, true>(s, a, part, st) : launch_fwd_dims<float, false>(s, a, part, st);
 }
 
 }  // namespace egnn

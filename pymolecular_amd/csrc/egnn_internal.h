@@ -116,7 +116,8 @@ struct FwdArgs {
   float* carry;
   const int32_t* fix_rows; const int32_t* n_fix;
 };
-int launch_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
+// part 0: edge tiles, part 1: split/empty-row fix-up
+int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
 
 struct BwdArgs {
   int64_t N, E, ntiles;

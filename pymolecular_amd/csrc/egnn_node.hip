@@ -202,9 +202,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   f32x4 acc[2][2];
   for (int a = 0; a < 2; ++a) for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
   for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    // walk the tile along whichever operand dimension is contiguous in memory
+    const bool a_m_fast = g.sam == 1 && g.sak != 1;
+    const bool b_k_fast = g.sbk == 1 && g.sbn != 1 && !g.b_kidx;
     for (int it = 0; it < (BM * BK) / 256; ++it) {
       int idx = tid + it * 256;
-      int mm = idx / BK, kk = idx % BK;
+      int mm = a_m_fast ? idx % BM : idx / BK, kk = a_m_fast ? idx / BM : idx % BK;
       int64_t m = m0 + mm, k = k0 + kk;
       float v = 0.0f;
       if (m < g.M && k < kend) v = (m == g.a_ones_row) ? 1.0f : ld_elem(g.A, m * g.sam + k * g.sak, g.a_bf16);
@@ -212,7 +215,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     }
     for (int it = 0; it < (BN * BK) / 256; ++it) {
       int idx = tid + it * 256;
-      int nn = idx % BN, kk = idx / BN;
+      int nn = b_k_fast ? idx / BK : idx % BN, kk = b_k_fast ? idx % BK : idx / BN;
       int64_t n = n0 + nn, k = k0 + kk;
       float v = 0.0f;
       if (n < g.N && k < kend) {

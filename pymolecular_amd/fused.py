@@ -50,6 +50,22 @@ class Schedule:
     E: int
 
 
+def schedule_arrays(sched: Schedule) -> dict:
+    """int32 views of a schedule buffer, in the layout egnn_schedule_build writes:
+    erow [E], fix_rows [n_fix], csc_ptr [N+1], csc_eid [E] (each 256-byte aligned)."""
+    N, E = sched.N, sched.E
+    off = 0
+    out = {}
+    for name, n in (("erow", max(E, 1)), ("fix_rows", N), ("n_fix", 1), ("csc_ptr", N + 1), ("csc_eid", max(E, 1))):
+        out[name] = sched.buf[off:off + 4 * n].view(torch.int32)
+        off = (off + 4 * n + 255) // 256 * 256
+    nf = int(out.pop("n_fix")[0])
+    out["fix_rows"] = out["fix_rows"][:nf]
+    out["erow"] = out["erow"][:E]
+    out["csc_eid"] = out["csc_eid"][:E]
+    return out
+
+
 _SCHED_CACHE: "dict[tuple, tuple[weakref.ref, weakref.ref, Schedule]]" = {}
 
 
@@ -260,6 +276,14 @@ class EGNNFusedFn(torch.autograd.Function):
 
 def egnn_fused(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None, w2_mov=None,
                b1=None, b2=None, bx1=None, *, mean_agg=False, equivariant=True):
-    """Differentiable fused layer (see :class:`EGNNFusedFn`)."""
+    """Differentiable fused layer (see :class:`EGNNFusedFn`).
+
+    Edge-feature widths that are not a multiple of 8 are zero-padded (with
+    matching zero rows of W_e) outside the Function, so gradients stay exact.
+    """
+    if edge_feat is not None and edge_feat.shape[1] % 8:
+        pad = 8 - edge_feat.shape[1] % 8
+        edge_feat = torch.nn.functional.pad(edge_feat, (0, pad))
+        w1_msg = torch.cat([w1_msg, w1_msg.new_zeros((pad, w1_msg.shape[1]))], dim=0)
     return EGNNFusedFn.apply(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                              b1, b2, bx1, mean_agg, equivariant)

@@ -1,0 +1,87 @@
+"""Schedule (integer work): numpy restatement on the CPU, bit-exact parity on the GPU."""
+import numpy as np
+import pytest
+import torch
+
+from pymolecular_amd import graphs
+from tests.cases import random_csr
+
+TILE = 32
+
+
+def schedule_ref(rowptr, col):
+    """numpy restatement of the schedule: per-edge rows, split/empty rows, stable CSC."""
+    rowptr = np.asarray(rowptr, np.int64)
+    N = len(rowptr) - 1
+    deg = np.diff(rowptr)
+    erow = np.repeat(np.arange(N), deg)
+    first_tile = rowptr[:-1] // TILE
+    last_tile = (rowptr[1:] - 1) // TILE
+    fix = np.flatnonzero((deg == 0) | (first_tile != last_tile))
+    csc_eid = np.argsort(np.asarray(col), kind="stable")
+    csc_ptr = np.searchsorted(np.asarray(col)[csc_eid], np.arange(N + 1), side="left")
+    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid)
+
+
+def brute_force_schedule(rowptr, col):
+    """Pure-Python loops for tiny graphs (pins schedule_ref)."""
+    N = len(rowptr) - 1
+    erow, fix = [], []
+    for r in range(N):
+        a, b = int(rowptr[r]), int(rowptr[r + 1])
+        erow += [r] * (b - a)
+        if a == b or len({e // TILE for e in range(a, b)}) > 1:
+            fix.append(r)
+    buckets = [[] for _ in range(N)]
+    for e, j in enumerate(col):
+        buckets[int(j)].append(e)
+    csc_eid = [e for bkt in buckets for e in bkt]
+    csc_ptr = [0]
+    for bkt in buckets:
+        csc_ptr.append(csc_ptr[-1] + len(bkt))
+    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid)
+
+
+def test_schedule_ref_matches_brute_force():
+    for seed in range(5):
+        degs = np.random.Generator(np.random.PCG64(seed)).integers(0, 70, size=37)
+        rowptr, col = random_csr(37, degs, seed)
+        a, b = schedule_ref(rowptr, col), brute_force_schedule(rowptr, col)
+        for k in a:
+            np.testing.assert_array_equal(a[k], np.asarray(b[k]), err_msg=k)
+
+
+GRAPHS = {
+    "skewed": lambda: random_csr(300, np.random.Generator(np.random.PCG64(1)).integers(0, 300, 300) *
+                                 (np.arange(300) % 7 == 0), seed=2),
+    "molecules": lambda: (lambda g: (g.rowptr, g.col))(graphs.molecule_batch(40, seed=3)),
+    "powerlaw": lambda: (lambda g: (g.rowptr, g.col))(graphs.powerlaw_graph(N=20000, seed=4, with_features=False)),
+}
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", list(GRAPHS))
+def test_device_schedule_bit_exact(name):
+    from pymolecular_amd import fused
+    rowptr, col = GRAPHS[name]()
+    print(f"[schedule] {name} N={len(rowptr) - 1} E={len(col)}", flush=True)
+    rp = torch.from_numpy(np.asarray(rowptr, np.int32)).cuda()
+    cl = torch.from_numpy(np.asarray(col, np.int32)).cuda()
+    got = fused.schedule_arrays(fused.get_schedule(rp, cl, len(rowptr) - 1))
+    ref = schedule_ref(rowptr, col)
+    for k, v in ref.items():
+        np.testing.assert_array_equal(got[k].cpu().numpy(), v, err_msg=k)
+
+
+@pytest.mark.gpu
+def test_invalid_csr_is_reported():
+    from pymolecular_amd import _capi, fused
+    rp = torch.tensor([0, 2, 1, 3], dtype=torch.int32, device="cuda")     # not monotone
+    cl = torch.tensor([0, 1, 2], dtype=torch.int32, device="cuda")
+    with pytest.raises(_capi.EgnnError) as ei:
+        fused.get_schedule(rp, cl, 3)
+    assert ei.value.status == 6
+    rp = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device="cuda")
+    cl = torch.tensor([0, 5, 2], dtype=torch.int32, device="cuda")      # col out of range
+    with pytest.raises(_capi.EgnnError):
+        fused.get_schedule(rp, cl, 3)
