@@ -44,7 +44,7 @@ extern "C" {
 #define EGNN_ERR_NULL 1        /* a required pointer is NULL */
 #define EGNN_ERR_DIMS 2        /* unsupported or inconsistent dimensions */
 #define EGNN_ERR_STRIDE 3      /* a row stride is too small or not a multiple of the vector width */
-#define EGNN_ERR_ALIGN 4       /* a pointer is not 16-byte aligned */
+#define EGNN_ERR_ALIGN 4       /* h, grad_h, edge_feat, out_msg, grad_out_msg or workspace not 16-byte aligned */
 #define EGNN_ERR_WORKSPACE 5   /* workspace or schedule buffer too small */
 #define EGNN_ERR_CSR 6         /* rowptr not monotone / not [0..E], or a col index out of [0, N) */
 #define EGNN_ERR_HIP 7         /* a HIP runtime call or kernel launch failed */
@@ -69,7 +69,7 @@ typedef struct EgnnDims {
 
 /* Row strides in elements; the inner dimension is always contiguous. */
 typedef struct EgnnStrides {
-  int64_t h;           /* h and grad_h                                  */
+  int64_t h;           /* h and grad_h (rows 16-byte aligned)           */
   int64_t coord;       /* coord and grad_coord (>= 3)                   */
   int64_t edge;        /* edge_feat                                     */
   int64_t msg;         /* out_msg and grad_out_msg                      */
@@ -100,6 +100,15 @@ int32_t egnn_schedule_build(const int32_t* rowptr, const int32_t* col, int64_t N
 size_t egnn_fwd_workspace_bytes(const EgnnDims* dims);
 size_t egnn_bwd_workspace_bytes(const EgnnDims* dims);
 
+/* Bytes of the optional node_proj buffer: the per-node projections
+ * [h W_n1 + b1 | h W_n2] (N x 2H, activation dtype, internal column order).
+ * The first phi_e layer is linear in h_i and h_j, so these are computed once
+ * per node instead of once per edge (forward_kernel.py:207 recomputes h_i W_n1
+ * for every edge).  egnn_fwd fills the buffer when it is given one; egnn_bwd
+ * given the same buffer (with h, w1_msg and b1 unchanged) reuses it instead of
+ * recomputing; NULL means computed internally. */
+size_t egnn_node_proj_bytes(const EgnnDims* dims);
+
 /* Fused forward.  b1/b2/bx1 may be NULL (no bias); edge_ids may be NULL
  * (identity, datasets_loaders.py:11); edge_feat may be NULL when FE = 0.
  * For MPNN (equivariant = 0) coord, w1_mov, w2_mov, bx1 and out_mov are
@@ -109,7 +118,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides,
                  const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
                  const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov,
                  const void* b1, const void* b2, const void* bx1,
-                 void* out_msg, float* out_mov,
+                 void* out_msg, float* out_mov, void* node_proj,
                  const void* sched, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Fused backward by recomputation.  Takes the forward inputs plus the
@@ -126,7 +135,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides,
                  const void* grad_out_msg, const float* grad_out_mov,
                  void* grad_h, float* grad_coord,
                  void* grad_w1_msg, void* grad_w2_msg, void* grad_w1_mov, void* grad_w2_mov,
-                 void* grad_b1, void* grad_b2, void* grad_bx1,
+                 void* grad_b1, void* grad_b2, void* grad_bx1, const void* node_proj,
                  const void* sched, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---- instrumentation (no reference counterpart) ---------------------------

@@ -18,7 +18,8 @@ EGNN_BF16 = 1
 # every symbol include/egnn.h declares
 EXPORTED = (
     "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
-    "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_fwd", "egnn_bwd",
+    "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_node_proj_bytes",
+    "egnn_fwd", "egnn_bwd",
     "egnn_profile_enable", "egnn_profile_read",
 )
 
@@ -72,10 +73,12 @@ def lib() -> ctypes.CDLL:
     L.egnn_fwd_workspace_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
     L.egnn_bwd_workspace_bytes.restype = c_size_t
     L.egnn_bwd_workspace_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
+    L.egnn_node_proj_bytes.restype = c_size_t
+    L.egnn_node_proj_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
     L.egnn_fwd.restype = c_int32
-    L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 17 + [c_size_t, P]
+    L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 18 + [c_size_t, P]
     L.egnn_bwd.restype = c_int32
-    L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 26 + [c_size_t, P]
+    L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 27 + [c_size_t, P]
     L.egnn_profile_enable.restype = c_int32
     L.egnn_profile_enable.argtypes = [c_int32]
     L.egnn_profile_read.restype = c_int32

@@ -10,7 +10,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 1;
+constexpr int32_t kAbiVersion = 2;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -42,24 +42,22 @@ void prof_clear() {
 
 // Per-node projection  P | Q = h [W_n1 | W_n2] + [b1 | 0], stored in the
 // activation dtype with each 32-feature group in chain order.
-int32_t project_nodes(const LayerShape& s, const void* h, int64_t sh, const void* w1, const void* b1, void* PQ,
+int32_t project_nodes(const LayerShape& s, const void* h, int64_t sh, const FragSet& fr, const void* b1, void* PQ,
                       hipStream_t st) {
-  GemmArgs g{};
+  Gemm2Args g{};
   g.M = s.N; g.N = 2 * s.H; g.K = s.F;
-  g.A = h; g.sam = sh; g.sak = 1; g.a_bf16 = s.bf16; g.a_ones_row = -1;
-  g.B = w1; g.sbk = s.H; g.sbn = 1; g.b_bf16 = s.bf16;
-  g.b_kjump_at = INT64_MAX; g.b_kjump = 0;
-  g.b_njump_at = s.H; g.b_njump = (int64_t)s.F * s.H - s.H;   // columns H..2H read W_n2 = rows F..2F-1
+  g.A = h; g.lda = sh; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
+  g.B = fr.wn; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 1;     // [W_n1 | W_n2] (F x 2H)
   g.bias = b1; g.bias_bf16 = s.bf16; g.bias_len = b1 ? s.H : 0;
-  g.C = PQ; g.scm = 2 * s.H; g.scn = 1; g.c_bf16 = s.bf16;
+  g.C = PQ; g.ldc = 2 * s.H; g.c_bf16 = s.bf16;
   g.perm_half = s.H;
-  return hip_status(launch_gemm(g, s.bf16, st));
+  return hip_status(launch_gemm2(g, s.bf16, st));
 }
 
 int32_t check_strides(const LayerShape& s, const EgnnStrides* st, bool bwd) {
   if (!st) return EGNN_ERR_NULL;
   const int vec = s.bf16 ? 8 : 4;  // elements per 16 bytes
-  if (st->h < s.F) return EGNN_ERR_STRIDE;
+  if (st->h < s.F || (st->h * (int64_t)s.esz) % 16 != 0) return EGNN_ERR_STRIDE;
   if (st->msg < s.O || st->msg % 4 != 0) return EGNN_ERR_STRIDE;
   if (s.FE > 0 && (st->edge < s.FE || st->edge % vec != 0)) return EGNN_ERR_STRIDE;
   if (s.eq && st->coord < 3) return EGNN_ERR_STRIDE;
@@ -118,11 +116,17 @@ size_t egnn_bwd_workspace_bytes(const EgnnDims* dims) {
   return bwd_ws_layout(s, nullptr, &w);
 }
 
+size_t egnn_node_proj_bytes(const EgnnDims* dims) {
+  LayerShape s;
+  if (make_shape(dims, &s) != EGNN_OK) return 0;
+  return (size_t)s.N * 2 * s.H * s.esz;
+}
+
 int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h, const float* coord,
                  const void* edge_feat, const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
                  const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov, const void* b1,
-                 const void* b2, const void* bx1, void* out_msg, float* out_mov, const void* sched, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 const void* b2, const void* bx1, void* out_msg, float* out_mov, void* node_proj, const void* sched,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   LayerShape s;
   int32_t rc = make_shape(dims, &s);
   if (rc != EGNN_OK) return rc;
@@ -131,7 +135,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   if (s.E > 0 && !col) return EGNN_ERR_NULL;
   if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
   if (s.eq && (!coord || !w1_mov || !w2_mov || !out_mov)) return EGNN_ERR_NULL;
-  if (!aligned16(edge_feat) || !aligned16(out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
+  if (!aligned16(h) || !aligned16(edge_feat) || !aligned16(out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
   FwdWs w;
   if (fwd_ws_layout(s, workspace, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
   SchedView v;
@@ -142,14 +146,16 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     ProfScope ps(EGNN_K_PREP, st);
     if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, st))) != EGNN_OK) return rc;
   }
+  if (!aligned16(node_proj)) return EGNN_ERR_ALIGN;
+  void* PQ = node_proj ? node_proj : w.PQ;
   {
     ProfScope ps(EGNN_K_NODE_GEMM, st);
-    if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+    if ((rc = project_nodes(s, h, strides->h, w.fr, b1, PQ, st)) != EGNN_OK) return rc;
   }
   FwdArgs a{};
   a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, kTileEdges);
   a.FE = s.FE; a.NUC = s.NUC; a.mean = s.mean;
-  a.PQ = w.PQ;
+  a.PQ = PQ;
   a.coord = coord; a.sc = strides->coord;
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
@@ -160,7 +166,8 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
-    if ((rc = hip_status(launch_fwd(s, a, 0, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(coop_supported(s) ? launch_coop_fwd(s, a, st) : launch_fwd(s, a, 0, st))) != EGNN_OK)
+      return rc;
   }
   ProfScope ps(EGNN_K_FWD_FIXUP, st);
   return hip_status(launch_fwd(s, a, 1, st));
@@ -171,8 +178,8 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
                  const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov, const void* b1,
                  const void* b2, const void* bx1, const void* grad_out_msg, const float* grad_out_mov, void* grad_h,
                  float* grad_coord, void* grad_w1_msg, void* grad_w2_msg, void* grad_w1_mov, void* grad_w2_mov,
-                 void* grad_b1, void* grad_b2, void* grad_bx1, const void* sched, void* workspace,
-                 size_t workspace_bytes, void* stream) {
+                 void* grad_b1, void* grad_b2, void* grad_bx1, const void* node_proj, const void* sched,
+                 void* workspace, size_t workspace_bytes, void* stream) {
   LayerShape s;
   int32_t rc = make_shape(dims, &s);
   if (rc != EGNN_OK) return rc;
@@ -184,7 +191,8 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
   if (s.eq && (!coord || !w1_mov || !w2_mov || !grad_out_mov || !grad_coord || !grad_w1_mov || !grad_w2_mov))
     return EGNN_ERR_NULL;
-  if (!aligned16(edge_feat) || !aligned16(grad_out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
+  if (!aligned16(h) || !aligned16(grad_h) || !aligned16(edge_feat) || !aligned16(grad_out_msg) || !aligned16(workspace))
+    return EGNN_ERR_ALIGN;
   BwdWs w;
   if (bwd_ws_layout(s, workspace, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
   SchedView v;
@@ -195,15 +203,17 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     ProfScope ps(EGNN_K_PREP, st);
     if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, st))) != EGNN_OK) return rc;
   }
-  {
+  if (!aligned16(node_proj)) return EGNN_ERR_ALIGN;
+  const void* PQ = node_proj ? node_proj : w.PQ;
+  if (!node_proj) {
     ProfScope ps(EGNN_K_NODE_GEMM, st);
-    if ((rc = project_nodes(s, h, strides->h, w1_msg, b1, w.PQ, st)) != EGNN_OK) return rc;
+    if ((rc = project_nodes(s, h, strides->h, w.fr, b1, w.PQ, st)) != EGNN_OK) return rc;
   }
 
   BwdArgs a{};
   a.N = s.N; a.E = s.E; a.ntiles = cdiv(s.E, bwd_tile_edges(s));
   a.FE = s.FE; a.NUC = s.NUC; a.mean = s.mean;
-  a.PQ = w.PQ;
+  a.PQ = PQ;
   a.coord = coord; a.sc = strides->coord;
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
@@ -211,9 +221,12 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.gmsg = grad_out_msg; a.sgm = strides->msg;
   a.gmov = grad_out_mov; a.sgx = strides->mov;
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
+  const bool coop = coop_supported(s);
+  a.dwpart = w.dwpart; a.LW = w.LW;
+  if (coop) a.ntiles = cdiv(s.E, kTileEdges);
   {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
-    if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_bwd(s, a, st))) != EGNN_OK) return rc;
   }
 
   // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
@@ -225,17 +238,15 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       return rc;
   }
 
-  // dh = dP W_n1^T + dQ W_n2^T
+  // dh = [dP | dQ] [W_n1 | W_n2]^T
   {
-    GemmArgs g{};
+    Gemm2Args g{};
     g.M = s.N; g.N = s.F; g.K = 2 * s.H;
-    g.A = w.dPQ; g.sam = 2 * s.H; g.sak = 1; g.a_bf16 = 0; g.a_ones_row = -1;
-    g.B = w1_msg; g.sbk = 1; g.sbn = s.H; g.b_bf16 = s.bf16;
-    g.b_kjump_at = s.H; g.b_kjump = (int64_t)s.F * s.H - s.H;
-    g.b_njump_at = INT64_MAX;
-    g.C = grad_h; g.scm = strides->h; g.scn = 1; g.c_bf16 = s.bf16;
+    g.A = w.dPQ; g.lda = 2 * s.H; g.a_bf16 = 0; g.a_kc = 1; g.a_ones_row = -1;
+    g.B = w.fr.wn; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 0;   // B[k][f] = Wn[f][k]
+    g.C = grad_h; g.ldc = strides->h; g.c_bf16 = s.bf16;
     ProfScope ps(EGNN_K_NODE_GEMM, st);
-    if ((rc = hip_status(launch_gemm(g, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
   }
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
@@ -249,14 +260,22 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     if (r != EGNN_OK) return r;
     return hip_status(launch_sum_rows(w.part, nsplit, g.M * g.N, dst, st));
   };
-  {
+  if (coop) {
+    ProfScope ps(EGNN_K_WGRAD, st);
+    if (s.E > 0) {
+      if ((rc = hip_status(launch_sum_rows(w.dwpart, w.nblk, w.LW, w.dwsum, st))) != EGNN_OK) return rc;
+    } else {
+      if ((rc = hip_status(launch_sum_rows(w.dwpart, 0, w.LW, w.dwsum, st))) != EGNN_OK) return rc;
+    }
+  }
+  if (!coop) {
     GemmArgs g{};
     g.M = s.H + 1; g.N = s.O; g.K = s.E;
     g.A = w.Dm1; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = s.H;
     g.B = w.Dga2; g.sbk = s.O; g.sbn = 1; g.b_bf16 = s.bf16;
     if ((rc = splitk(g, w.dWhl)) != EGNN_OK) return rc;
   }
-  if (s.eq) {
+  if (s.eq && !coop) {
     GemmArgs g{};
     g.M = s.O + 1; g.N = s.M; g.K = s.E;
     g.A = w.Dm; g.sam = 1; g.sak = s.O; g.a_bf16 = s.bf16; g.a_ones_row = s.O;
@@ -273,7 +292,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     d.B = w.R2; d.sbk = 1; d.sbn = 0; d.b_bf16 = 0;
     if ((rc = splitk(d, w.dwd)) != EGNN_OK) return rc;
   }
-  if (s.FE > 0) {
+  if (s.FE > 0 && !coop) {
     GemmArgs g{};
     g.M = s.H; g.N = s.FE; g.K = s.E;
     g.A = w.Gh; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = -1;
@@ -281,14 +300,28 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     if ((rc = splitk(g, w.dWe)) != EGNN_OK) return rc;
   }
   {
-    GemmArgs g{};
+    // [dW_n1 | dW_n2 ; db1 | .] = [h | 1]^T [dP | dQ], split over nodes, fixed-order sum
+    Gemm2Args g{};
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
-    g.A = h; g.sam = 1; g.sak = strides->h; g.a_bf16 = s.bf16; g.a_ones_row = s.F;
-    g.B = w.dPQ; g.sbk = 2 * s.H; g.sbn = 1; g.b_bf16 = 0;
-    if ((rc = splitk(g, w.dWn)) != EGNN_OK) return rc;
+    g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;
+    g.B = w.dPQ; g.ldb = 2 * s.H; g.b_bf16 = 0; g.b_nc = 1;
+    g.ksplit = splitk_len(s.N);
+    g.partial = w.part;
+    const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), g.ksplit);
+    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    ProfScope ps(EGNN_K_WGRAD, st);
+    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_sum_rows(w.part, nsplit, g.M * g.N, w.dWn, st))) != EGNN_OK) return rc;
   }
   FinalizeArgs f{};
   f.dWhl = w.dWhl; f.dW1m = w.dW1m; f.dw2m = w.dw2m; f.dWe = w.dWe; f.dwd = w.dwd; f.dWn = w.dWn;
+  if (coop) {
+    f.dWhl = w.dwsum;
+    f.dW1m = f.dWhl + (int64_t)(s.H + 1) * s.O;
+    f.dw2m = f.dW1m + (s.eq ? (int64_t)(s.O + 1) * s.M : 0);
+    f.dWe = f.dw2m + (s.eq ? s.M : 0);
+    f.dwd = f.dWe + (int64_t)s.H * s.FE;
+  }
   f.gw1 = grad_w1_msg; f.gw2 = grad_w2_msg; f.gw1m = grad_w1_mov; f.gw2m = grad_w2_mov;
   f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1;
   ProfScope ps(EGNN_K_WGRAD, st);

@@ -1,0 +1,751 @@
+// Workgroup-cooperative fused forward and backward of the EGNN/MPNN layer (bf16, gfx950).
+//
+// All W waves of a workgroup work on the same 32-edge tile; wave w owns rows
+// [w*D/W, (w+1)*D/W) of every feature dimension D (H, O, M).  Consequences:
+//  * each wave keeps the A-operand fragments of its weight rows in registers
+//    for the whole kernel (loaded once, never re-read from memory);
+//  * the elementwise work (SiLU, SiLU', bias, gathers of P_i/Q_j/gm_i) is
+//    split across the waves with no redundancy;
+//  * a stage's output passes to the next stage through a small chain-ordered
+//    LDS buffer: the writer stores its 16-row C-blocks as halves of 32-row
+//    chunks, every reader loads whole 16-byte chunks (the B operands of the
+//    next product, kappa_chain order);
+//  * the weight gradients dW_hl, dW1_mov and [dW_e | dw_d] accumulate in
+//    registers, each wave owning the rows of its slice: the row operand is the
+//    wave's own activation turned edge-major by one identity MFMA per block,
+//    the column operand is read from an edge-major LDS buffer written the same
+//    way by its owner.  Nothing per edge is written to memory for the weight
+//    gradients; each block writes one partial that a fixed-order sum reduces;
+//  * per-row sums of the forward are one more MFMA against the 0/1 matrix
+//    S[edge][row-rank] built from a ballot of row starts, so a tile may cover
+//    any number of rows; rows that cross a tile go through the carry fix-up.
+// Reference: forward_kernel.py:89-153 and backward_kernel.py:143-257 compute
+// the same quantities one program per CSR row.
+#include "egnn_device.h"
+#include "egnn_internal.h"
+
+namespace egnn {
+namespace {
+
+constexpr int TE = kTileEdges;  // 32 edges = two 16-column MFMA blocks
+
+__device__ __forceinline__ bf16x4 pack4(const f32x4& v) {
+  bf16x4 r;
+  r[0] = (bf16)v[0]; r[1] = (bf16)v[1]; r[2] = (bf16)v[2]; r[3] = (bf16)v[3];
+  return r;
+}
+__device__ __forceinline__ f32x4 unpack4(const bf16x4& v) {
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// chain buffer: chunk (kc, nb) = 64 lanes x 8 bf16; 16-row block blk fills half (blk & 1) of chunk blk >> 1
+__device__ __forceinline__ void put_chain(bf16* buf, int blk, int nb, int l, const f32x4& v) {
+  *reinterpret_cast<bf16x4*>(buf + (((blk >> 1) * 2 + nb) * 64 + l) * 8 + 4 * (blk & 1)) = pack4(v);
+}
+__device__ __forceinline__ bf16x8 get_chain(const bf16* buf, int kc, int nb, int l) {
+  return *reinterpret_cast<const bf16x8*>(buf + ((kc * 2 + nb) * 64 + l) * 8);
+}
+// edge-major buffer: feature block blk, lane (c = feature, g) holds 8 edges in kappa_chain order
+__device__ __forceinline__ void put_norm(bf16* buf, int blk, int l, const bf16x8& v) {
+  *reinterpret_cast<bf16x8*>(buf + (blk * 64 + l) * 8) = v;
+}
+__device__ __forceinline__ bf16x8 get_norm(const bf16* buf, int blk, int l) {
+  return *reinterpret_cast<const bf16x8*>(buf + (blk * 64 + l) * 8);
+}
+
+// B operand that transposes one 16-row C-block: B[s][n] = (s < 4 && 4g + s == n)
+__device__ __forceinline__ bf16x8 ident_chunk(int c, int g) {
+  bf16x8 r = zero_chunk<bf16>();
+  const int s = c - 4 * g;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) r[q] = (s == q) ? (bf16)1.0f : (bf16)0.0f;
+  return r;
+}
+// C-block (rows = 16 features, col = edge c) -> C-block (col = feature c, rows = edges 4g+i), bf16-rounded
+__device__ __forceinline__ f32x4 transpose_block(const f32x4& v, const bf16x8& I) {
+  bf16x8 a = zero_chunk<bf16>();
+  a[0] = (bf16)v[0]; a[1] = (bf16)v[1]; a[2] = (bf16)v[2]; a[3] = (bf16)v[3];
+  f32x4 t = zero4();
+  mma(t, a, I);
+  return t;
+}
+// edge-major chunk of a feature block over the 32 edges of the tile (kappa_chain over edges)
+__device__ __forceinline__ bf16x8 edge_major(const f32x4& nb0, const f32x4& nb1, const bf16x8& I) {
+  return pack_chunk<bf16>(transpose_block(nb0, I), transpose_block(nb1, I));
+}
+
+__device__ __forceinline__ int rank_of(uint32_t mask, int k) {
+  const uint32_t below = (k >= 31) ? 0xffffffffu : ((2u << k) - 1u);
+  return __popc(mask & below) - 1;
+}
+// B operand S[edge][rank]: column n = rank 16*rb + c, rows = edges kappa_chain(g, s)
+__device__ __forceinline__ bf16x8 seg_chunk(uint32_t mask, int nvalid, int rb, int c, int g) {
+  bf16x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int k = kappa_chain(g, s);
+    r[s] = (k < nvalid && rank_of(mask, k) == 16 * rb + c) ? (bf16)1.0f : (bf16)0.0f;
+  }
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int eid, int FE, int g, float r2, bool eq) {
+  const int slot0 = 8 * g;
+  if (slot0 + 8 <= FE) return load_chunk(ef + (int64_t)eid * se + slot0);
+  bf16x8 z = zero_chunk<bf16>();
+  if (eq && slot0 == FE) {
+    const bf16 hi = (bf16)r2;
+    z[0] = hi;
+    z[1] = (bf16)(r2 - (float)hi);
+  }
+  return z;
+}
+
+__device__ __forceinline__ uint32_t lo16(unsigned long long b) { return (uint32_t)(b & 0xffffull); }
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <int H, int O, int M, int W, bool EQ>
+__global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
+  constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
+  constexpr int KH = H / 32, KO = O / 32;
+  constexpr int SEGW = O + (EQ ? 4 : 0);
+  static_assert(BH >= 1 && BO >= 1 && BM >= 1, "slice smaller than one 16-row block");
+  __shared__ __attribute__((aligned(16))) bf16 s_m1[KH * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_m[KO * 2 * 64 * 8];
+  __shared__ float s_phi[W][TE];
+  __shared__ float s_d[TE][4];
+  __shared__ int s_rowof[TE];
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const bf16* PQ = (const bf16*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const int64_t E = a.E;
+  const int N = (int)a.N;
+
+  bf16x8 wu[BH], whlT[BO][KH], wmovT[EQ ? BM : 1][KO];
+  f32x4 b2v[BO], bx1v[BM], w2mv[BM];
+#pragma unroll
+  for (int j = 0; j < BH; ++j)
+    wu[j] = load_chunk((const bf16*)a.fr.u + (int64_t)(w * BH + j) * kFragElems + l * 8);
+#pragma unroll
+  for (int j = 0; j < BO; ++j) {
+#pragma unroll
+    for (int kc = 0; kc < KH; ++kc)
+      whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)(w * BO + j) * KH + kc) * kFragElems + l * 8);
+    b2v[j] = load4_f32(a.fr.b2f + 16 * (w * BO + j) + 4 * g);
+  }
+  if constexpr (EQ) {
+#pragma unroll
+    for (int j = 0; j < BM; ++j) {
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc)
+        wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)(w * BM + j) * KO + kc) * kFragElems + l * 8);
+      bx1v[j] = load4_f32(a.fr.bx1f + 16 * (w * BM + j) + 4 * g);
+      w2mv[j] = load4_f32(a.fr.w2mf + 16 * (w * BM + j) + 4 * g);
+    }
+  }
+  const bf16x8 I = ident_chunk(c, g);
+
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+    const int64_t base = t * TE;
+    const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
+    int ri[2], rj[2], eid[2];
+    float dx[2], dy[2], dz[2], r2[2];
+    bool nf[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = base + nb * 16 + c;
+      const bool valid = e < E;
+      const int64_t ec = valid ? e : E - 1;
+      ri[nb] = clampi(a.erow[ec], N);
+      rj[nb] = clampi(a.col[ec], N);
+      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
+      nf[nb] = valid && (e == base || a.erow[e - 1] != a.erow[e]);
+      dx[nb] = dy[nb] = dz[nb] = r2[nb] = 0.f;
+      if constexpr (EQ) {
+        const float* xi = a.coord + (int64_t)ri[nb] * a.sc;
+        const float* xj = a.coord + (int64_t)rj[nb] * a.sc;
+        dx[nb] = xi[0] - xj[0];
+        dy[nb] = xi[1] - xj[1];
+        dz[nb] = xi[2] - xj[2];
+        r2[nb] = dx[nb] * dx[nb] + dy[nb] * dy[nb] + dz[nb] * dz[nb];
+      }
+    }
+    const uint32_t mask = lo16(__ballot(nf[0])) | (lo16(__ballot(nf[1])) << 16);
+    const int nrank = __popc(mask);
+
+    // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
+    bf16x8 u[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], a.FE, g, r2[nb], EQ);
+#pragma unroll
+    for (int j = 0; j < BH; ++j) {
+      const int hb = w * BH + j;
+      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+        mma(acc, wu[j], u[nb]);
+        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
+        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        f32x4 x;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i] + p[i] + q[i]);
+        put_chain(s_m1, hb, nb, l, x);
+      }
+    }
+    if (w == 0 && g == 0) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const int k = nb * 16 + c;
+        if (nf[nb]) s_rowof[rank_of(mask, k)] = ri[nb];
+        if (EQ) { s_d[k][0] = dx[nb]; s_d[k][1] = dy[nb]; s_d[k][2] = dz[nb]; }
+      }
+    }
+    __syncthreads();
+
+    // ---- S2: m = SiLU(W_hl^T m1 + b2) for the wave's O rows; row sums -----
+    f32x4 mreg[BO][2];
+#pragma unroll
+    for (int j = 0; j < BO; ++j) {
+      const int ob = w * BO + j;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1, kc, nb, l));
+        f32x4 m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) m[i] = silu_t<bf16>(acc[i] + b2v[j][i]);
+        mreg[j][nb] = m;
+        if (EQ) put_chain(s_m, ob, nb, l, m);
+      }
+    }
+    const int rfirst = s_rowof[0];
+#pragma unroll
+    for (int j = 0; j < BO; ++j) {
+      const int ob = w * BO + j;
+      const bf16x8 A = edge_major(mreg[j][0], mreg[j][1], I);
+      for (int rb = 0; rb * 16 < nrank; ++rb) {
+        f32x4 D = zero4();
+        mma(D, A, seg_chunk(mask, nvalid, rb, c, g));
+        const int r = rb * 16 + c;
+        if (r < nrank) {
+          const int R = s_rowof[r];
+          const int rs = a.rowptr[R], re = a.rowptr[R + 1];
+          if (rs >= base && re <= base + TE) {
+            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)R * a.smsg + 16 * ob + 4 * g) = pack4(D);
+          } else {
+            const int slot = (R == rfirst) ? 0 : 1;
+            *reinterpret_cast<f32x4*>(a.carry + ((int64_t)t * 2 + slot) * SEGW + 16 * ob + 4 * g) = D;
+          }
+        }
+      }
+    }
+    if constexpr (EQ) {
+      __syncthreads();
+      // ---- S3: phi = SiLU(W1mov^T m + bx1) . w2mov (partial over the wave's M rows)
+      float phi[2] = {0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < BM; ++j) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[i] + bx1v[j][i]) * w2mv[j][i];
+        }
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        phi[nb] += shfl_xor(phi[nb], 16);
+        phi[nb] += shfl_xor(phi[nb], 32);
+        if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
+      }
+      __syncthreads();
+      // ---- coordinate sums: sum_j delta phi per row (hi + lo bf16 split) -----
+      if (w == W - 1) {
+        bf16x8 ahi = zero_chunk<bf16>(), alo = zero_chunk<bf16>();
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int k = kappa_chain(g, s);
+          float v = 0.f;
+          if (c < 3 && k < nvalid) {
+            float ph = 0.f;
+#pragma unroll
+            for (int ww = 0; ww < W; ++ww) ph += s_phi[ww][k];
+            v = s_d[k][c] * ph;
+          }
+          const bf16 hi = (bf16)v;
+          ahi[s] = hi;
+          alo[s] = (bf16)(v - (float)hi);
+        }
+        for (int rb = 0; rb * 16 < nrank; ++rb) {
+          const bf16x8 S = seg_chunk(mask, nvalid, rb, c, g);
+          f32x4 D = zero4();
+          mma(D, ahi, S);
+          mma(D, alo, S);
+          const int r = rb * 16 + c;
+          if (g == 0 && r < nrank) {
+            const int R = s_rowof[r];
+            const int rs = a.rowptr[R], re = a.rowptr[R + 1];
+            if (rs >= base && re <= base + TE) {
+              const float sc = a.mean ? 1.0f / (float)(re - rs) : 1.0f;
+              float* o = a.out_mov + (int64_t)R * a.smov;
+              o[0] = D[0] * sc;
+              o[1] = D[1] * sc;
+              o[2] = D[2] * sc;
+            } else {
+              const int slot = (R == rfirst) ? 0 : 1;
+              float* o = a.carry + ((int64_t)t * 2 + slot) * SEGW + O;
+              o[0] = D[0];
+              o[1] = D[1];
+              o[2] = D[2];
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward
+// ---------------------------------------------------------------------------
+template <int H, int O, int M, int W, bool EQ>
+__global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
+  constexpr int BH = H / W / 16, BO = O / W / 16, BM = EQ ? M / W / 16 : 1;
+  constexpr int KH = H / 32, KO = O / 32, KM = M / 32;
+  constexpr int NO = O / 16, NM = M / 16, NU = 2;  // edge-input slots: 32 (F_E + 2 <= 32)
+  // buffers whose live ranges do not overlap share storage:
+  //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5)
+  constexpr int CH1 = (KH > KO ? KH : KO) * 2 * 64 * 8, CH2 = ((EQ ? KO : 1) * 2 > NO ? (EQ ? KO : 1) * 2 : NO) * 64 * 8;
+  __shared__ __attribute__((aligned(16))) bf16 s_buf1[CH1];
+  __shared__ __attribute__((aligned(16))) bf16 s_buf2[CH2];
+  __shared__ __attribute__((aligned(16))) bf16 s_gq[(EQ ? KM : 1) * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_gqN[(EQ ? NM : 1) * 64 * 8];
+  // A-operand fragments of W1_mov (g_m) and W_hl (g_a1), read by their row owners
+  __shared__ __attribute__((aligned(16))) bf16 s_wmov[(EQ ? (O / 16) * KM : 1) * kFragElems];
+  __shared__ __attribute__((aligned(16))) bf16 s_whl[(H / 16) * KO * kFragElems];
+  bf16* const s_m1 = s_buf1;
+  bf16* const s_ga2 = s_buf1;
+  bf16* const s_m = s_buf2;
+  bf16* const s_ga2N = s_buf2;
+  __shared__ float s_phi[W][TE];
+  __shared__ float s_gr[W][TE];
+  __shared__ float s_r2[TE];
+  __shared__ int s_eid[TE];
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const bf16* PQ = (const bf16*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const bf16* gmsg = (const bf16*)a.gmsg;
+  bf16* Gh = (bf16*)a.Gh;
+  const int64_t E = a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+
+  bf16x8 wu[BH], whlT[BO][KH];
+  bf16x8 wmovT[BM][EQ ? KO : 1];
+  f32x4 b2v[BO], bx1v[BM], w2mv[BM], wdv[BH];
+  {
+    const int nthr = W * 64;
+    const int nwh = (H / 16) * KO * kFragElems / 8;
+    for (int q = threadIdx.x; q < nwh; q += nthr)
+      reinterpret_cast<bf16x8*>(s_whl)[q] = reinterpret_cast<const bf16x8*>(a.fr.hl)[q];
+    if constexpr (EQ) {
+      const int nwm = (O / 16) * KM * kFragElems / 8;
+      for (int q = threadIdx.x; q < nwm; q += nthr)
+        reinterpret_cast<bf16x8*>(s_wmov)[q] = reinterpret_cast<const bf16x8*>(a.fr.mov)[q];
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < BH; ++j) {
+    const int hb = w * BH + j;
+    wu[j] = load_chunk((const bf16*)a.fr.u + (int64_t)hb * kFragElems + l * 8);
+    wdv[j] = EQ ? load4_f32(a.fr.wdf + 16 * hb + 4 * g) : zero4();
+  }
+#pragma unroll
+  for (int j = 0; j < BO; ++j) {
+    const int ob = w * BO + j;
+#pragma unroll
+    for (int kc = 0; kc < KH; ++kc)
+      whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)ob * KH + kc) * kFragElems + l * 8);
+    b2v[j] = load4_f32(a.fr.b2f + 16 * ob + 4 * g);
+  }
+  if constexpr (EQ) {
+#pragma unroll
+    for (int j = 0; j < BM; ++j) {
+      const int mb = w * BM + j;
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc)
+        wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)mb * KO + kc) * kFragElems + l * 8);
+      bx1v[j] = load4_f32(a.fr.bx1f + 16 * mb + 4 * g);
+      w2mv[j] = load4_f32(a.fr.w2mf + 16 * mb + 4 * g);
+    }
+  }
+  const bf16x8 I = ident_chunk(c, g);
+
+  f32x4 acc_whl[BH][NO], acc_w1m[BO][EQ ? NM : 1], acc_wu[BH][NU];
+  f32x4 vb2[BO], vbx1[BM], vw2m[BM];
+#pragma unroll
+  for (int j = 0; j < BH; ++j) {
+#pragma unroll
+    for (int cb = 0; cb < NO; ++cb) acc_whl[j][cb] = zero4();
+#pragma unroll
+    for (int ub = 0; ub < NU; ++ub) acc_wu[j][ub] = zero4();
+  }
+#pragma unroll
+  for (int j = 0; j < BO; ++j) {
+    vb2[j] = zero4();
+#pragma unroll
+    for (int cb = 0; cb < (EQ ? NM : 1); ++cb) acc_w1m[j][cb] = zero4();
+  }
+#pragma unroll
+  for (int j = 0; j < BM; ++j) vbx1[j] = vw2m[j] = zero4();
+
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+    const int64_t base = t * TE;
+    const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
+    int ri[2], rj[2], eid[2];
+    bool valid[2];
+    float dx[2], dy[2], dz[2], r2[2], gxx[2], gxy[2], gxz[2], gphi[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = base + nb * 16 + c;
+      valid[nb] = e < E;
+      const int64_t ec = valid[nb] ? e : E - 1;
+      ri[nb] = clampi(a.erow[ec], N);
+      rj[nb] = clampi(a.col[ec], N);
+      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
+      dx[nb] = dy[nb] = dz[nb] = r2[nb] = gxx[nb] = gxy[nb] = gxz[nb] = gphi[nb] = 0.f;
+      if constexpr (EQ) {
+        const float* xi = a.coord + (int64_t)ri[nb] * a.sc;
+        const float* xj = a.coord + (int64_t)rj[nb] * a.sc;
+        dx[nb] = xi[0] - xj[0];
+        dy[nb] = xi[1] - xj[1];
+        dz[nb] = xi[2] - xj[2];
+        r2[nb] = dx[nb] * dx[nb] + dy[nb] * dy[nb] + dz[nb] * dz[nb];
+        if (valid[nb]) {
+          const float* gx = a.gmov + (int64_t)ri[nb] * a.sgx;
+          float sc = 1.0f;
+          if (a.mean) {
+            const int deg = a.rowptr[ri[nb] + 1] - a.rowptr[ri[nb]];
+            sc = 1.0f / (float)(deg > 1 ? deg : 1);
+          }
+          gxx[nb] = gx[0] * sc;
+          gxy[nb] = gx[1] * sc;
+          gxz[nb] = gx[2] * sc;
+        }
+        gphi[nb] = dx[nb] * gxx[nb] + dy[nb] * gxy[nb] + dz[nb] * gxz[nb];
+      }
+    }
+    if (w == 0 && g == 0) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        s_r2[nb * 16 + c] = r2[nb];
+        s_eid[nb * 16 + c] = valid[nb] ? eid[nb] : -1;
+      }
+    }
+
+    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
+    bf16x8 u[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], FE, g, r2[nb], EQ);
+    bf16x4 s1[BH][2];
+    bf16x8 m1N[BH];
+#pragma unroll
+    for (int j = 0; j < BH; ++j) {
+      const int hb = w * BH + j;
+      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+      f32x4 y[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+        mma(acc, wu[j], u[nb]);
+        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
+        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        f32x4 d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+          y[nb][i] = r.y;
+          d[i] = r.d;
+        }
+        s1[j][nb] = pack4(d);
+        put_chain(s_m1, hb, nb, l, y[nb]);
+      }
+      m1N[j] = edge_major(y[0], y[1], I);
+    }
+    __syncthreads();
+
+    // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
+    bf16x4 s2[BO][2];
+    bf16x8 mN[BO];
+#pragma unroll
+    for (int j = 0; j < BO; ++j) {
+      const int ob = w * BO + j;
+      f32x4 y[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1, kc, nb, l));
+        f32x4 d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const YD r = silu_yd<bf16>(acc[i] + b2v[j][i]);
+          y[nb][i] = r.y;
+          d[i] = r.d;
+        }
+        s2[j][nb] = pack4(d);
+        if (EQ) put_chain(s_m, ob, nb, l, y[nb]);
+      }
+      mN[j] = EQ ? edge_major(y[0], y[1], I) : zero_chunk<bf16>();
+    }
+    float phi[2] = {0.f, 0.f};
+    if constexpr (EQ) {
+      __syncthreads();
+      // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows --
+#pragma unroll
+      for (int j = 0; j < BM; ++j) {
+        const int mb = w * BM + j;
+        f32x4 gq[2];
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const YD r = silu_yd<bf16>(acc[i] + bx1v[j][i]);
+            phi[nb] += r.y * w2mv[j][i];
+            gq[nb][i] = gphi[nb] * w2mv[j][i] * r.d;
+            vw2m[j][i] += r.y * gphi[nb];
+            vbx1[j][i] += gq[nb][i];
+          }
+          put_chain(s_gq, mb, nb, l, gq[nb]);
+        }
+        put_norm(s_gqN, mb, l, edge_major(gq[0], gq[1], I));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        phi[nb] += shfl_xor(phi[nb], 16);
+        phi[nb] += shfl_xor(phi[nb], 32);
+        if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
+      }
+    }
+    __syncthreads();
+
+    // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
+#pragma unroll
+    for (int j = 0; j < BO; ++j) {
+      const int ob = w * BO + j;
+      f32x4 ga[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = valid[nb] ? load4_f32(gmsg + (int64_t)ri[nb] * a.sgm + 16 * ob + 4 * g) : zero4();
+        if constexpr (EQ) {
+#pragma unroll
+          for (int kc = 0; kc < KM; ++kc)
+            mma(acc, *reinterpret_cast<const bf16x8*>(s_wmov + ((ob * KM + kc) * 64 + l) * 8),
+                get_chain(s_gq, kc, nb, l));
+        }
+        const f32x4 d = unpack4(s2[j][nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ga[nb][i] = acc[i] * d[i];
+          vb2[j][i] += ga[nb][i];
+        }
+        put_chain(s_ga2, ob, nb, l, ga[nb]);
+      }
+      put_norm(s_ga2N, ob, l, edge_major(ga[0], ga[1], I));
+    }
+    if constexpr (EQ) {
+      // dW1_mov rows of this wave: sum_e m[o][e] g_q[m][e]
+#pragma unroll
+      for (int j = 0; j < BO; ++j)
+#pragma unroll
+        for (int cb = 0; cb < NM; ++cb) mma(acc_w1m[j][cb], mN[j], get_norm(s_gqN, cb, l));
+    }
+    __syncthreads();
+
+    // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1), the wave's H rows --------------
+    float gr[2] = {0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < BH; ++j) {
+      const int hb = w * BH + j;
+      f32x4 g1[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kc = 0; kc < KO; ++kc)
+          mma(acc, *reinterpret_cast<const bf16x8*>(s_whl + ((hb * KO + kc) * 64 + l) * 8),
+              get_chain(s_ga2, kc, nb, l));
+        const f32x4 d = unpack4(s1[j][nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          g1[nb][i] = acc[i] * d[i];
+          gr[nb] += wdv[j][i] * g1[nb][i];
+        }
+        if (valid[nb])
+          *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * hb + 4 * g) = pack4(g1[nb]);
+      }
+      const bf16x8 ga1N = edge_major(g1[0], g1[1], I);
+      // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e]
+#pragma unroll
+      for (int cb = 0; cb < NO; ++cb) mma(acc_whl[j][cb], m1N[j], get_norm(s_ga2N, cb, l));
+      // [dW_e | dw_d] rows of this wave: sum_e g_a1[h][e] U[slot][e]
+#pragma unroll
+      for (int ub = 0; ub < NU; ++ub) {
+        if (16 * ub >= FE + (EQ ? 2 : 0)) continue;   // column block of zero slots
+        const int slot = 16 * ub + c;
+        bf16x8 un;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const int k = kappa_chain(g, s);
+          float v = 0.f;
+          if (k < nvalid) {
+            if (slot < FE) v = (float)ef[(int64_t)s_eid[k] * a.se + slot];
+            else if (EQ && slot == FE) v = (float)(bf16)s_r2[k];
+            else if (EQ && slot == FE + 1) v = s_r2[k] - (float)(bf16)s_r2[k];
+          }
+          un[s] = (bf16)v;
+        }
+        mma(acc_wu[j][ub], ga1N, un);
+      }
+    }
+    if constexpr (EQ) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        gr[nb] += shfl_xor(gr[nb], 16);
+        gr[nb] += shfl_xor(gr[nb], 32);
+        if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
+      }
+      __syncthreads();
+      // ---- S6: dL/ddelta = phi gx + 2 g_r delta -------------------------------
+      if (w == 0 && g == 0) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          if (!valid[nb]) continue;
+          const int k = nb * 16 + c;
+          float grt = 0.f, pht = 0.f;
+#pragma unroll
+          for (int ww = 0; ww < W; ++ww) {
+            grt += s_gr[ww][k];
+            pht += s_phi[ww][k];
+          }
+          const float k2 = 2.0f * grt;
+          *reinterpret_cast<f32x4*>(a.Gx + (base + k) * 4) =
+              f32x4{pht * gxx[nb] + k2 * dx[nb], pht * gxy[nb] + k2 * dy[nb], pht * gxz[nb] + k2 * dz[nb], 0.f};
+        }
+      }
+    }
+    __syncthreads();
+  }
+
+  // ---- this block's weight-gradient partial ---------------------------------
+  float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
+  const int64_t oW1 = (int64_t)(H + 1) * O;
+  const int64_t oW2 = oW1 + (EQ ? (int64_t)(O + 1) * M : 0);
+  const int64_t oWE = oW2 + (EQ ? M : 0);
+  const int64_t oWD = oWE + (int64_t)H * FE;
+#pragma unroll
+  for (int j = 0; j < BH; ++j) {
+    const int hb = w * BH + j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 16 * hb + 4 * g + i;
+#pragma unroll
+      for (int cb = 0; cb < NO; ++cb) P[(int64_t)h * O + 16 * cb + c] = acc_whl[j][cb][i];
+#pragma unroll
+      for (int ub = 0; ub < NU; ++ub) {
+        const int slot = 16 * ub + c;
+        const float v = acc_wu[j][ub][i];
+        const float vn = shfl(v, (l & ~15) | ((c + 1) & 15));
+        if (slot < FE) P[oWE + (int64_t)h * FE + slot] = v;
+        else if (EQ && slot == FE) P[oWD + h] = v + vn;
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < BO; ++j) {
+    const int ob = w * BO + j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = vb2[j][i];
+      v += shfl_xor(v, 1); v += shfl_xor(v, 2); v += shfl_xor(v, 4); v += shfl_xor(v, 8);
+      if (c == 0) P[(int64_t)H * O + 16 * ob + 4 * g + i] = v;
+      if constexpr (EQ) {
+#pragma unroll
+        for (int cb = 0; cb < NM; ++cb) P[oW1 + (int64_t)(16 * ob + 4 * g + i) * M + 16 * cb + c] = acc_w1m[j][cb][i];
+      }
+    }
+  }
+  if constexpr (EQ) {
+#pragma unroll
+    for (int j = 0; j < BM; ++j) {
+      const int mb = w * BM + j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float v = vbx1[j][i], q = vw2m[j][i];
+        v += shfl_xor(v, 1); v += shfl_xor(v, 2); v += shfl_xor(v, 4); v += shfl_xor(v, 8);
+        q += shfl_xor(q, 1); q += shfl_xor(q, 2); q += shfl_xor(q, 4); q += shfl_xor(q, 8);
+        if (c == 0) {
+          P[oW1 + (int64_t)O * M + 16 * mb + 4 * g + i] = v;
+          P[oW2 + 16 * mb + 4 * g + i] = q;
+        }
+      }
+    }
+  }
+}
+
+template <int H, int O, int M, int W, bool EQ>
+int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
+  if (a.ntiles > 0) {
+    const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * 4);
+    hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ>), dim3(blocks), dim3(W * 64), 0, st, a);
+  }
+  return (int)hipGetLastError();
+}
+
+template <int H, int O, int M, int W, bool EQ>
+int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.ntiles > 0) hipLaunchKernelGGL((coop_bwd_kernel<H, O, M, W, EQ>), dim3(nblk), dim3(W * 64), 0, st, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace
+
+bool coop_supported(const LayerShape& s) {
+  const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);
+  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32;
+}
+
+int coop_bwd_blocks(const LayerShape& s) {
+  return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(s.E, TE), 256));
+}
+
+int64_t coop_dw_len(const LayerShape& s) {
+  return (int64_t)(s.H + 1) * s.O + (s.eq ? (int64_t)(s.O + 1) * s.M + s.M : 0) + (int64_t)s.H * s.FE +
+         (s.eq ? s.H : 0);
+}
+
+int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+  if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
+  return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
+}
+
+int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
+  if (s.H == 128)
+    return s.eq ? launch_bwd_t<128, 128, 128, 8, true>(a, nblk, st) : launch_bwd_t<128, 128, 128, 8, false>(a, nblk, st);
+  return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
+}
+
+}  // namespace egnn

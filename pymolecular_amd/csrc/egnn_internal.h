@@ -38,6 +38,8 @@ struct FragSet {
   float* b2f;  // [O]  fp32 copies of the small vectors
   float* bx1f; // [M]
   float* w2mf; // [M]
+  float* wdf;  // [H]  w_d in fp32 (EGNN only)
+  void* wn;    // [F][2H] activation dtype: [W_n1 | W_n2] side by side (node projections)
 };
 
 struct LayerShape {
@@ -74,6 +76,11 @@ struct BwdWs {
   float* dwd;      // H
   float* dWn;      // (F+1) x 2H  last row = [db1 | sum dQ]
   int64_t part_elems;
+  // workgroup-cooperative path: per-block partials of [dWhl | dW1m | dw2m | dWe | dwd] and their sum
+  float* dwpart;
+  float* dwsum;
+  int nblk;
+  int64_t LW;
 };
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
@@ -103,6 +110,20 @@ struct GemmArgs {
 };
 int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st);
 
+// Node-level GEMM with 16-byte loads along the contiguous dimension of each
+// operand.  A is (M x K) row-major ("k contiguous") or given as its transpose
+// (K x M row-major, "m contiguous"); B is (K x N) row-major ("n contiguous") or
+// (N x K) row-major ("k contiguous").  Row a_ones_row of A reads as all ones.
+struct Gemm2Args {
+  int64_t M, N, K;
+  const void* A; int64_t lda; int a_bf16; int a_kc; int64_t a_ones_row;
+  const void* B; int64_t ldb; int b_bf16; int b_nc;
+  const void* bias; int bias_bf16; int64_t bias_len;
+  void* C; int64_t ldc; int c_bf16; int perm_half;
+  float* partial; int64_t ksplit;
+};
+int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
+
 struct FwdArgs {
   int64_t N, E, ntiles;
   int FE, NUC, mean;
@@ -130,8 +151,17 @@ struct BwdArgs {
   const void* gmsg; int64_t sgm;
   const float* gmov; int64_t sgx;
   void* Dm1; void* Dm; void* Dgq; void* Dga2; void* Dp; void* Gh; float* Gx; float* R2;
+  float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
+  int64_t LW;
 };
 int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
+
+// Workgroup-cooperative fused kernels (bf16, H = 128 or H = 64 / O = M = 32, NUC = 1).
+bool coop_supported(const LayerShape& s);
+int coop_bwd_blocks(const LayerShape& s);
+int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
+int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
+int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
 int bwd_tile_edges(const LayerShape& s);
 
 // dPQ[n] = [sum_row Gh | sum_csc Gh] (fp32); grad_coord = sum_row Gx - sum_csc Gx

@@ -47,6 +47,8 @@ static size_t frag_layout(const LayerShape& s, char* base, FragSet* f, size_t of
   f->b2f = (float*)take(sizeof(float) * s.O);
   f->bx1f = (float*)take(sizeof(float) * (s.M + 4));
   f->w2mf = (float*)take(sizeof(float) * (s.M + 4));
+  f->wdf = (float*)take(sizeof(float) * s.H);
+  f->wn = take((size_t)s.F * 2 * s.H * s.esz);
   return off;
 }
 
@@ -69,20 +71,25 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   size_t off = frag_layout(s, b, &w->fr, 0, true);
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
   const size_t E = (size_t)std::max<int64_t>(s.E, 1);
+  const bool coop = coop_supported(s);
   w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
-  w->Dm1 = take(E * s.H * s.esz);
-  w->Dm = take(E * s.O * s.esz);
-  w->Dgq = s.eq ? take(E * s.M * s.esz) : nullptr;
-  w->Dga2 = take(E * s.O * s.esz);
-  w->Dp = s.eq ? take(E * s.M * s.esz) : nullptr;
+  w->Dm1 = coop ? nullptr : take(E * s.H * s.esz);
+  w->Dm = coop ? nullptr : take(E * s.O * s.esz);
+  w->Dgq = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
+  w->Dga2 = coop ? nullptr : take(E * s.O * s.esz);
+  w->Dp = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
   w->Gh = take(E * s.H * s.esz);
   w->Gx = (float*)take(E * 4 * sizeof(float));
-  w->R2 = (float*)take(E * sizeof(float));
+  w->R2 = coop ? nullptr : (float*)take(E * sizeof(float));
+  w->nblk = coop ? coop_bwd_blocks(s) : 0;
+  w->LW = coop ? coop_dw_len(s) : 0;
+  w->dwpart = coop ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
+  w->dwsum = coop ? (float*)take((size_t)w->LW * sizeof(float)) : nullptr;
   w->dPQ = (float*)take((size_t)s.N * 2 * s.H * sizeof(float));
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
   int64_t se = cdiv(std::max<int64_t>(s.E, 1), splitk_len(s.E)), sn = cdiv(s.N, splitk_len(s.N));
-  int64_t pe = std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
-                                  (int64_t)s.H * std::max(s.FE, 1), (int64_t)s.H});
+  int64_t pe = coop ? 0 : std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
+                                             (int64_t)s.H * std::max(s.FE, 1), (int64_t)s.H});
   w->part_elems = std::max<int64_t>(se * pe, sn * (int64_t)(s.F + 1) * 2 * s.H);
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
@@ -137,12 +144,23 @@ __global__ void frag_build_kernel(FragDesc d, int F, int FE, int H, int eq) {
 }
 
 template <typename T>
-__global__ void vec_prep_kernel(const T* b2, const T* bx1, const T* w2m, float* b2f, float* bx1f, float* w2mf, int O, int M) {
+__global__ void vec_prep_kernel(const T* b2, const T* bx1, const T* w2m, const T* wd, float* b2f, float* bx1f,
+                                float* w2mf, float* wdf, int O, int M, int H) {
   int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t < O) b2f[t] = b2 ? to_f32(b2[t]) : 0.0f;
+  if (t < H) wdf[t] = wd ? to_f32(wd[t]) : 0.0f;
   if (t < M + 4) {
     bx1f[t] = (bx1 && t < M) ? to_f32(bx1[t]) : 0.0f;
     w2mf[t] = (w2m && t < M) ? to_f32(w2m[t]) : 0.0f;
+  }
+}
+
+template <typename T>
+__global__ void wn_prep_kernel(const T* __restrict__ w1, T* __restrict__ wn, int F, int H) {
+  const int64_t total = (int64_t)F * 2 * H;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t f = t / (2 * H), n = t % (2 * H);
+    wn[t] = n < H ? w1[f * H + n] : w1[(F + f) * H + (n - H)];
   }
 }
 
@@ -164,10 +182,16 @@ static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const 
     build(fr.hl, s.H, s.O, FK_W, 1, w2, s.O);               // A[h][o] = W_hl[h][o]
     if (s.eq) build(fr.uT, 16, s.H, FK_UT, 1, w1, s.H);
   }
-  int n = std::max(s.O, s.M + 4);
+  {
+    const int64_t tot = (int64_t)s.F * 2 * s.H;
+    hipLaunchKernelGGL(wn_prep_kernel<T>, dim3((unsigned)std::min<int64_t>(cdiv(tot, 256), 2048)), dim3(256), 0, st,
+                       (const T*)w1, (T*)fr.wn, s.F, s.H);
+  }
+  int n = std::max({s.O, s.M + 4, s.H});
+  const T* wd = s.eq ? (const T*)w1 + (int64_t)(2 * s.F) * s.H : nullptr;
   hipLaunchKernelGGL(vec_prep_kernel<T>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const T*)b2,
-                     (const T*)(s.eq ? bx1 : nullptr), (const T*)(s.eq ? w2m : nullptr), fr.b2f, fr.bx1f, fr.w2mf,
-                     s.O, s.M);
+                     (const T*)(s.eq ? bx1 : nullptr), (const T*)(s.eq ? w2m : nullptr), wd, fr.b2f, fr.bx1f,
+                     fr.w2mf, fr.wdf, s.O, s.M, s.H);
   return (int)hipGetLastError();
 }
 
@@ -180,6 +204,8 @@ int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void*
 // ---------------------------------------------------------------------------
 // generic MFMA GEMM (64 x 64 tile per 4-wave block, k step 32)
 // ---------------------------------------------------------------------------
+__device__ __forceinline__ int ce_minus(const int32_t* p, int64_t n) { return p[n + 1] - p[n]; }
+
 __device__ __forceinline__ float ld_elem(const void* p, int64_t off, int is_bf16) {
   return is_bf16 ? (float)((const bf16*)p)[off] : ((const float*)p)[off];
 }
@@ -269,43 +295,241 @@ int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------------------
+// node-level GEMM with vector loads (64 x 64 tile per 4-wave block, k step 32)
+// ---------------------------------------------------------------------------
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16> { typedef bf16x8 type; };
+template <> struct Vec16<float> { typedef f32x4 type; };
+template <typename T> __device__ __forceinline__ typename Vec16<T>::type ld16(const T* p) {
+  return *reinterpret_cast<const typename Vec16<T>::type*>(p);
+}
+
+// Operand pointers and leading dimensions are 16-byte aligned (checked by the caller).
+template <typename TA, typename TB, typename TC, bool A_KC, bool B_NC>
+__global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
+  constexpr int BM = 64, BN = 64, BK = 32, PAD = sizeof(TC) == 2 ? 8 : 4, LDK = BK + PAD;
+  constexpr int VA = 16 / sizeof(TA), VB = 16 / sizeof(TB);
+  __shared__ __attribute__((aligned(16))) TC As[BM * LDK];
+  __shared__ __attribute__((aligned(16))) TC Bs[BN * LDK];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
+  int64_t kbeg = 0, kend = g.K;
+  if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
+  const TA* A = (const TA*)g.A;
+  const TB* B = (const TB*)g.B;
+  f32x4 acc[2][2];
+  for (int a = 0; a < 2; ++a) for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    // ---- A tile -> As[m][k]
+    constexpr int NVA = BM * BK / VA;
+    for (int v = tid; v < NVA; v += 256) {
+      if constexpr (A_KC) {   // A[m * lda + k]
+        const int mm = v / (BK / VA), kk = (v % (BK / VA)) * VA;
+        const int64_t m = m0 + mm, k = k0 + kk;
+        TC* dst = &As[mm * LDK + kk];
+        if (m < g.M && k + VA <= kend && m != g.a_ones_row) {
+          const auto vv = ld16(A + m * g.lda + k);
+#pragma unroll
+          for (int u = 0; u < VA; ++u) dst[u] = from_f32<TC>((float)vv[u]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < VA; ++u) {
+            float x = 0.f;
+            if (m < g.M && k + u < kend) x = (m == g.a_ones_row) ? 1.0f : to_f32(A[m * g.lda + k + u]);
+            dst[u] = from_f32<TC>(x);
+          }
+        }
+      } else {                // A[k * lda + m]
+        const int kk = v / (BM / VA), mm = (v % (BM / VA)) * VA;
+        const int64_t k = k0 + kk, m = m0 + mm;
+        const bool full = k < kend && m + VA <= g.M && !(g.a_ones_row >= m && g.a_ones_row < m + VA);
+        if (full) {
+          const auto vv = ld16(A + k * g.lda + m);
+#pragma unroll
+          for (int u = 0; u < VA; ++u) As[(mm + u) * LDK + kk] = from_f32<TC>((float)vv[u]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < VA; ++u) {
+            float x = 0.f;
+            if (k < kend && m + u < g.M) x = (m + u == g.a_ones_row) ? 1.0f : to_f32(A[k * g.lda + m + u]);
+            As[(mm + u) * LDK + kk] = from_f32<TC>(x);
+          }
+        }
+      }
+    }
+    // ---- B tile -> Bs[n][k]
+    constexpr int NVB = BN * BK / VB;
+    for (int v = tid; v < NVB; v += 256) {
+      if constexpr (B_NC) {   // B[k * ldb + n]
+        const int kk = v / (BN / VB), nn = (v % (BN / VB)) * VB;
+        const int64_t k = k0 + kk, n = n0 + nn;
+        const bool full = k < kend && n + VB <= g.N;
+        if (full) {
+          const auto vv = ld16(B + k * g.ldb + n);
+#pragma unroll
+          for (int u = 0; u < VB; ++u) Bs[(nn + u) * LDK + kk] = from_f32<TC>((float)vv[u]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < VB; ++u) {
+            float x = 0.f;
+            if (k < kend && n + u < g.N) x = to_f32(B[k * g.ldb + n + u]);
+            Bs[(nn + u) * LDK + kk] = from_f32<TC>(x);
+          }
+        }
+      } else {                // B[n * ldb + k]
+        const int nn = v / (BK / VB), kk = (v % (BK / VB)) * VB;
+        const int64_t n = n0 + nn, k = k0 + kk;
+        TC* dst = &Bs[nn * LDK + kk];
+        if (n < g.N && k + VB <= kend) {
+          const auto vv = ld16(B + n * g.ldb + k);
+#pragma unroll
+          for (int u = 0; u < VB; ++u) dst[u] = from_f32<TC>((float)vv[u]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < VB; ++u) {
+            float x = 0.f;
+            if (n < g.N && k + u < kend) x = to_f32(B[n * g.ldb + k + u]);
+            dst[u] = from_f32<TC>(x);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    typedef typename ChunkOf<TC>::type Ch;
+    Ch a[2], b[2];
+    for (int i = 0; i < 2; ++i) {
+      a[i] = load_chunk(&As[(wm * 32 + i * 16 + c) * LDK + 8 * gq]);
+      b[i] = load_chunk(&Bs[(wn * 32 + i * 16 + c) * LDK + 8 * gq]);
+    }
+    for (int i = 0; i < 2; ++i)
+      for (int j = 0; j < 2; ++j) mma(acc[i][j], a[i], b[j]);
+    __syncthreads();
+  }
+  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 2; ++j)
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * 32 + i * 16 + 4 * gq + r;
+        const int64_t n = n0 + wn * 32 + j * 16 + c;
+        if (m >= g.M || n >= g.N) continue;
+        float v = acc[i][j][r];
+        if (g.partial) {
+          g.partial[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
+          continue;
+        }
+        if (g.bias && n < g.bias_len) v += ld_elem(g.bias, n, g.bias_bf16);
+        int64_t pn = n;
+        if (g.perm_half > 0) {
+          const int64_t half = n / g.perm_half, f = n % g.perm_half;
+          pn = half * g.perm_half + (f & ~31) + chain_pos((int)(f & 31));
+        }
+        if (g.c_bf16) ((bf16*)g.C)[m * g.ldc + pn] = (bf16)v;
+        else ((float*)g.C)[m * g.ldc + pn] = v;
+      }
+}
+
+template <typename TA, typename TB, typename TC>
+static void gemm2_dispatch(const Gemm2Args& g, dim3 grid, hipStream_t st) {
+  if (g.a_kc && g.b_nc) hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, true, true>), grid, dim3(256), 0, st, g);
+  else if (g.a_kc) hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, true, false>), grid, dim3(256), 0, st, g);
+  else if (g.b_nc) hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, false, true>), grid, dim3(256), 0, st, g);
+  else hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, false, false>), grid, dim3(256), 0, st, g);
+}
+
+int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
+  if (g.M <= 0 || g.N <= 0) return 0;
+  const unsigned gz = g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
+  const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
+  if (compute_bf16) {
+    if (g.a_bf16 && g.b_bf16) gemm2_dispatch<bf16, bf16, bf16>(g, grid, st);
+    else if (g.a_bf16) gemm2_dispatch<bf16, float, bf16>(g, grid, st);
+    else if (g.b_bf16) gemm2_dispatch<float, bf16, bf16>(g, grid, st);
+    else gemm2_dispatch<float, float, bf16>(g, grid, st);
+  } else {
+    if (g.a_bf16 || g.b_bf16) return (int)hipErrorInvalidValue;
+    gemm2_dispatch<float, float, float>(g, grid, st);
+  }
+  return (int)hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
 // node gradient reduction: one wave per node
 // ---------------------------------------------------------------------------
+// One wave per node.  Each edge row of Gh (H values) is read as 16-byte vectors
+// by LPE = H*sizeof(T)/16 lanes, so one wave-wide load covers EPW = 64/LPE
+// edges; the EPW partial sums are combined with lane shuffles at the end, in a
+// fixed order, so the result does not depend on timing.
 template <typename T, int H>
 __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ Gh, const float* __restrict__ Gx,
                                                           const int32_t* __restrict__ rowptr,
                                                           const int32_t* __restrict__ csc_ptr,
                                                           const int32_t* __restrict__ csc_eid, float* __restrict__ dPQ,
                                                           float* __restrict__ gcoord, int64_t sgc, int64_t N, int eq) {
-  constexpr int PER = (H + 63) / 64;
+  constexpr int VPL = 16 / sizeof(T);          // values per lane per load
+  constexpr int LPE = H / VPL;                 // lanes per edge row
+  constexpr int EPW = 64 / LPE;                // edges per wave-wide load
+  static_assert(LPE >= 1 && LPE <= 64 && 64 % LPE == 0, "row width");
   const int l = threadIdx.x & 63;
+  const int sub = l / LPE, q = l % LPE;
   const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
   for (int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); n < N; n += nw) {
-    float ap[PER], aq[PER];
-    for (int u = 0; u < PER; ++u) { ap[u] = 0.f; aq[u] = 0.f; }
+    float ap[VPL], aq[VPL];
+#pragma unroll
+    for (int u = 0; u < VPL; ++u) ap[u] = aq[u] = 0.f;
     float ax = 0.f;
     const int rs = rowptr[n], re = rowptr[n + 1];
-    for (int e = rs; e < re; ++e) {
-      const T* row = Gh + (int64_t)e * H;
-      for (int u = 0; u < PER; ++u) { int p = l + 64 * u; if (p < H) ap[u] += to_f32(row[p]); }
-      if (eq && l < 3) ax += Gx[(int64_t)e * 4 + l];
-    }
-    const int cs = csc_ptr[n], ce = csc_ptr[n + 1];
-    for (int k = cs; k < ce; ++k) {
-      const int e = csc_eid[k];
-      const T* row = Gh + (int64_t)e * H;
-      for (int u = 0; u < PER; ++u) { int p = l + 64 * u; if (p < H) aq[u] += to_f32(row[p]); }
-      if (eq && l < 3) ax -= Gx[(int64_t)e * 4 + l];
-    }
-    float* out = dPQ + n * 2 * H;
-    for (int u = 0; u < PER; ++u) {
-      int p = l + 64 * u;
-      if (p < H) {
-        out[p] = ap[u];
-        out[H + p] = aq[u];
+    for (int e0 = rs; e0 < re; e0 += EPW) {
+      const int e = e0 + sub;
+      if (e < re) {
+        const T* row = Gh + (int64_t)e * H + q * VPL;
+        if constexpr (sizeof(T) == 2) {
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(row);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) ap[u] += (float)v[u];
+        } else {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(row);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) ap[u] += v[u];
+        }
+        if (eq && q < 3) ax += Gx[(int64_t)e * 4 + q];
       }
     }
+    for (int k0 = 0; k0 < ce_minus(csc_ptr, n); k0 += EPW) {
+      const int k = csc_ptr[n] + k0 + sub;
+      if (k < csc_ptr[n + 1]) {
+        const int e = csc_eid[k];
+        const T* row = Gh + (int64_t)e * H + q * VPL;
+        if constexpr (sizeof(T) == 2) {
+          const bf16x8 v = *reinterpret_cast<const bf16x8*>(row);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) aq[u] += (float)v[u];
+        } else {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(row);
+#pragma unroll
+          for (int u = 0; u < VPL; ++u) aq[u] += v[u];
+        }
+        if (eq && q < 3) ax -= Gx[(int64_t)e * 4 + q];
+      }
+    }
+    // combine the EPW edge groups (lanes q, q + LPE, q + 2 LPE, ...) in a fixed order
+#pragma unroll
+    for (int off = LPE; off < 64; off <<= 1) {
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        ap[u] += shfl_xor(ap[u], off);
+        aq[u] += shfl_xor(aq[u], off);
+      }
+      ax += shfl_xor(ax, off);
+    }
     if (eq && l < 3) gcoord[n * sgc + l] = ax;
+    if (sub == 0) {
+      float* out = dPQ + n * 2 * H + q * VPL;
+#pragma unroll
+      for (int u = 0; u < VPL; ++u) {
+        out[u] = ap[u];
+        out[H + u] = aq[u];
+      }
+    }
   }
 }
 
@@ -327,17 +551,34 @@ int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, con
 // ---------------------------------------------------------------------------
 // fixed-order partial sums and gradient scatter
 // ---------------------------------------------------------------------------
-__global__ void sum_rows_kernel(const float* __restrict__ part, int64_t nrows, int64_t L, float* __restrict__ out) {
-  for (int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; l < L; l += (int64_t)gridDim.x * blockDim.x) {
-    float acc = 0.f;
-    for (int64_t b = 0; b < nrows; ++b) acc += part[b * L + l];
-    out[l] = acc;
+// out[l] = sum_b part[b][l].  A block covers 64 columns with 4 row groups;
+// group r sums rows r, r+4, r+8, ... and the 4 group sums are added in order,
+// so the result is the same on every run.
+__global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ part, int64_t nrows, int64_t L,
+                                                       float* __restrict__ out) {
+  __shared__ float red[4][64];
+  const int cx = threadIdx.x & 63, r = threadIdx.x >> 6;
+  for (int64_t l0 = (int64_t)blockIdx.x * 64; l0 < L; l0 += (int64_t)gridDim.x * 64) {
+    const int64_t l = l0 + cx;
+    float a0 = 0.f, a1 = 0.f;
+    if (l < L) {
+      int64_t b = r;
+      for (; b + 4 < nrows; b += 8) {
+        a0 += part[b * L + l];
+        a1 += part[(b + 4) * L + l];
+      }
+      if (b < nrows) a0 += part[b * L + l];
+    }
+    red[r][cx] = a0 + a1;
+    __syncthreads();
+    if (r == 0 && l < L) out[l] = ((red[0][cx] + red[1][cx]) + red[2][cx]) + red[3][cx];
+    __syncthreads();
   }
 }
 
 int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st) {
   if (L <= 0) return 0;
-  int blocks = (int)std::min<int64_t>(cdiv(L, 256), 2048);
+  int blocks = (int)std::min<int64_t>(cdiv(L, 64), 4096);
   hipLaunchKernelGGL(sum_rows_kernel, dim3(blocks), dim3(256), 0, st, part, nrows, L, out);
   return (int)hipGetLastError();
 }

@@ -159,8 +159,12 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
 
 def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
                        w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
-                       equivariant: bool = True):
-    """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``."""
+                       equivariant: bool = True, node_proj: Optional[torch.Tensor] = None):
+    """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``.
+
+    ``node_proj`` (uint8 device buffer of ``egnn_node_proj_bytes``): when given,
+    receives the per-node projections so that a following backward can reuse them.
+    """
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
     dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg)
@@ -180,16 +184,20 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     rc = L.egnn_fwd(dims, strides, _ptr(h), _ptr(coord) if equivariant else None, _ptr(edge_feat),
                     _ptr(row_ptrs.contiguous()), _ptr(col_indices.contiguous()), _ptr(eids), _ptr(w1), _ptr(w2),
                     _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
-                    _ptr(bx1) if equivariant else None, _ptr(out_msg), _ptr(out_mov), sched.buf.data_ptr(),
-                    ws.data_ptr(), ws_bytes, _stream(dev))
+                    _ptr(bx1) if equivariant else None, _ptr(out_msg), _ptr(out_mov), _ptr(node_proj),
+                    sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
     check("egnn_fwd", rc)
     return out_msg, out_mov
 
 
 def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                         b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
-                        equivariant: bool = True):
-    """Backward by recomputation.  Returns a dict of gradients (None where absent)."""
+                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None):
+    """Backward by recomputation.  Returns a dict of gradients (None where absent).
+
+    ``node_proj``: the buffer a forward with the same inputs filled (skips the
+    per-node projection GEMM), or None.
+    """
     w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
@@ -223,12 +231,19 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
                     _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
                     _ptr(bx1) if equivariant else None, _ptr(gm), _ptr(gx), _ptr(grad_h), _ptr(grad_coord),
                     _ptr(g_w1), _ptr(g_w2), _ptr(g_w1m), _ptr(g_w2m), _ptr(g_b1), _ptr(g_b2), _ptr(g_bx1),
-                    sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
+                    _ptr(node_proj), sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
     check("egnn_bwd", rc)
     if g_w2m is not None and w2m_shape is not None:
         g_w2m = g_w2m.reshape(w2m_shape)
     return dict(h=grad_h, coord=grad_coord, w1_msg=g_w1, w2_msg=g_w2, w1_mov=g_w1m, w2_mov=g_w2m, b1=g_b1,
                 b2=g_b2, bx1=g_bx1)
+
+
+def _node_proj_buffer(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg):
+    ef = None if (edge_feat is None or edge_feat.shape[1] == 0) else edge_feat
+    dims = _dims(h, ef, col, w1, w2, w1m, equivariant, mean_agg)
+    n = _capi.lib().egnn_node_proj_bytes(dims)
+    return torch.empty(max(n, 16), dtype=torch.uint8, device=h.device)
 
 
 class EGNNFusedFn(torch.autograd.Function):
@@ -242,11 +257,12 @@ class EGNNFusedFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                 b1=None, b2=None, bx1=None, mean_agg=False, equivariant=True):
+        pq = _node_proj_buffer(h, edge_feat, col_indices, w1_msg, w2_msg, w1_mov, equivariant, mean_agg)
         out_msg, out_mov = egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg,
                                               w2_msg, w1_mov, w2_mov, b1, b2, bx1, mean_agg=mean_agg,
-                                              equivariant=equivariant)
+                                              equivariant=equivariant, node_proj=pq)
         ctx.save_for_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov,
-                              w2_mov, b1, b2, bx1)
+                              w2_mov, b1, b2, bx1, pq)
         ctx.mean_agg = mean_agg
         ctx.equivariant = equivariant
         ctx.coord_shape = None if coord is None else tuple(coord.shape)
@@ -256,13 +272,14 @@ class EGNNFusedFn(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_msg, g_mov):
-        (h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1) = ctx.saved_tensors
+        (h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1, pq) = ctx.saved_tensors
         if g_msg is None:
             g_msg = torch.zeros((h.shape[0], w2.shape[1]), dtype=h.dtype, device=h.device)
         if g_mov is None:
             g_mov = torch.zeros((h.shape[0], 3), dtype=torch.float32, device=h.device)
         g = egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2,
-                                bx1, g_msg, g_mov, mean_agg=ctx.mean_agg, equivariant=ctx.equivariant)
+                                bx1, g_msg, g_mov, mean_agg=ctx.mean_agg, equivariant=ctx.equivariant,
+                                node_proj=pq)
         gc = g["coord"]
         if gc is not None and ctx.coord_shape is not None and ctx.coord_shape[1] != 3:
             full = torch.zeros(ctx.coord_shape, dtype=torch.float32, device=gc.device)

@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_entry_points():
     L = _capi.lib()
-    assert L.egnn_abi_version() == 1
+    assert L.egnn_abi_version() == 2
     assert _capi.status_string(0) == "ok"
     assert "CSR" in _capi.status_string(6)
     assert L.egnn_schedule_bytes(100, 1000) > 4 * 1000
@@ -51,9 +51,9 @@ def test_bad_arguments_return_status_not_crash():
     d = _capi.EgnnDims(N=10, E=20, F=128, FE=0, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=0)
     s = _capi.EgnnStrides(h=128, coord=3, edge=0, msg=128, mov=3)
     # NULL inputs are reported before anything touches the device
-    rc = L.egnn_fwd(d, s, *([None] * 17), 0, None)
+    rc = L.egnn_fwd(d, s, *([None] * 18), 0, None)
     assert rc == 1
     s_bad = _capi.EgnnStrides(h=16, coord=3, edge=0, msg=128, mov=3)
-    assert L.egnn_fwd(d, s_bad, *([None] * 17), 0, None) == 3
+    assert L.egnn_fwd(d, s_bad, *([None] * 18), 0, None) == 3
     assert L.egnn_schedule_build(None, None, 10, 20, None, 0, None, 0, None) == 1
     assert L.egnn_schedule_build(1, 1, 0, 20, 1, 0, 1, 0, None) == 2
