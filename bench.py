@@ -1,28 +1,35 @@
 #!/usr/bin/env python
-"""Throughput of the fused EGNN layer, forward + backward, on one MI355X.
+"""Throughput of the fused EGNN/MPNN layer, forward + backward, on one MI355X.
 
-Workload (default): 1024 fully connected molecules (9..29 atoms, seeds
-1002/2002/3002; N = 19,363, E = 383,714), an EGNN stack of 4 E_GCL layers at
-H = 128 (embedding_in 5 -> 128, embedding_out 128 -> 128), forward + backward
-of the sum-of-outputs loss sum(h_out) + sum(x_out) w.r.t. all parameters, no
-optimizer (the metric is the layer's fwd+bwd).  bf16 activations and weights
-with fp32 accumulation by default (``--dtype fp32`` for the fp32 run).
+Default workload: 1024 fully connected molecules (9..29 atoms; N = 19,363,
+E = 383,714), an EGNN stack of 4 E_GCL layers at H = 128 (embedding_in 5 ->
+128, embedding_out 128 -> 128), forward + backward of the sum-of-outputs loss
+sum(h_out) + sum(x_out) w.r.t. all parameters.  bf16 activations and weights
+with fp32 accumulation (``--dtype fp32`` for the fp32 run).  ``--workload k``
+selects the other workloads (1 molecules-128 fp32 1 layer, 3 proteins kNN-30
+with 16 RBFs, 4 slabs H = 256 with 32 RBFs, 5 power-law MPNN 2M nodes).
 
-value = E * layers / t_step (edges per second through the fused layer, whole
-stack timed: fused kernels, per-node GEMMs, node MLPs and autograd glue).
-Inputs are resident in HBM before the timed region.
+value = E * layers / t_step: edges per second through the fused layer, whole
+stack timed (fused kernels, per-node GEMMs, node MLPs, autograd glue), inputs
+resident in HBM before the timed region.
 
-roofline: the dominant kernel class of one step (measured with HIP events on
-the stream the kernels run on, through the library's instrumentation hook),
-its algorithmic work per launch, and the MI355X peak of its bound.
+roofline: the dominant kernel class of one step, timed with HIP events on
+the stream its kernels run on (the library's instrumentation hook), its
+algorithmic work per launch (MFMA FLOPs of the products it must execute;
+HBM bytes with every gathered row counted once per edge) and the MI355X peak
+of whichever of the two bounds it.  ``traffic`` is the measured HBM bytes per
+launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/
+when one exists for this workload and dtype, else null.
 cpu_baseline: the torch-eager CPU restatement (oracle/torch_ref.py) of the
-same stack in fp32 on a bounded prefix of the molecules, on this host's cores.
+same stack in fp32 on a bounded sample of the same workload, on this host's
+cores.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import re
 import statistics
 import sys
 import time
@@ -34,6 +41,13 @@ sys.path.insert(0, ROOT)
 
 METRIC = "edges/sec fused EGNN layer fwd+bwd; % of MFMA / HBM roofline achieved"
 PEAK = {"bf16_mfma_tflops": 2516.6, "fp32_mfma_tflops": 157.3, "hbm_gbs": 8000.0}
+DESCR = {
+    1: "molecules-128: 1 x E_GCL, H=128, fully connected molecules (9..29 atoms), F_E=0",
+    2: "molecules-1024: 4 x E_GCL, H=128, fully connected molecules (9..29 atoms), F_E=0",
+    3: "proteins-64x512: 4 x E_GCL, H=128, kNN-30 chains, F_E=16 RBF",
+    4: "slabs-256x80: 6 x E_GCL, H=256, radius 6 A capped at 50, F_E=32 RBF",
+    5: "powerlaw-2M: 2 x MPNN layer, H=128, power-law in-degree (alpha 2.1, 2..4096), F_E=16",
+}
 
 
 def parse():
@@ -41,43 +55,106 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--dtype", choices=["bf16", "fp32"], default="bf16")
-    ap.add_argument("--cpu-graphs", type=int, default=512, help="molecules in the CPU-baseline sample")
+    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--dtype", choices=["bf16", "fp32"], default=None,
+                    help="default: bf16, except fp32 for the one-layer molecules-128 workload")
+    ap.add_argument("--cpu-edges", type=int, default=200_000, help="edge budget of the CPU-baseline sample")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="end with three 256 MiB device copies (scale reference for HBM byte counters)")
     return ap.parse_args()
 
 
-def per_edge_work(H, O, M, FE, g, s):
-    """Algorithmic MFMA FLOPs and HBM bytes per edge of the fused kernels."""
-    fwd_flops = 2 * (H * O + g * O * M) + 2 * (g + FE) * H
-    bwd_flops = 4 * (H * O + g * O * M) + 2 * (g + FE) * H + 2 * g * H
-    gather = 2 * H * s + 8 + g * 24 + FE * s          # P_i, Q_j, erow/col, x_i/x_j, e
-    fwd_bytes = gather                                   # row sums stay on chip
-    bwd_bytes = gather + O * s + g * 12 + (2 * H + 2 * O + 2 * g * M) * s + g * 20   # + gm_i, gx_i, stores
-    model_fwd = 2 * ((2 * H + g + FE) * H + H * O + g * (O * M + M))
-    return dict(fwd_flops=fwd_flops, bwd_flops=bwd_flops, fwd_bytes=fwd_bytes, bwd_bytes=bwd_bytes,
-                model_fwdbwd=3 * model_fwd)
+def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
+    """Algorithmic (MFMA FLOPs, HBM bytes) of one launch of a kernel class.
+
+    FLOPs count the products the kernel must execute (identity transposes and
+    segment-sum products are overhead, not work).  Bytes count every gathered
+    row once per edge: P_i, Q_j (H each), col and row id (8), edge id and
+    features, x_i and x_j (24); node outputs once per node.
+    """
+    eb = 8 + (4 + FE * s if FE else 0) + 24 * g
+    if cls == "fwd_edge":
+        flops = 2 * ((g + FE) * H + H * O + g * O * M)
+        return flops * E, E * (2 * H * s + eb) + N * (O * s + 12 * g)
+    if cls == "bwd_edge":
+        flops = 4 * (g + FE) * H + 6 * H * O + 6 * g * O * M
+        per_edge = 2 * H * s + eb + O * s + 12 * g + H * s + 16 * g      # + grad rows of i, Gh and Gx stores
+        if not coop:
+            per_edge += (O + O + 2 * g * M) * s                          # stored weight-gradient factors
+        return flops * E, E * per_edge
+    if cls == "node_reduce":
+        return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
+    if cls == "node_gemm":
+        return 2 * N * F * 2 * H, N * (F + 2 * H) * s
+    return 0, 0
 
 
-def cpu_baseline(g, n_graphs, H, layers, repeats, seed=3002):
+def model_flops_per_edge(F, H, O, M, FE, g):
+    """Model-FLOPs convention of the concat formulation, forward + backward = 3 x forward."""
+    return 3 * 2 * ((2 * F + g + FE) * H + H * O + g * (O * M + M))
+
+
+def read_traffic(name, dtype, cls):
+    """HBM bytes per launch from a profiles/ summary line 'TRAFFIC <workload> <dtype> <class> <bytes>'."""
+    d = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(d):
+        return None
+    pat = re.compile(rf"^TRAFFIC\s+{re.escape(name)}\s+{dtype}\s+{cls}\s+([0-9.eE+]+)\s*$")
+    for fn in sorted(os.listdir(d)):
+        if not fn.endswith((".md", ".txt")):
+            continue
+        with open(os.path.join(d, fn)) as f:
+            for line in f:
+                m = pat.match(line.strip())
+                if m:
+                    return float(m.group(1))
+    return None
+
+
+def _closed_prefix(rowptr, col, n_edges):
+    """Largest row prefix [0, r) with at most about n_edges edges whose sources all lie in [0, r)."""
+    N = rowptr.shape[0] - 1
+    deg = np.diff(rowptr)
+    rowmax = np.full(N, -1, dtype=np.int64)
+    nz = deg > 0
+    rowmax[nz] = np.maximum.reduceat(col.astype(np.int64), rowptr[:-1][nz])
+    mx = np.maximum.accumulate(rowmax)
+    r_ok = np.nonzero(mx < np.arange(1, N + 1))[0] + 1     # prefixes closed under sources
+    r_ok = r_ok[rowptr[r_ok] <= n_edges]
+    return int(r_ok[-1]) if r_ok.size else 0
+
+
+def cpu_baseline(k, g, H, layers, eq, n_edges, repeats, seed):
     import torch
-    from oracle.torch_ref import EGNNRef
+    from oracle.torch_ref import EGNNRef, MPNNRef
     torch.set_num_threads(len(os.sched_getaffinity(0)))
-    offs = g.info["graph_offsets"]
-    n_nodes = int(offs[n_graphs])
-    e_end = int(g.rowptr[n_nodes])
-    rows = np.repeat(np.arange(n_nodes), np.diff(g.rowptr[:n_nodes + 1]))
-    edges = (torch.from_numpy(rows.astype(np.int64)), torch.from_numpy(g.col[:e_end].astype(np.int64)))
-    h0 = torch.from_numpy(g.node_feat[:n_nodes])
-    x0 = torch.from_numpy(g.coord[:n_nodes])
+    r = _closed_prefix(g.rowptr, g.col, n_edges)
+    folded = False
+    if r == 0:        # one connected graph: the first rows, their sources folded into the sample
+        deg_cum = g.rowptr.astype(np.int64)
+        r = int(np.searchsorted(deg_cum, n_edges, side="right") - 1)
+        folded = True
+    e_end = int(g.rowptr[r])
+    rows = np.repeat(np.arange(r), np.diff(g.rowptr[:r + 1]))
+    cols = g.col[:e_end].astype(np.int64) % r if folded else g.col[:e_end].astype(np.int64)
+    edges = (torch.from_numpy(rows.astype(np.int64)), torch.from_numpy(cols))
+    h0 = torch.from_numpy(g.node_feat[:r])
+    ea = None if g.edge_attr is None else torch.from_numpy(g.edge_attr[:e_end])
+    FE = 0 if ea is None else ea.shape[1]
     torch.manual_seed(seed)
-    model = EGNNRef(h0.shape[1], H, H, 0, n_layers=layers)
+    if eq:
+        x0 = torch.from_numpy(g.coord[:r])
+        model = EGNNRef(h0.shape[1], H, H, FE, n_layers=layers)
+        run = lambda: sum(t.sum() for t in model(h0, x0, edges, ea))  # noqa: E731
+    else:
+        model = MPNNRef(h0.shape[1], H, H, FE, n_layers=layers)
+        run = lambda: model(h0, edges, ea).sum()  # noqa: E731
 
     def step():
         model.zero_grad(set_to_none=True)
-        out_h, out_x = model(h0, x0, edges)
-        (out_h.sum() + out_x.sum()).backward()
+        run().backward()
 
     step()
     ts = []
@@ -86,38 +163,47 @@ def cpu_baseline(g, n_graphs, H, layers, repeats, seed=3002):
         step()
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
+    how = "first %d rows, sources folded into them" % r if folded else "first %d nodes (whole graphs)" % r
     return dict(value=e_end * layers / t, unit="edges/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"first {n_graphs} of 1024 molecules (N={n_nodes}, E={e_end}), {layers} layers fwd+bwd, "
-                       f"fp32 torch eager (oracle/torch_ref.py), median of {repeats} after 1 warm-up; "
-                       f"{t * 1e3:.1f} ms per step")
+                sample=f"{how}: N={r}, E={e_end}, {layers} layers fwd+bwd, fp32 torch eager "
+                       f"(oracle/torch_ref.py), median of {repeats} after 1 warm-up; {t * 1e3:.1f} ms per step")
 
 
 def main():
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {a.gpus}); multi-GPU sharding is designed "
-              "(DESIGN.md) but not part of this build", file=sys.stderr)
+        print(f"bench.py measures one GPU (asked for --gpus {a.gpus}): the multi-GPU sharding of this layer "
+              "is designed but not built", file=sys.stderr)
         sys.exit(2)
     import torch
     from pymolecular_amd import _capi, graphs
-    from pymolecular_amd.models.EGNN import EGNN
+    from pymolecular_amd.models.EGNN import EGNN, MPNN
 
+    k = a.workload
+    W = graphs.WORKLOADS[k]
+    dtype = a.dtype or W["dtypes"][-1]
     dev = torch.device("cuda:0")
-    dt = torch.bfloat16 if a.dtype == "bf16" else torch.float32
-    H, L = 128, 4
-    g = graphs.make_workload(2)
+    dt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    H, L, eq = W["H"], W["layers"], W["eq"]
+    g = graphs.make_workload(k)
     N, E = g.N, g.E
-    rows = np.repeat(np.arange(N), np.diff(g.rowptr)).astype(np.int64)
-    edges = [torch.from_numpy(rows).to(dev), torch.from_numpy(g.col.astype(np.int64)).to(dev)]
+    F0 = g.node_feat.shape[1]
+    FE = 0 if g.edge_attr is None else g.edge_attr.shape[1]
+    edges = [torch.from_numpy(g.rows().astype(np.int64)).to(dev), torch.from_numpy(g.col.astype(np.int64)).to(dev)]
     h0 = torch.from_numpy(g.node_feat).to(dev, dt)
-    x0 = torch.from_numpy(g.coord).to(dev)
-    torch.manual_seed(3002)
-    model = EGNN(in_node_nf=h0.shape[1], hidden_nf=H, out_node_nf=H, in_edge_nf=0, n_layers=L).to(dev, dt)
+    ea = None if g.edge_attr is None else torch.from_numpy(g.edge_attr).to(dev, dt)
+    torch.manual_seed(3000 + k)
+    if eq:
+        x0 = torch.from_numpy(g.coord).to(dev)
+        model = EGNN(in_node_nf=F0, hidden_nf=H, out_node_nf=H, in_edge_nf=FE, n_layers=L).to(dev, dt)
+        loss = lambda: sum(t.float().sum() for t in model(h0, x0, edges, ea))  # noqa: E731
+    else:
+        model = MPNN(in_node_nf=F0, hidden_nf=H, out_node_nf=H, in_edge_nf=FE, n_layers=L).to(dev, dt)
+        loss = lambda: model(h0, edges, ea).float().sum()  # noqa: E731
 
     def step():
         model.zero_grad(set_to_none=True)
-        out_h, out_x = model(h0, x0, edges, None)
-        (out_h.float().sum() + out_x.float().sum()).backward()
+        loss().backward()
 
     for _ in range(a.warmup):
         step()
@@ -131,7 +217,7 @@ def main():
     ms = e0.elapsed_time(e1) / a.steps
     value = E * L / (ms / 1e3)
 
-    # per-kernel device time (HIP events on the launch stream, via the library hook)
+    # per-kernel device time: HIP events on the launch stream, through the library hook
     _capi.profile_enable(True)
     nprof = max(3, min(a.steps, 10))
     for _ in range(nprof):
@@ -139,46 +225,57 @@ def main():
     torch.cuda.synchronize()
     prof = _capi.profile_read()
     _capi.profile_enable(False)
+
     s = 2 if dt == torch.bfloat16 else 4
-    w = per_edge_work(H, H, H, 0, 1, s)
-    kern = {k: dict(ms_per_launch=(t / n if n else 0.0), launches_per_step=n / nprof,
-                    share=0.0) for k, (t, n) in prof.items()}
-    tot = sum(t for t, _ in prof.values()) / nprof
-    for k, (t, n) in prof.items():
-        kern[k]["share"] = (t / nprof) / ms if ms else 0.0
-    dom = max(prof, key=lambda k: prof[k][0])
-    dur_s = kern[dom]["ms_per_launch"] / 1e3
+    g1 = 1 if eq else 0
+    coop = s == 2 and H == 128 and FE + 2 * g1 <= 32
     peak_mfma = PEAK["bf16_mfma_tflops"] if s == 2 else PEAK["fp32_mfma_tflops"]
-    flops = {"bwd_edge": w["bwd_flops"], "fwd_edge": w["fwd_flops"]}.get(dom, 0) * E
-    nbytes = {"bwd_edge": w["bwd_bytes"], "fwd_edge": w["fwd_bytes"]}.get(dom, 0) * E
-    t_mfma = flops / (peak_mfma * 1e12)
-    t_hbm = nbytes / (PEAK["hbm_gbs"] * 1e9)
-    if t_hbm >= t_mfma:
+    kern, portions = {}, {}
+    for cls, (t, n) in prof.items():
+        if not n:
+            continue
+        per = t / n
+        kern[cls] = dict(ms_per_launch=per, launches_per_step=n / nprof, share=(t / nprof) / ms)
+        fl, by = kernel_work(cls, coop, N, E, H, H, H, H, FE, g1, s)
+        if fl or by:
+            portions[cls] = dict(mfma_frac=fl / (per / 1e3) / (peak_mfma * 1e12),
+                                 hbm_frac=by / (per / 1e3) / (PEAK["hbm_gbs"] * 1e9),
+                                 flops=fl, bytes=by)
+    dom = max(kern, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
+    dur_s = kern[dom]["ms_per_launch"] / 1e3
+    flops, nbytes = kernel_work(dom, coop, N, E, H, H, H, H, FE, g1, s)
+    if nbytes / (PEAK["hbm_gbs"] * 1e9) >= flops / (peak_mfma * 1e12):
         roof = dict(bound="hbm", achieved=nbytes / dur_s / 1e9, peak=PEAK["hbm_gbs"], unit="GB/s")
     else:
         roof = dict(bound="mfma", achieved=flops / dur_s / 1e12, peak=peak_mfma, unit="TFLOP/s")
     roof["frac"] = roof["achieved"] / roof["peak"]
-    roof["traffic"] = None
-    roof["kernel"] = dom
-    roof["ms_per_launch"] = kern[dom]["ms_per_launch"]
-    roof["mfma_frac"] = (flops / dur_s / 1e12) / peak_mfma if dur_s else 0.0
-    roof["hbm_frac"] = (nbytes / dur_s / 1e9) / PEAK["hbm_gbs"] if dur_s else 0.0
-    model_mfu = (w["model_fwdbwd"] * E * L) / (ms / 1e3) / (peak_mfma * 1e12)
+    name = DESCR[k].split(":")[0]
+    roof["traffic"] = read_traffic(name, dtype, dom)
+    roof.update(kernel=dom, ms_per_launch=kern[dom]["ms_per_launch"], algorithmic_flops=flops,
+                algorithmic_bytes=nbytes)
+    model_mfu = model_flops_per_edge(H, H, H, H, FE, g1) * E * L / (ms / 1e3) / (peak_mfma * 1e12)
 
     out = {
         "metric": METRIC, "value": value, "unit": "edges/s", "n_gpus": 1, "steps": a.steps, "warmup": a.warmup,
         "ms_per_step": ms, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": a.dtype, "data": "synthetic (seeded numpy PCG64 molecules; random-init weights, seed 3002)",
-        "config": {"workload": "molecules-1024: 4 x E_GCL, H=128, fully connected molecules, fwd+bwd of "
-                               "sum-of-outputs loss", "N": N, "E": E, "layers": L, "H": H, "F_E": 0,
-                   "dtype": a.dtype},
+        "dtype": dtype, "data": f"synthetic (seeded numpy PCG64 graphs, seeds {1000 + k}/{2000 + k}; "
+                                f"random-init weights, seed {3000 + k})",
+        "config": {"workload": DESCR[k] + ", fwd+bwd of the sum-of-outputs loss", "N": N, "E": E, "layers": L,
+                   "H": H, "F_E": FE, "dtype": dtype},
         "roofline": roof,
+        "portions": portions,
         "model_flops_mfma_frac": model_mfu,
-        "kernels": {k: {kk: round(vv, 5) for kk, vv in v.items()} for k, v in kern.items()},
-        "kernel_ms_per_step": tot,
+        "kernels": {c: {kk: round(vv, 5) for kk, vv in v.items()} for c, v in kern.items()},
+        "kernel_ms_per_step": sum(t for t, _ in prof.values()) / nprof,
     }
     if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(g, a.cpu_graphs, H, L, a.cpu_repeats)
+        out["cpu_baseline"] = cpu_baseline(k, g, H, L, eq, a.cpu_edges, a.cpu_repeats, 3000 + k)
+    if a.copy_probe:
+        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
     print(json.dumps(out), flush=True)
 
 

@@ -25,7 +25,8 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-__all__ = ["fused_concat", "EGCLRef", "EGNNRef", "egcl_params_packed", "segment_sum", "segment_mean"]
+__all__ = ["fused_concat", "EGCLRef", "EGNNRef", "MPNNGCLRef", "MPNNRef", "egcl_params_packed", "segment_sum",
+           "segment_mean"]
 
 
 def segment_sum(data, seg, n):
@@ -117,6 +118,46 @@ class EGNNRef(nn.Module):
         for layer in self.layers:
             h, x, _ = layer(h, edges, x, edge_attr=edge_attr)
         return self.embedding_out(h), x
+
+
+class MPNNGCLRef(nn.Module):
+    """E_GCL without the coordinate branch and without the radial input: the
+    non-equivariant message-passing layer (edge_mlp on cat([h_i, h_j, e]))."""
+
+    def __init__(self, input_nf, output_nf, hidden_nf, edges_in_d=0, residual=True):
+        super().__init__()
+        self.residual = residual
+        self.edge_mlp = nn.Sequential(nn.Linear(2 * input_nf + edges_in_d, hidden_nf), nn.SiLU(),
+                                      nn.Linear(hidden_nf, hidden_nf), nn.SiLU())
+        self.node_mlp = nn.Sequential(nn.Linear(hidden_nf + input_nf, hidden_nf), nn.SiLU(),
+                                      nn.Linear(hidden_nf, output_nf))
+
+    def forward(self, h, edge_index, edge_attr=None):
+        row, col = edge_index
+        parts = [h[row], h[col]] + ([edge_attr] if edge_attr is not None else [])
+        m = self.edge_mlp(torch.cat(parts, dim=1))
+        agg = segment_sum(m, row, h.shape[0])
+        out = self.node_mlp(torch.cat([h, agg], dim=1))
+        if self.residual:
+            out = h + out
+        return out, edge_attr
+
+
+class MPNNRef(nn.Module):
+    """embedding_in, n_layers x MPNNGCLRef, embedding_out."""
+
+    def __init__(self, in_node_nf, hidden_nf, out_node_nf, in_edge_nf=0, n_layers=2):
+        super().__init__()
+        self.embedding_in = nn.Linear(in_node_nf, hidden_nf)
+        self.embedding_out = nn.Linear(hidden_nf, out_node_nf)
+        self.layers = nn.ModuleList([MPNNGCLRef(hidden_nf, hidden_nf, hidden_nf, edges_in_d=in_edge_nf)
+                                     for _ in range(n_layers)])
+
+    def forward(self, h, edges, edge_attr=None):
+        h = self.embedding_in(h)
+        for layer in self.layers:
+            h, _ = layer(h, edges, edge_attr=edge_attr)
+        return self.embedding_out(h)
 
 
 def egcl_params_packed(layer) -> dict:

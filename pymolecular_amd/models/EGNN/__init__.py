@@ -4,3 +4,4 @@ from .layer import EGNN_HIP_Layer, EGNN_Triton_Layer  # noqa: F401
 from .forward_kernel import egnn_forward_kernel_node_parallel  # noqa: F401
 from .backward_kernel import egnn_backward_kernel_node_parallel  # noqa: F401
 from .pytorch_baseline import pytorch_egnn_baseline, swish_torch  # noqa: F401
+from .mpnn import MPNN, MPNN_GCL  # noqa: F401

@@ -253,6 +253,26 @@ def test_egcl_mapping_matches_module():
     np.testing.assert_allclose(h_out.detach().numpy(), h_ref.numpy(), rtol=1e-12, atol=1e-12)
 
 
+def test_mpnn_mapping_matches_module():
+    # the non-equivariant layer (no radial input, no coordinates) is the oracle with equivariant=False
+    torch.manual_seed(1)
+    layer = torch_ref.MPNNGCLRef(8, 8, 8, edges_in_d=3).double()
+    c = small_case(17, N=11, eq=False)
+    rows = torch.tensor(orc.csr_row_of_edge(c["rowptr"]))
+    col = torch.tensor(c["col"], dtype=torch.int64)
+    h = torch.tensor(rng(3).standard_normal((11, 8)))
+    ea = torch.tensor(rng(4).standard_normal((len(col), 3)))
+    h_out, _ = layer(h, (rows, col), ea)
+    e0, e2 = layer.edge_mlp[0], layer.edge_mlp[2]
+    pk = dict(w1_msg=e0.weight.t().detach().numpy(), b1=e0.bias.detach().numpy(),
+              w2_msg=e2.weight.t().detach().numpy(), b2=e2.bias.detach().numpy())
+    om, ox = orc.fused_forward(h.numpy(), None, ea.numpy(), c["rowptr"], c["col"], None, pk, equivariant=False)
+    assert ox is None
+    with torch.no_grad():
+        h_ref = h + layer.node_mlp(torch.cat([h, torch.tensor(om)], dim=1))
+    np.testing.assert_allclose(h_out.detach().numpy(), h_ref.numpy(), rtol=1e-12, atol=1e-12)
+
+
 def test_round_bf16_matches_torch():
     a = rng(16).standard_normal(10000).astype(np.float32) * 100
     ref = torch.tensor(a).to(torch.bfloat16).to(torch.float64).numpy()
