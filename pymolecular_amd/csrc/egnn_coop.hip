@@ -317,11 +317,12 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward
 // ---------------------------------------------------------------------------
-template <int H, int O, int M, int W, bool EQ>
+template <int H, int O, int M, int W, bool EQ, int NU>
 __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = EQ ? M / W / 16 : 1;
   constexpr int KH = H / 32, KO = O / 32, KM = M / 32;
-  constexpr int NO = O / 16, NM = M / 16, NU = 2;  // edge-input slots: 32 (F_E + 2 <= 32)
+  constexpr int NO = O / 16, NM = M / 16;          // NU: 16-column blocks of edge features (F_E <= 16 NU)
+  constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
   // buffers whose live ranges do not overlap share storage:
   //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5)
   constexpr int CH1 = (KH > KO ? KH : KO) * 2 * 64 * 8, CH2 = ((EQ ? KO : 1) * 2 > NO ? (EQ ? KO : 1) * 2 : NO) * 64 * 8;
@@ -338,8 +339,8 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   bf16* const s_ga2N = s_buf2;
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
-  __shared__ float s_r2[TE];
-  __shared__ int s_eid[TE];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];   // [edge][slot] edge features of the tile
+  __shared__ float s_geo[TE][8];                                  // delta, scaled grad of x_i per edge
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* PQ = (const bf16*)a.PQ;
@@ -352,7 +353,20 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 
   bf16x8 wu[BH], whlT[BO][KH];
   bf16x8 wmovT[BM][EQ ? KO : 1];
-  f32x4 b2v[BO], bx1v[BM], w2mv[BM], wdv[BH];
+  // per-row vectors, read from LDS where they are used: b2 (O), bx1 (M), w2_mov (M), w_d (H)
+  __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
+  float* const s_b2 = s_vec;
+  float* const s_bx1 = s_vec + O;
+  float* const s_w2m = s_vec + O + M;
+  float* const s_wd = s_vec + O + 2 * M;
+  for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
+  if constexpr (EQ) {
+    for (int q = threadIdx.x; q < M; q += W * 64) {
+      s_bx1[q] = a.fr.bx1f[q];
+      s_w2m[q] = a.fr.w2mf[q];
+    }
+    for (int q = threadIdx.x; q < H; q += W * 64) s_wd[q] = a.fr.wdf[q];
+  }
   {
     const int nthr = W * 64;
     const int nwh = (H / 16) * KO * kFragElems / 8;
@@ -368,7 +382,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   for (int j = 0; j < BH; ++j) {
     const int hb = w * BH + j;
     wu[j] = load_chunk((const bf16*)a.fr.u + (int64_t)hb * kFragElems + l * 8);
-    wdv[j] = EQ ? load4_f32(a.fr.wdf + 16 * hb + 4 * g) : zero4();
   }
 #pragma unroll
   for (int j = 0; j < BO; ++j) {
@@ -376,7 +389,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KH; ++kc)
       whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)ob * KH + kc) * kFragElems + l * 8);
-    b2v[j] = load4_f32(a.fr.b2f + 16 * ob + 4 * g);
   }
   if constexpr (EQ) {
 #pragma unroll
@@ -385,20 +397,19 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc)
         wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)mb * KO + kc) * kFragElems + l * 8);
-      bx1v[j] = load4_f32(a.fr.bx1f + 16 * mb + 4 * g);
-      w2mv[j] = load4_f32(a.fr.w2mf + 16 * mb + 4 * g);
     }
   }
   const bf16x8 I = ident_chunk(c, g);
 
-  f32x4 acc_whl[BH][NO], acc_w1m[BO][EQ ? NM : 1], acc_wu[BH][NU];
-  f32x4 vb2[BO], vbx1[BM], vw2m[BM];
+  f32x4 acc_whl[BH][NO], acc_w1m[BO][EQ ? NM : 1], acc_wu[BH][NU > 0 ? NU : 1];
+  f32x4 vb2[BO], vbx1[BM], vw2m[BM], vwd[BH];
 #pragma unroll
   for (int j = 0; j < BH; ++j) {
 #pragma unroll
     for (int cb = 0; cb < NO; ++cb) acc_whl[j][cb] = zero4();
 #pragma unroll
     for (int ub = 0; ub < NU; ++ub) acc_wu[j][ub] = zero4();
+    vwd[j] = zero4();
   }
 #pragma unroll
   for (int j = 0; j < BO; ++j) {
@@ -443,13 +454,11 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
           gxz[nb] = gx[2] * sc;
         }
         gphi[nb] = dx[nb] * gxx[nb] + dy[nb] * gxy[nb] + dz[nb] * gxz[nb];
-      }
-    }
-    if (w == 0 && g == 0) {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        s_r2[nb * 16 + c] = r2[nb];
-        s_eid[nb * 16 + c] = valid[nb] ? eid[nb] : -1;
+        if (w == 0 && g == 0) {
+          float* q = s_geo[nb * 16 + c];
+          q[0] = dx[nb]; q[1] = dy[nb]; q[2] = dz[nb];
+          q[4] = gxx[nb]; q[5] = gxy[nb]; q[6] = gxz[nb];
+        }
       }
     }
 
@@ -457,6 +466,12 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
     bf16x8 u[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], FE, g, r2[nb], EQ);
+    // the tile's edge features, [edge][slot], for the dW_e product (zero rows past the end)
+    if (NU > 0 && w == 0 && 8 * g < FE) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        *reinterpret_cast<bf16x8*>(s_u + (nb * 16 + c) * FEP + 8 * g) = valid[nb] ? u[nb] : zero_chunk<bf16>();
+    }
     bf16x4 s1[BH][2];
     bf16x8 m1N[BH];
 #pragma unroll
@@ -491,6 +506,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;
       f32x4 y[2];
+      const f32x4 b2v = *reinterpret_cast<const f32x4*>(s_b2 + 16 * ob + 4 * g);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
@@ -499,7 +515,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
         f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const YD r = silu_yd<bf16>(acc[i] + b2v[j][i]);
+          const YD r = silu_yd<bf16>(acc[i] + b2v[i]);
           y[nb][i] = r.y;
           d[i] = r.d;
         }
@@ -515,6 +531,8 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int j = 0; j < BM; ++j) {
         const int mb = w * BM + j;
+        const f32x4 bx1v = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * mb + 4 * g);
+        const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * mb + 4 * g);
         f32x4 gq[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
@@ -523,9 +541,9 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
           for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const YD r = silu_yd<bf16>(acc[i] + bx1v[j][i]);
-            phi[nb] += r.y * w2mv[j][i];
-            gq[nb][i] = gphi[nb] * w2mv[j][i] * r.d;
+            const YD r = silu_yd<bf16>(acc[i] + bx1v[i]);
+            phi[nb] += r.y * w2mv[i];
+            gq[nb][i] = gphi[nb] * w2mv[i] * r.d;
             vw2m[j][i] += r.y * gphi[nb];
             vbx1[j][i] += gq[nb][i];
           }
@@ -580,6 +598,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
       const int hb = w * BH + j;
+      const f32x4 wdv = EQ ? *reinterpret_cast<const f32x4*>(s_wd + 16 * hb + 4 * g) : zero4();
       f32x4 g1[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -592,7 +611,8 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           g1[nb][i] = acc[i] * d[i];
-          gr[nb] += wdv[j][i] * g1[nb][i];
+          gr[nb] += wdv[i] * g1[nb][i];
+          if (EQ) vwd[j][i] += g1[nb][i] * r2[nb];
         }
         if (valid[nb])
           *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * hb + 4 * g) = pack4(g1[nb]);
@@ -601,23 +621,14 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e]
 #pragma unroll
       for (int cb = 0; cb < NO; ++cb) mma(acc_whl[j][cb], m1N[j], get_norm(s_ga2N, cb, l));
-      // [dW_e | dw_d] rows of this wave: sum_e g_a1[h][e] U[slot][e]
+      // dW_e rows of this wave: sum_e g_a1[h][e] e[e][slot] (the r^2 column is accumulated above)
 #pragma unroll
       for (int ub = 0; ub < NU; ++ub) {
-        if (16 * ub >= FE + (EQ ? 2 : 0)) continue;   // column block of zero slots
+        if (16 * ub >= FE) continue;   // column block past the edge features
         const int slot = 16 * ub + c;
         bf16x8 un;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) {
-          const int k = kappa_chain(g, s);
-          float v = 0.f;
-          if (k < nvalid) {
-            if (slot < FE) v = (float)ef[(int64_t)s_eid[k] * a.se + slot];
-            else if (EQ && slot == FE) v = (float)(bf16)s_r2[k];
-            else if (EQ && slot == FE + 1) v = s_r2[k] - (float)(bf16)s_r2[k];
-          }
-          un[s] = (bf16)v;
-        }
+        for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
         mma(acc_wu[j][ub], ga1N, un);
       }
     }
@@ -642,8 +653,9 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
             pht += s_phi[ww][k];
           }
           const float k2 = 2.0f * grt;
+          const float* q = s_geo[k];
           *reinterpret_cast<f32x4*>(a.Gx + (base + k) * 4) =
-              f32x4{pht * gxx[nb] + k2 * dx[nb], pht * gxy[nb] + k2 * dy[nb], pht * gxz[nb] + k2 * dz[nb], 0.f};
+              f32x4{pht * q[4] + k2 * q[0], pht * q[5] + k2 * q[1], pht * q[6] + k2 * q[2], 0.f};
         }
       }
     }
@@ -667,10 +679,12 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int ub = 0; ub < NU; ++ub) {
         const int slot = 16 * ub + c;
-        const float v = acc_wu[j][ub][i];
-        const float vn = shfl(v, (l & ~15) | ((c + 1) & 15));
-        if (slot < FE) P[oWE + (int64_t)h * FE + slot] = v;
-        else if (EQ && slot == FE) P[oWD + h] = v + vn;
+        if (slot < FE) P[oWE + (int64_t)h * FE + slot] = acc_wu[j][ub][i];
+      }
+      if constexpr (EQ) {
+        float v = vwd[j][i];
+        v += shfl_xor(v, 1); v += shfl_xor(v, 2); v += shfl_xor(v, 4); v += shfl_xor(v, 8);
+        if (c == 0) P[oWD + h] = v;
       }
     }
   }
@@ -717,7 +731,14 @@ int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
 
 template <int H, int O, int M, int W, bool EQ>
 int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
-  if (a.ntiles > 0) hipLaunchKernelGGL((coop_bwd_kernel<H, O, M, W, EQ>), dim3(nblk), dim3(W * 64), 0, st, a);
+  if (a.ntiles > 0) {
+    if (a.FE == 0)
+      hipLaunchKernelGGL((coop_bwd_kernel<H, O, M, W, EQ, 0>), dim3(nblk), dim3(W * 64), 0, st, a);
+    else if (a.FE <= 16)
+      hipLaunchKernelGGL((coop_bwd_kernel<H, O, M, W, EQ, 1>), dim3(nblk), dim3(W * 64), 0, st, a);
+    else
+      hipLaunchKernelGGL((coop_bwd_kernel<H, O, M, W, EQ, 2>), dim3(nblk), dim3(W * 64), 0, st, a);
+  }
   return (int)hipGetLastError();
 }
 
@@ -725,7 +746,7 @@ int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
 
 bool coop_supported(const LayerShape& s) {
   const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);
-  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32;
+  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32;   // forward: F_E features + r^2 hi/lo in 32 slots
 }
 
 int coop_bwd_blocks(const LayerShape& s) {
