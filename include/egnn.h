@@ -12,6 +12,9 @@
  *   egnn_bwd            <- egnn_backward_kernel_node_parallel[grid](...)
  *                          models/EGNN/backward_kernel.py:14-50, launched by
  *                          launch_triton, test_mem.py:7-35
+ *   egnn_node_fwd/bwd   <- the node MLP of E_GCL.node_model (egnn_clean.py:60-70)
+ *                          and EGNN_Triton_Layer (layer.py:97-101), torch
+ *                          modules in the reference
  *   egnn_schedule_build <- no reference counterpart: the reference runs one
  *                          program per CSR row (forward_kernel.py:47,
  *                          test_mem.py:22); this builds the degree-aware edge
@@ -138,8 +141,44 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides,
                  void* grad_b1, void* grad_b2, void* grad_bx1, const void* node_proj,
                  const void* sched, void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- node update (the per-node epilogue of a layer) ------------------------
+ * Replaces the host-side node MLP of E_GCL.node_model (egnn_clean.py:60-70)
+ * and of EGNN_Triton_Layer.forward (layer.py:97-101):
+ *   z = [x1 | x2] W1^T + b1,  a = SiLU(z),  out = a W2^T + b2 (+ x1 if residual)
+ * x1 = h (N, K1), x2 = aggregated messages (N, K2), optionally with node
+ * attributes appended by the caller.  W1 (Hn, K1 + K2) and W2 (Fo, Hn) are in
+ * torch.nn.Linear layout (out, in); b1 (Hn) and b2 (Fo) may be NULL.
+ * K1, K2, Hn and Fo are multiples of 8; Fo == K1 when residual.  Activations,
+ * weights and gradients share one dtype (EGNN_F32 or EGNN_BF16), with fp32
+ * accumulation.  Row strides (ld*) are in elements, rows 16-byte aligned. */
+typedef struct EgnnNodeDims {
+  int64_t N;
+  int32_t K1, K2, Hn, Fo;
+  int32_t residual;
+  int32_t dtype;
+} EgnnNodeDims;
+
+/* Workspace bytes for egnn_node_bwd. */
+size_t egnn_node_bwd_workspace_bytes(const EgnnNodeDims* dims);
+
+/* Forward.  Writes out (N, Fo, row stride ldo) and the pre-activation `pre`
+ * and activation `act` (both (N, Hn) contiguous) that egnn_node_bwd reads. */
+int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
+                      const void* w1, const void* b1, const void* w2, const void* b2,
+                      void* pre, void* act, void* out, int64_t ldo, void* stream);
+
+/* Backward.  Writes grad_x (N, K1 + K2) contiguous: columns [0, K1) are dL/dx1
+ * (including the residual term), [K1, K1 + K2) dL/dx2; grad_w1 (Hn, K1 + K2),
+ * grad_w2 (Fo, Hn), and grad_b1 / grad_b2 when non-NULL.  Weight gradients are
+ * split-K partial products summed in a fixed order (deterministic). */
+int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
+                      const void* w1, const void* w2, const void* pre, const void* act,
+                      const void* grad_out, int64_t ldgo, void* grad_x,
+                      void* grad_w1, void* grad_b1, void* grad_w2, void* grad_b2,
+                      void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- instrumentation (no reference counterpart) ---------------------------
- * When enabled, every kernel launch made by egnn_fwd / egnn_bwd is bracketed
+ * When enabled, every kernel launch made by egnn_fwd / egnn_bwd / egnn_node_* is bracketed
  * by HIP events recorded on the caller's stream, grouped by kernel class.
  * egnn_profile_read synchronises on those events and returns the summed
  * device time and the launch count of one class.  Off by default; enabling
@@ -151,7 +190,8 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides,
 #define EGNN_K_WGRAD 4        /* weight-gradient split-K GEMMs + sums  */
 #define EGNN_K_NODE_REDUCE 5  /* CSR/CSC node gradient reduction       */
 #define EGNN_K_PREP 6         /* weight-fragment preparation           */
-#define EGNN_K_COUNT 7
+#define EGNN_K_NODE_UPDATE 7  /* node update GEMMs (egnn_node_fwd/bwd) */
+#define EGNN_K_COUNT 8
 int32_t egnn_profile_enable(int32_t on);
 int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches);
 

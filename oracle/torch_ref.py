@@ -25,7 +25,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-__all__ = ["fused_concat", "EGCLRef", "EGNNRef", "MPNNGCLRef", "MPNNRef", "egcl_params_packed", "segment_sum",
+__all__ = ["fused_concat", "node_update_ref", "EGCLRef", "EGNNRef", "MPNNGCLRef", "MPNNRef", "egcl_params_packed", "segment_sum",
            "segment_mean"]
 
 
@@ -68,6 +68,13 @@ def fused_concat(h, coord, edge_feat, row, col, w1_packed, w2, w1_mov=None, w2_m
     trans = diff * phi
     out_mov = segment_mean(trans, row, n) if mean_agg else segment_sum(trans, row, n)
     return out_msg, out_mov
+
+
+def node_update_ref(x1, x2, w1, b1, w2, b2, residual=True):
+    """node_mlp(cat([x1, x2])) (+ x1): egnn_clean.py:60-70 with nn.Linear-layout weights."""
+    x = x1 if x2 is None else torch.cat([x1, x2], dim=1)
+    out = nn.functional.linear(nn.functional.silu(nn.functional.linear(x, w1, b1)), w2, b2)
+    return x1 + out if residual else out
 
 
 class EGCLRef(nn.Module):

@@ -20,12 +20,13 @@ EXPORTED = (
     "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
     "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_node_proj_bytes",
     "egnn_fwd", "egnn_bwd",
+    "egnn_node_bwd_workspace_bytes", "egnn_node_fwd", "egnn_node_bwd",
     "egnn_profile_enable", "egnn_profile_read",
 )
 
 # kernel classes of the instrumentation hook
-K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP = range(7)
-K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep")
+K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP, K_NODE_UPDATE = range(8)
+K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep", "node_update")
 
 
 class EgnnDims(ctypes.Structure):
@@ -36,6 +37,11 @@ class EgnnDims(ctypes.Structure):
 
 class EgnnStrides(ctypes.Structure):
     _fields_ = [("h", c_int64), ("coord", c_int64), ("edge", c_int64), ("msg", c_int64), ("mov", c_int64)]
+
+
+class EgnnNodeDims(ctypes.Structure):
+    _fields_ = [("N", c_int64), ("K1", c_int32), ("K2", c_int32), ("Hn", c_int32), ("Fo", c_int32),
+                ("residual", c_int32), ("dtype", c_int32)]
 
 
 _lib = None
@@ -79,6 +85,13 @@ def lib() -> ctypes.CDLL:
     L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 18 + [c_size_t, P]
     L.egnn_bwd.restype = c_int32
     L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 27 + [c_size_t, P]
+    ND = ctypes.POINTER(EgnnNodeDims)
+    L.egnn_node_bwd_workspace_bytes.restype = c_size_t
+    L.egnn_node_bwd_workspace_bytes.argtypes = [ND]
+    L.egnn_node_fwd.restype = c_int32
+    L.egnn_node_fwd.argtypes = [ND, P, c_int64, P, c_int64, P, P, P, P, P, P, P, c_int64, P]
+    L.egnn_node_bwd.restype = c_int32
+    L.egnn_node_bwd.argtypes = [ND, P, c_int64, P, c_int64, P, P, P, P, P, c_int64, P, P, P, P, P, P, c_size_t, P]
     L.egnn_profile_enable.restype = c_int32
     L.egnn_profile_enable.argtypes = [c_int32]
     L.egnn_profile_read.restype = c_int32

@@ -3,6 +3,7 @@
 // kernels on the caller's stream.  No allocation, no host synchronisation
 // (except the one documented in egnn_schedule_build).
 #include "egnn_device.h"
+#include <initializer_list>
 #include <vector>
 #include "egnn_internal.h"
 
@@ -349,6 +350,157 @@ int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launc
   *total_ms = t;
   *launches = n;
   return EGNN_OK;
+}
+
+}  // extern "C"
+
+// ---- node update --------------------------------------------------------------
+namespace {
+
+struct NodeShape {
+  int64_t N; int K1, K2, K, Hn, Fo; bool residual, bf16; size_t esz;
+};
+
+int32_t node_shape(const EgnnNodeDims* d, NodeShape* s) {
+  if (!d) return EGNN_ERR_NULL;
+  if (d->N < 0 || d->K1 <= 0 || d->K2 < 0 || d->Hn <= 0 || d->Fo <= 0) return EGNN_ERR_DIMS;
+  if (d->K1 % 8 || d->K2 % 8 || d->Hn % 8 || d->Fo % 8) return EGNN_ERR_DIMS;
+  if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (d->residual && d->Fo != d->K1) return EGNN_ERR_DIMS;
+  s->N = d->N; s->K1 = d->K1; s->K2 = d->K2; s->K = d->K1 + d->K2; s->Hn = d->Hn; s->Fo = d->Fo;
+  s->residual = d->residual != 0; s->bf16 = d->dtype == EGNN_BF16; s->esz = s->bf16 ? 2 : 4;
+  return EGNN_OK;
+}
+
+bool ld_ok(int64_t ld, int64_t width, size_t esz) { return ld >= width && (ld * (int64_t)esz) % 16 == 0; }
+
+struct NodeWs { void* dz; float* part; float* S1; float* S2; int64_t part_elems; };
+
+size_t node_ws_layout(const NodeShape& s, void* base, NodeWs* w) {
+  char* b = (char*)base;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
+  const int64_t ns = cdiv(std::max<int64_t>(s.N, 1), splitk_len(std::max<int64_t>(s.N, 1)));
+  w->part_elems = ns * std::max<int64_t>((int64_t)(s.K + 1) * s.Hn, (int64_t)(s.Hn + 1) * s.Fo);
+  w->dz = take((size_t)s.N * s.Hn * s.esz);
+  w->part = (float*)take((size_t)w->part_elems * sizeof(float));
+  w->S1 = (float*)take((size_t)(s.K + 1) * s.Hn * sizeof(float));
+  w->S2 = (float*)take((size_t)(s.Hn + 1) * s.Fo * sizeof(float));
+  return off;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t egnn_node_bwd_workspace_bytes(const EgnnNodeDims* dims) {
+  NodeShape s;
+  if (node_shape(dims, &s) != EGNN_OK) return 0;
+  NodeWs w;
+  return node_ws_layout(s, nullptr, &w);
+}
+
+int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
+                      const void* w1, const void* b1, const void* w2, const void* b2,
+                      void* pre, void* act, void* out, int64_t ldo, void* stream) {
+  NodeShape s;
+  int32_t rc = node_shape(dims, &s);
+  if (rc != EGNN_OK) return rc;
+  if (s.N == 0) return EGNN_OK;
+  if (!x1 || (s.K2 > 0 && !x2) || !w1 || !w2 || !pre || !act || !out) return EGNN_ERR_NULL;
+  if (!ld_ok(ld1, s.K1, s.esz) || (s.K2 > 0 && !ld_ok(ld2, s.K2, s.esz)) || !ld_ok(ldo, s.Fo, s.esz))
+    return EGNN_ERR_STRIDE;
+  for (const void* p : std::initializer_list<const void*>{x1, x2, w1, w2, pre, act, out})
+    if (!aligned16(p)) return EGNN_ERR_ALIGN;
+  hipStream_t st = (hipStream_t)stream;
+  ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  {  // pre = [x1 | x2] W1^T + b1 ; act = SiLU(pre)
+    Gemm2Args g{};
+    g.M = s.N; g.N = s.Hn; g.K = s.K;
+    g.A = x1; g.lda = ld1; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
+    if (s.K2 > 0) { g.A2 = x2; g.lda2 = ld2; g.a_split = s.K1; }
+    g.B = w1; g.ldb = s.K; g.b_bf16 = s.bf16; g.b_nc = 0;          // B[k][n] = W1[n][k]
+    g.bias = b1; g.bias_bf16 = s.bf16; g.bias_len = b1 ? s.Hn : 0;
+    g.C = act; g.ldc = s.Hn; g.c_bf16 = s.bf16;
+    g.act = 1; g.Cpre = pre; g.ldpre = s.Hn;
+    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+  }
+  {  // out = act W2^T + b2 (+ x1)
+    Gemm2Args g{};
+    g.M = s.N; g.N = s.Fo; g.K = s.Hn;
+    g.A = act; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
+    g.B = w2; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 0;         // B[k][n] = W2[n][k]
+    g.bias = b2; g.bias_bf16 = s.bf16; g.bias_len = b2 ? s.Fo : 0;
+    g.C = out; g.ldc = ldo; g.c_bf16 = s.bf16;
+    if (s.residual) { g.resid = x1; g.ldr = ld1; g.resid_len = s.Fo; }
+    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+  }
+  return EGNN_OK;
+}
+
+int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
+                      const void* w1, const void* w2, const void* pre, const void* act,
+                      const void* grad_out, int64_t ldgo, void* grad_x,
+                      void* grad_w1, void* grad_b1, void* grad_w2, void* grad_b2,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  NodeShape s;
+  int32_t rc = node_shape(dims, &s);
+  if (rc != EGNN_OK) return rc;
+  if (!w1 || !w2 || !grad_w1 || !grad_w2 || !workspace) return EGNN_ERR_NULL;
+  if (s.N > 0 && (!x1 || (s.K2 > 0 && !x2) || !pre || !act || !grad_out || !grad_x)) return EGNN_ERR_NULL;
+  if (s.N > 0 && (!ld_ok(ld1, s.K1, s.esz) || (s.K2 > 0 && !ld_ok(ld2, s.K2, s.esz)) || !ld_ok(ldgo, s.Fo, s.esz)))
+    return EGNN_ERR_STRIDE;
+  for (const void* p : std::initializer_list<const void*>{x1, x2, w1, w2, pre, act, grad_out, grad_x, workspace})
+    if (!aligned16(p)) return EGNN_ERR_ALIGN;
+  NodeWs w;
+  if (node_ws_layout(s, nullptr, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
+  node_ws_layout(s, workspace, &w);
+  hipStream_t st = (hipStream_t)stream;
+  ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  if (s.N > 0) {
+    {  // dz = (dout W2) * SiLU'(pre)
+      Gemm2Args g{};
+      g.M = s.N; g.N = s.Hn; g.K = s.Fo;
+      g.A = grad_out; g.lda = ldgo; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
+      g.B = w2; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 1;        // B[k][n] = W2[k][n]
+      g.C = w.dz; g.ldc = s.Hn; g.c_bf16 = s.bf16;
+      g.zd = pre; g.ldz = s.Hn;
+      if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    }
+    {  // grad_x = dz W1 (+ dout on the first K1 columns)
+      Gemm2Args g{};
+      g.M = s.N; g.N = s.K; g.K = s.Hn;
+      g.A = w.dz; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
+      g.B = w1; g.ldb = s.K; g.b_bf16 = s.bf16; g.b_nc = 1;         // B[k][n] = W1[k][n]
+      g.C = grad_x; g.ldc = s.K; g.c_bf16 = s.bf16;
+      if (s.residual) { g.resid = grad_out; g.ldr = ldgo; g.resid_len = s.K1; }
+      if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    }
+  }
+  const int64_t ksplit = splitk_len(std::max<int64_t>(s.N, 1));
+  const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
+  {  // S1 = [x1 | x2 | 1]^T dz
+    Gemm2Args g{};
+    g.M = s.K + 1; g.N = s.Hn; g.K = s.N;
+    g.A = x1; g.lda = ld1; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.K;
+    if (s.K2 > 0) { g.A2 = x2; g.lda2 = ld2; g.a_split = s.K1; }
+    g.B = w.dz; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 1;
+    g.ksplit = ksplit; g.partial = w.part;
+    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    if (s.N > 0 && (rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_sum_rows(w.part, s.N > 0 ? nsplit : 0, g.M * g.N, w.S1, st))) != EGNN_OK) return rc;
+  }
+  {  // S2 = [act | 1]^T dout
+    Gemm2Args g{};
+    g.M = s.Hn + 1; g.N = s.Fo; g.K = s.N;
+    g.A = act; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.Hn;
+    g.B = grad_out; g.ldb = ldgo; g.b_bf16 = s.bf16; g.b_nc = 1;
+    g.ksplit = ksplit; g.partial = w.part;
+    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    if (s.N > 0 && (rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_sum_rows(w.part, s.N > 0 ? nsplit : 0, g.M * g.N, w.S2, st))) != EGNN_OK) return rc;
+  }
+  return hip_status(launch_node_finalize(s.bf16, w.S1, w.S2, s.K, s.Hn, s.Fo, grad_w1, grad_b1, grad_w2, grad_b2, st));
 }
 
 }  // extern "C"

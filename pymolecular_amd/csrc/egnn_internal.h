@@ -114,6 +114,11 @@ int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st);
 // operand.  A is (M x K) row-major ("k contiguous") or given as its transpose
 // (K x M row-major, "m contiguous"); B is (K x N) row-major ("n contiguous") or
 // (N x K) row-major ("k contiguous").  Row a_ones_row of A reads as all ones.
+// A second A pointer concatenates two matrices: with a k-contiguous A, columns
+// k >= a_split come from A2 (column k - a_split); with an m-contiguous A, rows
+// m >= a_split do.  a_split is a multiple of 8.  Epilogue, in this order:
+// + bias[n]; * SiLU'(zd[m][n]); store the value to Cpre and apply SiLU (act);
+// + resid[m][n] for n < resid_len.  Cpre, resid and zd share C's dtype.
 struct Gemm2Args {
   int64_t M, N, K;
   const void* A; int64_t lda; int a_bf16; int a_kc; int64_t a_ones_row;
@@ -121,8 +126,14 @@ struct Gemm2Args {
   const void* bias; int bias_bf16; int64_t bias_len;
   void* C; int64_t ldc; int c_bf16; int perm_half;
   float* partial; int64_t ksplit;
+  const void* A2; int64_t lda2; int64_t a_split;
+  int act; void* Cpre; int64_t ldpre;
+  const void* resid; int64_t ldr; int64_t resid_len;
+  const void* zd; int64_t ldz;
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
+int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,
+                         void* gw2, void* gb2, hipStream_t st);
 
 struct FwdArgs {
   int64_t N, E, ntiles;

@@ -317,6 +317,7 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
   int64_t kbeg = 0, kend = g.K;
   if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
   const TA* A = (const TA*)g.A;
+  const TA* A2 = (const TA*)g.A2;
   const TB* B = (const TB*)g.B;
   f32x4 acc[2][2];
   for (int a = 0; a < 2; ++a) for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -324,35 +325,37 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
     // ---- A tile -> As[m][k]
     constexpr int NVA = BM * BK / VA;
     for (int v = tid; v < NVA; v += 256) {
-      if constexpr (A_KC) {   // A[m * lda + k]
+      if constexpr (A_KC) {   // A[m * lda + k], or A2[m * lda2 + k - a_split] for k >= a_split
         const int mm = v / (BK / VA), kk = (v % (BK / VA)) * VA;
         const int64_t m = m0 + mm, k = k0 + kk;
+        const TA* Ab = (A2 && k >= g.a_split) ? A2 + m * g.lda2 - g.a_split : A + m * g.lda;
         TC* dst = &As[mm * LDK + kk];
         if (m < g.M && k + VA <= kend && m != g.a_ones_row) {
-          const auto vv = ld16(A + m * g.lda + k);
+          const auto vv = ld16(Ab + k);
 #pragma unroll
           for (int u = 0; u < VA; ++u) dst[u] = from_f32<TC>((float)vv[u]);
         } else {
 #pragma unroll
           for (int u = 0; u < VA; ++u) {
             float x = 0.f;
-            if (m < g.M && k + u < kend) x = (m == g.a_ones_row) ? 1.0f : to_f32(A[m * g.lda + k + u]);
+            if (m < g.M && k + u < kend) x = (m == g.a_ones_row) ? 1.0f : to_f32(Ab[k + u]);
             dst[u] = from_f32<TC>(x);
           }
         }
-      } else {                // A[k * lda + m]
+      } else {                // A[k * lda + m], or A2[k * lda2 + m - a_split] for m >= a_split
         const int kk = v / (BM / VA), mm = (v % (BM / VA)) * VA;
         const int64_t k = k0 + kk, m = m0 + mm;
+        const TA* Ab = (A2 && m >= g.a_split) ? A2 + k * g.lda2 - g.a_split : A + k * g.lda;
         const bool full = k < kend && m + VA <= g.M && !(g.a_ones_row >= m && g.a_ones_row < m + VA);
         if (full) {
-          const auto vv = ld16(A + k * g.lda + m);
+          const auto vv = ld16(Ab + m);
 #pragma unroll
           for (int u = 0; u < VA; ++u) As[(mm + u) * LDK + kk] = from_f32<TC>((float)vv[u]);
         } else {
 #pragma unroll
           for (int u = 0; u < VA; ++u) {
             float x = 0.f;
-            if (k < kend && m + u < g.M) x = (m + u == g.a_ones_row) ? 1.0f : to_f32(A[k * g.lda + m + u]);
+            if (k < kend && m + u < g.M) x = (m + u == g.a_ones_row) ? 1.0f : to_f32(Ab[m + u]);
             As[(mm + u) * LDK + kk] = from_f32<TC>(x);
           }
         }
@@ -418,6 +421,20 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
           continue;
         }
         if (g.bias && n < g.bias_len) v += ld_elem(g.bias, n, g.bias_bf16);
+        if (g.zd) {   // * SiLU'(z)
+          const float z = ld_elem(g.zd, m * g.ldz + n, g.c_bf16);
+          const float sg = 1.0f / (1.0f + __expf(-z));
+          v *= sg * (1.0f + z * (1.0f - sg));
+        }
+        if (g.act) {
+          if (g.Cpre) {
+            if (g.c_bf16) ((bf16*)g.Cpre)[m * g.ldpre + n] = (bf16)v;
+            else ((float*)g.Cpre)[m * g.ldpre + n] = v;
+            if (g.c_bf16) v = (float)(bf16)v;   // SiLU of the stored pre-activation
+          }
+          v = v / (1.0f + __expf(-v));
+        }
+        if (g.resid && n < g.resid_len) v += ld_elem(g.resid, m * g.ldr + n, g.c_bf16);
         int64_t pn = n;
         if (g.perm_half > 0) {
           const int64_t half = n / g.perm_half, f = n % g.perm_half;
@@ -621,6 +638,46 @@ int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st) 
     hipLaunchKernelGGL(finalize_kernel<bf16>, dim3(512), dim3(256), 0, st, f, s.F, s.FE, s.H, s.O, s.M, s.eq ? 1 : 0);
   else
     hipLaunchKernelGGL(finalize_kernel<float>, dim3(512), dim3(256), 0, st, f, s.F, s.FE, s.H, s.O, s.M, s.eq ? 1 : 0);
+  return (int)hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------
+// node update: weight-gradient finalize (transpose to nn.Linear layout, cast)
+// ---------------------------------------------------------------------------
+// S1 = [x1 | x2 | 1]^T dz   ((K + 1) x Hn),  S2 = [a | 1]^T dout   ((Hn + 1) x Fo)
+template <typename T>
+__global__ void node_finalize_kernel(const float* __restrict__ S1, const float* __restrict__ S2, int K, int Hn,
+                                     int Fo, T* gw1, T* gb1, T* gw2, T* gb2) {
+  const int64_t n1 = (int64_t)Hn * K, n2 = (int64_t)Fo * Hn;
+  const int64_t total = n1 + Hn + n2 + Fo;
+  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    if (t < n1) {
+      const int64_t hn = t / K, k = t % K;
+      gw1[t] = from_f32<T>(S1[k * Hn + hn]);
+    } else if (t < n1 + Hn) {
+      const int64_t hn = t - n1;
+      if (gb1) gb1[hn] = from_f32<T>(S1[(int64_t)K * Hn + hn]);
+    } else if (t < n1 + Hn + n2) {
+      const int64_t u = t - n1 - Hn, fo = u / Hn, hn = u % Hn;
+      gw2[u] = from_f32<T>(S2[hn * Fo + fo]);
+    } else {
+      const int64_t fo = t - n1 - Hn - n2;
+      if (gb2) gb2[fo] = from_f32<T>(S2[(int64_t)Hn * Fo + fo]);
+    }
+  }
+}
+
+int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,
+                         void* gw2, void* gb2, hipStream_t st) {
+  const int64_t total = (int64_t)Hn * K + Hn + (int64_t)Fo * Hn + Fo;
+  const int blocks = (int)std::min<int64_t>(cdiv(total, 256), 1024);
+  if (bf16_out)
+    hipLaunchKernelGGL(node_finalize_kernel<bf16>, dim3(blocks), dim3(256), 0, st, S1, S2, K, Hn, Fo, (bf16*)gw1,
+                       (bf16*)gb1, (bf16*)gw2, (bf16*)gb2);
+  else
+    hipLaunchKernelGGL(node_finalize_kernel<float>, dim3(blocks), dim3(256), 0, st, S1, S2, K, Hn, Fo, (float*)gw1,
+                       (float*)gb1, (float*)gw2, (float*)gb2);
   return (int)hipGetLastError();
 }
 

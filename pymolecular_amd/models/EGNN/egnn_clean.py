@@ -7,8 +7,10 @@ models/EGNN/egnn_clean.py of the reference (``E_GCL`` :5-103, ``EGNN``
 ``E_GCL.forward`` -- edge_model (:49-58), the coordinate update of
 coord_model (:72-82) and the message sum of node_model (:62) -- runs as one
 fused HIP op (:class:`pymolecular_amd.fused.EGNNFusedFn`) that never
-materialises the E x (2H+1+F_E) concatenation or the E x H messages.  The
-per-node part (node_mlp, residual) stays a torch module.
+materialises the E x (2H+1+F_E) concatenation or the E x H messages; the
+per-node part (node_mlp on cat([h, agg]) and the residual, :60-70) is the
+fused node update (:func:`pymolecular_amd.node_update.node_update`), with the
+same nn.Linear parameters.
 
 Supported options of the fused path: act_fn = SiLU, attention = False,
 normalize = False, tanh = False (the reference's defaults and the only
@@ -20,6 +22,7 @@ import torch
 from torch import nn
 
 from ...fused import coo_to_csr, egnn_fused
+from ...node_update import node_update
 
 __all__ = ["E_GCL", "EGNN", "unsorted_segment_sum", "unsorted_segment_mean", "get_edges", "get_edges_batch"]
 
@@ -105,13 +108,9 @@ class E_GCL(nn.Module):
     def forward(self, h, edge_index, coord, edge_attr=None, node_attr=None, csr=None):
         agg, agg_x = self.fused_messages(h, edge_index, coord, edge_attr, csr)
         coord = coord + agg_x.to(coord.dtype)
-        if node_attr is not None:
-            inp = torch.cat([h, agg, node_attr], dim=1)
-        else:
-            inp = torch.cat([h, agg], dim=1)
-        out = self.node_mlp(inp)
-        if self.residual:
-            out = h + out
+        # node_model (:60-70): node_mlp(cat([h, agg(, node_attr)])) (+ h), as one fused node update
+        x2 = agg if node_attr is None else torch.cat([agg, node_attr.to(agg.dtype)], dim=1)
+        out = node_update(h, x2, self.node_mlp[0], self.node_mlp[2], residual=self.residual)
         return out, coord, edge_attr
 
 

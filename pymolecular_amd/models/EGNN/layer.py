@@ -10,8 +10,8 @@ both ways (``out_msg1``/``out_mov1`` at the source, ``out_msg2``/``out_mov2``
 at the destination), and the host divides the coordinate sum by the total
 incident degree (:54-63, 93-95).  Here that is one fused call over the
 symmetrised, dst-sorted edge list (both directions share the edge's
-features through ``edge_ids``), followed by the same host epilogue:
-x' = x + sum(delta phi) / max(deg, 1) and h' = h + node_mlp([h, sum m]).
+features through ``edge_ids``), followed by the same epilogue: x' = x + sum(delta phi) / max(deg, 1) and
+h' = h + node_mlp([h, sum m]) (the fused node update).
 """
 from __future__ import annotations
 
@@ -19,6 +19,7 @@ import torch
 import torch.nn as nn
 
 from ...fused import coo_to_csr, egnn_fused
+from ...node_update import node_update
 
 
 class EGNN_HIP_Layer(nn.Module):
@@ -63,8 +64,9 @@ class EGNN_HIP_Layer(nn.Module):
                                           equivariant=True)
         new_coord = coord.clone()
         new_coord[:, :3] = coord[:, :3] + total_mov / deg[:, None]
-        update_feat = self.node_mlp(torch.cat([node_feat, total_msg.to(node_feat.dtype)], dim=-1))
-        return node_feat + update_feat, new_coord
+        # node_feat + node_mlp(cat([node_feat, total_msg])) (:97-101) as one fused node update
+        return node_update(node_feat, total_msg.to(node_feat.dtype), self.node_mlp[0], self.node_mlp[2],
+                           residual=True), new_coord
 
 
 # the reference's name for the same module (layer.py:7)

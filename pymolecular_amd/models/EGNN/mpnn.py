@@ -16,6 +16,7 @@ import torch
 from torch import nn
 
 from ...fused import egnn_fused
+from ...node_update import node_update
 from .egnn_clean import _csr_cache
 
 __all__ = ["MPNN_GCL", "MPNN"]
@@ -47,11 +48,8 @@ class MPNN_GCL(nn.Module):
 
     def forward(self, h, edge_index, edge_attr=None, node_attr=None, csr=None):
         agg = self.fused_messages(h, edge_index, edge_attr, csr)
-        parts = [h, agg] if node_attr is None else [h, agg, node_attr]
-        out = self.node_mlp(torch.cat(parts, dim=1))
-        if self.residual:
-            out = h + out
-        return out, edge_attr
+        x2 = agg if node_attr is None else torch.cat([agg, node_attr.to(agg.dtype)], dim=1)
+        return node_update(h, x2, self.node_mlp[0], self.node_mlp[2], residual=self.residual), edge_attr
 
 
 class MPNN(nn.Module):

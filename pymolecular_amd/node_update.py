@@ -1,0 +1,121 @@
+"""Node update of a layer on the HIP library: ``[x1 | x2] -> Linear -> SiLU -> Linear (+ x1)``.
+
+This is the per-node epilogue the reference runs as torch modules after the
+message sum: ``E_GCL.node_model`` (egnn_clean.py:60-70: node_mlp on
+``cat([h, agg])`` plus the residual) and ``EGNN_Triton_Layer.forward``
+(layer.py:97-101: ``node_feat + node_mlp(cat([node_feat, total_msg]))``).
+Here the concatenation is never materialised (the first GEMM reads both
+inputs), bias, SiLU and residual are GEMM epilogues, and the backward's weight
+gradients are split-K products summed in a fixed order (``egnn_node_fwd`` /
+``egnn_node_bwd`` in include/egnn.h).  No CPU path: ROCm tensors only.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _capi
+from ._capi import EgnnNodeDims, check
+
+__all__ = ["NodeUpdateFn", "node_update"]
+
+
+def _rowmajor(t: torch.Tensor) -> torch.Tensor:
+    """``t`` if its rows are unit-stride with 16-byte aligned row starts, else a contiguous copy."""
+    esz = t.element_size()
+    if t.stride(1) == 1 and (t.stride(0) * esz) % 16 == 0 and t.data_ptr() % 16 == 0:
+        return t
+    return t.contiguous()
+
+
+def _dims(x1, x2, w1, w2, residual) -> EgnnNodeDims:
+    if x1.dtype == torch.float32:
+        dt = _capi.EGNN_F32
+    elif x1.dtype == torch.bfloat16:
+        dt = _capi.EGNN_BF16
+    else:
+        raise TypeError(f"unsupported dtype {x1.dtype}: the node update runs in float32 or bfloat16")
+    N, K1 = x1.shape
+    K2 = 0 if x2 is None else int(x2.shape[1])
+    Hn, K = w1.shape
+    Fo = int(w2.shape[0])
+    if K != K1 + K2 or w2.shape[1] != Hn:
+        raise ValueError(f"weight shapes {tuple(w1.shape)}, {tuple(w2.shape)} do not match inputs of width "
+                         f"{K1} + {K2}")
+    if K1 % 8 or K2 % 8 or Hn % 8 or Fo % 8:
+        raise ValueError(f"the node update needs widths that are multiples of 8 (got {K1}, {K2}, {Hn}, {Fo})")
+    if residual and Fo != K1:
+        raise ValueError(f"residual update needs output width {Fo} == input width {K1}")
+    return EgnnNodeDims(N=N, K1=K1, K2=K2, Hn=Hn, Fo=Fo, residual=1 if residual else 0, dtype=dt)
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+class NodeUpdateFn(torch.autograd.Function):
+    """``out = NodeUpdateFn.apply(x1, x2, w1, b1, w2, b2, residual)``.
+
+    ``w1`` (Hn, K1 + K2) and ``w2`` (Fo, Hn) in torch.nn.Linear layout; ``b1``
+    and ``b2`` may be None.  Saves the pre-activation and the activation
+    (N x Hn each) for the backward.
+    """
+
+    @staticmethod
+    def forward(ctx, x1, x2, w1, b1, w2, b2, residual=True):
+        if not x1.is_cuda:
+            raise RuntimeError("x1 must be a ROCm device tensor: the node update has no CPU path")
+        dt = x1.dtype
+        x1 = _rowmajor(x1)
+        x2 = None if x2 is None else _rowmajor(x2.to(dt))
+        cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
+        w1c, b1c, w2c, b2c = cv(w1), cv(b1), cv(w2), cv(b2)
+        d = _dims(x1, x2, w1c, w2c, residual)
+        N = x1.shape[0]
+        pre = torch.empty((N, d.Hn), dtype=dt, device=x1.device)
+        act = torch.empty_like(pre)
+        out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
+        L = _capi.lib()
+        st = torch.cuda.current_stream(x1.device).cuda_stream
+        rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
+                             w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), act.data_ptr(),
+                             out.data_ptr(), out.stride(0), st)
+        check("egnn_node_fwd", rc)
+        ctx.save_for_backward(x1, x2, w1c, w2c, pre, act)
+        ctx.residual = residual
+        ctx.has_b = (b1 is not None, b2 is not None)
+        ctx.wdt = (w1.dtype, None if b1 is None else b1.dtype, w2.dtype, None if b2 is None else b2.dtype)
+        return out
+
+    @staticmethod
+    def backward(ctx, gout):
+        x1, x2, w1, w2, pre, act = ctx.saved_tensors
+        dt = x1.dtype
+        gout = _rowmajor(gout.to(dt))
+        d = _dims(x1, x2, w1, w2, ctx.residual)
+        N = x1.shape[0]
+        dev = x1.device
+        grad_x = torch.empty((N, d.K1 + d.K2), dtype=dt, device=dev)
+        gw1, gw2 = torch.empty_like(w1), torch.empty_like(w2)
+        gb1 = torch.empty((d.Hn,), dtype=dt, device=dev) if ctx.has_b[0] else None
+        gb2 = torch.empty((d.Fo,), dtype=dt, device=dev) if ctx.has_b[1] else None
+        L = _capi.lib()
+        nbytes = L.egnn_node_bwd_workspace_bytes(d)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+        st = torch.cuda.current_stream(dev).cuda_stream
+        rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
+                             w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), act.data_ptr(), gout.data_ptr(),
+                             gout.stride(0), grad_x.data_ptr(), gw1.data_ptr(), _ptr(gb1), gw2.data_ptr(),
+                             _ptr(gb2), ws.data_ptr(), nbytes, st)
+        check("egnn_node_bwd", rc)
+        w1dt, b1dt, w2dt, b2dt = ctx.wdt
+        g_x2 = None if x2 is None else grad_x[:, d.K1:]
+        return (grad_x[:, :d.K1], g_x2, gw1.to(w1dt), None if gb1 is None else gb1.to(b1dt), gw2.to(w2dt),
+                None if gb2 is None else gb2.to(b2dt), None)
+
+
+def node_update(x1: torch.Tensor, x2: Optional[torch.Tensor], lin1: torch.nn.Linear, lin2: torch.nn.Linear,
+                residual: bool = True) -> torch.Tensor:
+    """``x1 + lin2(SiLU(lin1(cat([x1, x2]))))`` (without ``x1 +`` when not residual)."""
+    return NodeUpdateFn.apply(x1, x2, lin1.weight, lin1.bias, lin2.weight, lin2.bias, residual)
