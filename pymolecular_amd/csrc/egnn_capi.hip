@@ -165,6 +165,13 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;
   a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
+  a.geo = w.geo;
+  if (w.geo) {
+    ProfScope ps(EGNN_K_PREP, st);
+    if ((rc = hip_status(launch_edge_geo(s.E, s.N, v.erow, col, coord, strides->coord, nullptr, 0, rowptr, 0, w.geo,
+                                         st))) != EGNN_OK)
+      return rc;
+  }
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
     if ((rc = hip_status(coop_supported(s) ? launch_coop_fwd(s, a, st) : launch_fwd(s, a, 0, st))) != EGNN_OK)
@@ -224,6 +231,13 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
   const bool coop = coop_supported(s);
   a.dwpart = w.dwpart; a.LW = w.LW;
+  a.geo = w.geo;
+  if (w.geo) {
+    ProfScope ps(EGNN_K_PREP, st);
+    if ((rc = hip_status(launch_edge_geo(s.E, s.N, v.erow, col, coord, strides->coord, grad_out_mov, strides->mov,
+                                         rowptr, s.mean, w.geo, st))) != EGNN_OK)
+      return rc;
+  }
   if (coop) a.ntiles = cdiv(s.E, kTileEdges);
   {
     ProfScope ps(EGNN_K_BWD_EDGE, st);

@@ -104,6 +104,39 @@ __device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int ei
 
 __device__ __forceinline__ uint32_t lo16(unsigned long long b) { return (uint32_t)(b & 0xffffull); }
 
+// One thread per edge: delta = x_i - x_j and r^2 (forward record), plus the
+// incoming coordinate gradient of row i (scaled by 1/deg for mean aggregation)
+// and g_phi = delta . grad (backward record).  Gathers and the degree division
+// happen here, off the fused kernels' critical path.
+__global__ __launch_bounds__(256) void edge_geo_kernel(int64_t E, int N, const int32_t* __restrict__ erow,
+                                                       const int32_t* __restrict__ col,
+                                                       const float* __restrict__ coord, int64_t sc,
+                                                       const float* __restrict__ gmov, int64_t sgx,
+                                                       const int32_t* __restrict__ rowptr, int mean,
+                                                       float* __restrict__ out) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < E; e += (int64_t)gridDim.x * blockDim.x) {
+    const int i = clampi(erow[e], N), j = clampi(col[e], N);
+    const float* xi = coord + (int64_t)i * sc;
+    const float* xj = coord + (int64_t)j * sc;
+    const float dx = xi[0] - xj[0], dy = xi[1] - xj[1], dz = xi[2] - xj[2];
+    const float r2 = dx * dx + dy * dy + dz * dz;
+    if (!gmov) {
+      *reinterpret_cast<f32x4*>(out + e * 4) = f32x4{dx, dy, dz, r2};
+      continue;
+    }
+    float s = 1.0f;
+    if (mean) {
+      const int deg = rowptr[i + 1] - rowptr[i];
+      s = 1.0f / (float)(deg > 1 ? deg : 1);
+    }
+    const float* gx = gmov + (int64_t)i * sgx;
+    const float g0 = gx[0] * s, g1 = gx[1] * s, g2 = gx[2] * s;
+    const float gphi = dx * g0 + dy * g1 + dz * g2;
+    *reinterpret_cast<f32x4*>(out + e * 8) = f32x4{r2, gphi, dx, dy};
+    *reinterpret_cast<f32x4*>(out + e * 8 + 4) = f32x4{dz, g0, g1, g2};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -166,12 +199,8 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
       nf[nb] = valid && (e == base || a.erow[e - 1] != a.erow[e]);
       dx[nb] = dy[nb] = dz[nb] = r2[nb] = 0.f;
       if constexpr (EQ) {
-        const float* xi = a.coord + (int64_t)ri[nb] * a.sc;
-        const float* xj = a.coord + (int64_t)rj[nb] * a.sc;
-        dx[nb] = xi[0] - xj[0];
-        dy[nb] = xi[1] - xj[1];
-        dz[nb] = xi[2] - xj[2];
-        r2[nb] = dx[nb] * dx[nb] + dy[nb] * dy[nb] + dz[nb] * dz[nb];
+        const f32x4 q = *reinterpret_cast<const f32x4*>(a.geo + ec * 4);
+        dx[nb] = q[0]; dy[nb] = q[1]; dz[nb] = q[2]; r2[nb] = q[3];
       }
     }
     const uint32_t mask = lo16(__ballot(nf[0])) | (lo16(__ballot(nf[1])) << 16);
@@ -340,7 +369,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
   __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];   // [edge][slot] edge features of the tile
-  __shared__ float s_geo[TE][8];                                  // delta, scaled grad of x_i per edge
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* PQ = (const bf16*)a.PQ;
@@ -425,7 +453,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
     const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
     int ri[2], rj[2], eid[2];
     bool valid[2];
-    float dx[2], dy[2], dz[2], r2[2], gxx[2], gxy[2], gxz[2], gphi[2];
+    float r2[2], gphi[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const int64_t e = base + nb * 16 + c;
@@ -434,31 +462,11 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       ri[nb] = clampi(a.erow[ec], N);
       rj[nb] = clampi(a.col[ec], N);
       eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
-      dx[nb] = dy[nb] = dz[nb] = r2[nb] = gxx[nb] = gxy[nb] = gxz[nb] = gphi[nb] = 0.f;
-      if constexpr (EQ) {
-        const float* xi = a.coord + (int64_t)ri[nb] * a.sc;
-        const float* xj = a.coord + (int64_t)rj[nb] * a.sc;
-        dx[nb] = xi[0] - xj[0];
-        dy[nb] = xi[1] - xj[1];
-        dz[nb] = xi[2] - xj[2];
-        r2[nb] = dx[nb] * dx[nb] + dy[nb] * dy[nb] + dz[nb] * dz[nb];
-        if (valid[nb]) {
-          const float* gx = a.gmov + (int64_t)ri[nb] * a.sgx;
-          float sc = 1.0f;
-          if (a.mean) {
-            const int deg = a.rowptr[ri[nb] + 1] - a.rowptr[ri[nb]];
-            sc = 1.0f / (float)(deg > 1 ? deg : 1);
-          }
-          gxx[nb] = gx[0] * sc;
-          gxy[nb] = gx[1] * sc;
-          gxz[nb] = gx[2] * sc;
-        }
-        gphi[nb] = dx[nb] * gxx[nb] + dy[nb] * gxy[nb] + dz[nb] * gxz[nb];
-        if (w == 0 && g == 0) {
-          float* q = s_geo[nb * 16 + c];
-          q[0] = dx[nb]; q[1] = dy[nb]; q[2] = dz[nb];
-          q[4] = gxx[nb]; q[5] = gxy[nb]; q[6] = gxz[nb];
-        }
+      r2[nb] = gphi[nb] = 0.f;
+      if constexpr (EQ) {   // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
+        const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
+        r2[nb] = q.x;
+        gphi[nb] = valid[nb] ? q.y : 0.f;
       }
     }
 
@@ -653,9 +661,9 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
             pht += s_phi[ww][k];
           }
           const float k2 = 2.0f * grt;
-          const float* q = s_geo[k];
+          const float* q = a.geo + (base + k) * 8;   // delta at 2..4, grad x_i at 5..7
           *reinterpret_cast<f32x4*>(a.Gx + (base + k) * 4) =
-              f32x4{pht * q[4] + k2 * q[0], pht * q[5] + k2 * q[1], pht * q[6] + k2 * q[2], 0.f};
+              f32x4{pht * q[5] + k2 * q[2], pht * q[6] + k2 * q[3], pht * q[7] + k2 * q[4], 0.f};
         }
       }
     }
@@ -743,6 +751,15 @@ int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
 }
 
 }  // namespace
+
+int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* col, const float* coord, int64_t sc,
+                    const float* gmov, int64_t sgx, const int32_t* rowptr, int mean, float* out, hipStream_t st) {
+  if (E <= 0) return 0;
+  const int blocks = (int)std::min<int64_t>(cdiv(E, 256), 8192);
+  hipLaunchKernelGGL(edge_geo_kernel, dim3(blocks), dim3(256), 0, st, E, (int)N, erow, col, coord, sc, gmov, sgx,
+                     rowptr, mean, out);
+  return (int)hipGetLastError();
+}
 
 bool coop_supported(const LayerShape& s) {
   const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);

@@ -55,6 +55,7 @@ struct FwdWs {
   FragSet fr;
   void* PQ;        // [N][2H] activation dtype, chain-permuted per 32 features
   float* carry;    // [ntiles][2][O+4]
+  float* geo;      // cooperative EGNN kernel: [E][4] = delta, r^2 per edge
 };
 struct BwdWs {
   FragSet fr;
@@ -81,6 +82,7 @@ struct BwdWs {
   float* dwsum;
   int nblk;
   int64_t LW;
+  float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
 };
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
@@ -138,6 +140,7 @@ int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K,
 struct FwdArgs {
   int64_t N, E, ntiles;
   int FE, NUC, mean;
+  const float* geo;   // cooperative EGNN kernel: [E][4] = delta, r^2
   const void* PQ;
   const float* coord; int64_t sc;
   const void* ef; int64_t se;
@@ -154,6 +157,7 @@ int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
 struct BwdArgs {
   int64_t N, E, ntiles;
   int FE, NUC, mean;
+  const float* geo;   // cooperative EGNN kernel: [E][8] = r^2, g_phi, delta, grad x_i (/ deg if mean)
   const void* PQ;
   const float* coord; int64_t sc;
   const void* ef; int64_t se;
@@ -173,6 +177,10 @@ int coop_bwd_blocks(const LayerShape& s);
 int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
+// Per-edge geometry records for the cooperative kernels (one thread per edge):
+// forward [E][4] = (delta, r^2); backward [E][8] = (r^2, g_phi, delta, grad x_i / deg).
+int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* col, const float* coord, int64_t sc,
+                    const float* gmov, int64_t sgx, const int32_t* rowptr, int mean, float* out, hipStream_t st);
 int bwd_tile_edges(const LayerShape& s);
 
 // dPQ[n] = [sum_row Gh | sum_csc Gh] (fp32); grad_coord = sum_row Gx - sum_csc Gx
