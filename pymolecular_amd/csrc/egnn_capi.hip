@@ -283,19 +283,30 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       if ((rc = hip_status(launch_sum_rows(w.dwpart, 0, w.LW, w.dwsum, st))) != EGNN_OK) return rc;
     }
   }
+  // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
+  auto splitk2 = [&](Gemm2Args g, float* dst) -> int32_t {
+    g.ksplit = splitk_len(std::max<int64_t>(g.K, 1));
+    g.partial = w.part;
+    const int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
+    ProfScope ps(EGNN_K_WGRAD, st);
+    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    int32_t r = s.E > 0 ? hip_status(launch_gemm2(g, s.bf16, st)) : EGNN_OK;
+    if (r != EGNN_OK) return r;
+    return hip_status(launch_sum_rows(w.part, s.E > 0 ? nsplit : 0, g.M * g.N, dst, st));
+  };
   if (!coop) {
-    GemmArgs g{};
+    Gemm2Args g{};
     g.M = s.H + 1; g.N = s.O; g.K = s.E;
-    g.A = w.Dm1; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = s.H;
-    g.B = w.Dga2; g.sbk = s.O; g.sbn = 1; g.b_bf16 = s.bf16;
-    if ((rc = splitk(g, w.dWhl)) != EGNN_OK) return rc;
+    g.A = w.Dm1; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.H;
+    g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = s.bf16; g.b_nc = 1;
+    if ((rc = splitk2(g, w.dWhl)) != EGNN_OK) return rc;
   }
   if (s.eq && !coop) {
-    GemmArgs g{};
+    Gemm2Args g{};
     g.M = s.O + 1; g.N = s.M; g.K = s.E;
-    g.A = w.Dm; g.sam = 1; g.sak = s.O; g.a_bf16 = s.bf16; g.a_ones_row = s.O;
-    g.B = w.Dgq; g.sbk = s.M; g.sbn = 1; g.b_bf16 = s.bf16;
-    if ((rc = splitk(g, w.dW1m)) != EGNN_OK) return rc;
+    g.A = w.Dm; g.lda = s.O; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.O;
+    g.B = w.Dgq; g.ldb = s.M; g.b_bf16 = s.bf16; g.b_nc = 1;
+    if ((rc = splitk2(g, w.dW1m)) != EGNN_OK) return rc;
     GemmArgs p{};
     p.M = s.M; p.N = 1; p.K = s.E;
     p.A = w.Dp; p.sam = 1; p.sak = s.M; p.a_bf16 = s.bf16; p.a_ones_row = -1;

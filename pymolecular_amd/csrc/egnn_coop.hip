@@ -362,6 +362,8 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   // A-operand fragments of W1_mov (g_m) and W_hl (g_a1), read by their row owners
   __shared__ __attribute__((aligned(16))) bf16 s_wmov[(EQ ? (O / 16) * KM : 1) * kFragElems];
   __shared__ __attribute__((aligned(16))) bf16 s_whl[(H / 16) * KO * kFragElems];
+  // A-operand fragments of W1_mov^T (q = W1_mov^T m), rows M, read by their row owners
+  __shared__ __attribute__((aligned(16))) bf16 s_wmovT[(EQ ? (M / 16) * KO : 1) * kFragElems];
   bf16* const s_m1 = s_buf1;
   bf16* const s_ga2 = s_buf1;
   bf16* const s_m = s_buf2;
@@ -380,7 +382,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   const int FE = a.FE;
 
   bf16x8 wu[BH], whlT[BO][KH];
-  bf16x8 wmovT[BM][EQ ? KO : 1];
   // per-row vectors, read from LDS where they are used: b2 (O), bx1 (M), w2_mov (M), w_d (H)
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
   float* const s_b2 = s_vec;
@@ -404,6 +405,9 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       const int nwm = (O / 16) * KM * kFragElems / 8;
       for (int q = threadIdx.x; q < nwm; q += nthr)
         reinterpret_cast<bf16x8*>(s_wmov)[q] = reinterpret_cast<const bf16x8*>(a.fr.mov)[q];
+      const int nwt = (M / 16) * KO * kFragElems / 8;
+      for (int q = threadIdx.x; q < nwt; q += nthr)
+        reinterpret_cast<bf16x8*>(s_wmovT)[q] = reinterpret_cast<const bf16x8*>(a.fr.movT)[q];
     }
   }
 #pragma unroll
@@ -417,15 +421,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KH; ++kc)
       whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)ob * KH + kc) * kFragElems + l * 8);
-  }
-  if constexpr (EQ) {
-#pragma unroll
-    for (int j = 0; j < BM; ++j) {
-      const int mb = w * BM + j;
-#pragma unroll
-      for (int kc = 0; kc < KO; ++kc)
-        wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)mb * KO + kc) * kFragElems + l * 8);
-    }
   }
   const bf16x8 I = ident_chunk(c, g);
 
@@ -448,27 +443,41 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
   for (int j = 0; j < BM; ++j) vbx1[j] = vw2m[j] = zero4();
 
+  // indices and geometry of a tile, loaded one tile ahead of its use
+  int ri[2], rj[2], eid[2];
+  float r2[2], gphi[2];
+  auto load_tile = [&](int64_t t, int* pri, int* prj, int* peid, float* pr2, float* pgp) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = t * TE + nb * 16 + c;
+      const bool ok = e < E;
+      const int64_t ec = ok ? e : E - 1;
+      pri[nb] = clampi(a.erow[ec], N);
+      prj[nb] = clampi(a.col[ec], N);
+      peid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
+      pr2[nb] = pgp[nb] = 0.f;
+      if constexpr (EQ) {   // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
+        const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
+        pr2[nb] = q.x;
+        pgp[nb] = ok ? q.y : 0.f;
+      }
+    }
+  };
+  if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, ri, rj, eid, r2, gphi);
+
   for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
     const int64_t base = t * TE;
     const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
-    int ri[2], rj[2], eid[2];
     bool valid[2];
-    float r2[2], gphi[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      valid[nb] = e < E;
-      const int64_t ec = valid[nb] ? e : E - 1;
-      ri[nb] = clampi(a.erow[ec], N);
-      rj[nb] = clampi(a.col[ec], N);
-      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
-      r2[nb] = gphi[nb] = 0.f;
-      if constexpr (EQ) {   // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
-        const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
-        r2[nb] = q.x;
-        gphi[nb] = valid[nb] ? q.y : 0.f;
-      }
-    }
+    for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
+    // rows of the incoming message gradient (used in S4), issued early
+    bf16x4 gmr[BO][2];
+#pragma unroll
+    for (int j = 0; j < BO; ++j)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        gmr[j][nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri[nb] * a.sgm + 16 * (w * BO + j) + 4 * g);
 
     // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
     bf16x8 u[2];
@@ -541,12 +550,16 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
         const int mb = w * BM + j;
         const f32x4 bx1v = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * mb + 4 * g);
         const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * mb + 4 * g);
-        f32x4 gq[2];
+        f32x4 gq[2], accq[2] = {zero4(), zero4()};
+#pragma unroll
+        for (int kc = 0; kc < KO; ++kc) {   // each A fragment read once for both edge blocks
+          const bf16x8 A = *reinterpret_cast<const bf16x8*>(s_wmovT + ((mb * KO + kc) * 64 + l) * 8);
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) mma(accq[nb], A, get_chain(s_m, kc, nb, l));
+        }
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
+          const f32x4 acc = accq[nb];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const YD r = silu_yd<bf16>(acc[i] + bx1v[i]);
@@ -568,20 +581,30 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
     }
     __syncthreads();
 
+    // the next tile's indices (consumed by the next iteration)
+    int n_ri[2], n_rj[2], n_eid[2];
+    float n_r2[2], n_gphi[2];
+    const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
+    load_tile(tn, n_ri, n_rj, n_eid, n_r2, n_gphi);
+
     // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
 #pragma unroll
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;
-      f32x4 ga[2];
+      f32x4 ga[2], acca[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acca[nb] = valid[nb] ? unpack4(gmr[j][nb]) : zero4();
+      if constexpr (EQ) {
+#pragma unroll
+        for (int kc = 0; kc < KM; ++kc) {
+          const bf16x8 A = *reinterpret_cast<const bf16x8*>(s_wmov + ((ob * KM + kc) * 64 + l) * 8);
+#pragma unroll
+          for (int nb = 0; nb < 2; ++nb) mma(acca[nb], A, get_chain(s_gq, kc, nb, l));
+        }
+      }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        f32x4 acc = valid[nb] ? load4_f32(gmsg + (int64_t)ri[nb] * a.sgm + 16 * ob + 4 * g) : zero4();
-        if constexpr (EQ) {
-#pragma unroll
-          for (int kc = 0; kc < KM; ++kc)
-            mma(acc, *reinterpret_cast<const bf16x8*>(s_wmov + ((ob * KM + kc) * 64 + l) * 8),
-                get_chain(s_gq, kc, nb, l));
-        }
+        const f32x4 acc = acca[nb];
         const f32x4 d = unpack4(s2[j][nb]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -607,14 +630,16 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
     for (int j = 0; j < BH; ++j) {
       const int hb = w * BH + j;
       const f32x4 wdv = EQ ? *reinterpret_cast<const f32x4*>(s_wd + 16 * hb + 4 * g) : zero4();
-      f32x4 g1[2];
+      f32x4 g1[2], acch[2] = {zero4(), zero4()};
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc) {
+        const bf16x8 A = *reinterpret_cast<const bf16x8*>(s_whl + ((hb * KO + kc) * 64 + l) * 8);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) mma(acch[nb], A, get_chain(s_ga2, kc, nb, l));
+      }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int kc = 0; kc < KO; ++kc)
-          mma(acc, *reinterpret_cast<const bf16x8*>(s_whl + ((hb * KO + kc) * 64 + l) * 8),
-              get_chain(s_ga2, kc, nb, l));
+        const f32x4 acc = acch[nb];
         const f32x4 d = unpack4(s1[j][nb]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -668,6 +693,10 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       }
     }
     __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      ri[nb] = n_ri[nb]; rj[nb] = n_rj[nb]; eid[nb] = n_eid[nb]; r2[nb] = n_r2[nb]; gphi[nb] = n_gphi[nb];
+    }
   }
 
   // ---- this block's weight-gradient partial ---------------------------------
