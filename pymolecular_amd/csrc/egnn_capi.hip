@@ -174,8 +174,9 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   }
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
-    if ((rc = hip_status(coop_supported(s) ? launch_coop_fwd(s, a, st) : launch_fwd(s, a, 0, st))) != EGNN_OK)
-      return rc;
+    const int r = coop_supported(s) ? launch_coop_fwd(s, a, st)
+                  : wide_supported(s) ? launch_wide_fwd(s, a, st) : launch_fwd(s, a, 0, st);
+    if ((rc = hip_status(r)) != EGNN_OK) return rc;
   }
   ProfScope ps(EGNN_K_FWD_FIXUP, st);
   return hip_status(launch_fwd(s, a, 1, st));
@@ -238,10 +239,12 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
                                          rowptr, s.mean, w.geo, st))) != EGNN_OK)
       return rc;
   }
-  if (coop) a.ntiles = cdiv(s.E, kTileEdges);
+  if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
-    if ((rc = hip_status(coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_bwd(s, a, st))) != EGNN_OK) return rc;
+    const int r = coop ? launch_coop_bwd(s, a, w.nblk, st)
+                  : wide_supported(s) ? launch_wide_bwd(s, a, st) : launch_bwd(s, a, st);
+    if ((rc = hip_status(r)) != EGNN_OK) return rc;
   }
 
   // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)

@@ -23,86 +23,13 @@
 // the same quantities one program per CSR row.
 #include "egnn_device.h"
 #include "egnn_internal.h"
+#include "egnn_tile.h"
 
 namespace egnn {
 namespace {
 
-constexpr int TE = kTileEdges;  // 32 edges = two 16-column MFMA blocks
+using namespace tile;
 
-__device__ __forceinline__ bf16x4 pack4(const f32x4& v) {
-  bf16x4 r;
-  r[0] = (bf16)v[0]; r[1] = (bf16)v[1]; r[2] = (bf16)v[2]; r[3] = (bf16)v[3];
-  return r;
-}
-__device__ __forceinline__ f32x4 unpack4(const bf16x4& v) {
-  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
-}
-__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
-
-// chain buffer: chunk (kc, nb) = 64 lanes x 8 bf16; 16-row block blk fills half (blk & 1) of chunk blk >> 1
-__device__ __forceinline__ void put_chain(bf16* buf, int blk, int nb, int l, const f32x4& v) {
-  *reinterpret_cast<bf16x4*>(buf + (((blk >> 1) * 2 + nb) * 64 + l) * 8 + 4 * (blk & 1)) = pack4(v);
-}
-__device__ __forceinline__ bf16x8 get_chain(const bf16* buf, int kc, int nb, int l) {
-  return *reinterpret_cast<const bf16x8*>(buf + ((kc * 2 + nb) * 64 + l) * 8);
-}
-// edge-major buffer: feature block blk, lane (c = feature, g) holds 8 edges in kappa_chain order
-__device__ __forceinline__ void put_norm(bf16* buf, int blk, int l, const bf16x8& v) {
-  *reinterpret_cast<bf16x8*>(buf + (blk * 64 + l) * 8) = v;
-}
-__device__ __forceinline__ bf16x8 get_norm(const bf16* buf, int blk, int l) {
-  return *reinterpret_cast<const bf16x8*>(buf + (blk * 64 + l) * 8);
-}
-
-// B operand that transposes one 16-row C-block: B[s][n] = (s < 4 && 4g + s == n)
-__device__ __forceinline__ bf16x8 ident_chunk(int c, int g) {
-  bf16x8 r = zero_chunk<bf16>();
-  const int s = c - 4 * g;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) r[q] = (s == q) ? (bf16)1.0f : (bf16)0.0f;
-  return r;
-}
-// C-block (rows = 16 features, col = edge c) -> C-block (col = feature c, rows = edges 4g+i), bf16-rounded
-__device__ __forceinline__ f32x4 transpose_block(const f32x4& v, const bf16x8& I) {
-  bf16x8 a = zero_chunk<bf16>();
-  a[0] = (bf16)v[0]; a[1] = (bf16)v[1]; a[2] = (bf16)v[2]; a[3] = (bf16)v[3];
-  f32x4 t = zero4();
-  mma(t, a, I);
-  return t;
-}
-// edge-major chunk of a feature block over the 32 edges of the tile (kappa_chain over edges)
-__device__ __forceinline__ bf16x8 edge_major(const f32x4& nb0, const f32x4& nb1, const bf16x8& I) {
-  return pack_chunk<bf16>(transpose_block(nb0, I), transpose_block(nb1, I));
-}
-
-__device__ __forceinline__ int rank_of(uint32_t mask, int k) {
-  const uint32_t below = (k >= 31) ? 0xffffffffu : ((2u << k) - 1u);
-  return __popc(mask & below) - 1;
-}
-// B operand S[edge][rank]: column n = rank 16*rb + c, rows = edges kappa_chain(g, s)
-__device__ __forceinline__ bf16x8 seg_chunk(uint32_t mask, int nvalid, int rb, int c, int g) {
-  bf16x8 r;
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int k = kappa_chain(g, s);
-    r[s] = (k < nvalid && rank_of(mask, k) == 16 * rb + c) ? (bf16)1.0f : (bf16)0.0f;
-  }
-  return r;
-}
-
-__device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int eid, int FE, int g, float r2, bool eq) {
-  const int slot0 = 8 * g;
-  if (slot0 + 8 <= FE) return load_chunk(ef + (int64_t)eid * se + slot0);
-  bf16x8 z = zero_chunk<bf16>();
-  if (eq && slot0 == FE) {
-    const bf16 hi = (bf16)r2;
-    z[0] = hi;
-    z[1] = (bf16)(r2 - (float)hi);
-  }
-  return z;
-}
-
-__device__ __forceinline__ uint32_t lo16(unsigned long long b) { return (uint32_t)(b & 0xffffull); }
 
 // One thread per edge: delta = x_i - x_j and r^2 (forward record), plus the
 // incoming coordinate gradient of row i (scaled by 1/deg for mean aggregation)

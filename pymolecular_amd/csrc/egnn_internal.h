@@ -177,6 +177,11 @@ int coop_bwd_blocks(const LayerShape& s);
 int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
+// Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
+// from L2, backward writes the per-edge weight-gradient factors (Dm1 ... R2).
+bool wide_supported(const LayerShape& s);
+int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
+int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 // Per-edge geometry records for the cooperative kernels (one thread per edge):
 // forward [E][4] = (delta, r^2); backward [E][8] = (r^2, g_phi, delta, grad x_i / deg).
 int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* col, const float* coord, int64_t sc,

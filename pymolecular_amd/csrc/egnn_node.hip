@@ -58,7 +58,7 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
   w->PQ = b ? b + off : nullptr; off = align_up(off + (size_t)s.N * 2 * s.H * s.esz);
   int64_t ntiles = cdiv(s.E, kTileEdges);
   w->carry = (float*)(b ? b + off : nullptr); off = align_up(off + (size_t)ntiles * 2 * (s.O + 4) * sizeof(float));
-  const bool geo = s.eq && coop_supported(s);
+  const bool geo = s.eq && (coop_supported(s) || wide_supported(s));
   w->geo = (float*)(b && geo ? b + off : nullptr);
   if (geo) off = align_up(off + (size_t)std::max<int64_t>(s.E, 1) * 4 * sizeof(float));
   return off;
@@ -84,7 +84,7 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Gh = take(E * s.H * s.esz);
   w->Gx = (float*)take(E * 4 * sizeof(float));
   w->R2 = coop ? nullptr : (float*)take(E * sizeof(float));
-  w->geo = (coop && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
+  w->geo = ((coop || wide_supported(s)) && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
   w->nblk = coop ? coop_bwd_blocks(s) : 0;
   w->LW = coop ? coop_dw_len(s) : 0;
   w->dwpart = coop ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
