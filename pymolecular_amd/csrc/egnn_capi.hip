@@ -268,16 +268,6 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   }
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
-  auto splitk = [&](GemmArgs g, float* dst) -> int32_t {
-    g.ksplit = splitk_len(std::max<int64_t>(g.K, 1));
-    g.partial = w.part;
-    int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
-    ProfScope ps(EGNN_K_WGRAD, st);
-    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
-    int32_t r = hip_status(launch_gemm(g, s.bf16, st));
-    if (r != EGNN_OK) return r;
-    return hip_status(launch_sum_rows(w.part, nsplit, g.M * g.N, dst, st));
-  };
   if (coop) {
     ProfScope ps(EGNN_K_WGRAD, st);
     if (s.E > 0) {
@@ -310,23 +300,23 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     g.A = w.Dm; g.lda = s.O; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.O;
     g.B = w.Dgq; g.ldb = s.M; g.b_bf16 = s.bf16; g.b_nc = 1;
     if ((rc = splitk2(g, w.dW1m)) != EGNN_OK) return rc;
-    GemmArgs p{};
+    Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (g_phi in column 3 of Gx)
     p.M = s.M; p.N = 1; p.K = s.E;
-    p.A = w.Dp; p.sam = 1; p.sak = s.M; p.a_bf16 = s.bf16; p.a_ones_row = -1;
-    p.B = w.Gx + 3; p.sbk = 4; p.sbn = 0; p.b_bf16 = 0;
-    if ((rc = splitk(p, w.dw2m)) != EGNN_OK) return rc;
-    GemmArgs d{};
+    p.A = w.Dp; p.lda = s.M; p.a_bf16 = s.bf16; p.a_kc = 0; p.a_ones_row = -1;
+    p.B = w.Gx + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
+    if ((rc = splitk2(p, w.dw2m)) != EGNN_OK) return rc;
+    Gemm2Args d{};   // dw_d = sum_e g_a1[e] r^2[e]
     d.M = s.H; d.N = 1; d.K = s.E;
-    d.A = w.Gh; d.sam = 1; d.sak = s.H; d.a_bf16 = s.bf16; d.a_ones_row = -1;
-    d.B = w.R2; d.sbk = 1; d.sbn = 0; d.b_bf16 = 0;
-    if ((rc = splitk(d, w.dwd)) != EGNN_OK) return rc;
+    d.A = w.Gh; d.lda = s.H; d.a_bf16 = s.bf16; d.a_kc = 0; d.a_ones_row = -1;
+    d.B = w.R2; d.ldb = 1; d.b_bf16 = 0; d.b_nc = 1;
+    if ((rc = splitk2(d, w.dwd)) != EGNN_OK) return rc;
   }
-  if (s.FE > 0 && !coop) {
-    GemmArgs g{};
+  if (s.FE > 0 && !coop) {   // dW_e = sum_e g_a1[e] e[edge_ids[e]]
+    Gemm2Args g{};
     g.M = s.H; g.N = s.FE; g.K = s.E;
-    g.A = w.Gh; g.sam = 1; g.sak = s.H; g.a_bf16 = s.bf16; g.a_ones_row = -1;
-    g.B = edge_feat; g.sbk = strides->edge; g.sbn = 1; g.b_bf16 = s.bf16; g.b_kidx = edge_ids;
-    if ((rc = splitk(g, w.dWe)) != EGNN_OK) return rc;
+    g.A = w.Gh; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = -1;
+    g.B = edge_feat; g.ldb = strides->edge; g.b_bf16 = s.bf16; g.b_nc = 1; g.b_kidx = edge_ids;
+    if ((rc = splitk2(g, w.dWe)) != EGNN_OK) return rc;
   }
   {
     // [dW_n1 | dW_n2 ; db1 | .] = [h | 1]^T [dP | dQ], split over nodes, fixed-order sum

@@ -96,22 +96,6 @@ size_t schedule_tmp_bytes(int64_t N, int64_t E);
 int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
                 const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st);
 
-// Generic MFMA GEMM: C(m,n) = sum_k A(m,k) B(k,n) [+ bias(n)], fp32 accumulate.
-struct GemmArgs {
-  int64_t M, N, K;
-  const void* A; int64_t sam, sak; int a_bf16; int64_t a_ones_row;  // row index that reads as all-ones (-1: none)
-  const void* B; int64_t sbk, sbn; int b_bf16;
-  const int32_t* b_kidx;          // non-null: B's k index goes through b_kidx[k] (edge_ids gather)
-  int64_t b_kjump_at, b_kjump;    // B offset += b_kjump for k >= b_kjump_at (two stacked blocks)
-  int64_t b_njump_at, b_njump;    // B offset += b_njump for n >= b_njump_at (two side-by-side blocks)
-  const void* bias; int bias_bf16; int64_t bias_len;   // bias(n) for n < bias_len
-  void* C; int64_t scm, scn; int c_bf16;
-  int perm_half;        // >0: column n stored at chain-permuted position within 32-column groups
-  float* partial;       // split-K partial output [split][M][N] (then C unused)
-  int64_t ksplit;       // K per split (0: no split)
-};
-int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st);
-
 // Node-level GEMM with 16-byte loads along the contiguous dimension of each
 // operand.  A is (M x K) row-major ("k contiguous") or given as its transpose
 // (K x M row-major, "m contiguous"); B is (K x N) row-major ("n contiguous") or
@@ -132,6 +116,7 @@ struct Gemm2Args {
   int act; void* Cpre; int64_t ldpre;
   const void* resid; int64_t ldr; int64_t resid_len;
   const void* zd; int64_t ldz;
+  const int32_t* b_kidx;   // n-contiguous B only: row k of B is row b_kidx[k] of the array
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
 int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,

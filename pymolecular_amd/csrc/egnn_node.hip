@@ -206,7 +206,7 @@ int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void*
 }
 
 // ---------------------------------------------------------------------------
-// generic MFMA GEMM (64 x 64 tile per 4-wave block, k step 32)
+// node-level GEMM helpers
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int ce_minus(const int32_t* p, int64_t n) { return p[n + 1] - p[n]; }
 
@@ -219,84 +219,6 @@ __device__ __forceinline__ int chain_pos(int f) {
   return f < 16 ? 8 * (f >> 2) + (f & 3) : 8 * ((f - 16) >> 2) + 4 + ((f - 16) & 3);
 }
 
-template <typename TC>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  constexpr int BM = 64, BN = 64, BK = 32, PAD = sizeof(TC) == 2 ? 8 : 4, LDK = BK + PAD;
-  __shared__ __attribute__((aligned(16))) TC As[BM * LDK];
-  __shared__ __attribute__((aligned(16))) TC Bs[BN * LDK];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
-  int64_t kbeg = 0, kend = g.K;
-  if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
-  f32x4 acc[2][2];
-  for (int a = 0; a < 2; ++a) for (int b = 0; b < 2; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
-    // walk the tile along whichever operand dimension is contiguous in memory
-    const bool a_m_fast = g.sam == 1 && g.sak != 1;
-    const bool b_k_fast = g.sbk == 1 && g.sbn != 1 && !g.b_kidx;
-    for (int it = 0; it < (BM * BK) / 256; ++it) {
-      int idx = tid + it * 256;
-      int mm = a_m_fast ? idx % BM : idx / BK, kk = a_m_fast ? idx / BM : idx % BK;
-      int64_t m = m0 + mm, k = k0 + kk;
-      float v = 0.0f;
-      if (m < g.M && k < kend) v = (m == g.a_ones_row) ? 1.0f : ld_elem(g.A, m * g.sam + k * g.sak, g.a_bf16);
-      As[mm * LDK + kk] = from_f32<TC>(v);
-    }
-    for (int it = 0; it < (BN * BK) / 256; ++it) {
-      int idx = tid + it * 256;
-      int nn = b_k_fast ? idx / BK : idx % BN, kk = b_k_fast ? idx % BK : idx / BN;
-      int64_t n = n0 + nn, k = k0 + kk;
-      float v = 0.0f;
-      if (n < g.N && k < kend) {
-        const int64_t kk2 = g.b_kidx ? (int64_t)clampi(g.b_kidx[k], (int)g.K) : k;
-        const int64_t off = kk2 * g.sbk + n * g.sbn + (k >= g.b_kjump_at ? g.b_kjump : 0) + (n >= g.b_njump_at ? g.b_njump : 0);
-        v = ld_elem(g.B, off, g.b_bf16);
-      }
-      Bs[nn * LDK + kk] = from_f32<TC>(v);
-    }
-    __syncthreads();
-    typedef typename ChunkOf<TC>::type Ch;
-    Ch a[2], b[2];
-    for (int i = 0; i < 2; ++i) {
-      a[i] = load_chunk(&As[(wm * 32 + i * 16 + c) * LDK + 8 * gq]);
-      b[i] = load_chunk(&Bs[(wn * 32 + i * 16 + c) * LDK + 8 * gq]);
-    }
-    for (int i = 0; i < 2; ++i)
-      for (int j = 0; j < 2; ++j) mma(acc[i][j], a[i], b[j]);
-    __syncthreads();
-  }
-  for (int i = 0; i < 2; ++i)
-    for (int j = 0; j < 2; ++j)
-      for (int r = 0; r < 4; ++r) {
-        int64_t m = m0 + wm * 32 + i * 16 + 4 * gq + r;
-        int64_t n = n0 + wn * 32 + j * 16 + c;
-        if (m >= g.M || n >= g.N) continue;
-        float v = acc[i][j][r];
-        if (g.partial) {
-          g.partial[((int64_t)blockIdx.z * g.M + m) * g.N + n] = v;
-          continue;
-        }
-        if (g.bias && n < g.bias_len) v += ld_elem(g.bias, n, g.bias_bf16);
-        int64_t pn = n;
-        if (g.perm_half > 0) {
-          int64_t half = n / g.perm_half, f = n % g.perm_half;
-          pn = half * g.perm_half + (f & ~31) + chain_pos((int)(f & 31));
-        }
-        int64_t off = m * g.scm + pn * g.scn;
-        if (g.c_bf16) ((bf16*)g.C)[off] = (bf16)v;
-        else ((float*)g.C)[off] = v;
-      }
-}
-
-int launch_gemm(const GemmArgs& g, bool compute_bf16, hipStream_t st) {
-  if (g.M <= 0 || g.N <= 0) return 0;
-  unsigned gz = g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
-  dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
-  if (compute_bf16) hipLaunchKernelGGL(gemm_kernel<bf16>, grid, dim3(256), 0, st, g);
-  else hipLaunchKernelGGL(gemm_kernel<float>, grid, dim3(256), 0, st, g);
-  return (int)hipGetLastError();
-}
 
 // ---------------------------------------------------------------------------
 // node-level GEMM with vector loads (64 x 64 tile per 4-wave block, k step 32)
@@ -368,19 +290,20 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
     // ---- B tile -> Bs[n][k]
     constexpr int NVB = BN * BK / VB;
     for (int v = tid; v < NVB; v += 256) {
-      if constexpr (B_NC) {   // B[k * ldb + n]
+      if constexpr (B_NC) {   // B[k * ldb + n], or B[b_kidx[k] * ldb + n]
         const int kk = v / (BN / VB), nn = (v % (BN / VB)) * VB;
         const int64_t k = k0 + kk, n = n0 + nn;
         const bool full = k < kend && n + VB <= g.N;
+        const int64_t kr = (g.b_kidx && k < kend) ? (int64_t)g.b_kidx[k] : k;
         if (full) {
-          const auto vv = ld16(B + k * g.ldb + n);
+          const auto vv = ld16(B + kr * g.ldb + n);
 #pragma unroll
           for (int u = 0; u < VB; ++u) Bs[(nn + u) * LDK + kk] = from_f32<TC>((float)vv[u]);
         } else {
 #pragma unroll
           for (int u = 0; u < VB; ++u) {
             float x = 0.f;
-            if (k < kend && n + u < g.N) x = to_f32(B[k * g.ldb + n + u]);
+            if (k < kend && n + u < g.N) x = to_f32(B[kr * g.ldb + n + u]);
             Bs[(nn + u) * LDK + kk] = from_f32<TC>(x);
           }
         }
