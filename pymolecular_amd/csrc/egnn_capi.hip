@@ -232,6 +232,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
   const bool coop = coop_supported(s);
   a.dwpart = w.dwpart; a.LW = w.LW;
+  a.ldE = w.ldE;
   a.geo = w.geo;
   if (w.geo) {
     ProfScope ps(EGNN_K_PREP, st);
@@ -287,14 +288,46 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     if (r != EGNN_OK) return r;
     return hip_status(launch_sum_rows(w.part, s.E > 0 ? nsplit : 0, g.M * g.N, dst, st));
   };
-  if (!coop) {
+  const bool wide = wide_supported(s);
+  // wide kernels: feature-major bf16 factors, [A | bias row]^T B by the edge-factor GEMM
+  auto wgrad = [&](const void* A, const void* B, int64_t M, int64_t N, float* dst) -> int32_t {
+    WgradArgs g{};
+    g.M = M; g.N = N; g.K = s.E;
+    g.A = (const bf16*)A; g.lda = w.ldE;
+    g.B = (const bf16*)B; g.ldb = w.ldE;
+    g.ksplit = wgrad_ksplit(s.E);
+    g.partial = w.part; g.b_colsum = 1;
+    const int64_t nsplit = cdiv(std::max<int64_t>(s.E, 1), g.ksplit);
+    if (nsplit * (M + 1) * N > w.part_elems) return EGNN_ERR_WORKSPACE;
+    ProfScope ps(EGNN_K_WGRAD, st);
+    int32_t r = s.E > 0 ? hip_status(launch_wgrad_gemm(g, st)) : EGNN_OK;
+    if (r != EGNN_OK) return r;
+    return hip_status(launch_sum_rows(w.part, s.E > 0 ? nsplit : 0, (M + 1) * N, dst, st));
+  };
+  if (wide) {
+    if ((rc = wgrad(w.Dm1, w.Dga2, s.H, s.O, w.dWhl)) != EGNN_OK) return rc;   // [dW_hl ; db2]
+    if (s.eq) {
+      if ((rc = wgrad(w.Dm, w.Dgq, s.O, s.M, w.dW1m)) != EGNN_OK) return rc;  // [dW1_mov ; dbx1]
+      Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (p feature-major, g_phi in column 3 of Gx)
+      p.M = s.M; p.N = 1; p.K = s.E;
+      p.A = w.Dp; p.lda = w.ldE; p.a_bf16 = 1; p.a_kc = 1; p.a_ones_row = -1;
+      p.B = w.Gx + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
+      if ((rc = splitk2(p, w.dw2m)) != EGNN_OK) return rc;
+      Gemm2Args d{};   // dw_d = sum_e g_a1[e] r^2[e]
+      d.M = s.H; d.N = 1; d.K = s.E;
+      d.A = w.Gh; d.lda = s.H; d.a_bf16 = 1; d.a_kc = 0; d.a_ones_row = -1;
+      d.B = w.R2; d.ldb = 1; d.b_bf16 = 0; d.b_nc = 1;
+      if ((rc = splitk2(d, w.dwd)) != EGNN_OK) return rc;
+    }
+  }
+  if (!coop && !wide) {
     Gemm2Args g{};
     g.M = s.H + 1; g.N = s.O; g.K = s.E;
     g.A = w.Dm1; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.H;
     g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = s.bf16; g.b_nc = 1;
     if ((rc = splitk2(g, w.dWhl)) != EGNN_OK) return rc;
   }
-  if (s.eq && !coop) {
+  if (s.eq && !coop && !wide) {
     Gemm2Args g{};
     g.M = s.O + 1; g.N = s.M; g.K = s.E;
     g.A = w.Dm; g.lda = s.O; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.O;

@@ -83,6 +83,7 @@ struct BwdWs {
   int nblk;
   int64_t LW;
   float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
+  int64_t ldE;     // row pitch of the factors (feature-major for the wide kernels)
 };
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
@@ -119,6 +120,19 @@ struct Gemm2Args {
   const int32_t* b_kidx;   // n-contiguous B only: row k of B is row b_kidx[k] of the array
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
+// Weight-gradient GEMM over edges with k-contiguous bf16 operands (feature-major
+// per-edge factors): partial[z][m][n] = sum_{k in split z} A[m][k] B[n][k];
+// b_colsum adds row M = sum_k B[n][k].  ksplit is a multiple of 64.
+struct WgradArgs {
+  int64_t M, N, K;
+  const bf16* A; int64_t lda;
+  const bf16* B; int64_t ldb;
+  int64_t ksplit;
+  float* partial;    // [nsplit][M (+1)][N]
+  int b_colsum;
+};
+int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st);
+int64_t wgrad_ksplit(int64_t K);   // k per split of the edge-factor GEMMs (multiple of 64)
 int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,
                          void* gw2, void* gb2, hipStream_t st);
 
@@ -153,6 +167,7 @@ struct BwdArgs {
   void* Dm1; void* Dm; void* Dgq; void* Dga2; void* Dp; void* Gh; float* Gx; float* R2;
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
+  int64_t ldE;     // wide kernels: row pitch of the feature-major factors Dm1 ... Dp
 };
 int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 

@@ -69,12 +69,19 @@ int64_t splitk_len(int64_t K) {
   return cdiv(ks, 32) * 32;
 }
 
+int64_t wgrad_ksplit(int64_t K) {
+  const int64_t ks = std::max<int64_t>(512, cdiv(std::max<int64_t>(K, 1), 128));
+  return cdiv(ks, 64) * 64;
+}
+
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   char* b = (char*)base;
   size_t off = frag_layout(s, b, &w->fr, 0, true);
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
-  const size_t E = (size_t)std::max<int64_t>(s.E, 1);
-  const bool coop = coop_supported(s);
+  const bool coop = coop_supported(s), wide = wide_supported(s);
+  // wide kernels store the factors feature-major with a 16-byte aligned row pitch
+  w->ldE = wide ? (int64_t)align_up((size_t)std::max<int64_t>(s.E, 1), 8) : std::max<int64_t>(s.E, 1);
+  const size_t E = (size_t)w->ldE;
   w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
   w->Dm1 = coop ? nullptr : take(E * s.H * s.esz);
   w->Dm = coop ? nullptr : take(E * s.O * s.esz);
@@ -95,6 +102,11 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   int64_t pe = coop ? 0 : std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
                                              (int64_t)s.H * std::max(s.FE, 1), (int64_t)s.H});
   w->part_elems = std::max<int64_t>(se * pe, sn * (int64_t)(s.F + 1) * 2 * s.H);
+  if (wide) {
+    const int64_t ks = wgrad_ksplit(s.E);
+    const int64_t nw = cdiv(std::max<int64_t>(s.E, 1), ks);
+    w->part_elems = std::max<int64_t>(w->part_elems, nw * (int64_t)(std::max(s.H, s.O) + 1) * std::max(s.O, s.M));
+  }
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
   w->dW1m = (float*)take((size_t)(s.O + 1) * s.M * sizeof(float));
@@ -605,6 +617,136 @@ int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K,
   else
     hipLaunchKernelGGL(node_finalize_kernel<float>, dim3(blocks), dim3(256), 0, st, S1, S2, K, Hn, Fo, (float*)gw1,
                        (float*)gb1, (float*)gw2, (float*)gb2);
+  return (int)hipGetLastError();
+}
+
+
+// ---------------------------------------------------------------------------
+// weight-gradient GEMM over edges: partial[z][m][n] = sum_{k in split z} A[m][k] B[n][k]
+// ---------------------------------------------------------------------------
+// A (M x K) and B (N x K) are bf16 with k contiguous (feature-major per-edge
+// factors), K = number of edges.  128 x 128 output tile per 4-wave block
+// (each wave 64 x 64 = 4 x 4 MFMA blocks), k step 64, double-buffered LDS,
+// operand rows copied to LDS with 16-byte loads and stores.  With b_colsum,
+// the blocks of the first M tile also write sum_k B[n][k] as row M (the bias
+// gradient that rides along with a weight gradient).
+namespace {
+constexpr int WG_BM = 128, WG_BN = 128, WG_BK = 64, WG_P = WG_BK + 8;
+}
+
+__global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16 As[2][WG_BM * WG_P];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[2][WG_BN * WG_P];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * WG_BM, n0 = (int64_t)blockIdx.y * WG_BN;
+  const int64_t kbeg = (int64_t)blockIdx.z * g.ksplit;
+  const int64_t kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
+  const bool colsum = g.b_colsum && blockIdx.x == 0;
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float bsum[4] = {0.f, 0.f, 0.f, 0.f};
+
+  // thread -> (row, 8-element k segment) of the 128 x 64 operand tiles, 4 per operand
+  bf16x8 ra[4], rb[4];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
+      const int64_t k = k0 + 8 * q;
+      const int64_t m = m0 + r, n = n0 + r;
+      bf16x8 va = zero_chunk<bf16>(), vb = zero_chunk<bf16>();
+      if (k + 8 <= kend) {
+        if (m < g.M) va = *reinterpret_cast<const bf16x8*>(g.A + m * g.lda + k);
+        if (n < g.N) vb = *reinterpret_cast<const bf16x8*>(g.B + n * g.ldb + k);
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (k + u < kend) {
+            if (m < g.M) va[u] = g.A[m * g.lda + k + u];
+            if (n < g.N) vb[u] = g.B[n * g.ldb + k + u];
+          }
+        }
+      }
+      ra[i] = va;
+      rb[i] = vb;
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
+      *reinterpret_cast<bf16x8*>(&As[buf][r * WG_P + 8 * q]) = ra[i];
+      *reinterpret_cast<bf16x8*>(&Bs[buf][r * WG_P + 8 * q]) = rb[i];
+      if (colsum) {
+        float t = 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) t += (float)rb[i][u];
+        bsum[i] += t;
+      }
+    }
+  };
+
+  int buf = 0;
+  if (kbeg < kend) {
+    load_stage(kbeg);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int64_t k0 = kbeg; k0 < kend; k0 += WG_BK) {
+    const bool more = k0 + WG_BK < kend;
+    if (more) load_stage(k0 + WG_BK);
+#pragma unroll
+    for (int ks = 0; ks < WG_BK / 32; ++ks) {
+      bf16x8 a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(wm * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
+        b[i] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(wn * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
+    }
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  float* P = g.partial + (int64_t)blockIdx.z * (g.M + (g.b_colsum ? 1 : 0)) * g.N;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * 64 + i * 16 + 4 * gq + r;
+        const int64_t n = n0 + wn * 64 + j * 16 + c;
+        if (m < g.M && n < g.N) P[m * g.N + n] = acc[i][j][r];
+      }
+  if (colsum) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float t = bsum[i];
+      t += __shfl_xor(t, 1, 64);
+      t += __shfl_xor(t, 2, 64);
+      t += __shfl_xor(t, 4, 64);
+      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
+      const int64_t n = n0 + r;
+      if (q == 0 && n < g.N) P[g.M * g.N + n] = t;
+    }
+  }
+}
+
+int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st) {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0) return 0;
+  const dim3 grid((unsigned)cdiv(g.M, WG_BM), (unsigned)cdiv(g.N, WG_BN), (unsigned)cdiv(g.K, g.ksplit));
+  hipLaunchKernelGGL(wgrad_gemm_kernel, grid, dim3(256), 0, st, g);
   return (int)hipGetLastError();
 }
 

@@ -10,8 +10,9 @@
 //    global memory (L2) in the stage that uses them;
 //  * register-resident weight-gradient accumulators would need 256 KB per
 //    matrix per workgroup, so the backward writes the per-edge factors of the
-//    weight gradients (m1, m, g_q, p, g_a2, like the one-wave-per-tile path)
-//    and fixed-order split-K GEMMs reduce them.
+//    weight gradients (m1, m, g_q, p, g_a2) feature-major ([feature][edge],
+//    turned edge-major in registers by identity MFMAs) and fixed-order
+//    split-K GEMMs with k-contiguous operands reduce them.
 // Edge inputs of up to NUC x 32 slots ([e | r^2 hi | r^2 lo]) are supported.
 // Reference: forward_kernel.py:89-153 and backward_kernel.py:143-257 compute
 // the same quantities one program per CSR row.
@@ -39,6 +40,27 @@ __device__ __forceinline__ bf16x8 input_chunk_u(const bf16* ef, int64_t se, int 
 }
 
 __device__ __forceinline__ void store_bf16x4(bf16* p, const f32x4& v) { *reinterpret_cast<bf16x4*>(p) = pack4(v); }
+
+// Feature-major store of one 16-feature block of a tile: v is the edge-major
+// chunk of lane (c = feature 16 b + c, g) over the edges kappa_chain(g, s);
+// DT[f][e] with row pitch ldE (a multiple of 8).  Edges past E are not written.
+__device__ __forceinline__ void store_fmajor(bf16* DT, int64_t ldE, int64_t row, int64_t base, int64_t E, int g,
+                                             const bf16x8& v) {
+  bf16* p = DT + row * ldE + base;
+  if (base + TE <= E) {
+    bf16x4 lo, hi;
+    lo[0] = v[0]; lo[1] = v[1]; lo[2] = v[2]; lo[3] = v[3];
+    hi[0] = v[4]; hi[1] = v[5]; hi[2] = v[6]; hi[3] = v[7];
+    *reinterpret_cast<bf16x4*>(p + 4 * g) = lo;
+    *reinterpret_cast<bf16x4*>(p + 16 + 4 * g) = hi;
+  } else {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int k = kappa_chain(g, s);
+      if (base + k < E) p[k] = v[s];
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------
 // forward
@@ -293,6 +315,8 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
   }
   __syncthreads();
 
+  const bf16x8 I = ident_chunk(c, g);
+
   for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
     const int64_t base = t * TE;
     int ri[2], rj[2], eid[2];
@@ -321,6 +345,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
       const int hb = w * BH + j;
       __asm__ __volatile__("" ::: "memory");   // keep each row block's fragment loads in its own iteration
       const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+      f32x4 y[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
@@ -329,17 +354,17 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
           mma(acc, wu[j][uc], input_chunk_u(ef, a.se, eid[nb], a.FE, uc, g, r2[nb], EQ));
         const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
         const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
-        f32x4 y, d;
+        f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
-          y[i] = r.y;
+          y[nb][i] = r.y;
           d[i] = r.d;
         }
         s1[j][nb] = pack4(d);
-        put_chain(s_m1, hb, nb, l, y);
-        if (valid[nb]) store_bf16x4(Dm1 + (base + nb * 16 + c) * H + 16 * hb + 4 * g, y);
+        put_chain(s_m1, hb, nb, l, y[nb]);
       }
+      store_fmajor(Dm1, a.ldE, 16 * hb + c, base, E, g, edge_major(y[0], y[1], I));
     }
     __syncthreads();
 
@@ -356,19 +381,20 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
       }
+      f32x4 y[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        f32x4 y, d;
+        f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const YD r = silu_yd<bf16>(acc[nb][i] + s_b2[16 * ob + 4 * g + i]);
-          y[i] = r.y;
+          y[nb][i] = r.y;
           d[i] = r.d;
         }
         s2[j][nb] = pack4(d);
-        if (EQ) put_chain(s_m, ob, nb, l, y);
-        if (valid[nb]) store_bf16x4(Dm + (base + nb * 16 + c) * O + 16 * ob + 4 * g, y);
+        if (EQ) put_chain(s_m, ob, nb, l, y[nb]);
       }
+      if (EQ) store_fmajor(Dm, a.ldE, 16 * ob + c, base, E, g, edge_major(y[0], y[1], I));
     }
     float phi[2] = {0.f, 0.f};
     if constexpr (EQ) {
@@ -385,24 +411,21 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m, kc, nb, l));
         }
+        f32x4 p[2], gq[2];
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          f32x4 p, gq;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float w2 = s_w2m[16 * mb + 4 * g + i];
             const YD r = silu_yd<bf16>(acc[nb][i] + s_bx1[16 * mb + 4 * g + i]);
-            p[i] = r.y;
+            p[nb][i] = r.y;
             phi[nb] += r.y * w2;
-            gq[i] = gphi[nb] * w2 * r.d;
+            gq[nb][i] = gphi[nb] * w2 * r.d;
           }
-          put_chain(s_gq, mb, nb, l, gq);
-          if (valid[nb]) {
-            const int64_t e = base + nb * 16 + c;
-            store_bf16x4(Dgq + e * M + 16 * mb + 4 * g, gq);
-            store_bf16x4(Dp + e * M + 16 * mb + 4 * g, p);
-          }
+          put_chain(s_gq, mb, nb, l, gq[nb]);
         }
+        store_fmajor(Dgq, a.ldE, 16 * mb + c, base, E, g, edge_major(gq[0], gq[1], I));
+        store_fmajor(Dp, a.ldE, 16 * mb + c, base, E, g, edge_major(p[0], p[1], I));
       }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -431,15 +454,15 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
           for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_gq, kc, nb, l));
         }
       }
+      f32x4 ga[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const f32x4 d = unpack4(s2[j][nb]);
-        f32x4 ga;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ga[i] = acc[nb][i] * d[i];
-        put_chain(s_ga2, ob, nb, l, ga);
-        if (valid[nb]) store_bf16x4(Dga2 + (base + nb * 16 + c) * O + 16 * ob + 4 * g, ga);
+        for (int i = 0; i < 4; ++i) ga[nb][i] = acc[nb][i] * d[i];
+        put_chain(s_ga2, ob, nb, l, ga[nb]);
       }
+      store_fmajor(Dga2, a.ldE, 16 * ob + c, base, E, g, edge_major(ga[0], ga[1], I));
     }
     __syncthreads();
 

@@ -118,6 +118,14 @@ def test_hidden_256(dtype):
     check_case(Case(rowptr, col, 256, 32, 256, 256, 256, seed=17, mean_agg=True), dtype)
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("fe,eq,mean", [(16, True, False), (0, True, True), (16, False, False)])
+def test_hidden_256_ragged(dtype, fe, eq, mean):
+    # ragged degrees, a partial last tile, one or two edge-input chunks, EGNN and MPNN
+    rowptr, col = random_csr(701, (np.arange(701) * 11) % 37, seed=33)
+    check_case(Case(rowptr, col, 256, fe, 256, 256, 256, seed=19, mean_agg=mean, eq=eq), dtype)
+
+
 def test_determinism_bitwise():
     rowptr, col = random_csr(500, (np.arange(500) * 13) % 50, seed=41)
     case = Case(rowptr, col, 128, 16, 128, 128, 128, seed=18)
