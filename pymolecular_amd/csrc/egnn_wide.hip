@@ -548,8 +548,8 @@ bool wide_supported(const LayerShape& s) {
 }
 
 int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
-  if (s.eq) return s.NUC == 1 ? launch_wide_fwd_t<256, 8, true, 1>(a, st) : launch_wide_fwd_t<256, 8, true, 2>(a, st);
-  return s.NUC == 1 ? launch_wide_fwd_t<256, 8, false, 1>(a, st) : launch_wide_fwd_t<256, 8, false, 2>(a, st);
+  if (s.eq) return s.NUC == 1 ? launch_wide_fwd_t<256, 16, true, 1>(a, st) : launch_wide_fwd_t<256, 16, true, 2>(a, st);
+  return s.NUC == 1 ? launch_wide_fwd_t<256, 16, false, 1>(a, st) : launch_wide_fwd_t<256, 16, false, 2>(a, st);
 }
 
 int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st) {
