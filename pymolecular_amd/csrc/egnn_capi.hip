@@ -261,7 +261,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   {
     Gemm2Args g{};
     g.M = s.N; g.N = s.F; g.K = 2 * s.H;
-    g.A = w.dPQ; g.lda = 2 * s.H; g.a_bf16 = 0; g.a_kc = 1; g.a_ones_row = -1;
+    g.A = w.dPQ; g.lda = 2 * s.H; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
     g.B = w.fr.wn; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 0;   // B[k][f] = Wn[f][k]
     g.C = grad_h; g.ldc = strides->h; g.c_bf16 = s.bf16;
     ProfScope ps(EGNN_K_NODE_GEMM, st);
@@ -356,7 +356,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     Gemm2Args g{};
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
     g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;
-    g.B = w.dPQ; g.ldb = 2 * s.H; g.b_bf16 = 0; g.b_nc = 1;
+    g.B = w.dPQ; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 1;
     g.ksplit = splitk_len(s.N);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), g.ksplit);

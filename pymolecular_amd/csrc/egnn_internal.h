@@ -68,7 +68,7 @@ struct BwdWs {
   void* Gh;        // [E][H] dL/dpre1 per edge
   float* Gx;       // [E][4] (dL/ddelta xyz, dL/dphi)
   float* R2;       // [E]
-  float* dPQ;      // [N][2H] fp32
+  void* dPQ;       // [N][2H] activation dtype (fp32 sums, rounded once)
   float* part;     // split-K partials
   float* dWhl;     // (H+1) x O   last row = db2
   float* dW1m;     // (O+1) x M   last row = dbx1
@@ -188,9 +188,10 @@ int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* co
                     const float* gmov, int64_t sgx, const int32_t* rowptr, int mean, float* out, hipStream_t st);
 int bwd_tile_edges(const LayerShape& s);
 
-// dPQ[n] = [sum_row Gh | sum_csc Gh] (fp32); grad_coord = sum_row Gx - sum_csc Gx
+// dPQ[n] = [sum_row Gh | sum_csc Gh] (summed in fp32, stored in the activation dtype);
+// grad_coord = sum_row Gx - sum_csc Gx
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
-                       const int32_t* csc_ptr, const int32_t* csc_eid, float* dPQ, float* gcoord,
+                       const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord,
                        int64_t sgc, hipStream_t st);
 // out[l] = sum_b part[b][l] for l < L (fixed order)
 int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st);

@@ -96,7 +96,7 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->LW = coop ? coop_dw_len(s) : 0;
   w->dwpart = coop ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
   w->dwsum = coop ? (float*)take((size_t)w->LW * sizeof(float)) : nullptr;
-  w->dPQ = (float*)take((size_t)s.N * 2 * s.H * sizeof(float));
+  w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
   int64_t se = cdiv(std::max<int64_t>(s.E, 1), splitk_len(s.E)), sn = cdiv(s.N, splitk_len(s.N));
   int64_t pe = coop ? 0 : std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
@@ -384,6 +384,270 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
       }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 node-level GEMM: 128 x 128 tile per 4-wave block (each wave 64 x 64 =
+// 4 x 4 MFMA blocks), 64-deep k stages, double-buffered LDS.  Operand tiles
+// are copied to LDS in their global layout with 16-byte loads and stores; a
+// k-contiguous tile feeds the MFMA with one 16-byte LDS read per operand
+// chunk, an m/n-contiguous tile with two ds_read_b64_tr_b16 transposing reads
+// (lane (c, g) of a 16-lane group gets 4 consecutive k of column c).  Same
+// arguments, concatenated A, ones row, B row gather, split-K and epilogues
+// as gemm2_kernel.
+// ---------------------------------------------------------------------------
+namespace {
+constexpr int GB_M = 128, GB_N = 128, GB_K = 64;
+constexpr int GB_PK = GB_K + 8;     // row pitch of a k-contiguous tile (bf16)
+constexpr int GB_PM = GB_M + 16;    // row pitch of an m/n-contiguous tile (bf16)
+constexpr int GB_TILE = (GB_M * GB_PK > GB_K * GB_PM) ? GB_M * GB_PK : GB_K * GB_PM;
+
+typedef bf16 bf16x4v __attribute__((ext_vector_type(4)));
+
+// 4 consecutive k (rows kb .. kb+3) of column col0 + c from an m/n-contiguous tile:
+// within a 16-lane group, lane j supplies the address of row kb + j/4, columns
+// col0 + 4 (j % 4) .. + 3, and lane c receives element c % 4 of the rows
+// supplied by lanes c/4 + 4 i, i = 0..3
+__device__ __forceinline__ bf16x4v ld_tr4(const bf16* tile, int kb, int col0, int lane16) {
+  const bf16* p = tile + (kb + (lane16 >> 2)) * GB_PM + col0 + 4 * (lane16 & 3);
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)p);
+}
+__device__ __forceinline__ bf16x8 join_tr(const bf16x4v& lo, const bf16x4v& hi) {
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+}  // namespace
+
+template <bool A_KC, bool B_NC, int BM>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
+  constexpr int WM = BM / 2, MI = WM / 16;              // rows per wave, MFMA row blocks per wave
+  constexpr int NLA = BM * GB_K / 8 / 256;              // 16-byte A vectors per thread per stage
+  constexpr int TA_ = A_KC ? BM * GB_PK : GB_K * (BM + 16);
+  constexpr int PA = BM + 16;                           // row pitch of an m-contiguous A tile
+  constexpr int CP = GB_N + 4;                          // row pitch of the fp32 output tile
+  constexpr int MAIN = 2 * TA_ + 2 * GB_TILE;           // bf16 elements of the operand buffers
+  constexpr int OUTB = BM * CP * 2;                     // bf16-element size of the fp32 output tile
+  __shared__ __attribute__((aligned(16))) bf16 smem[MAIN > OUTB ? MAIN : OUTB];
+  bf16* const As0 = smem;
+  bf16* const Bs0 = smem + 2 * TA_;
+  float* const Cs = reinterpret_cast<float*>(smem);
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * GB_N;
+  int64_t kbeg = 0, kend = g.K;
+  if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
+  const bf16* A = (const bf16*)g.A;
+  const bf16* A2 = (const bf16*)g.A2;
+  const bf16* B = (const bf16*)g.B;
+
+  f32x4 acc[MI][4];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  bf16x8 ra[NLA], rb[4];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      const int idx = tid + 256 * i;
+      bf16x8 va = zero_chunk<bf16>();
+      if constexpr (A_KC) {   // A[m][k], or A2[m][k - a_split]
+        const int r = idx >> 3, q = idx & 7;
+        const int64_t m = m0 + r, k = k0 + 8 * q;
+        if (m < g.M && m != g.a_ones_row && k < kend) {
+          const bf16* Ab = (A2 && k >= g.a_split) ? A2 + m * g.lda2 - g.a_split : A + m * g.lda;
+          if (k + 8 <= kend) va = *reinterpret_cast<const bf16x8*>(Ab + k);
+          else
+            for (int u = 0; u < 8; ++u) if (k + u < kend) va[u] = Ab[k + u];
+        } else if (m == g.a_ones_row && k < kend) {
+          for (int u = 0; u < 8; ++u) if (k + u < kend) va[u] = (bf16)1.0f;
+        }
+      } else {                // A[k][m], or A2[k][m - a_split]
+        const int r = idx / (BM / 8), q = idx % (BM / 8);
+        const int64_t k = k0 + r, m = m0 + 8 * q;
+        if (k < kend && m < g.M) {
+          const bf16* Ab = (A2 && m >= g.a_split) ? A2 + k * g.lda2 - g.a_split : A + k * g.lda;
+          const bool ones = g.a_ones_row >= m && g.a_ones_row < m + 8;
+          if (m + 8 <= g.M && !ones) va = *reinterpret_cast<const bf16x8*>(Ab + m);
+          else
+            for (int u = 0; u < 8; ++u)
+              if (m + u < g.M) va[u] = (m + u == g.a_ones_row) ? (bf16)1.0f : Ab[m + u];
+        }
+      }
+      ra[i] = va;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      bf16x8 vb = zero_chunk<bf16>();
+      if constexpr (B_NC) {   // B[k][n], or B[b_kidx[k]][n]
+        const int r = idx >> 4, q = idx & 15;
+        const int64_t k = k0 + r, n = n0 + 8 * q;
+        if (k < kend && n < g.N) {
+          const int64_t kr = g.b_kidx ? (int64_t)g.b_kidx[k] : k;
+          if (n + 8 <= g.N) vb = *reinterpret_cast<const bf16x8*>(B + kr * g.ldb + n);
+          else
+            for (int u = 0; u < 8; ++u) if (n + u < g.N) vb[u] = B[kr * g.ldb + n + u];
+        }
+      } else {                // B[n][k]
+        const int r = idx >> 3, q = idx & 7;
+        const int64_t n = n0 + r, k = k0 + 8 * q;
+        if (n < g.N && k < kend) {
+          if (k + 8 <= kend) vb = *reinterpret_cast<const bf16x8*>(B + n * g.ldb + k);
+          else
+            for (int u = 0; u < 8; ++u) if (k + u < kend) vb[u] = B[n * g.ldb + k + u];
+        }
+      }
+      rb[i] = vb;
+    }
+  };
+  auto store_stage = [&](int buf) {
+    bf16* At = As0 + buf * TA_;
+    bf16* Bt = Bs0 + buf * GB_TILE;
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      const int idx = tid + 256 * i;
+      if constexpr (A_KC) *reinterpret_cast<bf16x8*>(&At[(idx >> 3) * GB_PK + 8 * (idx & 7)]) = ra[i];
+      else *reinterpret_cast<bf16x8*>(&At[(idx / (BM / 8)) * PA + 8 * (idx % (BM / 8))]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int idx = tid + 256 * i;
+      if constexpr (!B_NC) *reinterpret_cast<bf16x8*>(&Bt[(idx >> 3) * GB_PK + 8 * (idx & 7)]) = rb[i];
+      else *reinterpret_cast<bf16x8*>(&Bt[(idx >> 4) * GB_PM + 8 * (idx & 15)]) = rb[i];
+    }
+  };
+
+  int buf = 0;
+  if (kbeg < kend) {
+    load_stage(kbeg);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int64_t k0 = kbeg; k0 < kend; k0 += GB_K) {
+    const bool more = k0 + GB_K < kend;
+    if (more) load_stage(k0 + GB_K);
+    const bf16* At = As0 + buf * TA_;
+    const bf16* Bt = Bs0 + buf * GB_TILE;
+#pragma unroll
+    for (int ks = 0; ks < GB_K / 32; ++ks) {
+      bf16x8 a[MI], b[4];
+#pragma unroll
+      for (int i = 0; i < MI; ++i) {
+        if constexpr (A_KC) a[i] = *reinterpret_cast<const bf16x8*>(&At[(wm * WM + 16 * i + c) * GB_PK + 32 * ks + 8 * gq]);
+        else {
+          const bf16* p = At + (32 * ks + 8 * gq + (c >> 2)) * PA + wm * WM + 16 * i + 4 * (c & 3);
+          const bf16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)p);
+          const bf16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)(p + 4 * PA));
+          a[i] = join_tr(lo, hi);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        if constexpr (!B_NC) b[j] = *reinterpret_cast<const bf16x8*>(&Bt[(wn * 64 + 16 * j + c) * GB_PK + 32 * ks + 8 * gq]);
+        else b[j] = join_tr(ld_tr4(Bt, 32 * ks + 8 * gq, wn * 64 + 16 * j, c), ld_tr4(Bt, 32 * ks + 8 * gq + 4, wn * 64 + 16 * j, c));
+      }
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
+    }
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+
+  // ---- epilogue: the fp32 tile goes through LDS so that every global access is a 16-byte row segment
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Cs[(wm * WM + 16 * i + 4 * gq + r) * CP + wn * 64 + 16 * j + c] = acc[i][j][r];
+  __syncthreads();
+  const bool vec_n = (g.N % 8 == 0);
+  for (int v = tid; v < BM * (GB_N / 8); v += 256) {
+    const int r = v / (GB_N / 8), q = v % (GB_N / 8);
+    const int64_t m = m0 + r, n = n0 + 8 * q;
+    if (m >= g.M || n >= g.N) continue;
+    float x[8];
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(&Cs[r * CP + 8 * q]);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(&Cs[r * CP + 8 * q + 4]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) { x[u] = x0[u]; x[4 + u] = x1[u]; }
+    const int nv = (int)((g.N - n) < 8 ? (g.N - n) : 8);
+    if (g.partial) {
+      float* P = g.partial + ((int64_t)blockIdx.z * g.M + m) * g.N + n;
+      if (nv == 8 && vec_n) {
+        *reinterpret_cast<f32x4*>(P) = x0;
+        *reinterpret_cast<f32x4*>(P + 4) = x1;
+      } else {
+        for (int u = 0; u < nv; ++u) P[u] = x[u];
+      }
+      continue;
+    }
+    if (g.bias)
+#pragma unroll
+      for (int u = 0; u < 8; ++u) if (u < nv && n + u < g.bias_len) x[u] += ld_elem(g.bias, n + u, g.bias_bf16);
+    const bool full = nv == 8 && vec_n;
+    if (g.zd) {   // * SiLU'(z)
+      bf16x8 z;
+      if (full) z = *reinterpret_cast<const bf16x8*>((const bf16*)g.zd + m * g.ldz + n);
+      else for (int u = 0; u < 8; ++u) z[u] = u < nv ? ((const bf16*)g.zd)[m * g.ldz + n + u] : (bf16)0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float zz = (float)z[u];
+        const float sg = 1.0f / (1.0f + __expf(-zz));
+        x[u] *= sg * (1.0f + zz * (1.0f - sg));
+      }
+    }
+    if (g.act) {
+      bf16x8 pre;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        pre[u] = (bf16)x[u];
+        const float xv = g.Cpre ? (float)pre[u] : x[u];   // SiLU of the stored pre-activation
+        x[u] = xv / (1.0f + __expf(-xv));
+      }
+      if (g.Cpre) {
+        bf16* P = (bf16*)g.Cpre + m * g.ldpre + n;
+        if (full) *reinterpret_cast<bf16x8*>(P) = pre;
+        else for (int u = 0; u < nv; ++u) P[u] = pre[u];
+      }
+    }
+    if (g.resid && n < g.resid_len) {
+      bf16x8 rr;
+      const bf16* R = (const bf16*)g.resid + m * g.ldr + n;
+      if (full && n + 8 <= g.resid_len) rr = *reinterpret_cast<const bf16x8*>(R);
+      else for (int u = 0; u < 8; ++u) rr[u] = (u < nv && n + u < g.resid_len) ? R[u] : (bf16)0.0f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] += (float)rr[u];
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) o[u] = (bf16)x[u];
+    if (g.perm_half > 0 && full && g.perm_half % 32 == 0) {
+      // 8 consecutive features of a 32-group land in two runs of 4 chain positions
+      const int64_t half = n / g.perm_half, f = n % g.perm_half;
+      bf16* Cr = (bf16*)g.C + m * g.ldc + half * g.perm_half + (f & ~31);
+      bf16x4 lo, hi;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) { lo[u] = o[u]; hi[u] = o[4 + u]; }
+      *reinterpret_cast<bf16x4*>(Cr + chain_pos((int)(f & 31))) = lo;
+      *reinterpret_cast<bf16x4*>(Cr + chain_pos((int)((f + 4) & 31))) = hi;
+    } else if (g.perm_half > 0 || !full) {
+      for (int u = 0; u < nv; ++u) {
+        int64_t pn = n + u;
+        if (g.perm_half > 0) {
+          const int64_t half = pn / g.perm_half, f = pn % g.perm_half;
+          pn = half * g.perm_half + (f & ~31) + chain_pos((int)(f & 31));
+        }
+        ((bf16*)g.C)[m * g.ldc + pn] = o[u];
+      }
+    } else {
+      *reinterpret_cast<bf16x8*>((bf16*)g.C + m * g.ldc + n) = o;
+    }
+  }
+}
+
 template <typename TA, typename TB, typename TC>
 static void gemm2_dispatch(const Gemm2Args& g, dim3 grid, hipStream_t st) {
   if (g.a_kc && g.b_nc) hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, true, true>), grid, dim3(256), 0, st, g);
@@ -396,7 +660,26 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0) return 0;
   const unsigned gz = g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
   const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
-  if (compute_bf16) {
+  // the tiled bf16 kernel moves 16-byte row segments: every operand row must start 16-byte aligned
+  auto al = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 8 == 0); };
+  const bool rows16 = al(g.A, g.lda) && al(g.A2, g.lda2) && al(g.B, g.ldb) &&
+                      (g.partial ? (((uintptr_t)g.partial) & 15) == 0
+                                 : al(g.C, g.ldc) && al(g.Cpre, g.ldpre) && al(g.resid, g.ldr) && al(g.zd, g.ldz));
+  if (compute_bf16 && g.a_bf16 && g.b_bf16 && (g.c_bf16 || g.partial) && rows16) {
+    // 128-row tiles when they fill the device twice over, else 64-row tiles
+    const bool big = cdiv(g.M, 128) * cdiv(g.N, GB_N) * (int64_t)gz >= 512;
+    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 64), (unsigned)cdiv(g.N, GB_N), gz);
+#define GB_LAUNCH(AK, BN)                                                                  \
+    do {                                                                                   \
+      if (big) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BN, 128>), gb, dim3(256), 0, st, g); \
+      else hipLaunchKernelGGL((gemm_bf16_kernel<AK, BN, 64>), gb, dim3(256), 0, st, g);      \
+    } while (0)
+    if (g.a_kc && g.b_nc) GB_LAUNCH(true, true);
+    else if (g.a_kc) GB_LAUNCH(true, false);
+    else if (g.b_nc) GB_LAUNCH(false, true);
+    else GB_LAUNCH(false, false);
+#undef GB_LAUNCH
+  } else if (compute_bf16) {
     if (g.a_bf16 && g.b_bf16) gemm2_dispatch<bf16, bf16, bf16>(g, grid, st);
     else if (g.a_bf16) gemm2_dispatch<bf16, float, bf16>(g, grid, st);
     else if (g.b_bf16) gemm2_dispatch<float, bf16, bf16>(g, grid, st);
@@ -419,7 +702,7 @@ template <typename T, int H>
 __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ Gh, const float* __restrict__ Gx,
                                                           const int32_t* __restrict__ rowptr,
                                                           const int32_t* __restrict__ csc_ptr,
-                                                          const int32_t* __restrict__ csc_eid, float* __restrict__ dPQ,
+                                                          const int32_t* __restrict__ csc_eid, T* __restrict__ dPQ,
                                                           float* __restrict__ gcoord, int64_t sgc, int64_t N, int eq) {
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
@@ -478,23 +761,28 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
       ax += shfl_xor(ax, off);
     }
     if (eq && l < 3) gcoord[n * sgc + l] = ax;
-    if (sub == 0) {
-      float* out = dPQ + n * 2 * H + q * VPL;
+    if (sub == 0) {   // one 16-byte store per half
+      T* out = dPQ + n * 2 * H + q * VPL;
+      if constexpr (sizeof(T) == 2) {
+        bf16x8 vp, vq;
 #pragma unroll
-      for (int u = 0; u < VPL; ++u) {
-        out[u] = ap[u];
-        out[H + u] = aq[u];
+        for (int u = 0; u < VPL; ++u) { vp[u] = (bf16)ap[u]; vq[u] = (bf16)aq[u]; }
+        *reinterpret_cast<bf16x8*>(out) = vp;
+        *reinterpret_cast<bf16x8*>(out + H) = vq;
+      } else {
+        *reinterpret_cast<f32x4*>(out) = f32x4{ap[0], ap[1], ap[2], ap[3]};
+        *reinterpret_cast<f32x4*>(out + H) = f32x4{aq[0], aq[1], aq[2], aq[3]};
       }
     }
   }
 }
 
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
-                       const int32_t* csc_ptr, const int32_t* csc_eid, float* dPQ, float* gcoord, int64_t sgc,
+                       const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord, int64_t sgc,
                        hipStream_t st) {
   int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
   int eq = s.eq ? 1 : 0;
-#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, dPQ, gcoord, sgc, s.N, eq)
+#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, s.N, eq)
   if (s.bf16) {
     if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
   } else {
