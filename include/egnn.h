@@ -177,6 +177,19 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
                       void* grad_w1, void* grad_b1, void* grad_w2, void* grad_b2,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- dense-layer weight gradient ---------------------------------------------
+ * No kernel counterpart in the reference: the weight gradient of a plain
+ * torch.nn.Linear over all nodes, as used by the stack's embedding_in /
+ * embedding_out (egnn_clean.py:127-128, 139-145), where K = number of nodes is
+ * far larger than the weight.  grad_w (Nout, Kin) in nn.Linear layout and
+ * grad_b (Nout, may be NULL) = column sums of dy; deterministic split-K sums.
+ * x (N, Kin) and dy (N, Nout) row-major with row strides ldx, lddy (any
+ * widths).  One dtype for all tensors (EGNN_F32 / EGNN_BF16). */
+size_t egnn_dense_wgrad_workspace_bytes(int64_t N, int32_t Kin, int32_t Nout);
+int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
+                         const void* dy, int64_t lddy, void* grad_w, void* grad_b, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
 /* ---- instrumentation (no reference counterpart) ---------------------------
  * When enabled, every kernel launch made by egnn_fwd / egnn_bwd / egnn_node_* is bracketed
  * by HIP events recorded on the caller's stream, grouped by kernel class.

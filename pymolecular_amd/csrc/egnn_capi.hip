@@ -555,3 +555,58 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
 }
 
 }  // extern "C"
+
+// ---- dense-layer weight gradient ------------------------------------------------
+namespace {
+struct DenseWs { float* part; float* S; int64_t part_elems; };
+size_t dense_ws_layout(int64_t N, int Kin, int Nout, void* base, DenseWs* w) {
+  char* b = (char*)base;
+  size_t off = 0;
+  auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
+  const int64_t ns = cdiv(std::max<int64_t>(N, 1), splitk_len(std::max<int64_t>(N, 1)));
+  w->part_elems = ns * (int64_t)(Kin + 1) * Nout;
+  w->part = (float*)take((size_t)w->part_elems * sizeof(float));
+  w->S = (float*)take((size_t)(Kin + 1) * Nout * sizeof(float));
+  return off;
+}
+}  // namespace
+
+extern "C" {
+
+size_t egnn_dense_wgrad_workspace_bytes(int64_t N, int32_t Kin, int32_t Nout) {
+  if (N < 0 || Kin <= 0 || Nout <= 0) return 0;
+  DenseWs w;
+  return dense_ws_layout(N, Kin, Nout, nullptr, &w);
+}
+
+int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
+                         const void* dy, int64_t lddy, void* grad_w, void* grad_b, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  if (dtype != EGNN_F32 && dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (N < 0 || Kin <= 0 || Nout <= 0) return EGNN_ERR_DIMS;
+  if (!grad_w || !workspace || (N > 0 && (!x || !dy))) return EGNN_ERR_NULL;
+  const bool bf16 = dtype == EGNN_BF16;
+  if (N > 0 && (ldx < Kin || lddy < Nout)) return EGNN_ERR_STRIDE;
+  if (!aligned16(workspace)) return EGNN_ERR_ALIGN;
+  DenseWs w;
+  if (dense_ws_layout(N, Kin, Nout, nullptr, &w) > workspace_bytes) return EGNN_ERR_WORKSPACE;
+  dense_ws_layout(N, Kin, Nout, workspace, &w);
+  hipStream_t st = (hipStream_t)stream;
+  ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  const int64_t ksplit = splitk_len(std::max<int64_t>(N, 1));
+  const int64_t nsplit = cdiv(std::max<int64_t>(N, 1), ksplit);
+  int32_t rc;
+  if (N > 0) {   // S = [x | 1]^T dy, split over the nodes
+    Gemm2Args g{};
+    g.M = Kin + 1; g.N = Nout; g.K = N;
+    g.A = x; g.lda = ldx; g.a_bf16 = bf16; g.a_kc = 0; g.a_ones_row = Kin;
+    g.B = dy; g.ldb = lddy; g.b_bf16 = bf16; g.b_nc = 1;
+    g.ksplit = ksplit; g.partial = w.part;
+    if ((rc = hip_status(launch_gemm2(g, bf16, st))) != EGNN_OK) return rc;
+  }
+  if ((rc = hip_status(launch_sum_rows(w.part, N > 0 ? nsplit : 0, (int64_t)(Kin + 1) * Nout, w.S, st))) != EGNN_OK)
+    return rc;
+  return hip_status(launch_node_finalize(bf16, w.S, nullptr, Kin, Nout, 0, grad_w, grad_b, nullptr, nullptr, st));
+}
+
+}  // extern "C"

@@ -257,15 +257,20 @@ class EGNNFusedFn(torch.autograd.Function):
     @staticmethod
     def forward(ctx, h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                 b1=None, b2=None, bx1=None, mean_agg=False, equivariant=True):
+        # dtype/layout conversion once; the backward reuses the converted tensors
+        ctx.shapes = [None if t is None else tuple(t.shape) for t in (w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1)]
+        h, coord_p, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1 = _prep_inputs(
+            h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
         pq = _node_proj_buffer(h, edge_feat, col_indices, w1_msg, w2_msg, w1_mov, equivariant, mean_agg)
-        out_msg, out_mov = egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg,
+        out_msg, out_mov = egnn_fused_forward(h, coord_p, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg,
                                               w2_msg, w1_mov, w2_mov, b1, b2, bx1, mean_agg=mean_agg,
                                               equivariant=equivariant, node_proj=pq)
-        ctx.save_for_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov,
+        ctx.save_for_backward(h, coord_p, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov,
                               w2_mov, b1, b2, bx1, pq)
         ctx.mean_agg = mean_agg
         ctx.equivariant = equivariant
         ctx.coord_shape = None if coord is None else tuple(coord.shape)
+        ctx.coord_dtype = None if coord is None else coord.dtype
         if out_mov is None:
             out_mov = torch.zeros((h.shape[0], 3), dtype=torch.float32, device=h.device)
         return out_msg, out_mov
@@ -285,10 +290,11 @@ class EGNNFusedFn(torch.autograd.Function):
             full = torch.zeros(ctx.coord_shape, dtype=torch.float32, device=gc.device)
             full[:, :3] = gc
             gc = full
-        if gc is not None and coord is not None:
-            gc = gc.to(coord.dtype)
-        return (g["h"], gc, None, None, None, None, g["w1_msg"], g["w2_msg"], g["w1_mov"], g["w2_mov"], g["b1"],
-                g["b2"], g["bx1"], None, None)
+        if gc is not None and ctx.coord_dtype is not None:
+            gc = gc.to(ctx.coord_dtype)
+        wg = [g[k] for k in ("w1_msg", "w2_msg", "w1_mov", "w2_mov", "b1", "b2", "bx1")]
+        wg = [None if (t is None or shp is None) else t.reshape(shp) for t, shp in zip(wg, ctx.shapes)]
+        return (g["h"], gc, None, None, None, None, *wg, None, None)
 
 
 def egnn_fused(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None, w2_mov=None,

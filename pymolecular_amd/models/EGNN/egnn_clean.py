@@ -22,7 +22,7 @@ import torch
 from torch import nn
 
 from ...fused import coo_to_csr, egnn_fused
-from ...node_update import node_update
+from ...node_update import dense, node_update
 
 __all__ = ["E_GCL", "EGNN", "unsorted_segment_sum", "unsorted_segment_mean", "get_edges", "get_edges_batch"]
 
@@ -132,12 +132,12 @@ class EGNN(nn.Module):
         self.to(self.device)
 
     def forward(self, h, x, edges, edge_attr):
-        h = self.embedding_in(h)
+        h = dense(h, self.embedding_in)
         row, col = edges
         csr = _csr_cache.get(row, col, h.shape[0])   # one CSR for all layers, cached per edge tensor
         for i in range(0, self.n_layers):
             h, x, _ = self._modules["gcl_%d" % i](h, edges, x, edge_attr=edge_attr, csr=csr)
-        h = self.embedding_out(h)
+        h = dense(h, self.embedding_out)
         return h, x
 
 

@@ -16,7 +16,7 @@ import torch
 from torch import nn
 
 from ...fused import egnn_fused
-from ...node_update import node_update
+from ...node_update import dense, node_update
 from .egnn_clean import _csr_cache
 
 __all__ = ["MPNN_GCL", "MPNN"]
@@ -69,9 +69,9 @@ class MPNN(nn.Module):
         self.to(device)
 
     def forward(self, h, edges, edge_attr=None):
-        h = self.embedding_in(h)
+        h = dense(h, self.embedding_in)
         row, col = edges
         csr = _csr_cache.get(row, col, h.shape[0])
         for i in range(self.n_layers):
             h, _ = self._modules["gcl_%d" % i](h, edges, edge_attr=edge_attr, csr=csr)
-        return self.embedding_out(h)
+        return dense(h, self.embedding_out)

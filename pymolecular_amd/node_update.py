@@ -18,7 +18,7 @@ import torch
 from . import _capi
 from ._capi import EgnnNodeDims, check
 
-__all__ = ["NodeUpdateFn", "node_update"]
+__all__ = ["NodeUpdateFn", "node_update", "DenseFn", "dense"]
 
 
 def _rowmajor(t: torch.Tensor) -> torch.Tensor:
@@ -119,3 +119,51 @@ def node_update(x1: torch.Tensor, x2: Optional[torch.Tensor], lin1: torch.nn.Lin
                 residual: bool = True) -> torch.Tensor:
     """``x1 + lin2(SiLU(lin1(cat([x1, x2]))))`` (without ``x1 +`` when not residual)."""
     return NodeUpdateFn.apply(x1, x2, lin1.weight, lin1.bias, lin2.weight, lin2.bias, residual)
+
+
+class DenseFn(torch.autograd.Function):
+    """``y = DenseFn.apply(x, weight, bias)``: torch.nn.functional.linear whose
+    weight gradient over the N rows is the library's deterministic split-K
+    product (``egnn_dense_wgrad``); the stack's embedding layers use it
+    (egnn_clean.py:127-128, 139-145), where N is far larger than the weight."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias):
+        if not x.is_cuda:
+            raise RuntimeError("x must be a ROCm device tensor")
+        w = weight.to(x.dtype)
+        b = None if bias is None else bias.to(x.dtype)
+        ctx.save_for_backward(x, w)
+        ctx.has_b = bias is not None
+        ctx.wdt = (weight.dtype, None if bias is None else bias.dtype)
+        return torch.nn.functional.linear(x, w, b)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        dt = x.dtype
+        if dt not in (torch.float32, torch.bfloat16):
+            raise TypeError(f"unsupported dtype {dt}")
+        x2 = x.reshape(-1, x.shape[-1])
+        x2 = x2 if x2.stride(-1) == 1 else x2.contiguous()
+        gy2 = gy.to(dt).reshape(-1, gy.shape[-1])
+        gy2 = gy2 if gy2.stride(-1) == 1 else gy2.contiguous()
+        N, Kin = x2.shape
+        Nout = gy2.shape[1]
+        gx = (gy2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
+        gw = torch.empty((Nout, Kin), dtype=dt, device=x.device)
+        gb = torch.empty((Nout,), dtype=dt, device=x.device) if ctx.has_b else None
+        L = _capi.lib()
+        nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kin, Nout)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+        code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
+        rc = L.egnn_dense_wgrad(code, N, Kin, Nout, x2.data_ptr() if N else None, x2.stride(0),
+                                gy2.data_ptr() if N else None, gy2.stride(0), gw.data_ptr(), _ptr(gb), ws.data_ptr(),
+                                nbytes, torch.cuda.current_stream(x.device).cuda_stream)
+        check("egnn_dense_wgrad", rc)
+        return gx, gw.to(ctx.wdt[0]), None if gb is None else gb.to(ctx.wdt[1])
+
+
+def dense(x: torch.Tensor, lin: torch.nn.Linear) -> torch.Tensor:
+    """``lin(x)`` with the split-K weight gradient of :class:`DenseFn`."""
+    return DenseFn.apply(x, lin.weight, lin.bias)

@@ -74,3 +74,30 @@ def test_node_update_deterministic_and_empty():
     assert out.shape == (0, 128)
     out.sum().backward()
     assert torch.count_nonzero(leaves[2].grad) == 0 and torch.count_nonzero(leaves[5].grad) == 0
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
+@pytest.mark.parametrize("N,K,Nout,bias", [(19363, 5, 128, True), (3000, 128, 128, False), (0, 16, 24, True)])
+def test_dense_weight_gradient(dtype, tol, N, K, Nout, bias):
+    from pymolecular_amd.node_update import DenseFn
+    r = np.random.Generator(np.random.PCG64(N + K))
+    x = torch.from_numpy(r.standard_normal((N, K)))
+    w = torch.from_numpy(r.standard_normal((Nout, K)) / np.sqrt(K))
+    b = torch.from_numpy(r.standard_normal(Nout)) if bias else None
+    gy = torch.from_numpy(r.standard_normal((N, Nout)))
+    rd = (lambda t: None if t is None else t.to(torch.bfloat16).double()) if dtype == torch.bfloat16 else \
+        (lambda t: t)
+    ref = [None if t is None else rd(t).clone().requires_grad_() for t in (x, w, b)]
+    (torch.nn.functional.linear(*ref) * rd(gy)).sum().backward()
+    dev = [None if t is None else t.to(dtype).cuda().requires_grad_() for t in (x, w, b)]
+    y = DenseFn.apply(*dev)
+    (y.float() * gy.to(dtype).float().cuda()).sum().backward()
+    errs = {"y": _rel(y, torch.nn.functional.linear(*[None if t is None else t.detach() for t in ref]))}
+    for name, a, q in zip(["x", "w", "b"], dev, ref):
+        if a is not None and N > 0:
+            errs["d" + name] = _rel(a.grad, q.grad)
+    if N == 0:
+        assert torch.count_nonzero(dev[1].grad) == 0
+    print({k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
+    bad = {k: v for k, v in errs.items() if not v <= tol}
+    assert not bad, bad
