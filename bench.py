@@ -79,10 +79,12 @@ def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
         flops = 2 * ((g + FE) * H + H * O + g * O * M)
         return flops * E, E * (2 * H * s + eb) + N * (O * s + 12 * g)
     if cls == "bwd_edge":
-        flops = 4 * (g + FE) * H + 6 * H * O + 6 * g * O * M
         per_edge = 2 * H * s + eb + O * s + 12 * g + H * s + 16 * g      # + grad rows of i, Gh and Gx stores
-        if not coop:
-            per_edge += (O + O + 2 * g * M) * s                          # stored weight-gradient factors
+        if coop:      # weight gradients accumulated in registers
+            flops = 4 * (g + FE) * H + 6 * H * O + 6 * g * O * M
+        else:         # weight-gradient factors m1, m, g_q, p, g_a2 stored for the split-K GEMMs
+            flops = 2 * (g + FE) * H + 4 * H * O + 4 * g * O * M
+            per_edge += (H + O + 2 * g * M + O) * s + 4 * g
         return flops * E, E * per_edge
     if cls == "node_reduce":
         return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
