@@ -90,6 +90,12 @@ def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
         return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
     if cls == "node_gemm":
         return 2 * N * F * 2 * H, N * (F + 2 * H) * s
+    if cls == "wgrad":   # whole layer: [dW_n1 | dW_n2; db1] over the nodes, plus the edge-factor products
+        flops, nbytes = 2 * N * (F + 1) * 2 * H, N * (F + 2 * H) * s
+        if not coop:
+            flops += 2 * E * ((H + 1) * O + g * ((O + 1) * M + M + H) + H * FE)
+            nbytes += E * ((H + O) * s + g * ((O + M) * s + M * s + 4 + H * s + 4) + (H * s + FE * s + 4 if FE else 0))
+        return flops, nbytes
     return 0, 0
 
 
@@ -232,20 +238,26 @@ def main():
     g1 = 1 if eq else 0
     coop = s == 2 and H == 128 and FE + 2 * g1 <= 32
     peak_mfma = PEAK["bf16_mfma_tflops"] if s == 2 else PEAK["fp32_mfma_tflops"]
+    def work_per_launch(cls, launches_per_step):
+        fl, by = kernel_work(cls, coop, N, E, H, H, H, H, FE, g1, s)
+        if cls == "wgrad":   # a class of several launches per layer: the average launch
+            return fl * L / launches_per_step, by * L / launches_per_step
+        return fl, by
+
     kern, portions = {}, {}
     for cls, (t, n) in prof.items():
         if not n:
             continue
         per = t / n
         kern[cls] = dict(ms_per_launch=per, launches_per_step=n / nprof, share=(t / nprof) / ms)
-        fl, by = kernel_work(cls, coop, N, E, H, H, H, H, FE, g1, s)
+        fl, by = work_per_launch(cls, n / nprof)
         if fl or by:
             portions[cls] = dict(mfma_frac=fl / (per / 1e3) / (peak_mfma * 1e12),
                                  hbm_frac=by / (per / 1e3) / (PEAK["hbm_gbs"] * 1e9),
                                  flops=fl, bytes=by)
     dom = max(kern, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
     dur_s = kern[dom]["ms_per_launch"] / 1e3
-    flops, nbytes = kernel_work(dom, coop, N, E, H, H, H, H, FE, g1, s)
+    flops, nbytes = work_per_launch(dom, kern[dom]["launches_per_step"])
     if nbytes / (PEAK["hbm_gbs"] * 1e9) >= flops / (peak_mfma * 1e12):
         roof = dict(bound="hbm", achieved=nbytes / dur_s / 1e9, peak=PEAK["hbm_gbs"], unit="GB/s")
     else:
