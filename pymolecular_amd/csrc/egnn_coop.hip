@@ -68,25 +68,40 @@ __global__ __launch_bounds__(256) void edge_geo_kernel(int64_t E, int N, const i
 // forward
 // ---------------------------------------------------------------------------
 template <int H, int O, int M, int W, bool EQ>
-__global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
+__global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
   constexpr int KH = H / 32, KO = O / 32;
   constexpr int SEGW = O + (EQ ? 4 : 0);
   static_assert(BH >= 1 && BO >= 1 && BM >= 1, "slice smaller than one 16-row block");
   __shared__ __attribute__((aligned(16))) bf16 s_m1[KH * 2 * 64 * 8];
   __shared__ __attribute__((aligned(16))) bf16 s_m[KO * 2 * 64 * 8];
-  __shared__ float s_phi[W][TE];
+  __shared__ __attribute__((aligned(16))) float s_phi[TE][W];   // per-wave partial phi, edge-major
+  __shared__ __attribute__((aligned(16))) float s_pht[TE];      // phi of each edge
   __shared__ float s_d[TE][4];
   __shared__ int s_rowof[TE];
+  __shared__ int s_rspan[TE];
+  __shared__ uint2 s_lut[16];
+  seg_lut_init(s_lut, threadIdx.x);
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  const bf16* PQ = (const bf16*)a.PQ;
   const bf16* ef = (const bf16*)a.ef;
   const int64_t E = a.E;
   const int N = (int)a.N;
+  const bool use_eids = a.eids != nullptr && a.FE > 0;
 
   bf16x8 wu[BH], whlT[BO][KH], wmovT[EQ ? BM : 1][KO];
-  f32x4 b2v[BO], bx1v[BM], w2mv[BM];
+  // per-row vectors b2 (O), bx1 (M), w2_mov (M), read from LDS where they are used
+  __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M];
+  float* const s_b2 = s_vec;
+  float* const s_bx1 = s_vec + O;
+  float* const s_w2m = s_vec + O + M;
+  for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
+  if constexpr (EQ) {
+    for (int q = threadIdx.x; q < M; q += W * 64) {
+      s_bx1[q] = a.fr.bx1f[q];
+      s_w2m[q] = a.fr.w2mf[q];
+    }
+  }
 #pragma unroll
   for (int j = 0; j < BH; ++j)
     wu[j] = load_chunk((const bf16*)a.fr.u + (int64_t)(w * BH + j) * kFragElems + l * 8);
@@ -95,7 +110,6 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KH; ++kc)
       whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)(w * BO + j) * KH + kc) * kFragElems + l * 8);
-    b2v[j] = load4_f32(a.fr.b2f + 16 * (w * BO + j) + 4 * g);
   }
   if constexpr (EQ) {
 #pragma unroll
@@ -103,64 +117,118 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc)
         wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)(w * BM + j) * KO + kc) * kFragElems + l * 8);
-      bx1v[j] = load4_f32(a.fr.bx1f + 16 * (w * BM + j) + 4 * g);
-      w2mv[j] = load4_f32(a.fr.w2mf + 16 * (w * BM + j) + 4 * g);
     }
   }
   const bf16x8 I = ident_chunk(c, g);
+  const bf16x8 Ipq = pair_sum_chunk(c, g);
+  const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
+
+  // row ids, sources and edge ids of a tile, loaded one tile ahead; `ex` holds
+  // the rows of the edges just before (lane 0) and just after (lane 1) the tile
+  int er[2], co[2], eid[2], ex;
+  auto load_tile = [&](int64_t t, int* per, int* pco, int* peid, int& pex) {
+    const int64_t base = t * TE;
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = base + nb * 16 + c;
+      const int64_t ec = e < E ? e : E - 1;
+      per[nb] = a.erow[ec];
+      pco[nb] = a.col[ec];
+      peid[nb] = use_eids ? a.eids[ec] : (int)ec;
+    }
+    const int64_t ee = l == 0 ? base - 1 : base + TE;
+    pex = a.erow[ee < 0 ? 0 : (ee < E ? ee : E - 1)];
+  };
+  if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, er, co, eid, ex);
 
   for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
     const int64_t base = t * TE;
     const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
-    int ri[2], rj[2], eid[2];
-    float dx[2], dy[2], dz[2], r2[2];
-    bool nf[2];
+    int ri[2], rj[2];
+    bool valid[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      const bool valid = e < E;
-      const int64_t ec = valid ? e : E - 1;
-      ri[nb] = clampi(a.erow[ec], N);
-      rj[nb] = clampi(a.col[ec], N);
-      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
-      nf[nb] = valid && (e == base || a.erow[e - 1] != a.erow[e]);
-      dx[nb] = dy[nb] = dz[nb] = r2[nb] = 0.f;
-      if constexpr (EQ) {
-        const f32x4 q = *reinterpret_cast<const f32x4*>(a.geo + ec * 4);
-        dx[nb] = q[0]; dy[nb] = q[1]; dz[nb] = q[2]; r2[nb] = q[3];
-      }
+      ri[nb] = clampi(er[nb], N);
+      rj[nb] = clampi(co[nb], N);
+      valid[nb] = nb * 16 + c < nvalid;
     }
-    const uint32_t mask = lo16(__ballot(nf[0])) | (lo16(__ballot(nf[1])) << 16);
-    const int nrank = __popc(mask);
-
-    // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
-    bf16x8 u[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], a.FE, g, r2[nb], EQ);
+    // this tile's gathers and geometry
+    bf16x4 pv[BH][2], qv[BH][2];
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
       const int hb = w * BH + j;
       const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
+        pv[j][nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)ri[nb] * (4u * H) + 2u * poff));
+        qv[j][nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)rj[nb] * (4u * H) + 2u * (H + poff)));
+      }
+    }
+    float r2[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = base + nb * 16 + c;
+      r2[nb] = EQ ? a.geo[(e < E ? e : E - 1) * 4 + 3] : 0.f;
+    }
+    bf16x8 u[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], a.FE, g, r2[nb], EQ);
+    f32x4 dgeo = zero4();   // delta of edge l, for the coordinate sums (last wave)
+    if (EQ && w == W - 1) {
+      const int64_t e = base + l;
+      dgeo = *reinterpret_cast<const f32x4*>(a.geo + (e < E ? e : E - 1) * 4);
+    }
+    // edge k starts a rank when it is the tile's first edge or its row differs
+    // from that of edge k - 1 (lane c - 1 of the same 16-lane row, or lane 15
+    // of the first block); the four 16-lane rows hold the same edges
+    const int up0 = __builtin_amdgcn_update_dpp(0, er[0], 0x111, 0xf, 0xf, false);
+    const int up1 = __builtin_amdgcn_update_dpp(0, er[1], 0x111, 0xf, 0xf, false);
+    const int last0 = __builtin_amdgcn_readlane(er[0], 15);
+    const bool nf0 = valid[0] && (c == 0 || up0 != er[0]);
+    const bool nf1 = valid[1] && ((c == 0 ? last0 : up1) != er[1]);
+    const uint32_t mask = lo16(__ballot(nf0)) | (lo16(__ballot(nf1)) << 16);
+    const int nrank = __popc(mask);
+    // the first rank's row starts in this tile unless edge base - 1 has the same
+    // row; the last rank's row ends in it unless edge base + TE has the same row
+    const bool start_in = base == 0 || __builtin_amdgcn_readlane(ex, 0) != __builtin_amdgcn_readlane(er[0], 0);
+    const bool end_in = base + TE >= E || __builtin_amdgcn_readlane(ex, 1) != __builtin_amdgcn_readlane(er[1], 15);
+    // the next tile's indices (consumed by the next iteration), issued after
+    // this tile's loads so that waiting for those does not wait for these
+    {
+      const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
+      load_tile(tn, er, co, eid, ex);
+    }
+
+    // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
+#pragma unroll
+    for (int j = 0; j < BH; ++j) {
+      const int hb = w * BH + j;
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
         mma(acc, wu[j], u[nb]);
-        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
-        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        mma(acc, Ipq, __builtin_shufflevector(pv[j][nb], qv[j][nb], 0, 1, 2, 3, 4, 5, 6, 7));   // + P_i + Q_j
         f32x4 x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i] + p[i] + q[i]);
+        for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
         put_chain(s_m1, hb, nb, l, x);
       }
     }
     if (w == 0 && g == 0) {
+      const bool nf[2] = {nf0, nf1};
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         const int k = nb * 16 + c;
-        if (nf[nb]) s_rowof[rank_of(mask, k)] = ri[nb];
-        if (EQ) { s_d[k][0] = dx[nb]; s_d[k][1] = dy[nb]; s_d[k][2] = dz[nb]; }
+        if (nf[nb]) {   // rank of edge k: its row and the row's edge count in this tile
+          const uint32_t rest = k >= 31 ? 0u : (mask & ~((2u << k) - 1u));
+          const int end = rest ? __ffs(rest) - 1 : nvalid;
+          const int r = rank_of(mask, k);
+          s_rowof[r] = ri[nb];
+          s_rspan[r] = rank_span(k, end - k);
+        }
       }
     }
+    if (EQ && w == W - 1 && l < TE) { s_d[l][0] = dgeo[0]; s_d[l][1] = dgeo[1]; s_d[l][2] = dgeo[2]; }
     __syncthreads();
 
     // ---- S2: m = SiLU(W_hl^T m1 + b2) for the wave's O rows; row sums -----
@@ -168,34 +236,35 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;
+      const f32x4 b2v = *reinterpret_cast<const f32x4*>(s_b2 + 16 * ob + 4 * g);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        f32x4 acc = zero4();
+        f32x4 acc = b2v;
 #pragma unroll
         for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1, kc, nb, l));
         f32x4 m;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) m[i] = silu_t<bf16>(acc[i] + b2v[j][i]);
+        for (int i = 0; i < 4; ++i) m[i] = silu_t<bf16>(acc[i]);
         mreg[j][nb] = m;
         if (EQ) put_chain(s_m, ob, nb, l, m);
       }
     }
-    const int rfirst = s_rowof[0];
+    // rank r is a whole row when it neither continues from the previous tile nor into the next
+    auto whole = [&](int r) { return (r > 0 || start_in) && (r < nrank - 1 || end_in); };
 #pragma unroll
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;
       const bf16x8 A = edge_major(mreg[j][0], mreg[j][1], I);
       for (int rb = 0; rb * 16 < nrank; ++rb) {
         f32x4 D = zero4();
-        mma(D, A, seg_chunk(mask, nvalid, rb, c, g));
+        const int r0 = rb * 16 + c;
+        mma(D, A, seg_chunk_span(r0 < nrank ? s_rspan[r0] : 0, g, s_lut));
         const int r = rb * 16 + c;
         if (r < nrank) {
-          const int R = s_rowof[r];
-          const int rs = a.rowptr[R], re = a.rowptr[R + 1];
-          if (rs >= base && re <= base + TE) {
-            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)R * a.smsg + 16 * ob + 4 * g) = pack4(D);
+          if (whole(r)) {
+            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)s_rowof[r] * a.smsg + 16 * ob + 4 * g) = pack4(D);
           } else {
-            const int slot = (R == rfirst) ? 0 : 1;
+            const int slot = r == 0 ? 0 : 1;
             *reinterpret_cast<f32x4*>(a.carry + ((int64_t)t * 2 + slot) * SEGW + 16 * ob + 4 * g) = D;
           }
         }
@@ -207,56 +276,72 @@ __global__ __launch_bounds__(W * 64) void coop_fwd_kernel(FwdArgs a) {
       float phi[2] = {0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < BM; ++j) {
+        const int mb = w * BM + j;
+        const f32x4 bx1v = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * mb + 4 * g);
+        const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * mb + 4 * g);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          f32x4 acc = zero4();
+          f32x4 acc = bx1v;
 #pragma unroll
           for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[i] + bx1v[j][i]) * w2mv[j][i];
+          for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[i]) * w2mv[i];
         }
       }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         phi[nb] += shfl_xor(phi[nb], 16);
         phi[nb] += shfl_xor(phi[nb], 32);
-        if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
+        if (g == 0) s_phi[nb * 16 + c][w] = phi[nb];
       }
       __syncthreads();
       // ---- coordinate sums: sum_j delta phi per row (hi + lo bf16 split) -----
       if (w == W - 1) {
+        if (l < TE) {   // phi of edge l: the waves' partials in wave order
+          float ph = 0.f;
+          if constexpr (W % 4 == 0) {
+#pragma unroll
+            for (int q = 0; q < W; q += 4) {
+              const f32x4 v = *reinterpret_cast<const f32x4*>(&s_phi[l][q]);
+              ph += v[0]; ph += v[1]; ph += v[2]; ph += v[3];
+            }
+          } else {
+#pragma unroll
+            for (int q = 0; q < W; ++q) ph += s_phi[l][q];
+          }
+          s_pht[l] = l < nvalid ? ph : 0.f;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        // lane (c, g) holds edges kappa_chain(g, s): 4g..4g+3 and 16+4g..16+4g+3
+        const f32x4 ph_lo = *reinterpret_cast<const f32x4*>(s_pht + 4 * g);
+        const f32x4 ph_hi = *reinterpret_cast<const f32x4*>(s_pht + 16 + 4 * g);
         bf16x8 ahi = zero_chunk<bf16>(), alo = zero_chunk<bf16>();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const int k = kappa_chain(g, s);
-          float v = 0.f;
-          if (c < 3 && k < nvalid) {
-            float ph = 0.f;
-#pragma unroll
-            for (int ww = 0; ww < W; ++ww) ph += s_phi[ww][k];
-            v = s_d[k][c] * ph;
-          }
+          const float v = c < 3 ? s_d[k][c < 3 ? c : 0] * (s < 4 ? ph_lo[s] : ph_hi[s - 4]) : 0.f;
           const bf16 hi = (bf16)v;
           ahi[s] = hi;
           alo[s] = (bf16)(v - (float)hi);
         }
         for (int rb = 0; rb * 16 < nrank; ++rb) {
-          const bf16x8 S = seg_chunk(mask, nvalid, rb, c, g);
+          const int r0 = rb * 16 + c;
+          const bf16x8 S = seg_chunk_span(r0 < nrank ? s_rspan[r0] : 0, g, s_lut);
           f32x4 D = zero4();
           mma(D, ahi, S);
           mma(D, alo, S);
           const int r = rb * 16 + c;
           if (g == 0 && r < nrank) {
-            const int R = s_rowof[r];
-            const int rs = a.rowptr[R], re = a.rowptr[R + 1];
-            if (rs >= base && re <= base + TE) {
-              const float sc = a.mean ? 1.0f / (float)(re - rs) : 1.0f;
-              float* o = a.out_mov + (int64_t)R * a.smov;
+            if (whole(r)) {
+              const float sc = a.mean ? 1.0f / (float)(s_rspan[r] >> 8) : 1.0f;
+              float* o = a.out_mov + (int64_t)s_rowof[r] * a.smov;
               o[0] = D[0] * sc;
               o[1] = D[1] * sc;
               o[2] = D[2] * sc;
             } else {
-              const int slot = (R == rfirst) ? 0 : 1;
+              const int slot = r == 0 ? 0 : 1;
               float* o = a.carry + ((int64_t)t * 2 + slot) * SEGW + O;
               o[0] = D[0];
               o[1] = D[1];
@@ -719,7 +804,8 @@ int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* co
 
 bool coop_supported(const LayerShape& s) {
   const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);
-  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32;   // forward: F_E features + r^2 hi/lo in 32 slots
+  // forward: F_E features + r^2 hi/lo in 32 slots; P | Q byte offsets in 32 bits
+  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32 && s.N * 4 * (int64_t)s.H < (int64_t(1) << 32);
 }
 
 int coop_bwd_blocks(const LayerShape& s) {

@@ -73,6 +73,38 @@ __device__ __forceinline__ bf16x8 seg_chunk(uint32_t mask, int nvalid, int rb, i
   return r;
 }
 
+// A operand that adds two 4-row halves of a B chunk: A[r][8g + s] = (r == 4g + (s & 3)), so
+// the product with B = [P rows 4g..4g+3 | Q rows 4g..4g+3] (lane g) is P + Q on rows 4g..4g+3
+__device__ __forceinline__ bf16x8 pair_sum_chunk(int c, int g) {
+  bf16x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = (c - 4 * g == (s & 3)) ? (bf16)1.0f : (bf16)0.0f;
+  return r;
+}
+
+// 16 bf16x4 patterns: element s of entry n is 1.0 when bit s of n is set
+__device__ __forceinline__ void seg_lut_init(uint2* lut, int tid) {
+  if (tid < 16) {
+    const uint32_t one = 0x3F80u;
+    lut[tid] = make_uint2(((tid & 1) ? one : 0u) | ((tid & 2) ? one << 16 : 0u),
+                          ((tid & 4) ? one : 0u) | ((tid & 8) ? one << 16 : 0u));
+  }
+}
+// Span of a rank within the tile: first edge (bits 0-7) and edge count (bits 8-15).
+__device__ __forceinline__ int rank_span(int start, int count) { return start | (count << 8); }
+// B operand S[edge][rank] from the span of rank 16 rb + c (0 when there is no such rank):
+// lane (c, g) covers edges kappa_chain(g, s) = 4g..4g+3 and 16+4g..16+4g+3
+__device__ __forceinline__ bf16x8 seg_chunk_span(int span, int g, const uint2* lut) {
+  const int start = span & 0xff, cnt = span >> 8;
+  const uint32_t mrow = cnt >= 32 ? 0xffffffffu : (((1u << cnt) - 1u) << start);
+  const uint2 lo = lut[(mrow >> (4 * g)) & 15u];
+  const uint2 hi = lut[(mrow >> (16 + 4 * g)) & 15u];
+  bf16x8 r;
+  const uint4 v = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
 __device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int eid, int FE, int g, float r2, bool eq) {
   const int slot0 = 8 * g;
   if (slot0 + 8 <= FE) return load_chunk(ef + (int64_t)eid * se + slot0);
