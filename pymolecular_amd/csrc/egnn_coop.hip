@@ -78,8 +78,10 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) float s_phi[TE][W];   // per-wave partial phi, edge-major
   __shared__ __attribute__((aligned(16))) float s_pht[TE];      // phi of each edge
   __shared__ float s_d[TE][4];
-  __shared__ int s_rowof[TE];
-  __shared__ int s_rspan[TE];
+  // row and span of each rank, double-buffered by tile parity: the last wave
+  // reads them for the coordinate sums while the next tile's ranks are written
+  __shared__ int s_rowof[2][TE];
+  __shared__ int s_rspan[2][TE];
   __shared__ uint2 s_lut[16];
   seg_lut_init(s_lut, threadIdx.x);
 
@@ -141,7 +143,8 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   };
   if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, er, co, eid, ex);
 
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+  int par = 0;
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x, par ^= 1) {
     const int64_t base = t * TE;
     const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
     int ri[2], rj[2];
@@ -223,8 +226,8 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
           const uint32_t rest = k >= 31 ? 0u : (mask & ~((2u << k) - 1u));
           const int end = rest ? __ffs(rest) - 1 : nvalid;
           const int r = rank_of(mask, k);
-          s_rowof[r] = ri[nb];
-          s_rspan[r] = rank_span(k, end - k);
+          s_rowof[par][r] = ri[nb];
+          s_rspan[par][r] = rank_span(k, end - k);
         }
       }
     }
@@ -258,11 +261,11 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       for (int rb = 0; rb * 16 < nrank; ++rb) {
         f32x4 D = zero4();
         const int r0 = rb * 16 + c;
-        mma(D, A, seg_chunk_span(r0 < nrank ? s_rspan[r0] : 0, g, s_lut));
+        mma(D, A, seg_chunk_span(r0 < nrank ? s_rspan[par][r0] : 0, g, s_lut));
         const int r = rb * 16 + c;
         if (r < nrank) {
           if (whole(r)) {
-            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)s_rowof[r] * a.smsg + 16 * ob + 4 * g) = pack4(D);
+            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)s_rowof[par][r] * a.smsg + 16 * ob + 4 * g) = pack4(D);
           } else {
             const int slot = r == 0 ? 0 : 1;
             *reinterpret_cast<f32x4*>(a.carry + ((int64_t)t * 2 + slot) * SEGW + 16 * ob + 4 * g) = D;
@@ -328,15 +331,15 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         }
         for (int rb = 0; rb * 16 < nrank; ++rb) {
           const int r0 = rb * 16 + c;
-          const bf16x8 S = seg_chunk_span(r0 < nrank ? s_rspan[r0] : 0, g, s_lut);
+          const bf16x8 S = seg_chunk_span(r0 < nrank ? s_rspan[par][r0] : 0, g, s_lut);
           f32x4 D = zero4();
           mma(D, ahi, S);
           mma(D, alo, S);
           const int r = rb * 16 + c;
           if (g == 0 && r < nrank) {
             if (whole(r)) {
-              const float sc = a.mean ? 1.0f / (float)(s_rspan[r] >> 8) : 1.0f;
-              float* o = a.out_mov + (int64_t)s_rowof[r] * a.smov;
+              const float sc = a.mean ? 1.0f / (float)(s_rspan[par][r] >> 8) : 1.0f;
+              float* o = a.out_mov + (int64_t)s_rowof[par][r] * a.smov;
               o[0] = D[0] * sc;
               o[1] = D[1] * sc;
               o[2] = D[2] * sc;
@@ -351,7 +354,9 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         }
       }
     }
-    __syncthreads();
+    // With the coordinate stages the S3 barrier orders this tile's reads of
+    // s_m1 before the next tile's writes; the rank tables are double-buffered.
+    if constexpr (!EQ) __syncthreads();
   }
 }
 
@@ -385,7 +390,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];   // [edge][slot] edge features of the tile
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  const bf16* PQ = (const bf16*)a.PQ;
+  const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
   const bf16* ef = (const bf16*)a.ef;
   const bf16* gmsg = (const bf16*)a.gmsg;
   bf16* Gh = (bf16*)a.Gh;
@@ -490,7 +495,6 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
         gmr[j][nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri[nb] * a.sgm + 16 * (w * BO + j) + 4 * g);
-
     // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
     bf16x8 u[2];
 #pragma unroll
@@ -512,8 +516,8 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
         mma(acc, wu[j], u[nb]);
-        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
-        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>((const bf16*)(PQb) + (int64_t)ri[nb] * 2 * H + poff));
+        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>((const bf16*)(PQb) + (int64_t)rj[nb] * 2 * H + H + poff));
         f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -538,13 +542,13 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
       const f32x4 b2v = *reinterpret_cast<const f32x4*>(s_b2 + 16 * ob + 4 * g);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        f32x4 acc = zero4();
+        f32x4 acc = b2v;
 #pragma unroll
         for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1, kc, nb, l));
         f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const YD r = silu_yd<bf16>(acc[i] + b2v[i]);
+          const YD r = silu_yd<bf16>(acc[i]);
           y[nb][i] = r.y;
           d[i] = r.d;
         }
@@ -562,7 +566,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
         const int mb = w * BM + j;
         const f32x4 bx1v = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * mb + 4 * g);
         const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * mb + 4 * g);
-        f32x4 gq[2], accq[2] = {zero4(), zero4()};
+        f32x4 gq[2], accq[2] = {bx1v, bx1v};
 #pragma unroll
         for (int kc = 0; kc < KO; ++kc) {   // each A fragment read once for both edge blocks
           const bf16x8 A = *reinterpret_cast<const bf16x8*>(s_wmovT + ((mb * KO + kc) * 64 + l) * 8);
@@ -574,7 +578,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
           const f32x4 acc = accq[nb];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const YD r = silu_yd<bf16>(acc[i] + bx1v[i]);
+            const YD r = silu_yd<bf16>(acc[i]);
             phi[nb] += r.y * w2mv[i];
             gq[nb][i] = gphi[nb] * w2mv[i] * r.d;
             vw2m[j][i] += r.y * gphi[nb];
@@ -704,7 +708,10 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
         }
       }
     }
-    __syncthreads();
+    // With the coordinate stages, every buffer the next tile writes before its
+    // first barrier (s_m1 = s_ga2, s_u) was last read before this tile's g_r
+    // barrier, so the tile needs no closing barrier.
+    if constexpr (!EQ) __syncthreads();
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       ri[nb] = n_ri[nb]; rj[nb] = n_rj[nb]; eid[nb] = n_eid[nb]; r2[nb] = n_r2[nb]; gphi[nb] = n_gphi[nb];
