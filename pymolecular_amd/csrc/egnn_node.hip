@@ -126,8 +126,20 @@ struct FragDesc {
   const void* src; int64_t ld;
 };
 
+// All weight preparation of one layer call in one launch: blockIdx.y selects the
+// job (fragment sets 0..nfrag-1, then the [W_n1 | W_n2] copy, then the fp32
+// vectors), blockIdx.x strides over the job's elements.
+struct PrepArgs {
+  FragDesc f0, f1, f2, f3, f4, f5;
+  int nfrag;
+  const void* w1; void* wn;                 // [W_n1 | W_n2] (F x 2H) from the packed w1_msg rows
+  const void *b2, *bx1, *w2m, *wd;
+  float *b2f, *bx1f, *w2mf, *wdf;
+  int F, FE, H, O, M, eq;
+};
+
 template <typename T>
-__global__ void frag_build_kernel(FragDesc d, int F, int FE, int H, int eq) {
+__device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq) {
   const int64_t total = (int64_t)(d.R / 16) * d.nkc * kFragElems;
   const T* src = (const T*)d.src;
   T* dst = (T*)d.dst;
@@ -160,54 +172,65 @@ __global__ void frag_build_kernel(FragDesc d, int F, int FE, int H, int eq) {
 }
 
 template <typename T>
-__global__ void vec_prep_kernel(const T* b2, const T* bx1, const T* w2m, const T* wd, float* b2f, float* bx1f,
-                                float* w2mf, float* wdf, int O, int M, int H) {
-  int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < O) b2f[t] = b2 ? to_f32(b2[t]) : 0.0f;
-  if (t < H) wdf[t] = wd ? to_f32(wd[t]) : 0.0f;
-  if (t < M + 4) {
-    bx1f[t] = (bx1 && t < M) ? to_f32(bx1[t]) : 0.0f;
-    w2mf[t] = (w2m && t < M) ? to_f32(w2m[t]) : 0.0f;
-  }
-}
-
-template <typename T>
-__global__ void wn_prep_kernel(const T* __restrict__ w1, T* __restrict__ wn, int F, int H) {
-  const int64_t total = (int64_t)F * 2 * H;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t f = t / (2 * H), n = t % (2 * H);
-    wn[t] = n < H ? w1[f * H + n] : w1[(F + f) * H + (n - H)];
+__global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
+  const int job = blockIdx.y;
+  if (job < p.nfrag) {
+    switch (job) {
+      case 0: frag_build<T>(p.f0, p.F, p.FE, p.H, p.eq); break;
+      case 1: frag_build<T>(p.f1, p.F, p.FE, p.H, p.eq); break;
+      case 2: frag_build<T>(p.f2, p.F, p.FE, p.H, p.eq); break;
+      case 3: frag_build<T>(p.f3, p.F, p.FE, p.H, p.eq); break;
+      case 4: frag_build<T>(p.f4, p.F, p.FE, p.H, p.eq); break;
+      default: frag_build<T>(p.f5, p.F, p.FE, p.H, p.eq); break;
+    }
+  } else if (job == p.nfrag) {
+    const T* w1 = (const T*)p.w1;
+    T* wn = (T*)p.wn;
+    const int64_t total = (int64_t)p.F * 2 * p.H;
+    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+      const int64_t f = t / (2 * p.H), n = t % (2 * p.H);
+      wn[t] = n < p.H ? w1[f * p.H + n] : w1[(p.F + f) * p.H + (n - p.H)];
+    }
+  } else {
+    const int n = p.O > p.M + 4 ? (p.O > p.H ? p.O : p.H) : (p.M + 4 > p.H ? p.M + 4 : p.H);
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x) {
+      if (t < p.O) p.b2f[t] = p.b2 ? to_f32(((const T*)p.b2)[t]) : 0.0f;
+      if (t < p.H) p.wdf[t] = p.wd ? to_f32(((const T*)p.wd)[t]) : 0.0f;
+      if (t < p.M + 4) {
+        p.bx1f[t] = (p.bx1 && t < p.M) ? to_f32(((const T*)p.bx1)[t]) : 0.0f;
+        p.w2mf[t] = (p.w2m && t < p.M) ? to_f32(((const T*)p.w2m)[t]) : 0.0f;
+      }
+    }
   }
 }
 
 template <typename T>
 static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
                      const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st) {
-  auto build = [&](void* dst, int R, int K, int kind, int chain, const void* src, int64_t ld) {
+  PrepArgs p{};
+  FragDesc* slots[6] = {&p.f0, &p.f1, &p.f2, &p.f3, &p.f4, &p.f5};
+  int64_t most = 0;
+  auto add = [&](void* dst, int R, int K, int kind, int chain, const void* src, int64_t ld) {
     if (!dst) return;
-    FragDesc d{dst, R, K, (int)cdiv(K, 32), kind, chain, src, ld};
-    int64_t total = (int64_t)(R / 16) * d.nkc * kFragElems;
-    int blocks = (int)std::min<int64_t>(cdiv(total, 256), 4096);
-    hipLaunchKernelGGL(frag_build_kernel<T>, dim3(blocks), dim3(256), 0, st, d, s.F, s.FE, s.H, s.eq ? 1 : 0);
+    *slots[p.nfrag++] = FragDesc{dst, R, K, (int)cdiv(K, 32), kind, chain, src, ld};
+    most = std::max<int64_t>(most, (int64_t)(R / 16) * cdiv(K, 32) * kFragElems);
   };
-  build(fr.hlT, s.O, s.H, FK_WT, 1, w2, s.O);        // A[o][h] = W_hl[h][o]
-  if (s.eq) build(fr.movT, s.M, s.O, FK_WT, 1, w1m, s.M);  // A[m][o] = W1mov[o][m]
-  if (s.NUC) build(fr.u, s.H, s.KU, FK_U, 0, w1, s.H);
+  add(fr.hlT, s.O, s.H, FK_WT, 1, w2, s.O);               // A[o][h] = W_hl[h][o]
+  if (s.eq) add(fr.movT, s.M, s.O, FK_WT, 1, w1m, s.M);   // A[m][o] = W1mov[o][m]
+  if (s.NUC) add(fr.u, s.H, s.KU, FK_U, 0, w1, s.H);
   if (with_bwd) {
-    if (s.eq) build(fr.mov, s.O, s.M, FK_W, 1, w1m, s.M);   // A[o][m] = W1mov[o][m]
-    build(fr.hl, s.H, s.O, FK_W, 1, w2, s.O);               // A[h][o] = W_hl[h][o]
-    if (s.eq) build(fr.uT, 16, s.H, FK_UT, 1, w1, s.H);
+    if (s.eq) add(fr.mov, s.O, s.M, FK_W, 1, w1m, s.M);   // A[o][m] = W1mov[o][m]
+    add(fr.hl, s.H, s.O, FK_W, 1, w2, s.O);               // A[h][o] = W_hl[h][o]
+    if (s.eq) add(fr.uT, 16, s.H, FK_UT, 1, w1, s.H);
   }
-  {
-    const int64_t tot = (int64_t)s.F * 2 * s.H;
-    hipLaunchKernelGGL(wn_prep_kernel<T>, dim3((unsigned)std::min<int64_t>(cdiv(tot, 256), 2048)), dim3(256), 0, st,
-                       (const T*)w1, (T*)fr.wn, s.F, s.H);
-  }
-  int n = std::max({s.O, s.M + 4, s.H});
-  const T* wd = s.eq ? (const T*)w1 + (int64_t)(2 * s.F) * s.H : nullptr;
-  hipLaunchKernelGGL(vec_prep_kernel<T>, dim3((unsigned)cdiv(n, 256)), dim3(256), 0, st, (const T*)b2,
-                     (const T*)(s.eq ? bx1 : nullptr), (const T*)(s.eq ? w2m : nullptr), wd, fr.b2f, fr.bx1f,
-                     fr.w2mf, fr.wdf, s.O, s.M, s.H);
+  p.w1 = w1; p.wn = fr.wn;
+  most = std::max<int64_t>(most, (int64_t)s.F * 2 * s.H);
+  p.b2 = b2; p.bx1 = s.eq ? bx1 : nullptr; p.w2m = s.eq ? w2m : nullptr;
+  p.wd = s.eq ? (const T*)w1 + (int64_t)(2 * s.F) * s.H : nullptr;
+  p.b2f = fr.b2f; p.bx1f = fr.bx1f; p.w2mf = fr.w2mf; p.wdf = fr.wdf;
+  p.F = s.F; p.FE = s.FE; p.H = s.H; p.O = s.O; p.M = s.M; p.eq = s.eq ? 1 : 0;
+  const unsigned bx = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(most, 256), 1024));
+  hipLaunchKernelGGL(prep_kernel<T>, dim3(bx, (unsigned)(p.nfrag + 2)), dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
@@ -395,19 +418,15 @@ __global__ __launch_bounds__(256) void gemm2_kernel(Gemm2Args g) {
 // as gemm2_kernel.
 // ---------------------------------------------------------------------------
 namespace {
-constexpr int GB_M = 128, GB_N = 128, GB_K = 64;
-constexpr int GB_PK = GB_K + 8;     // row pitch of a k-contiguous tile (bf16)
-constexpr int GB_PM = GB_M + 16;    // row pitch of an m/n-contiguous tile (bf16)
-constexpr int GB_TILE = (GB_M * GB_PK > GB_K * GB_PM) ? GB_M * GB_PK : GB_K * GB_PM;
-
 typedef bf16 bf16x4v __attribute__((ext_vector_type(4)));
 
-// 4 consecutive k (rows kb .. kb+3) of column col0 + c from an m/n-contiguous tile:
-// within a 16-lane group, lane j supplies the address of row kb + j/4, columns
-// col0 + 4 (j % 4) .. + 3, and lane c receives element c % 4 of the rows
-// supplied by lanes c/4 + 4 i, i = 0..3
+// 4 consecutive k (rows kb .. kb+3) of column col0 + c from an m/n-contiguous tile
+// of row pitch P: within a 16-lane group, lane j supplies the address of row
+// kb + j/4, columns col0 + 4 (j % 4) .. + 3, and lane c receives element c % 4
+// of the rows supplied by lanes c/4 + 4 i, i = 0..3
+template <int P>
 __device__ __forceinline__ bf16x4v ld_tr4(const bf16* tile, int kb, int col0, int lane16) {
-  const bf16* p = tile + (kb + (lane16 >> 2)) * GB_PM + col0 + 4 * (lane16 & 3);
+  const bf16* p = tile + (kb + (lane16 >> 2)) * P + col0 + 4 * (lane16 & 3);
   return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)p);
 }
 __device__ __forceinline__ bf16x8 join_tr(const bf16x4v& lo, const bf16x4v& hi) {
@@ -415,42 +434,50 @@ __device__ __forceinline__ bf16x8 join_tr(const bf16x4v& lo, const bf16x4v& hi) 
 }
 }  // namespace
 
-template <bool A_KC, bool B_NC, int BM>
+// BM x BN output tile per 256-thread block (2 x 2 waves), K in slices of BK
+// staged through NBUF LDS buffers (2: the next slice is loaded into registers
+// while the current one is multiplied; 1: one buffer, refilled after each slice).
+template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
   constexpr int WM = BM / 2, MI = WM / 16;              // rows per wave, MFMA row blocks per wave
-  constexpr int NLA = BM * GB_K / 8 / 256;              // 16-byte A vectors per thread per stage
-  constexpr int TA_ = A_KC ? BM * GB_PK : GB_K * (BM + 16);
-  constexpr int PA = BM + 16;                           // row pitch of an m-contiguous A tile
-  constexpr int CP = GB_N + 4;                          // row pitch of the fp32 output tile
-  constexpr int MAIN = 2 * TA_ + 2 * GB_TILE;           // bf16 elements of the operand buffers
+  constexpr int WN = BN / 2, NJ = WN / 16;              // columns per wave, MFMA column blocks per wave
+  constexpr int PK = BK + 8;                            // row pitch of a k-contiguous tile (bf16)
+  constexpr int PA = BM + 16, PB = BN + 16;             // row pitches of m- / n-contiguous tiles
+  constexpr int NLA = BM * BK / 8 / 256;                // 16-byte A vectors per thread per slice
+  constexpr int NLB = BN * BK / 8 / 256;                // 16-byte B vectors per thread per slice
+  constexpr int TA_ = A_KC ? BM * PK : BK * PA;
+  constexpr int TB_ = B_NC ? BK * PB : BN * PK;
+  constexpr int CP = BN + 4;                            // row pitch of the fp32 output tile
+  constexpr int MAIN = NBUF * (TA_ + TB_);              // bf16 elements of the operand buffers
   constexpr int OUTB = BM * CP * 2;                     // bf16-element size of the fp32 output tile
+  static_assert(NLA >= 1 && NLB >= 1 && BM * BK % 2048 == 0 && BN * BK % 2048 == 0, "tile too small");
   __shared__ __attribute__((aligned(16))) bf16 smem[MAIN > OUTB ? MAIN : OUTB];
   bf16* const As0 = smem;
-  bf16* const Bs0 = smem + 2 * TA_;
+  bf16* const Bs0 = smem + NBUF * TA_;
   float* const Cs = reinterpret_cast<float*>(smem);
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * GB_N;
+  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
   int64_t kbeg = 0, kend = g.K;
   if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
   const bf16* A = (const bf16*)g.A;
   const bf16* A2 = (const bf16*)g.A2;
   const bf16* B = (const bf16*)g.B;
 
-  f32x4 acc[MI][4];
+  f32x4 acc[MI][NJ];
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  bf16x8 ra[NLA], rb[4];
+  bf16x8 ra[NLA], rb[NLB];
   auto load_stage = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < NLA; ++i) {
       const int idx = tid + 256 * i;
       bf16x8 va = zero_chunk<bf16>();
       if constexpr (A_KC) {   // A[m][k], or A2[m][k - a_split]
-        const int r = idx >> 3, q = idx & 7;
+        const int r = idx / (BK / 8), q = idx % (BK / 8);
         const int64_t m = m0 + r, k = k0 + 8 * q;
         if (m < g.M && m != g.a_ones_row && k < kend) {
           const bf16* Ab = (A2 && k >= g.a_split) ? A2 + m * g.lda2 - g.a_split : A + m * g.lda;
@@ -475,11 +502,11 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
       ra[i] = va;
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NLB; ++i) {
       const int idx = tid + 256 * i;
       bf16x8 vb = zero_chunk<bf16>();
       if constexpr (B_NC) {   // B[k][n], or B[b_kidx[k]][n]
-        const int r = idx >> 4, q = idx & 15;
+        const int r = idx / (BN / 8), q = idx % (BN / 8);
         const int64_t k = k0 + r, n = n0 + 8 * q;
         if (k < kend && n < g.N) {
           const int64_t kr = g.b_kidx ? (int64_t)g.b_kidx[k] : k;
@@ -488,7 +515,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
             for (int u = 0; u < 8; ++u) if (n + u < g.N) vb[u] = B[kr * g.ldb + n + u];
         }
       } else {                // B[n][k]
-        const int r = idx >> 3, q = idx & 7;
+        const int r = idx / (BK / 8), q = idx % (BK / 8);
         const int64_t n = n0 + r, k = k0 + 8 * q;
         if (n < g.N && k < kend) {
           if (k + 8 <= kend) vb = *reinterpret_cast<const bf16x8*>(B + n * g.ldb + k);
@@ -501,18 +528,18 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
   };
   auto store_stage = [&](int buf) {
     bf16* At = As0 + buf * TA_;
-    bf16* Bt = Bs0 + buf * GB_TILE;
+    bf16* Bt = Bs0 + buf * TB_;
 #pragma unroll
     for (int i = 0; i < NLA; ++i) {
       const int idx = tid + 256 * i;
-      if constexpr (A_KC) *reinterpret_cast<bf16x8*>(&At[(idx >> 3) * GB_PK + 8 * (idx & 7)]) = ra[i];
+      if constexpr (A_KC) *reinterpret_cast<bf16x8*>(&At[(idx / (BK / 8)) * PK + 8 * (idx % (BK / 8))]) = ra[i];
       else *reinterpret_cast<bf16x8*>(&At[(idx / (BM / 8)) * PA + 8 * (idx % (BM / 8))]) = ra[i];
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NLB; ++i) {
       const int idx = tid + 256 * i;
-      if constexpr (!B_NC) *reinterpret_cast<bf16x8*>(&Bt[(idx >> 3) * GB_PK + 8 * (idx & 7)]) = rb[i];
-      else *reinterpret_cast<bf16x8*>(&Bt[(idx >> 4) * GB_PM + 8 * (idx & 15)]) = rb[i];
+      if constexpr (!B_NC) *reinterpret_cast<bf16x8*>(&Bt[(idx / (BK / 8)) * PK + 8 * (idx % (BK / 8))]) = rb[i];
+      else *reinterpret_cast<bf16x8*>(&Bt[(idx / (BN / 8)) * PB + 8 * (idx % (BN / 8))]) = rb[i];
     }
   };
 
@@ -522,50 +549,63 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
     store_stage(0);
   }
   __syncthreads();
-  for (int64_t k0 = kbeg; k0 < kend; k0 += GB_K) {
-    const bool more = k0 + GB_K < kend;
-    if (more) load_stage(k0 + GB_K);
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (NBUF == 2 && more) load_stage(k0 + BK);
     const bf16* At = As0 + buf * TA_;
-    const bf16* Bt = Bs0 + buf * GB_TILE;
+    const bf16* Bt = Bs0 + buf * TB_;
 #pragma unroll
-    for (int ks = 0; ks < GB_K / 32; ++ks) {
-      bf16x8 a[MI], b[4];
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8 a[MI], b[NJ];
 #pragma unroll
       for (int i = 0; i < MI; ++i) {
-        if constexpr (A_KC) a[i] = *reinterpret_cast<const bf16x8*>(&At[(wm * WM + 16 * i + c) * GB_PK + 32 * ks + 8 * gq]);
-        else {
-          const bf16* p = At + (32 * ks + 8 * gq + (c >> 2)) * PA + wm * WM + 16 * i + 4 * (c & 3);
-          const bf16x4v lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)p);
-          const bf16x4v hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4v*)(p + 4 * PA));
-          a[i] = join_tr(lo, hi);
-        }
+        if constexpr (A_KC) a[i] = *reinterpret_cast<const bf16x8*>(&At[(wm * WM + 16 * i + c) * PK + 32 * ks + 8 * gq]);
+        else a[i] = join_tr(ld_tr4<PA>(At, 32 * ks + 8 * gq, wm * WM + 16 * i, c),
+                            ld_tr4<PA>(At, 32 * ks + 8 * gq + 4, wm * WM + 16 * i, c));
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        if constexpr (!B_NC) b[j] = *reinterpret_cast<const bf16x8*>(&Bt[(wn * 64 + 16 * j + c) * GB_PK + 32 * ks + 8 * gq]);
-        else b[j] = join_tr(ld_tr4(Bt, 32 * ks + 8 * gq, wn * 64 + 16 * j, c), ld_tr4(Bt, 32 * ks + 8 * gq + 4, wn * 64 + 16 * j, c));
+      for (int j = 0; j < NJ; ++j) {
+        if constexpr (!B_NC) b[j] = *reinterpret_cast<const bf16x8*>(&Bt[(wn * WN + 16 * j + c) * PK + 32 * ks + 8 * gq]);
+        else b[j] = join_tr(ld_tr4<PB>(Bt, 32 * ks + 8 * gq, wn * WN + 16 * j, c),
+                            ld_tr4<PB>(Bt, 32 * ks + 8 * gq + 4, wn * WN + 16 * j, c));
       }
 #pragma unroll
       for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
+        for (int j = 0; j < NJ; ++j) mma(acc[i][j], a[i], b[j]);
     }
-    if (more) store_stage(buf ^ 1);
+    if (NBUF == 1) {   // refill the one buffer once every wave is done with it
+      if (more) {
+        __syncthreads();
+        load_stage(k0 + BK);
+        store_stage(0);
+      }
+    } else {
+      if (more) store_stage(buf ^ 1);
+      buf ^= 1;
+    }
     __syncthreads();
-    buf ^= 1;
   }
 
   // ---- epilogue: the fp32 tile goes through LDS so that every global access is a 16-byte row segment
 #pragma unroll
   for (int i = 0; i < MI; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < NJ; ++j)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) Cs[(wm * WM + 16 * i + 4 * gq + r) * CP + wn * 64 + 16 * j + c] = acc[i][j][r];
+      for (int r = 0; r < 4; ++r) Cs[(wm * WM + 16 * i + 4 * gq + r) * CP + wn * WN + 16 * j + c] = acc[i][j][r];
   __syncthreads();
   const bool vec_n = (g.N % 8 == 0);
-  for (int v = tid; v < BM * (GB_N / 8); v += 256) {
-    const int r = v / (GB_N / 8), q = v % (GB_N / 8);
+  // each thread always handles the same 8 columns (256 is a multiple of BN / 8): bias loaded once
+  static_assert(256 % (BN / 8) == 0, "column group must not depend on the row");
+  float bv[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int64_t n = n0 + 8 * (tid % (BN / 8)) + u;
+    bv[u] = (g.bias && n < g.N && n < g.bias_len) ? ld_elem(g.bias, n, g.bias_bf16) : 0.f;
+  }
+  for (int v = tid; v < BM * (BN / 8); v += 256) {
+    const int r = v / (BN / 8), q = v % (BN / 8);
     const int64_t m = m0 + r, n = n0 + 8 * q;
     if (m >= g.M || n >= g.N) continue;
     float x[8];
@@ -584,9 +624,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
       }
       continue;
     }
-    if (g.bias)
 #pragma unroll
-      for (int u = 0; u < 8; ++u) if (u < nv && n + u < g.bias_len) x[u] += ld_elem(g.bias, n + u, g.bias_bf16);
+    for (int u = 0; u < 8; ++u) x[u] += bv[u];
     const bool full = nv == 8 && vec_n;
     if (g.zd) {   // * SiLU'(z)
       bf16x8 z;
@@ -667,12 +706,15 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
                                  : al(g.C, g.ldc) && al(g.Cpre, g.ldpre) && al(g.resid, g.ldr) && al(g.zd, g.ldz));
   if (compute_bf16 && g.a_bf16 && g.b_bf16 && (g.c_bf16 || g.partial) && rows16) {
     // 128-row tiles when they fill the device twice over, else 64-row tiles
-    const bool big = cdiv(g.M, 128) * cdiv(g.N, GB_N) * (int64_t)gz >= 512;
-    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 64), (unsigned)cdiv(g.N, GB_N), gz);
-#define GB_LAUNCH(AK, BN)                                                                  \
-    do {                                                                                   \
-      if (big) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BN, 128>), gb, dim3(256), 0, st, g); \
-      else hipLaunchKernelGGL((gemm_bf16_kernel<AK, BN, 64>), gb, dim3(256), 0, st, g);      \
+    // 128 x 128 tiles for long split-K reductions and for grids of 2048 or more
+    // such tiles; else 32 x 64 tiles, whose larger grids hide the memory latency
+    // of the short K loops of the node products
+    const bool big = (g.ksplit > 0 && g.ksplit >= 2048) || cdiv(g.M, 128) * cdiv(g.N, 128) * (int64_t)gz >= 2048;
+    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, big ? 128 : 64), gz);
+#define GB_LAUNCH(AK, BNC)                                                                         \
+    do {                                                                                           \
+      if (big) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 128, 64, 2>), gb, dim3(256), 0, st, g); \
+      else hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 32, 64, 64, 2>), gb, dim3(256), 0, st, g);   \
     } while (0)
     if (g.a_kc && g.b_nc) GB_LAUNCH(true, true);
     else if (g.a_kc) GB_LAUNCH(true, false);
