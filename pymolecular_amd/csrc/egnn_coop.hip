@@ -776,11 +776,235 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// backward of the non-equivariant layer (MPNN), H = O = 128, 16 waves per tile
+// ---------------------------------------------------------------------------
+// Wave w owns feature rows [16 rb, 16 rb + 16), rb = w & 7, of every stage for
+// the 16 edges of half hf = w >> 3 of the tile.  Compared with one wave per row
+// block over both halves, each wave holds half the per-edge state, so 16 waves
+// (4 per SIMD) fit one CU and hide each other's latencies.  The edge-major
+// operand of dW_hl is assembled in LDS from the two halves; the row-block owner
+// of half hf accumulates the columns [64 hf, 64 hf + 64) over all 32 edges.
+// Per-row sums over the edges (db2, dW_e) are per-half partials combined at the
+// end in half order.  Same stages and results as coop_bwd_kernel<..., false>.
+template <int NU>
+__global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
+  constexpr int H = 128, O = 128, NRB = 8;
+  constexpr int KH = H / 32, KO = O / 32;
+  constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
+  constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 halves (8 KB)
+  static_assert(CH == NRB * 64 * 8, "chain and edge-major buffers share one size");
+  // activation buffers, one array so that the final reduction can use all of it:
+  //   [0] m1 (S1 -> S2), g_a2 (S4 -> S5)   [1] g_a2 edge-major (S4 -> S5)   [2] m1 edge-major (S1 -> S5)
+  __shared__ __attribute__((aligned(16))) bf16 s_act[3 * CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];
+  __shared__ __attribute__((aligned(16))) float s_b2[O];
+  bf16* const s_m1 = s_act;
+  bf16* const s_ga2 = s_act;
+  bf16* const s_ga2N = s_act + CH;
+  bf16* const s_m1N = s_act + 2 * CH;
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int rb = w & 7, hf = w >> 3;
+  const bf16* PQ = (const bf16*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const bf16* gmsg = (const bf16*)a.gmsg;
+  bf16* Gh = (bf16*)a.Gh;
+  const int64_t E = a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+
+  for (int q = threadIdx.x; q < O; q += 1024) s_b2[q] = a.fr.b2f[q];
+  for (int q = threadIdx.x; q < NRB * KO * kFragElems / 8; q += 1024)
+    reinterpret_cast<bf16x8*>(s_whl)[q] = reinterpret_cast<const bf16x8*>(a.fr.hl)[q];
+  const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)rb * kFragElems + l * 8);
+  bf16x8 whlT[KH];
+#pragma unroll
+  for (int kc = 0; kc < KH; ++kc)
+    whlT[kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)rb * KH + kc) * kFragElems + l * 8);
+  const bf16x8 I = ident_chunk(c, g);
+
+  // weight-gradient accumulators: dW_hl columns [64 hf, 64 hf + 64) of the wave's rows
+  f32x4 acc_whl[4], acc_wu[NU > 0 ? NU : 1];
+  f32x4 vb2 = zero4();
+#pragma unroll
+  for (int cb = 0; cb < 4; ++cb) acc_whl[cb] = zero4();
+#pragma unroll
+  for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
+
+  // indices of this wave's 16 edges of a tile, loaded one tile ahead of use
+  int ri, rj, eid;
+  auto load_tile = [&](int64_t t, int& pri, int& prj, int& peid) {
+    const int64_t e = t * TE + hf * 16 + c;
+    const int64_t ec = e < E ? e : E - 1;
+    pri = clampi(a.erow[ec], N);
+    prj = clampi(a.col[ec], N);
+    peid = (a.eids && FE > 0) ? clampi(a.eids[ec], (int)E) : (int)ec;
+  };
+  if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, ri, rj, eid);
+  __syncthreads();   // weights and vectors in LDS
+
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+    const int64_t base = t * TE;
+    const bool valid = base + hf * 16 + c < E;
+    // the incoming message gradient of the wave's rows (used in S4), issued early
+    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri * a.sgm + 16 * rb + 4 * g);
+
+    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j) -----------------------------
+    const bf16x8 u = input_chunk(ef, a.se, eid, FE, g, 0.f, false);
+    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, [edge][slot], for dW_e
+      *reinterpret_cast<bf16x8*>(s_u + (hf * 16 + c) * FEP + 8 * g) = valid ? u : zero_chunk<bf16>();
+    bf16x4 s1;
+    {
+      const int poff = 32 * (rb >> 1) + 8 * g + 4 * (rb & 1);
+      f32x4 acc = zero4();
+      mma(acc, wu, u);
+      const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri * 2 * H + poff));
+      const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj * 2 * H + H + poff));
+      f32x4 y, d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+        y[i] = r.y;
+        d[i] = r.d;
+      }
+      s1 = pack4(d);
+      put_chain(s_m1, rb, hf, l, y);
+      *reinterpret_cast<bf16x4*>(s_m1N + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(y, I));
+    }
+    __syncthreads();
+
+    // ---- S2: s2 = SiLU'(W_hl^T m1 + b2) -------------------------------------------
+    bf16x4 s2;
+    {
+      f32x4 acc = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
+#pragma unroll
+      for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[kc], get_chain(s_m1, kc, hf, l));
+      f32x4 d;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) d[i] = silu_yd<bf16>(acc[i]).d;
+      s2 = pack4(d);
+    }
+    __syncthreads();
+
+    // the next tile's indices (consumed by the next iteration)
+    int n_ri, n_rj, n_eid;
+    load_tile(t + gridDim.x < a.ntiles ? t + gridDim.x : t, n_ri, n_rj, n_eid);
+
+    // ---- S4: g_a2 = gm_i SiLU'(pre2) ------------------------------------------------
+    {
+      const f32x4 gm = valid ? unpack4(gmr) : zero4();
+      const f32x4 d = unpack4(s2);
+      f32x4 ga;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ga[i] = gm[i] * d[i];
+        vb2[i] += ga[i];
+      }
+      put_chain(s_ga2, rb, hf, l, ga);
+      *reinterpret_cast<bf16x4*>(s_ga2N + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(ga, I));
+    }
+    __syncthreads();
+
+    // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1) ------------------------------------------
+    {
+      f32x4 acch = zero4();
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc)
+        mma(acch, *reinterpret_cast<const bf16x8*>(s_whl + ((rb * KO + kc) * 64 + l) * 8), get_chain(s_ga2, kc, hf, l));
+      const f32x4 d = unpack4(s1);
+      f32x4 g1;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) g1[i] = acch[i] * d[i];
+      if (valid) *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(g1);
+      // dW_hl rows rb, columns of half hf: sum_e m1[h][e] g_a2[o][e]
+      const bf16x8 m1N = get_norm(s_m1N, rb, l);
+#pragma unroll
+      for (int cb = 0; cb < 4; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, 4 * hf + cb, l));
+      // dW_e rows rb: sum over this half's edges of g_a1[h][e] e[e][slot] (the other half's slots are zero)
+      if constexpr (NU > 0) {
+        const f32x4 t1 = transpose_block(g1, I);
+        bf16x8 ga1N = zero_chunk<bf16>();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ga1N[4 * hf + i] = (bf16)t1[i];
+#pragma unroll
+        for (int ub = 0; ub < NU; ++ub) {
+          if (16 * ub >= FE) continue;   // column block past the edge features
+          const int slot = 16 * ub + c;
+          bf16x8 un;
+#pragma unroll
+          for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
+          mma(acc_wu[ub], ga1N, un);
+        }
+      }
+    }
+    __syncthreads();   // the next tile overwrites s_m1 = s_ga2, s_m1N and s_u
+    ri = n_ri; rj = n_rj; eid = n_eid;
+  }
+
+  // ---- this block's weight-gradient partial ---------------------------------
+  // db2 is first summed over the wave's 16 edge lanes; half 1 then leaves its
+  // partials in LDS and half 0 adds them after its own (fixed order).
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    vb2[i] += shfl_xor(vb2[i], 1); vb2[i] += shfl_xor(vb2[i], 2); vb2[i] += shfl_xor(vb2[i], 4); vb2[i] += shfl_xor(vb2[i], 8);
+  }
+  constexpr int NUR = NU > 0 ? NU : 1;
+  float* const red_v = reinterpret_cast<float*>(s_act);          // [rb][16 rows]
+  float* const red_u = red_v + NRB * 16;                          // [rb][ub][lane][4]
+  static_assert((NRB * 16 + NRB * NUR * 64 * 4) * 4 <= 3 * CH * 2, "reduction exceeds the LDS buffers");
+  if (hf == 1) {
+    if (c == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red_v[rb * 16 + 4 * g + i] = vb2[i];
+    }
+#pragma unroll
+    for (int ub = 0; ub < NUR; ++ub)
+      *reinterpret_cast<f32x4*>(red_u + ((rb * NUR + ub) * 64 + l) * 4) = acc_wu[ub];
+  }
+  __syncthreads();
+  float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
+  const int64_t oWE = (int64_t)(H + 1) * O;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * rb + 4 * g + i;
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) P[(int64_t)row * O + 64 * hf + 16 * cb + c] = acc_whl[cb][i];
+  }
+  if (hf == 0) {
+#pragma unroll
+    for (int ub = 0; ub < NU; ++ub) {
+      const f32x4 o = *reinterpret_cast<const f32x4*>(red_u + ((rb * NUR + ub) * 64 + l) * 4);
+      const int slot = 16 * ub + c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (slot < FE) P[oWE + (int64_t)(16 * rb + 4 * g + i) * FE + slot] = acc_wu[ub][i] + o[i];
+    }
+    if (c == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P[(int64_t)H * O + 16 * rb + 4 * g + i] = vb2[i] + red_v[rb * 16 + 4 * g + i];
+    }
+  }
+}
+
 template <int H, int O, int M, int W, bool EQ>
 int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (a.ntiles > 0) {
     const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * 4);
     hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ>), dim3(blocks), dim3(W * 64), 0, st, a);
+  }
+  return (int)hipGetLastError();
+}
+
+int launch_mpnn_bwd16(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.ntiles > 0) {
+    if (a.FE == 0)
+      hipLaunchKernelGGL((mpnn_bwd16_kernel<0>), dim3(nblk), dim3(1024), 0, st, a);
+    else if (a.FE <= 16)
+      hipLaunchKernelGGL((mpnn_bwd16_kernel<1>), dim3(nblk), dim3(1024), 0, st, a);
+    else
+      hipLaunchKernelGGL((mpnn_bwd16_kernel<2>), dim3(nblk), dim3(1024), 0, st, a);
   }
   return (int)hipGetLastError();
 }
@@ -830,8 +1054,7 @@ int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
 }
 
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
-  if (s.H == 128)
-    return s.eq ? launch_bwd_t<128, 128, 128, 8, true>(a, nblk, st) : launch_bwd_t<128, 128, 128, 8, false>(a, nblk, st);
+  if (s.H == 128) return s.eq ? launch_bwd_t<128, 128, 128, 8, true>(a, nblk, st) : launch_mpnn_bwd16(a, nblk, st);
   return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
 }
 
