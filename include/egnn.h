@@ -185,6 +185,13 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
  * grad_b (Nout, may be NULL) = column sums of dy; deterministic split-K sums.
  * x (N, Kin) and dy (N, Nout) row-major with row strides ldx, lddy (any
  * widths).  One dtype for all tensors (EGNN_F32 / EGNN_BF16). */
+/* Forward of the same layer: y (N, Nout, row stride ldy) = x w^T + b, with
+ * w (Nout, Kin) in nn.Linear layout and b (Nout) possibly NULL; replaces the
+ * torch.nn.Linear calls of embedding_in / embedding_out (egnn_clean.py:139,
+ * 145).  Kin, Nout, ldx and ldy are multiples of 8 (16-byte bf16 rows; the
+ * Python wrapper pads other widths with zero columns), fp32 accumulation. */
+int32_t egnn_dense_fwd(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
+                       const void* w, const void* b, void* y, int64_t ldy, void* stream);
 size_t egnn_dense_wgrad_workspace_bytes(int64_t N, int32_t Kin, int32_t Nout);
 int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
                          const void* dy, int64_t lddy, void* grad_w, void* grad_b, void* workspace,

@@ -279,7 +279,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   }
   // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
   auto splitk2 = [&](Gemm2Args g, float* dst) -> int32_t {
-    g.ksplit = splitk_len(std::max<int64_t>(g.K, 1));
+    g.ksplit = splitk_len(g.M, g.N, g.K);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
     ProfScope ps(EGNN_K_WGRAD, st);
@@ -357,7 +357,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
     g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;
     g.B = w.dPQ; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 1;
-    g.ksplit = splitk_len(s.N);
+    g.ksplit = splitk_len(g.M, g.N, g.K);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), g.ksplit);
     if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
@@ -431,8 +431,7 @@ size_t node_ws_layout(const NodeShape& s, void* base, NodeWs* w) {
   char* b = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
-  const int64_t ns = cdiv(std::max<int64_t>(s.N, 1), splitk_len(std::max<int64_t>(s.N, 1)));
-  w->part_elems = ns * std::max<int64_t>((int64_t)(s.K + 1) * s.Hn, (int64_t)(s.Hn + 1) * s.Fo);
+  w->part_elems = std::max<int64_t>(splitk_parts(s.K + 1, s.Hn, s.N), splitk_parts(s.Hn + 1, s.Fo, s.N));
   w->dz = take((size_t)s.N * s.Hn * s.esz);
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->S1 = (float*)take((size_t)(s.K + 1) * s.Hn * sizeof(float));
@@ -528,11 +527,11 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
       if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
     }
   }
-  const int64_t ksplit = splitk_len(std::max<int64_t>(s.N, 1));
-  const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
   {  // S1 = [x1 | x2 | 1]^T dz
     Gemm2Args g{};
     g.M = s.K + 1; g.N = s.Hn; g.K = s.N;
+    const int64_t ksplit = splitk_len(g.M, g.N, g.K);
+    const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
     g.A = x1; g.lda = ld1; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.K;
     if (s.K2 > 0) { g.A2 = x2; g.lda2 = ld2; g.a_split = s.K1; }
     g.B = w.dz; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 1;
@@ -544,6 +543,8 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   {  // S2 = [act | 1]^T dout
     Gemm2Args g{};
     g.M = s.Hn + 1; g.N = s.Fo; g.K = s.N;
+    const int64_t ksplit = splitk_len(g.M, g.N, g.K);
+    const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
     g.A = act; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.Hn;
     g.B = grad_out; g.ldb = ldgo; g.b_bf16 = s.bf16; g.b_nc = 1;
     g.ksplit = ksplit; g.partial = w.part;
@@ -563,8 +564,7 @@ size_t dense_ws_layout(int64_t N, int Kin, int Nout, void* base, DenseWs* w) {
   char* b = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
-  const int64_t ns = cdiv(std::max<int64_t>(N, 1), splitk_len(std::max<int64_t>(N, 1)));
-  w->part_elems = ns * (int64_t)(Kin + 1) * Nout;
+  w->part_elems = splitk_parts(Kin + 1, Nout, N);
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->S = (float*)take((size_t)(Kin + 1) * Nout * sizeof(float));
   return off;
@@ -577,6 +577,27 @@ size_t egnn_dense_wgrad_workspace_bytes(int64_t N, int32_t Kin, int32_t Nout) {
   if (N < 0 || Kin <= 0 || Nout <= 0) return 0;
   DenseWs w;
   return dense_ws_layout(N, Kin, Nout, nullptr, &w);
+}
+
+int32_t egnn_dense_fwd(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
+                       const void* w, const void* b, void* y, int64_t ldy, void* stream) {
+  if (dtype != EGNN_F32 && dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (N < 0 || Kin <= 0 || Nout <= 0 || Kin % 8 || Nout % 8) return EGNN_ERR_DIMS;
+  if (N == 0) return EGNN_OK;
+  if (!x || !w || !y) return EGNN_ERR_NULL;
+  if (ldx < Kin || ldy < Nout || ldx % 8 || ldy % 8) return EGNN_ERR_STRIDE;
+  for (const void* p : std::initializer_list<const void*>{x, w, b, y})
+    if (!aligned16(p)) return EGNN_ERR_ALIGN;
+  const bool bf16 = dtype == EGNN_BF16;
+  Gemm2Args g{};
+  g.M = N; g.N = Nout; g.K = Kin;
+  g.A = x; g.lda = ldx; g.a_bf16 = bf16; g.a_kc = 1; g.a_ones_row = -1;
+  g.B = w; g.ldb = Kin; g.b_bf16 = bf16; g.b_nc = 0;          // B[k][n] = w[n][k]
+  g.bias = b; g.bias_bf16 = bf16; g.bias_len = b ? Nout : 0;
+  g.C = y; g.ldc = ldy; g.c_bf16 = bf16;
+  hipStream_t st = (hipStream_t)stream;
+  ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  return hip_status(launch_gemm2(g, bf16, st));
 }
 
 int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
@@ -593,7 +614,7 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
   dense_ws_layout(N, Kin, Nout, workspace, &w);
   hipStream_t st = (hipStream_t)stream;
   ProfScope ps(EGNN_K_NODE_UPDATE, st);
-  const int64_t ksplit = splitk_len(std::max<int64_t>(N, 1));
+  const int64_t ksplit = splitk_len(Kin + 1, Nout, N);
   const int64_t nsplit = cdiv(std::max<int64_t>(N, 1), ksplit);
   int32_t rc;
   if (N > 0) {   // S = [x | 1]^T dy, split over the nodes

@@ -87,7 +87,13 @@ struct BwdWs {
 };
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
-int64_t splitk_len(int64_t K);
+// Split-K products [A | 1]^T B over K rows with an M x N result: rows per
+// slice (about 512 blocks of the launcher's tile, slices of 256 rows or more)
+// and the fp32 partial elements that need.  Reductions over kSplitKBig rows or
+// more use 128 x 128 tiles.
+constexpr int64_t kSplitKBig = 65536;
+int64_t splitk_len(int64_t M, int64_t N, int64_t K);
+int64_t splitk_parts(int64_t M, int64_t N, int64_t K);
 
 // ---- launchers (return hipError_t as int) --------------------------------
 int launch_schedule(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E, const SchedView& v,

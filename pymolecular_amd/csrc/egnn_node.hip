@@ -64,9 +64,16 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
   return off;
 }
 
-int64_t splitk_len(int64_t K) {
-  int64_t ks = std::max<int64_t>(256, cdiv(K, 256));
-  return cdiv(ks, 32) * 32;
+int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
+  K = std::max<int64_t>(K, 1);
+  const bool big = K >= kSplitKBig;   // the tile launch_gemm2 picks for this product
+  const int64_t tiles = big ? cdiv(M, 128) * cdiv(N, 128) : cdiv(M, 32) * cdiv(N, 64);
+  const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(512, std::max<int64_t>(tiles, 1)), cdiv(K, 256)));
+  return cdiv(cdiv(K, splits), 64) * 64;
+}
+
+int64_t splitk_parts(int64_t M, int64_t N, int64_t K) {
+  return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K)) * M * N;
 }
 
 int64_t wgrad_ksplit(int64_t K) {
@@ -98,10 +105,11 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->dwsum = coop ? (float*)take((size_t)w->LW * sizeof(float)) : nullptr;
   w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
-  int64_t se = cdiv(std::max<int64_t>(s.E, 1), splitk_len(s.E)), sn = cdiv(s.N, splitk_len(s.N));
-  int64_t pe = coop ? 0 : std::max<int64_t>({(int64_t)(s.H + 1) * s.O, (int64_t)(s.O + 1) * s.M, (int64_t)s.M,
-                                             (int64_t)s.H * std::max(s.FE, 1), (int64_t)s.H});
-  w->part_elems = std::max<int64_t>(se * pe, sn * (int64_t)(s.F + 1) * 2 * s.H);
+  w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N);
+  if (!coop)
+    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, s.E), splitk_parts(s.O + 1, s.M, s.E),
+                                       splitk_parts(s.M, 1, s.E), splitk_parts(s.H, 1, s.E),
+                                       splitk_parts(s.H, std::max(s.FE, 1), s.E)});
   if (wide) {
     const int64_t ks = wgrad_ksplit(s.E);
     const int64_t nw = cdiv(std::max<int64_t>(s.E, 1), ks);
@@ -706,10 +714,10 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
                                  : al(g.C, g.ldc) && al(g.Cpre, g.ldpre) && al(g.resid, g.ldr) && al(g.zd, g.ldz));
   if (compute_bf16 && g.a_bf16 && g.b_bf16 && (g.c_bf16 || g.partial) && rows16) {
     // 128-row tiles when they fill the device twice over, else 64-row tiles
-    // 128 x 128 tiles for long split-K reductions and for grids of 2048 or more
-    // such tiles; else 32 x 64 tiles, whose larger grids hide the memory latency
-    // of the short K loops of the node products
-    const bool big = (g.ksplit > 0 && g.ksplit >= 2048) || cdiv(g.M, 128) * cdiv(g.N, 128) * (int64_t)gz >= 2048;
+    // 128 x 128 tiles for split-K reductions over kSplitKBig rows or more and for
+    // grids of 2048 or more such tiles; else 32 x 64 tiles, whose larger grids
+    // hide the memory latency of the short K loops of the node products
+    const bool big = g.ksplit > 0 ? g.K >= kSplitKBig : cdiv(g.M, 128) * cdiv(g.N, 128) >= 2048;
     const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, big ? 128 : 64), gz);
 #define GB_LAUNCH(AK, BNC)                                                                         \
     do {                                                                                           \

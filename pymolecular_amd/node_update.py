@@ -121,47 +121,71 @@ def node_update(x1: torch.Tensor, x2: Optional[torch.Tensor], lin1: torch.nn.Lin
     return NodeUpdateFn.apply(x1, x2, lin1.weight, lin1.bias, lin2.weight, lin2.bias, residual)
 
 
+def _pad_to8(t: torch.Tensor, dim: int) -> torch.Tensor:
+    """``t`` with zeros appended along ``dim`` up to a multiple of 8 (16-byte bf16 rows)."""
+    n = t.shape[dim]
+    if n % 8 == 0:
+        return t
+    pad = [0, 0] * (t.dim() - 1 - (dim % t.dim())) + [0, 8 - n % 8]
+    return torch.nn.functional.pad(t, pad)
+
+
 class DenseFn(torch.autograd.Function):
-    """``y = DenseFn.apply(x, weight, bias)``: torch.nn.functional.linear whose
-    weight gradient over the N rows is the library's deterministic split-K
-    product (``egnn_dense_wgrad``); the stack's embedding layers use it
-    (egnn_clean.py:127-128, 139-145), where N is far larger than the weight."""
+    """``y = DenseFn.apply(x, weight, bias)``: torch.nn.functional.linear on the
+    library's GEMM (``egnn_dense_fwd``), with the weight gradient over the N
+    rows as its deterministic split-K product (``egnn_dense_wgrad``); the
+    stack's embedding layers use it (egnn_clean.py:127-128, 139-145).  Input and
+    output widths that are not multiples of 8 are padded with zero columns."""
 
     @staticmethod
     def forward(ctx, x, weight, bias):
         if not x.is_cuda:
             raise RuntimeError("x must be a ROCm device tensor")
-        w = weight.to(x.dtype)
-        b = None if bias is None else bias.to(x.dtype)
-        ctx.save_for_backward(x, w)
-        ctx.has_b = bias is not None
-        ctx.wdt = (weight.dtype, None if bias is None else bias.dtype)
-        return torch.nn.functional.linear(x, w, b)
-
-    @staticmethod
-    def backward(ctx, gy):
-        x, w = ctx.saved_tensors
         dt = x.dtype
         if dt not in (torch.float32, torch.bfloat16):
             raise TypeError(f"unsupported dtype {dt}")
-        x2 = x.reshape(-1, x.shape[-1])
-        x2 = x2 if x2.stride(-1) == 1 else x2.contiguous()
-        gy2 = gy.to(dt).reshape(-1, gy.shape[-1])
-        gy2 = gy2 if gy2.stride(-1) == 1 else gy2.contiguous()
-        N, Kin = x2.shape
-        Nout = gy2.shape[1]
-        gx = (gy2 @ w).reshape(x.shape) if ctx.needs_input_grad[0] else None
-        gw = torch.empty((Nout, Kin), dtype=dt, device=x.device)
-        gb = torch.empty((Nout,), dtype=dt, device=x.device) if ctx.has_b else None
-        L = _capi.lib()
-        nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kin, Nout)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=x.device)
+        Nout, Kin = weight.shape
+        lead = x.shape[:-1]
+        xp = _rowmajor(_pad_to8(x.reshape(-1, Kin), 1))
+        wp = _pad_to8(_pad_to8(weight.to(dt), 1), 0).contiguous()
+        bp = None if bias is None else _pad_to8(bias.to(dt), 0).contiguous()
+        N, Kp = xp.shape
+        Np = wp.shape[0]
+        y = torch.empty((N, Np), dtype=dt, device=x.device)
         code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
-        rc = L.egnn_dense_wgrad(code, N, Kin, Nout, x2.data_ptr() if N else None, x2.stride(0),
-                                gy2.data_ptr() if N else None, gy2.stride(0), gw.data_ptr(), _ptr(gb), ws.data_ptr(),
-                                nbytes, torch.cuda.current_stream(x.device).cuda_stream)
+        st = torch.cuda.current_stream(x.device).cuda_stream
+        rc = _capi.lib().egnn_dense_fwd(code, N, Kp, Np, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
+                                        wp.data_ptr(), _ptr(bp), y.data_ptr() if N else None, Np, st)
+        check("egnn_dense_fwd", rc)
+        ctx.save_for_backward(xp, wp)
+        ctx.dims = (Kin, Nout, lead)
+        ctx.has_b = bias is not None
+        ctx.wdt = (weight.dtype, None if bias is None else bias.dtype)
+        return (y if Np == Nout else y[:, :Nout]).reshape(*lead, Nout)
+
+    @staticmethod
+    def backward(ctx, gy):
+        xp, wp = ctx.saved_tensors
+        Kin, Nout, lead = ctx.dims
+        dt = xp.dtype
+        N, Kp = xp.shape
+        Np = wp.shape[0]
+        gy2 = _rowmajor(_pad_to8(gy.to(dt).reshape(-1, Nout), 1))
+        gx = None
+        if ctx.needs_input_grad[0]:
+            gx = (gy2 @ wp)[:, :Kin].reshape(*lead, Kin)
+        gw = torch.empty((Np, Kp), dtype=dt, device=xp.device)
+        gb = torch.empty((Np,), dtype=dt, device=xp.device) if ctx.has_b else None
+        L = _capi.lib()
+        nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kp, Np)
+        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=xp.device)
+        code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
+        rc = L.egnn_dense_wgrad(code, N, Kp, Np, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
+                                gy2.data_ptr() if N else None, gy2.stride(0) if N else Np, gw.data_ptr(), _ptr(gb),
+                                ws.data_ptr(), nbytes, torch.cuda.current_stream(xp.device).cuda_stream)
         check("egnn_dense_wgrad", rc)
-        return gx, gw.to(ctx.wdt[0]), None if gb is None else gb.to(ctx.wdt[1])
+        gw = gw[:Nout, :Kin].to(ctx.wdt[0])
+        return gx, gw, None if gb is None else gb[:Nout].to(ctx.wdt[1])
 
 
 def dense(x: torch.Tensor, lin: torch.nn.Linear) -> torch.Tensor:

@@ -77,7 +77,8 @@ def test_node_update_deterministic_and_empty():
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
-@pytest.mark.parametrize("N,K,Nout,bias", [(19363, 5, 128, True), (3000, 128, 128, False), (0, 16, 24, True)])
+@pytest.mark.parametrize("N,K,Nout,bias", [(19363, 5, 128, True), (3000, 128, 128, False), (500, 20, 36, True),
+                                         (0, 16, 24, True)])
 def test_dense_weight_gradient(dtype, tol, N, K, Nout, bias):
     from pymolecular_amd.node_update import DenseFn
     r = np.random.Generator(np.random.PCG64(N + K))
