@@ -227,6 +227,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
   a.fr = w.fr;
+  a.w2 = w2_msg; a.w1m = w1_mov;
   a.gmsg = grad_out_msg; a.sgm = strides->msg;
   a.gmov = grad_out_mov; a.sgx = strides->mov;
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;

@@ -777,6 +777,362 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// backward of the equivariant layer, H = O = M = 128, 8 waves per tile
+// ---------------------------------------------------------------------------
+// The stages of coop_bwd_kernel with two changes.  W_hl and W1_mov are held in
+// LDS once each, row-major: the A operands of W_hl m1-type products (rows of
+// W^T) come from transposing LDS reads, those of W products from plain 8-byte
+// reads, so no transposed copy and no weight registers are needed.  The
+// registers this frees carry the next tile's P_i / Q_j gathers, issued in the
+// middle of the current tile so that they have arrived when its S1 starts.
+template <int NU>
+__global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
+  constexpr int H = 128, O = 128, M = 128, W = 8;
+  constexpr int KH = H / 32, KO = O / 32, KM = M / 32;
+  constexpr int NO = O / 16, NM = M / 16;
+  constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
+  constexpr int WP = 136;                           // row pitch of the LDS weight matrices (bf16, 272 bytes)
+  constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 edge blocks (8 KB)
+  // buffers whose live ranges do not overlap share storage:
+  //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5)
+  __shared__ __attribute__((aligned(16))) bf16 s_buf1[CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_buf2[CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_gq[CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_gqN[NM * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_Whl[H * WP];    // W_hl[h][o]
+  __shared__ __attribute__((aligned(16))) bf16 s_Wmov[O * WP];   // W1_mov[o][m]
+  bf16* const s_m1 = s_buf1;
+  bf16* const s_ga2 = s_buf1;
+  bf16* const s_m = s_buf2;
+  bf16* const s_ga2N = s_buf2;
+  __shared__ float s_phi[W][TE];
+  __shared__ float s_gr[W][TE];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];   // [edge][slot] edge features of the tile
+  __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
+  float* const s_b2 = s_vec;
+  float* const s_bx1 = s_vec + O;
+  float* const s_w2m = s_vec + O + M;
+  float* const s_wd = s_vec + O + 2 * M;
+
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
+  const bf16* ef = (const bf16*)a.ef;
+  const bf16* gmsg = (const bf16*)a.gmsg;
+  bf16* Gh = (bf16*)a.Gh;
+  const int64_t E = a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+
+  for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
+  for (int q = threadIdx.x; q < M; q += W * 64) {
+    s_bx1[q] = a.fr.bx1f[q];
+    s_w2m[q] = a.fr.w2mf[q];
+  }
+  for (int q = threadIdx.x; q < H; q += W * 64) s_wd[q] = a.fr.wdf[q];
+  for (int q = threadIdx.x; q < H * O / 8; q += W * 64) {   // 16-byte row pieces of both matrices
+    const int r = q / (O / 8), p = q % (O / 8);
+    *reinterpret_cast<bf16x8*>(s_Whl + r * WP + 8 * p) = load_chunk((const bf16*)a.w2 + (int64_t)r * O + 8 * p);
+    *reinterpret_cast<bf16x8*>(s_Wmov + r * WP + 8 * p) = load_chunk((const bf16*)a.w1m + (int64_t)r * M + 8 * p);
+  }
+  // A operand of the product with W (rows r = 16 blk + c, K slice kc): W[r][32 kc + kappa_chain(g, s)]
+  auto a_rows = [&](const bf16* Wl, int blk, int kc) -> bf16x8 {
+    const bf16* p = Wl + (16 * blk + c) * WP + 32 * kc + 4 * g;
+    return __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16),
+                                   0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  // A operand of the product with W^T (rows r = 16 blk + c of W^T): W[32 kc + kappa_chain(g, s)][r]
+  auto a_cols = [&](const bf16* Wl, int blk, int kc) -> bf16x8 {
+    const int kb = 32 * kc + 4 * g;
+    const bf16* p0 = Wl + (kb + (c >> 2)) * WP + 16 * blk + 4 * (c & 3);
+    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
+    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p0 + 16 * WP));
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+  };
+  const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)w * kFragElems + l * 8);
+  const bf16x8 I = ident_chunk(c, g);
+
+  f32x4 acc_whl[NO], acc_w1m[NM], acc_wu[NU > 0 ? NU : 1];
+#pragma unroll
+  for (int cb = 0; cb < NO; ++cb) acc_whl[cb] = zero4();
+#pragma unroll
+  for (int cb = 0; cb < NM; ++cb) acc_w1m[cb] = zero4();
+#pragma unroll
+  for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
+  f32x4 vb2 = zero4(), vbx1 = zero4(), vw2m = zero4(), vwd = zero4();
+
+  // indices and geometry of a tile, loaded one tile ahead of their use
+  int ri[2], rj[2], eid[2];
+  float r2[2], gphi[2];
+  auto load_tile = [&](int64_t t, int* pri, int* prj, int* peid, float* pr2, float* pgp) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int64_t e = t * TE + nb * 16 + c;
+      const bool ok = e < E;
+      const int64_t ec = ok ? e : E - 1;
+      pri[nb] = clampi(a.erow[ec], N);
+      prj[nb] = clampi(a.col[ec], N);
+      peid[nb] = (a.eids && FE > 0) ? clampi(a.eids[ec], (int)E) : (int)ec;
+      // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
+      const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
+      pr2[nb] = q.x;
+      pgp[nb] = ok ? q.y : 0.f;
+    }
+  };
+  // P_i and Q_j of the wave's 16 rows, two edge blocks
+  const int poff = 32 * (w >> 1) + 8 * g + 4 * (w & 1);
+  bf16x4 pv[2], qv[2];
+  auto load_pq = [&](const int* pri, const int* prj) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      pv[nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)pri[nb] * (4u * H) + 2u * poff));
+      qv[nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)prj[nb] * (4u * H) + 2u * (H + poff)));
+    }
+  };
+  if (blockIdx.x < a.ntiles) {
+    load_tile(blockIdx.x, ri, rj, eid, r2, gphi);
+    load_pq(ri, rj);
+  }
+  __syncthreads();   // weights and vectors in LDS
+
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+    const int64_t base = t * TE;
+    bool valid[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
+    // rows of the incoming message gradient (used in S4), then the next tile's indices
+    bf16x4 gmr[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri[nb] * a.sgm + 16 * w + 4 * g);
+    int n_ri[2], n_rj[2], n_eid[2];
+    float n_r2[2], n_gphi[2];
+    const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
+    load_tile(tn, n_ri, n_rj, n_eid, n_r2, n_gphi);
+
+    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
+    bf16x8 u[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], FE, g, r2[nb], true);
+    // the tile's edge features, [edge][slot], for the dW_e product (zero rows past the end)
+    if (NU > 0 && w == 0 && 8 * g < FE) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        *reinterpret_cast<bf16x8*>(s_u + (nb * 16 + c) * FEP + 8 * g) = valid[nb] ? u[nb] : zero_chunk<bf16>();
+    }
+    bf16x4 s1[2];
+    bf16x8 m1N;
+    {
+      f32x4 y[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 acc = zero4();
+        mma(acc, wu, u[nb]);
+        const f32x4 p = unpack4(pv[nb]);
+        const f32x4 q = unpack4(qv[nb]);
+        f32x4 d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+          y[nb][i] = r.y;
+          d[i] = r.d;
+        }
+        s1[nb] = pack4(d);
+        put_chain(s_m1, w, nb, l, y[nb]);
+      }
+      m1N = edge_major(y[0], y[1], I);
+    }
+    __syncthreads();
+
+    // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
+    bf16x4 s2[2];
+    bf16x8 mN;
+    {
+      f32x4 y[2], acc[2];
+      acc[0] = acc[1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * w + 4 * g);
+#pragma unroll
+      for (int kc = 0; kc < KH; ++kc) {
+        const bf16x8 A = a_cols(s_Whl, w, kc);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        f32x4 d;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const YD r = silu_yd<bf16>(acc[nb][i]);
+          y[nb][i] = r.y;
+          d[i] = r.d;
+        }
+        s2[nb] = pack4(d);
+        put_chain(s_m, w, nb, l, y[nb]);
+      }
+      mN = edge_major(y[0], y[1], I);
+    }
+    __syncthreads();
+
+    // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows ----
+    float phi[2] = {0.f, 0.f};
+    {
+      const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * w + 4 * g);
+      f32x4 gq[2], accq[2];
+      accq[0] = accq[1] = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * w + 4 * g);
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc) {
+        const bf16x8 A = a_cols(s_Wmov, w, kc);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) mma(accq[nb], A, get_chain(s_m, kc, nb, l));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const YD r = silu_yd<bf16>(accq[nb][i]);
+          phi[nb] += r.y * w2mv[i];
+          gq[nb][i] = gphi[nb] * w2mv[i] * r.d;
+          vw2m[i] += r.y * gphi[nb];
+          vbx1[i] += gq[nb][i];
+        }
+        put_chain(s_gq, w, nb, l, gq[nb]);
+      }
+      put_norm(s_gqN, w, l, edge_major(gq[0], gq[1], I));
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        phi[nb] += shfl_xor(phi[nb], 16);
+        phi[nb] += shfl_xor(phi[nb], 32);
+        if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
+      }
+    }
+    __syncthreads();
+    load_pq(n_ri, n_rj);   // the next tile's gathers, consumed by its S1
+
+    // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
+    {
+      f32x4 ga[2], acca[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acca[nb] = valid[nb] ? unpack4(gmr[nb]) : zero4();
+#pragma unroll
+      for (int kc = 0; kc < KM; ++kc) {
+        const bf16x8 A = a_rows(s_Wmov, w, kc);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) mma(acca[nb], A, get_chain(s_gq, kc, nb, l));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const f32x4 d = unpack4(s2[nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ga[nb][i] = acca[nb][i] * d[i];
+          vb2[i] += ga[nb][i];
+        }
+        put_chain(s_ga2, w, nb, l, ga[nb]);
+      }
+      put_norm(s_ga2N, w, l, edge_major(ga[0], ga[1], I));
+    }
+    // dW1_mov rows of this wave: sum_e m[o][e] g_q[m][e]
+#pragma unroll
+    for (int cb = 0; cb < NM; ++cb) mma(acc_w1m[cb], mN, get_norm(s_gqN, cb, l));
+    __syncthreads();
+
+    // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1), the wave's H rows --------------
+    float gr[2] = {0.f, 0.f};
+    {
+      const f32x4 wdv = *reinterpret_cast<const f32x4*>(s_wd + 16 * w + 4 * g);
+      f32x4 g1[2], acch[2] = {zero4(), zero4()};
+#pragma unroll
+      for (int kc = 0; kc < KO; ++kc) {
+        const bf16x8 A = a_rows(s_Whl, w, kc);
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) mma(acch[nb], A, get_chain(s_ga2, kc, nb, l));
+      }
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const f32x4 d = unpack4(s1[nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          g1[nb][i] = acch[nb][i] * d[i];
+          gr[nb] += wdv[i] * g1[nb][i];
+          vwd[i] += g1[nb][i] * r2[nb];
+        }
+        if (valid[nb])
+          *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * w + 4 * g) = pack4(g1[nb]);
+      }
+      const bf16x8 ga1N = edge_major(g1[0], g1[1], I);
+      // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e]
+#pragma unroll
+      for (int cb = 0; cb < NO; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, cb, l));
+      // dW_e rows of this wave: sum_e g_a1[h][e] e[e][slot] (the r^2 column is accumulated above)
+#pragma unroll
+      for (int ub = 0; ub < NU; ++ub) {
+        if (16 * ub >= FE) continue;   // column block past the edge features
+        const int slot = 16 * ub + c;
+        bf16x8 un;
+#pragma unroll
+        for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
+        mma(acc_wu[ub], ga1N, un);
+      }
+    }
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      gr[nb] += shfl_xor(gr[nb], 16);
+      gr[nb] += shfl_xor(gr[nb], 32);
+      if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
+    }
+    __syncthreads();
+    // ---- S6: dL/ddelta = phi gx + 2 g_r delta -------------------------------
+    if (w == 0 && l < TE && base + l < E) {
+      float grt = 0.f, pht = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) {
+        grt += s_gr[ww][l];
+        pht += s_phi[ww][l];
+      }
+      const float k2 = 2.0f * grt;
+      const float* q = a.geo + (base + l) * 8;   // delta at 2..4, grad x_i at 5..7
+      *reinterpret_cast<f32x4*>(a.Gx + (base + l) * 4) =
+          f32x4{pht * q[5] + k2 * q[2], pht * q[6] + k2 * q[3], pht * q[7] + k2 * q[4], 0.f};
+    }
+    // Every buffer the next tile writes before its first barrier (s_m1 = s_ga2,
+    // s_u) was last read before this tile's g_r barrier: no closing barrier.
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      ri[nb] = n_ri[nb]; rj[nb] = n_rj[nb]; eid[nb] = n_eid[nb]; r2[nb] = n_r2[nb]; gphi[nb] = n_gphi[nb];
+    }
+  }
+
+  // ---- this block's weight-gradient partial ---------------------------------
+  float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
+  const int64_t oW1 = (int64_t)(H + 1) * O;
+  const int64_t oW2 = oW1 + (int64_t)(O + 1) * M;
+  const int64_t oWE = oW2 + M;
+  const int64_t oWD = oWE + (int64_t)H * FE;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = 16 * w + 4 * g + i;
+#pragma unroll
+    for (int cb = 0; cb < NO; ++cb) P[(int64_t)row * O + 16 * cb + c] = acc_whl[cb][i];
+#pragma unroll
+    for (int cb = 0; cb < NM; ++cb) P[oW1 + (int64_t)row * M + 16 * cb + c] = acc_w1m[cb][i];
+#pragma unroll
+    for (int ub = 0; ub < NU; ++ub) {
+      const int slot = 16 * ub + c;
+      if (slot < FE) P[oWE + (int64_t)row * FE + slot] = acc_wu[ub][i];
+    }
+    float b = vb2[i], x = vbx1[i], q = vw2m[i], d = vwd[i];
+    b += shfl_xor(b, 1); b += shfl_xor(b, 2); b += shfl_xor(b, 4); b += shfl_xor(b, 8);
+    x += shfl_xor(x, 1); x += shfl_xor(x, 2); x += shfl_xor(x, 4); x += shfl_xor(x, 8);
+    q += shfl_xor(q, 1); q += shfl_xor(q, 2); q += shfl_xor(q, 4); q += shfl_xor(q, 8);
+    d += shfl_xor(d, 1); d += shfl_xor(d, 2); d += shfl_xor(d, 4); d += shfl_xor(d, 8);
+    if (c == 0) {
+      P[(int64_t)H * O + row] = b;
+      P[oW1 + (int64_t)O * M + row] = x;
+      P[oW2 + row] = q;
+      P[oWD + row] = d;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // backward of the non-equivariant layer (MPNN), H = O = 128, 16 waves per tile
 // ---------------------------------------------------------------------------
 // Wave w owns feature rows [16 rb, 16 rb + 16), rb = w & 7, of every stage for
@@ -997,6 +1353,18 @@ int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+int launch_bwd_eq(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.ntiles > 0) {
+    if (a.FE == 0)
+      hipLaunchKernelGGL((coop_bwd_eq_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
+    else if (a.FE <= 16)
+      hipLaunchKernelGGL((coop_bwd_eq_kernel<1>), dim3(nblk), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((coop_bwd_eq_kernel<2>), dim3(nblk), dim3(512), 0, st, a);
+  }
+  return (int)hipGetLastError();
+}
+
 int launch_mpnn_bwd16(const BwdArgs& a, int nblk, hipStream_t st) {
   if (a.ntiles > 0) {
     if (a.FE == 0)
@@ -1054,7 +1422,7 @@ int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
 }
 
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
-  if (s.H == 128) return s.eq ? launch_bwd_t<128, 128, 128, 8, true>(a, nblk, st) : launch_mpnn_bwd16(a, nblk, st);
+  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16(a, nblk, st);
   return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
 }
 

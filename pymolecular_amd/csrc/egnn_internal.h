@@ -174,6 +174,8 @@ struct BwdArgs {
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
   int64_t ldE;     // wide kernels: row pitch of the feature-major factors Dm1 ... Dp
+  const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype
+  const void* w1m;
 };
 int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 
