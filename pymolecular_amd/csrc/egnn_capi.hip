@@ -161,6 +161,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
   a.fr = w.fr;
+  a.w1m = w1_mov;
   a.out_msg = out_msg; a.smsg = strides->msg;
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;

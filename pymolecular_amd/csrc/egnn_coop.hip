@@ -91,7 +91,16 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   const int N = (int)a.N;
   const bool use_eids = a.eids != nullptr && a.FE > 0;
 
-  bf16x8 wu[BH], whlT[BO][KH], wmovT[EQ ? BM : 1][KO];
+  bf16x8 wu[BH], whlT[BO][KH];
+  // W1_mov[o][m] row-major in LDS; the A operands of q = W1_mov^T m are transposing reads
+  constexpr int WPM = M + 8;
+  __shared__ __attribute__((aligned(16))) bf16 s_Wmov[EQ ? O * WPM : 8];
+  if constexpr (EQ) {
+    for (int q = threadIdx.x; q < O * M / 8; q += W * 64) {
+      const int r = q / (M / 8), p = q % (M / 8);
+      *reinterpret_cast<bf16x8*>(s_Wmov + r * WPM + 8 * p) = load_chunk((const bf16*)a.w1m + (int64_t)r * M + 8 * p);
+    }
+  }
   // per-row vectors b2 (O), bx1 (M), w2_mov (M), read from LDS where they are used
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M];
   float* const s_b2 = s_vec;
@@ -113,14 +122,6 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     for (int kc = 0; kc < KH; ++kc)
       whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)(w * BO + j) * KH + kc) * kFragElems + l * 8);
   }
-  if constexpr (EQ) {
-#pragma unroll
-    for (int j = 0; j < BM; ++j) {
-#pragma unroll
-      for (int kc = 0; kc < KO; ++kc)
-        wmovT[j][kc] = load_chunk((const bf16*)a.fr.movT + ((int64_t)(w * BM + j) * KO + kc) * kFragElems + l * 8);
-    }
-  }
   const bf16x8 I = ident_chunk(c, g);
   const bf16x8 Ipq = pair_sum_chunk(c, g);
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
@@ -141,7 +142,31 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     const int64_t ee = l == 0 ? base - 1 : base + TE;
     pex = a.erow[ee < 0 ? 0 : (ee < E ? ee : E - 1)];
   };
-  if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, er, co, eid, ex);
+  // the tile's P_i / Q_j gathers, r^2 and edge-feature chunks, loaded in the
+  // middle of the previous tile from its (then current) indices
+  bf16x4 pv[BH][2], qv[BH][2];
+  float r2[2];
+  bf16x8 uf[2];
+  auto load_data = [&](int64_t t, const int* per, const int* pco, const int* peid) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const uint32_t i = (uint32_t)clampi(per[nb], N), j = (uint32_t)clampi(pco[nb], N);
+#pragma unroll
+      for (int jb = 0; jb < BH; ++jb) {
+        const int hb = w * BH + jb;
+        const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+        pv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (i * (4u * H) + 2u * poff));
+        qv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (j * (4u * H) + 2u * (H + poff)));
+      }
+      const int64_t e = t * TE + nb * 16 + c;
+      r2[nb] = EQ ? a.geo[(e < E ? e : E - 1) * 4 + 3] : 0.f;
+      uf[nb] = 8 * g + 8 <= a.FE ? load_chunk(ef + (int64_t)clampi(peid[nb], (int)E) * a.se + 8 * g) : zero_chunk<bf16>();
+    }
+  };
+  if (blockIdx.x < a.ntiles) {
+    load_tile(blockIdx.x, er, co, eid, ex);
+    load_data(blockIdx.x, er, co, eid);
+  }
 
   int par = 0;
   for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x, par ^= 1) {
@@ -155,27 +180,17 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       rj[nb] = clampi(co[nb], N);
       valid[nb] = nb * 16 + c < nvalid;
     }
-    // this tile's gathers and geometry
-    bf16x4 pv[BH][2], qv[BH][2];
-#pragma unroll
-    for (int j = 0; j < BH; ++j) {
-      const int hb = w * BH + j;
-      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        pv[j][nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)ri[nb] * (4u * H) + 2u * poff));
-        qv[j][nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)rj[nb] * (4u * H) + 2u * (H + poff)));
-      }
-    }
-    float r2[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      r2[nb] = EQ ? a.geo[(e < E ? e : E - 1) * 4 + 3] : 0.f;
-    }
+    // the input chunk [e | r^2 hi, lo] of the tile's edges
     bf16x8 u[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], a.FE, g, r2[nb], EQ);
+    for (int nb = 0; nb < 2; ++nb) {
+      u[nb] = uf[nb];
+      if (EQ && 8 * g == a.FE) {
+        const bf16 hi = (bf16)r2[nb];
+        u[nb][0] = hi;
+        u[nb][1] = (bf16)(r2[nb] - (float)hi);
+      }
+    }
     f32x4 dgeo = zero4();   // delta of edge l, for the coordinate sums (last wave)
     if (EQ && w == W - 1) {
       const int64_t e = base + l;
@@ -197,10 +212,8 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     const bool end_in = base + TE >= E || __builtin_amdgcn_readlane(ex, 1) != __builtin_amdgcn_readlane(er[1], 15);
     // the next tile's indices (consumed by the next iteration), issued after
     // this tile's loads so that waiting for those does not wait for these
-    {
-      const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
-      load_tile(tn, er, co, eid, ex);
-    }
+    const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
+    load_tile(tn, er, co, eid, ex);
 
     // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
 #pragma unroll
@@ -273,6 +286,8 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         }
       }
     }
+    // the next tile's gathers (P_i, Q_j, r^2, edge features), consumed by its S1
+    load_data(tn, er, co, eid);
     if constexpr (EQ) {
       __syncthreads();
       // ---- S3: phi = SiLU(W1mov^T m + bx1) . w2mov (partial over the wave's M rows)
@@ -286,7 +301,13 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         for (int nb = 0; nb < 2; ++nb) {
           f32x4 acc = bx1v;
 #pragma unroll
-          for (int kc = 0; kc < KO; ++kc) mma(acc, wmovT[j][kc], get_chain(s_m, kc, nb, l));
+          for (int kc = 0; kc < KO; ++kc) {   // A[m][o] = W1_mov[o][m], o = 32 kc + kappa_chain(g, s)
+            const bf16* p0 = s_Wmov + (32 * kc + 4 * g + (c >> 2)) * WPM + 16 * mb + 4 * (c & 3);
+            const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
+            const bf16x4 hi =
+                __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p0 + 16 * WPM));
+            mma(acc, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), get_chain(s_m, kc, nb, l));
+          }
 #pragma unroll
           for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[i]) * w2mv[i];
         }

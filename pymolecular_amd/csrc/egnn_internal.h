@@ -155,6 +155,7 @@ struct FwdArgs {
   float* out_mov; int64_t smov;
   float* carry;
   const int32_t* fix_rows; const int32_t* n_fix;
+  const void* w1m;   // W1_mov (O x M), row-major, activation dtype
 };
 // part 0: edge tiles, part 1: split/empty-row fix-up
 int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
