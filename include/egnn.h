@@ -68,7 +68,15 @@ typedef struct EgnnDims {
   int32_t equivariant; /* 1 = EGNN (r2 input, phi_x, coordinate output), 0 = MPNN */
   int32_t mean_agg;    /* 1: out_mov divided by max(in-degree, 1) (egnn_clean.py:11,78) */
   int32_t dtype;       /* EGNN_F32 or EGNN_BF16 */
+  int32_t weight_layout; /* EGNN_WEIGHTS_PACKED: w1_msg (2F+g+F_E, H), w2_msg (H, O), w1_mov (O, M), the
+                            (in, out) layout of layer.py:24-28; EGNN_WEIGHTS_LINEAR: the same matrices
+                            transposed, as torch.nn.Linear stores them (egnn_clean.py:24-40): w1_msg
+                            (H, 2F+g+F_E), w2_msg (O, H), w1_mov (M, O).  Weight gradients are written
+                            in the same layout. */
 } EgnnDims;
+
+#define EGNN_WEIGHTS_PACKED 0
+#define EGNN_WEIGHTS_LINEAR 1
 
 /* Row strides in elements; the inner dimension is always contiguous. */
 typedef struct EgnnStrides {

@@ -30,10 +30,13 @@ K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP
 K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep", "node_update")
 
 
+WEIGHTS_PACKED, WEIGHTS_LINEAR = 0, 1   # include/egnn.h EGNN_WEIGHTS_*
+
+
 class EgnnDims(ctypes.Structure):
     _fields_ = [("N", c_int64), ("E", c_int64), ("F", c_int32), ("FE", c_int32), ("H", c_int32),
                 ("O", c_int32), ("M", c_int32), ("equivariant", c_int32), ("mean_agg", c_int32),
-                ("dtype", c_int32)]
+                ("dtype", c_int32), ("weight_layout", c_int32)]
 
 
 class EgnnStrides(ctypes.Structure):

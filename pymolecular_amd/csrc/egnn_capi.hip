@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 2;
+constexpr int32_t kAbiVersion = 3;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -161,7 +161,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
   a.fr = w.fr;
-  a.w1m = w1_mov;
+  a.w1m = w1_mov; a.lin = s.lin;
   a.out_msg = out_msg; a.smsg = strides->msg;
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;
@@ -228,7 +228,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.ef = edge_feat; a.se = strides->edge;
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
   a.fr = w.fr;
-  a.w2 = w2_msg; a.w1m = w1_mov;
+  a.w2 = w2_msg; a.w1m = w1_mov; a.lin = s.lin;
   a.gmsg = grad_out_msg; a.sgm = strides->msg;
   a.gmov = grad_out_mov; a.sgx = strides->mov;
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
@@ -377,7 +377,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     f.dwd = f.dWe + (int64_t)s.H * s.FE;
   }
   f.gw1 = grad_w1_msg; f.gw2 = grad_w2_msg; f.gw1m = grad_w1_mov; f.gw2m = grad_w2_mov;
-  f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1;
+  f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1; f.lin = s.lin;
   ProfScope ps(EGNN_K_WGRAD, st);
   return hip_status(launch_finalize(s, f, st));
 }

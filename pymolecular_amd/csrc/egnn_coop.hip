@@ -95,11 +95,9 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   // W1_mov[o][m] row-major in LDS; the A operands of q = W1_mov^T m are transposing reads
   constexpr int WPM = M + 8;
   __shared__ __attribute__((aligned(16))) bf16 s_Wmov[EQ ? O * WPM : 8];
-  if constexpr (EQ) {
-    for (int q = threadIdx.x; q < O * M / 8; q += W * 64) {
-      const int r = q / (M / 8), p = q % (M / 8);
-      *reinterpret_cast<bf16x8*>(s_Wmov + r * WPM + 8 * p) = load_chunk((const bf16*)a.w1m + (int64_t)r * M + 8 * p);
-    }
+  if constexpr (EQ) {   // W1_mov given as [o][m] (packed) or [m][o] (nn.Linear)
+    if (a.lin) fill_weight_lds_t<O, M, WPM, W * 64>(s_Wmov, (const bf16*)a.w1m);
+    else fill_weight_lds<O, M, WPM, W * 64>(s_Wmov, (const bf16*)a.w1m);
   }
   // per-row vectors b2 (O), bx1 (M), w2_mov (M), read from LDS where they are used
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M];
@@ -301,13 +299,8 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         for (int nb = 0; nb < 2; ++nb) {
           f32x4 acc = bx1v;
 #pragma unroll
-          for (int kc = 0; kc < KO; ++kc) {   // A[m][o] = W1_mov[o][m], o = 32 kc + kappa_chain(g, s)
-            const bf16* p0 = s_Wmov + (32 * kc + 4 * g + (c >> 2)) * WPM + 16 * mb + 4 * (c & 3);
-            const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
-            const bf16x4 hi =
-                __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p0 + 16 * WPM));
-            mma(acc, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7), get_chain(s_m, kc, nb, l));
-          }
+          for (int kc = 0; kc < KO; ++kc)   // A[m][o] = W1_mov[o][m], o = 32 kc + kappa_chain(g, s)
+            mma(acc, lds_cols<WPM>(s_Wmov, mb, kc, c, g), get_chain(s_m, kc, nb, l));
 #pragma unroll
           for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[i]) * w2mv[i];
         }
@@ -850,25 +843,16 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     s_w2m[q] = a.fr.w2mf[q];
   }
   for (int q = threadIdx.x; q < H; q += W * 64) s_wd[q] = a.fr.wdf[q];
-  for (int q = threadIdx.x; q < H * O / 8; q += W * 64) {   // 16-byte row pieces of both matrices
-    const int r = q / (O / 8), p = q % (O / 8);
-    *reinterpret_cast<bf16x8*>(s_Whl + r * WP + 8 * p) = load_chunk((const bf16*)a.w2 + (int64_t)r * O + 8 * p);
-    *reinterpret_cast<bf16x8*>(s_Wmov + r * WP + 8 * p) = load_chunk((const bf16*)a.w1m + (int64_t)r * M + 8 * p);
+  // W_hl[h][o], W1_mov[o][m], from the packed (in, out) layout or its nn.Linear transpose
+  if (a.lin) {
+    fill_weight_lds_t<H, O, WP, W * 64>(s_Whl, (const bf16*)a.w2);
+    fill_weight_lds_t<O, M, WP, W * 64>(s_Wmov, (const bf16*)a.w1m);
+  } else {
+    fill_weight_lds<H, O, WP, W * 64>(s_Whl, (const bf16*)a.w2);
+    fill_weight_lds<O, M, WP, W * 64>(s_Wmov, (const bf16*)a.w1m);
   }
-  // A operand of the product with W (rows r = 16 blk + c, K slice kc): W[r][32 kc + kappa_chain(g, s)]
-  auto a_rows = [&](const bf16* Wl, int blk, int kc) -> bf16x8 {
-    const bf16* p = Wl + (16 * blk + c) * WP + 32 * kc + 4 * g;
-    return __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16),
-                                   0, 1, 2, 3, 4, 5, 6, 7);
-  };
-  // A operand of the product with W^T (rows r = 16 blk + c of W^T): W[32 kc + kappa_chain(g, s)][r]
-  auto a_cols = [&](const bf16* Wl, int blk, int kc) -> bf16x8 {
-    const int kb = 32 * kc + 4 * g;
-    const bf16* p0 = Wl + (kb + (c >> 2)) * WP + 16 * blk + 4 * (c & 3);
-    const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
-    const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p0 + 16 * WP));
-    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-  };
+  auto a_rows = [&](const bf16* Wl, int blk, int kc) { return lds_rows<WP>(Wl, blk, kc, c, g); };
+  auto a_cols = [&](const bf16* Wl, int blk, int kc) { return lds_cols<WP>(Wl, blk, kc, c, g); };
   const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)w * kFragElems + l * 8);
   const bf16x8 I = ident_chunk(c, g);
 

@@ -46,6 +46,7 @@ struct LayerShape {
   int64_t N, E;
   int F, FE, H, O, M, KU, NUC;   // KU = 32 * NUC (edge-input slots incl. r2 hi/lo)
   bool eq, mean, bf16;
+  bool lin;                      // weights in torch.nn.Linear (out, in) layout
   size_t esz;                    // bytes per activation element
 };
 int make_shape(const EgnnDims* d, LayerShape* s);
@@ -155,7 +156,8 @@ struct FwdArgs {
   float* out_mov; int64_t smov;
   float* carry;
   const int32_t* fix_rows; const int32_t* n_fix;
-  const void* w1m;   // W1_mov (O x M), row-major, activation dtype
+  const void* w1m;   // W1_mov: (O x M) row-major, or (M x O) with lin
+  int lin;           // weights in torch.nn.Linear (out, in) layout
 };
 // part 0: edge tiles, part 1: split/empty-row fix-up
 int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
@@ -175,8 +177,9 @@ struct BwdArgs {
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
   int64_t ldE;     // wide kernels: row pitch of the feature-major factors Dm1 ... Dp
-  const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype
-  const void* w1m;
+  const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype;
+  const void* w1m; // (O x H) and (M x O) with lin
+  int lin;         // weights in torch.nn.Linear (out, in) layout
 };
 int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 
@@ -208,6 +211,7 @@ int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hip
 struct FinalizeArgs {
   const float *dWhl, *dW1m, *dw2m, *dWe, *dwd, *dWn;   // fp32 sums (see BwdWs)
   void* gw1; void* gw2; void* gw1m; void* gw2m; void* gb1; void* gb2; void* gbx1;
+  int lin;   // write the weight gradients in torch.nn.Linear (out, in) layout
 };
 int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st);
 

@@ -22,6 +22,8 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   s->N = d->N; s->E = d->E; s->F = d->F; s->FE = d->FE; s->H = d->H; s->O = d->O; s->M = d->M;
   s->eq = d->equivariant != 0; s->mean = d->mean_agg != 0; s->bf16 = d->dtype == EGNN_BF16;
   if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (d->weight_layout != EGNN_WEIGHTS_PACKED && d->weight_layout != EGNN_WEIGHTS_LINEAR) return EGNN_ERR_DIMS;
+  s->lin = d->weight_layout == EGNN_WEIGHTS_LINEAR;
   if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
   if (d->F < 1 || d->F > 512 || d->F % 16 != 0) return EGNN_ERR_DIMS;
   if (d->FE < 0 || d->FE > 480 || d->FE % 8 != 0) return EGNN_ERR_DIMS;
@@ -140,14 +142,21 @@ struct FragDesc {
 struct PrepArgs {
   FragDesc f0, f1, f2, f3, f4, f5;
   int nfrag;
-  const void* w1; void* wn;                 // [W_n1 | W_n2] (F x 2H) from the packed w1_msg rows
+  const void* w1; void* wn;                 // [W_n1 | W_n2] (F x 2H) from the w1_msg rows (columns)
   const void *b2, *bx1, *w2m, *wd;
   float *b2f, *bx1f, *w2mf, *wdf;
   int F, FE, H, O, M, eq;
+  int kw;                                   // 0: w1_msg is (K, H) packed; else its row length K (nn.Linear layout)
 };
 
+// w1_msg element (input row k, hidden unit h): packed (K, H), or (H, K) with kw = K
 template <typename T>
-__device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq) {
+__device__ __forceinline__ float w1_at(const T* w1, int64_t k, int64_t h, int H, int kw) {
+  return to_f32(kw ? w1[h * kw + k] : w1[k * H + h]);
+}
+
+template <typename T>
+__device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq, int kw) {
   const int64_t total = (int64_t)(d.R / 16) * d.nkc * kFragElems;
   const T* src = (const T*)d.src;
   T* dst = (T*)d.dst;
@@ -166,12 +175,12 @@ __device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq) {
         case FK_WT: v = to_f32(src[(int64_t)k * d.ld + r]); break;
         case FK_W: v = to_f32(src[(int64_t)r * d.ld + k]); break;
         case FK_U:  // r = hidden unit h, k = edge-input slot
-          if (k < FE) v = to_f32(src[(int64_t)(2 * F + eq + k) * H + r]);
-          else if (eq && k == FE) v = to_f32(src[(int64_t)(2 * F) * H + r]);
-          else if (eq && k == FE + 1 && sizeof(T) == 2) v = to_f32(src[(int64_t)(2 * F) * H + r]);
+          if (k < FE) v = w1_at(src, 2 * F + eq + k, r, H, kw);
+          else if (eq && k == FE) v = w1_at(src, 2 * F, r, H, kw);
+          else if (eq && k == FE + 1 && sizeof(T) == 2) v = w1_at(src, 2 * F, r, H, kw);
           break;
         case FK_UT:  // row 0 = w_d
-          if (eq && r == 0) v = to_f32(src[(int64_t)(2 * F) * H + k]);
+          if (eq && r == 0) v = w1_at(src, 2 * F, k, H, kw);
           break;
       }
     }
@@ -184,12 +193,12 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
   const int job = blockIdx.y;
   if (job < p.nfrag) {
     switch (job) {
-      case 0: frag_build<T>(p.f0, p.F, p.FE, p.H, p.eq); break;
-      case 1: frag_build<T>(p.f1, p.F, p.FE, p.H, p.eq); break;
-      case 2: frag_build<T>(p.f2, p.F, p.FE, p.H, p.eq); break;
-      case 3: frag_build<T>(p.f3, p.F, p.FE, p.H, p.eq); break;
-      case 4: frag_build<T>(p.f4, p.F, p.FE, p.H, p.eq); break;
-      default: frag_build<T>(p.f5, p.F, p.FE, p.H, p.eq); break;
+      case 0: frag_build<T>(p.f0, p.F, p.FE, p.H, p.eq, p.kw); break;
+      case 1: frag_build<T>(p.f1, p.F, p.FE, p.H, p.eq, p.kw); break;
+      case 2: frag_build<T>(p.f2, p.F, p.FE, p.H, p.eq, p.kw); break;
+      case 3: frag_build<T>(p.f3, p.F, p.FE, p.H, p.eq, p.kw); break;
+      case 4: frag_build<T>(p.f4, p.F, p.FE, p.H, p.eq, p.kw); break;
+      default: frag_build<T>(p.f5, p.F, p.FE, p.H, p.eq, p.kw); break;
     }
   } else if (job == p.nfrag) {
     const T* w1 = (const T*)p.w1;
@@ -197,13 +206,13 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
     const int64_t total = (int64_t)p.F * 2 * p.H;
     for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
       const int64_t f = t / (2 * p.H), n = t % (2 * p.H);
-      wn[t] = n < p.H ? w1[f * p.H + n] : w1[(p.F + f) * p.H + (n - p.H)];
+      wn[t] = from_f32<T>(n < p.H ? w1_at(w1, f, n, p.H, p.kw) : w1_at(w1, p.F + f, n - p.H, p.H, p.kw));
     }
   } else {
     const int n = p.O > p.M + 4 ? (p.O > p.H ? p.O : p.H) : (p.M + 4 > p.H ? p.M + 4 : p.H);
     for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x) {
       if (t < p.O) p.b2f[t] = p.b2 ? to_f32(((const T*)p.b2)[t]) : 0.0f;
-      if (t < p.H) p.wdf[t] = p.wd ? to_f32(((const T*)p.wd)[t]) : 0.0f;
+      if (t < p.H) p.wdf[t] = p.wd ? w1_at((const T*)p.w1, 2 * p.F, t, p.H, p.kw) : 0.0f;
       if (t < p.M + 4) {
         p.bx1f[t] = (p.bx1 && t < p.M) ? to_f32(((const T*)p.bx1)[t]) : 0.0f;
         p.w2mf[t] = (p.w2m && t < p.M) ? to_f32(((const T*)p.w2m)[t]) : 0.0f;
@@ -223,18 +232,21 @@ static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const 
     *slots[p.nfrag++] = FragDesc{dst, R, K, (int)cdiv(K, 32), kind, chain, src, ld};
     most = std::max<int64_t>(most, (int64_t)(R / 16) * cdiv(K, 32) * kFragElems);
   };
-  add(fr.hlT, s.O, s.H, FK_WT, 1, w2, s.O);               // A[o][h] = W_hl[h][o]
-  if (s.eq) add(fr.movT, s.M, s.O, FK_WT, 1, w1m, s.M);   // A[m][o] = W1mov[o][m]
+  // packed weights: W_hl (H x O), W1mov (O x M); nn.Linear layout: their transposes
+  const int kW = s.lin ? FK_W : FK_WT, kWT = s.lin ? FK_WT : FK_W;
+  add(fr.hlT, s.O, s.H, kW, 1, w2, s.lin ? s.H : s.O);                // A[o][h] = W_hl[h][o]
+  if (s.eq) add(fr.movT, s.M, s.O, kW, 1, w1m, s.lin ? s.O : s.M);    // A[m][o] = W1mov[o][m]
   if (s.NUC) add(fr.u, s.H, s.KU, FK_U, 0, w1, s.H);
   if (with_bwd) {
-    if (s.eq) add(fr.mov, s.O, s.M, FK_W, 1, w1m, s.M);   // A[o][m] = W1mov[o][m]
-    add(fr.hl, s.H, s.O, FK_W, 1, w2, s.O);               // A[h][o] = W_hl[h][o]
+    if (s.eq) add(fr.mov, s.O, s.M, kWT, 1, w1m, s.lin ? s.O : s.M);  // A[o][m] = W1mov[o][m]
+    add(fr.hl, s.H, s.O, kWT, 1, w2, s.lin ? s.H : s.O);              // A[h][o] = W_hl[h][o]
     if (s.eq) add(fr.uT, 16, s.H, FK_UT, 1, w1, s.H);
   }
   p.w1 = w1; p.wn = fr.wn;
   most = std::max<int64_t>(most, (int64_t)s.F * 2 * s.H);
   p.b2 = b2; p.bx1 = s.eq ? bx1 : nullptr; p.w2m = s.eq ? w2m : nullptr;
-  p.wd = s.eq ? (const T*)w1 + (int64_t)(2 * s.F) * s.H : nullptr;
+  p.wd = s.eq ? w1 : nullptr;
+  p.kw = s.lin ? 2 * s.F + (s.eq ? 1 : 0) + s.FE : 0;
   p.b2f = fr.b2f; p.bx1f = fr.bx1f; p.w2mf = fr.w2mf; p.wdf = fr.wdf;
   p.F = s.F; p.FE = s.FE; p.H = s.H; p.O = s.O; p.M = s.M; p.eq = s.eq ? 1 : 0;
   const unsigned bx = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(most, 256), 1024));
@@ -892,13 +904,19 @@ __global__ void finalize_kernel(FinalizeArgs f, int F, int FE, int H, int O, int
       if (row < 2 * F) v = f.dWn[(row % F) * 2 * H + (row >= F ? H : 0) + h];
       else if (eq && row == 2 * F) v = f.dwd[h];
       else v = f.dWe[h * FE + (row - 2 * F - g)];
-      ((T*)f.gw1)[u] = from_f32<T>(v);
+      ((T*)f.gw1)[f.lin ? h * (2 * F + g + FE) + row : u] = from_f32<T>(v);
       continue;
     }
     u -= n_w1;
-    if (u < n_w2) { ((T*)f.gw2)[u] = from_f32<T>(f.dWhl[u]); continue; }
+    if (u < n_w2) {   // dW_hl[h][o]
+      ((T*)f.gw2)[f.lin ? (u % O) * H + u / O : u] = from_f32<T>(f.dWhl[u]);
+      continue;
+    }
     u -= n_w2;
-    if (u < n_w1m) { ((T*)f.gw1m)[u] = from_f32<T>(f.dW1m[u]); continue; }
+    if (u < n_w1m) {   // dW1mov[o][m]
+      ((T*)f.gw1m)[f.lin ? (u % M) * O + u / M : u] = from_f32<T>(f.dW1m[u]);
+      continue;
+    }
     u -= n_w1m;
     if (u < n_w2m) { ((T*)f.gw2m)[u] = from_f32<T>(f.dw2m[u]); continue; }
     u -= n_w2m;

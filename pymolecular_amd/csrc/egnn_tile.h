@@ -119,5 +119,54 @@ __device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int ei
 
 __device__ __forceinline__ uint32_t lo16(unsigned long long b) { return (uint32_t)(b & 0xffffull); }
 
+// A operands from a row-major bf16 matrix W in LDS (row pitch P), K slice kc,
+// lane (c, g) element s <-> k = 32 kc + kappa_chain(g, s):
+//   lds_rows: A[r][k] = W[r][k] for rows r = 16 blk + c (two 8-byte reads)
+//   lds_cols: A[r][k] = W[k][r] (two transposing reads: within a 16-lane group,
+//             lane j addresses row kb + j/4, columns 16 blk + 4 (j % 4) .. + 3,
+//             and lane c receives column 16 blk + c of rows kb .. kb + 3)
+template <int P>
+__device__ __forceinline__ bf16x8 lds_rows(const bf16* W, int blk, int kc, int c, int g) {
+  const bf16* p = W + (16 * blk + c) * P + 32 * kc + 4 * g;
+  return __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+template <int P>
+__device__ __forceinline__ bf16x8 lds_cols(const bf16* W, int blk, int kc, int c, int g) {
+  const bf16* p0 = W + (32 * kc + 4 * g + (c >> 2)) * P + 16 * blk + 4 * (c & 3);
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p0 + 16 * P));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// dst[i][j] (DR x DC, row pitch P) = W[i][j] from W^T (DC x DR) row-major: one
+// 8 x 8 block per thread, transposed in registers, 16-byte reads and writes
+template <int DR, int DC, int P, int NT>
+__device__ __forceinline__ void fill_weight_lds_t(bf16* dst, const bf16* src) {
+  for (int q = threadIdx.x; q < (DR / 8) * (DC / 8); q += NT) {
+    const int ib = q % (DR / 8), jb = q / (DR / 8);   // rows 8 ib .. + 7, columns 8 jb .. + 7 of W
+    bf16x8 v[8];
+#pragma unroll
+    for (int r = 0; r < 8; ++r) v[r] = load_chunk(src + (int64_t)(8 * jb + r) * DR + 8 * ib);   // v[r][u] = W[8 ib + u][8 jb + r]
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      bf16x8 o;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) o[r] = v[r][u];
+      *reinterpret_cast<bf16x8*>(dst + (8 * ib + u) * P + 8 * jb) = o;
+    }
+  }
+}
+
+// dst[i][j] (DR x DC, row pitch P) = W[i][j] of a row-major weight matrix;
+// block-cooperative 16-byte reads and writes
+template <int DR, int DC, int P, int NT>
+__device__ __forceinline__ void fill_weight_lds(bf16* dst, const bf16* src) {
+  for (int q = threadIdx.x; q < DR * DC / 8; q += NT) {
+    const int i = q / (DC / 8), j = 8 * (q % (DC / 8));
+    *reinterpret_cast<bf16x8*>(dst + i * P + j) = load_chunk(src + (int64_t)i * DC + j);
+  }
+}
+
 }  // namespace tile
 }  // namespace egnn

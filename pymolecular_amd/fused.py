@@ -127,17 +127,20 @@ def _dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"unsupported dtype {dt}: the fused layer runs in float32 or bfloat16")
 
 
-def _dims(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg) -> EgnnDims:
+def _dims(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg, linear=False) -> EgnnDims:
+    """Dimensions of the layer; ``linear``: weights in torch.nn.Linear (out, in) layout."""
     N, F = h.shape
     FE = 0 if edge_feat is None else int(edge_feat.shape[1])
-    H = int(w1.shape[-1])
-    O = int(w2.shape[1])
-    M = int(w1m.shape[1]) if (equivariant and w1m is not None) else O
+    io = (lambda t: (int(t.shape[1]), int(t.shape[0]))) if linear else (lambda t: (int(t.shape[0]), int(t.shape[1])))  # noqa: E731
+    K1, H = io(w1)
+    O = io(w2)[1]
+    M = io(w1m)[1] if (equivariant and w1m is not None) else O
     g = 1 if equivariant else 0
-    if w1.shape[0] != 2 * F + g + FE:
-        raise ValueError(f"w1_msg has {w1.shape[0]} rows, expected 2*F + {g} + F_E = {2 * F + g + FE}")
+    if K1 != 2 * F + g + FE:
+        raise ValueError(f"w1_msg has {K1} input rows, expected 2*F + {g} + F_E = {2 * F + g + FE}")
     return EgnnDims(N=N, E=int(col.numel()), F=F, FE=FE, H=H, O=O, M=M, equivariant=g,
-                    mean_agg=1 if mean_agg else 0, dtype=_dtype_code(h.dtype))
+                    mean_agg=1 if mean_agg else 0, dtype=_dtype_code(h.dtype),
+                    weight_layout=_capi.WEIGHTS_LINEAR if linear else _capi.WEIGHTS_PACKED)
 
 
 def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant):
@@ -159,15 +162,18 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
 
 def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
                        w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
-                       equivariant: bool = True, node_proj: Optional[torch.Tensor] = None):
+                       equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
+                       linear_weights: bool = False):
     """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``.
 
     ``node_proj`` (uint8 device buffer of ``egnn_node_proj_bytes``): when given,
     receives the per-node projections so that a following backward can reuse them.
+    ``linear_weights``: w1_msg, w2_msg, w1_mov in torch.nn.Linear (out, in) layout
+    instead of the packed (in, out) layout of layer.py:24-28.
     """
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
-    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg)
+    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev = h.device
     N, O = h.shape[0], dims.O
@@ -192,8 +198,10 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
 
 def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                         b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
-                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None):
-    """Backward by recomputation.  Returns a dict of gradients (None where absent).
+                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
+                        linear_weights: bool = False):
+    """Backward by recomputation.  Returns a dict of gradients (None where absent),
+    weight gradients in the layout of the weights.
 
     ``node_proj``: the buffer a forward with the same inputs filled (skips the
     per-node projection GEMM), or None.
@@ -201,7 +209,7 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
     w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
-    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg)
+    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev, dt = h.device, h.dtype
     N = h.shape[0]
@@ -239,9 +247,9 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
                 b2=g_b2, bx1=g_bx1)
 
 
-def _node_proj_buffer(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg):
+def _node_proj_buffer(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg, linear=False):
     ef = None if (edge_feat is None or edge_feat.shape[1] == 0) else edge_feat
-    dims = _dims(h, ef, col, w1, w2, w1m, equivariant, mean_agg)
+    dims = _dims(h, ef, col, w1, w2, w1m, equivariant, mean_agg, linear)
     n = _capi.lib().egnn_node_proj_bytes(dims)
     return torch.empty(max(n, 16), dtype=torch.uint8, device=h.device)
 
@@ -256,19 +264,21 @@ class EGNNFusedFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
-                b1=None, b2=None, bx1=None, mean_agg=False, equivariant=True):
+                b1=None, b2=None, bx1=None, mean_agg=False, equivariant=True, linear_weights=False):
         # dtype/layout conversion once; the backward reuses the converted tensors
         ctx.shapes = [None if t is None else tuple(t.shape) for t in (w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1)]
         h, coord_p, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1 = _prep_inputs(
             h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
-        pq = _node_proj_buffer(h, edge_feat, col_indices, w1_msg, w2_msg, w1_mov, equivariant, mean_agg)
+        pq = _node_proj_buffer(h, edge_feat, col_indices, w1_msg, w2_msg, w1_mov, equivariant, mean_agg,
+                               linear_weights)
         out_msg, out_mov = egnn_fused_forward(h, coord_p, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg,
                                               w2_msg, w1_mov, w2_mov, b1, b2, bx1, mean_agg=mean_agg,
-                                              equivariant=equivariant, node_proj=pq)
+                                              equivariant=equivariant, node_proj=pq, linear_weights=linear_weights)
         ctx.save_for_backward(h, coord_p, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov,
                               w2_mov, b1, b2, bx1, pq)
         ctx.mean_agg = mean_agg
         ctx.equivariant = equivariant
+        ctx.linear_weights = linear_weights
         ctx.coord_shape = None if coord is None else tuple(coord.shape)
         ctx.coord_dtype = None if coord is None else coord.dtype
         if out_mov is None:
@@ -279,12 +289,13 @@ class EGNNFusedFn(torch.autograd.Function):
     def backward(ctx, g_msg, g_mov):
         (h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1, pq) = ctx.saved_tensors
         if g_msg is None:
-            g_msg = torch.zeros((h.shape[0], w2.shape[1]), dtype=h.dtype, device=h.device)
+            O = w2.shape[0] if ctx.linear_weights else w2.shape[1]
+            g_msg = torch.zeros((h.shape[0], O), dtype=h.dtype, device=h.device)
         if g_mov is None:
             g_mov = torch.zeros((h.shape[0], 3), dtype=torch.float32, device=h.device)
         g = egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2,
                                 bx1, g_msg, g_mov, mean_agg=ctx.mean_agg, equivariant=ctx.equivariant,
-                                node_proj=pq)
+                                node_proj=pq, linear_weights=ctx.linear_weights)
         gc = g["coord"]
         if gc is not None and ctx.coord_shape is not None and ctx.coord_shape[1] != 3:
             full = torch.zeros(ctx.coord_shape, dtype=torch.float32, device=gc.device)
@@ -294,19 +305,25 @@ class EGNNFusedFn(torch.autograd.Function):
             gc = gc.to(ctx.coord_dtype)
         wg = [g[k] for k in ("w1_msg", "w2_msg", "w1_mov", "w2_mov", "b1", "b2", "bx1")]
         wg = [None if (t is None or shp is None) else t.reshape(shp) for t, shp in zip(wg, ctx.shapes)]
-        return (g["h"], gc, None, None, None, None, *wg, None, None)
+        return (g["h"], gc, None, None, None, None, *wg, None, None, None)
 
 
 def egnn_fused(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None, w2_mov=None,
-               b1=None, b2=None, bx1=None, *, mean_agg=False, equivariant=True):
+               b1=None, b2=None, bx1=None, *, mean_agg=False, equivariant=True, linear_weights=False):
     """Differentiable fused layer (see :class:`EGNNFusedFn`).
 
+    ``linear_weights``: w1_msg (H, 2F+g+F_E), w2_msg (O, H), w1_mov (M, O) as
+    torch.nn.Linear stores them, used in place (no transposed copies) and with
+    gradients in the same layout; else the packed (in, out) layout.
     Edge-feature widths that are not a multiple of 8 are zero-padded (with
-    matching zero rows of W_e) outside the Function, so gradients stay exact.
+    matching zero W_e entries) outside the Function, so gradients stay exact.
     """
     if edge_feat is not None and edge_feat.shape[1] % 8:
         pad = 8 - edge_feat.shape[1] % 8
         edge_feat = torch.nn.functional.pad(edge_feat, (0, pad))
-        w1_msg = torch.cat([w1_msg, w1_msg.new_zeros((pad, w1_msg.shape[1]))], dim=0)
+        if linear_weights:
+            w1_msg = torch.cat([w1_msg, w1_msg.new_zeros((w1_msg.shape[0], pad))], dim=1)
+        else:
+            w1_msg = torch.cat([w1_msg, w1_msg.new_zeros((pad, w1_msg.shape[1]))], dim=0)
     return EGNNFusedFn.apply(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
-                             b1, b2, bx1, mean_agg, equivariant)
+                             b1, b2, bx1, mean_agg, equivariant, linear_weights)

@@ -100,9 +100,9 @@ class E_GCL(nn.Module):
         e0, e2 = self.edge_mlp[0], self.edge_mlp[2]
         c0, c2 = self.coord_mlp[0], self.coord_mlp[2]
         ef = edge_attr if (edge_attr is not None and self.edges_in_d > 0) else None
-        agg, agg_x = egnn_fused(h, coord, ef, row_ptrs, col_s, perm, e0.weight.t(), e2.weight.t(), c0.weight.t(),
+        agg, agg_x = egnn_fused(h, coord, ef, row_ptrs, col_s, perm, e0.weight, e2.weight, c0.weight,
                                 c2.weight.reshape(-1), e0.bias, e2.bias, c0.bias,
-                                mean_agg=self.coords_agg == "mean", equivariant=True)
+                                mean_agg=self.coords_agg == "mean", equivariant=True, linear_weights=True)
         return agg, agg_x
 
     def forward(self, h, edge_index, coord, edge_attr=None, node_attr=None, csr=None):

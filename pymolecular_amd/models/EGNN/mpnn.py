@@ -42,8 +42,8 @@ class MPNN_GCL(nn.Module):
         row_ptrs, col_s, perm = csr if csr is not None else _csr_cache.get(row, col, h.shape[0])
         e0, e2 = self.edge_mlp[0], self.edge_mlp[2]
         ef = edge_attr if (edge_attr is not None and self.edges_in_d > 0) else None
-        agg, _ = egnn_fused(h, None, ef, row_ptrs, col_s, perm, e0.weight.t(), e2.weight.t(), None, None,
-                            e0.bias, e2.bias, None, mean_agg=False, equivariant=False)
+        agg, _ = egnn_fused(h, None, ef, row_ptrs, col_s, perm, e0.weight, e2.weight, None, None,
+                            e0.bias, e2.bias, None, mean_agg=False, equivariant=False, linear_weights=True)
         return agg
 
     def forward(self, h, edge_index, edge_attr=None, node_attr=None, csr=None):

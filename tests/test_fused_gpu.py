@@ -24,7 +24,9 @@ def _dev(a, dt=None):
     return t.to(dt) if dt is not None else t
 
 
-def run_fused(case, dtype, backward=True):
+def run_fused(case, dtype, backward=True, linear=False):
+    """``linear``: pass w1_msg, w2_msg, w1_mov transposed (torch.nn.Linear layout); their
+    gradients are transposed back, so results compare with the packed-layout run."""
     from pymolecular_amd import fused
     dt = DT[dtype]
     rowptr, col = _dev(case.rowptr), _dev(case.col)
@@ -33,16 +35,23 @@ def run_fused(case, dtype, backward=True):
     coord = _dev(case.coord) if case.eq else None
     ef = _dev(case.ef, dt)
     p = {k: _dev(v, dt) for k, v in case.p.items()}
+    mats = ("w1_msg", "w2_msg", "w1_mov")
+    if linear:
+        p = {k: (v.t().contiguous() if k in mats and v is not None else v) for k, v in p.items()}
     print(f"[fused] N={case.N} E={case.E} F={case.F} FE={case.FE} H={case.H} O={case.O} M={case.M} "
-          f"eq={case.eq} mean={case.mean} dtype={dtype}", flush=True)
+          f"eq={case.eq} mean={case.mean} dtype={dtype} linear={linear}", flush=True)
     out_msg, out_mov = fused.egnn_fused_forward(h, coord, ef, rowptr, col, eids, p["w1_msg"], p["w2_msg"],
                                                 p.get("w1_mov"), p.get("w2_mov"), p.get("b1"), p.get("b2"),
-                                                p.get("bx1"), mean_agg=case.mean, equivariant=case.eq)
+                                                p.get("bx1"), mean_agg=case.mean, equivariant=case.eq,
+                                                linear_weights=linear)
     res = dict(out_msg=out_msg.float().cpu().numpy(), out_mov=None if out_mov is None else out_mov.cpu().numpy())
     if backward:
         g = fused.egnn_fused_backward(h, coord, ef, rowptr, col, eids, p["w1_msg"], p["w2_msg"], p.get("w1_mov"),
                                       p.get("w2_mov"), p.get("b1"), p.get("b2"), p.get("bx1"), _dev(case.gm, dt),
-                                      _dev(case.gx) if case.eq else None, mean_agg=case.mean, equivariant=case.eq)
+                                      _dev(case.gx) if case.eq else None, mean_agg=case.mean, equivariant=case.eq,
+                                      linear_weights=linear)
+        if linear:
+            g = {k: (v.t() if k in mats and v is not None else v) for k, v in g.items()}
         res["grads"] = {k: (None if v is None else v.float().cpu().numpy()) for k, v in g.items()}
     torch.cuda.synchronize()
     return res
@@ -132,6 +141,27 @@ def test_determinism_bitwise():
     a = run_fused(case, "bf16")
     b = run_fused(case, "bf16")
     assert np.array_equal(a["out_msg"], b["out_msg"]) and np.array_equal(a["out_mov"], b["out_mov"])
+    for k, v in a["grads"].items():
+        if v is not None:
+            assert np.array_equal(v, b["grads"][k]), k
+
+
+@pytest.mark.parametrize("dtype,F,FE,H,O,M,eq", [
+    ("bf16", 128, 0, 128, 128, 128, True),     # cooperative kernels
+    ("bf16", 128, 16, 128, 128, 128, False),   # MPNN backward with 16 waves
+    ("bf16", 64, 8, 64, 32, 32, True),         # cooperative kernels, H = 64
+    ("bf16", 256, 32, 256, 256, 256, True),    # wide kernels
+    ("fp32", 128, 16, 128, 128, 128, True),    # one wave per tile
+])
+def test_linear_weight_layout(dtype, F, FE, H, O, M, eq):
+    """Weights given in torch.nn.Linear layout give the packed-layout results bit for bit."""
+    rowptr, col = random_csr(300, (np.arange(300) * 7) % 29, seed=52)
+    case = Case(rowptr, col, F, FE, H, O, M, seed=23, eq=eq)
+    a = run_fused(case, dtype)
+    b = run_fused(case, dtype, linear=True)
+    assert np.array_equal(a["out_msg"], b["out_msg"])
+    if eq:
+        assert np.array_equal(a["out_mov"], b["out_mov"])
     for k, v in a["grads"].items():
         if v is not None:
             assert np.array_equal(v, b["grads"][k]), k
