@@ -707,6 +707,186 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// split-K matrix-vector product over rows: partial[z][m] = sum_{k in slice z}
+// A[k][m] b[k] with A k-major (row k of M values, row stride lda) and b of
+// stride ldb (the dw_d and dw2_mov reductions over the edges).  Each thread
+// owns 4 consecutive m of one row group; the RG row groups of a block are
+// combined in a fixed order through LDS, so results do not depend on timing.
+// ---------------------------------------------------------------------------
+template <typename T, int M4>
+__global__ __launch_bounds__(256) void gemv_splitk_kernel(const T* __restrict__ A, int64_t lda,
+                                                          const float* __restrict__ b, int64_t ldb, int64_t K,
+                                                          int64_t ksplit, int M, float* __restrict__ partial) {
+  constexpr int RG = 256 / M4;                        // row groups; M4 threads cover 4 * M4 >= M columns
+  __shared__ float red[RG][4 * M4];
+  const int q = threadIdx.x % M4, rg = threadIdx.x / M4;
+  const int m = 4 * q;
+  const int64_t kbeg = (int64_t)blockIdx.x * ksplit;
+  const int64_t kend = K < kbeg + ksplit ? K : kbeg + ksplit;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  if (m < M) {
+    for (int64_t k = kbeg + rg; k < kend; k += RG) {
+      const float bk = b[k * ldb];
+      const f32x4 a = load4_f32(A + k * lda + m);
+      acc[0] += a[0] * bk; acc[1] += a[1] * bk; acc[2] += a[2] * bk; acc[3] += a[3] * bk;
+    }
+  }
+  *reinterpret_cast<f32x4*>(&red[rg][m]) = acc;
+  __syncthreads();
+  for (int t = threadIdx.x; t < M; t += 256) {
+    float v = 0.f;
+#pragma unroll 8
+    for (int r = 0; r < RG; ++r) v += red[r][t];
+    partial[(int64_t)blockIdx.x * M + t] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 split-K product: partial[z] = A^T-or-A B over the K slice z, BM x BN tile
+// per 256-thread block (2 x 2 waves), K in slices of 32 double-buffered through
+// registers (the next slice is loaded while the current one is multiplied).
+// Both operands are staged k-contiguous ([m][k], [n][k]) so that one lane reads
+// 8 consecutive k with two 16-byte LDS reads (8 v_mfma_f32_16x16x4_f32).
+// Rows 16-byte aligned; the ones row and the B row indirection of Gemm2Args.
+// ---------------------------------------------------------------------------
+template <bool A_KC, bool B_NC, int BM, int BN>
+__global__ __launch_bounds__(256) void gemm_f32_splitk_kernel(Gemm2Args g) {
+  constexpr int BK = 32, PK = BK + 4;                   // row pitch of the k-contiguous tiles (floats)
+  constexpr int WM = BM / 2, MI = WM / 16, WN = BN / 2, NJ = WN / 16;
+  constexpr int NLA = BM * BK / 4 / 256, NLB = BN * BK / 4 / 256;   // 16-byte vectors per thread per slice
+  static_assert(NLA >= 1 && NLB >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) float As[2][BM * PK];
+  __shared__ __attribute__((aligned(16))) float Bs[2][BN * PK];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
+  const int64_t kbeg = (int64_t)blockIdx.z * g.ksplit;
+  const int64_t kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
+  const float* A = (const float*)g.A;
+  const float* B = (const float*)g.B;
+
+  f32x4 acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  f32x4 ra[NLA], rb[NLB];
+  auto load_stage = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      const int idx = tid + 256 * i;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (A_KC) {   // A[m][k]
+        const int r = idx / (BK / 4), q = idx % (BK / 4);
+        const int64_t m = m0 + r, k = k0 + 4 * q;
+        if (m < g.M && k < kend) {
+          if (m == g.a_ones_row) {
+            for (int u = 0; u < 4; ++u) v[u] = k + u < kend ? 1.0f : 0.0f;
+          } else if (k + 4 <= kend) {
+            v = *reinterpret_cast<const f32x4*>(A + m * g.lda + k);
+          } else {
+            for (int u = 0; u < 4; ++u) if (k + u < kend) v[u] = A[m * g.lda + k + u];
+          }
+        }
+      } else {                // A[k][m]
+        const int r = idx / (BM / 4), q = idx % (BM / 4);
+        const int64_t k = k0 + r, m = m0 + 4 * q;
+        if (k < kend && m < g.M) {
+          const bool ones = g.a_ones_row >= m && g.a_ones_row < m + 4;
+          if (m + 4 <= g.M && !ones) v = *reinterpret_cast<const f32x4*>(A + k * g.lda + m);
+          else
+            for (int u = 0; u < 4; ++u)
+              if (m + u < g.M) v[u] = (m + u == g.a_ones_row) ? 1.0f : A[k * g.lda + m + u];
+        }
+      }
+      ra[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < NLB; ++i) {
+      const int idx = tid + 256 * i;
+      f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+      if constexpr (B_NC) {   // B[k][n], or B[b_kidx[k]][n]
+        const int r = idx / (BN / 4), q = idx % (BN / 4);
+        const int64_t k = k0 + r, n = n0 + 4 * q;
+        if (k < kend && n < g.N) {
+          const int64_t kr = g.b_kidx ? (int64_t)g.b_kidx[k] : k;
+          if (n + 4 <= g.N) v = *reinterpret_cast<const f32x4*>(B + kr * g.ldb + n);
+          else
+            for (int u = 0; u < 4; ++u) if (n + u < g.N) v[u] = B[kr * g.ldb + n + u];
+        }
+      } else {                // B[n][k]
+        const int r = idx / (BK / 4), q = idx % (BK / 4);
+        const int64_t n = n0 + r, k = k0 + 4 * q;
+        if (n < g.N && k < kend) {
+          if (k + 4 <= kend) v = *reinterpret_cast<const f32x4*>(B + n * g.ldb + k);
+          else
+            for (int u = 0; u < 4; ++u) if (k + u < kend) v[u] = B[n * g.ldb + k + u];
+        }
+      }
+      rb[i] = v;
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < NLA; ++i) {
+      const int idx = tid + 256 * i;
+      if constexpr (A_KC) {
+        *reinterpret_cast<f32x4*>(&As[buf][(idx / (BK / 4)) * PK + 4 * (idx % (BK / 4))]) = ra[i];
+      } else {
+        const int r = idx / (BM / 4), q = idx % (BM / 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) As[buf][(4 * q + u) * PK + r] = ra[i][u];
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NLB; ++i) {
+      const int idx = tid + 256 * i;
+      if constexpr (!B_NC) {
+        *reinterpret_cast<f32x4*>(&Bs[buf][(idx / (BK / 4)) * PK + 4 * (idx % (BK / 4))]) = rb[i];
+      } else {
+        const int r = idx / (BN / 4), q = idx % (BN / 4);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) Bs[buf][(4 * q + u) * PK + r] = rb[i][u];
+      }
+    }
+  };
+
+  int buf = 0;
+  if (kbeg < kend) {
+    load_stage(kbeg);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) load_stage(k0 + BK);
+    f32x8 a[MI], b[NJ];
+#pragma unroll
+    for (int i = 0; i < MI; ++i) a[i] = load_chunk(&As[buf][(wm * WM + 16 * i + c) * PK + 8 * gq]);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) b[j] = load_chunk(&Bs[buf][(wn * WN + 16 * j + c) * PK + 8 * gq]);
+#pragma unroll
+    for (int i = 0; i < MI; ++i)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) mma(acc[i][j], a[i], b[j]);
+    if (more) store_stage(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
+  }
+  float* P = g.partial + (int64_t)blockIdx.z * g.M * g.N;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t m = m0 + wm * WM + 16 * i + 4 * gq + r, n = n0 + wn * WN + 16 * j + c;
+        if (m < g.M && n < g.N) P[m * g.N + n] = acc[i][j][r];
+      }
+}
+
 template <typename TA, typename TB, typename TC>
 static void gemm2_dispatch(const Gemm2Args& g, dim3 grid, hipStream_t st) {
   if (g.a_kc && g.b_nc) hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, true, true>), grid, dim3(256), 0, st, g);
@@ -721,6 +901,7 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
   // the tiled bf16 kernel moves 16-byte row segments: every operand row must start 16-byte aligned
   auto al = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 8 == 0); };
+  auto al4 = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 4 == 0); };
   const bool rows16 = al(g.A, g.lda) && al(g.A2, g.lda2) && al(g.B, g.ldb) &&
                       (g.partial ? (((uintptr_t)g.partial) & 15) == 0
                                  : al(g.C, g.ldc) && al(g.Cpre, g.ldpre) && al(g.resid, g.ldr) && al(g.zd, g.ldz));
@@ -741,6 +922,37 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
     else if (g.b_nc) GB_LAUNCH(false, true);
     else GB_LAUNCH(false, false);
 #undef GB_LAUNCH
+  } else if (g.N == 1 && g.partial && g.ksplit > 0 && !g.a_kc && g.b_nc && !g.b_bf16 && g.A2 == nullptr &&
+             g.a_ones_row < 0 && !g.b_kidx && g.M <= 256 && (((uintptr_t)g.A) & (g.a_bf16 ? 7 : 15)) == 0 &&
+             g.lda % 4 == 0 && g.M % 4 == 0) {
+    // matrix-vector products over the edges (dw_d, dw2_mov)
+    const float* b = (const float*)g.B;
+    if (g.a_bf16) {
+      if (g.M <= 128) hipLaunchKernelGGL((gemv_splitk_kernel<bf16, 32>), dim3(gz), dim3(256), 0, st, (const bf16*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+      else hipLaunchKernelGGL((gemv_splitk_kernel<bf16, 64>), dim3(gz), dim3(256), 0, st, (const bf16*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+    } else {
+      if (g.M <= 128) hipLaunchKernelGGL((gemv_splitk_kernel<float, 32>), dim3(gz), dim3(256), 0, st, (const float*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+      else hipLaunchKernelGGL((gemv_splitk_kernel<float, 64>), dim3(gz), dim3(256), 0, st, (const float*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+    }
+  } else if (!compute_bf16 && g.partial && g.ksplit > 0 && !g.a_bf16 && !g.b_bf16 && g.A2 == nullptr &&
+             al4(g.A, g.lda) && al4(g.B, g.ldb)) {
+    // fp32 split-K products, 64 columns per tile: one 160-row tile for the [W | bias]
+    // shapes of 129..160 rows (H + 1 at H = 128) when that still gives 256 blocks or
+    // more, else 64-row tiles, else 32-row tiles
+    auto nblk = [&](int bm) { return cdiv(g.M, bm) * cdiv(g.N, 64) * (int64_t)gz; };
+    const int bmf = (g.M > 128 && g.M <= 160 && nblk(160) >= 256) ? 160 : nblk(64) >= 256 ? 64 : 32;
+    const dim3 gf((unsigned)cdiv(g.M, bmf), (unsigned)cdiv(g.N, 64), gz);
+#define GF_LAUNCH(AK, BNC)                                                                          \
+    do {                                                                                            \
+      if (bmf == 160) hipLaunchKernelGGL((gemm_f32_splitk_kernel<AK, BNC, 160, 64>), gf, dim3(256), 0, st, g); \
+      else if (bmf == 64) hipLaunchKernelGGL((gemm_f32_splitk_kernel<AK, BNC, 64, 64>), gf, dim3(256), 0, st, g); \
+      else hipLaunchKernelGGL((gemm_f32_splitk_kernel<AK, BNC, 32, 64>), gf, dim3(256), 0, st, g);          \
+    } while (0)
+    if (g.a_kc && g.b_nc) GF_LAUNCH(true, true);
+    else if (g.a_kc) GF_LAUNCH(true, false);
+    else if (g.b_nc) GF_LAUNCH(false, true);
+    else GF_LAUNCH(false, false);
+#undef GF_LAUNCH
   } else if (compute_bf16) {
     if (g.a_bf16 && g.b_bf16) gemm2_dispatch<bf16, bf16, bf16>(g, grid, st);
     else if (g.a_bf16) gemm2_dispatch<bf16, float, bf16>(g, grid, st);
