@@ -69,8 +69,9 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
 int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
   K = std::max<int64_t>(K, 1);
   const bool big = K >= kSplitKBig;   // the tile launch_gemm2 picks for this product
-  const int64_t tiles = big ? cdiv(M, 128) * cdiv(N, 128) : cdiv(M, 32) * cdiv(N, 64);
-  const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(512, std::max<int64_t>(tiles, 1)), cdiv(K, 256)));
+  const int64_t tiles = N == 1 ? 1 : big ? cdiv(M, 128) * cdiv(N, N <= 32 ? 32 : 128) : cdiv(M, 32) * cdiv(N, 64);
+  const int64_t target = N == 1 ? 1024 : 512;   // matrix-vector products: one small block per split
+  const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(target, std::max<int64_t>(tiles, 1)), cdiv(K, 256)));
   return cdiv(cdiv(K, splits), 64) * 64;
 }
 
@@ -708,37 +709,103 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
 }
 
 // ---------------------------------------------------------------------------
-// split-K matrix-vector product over rows: partial[z][m] = sum_{k in slice z}
-// A[k][m] b[k] with A k-major (row k of M values, row stride lda) and b of
-// stride ldb (the dw_d and dw2_mov reductions over the edges).  Each thread
-// owns 4 consecutive m of one row group; the RG row groups of a block are
-// combined in a fixed order through LDS, so results do not depend on timing.
+// split-K matrix-vector products over the edges (dw_d, dw2_mov, the weight
+// gradients of a layer's one-output rows): partial[z][m] = sum over the rows k
+// of slice z of A(k, m) b[k], b of stride ldb.  Two operand orientations:
+//  * k-major A[k][m] (row stride lda): TPR threads cover a row with 16-byte
+//    loads, RG row groups stride over the slice, four rows in flight each;
+//  * m-major A[m][k] (row stride lda): 32 threads cover 256 k of a row with
+//    16-byte loads, b loaded once per k chunk for all rows of the thread.
+// Per-block sums are combined in a fixed order (LDS or lane shuffles).
 // ---------------------------------------------------------------------------
-template <typename T, int M4>
-__global__ __launch_bounds__(256) void gemv_splitk_kernel(const T* __restrict__ A, int64_t lda,
+template <typename T> struct Vec16T;
+template <> struct Vec16T<bf16> { typedef bf16x8 type; static constexpr int n = 8; };
+template <> struct Vec16T<float> { typedef f32x4 type; static constexpr int n = 4; };
+
+template <typename T, int M>
+__global__ __launch_bounds__(256) void gemv_kmajor_kernel(const T* __restrict__ A, int64_t lda,
                                                           const float* __restrict__ b, int64_t ldb, int64_t K,
-                                                          int64_t ksplit, int M, float* __restrict__ partial) {
-  constexpr int RG = 256 / M4;                        // row groups; M4 threads cover 4 * M4 >= M columns
-  __shared__ float red[RG][4 * M4];
-  const int q = threadIdx.x % M4, rg = threadIdx.x / M4;
-  const int m = 4 * q;
+                                                          int64_t ksplit, float* __restrict__ partial) {
+  typedef typename Vec16T<T>::type V;
+  constexpr int VE = Vec16T<T>::n, TPR = M / VE, RG = 256 / TPR;
+  static_assert(M % VE == 0 && TPR <= 256 && 256 % TPR == 0, "row width");
+  __shared__ float red[RG][M];
+  const int q = threadIdx.x % TPR, rg = threadIdx.x / TPR;
   const int64_t kbeg = (int64_t)blockIdx.x * ksplit;
   const int64_t kend = K < kbeg + ksplit ? K : kbeg + ksplit;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  if (m < M) {
-    for (int64_t k = kbeg + rg; k < kend; k += RG) {
-      const float bk = b[k * ldb];
-      const f32x4 a = load4_f32(A + k * lda + m);
-      acc[0] += a[0] * bk; acc[1] += a[1] * bk; acc[2] += a[2] * bk; acc[3] += a[3] * bk;
+  float acc[VE];
+#pragma unroll
+  for (int u = 0; u < VE; ++u) acc[u] = 0.f;
+  int64_t k = kbeg + rg;
+  for (; k + 3 * RG < kend; k += 4 * RG) {   // four rows in flight
+    V v[4];
+    float bk[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      v[r] = *reinterpret_cast<const V*>(A + (k + r * RG) * lda + VE * q);
+      bk[r] = b[(k + r * RG) * ldb];
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int u = 0; u < VE; ++u) acc[u] += to_f32(v[r][u]) * bk[r];
   }
-  *reinterpret_cast<f32x4*>(&red[rg][m]) = acc;
+  for (; k < kend; k += RG) {
+    const V v = *reinterpret_cast<const V*>(A + k * lda + VE * q);
+    const float bk = b[k * ldb];
+#pragma unroll
+    for (int u = 0; u < VE; ++u) acc[u] += to_f32(v[u]) * bk;
+  }
+#pragma unroll
+  for (int u = 0; u < VE; ++u) red[rg][VE * q + u] = acc[u];
   __syncthreads();
   for (int t = threadIdx.x; t < M; t += 256) {
-    float v = 0.f;
+    float s = 0.f;
 #pragma unroll 8
-    for (int r = 0; r < RG; ++r) v += red[r][t];
-    partial[(int64_t)blockIdx.x * M + t] = v;
+    for (int r = 0; r < RG; ++r) s += red[r][t];
+    partial[(int64_t)blockIdx.x * M + t] = s;
+  }
+}
+
+template <typename T, int MR>   // MR: rows per thread (M <= 8 MR)
+__global__ __launch_bounds__(256) void gemv_mmajor_kernel(const T* __restrict__ A, int64_t lda, int M,
+                                                          const float* __restrict__ b, int64_t ldb, int64_t K,
+                                                          int64_t ksplit, float* __restrict__ partial) {
+  const int kt = threadIdx.x & 31, rg = threadIdx.x >> 5;   // 32 threads along k, 8 row groups
+  const int64_t kbeg = (int64_t)blockIdx.x * ksplit;
+  const int64_t kend = K < kbeg + ksplit ? K : kbeg + ksplit;
+  float acc[MR];
+#pragma unroll
+  for (int j = 0; j < MR; ++j) acc[j] = 0.f;
+  for (int64_t c0 = kbeg; c0 < kend; c0 += 256) {
+    const int64_t k0 = c0 + 8 * kt;
+    float bv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) bv[u] = k0 + u < kend ? b[(k0 + u) * ldb] : 0.f;
+    const bool full = k0 + 8 <= kend;
+#pragma unroll
+    for (int j = 0; j < MR; ++j) {
+      const int m = rg + 8 * j;
+      if (m >= M || k0 >= kend) continue;
+      const T* row = A + (int64_t)m * lda + k0;
+      float s = 0.f;
+      if (full && sizeof(T) == 2) {
+        const bf16x8 v = *reinterpret_cast<const bf16x8*>(row);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += to_f32(v[u]) * bv[u];
+      } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) if (k0 + u < kend) s += to_f32(row[u]) * bv[u];
+      }
+      acc[j] += s;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MR; ++j) {
+    float v = acc[j];
+    v += shfl_xor(v, 1); v += shfl_xor(v, 2); v += shfl_xor(v, 4); v += shfl_xor(v, 8); v += shfl_xor(v, 16);
+    const int m = rg + 8 * j;
+    if (kt == 0 && m < M) partial[(int64_t)blockIdx.x * M + m] = v;
   }
 }
 
@@ -911,10 +978,12 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
     // grids of 2048 or more such tiles; else 32 x 64 tiles, whose larger grids
     // hide the memory latency of the short K loops of the node products
     const bool big = g.ksplit > 0 ? g.K >= kSplitKBig : cdiv(g.M, 128) * cdiv(g.N, 128) >= 2048;
-    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, big ? 128 : 64), gz);
+    const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
+    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
 #define GB_LAUNCH(AK, BNC)                                                                         \
     do {                                                                                           \
-      if (big) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 128, 64, 2>), gb, dim3(256), 0, st, g); \
+      if (narrow) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 32, 64, 2>), gb, dim3(256), 0, st, g); \
+      else if (big) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 128, 64, 2>), gb, dim3(256), 0, st, g); \
       else hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 32, 64, 64, 2>), gb, dim3(256), 0, st, g);   \
     } while (0)
     if (g.a_kc && g.b_nc) GB_LAUNCH(true, true);
@@ -922,18 +991,22 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
     else if (g.b_nc) GB_LAUNCH(false, true);
     else GB_LAUNCH(false, false);
 #undef GB_LAUNCH
-  } else if (g.N == 1 && g.partial && g.ksplit > 0 && !g.a_kc && g.b_nc && !g.b_bf16 && g.A2 == nullptr &&
-             g.a_ones_row < 0 && !g.b_kidx && g.M <= 256 && (((uintptr_t)g.A) & (g.a_bf16 ? 7 : 15)) == 0 &&
-             g.lda % 4 == 0 && g.M % 4 == 0) {
+  } else if (g.N == 1 && g.partial && g.ksplit > 0 && g.b_nc && !g.b_bf16 && g.A2 == nullptr && g.a_ones_row < 0 &&
+             !g.b_kidx && (((uintptr_t)g.A) & 15) == 0 && g.lda % (g.a_bf16 ? 8 : 4) == 0 &&
+             (g.a_kc ? g.M <= 256 : (g.M == 128 || g.M == 256))) {
     // matrix-vector products over the edges (dw_d, dw2_mov)
     const float* b = (const float*)g.B;
-    if (g.a_bf16) {
-      if (g.M <= 128) hipLaunchKernelGGL((gemv_splitk_kernel<bf16, 32>), dim3(gz), dim3(256), 0, st, (const bf16*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
-      else hipLaunchKernelGGL((gemv_splitk_kernel<bf16, 64>), dim3(gz), dim3(256), 0, st, (const bf16*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+#define GV_K(T, MM) hipLaunchKernelGGL((gemv_kmajor_kernel<T, MM>), dim3(gz), dim3(256), 0, st, (const T*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, g.partial)
+#define GV_M(T) hipLaunchKernelGGL((gemv_mmajor_kernel<T, 32>), dim3(gz), dim3(256), 0, st, (const T*)g.A, g.lda, (int)g.M, b, g.ldb, g.K, g.ksplit, g.partial)
+    if (g.a_kc) {
+      if (g.a_bf16) GV_M(bf16); else GV_M(float);
+    } else if (g.a_bf16) {
+      if (g.M == 128) GV_K(bf16, 128); else GV_K(bf16, 256);
     } else {
-      if (g.M <= 128) hipLaunchKernelGGL((gemv_splitk_kernel<float, 32>), dim3(gz), dim3(256), 0, st, (const float*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
-      else hipLaunchKernelGGL((gemv_splitk_kernel<float, 64>), dim3(gz), dim3(256), 0, st, (const float*)g.A, g.lda, b, g.ldb, g.K, g.ksplit, (int)g.M, g.partial);
+      if (g.M == 128) GV_K(float, 128); else GV_K(float, 256);
     }
+#undef GV_K
+#undef GV_M
   } else if (!compute_bf16 && g.partial && g.ksplit > 0 && !g.a_bf16 && !g.b_bf16 && g.A2 == nullptr &&
              al4(g.A, g.lda) && al4(g.B, g.ldb)) {
     // fp32 split-K products, 64 columns per tile: one 160-row tile for the [W | bias]
