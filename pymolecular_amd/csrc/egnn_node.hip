@@ -1054,48 +1054,48 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
   constexpr int EPW = 64 / LPE;                // edges per wave-wide load
+  constexpr int U = 4;                         // wave-wide loads in flight
   static_assert(LPE >= 1 && LPE <= 64 && 64 % LPE == 0, "row width");
+  typedef typename Vec16T<T>::type V;
   const int l = threadIdx.x & 63;
   const int sub = l / LPE, q = l % LPE;
   const int64_t nw = (int64_t)gridDim.x * (blockDim.x >> 6);
+  // add the rows of edges idx(j), j in [0, cnt): U x EPW rows per round, loads issued before use
+  auto gather = [&](int cnt, auto idx, float* acc, float& ax, float sign) {
+    for (int j0 = 0; j0 < cnt; j0 += U * EPW) {
+      V v[U];
+      float gx[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int j = j0 + u * EPW + sub;
+        const int e = idx(j < cnt ? j : cnt - 1);
+        v[u] = *reinterpret_cast<const V*>(Gh + (int64_t)e * H + q * VPL);
+        gx[u] = (eq && q < 3) ? Gx[(int64_t)e * 4 + q] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (j0 + u * EPW + sub < cnt) {
+#pragma unroll
+          for (int w = 0; w < VPL; ++w) acc[w] += to_f32(v[u][w]);
+          ax += sign * gx[u];
+        }
+      }
+    }
+  };
   for (int64_t n = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); n < N; n += nw) {
     float ap[VPL], aq[VPL];
 #pragma unroll
     for (int u = 0; u < VPL; ++u) ap[u] = aq[u] = 0.f;
     float ax = 0.f;
+    // destination sums: the row's edges are contiguous
     const int rs = rowptr[n], re = rowptr[n + 1];
-    for (int e0 = rs; e0 < re; e0 += EPW) {
-      const int e = e0 + sub;
-      if (e < re) {
-        const T* row = Gh + (int64_t)e * H + q * VPL;
-        if constexpr (sizeof(T) == 2) {
-          const bf16x8 v = *reinterpret_cast<const bf16x8*>(row);
-#pragma unroll
-          for (int u = 0; u < VPL; ++u) ap[u] += (float)v[u];
-        } else {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(row);
-#pragma unroll
-          for (int u = 0; u < VPL; ++u) ap[u] += v[u];
-        }
-        if (eq && q < 3) ax += Gx[(int64_t)e * 4 + q];
-      }
-    }
-    for (int k0 = 0; k0 < ce_minus(csc_ptr, n); k0 += EPW) {
-      const int k = csc_ptr[n] + k0 + sub;
-      if (k < csc_ptr[n + 1]) {
-        const int e = csc_eid[k];
-        const T* row = Gh + (int64_t)e * H + q * VPL;
-        if constexpr (sizeof(T) == 2) {
-          const bf16x8 v = *reinterpret_cast<const bf16x8*>(row);
-#pragma unroll
-          for (int u = 0; u < VPL; ++u) aq[u] += (float)v[u];
-        } else {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(row);
-#pragma unroll
-          for (int u = 0; u < VPL; ++u) aq[u] += v[u];
-        }
-        if (eq && q < 3) ax -= Gx[(int64_t)e * 4 + q];
-      }
+    gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+    // source sums: the edges listed for n by the stable CSC, edge ids 64 at a time, one per lane
+    const int cs = csc_ptr[n], ce = csc_ptr[n + 1];
+    for (int k0 = cs; k0 < ce; k0 += 64) {
+      const int cnt = ce - k0 < 64 ? ce - k0 : 64;
+      const int my = csc_eid[k0 + (l < cnt ? l : cnt - 1)];
+      gather(cnt, [&](int j) { return __shfl(my, j, 64); }, aq, ax, -1.0f);
     }
     // combine the EPW edge groups (lanes q, q + LPE, q + 2 LPE, ...) in a fixed order
 #pragma unroll
