@@ -90,8 +90,8 @@ def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
         return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
     if cls == "node_gemm":
         return 2 * N * F * 2 * H, N * (F + 2 * H) * s
-    if cls == "wgrad":   # whole layer: [dW_n1 | dW_n2; db1] over the nodes, plus the edge-factor products
-        flops, nbytes = 2 * N * (F + 1) * 2 * H, N * (F + 2 * H) * s
+    if cls == "wgrad":   # whole layer: dh and [dW_n1 | dW_n2; db1] over the nodes, plus the edge-factor products
+        flops, nbytes = 2 * N * (F + 1) * 2 * H + 2 * N * 2 * H * F, N * (F + 2 * H) * s + N * (2 * H + F) * s
         if not coop:
             flops += 2 * E * ((H + 1) * O + g * ((O + 1) * M + M + H) + H * FE)
             nbytes += E * ((H + O) * s + g * ((O + M) * s + M * s + 4 + H * s + 4) + (H * s + FE * s + 4 if FE else 0))

@@ -143,9 +143,11 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
   hipStream_t st = (hipStream_t)stream;
 
-  {
+  {   // weight fragments and the per-edge (delta, r^2) records
+    const GeoArgs geo{s.E, (int)s.N, v.erow, col, coord, strides->coord, nullptr, 0, rowptr, 0, w.geo};
     ProfScope ps(EGNN_K_PREP, st);
-    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, false, &geo, st))) != EGNN_OK)
+      return rc;
   }
   if (!aligned16(node_proj)) return EGNN_ERR_ALIGN;
   void* PQ = node_proj ? node_proj : w.PQ;
@@ -167,12 +169,6 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.carry = w.carry;
   a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
   a.geo = w.geo;
-  if (w.geo) {
-    ProfScope ps(EGNN_K_PREP, st);
-    if ((rc = hip_status(launch_edge_geo(s.E, s.N, v.erow, col, coord, strides->coord, nullptr, 0, rowptr, 0, w.geo,
-                                         st))) != EGNN_OK)
-      return rc;
-  }
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
     const int r = coop_supported(s) ? launch_coop_fwd(s, a, st)
@@ -209,9 +205,12 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   sched_layout(s.N, s.E, const_cast<void*>(sched), &v);
   hipStream_t st = (hipStream_t)stream;
 
-  {
+  {   // weight fragments and the per-edge (r^2, g_phi, delta, grad x_i / deg) records
+    const GeoArgs geo{s.E, (int)s.N, v.erow, col, coord, strides->coord, grad_out_mov, strides->mov, rowptr,
+                      s.mean ? 1 : 0, w.geo};
     ProfScope ps(EGNN_K_PREP, st);
-    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_prep(s, w1_msg, w2_msg, w1_mov, w2_mov, b2, bx1, w.fr, true, &geo, st))) != EGNN_OK)
+      return rc;
   }
   if (!aligned16(node_proj)) return EGNN_ERR_ALIGN;
   const void* PQ = node_proj ? node_proj : w.PQ;
@@ -236,12 +235,6 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.dwpart = w.dwpart; a.LW = w.LW;
   a.ldE = w.ldE;
   a.geo = w.geo;
-  if (w.geo) {
-    ProfScope ps(EGNN_K_PREP, st);
-    if ((rc = hip_status(launch_edge_geo(s.E, s.N, v.erow, col, coord, strides->coord, grad_out_mov, strides->mov,
-                                         rowptr, s.mean, w.geo, st))) != EGNN_OK)
-      return rc;
-  }
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
@@ -259,26 +252,8 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       return rc;
   }
 
-  // dh = [dP | dQ] [W_n1 | W_n2]^T
-  {
-    Gemm2Args g{};
-    g.M = s.N; g.N = s.F; g.K = 2 * s.H;
-    g.A = w.dPQ; g.lda = 2 * s.H; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
-    g.B = w.fr.wn; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 0;   // B[k][f] = Wn[f][k]
-    g.C = grad_h; g.ldc = strides->h; g.c_bf16 = s.bf16;
-    ProfScope ps(EGNN_K_NODE_GEMM, st);
-    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
-  }
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
-  if (coop) {
-    ProfScope ps(EGNN_K_WGRAD, st);
-    if (s.E > 0) {
-      if ((rc = hip_status(launch_sum_rows(w.dwpart, w.nblk, w.LW, w.dwsum, st))) != EGNN_OK) return rc;
-    } else {
-      if ((rc = hip_status(launch_sum_rows(w.dwpart, 0, w.LW, w.dwsum, st))) != EGNN_OK) return rc;
-    }
-  }
   // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
   auto splitk2 = [&](Gemm2Args g, float* dst) -> int32_t {
     g.ksplit = splitk_len(g.M, g.N, g.K);
@@ -354,7 +329,13 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     if ((rc = splitk2(g, w.dWe)) != EGNN_OK) return rc;
   }
   {
-    // [dW_n1 | dW_n2 ; db1 | .] = [h | 1]^T [dP | dQ], split over nodes, fixed-order sum
+    // dh = [dP | dQ] [W_n1 | W_n2]^T, and [dW_n1 | dW_n2 ; db1 | .] = [h | 1]^T [dP | dQ] split over the
+    // nodes with a fixed-order sum: two independent products, one launch
+    Gemm2Args d{};
+    d.M = s.N; d.N = s.F; d.K = 2 * s.H;
+    d.A = w.dPQ; d.lda = 2 * s.H; d.a_bf16 = s.bf16; d.a_kc = 1; d.a_ones_row = -1;
+    d.B = w.fr.wn; d.ldb = 2 * s.H; d.b_bf16 = s.bf16; d.b_nc = 0;   // B[k][f] = Wn[f][k]
+    d.C = grad_h; d.ldc = strides->h; d.c_bf16 = s.bf16;
     Gemm2Args g{};
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
     g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;
@@ -364,18 +345,20 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), g.ksplit);
     if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
     ProfScope ps(EGNN_K_WGRAD, st);
-    if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_gemm2_pair(d, g, s.bf16, st))) != EGNN_OK) return rc;
+    if (coop) {   // both sums, stored in the caller's layout by one launch
+      GradSumArgs q{};
+      q.part0 = w.dwpart; q.nrows0 = s.E > 0 ? w.nblk : 0; q.L0 = w.LW; q.kind0 = kGradCoop;
+      q.part1 = w.part; q.nrows1 = nsplit; q.L1 = g.M * g.N; q.kind1 = kGradWn;
+      q.f.gw1 = grad_w1_msg; q.f.gw2 = grad_w2_msg; q.f.gw1m = grad_w1_mov; q.f.gw2m = grad_w2_mov;
+      q.f.gb1 = grad_b1; q.f.gb2 = grad_b2; q.f.gbx1 = grad_bx1; q.f.lin = s.lin;
+      q.F = s.F; q.FE = s.FE; q.H = s.H; q.O = s.O; q.M = s.M; q.g = s.eq ? 1 : 0;
+      return hip_status(launch_grad_sum(s.bf16, q, st));
+    }
     if ((rc = hip_status(launch_sum_rows(w.part, nsplit, g.M * g.N, w.dWn, st))) != EGNN_OK) return rc;
   }
   FinalizeArgs f{};
   f.dWhl = w.dWhl; f.dW1m = w.dW1m; f.dw2m = w.dw2m; f.dWe = w.dWe; f.dwd = w.dwd; f.dWn = w.dWn;
-  if (coop) {
-    f.dWhl = w.dwsum;
-    f.dW1m = f.dWhl + (int64_t)(s.H + 1) * s.O;
-    f.dw2m = f.dW1m + (s.eq ? (int64_t)(s.O + 1) * s.M : 0);
-    f.dWe = f.dw2m + (s.eq ? s.M : 0);
-    f.dwd = f.dWe + (int64_t)s.H * s.FE;
-  }
   f.gw1 = grad_w1_msg; f.gw2 = grad_w2_msg; f.gw1m = grad_w1_mov; f.gw2m = grad_w2_mov;
   f.gb1 = grad_b1; f.gb2 = grad_b2; f.gbx1 = grad_bx1; f.lin = s.lin;
   ProfScope ps(EGNN_K_WGRAD, st);
@@ -427,17 +410,18 @@ int32_t node_shape(const EgnnNodeDims* d, NodeShape* s) {
 
 bool ld_ok(int64_t ld, int64_t width, size_t esz) { return ld >= width && (ld * (int64_t)esz) % 16 == 0; }
 
-struct NodeWs { void* dz; float* part; float* S1; float* S2; int64_t part_elems; };
+// dz, then the split-K partials of [x1 | x2 | 1]^T dz and of [act | 1]^T dout
+struct NodeWs { void* dz; float* part1; float* part2; int64_t part1_elems, part2_elems; };
 
 size_t node_ws_layout(const NodeShape& s, void* base, NodeWs* w) {
   char* b = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
-  w->part_elems = std::max<int64_t>(splitk_parts(s.K + 1, s.Hn, s.N), splitk_parts(s.Hn + 1, s.Fo, s.N));
+  w->part1_elems = splitk_parts(s.K + 1, s.Hn, s.N);
+  w->part2_elems = splitk_parts(s.Hn + 1, s.Fo, s.N);
   w->dz = take((size_t)s.N * s.Hn * s.esz);
-  w->part = (float*)take((size_t)w->part_elems * sizeof(float));
-  w->S1 = (float*)take((size_t)(s.K + 1) * s.Hn * sizeof(float));
-  w->S2 = (float*)take((size_t)(s.Hn + 1) * s.Fo * sizeof(float));
+  w->part1 = (float*)take((size_t)w->part1_elems * sizeof(float));
+  w->part2 = (float*)take((size_t)w->part2_elems * sizeof(float));
   return off;
 }
 
@@ -509,66 +493,58 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   node_ws_layout(s, workspace, &w);
   hipStream_t st = (hipStream_t)stream;
   ProfScope ps(EGNN_K_NODE_UPDATE, st);
-  if (s.N > 0) {
-    {  // dz = (dout W2) * SiLU'(pre)
-      Gemm2Args g{};
-      g.M = s.N; g.N = s.Hn; g.K = s.Fo;
-      g.A = grad_out; g.lda = ldgo; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
-      g.B = w2; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 1;        // B[k][n] = W2[k][n]
-      g.C = w.dz; g.ldc = s.Hn; g.c_bf16 = s.bf16;
-      g.zd = pre; g.ldz = s.Hn;
-      if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
-    }
-    {  // grad_x = dz W1 (+ dout on the first K1 columns)
-      Gemm2Args g{};
-      g.M = s.N; g.N = s.K; g.K = s.Hn;
-      g.A = w.dz; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 1; g.a_ones_row = -1;
-      g.B = w1; g.ldb = s.K; g.b_bf16 = s.bf16; g.b_nc = 1;         // B[k][n] = W1[k][n]
-      g.C = grad_x; g.ldc = s.K; g.c_bf16 = s.bf16;
-      if (s.residual) { g.resid = grad_out; g.ldr = ldgo; g.resid_len = s.K1; }
-      if ((rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
-    }
+  // dz = (dout W2) * SiLU'(pre)
+  Gemm2Args dz{};
+  dz.M = s.N; dz.N = s.Hn; dz.K = s.Fo;
+  dz.A = grad_out; dz.lda = ldgo; dz.a_bf16 = s.bf16; dz.a_kc = 1; dz.a_ones_row = -1;
+  dz.B = w2; dz.ldb = s.Hn; dz.b_bf16 = s.bf16; dz.b_nc = 1;        // B[k][n] = W2[k][n]
+  dz.C = w.dz; dz.ldc = s.Hn; dz.c_bf16 = s.bf16;
+  dz.zd = pre; dz.ldz = s.Hn;
+  // grad_x = dz W1 (+ dout on the first K1 columns)
+  Gemm2Args gx{};
+  gx.M = s.N; gx.N = s.K; gx.K = s.Hn;
+  gx.A = w.dz; gx.lda = s.Hn; gx.a_bf16 = s.bf16; gx.a_kc = 1; gx.a_ones_row = -1;
+  gx.B = w1; gx.ldb = s.K; gx.b_bf16 = s.bf16; gx.b_nc = 1;         // B[k][n] = W1[k][n]
+  gx.C = grad_x; gx.ldc = s.K; gx.c_bf16 = s.bf16;
+  if (s.residual) { gx.resid = grad_out; gx.ldr = ldgo; gx.resid_len = s.K1; }
+  // [x1 | x2 | 1]^T dz and [act | 1]^T dout, split over the nodes
+  Gemm2Args s1{};
+  s1.M = s.K + 1; s1.N = s.Hn; s1.K = s.N;
+  s1.A = x1; s1.lda = ld1; s1.a_bf16 = s.bf16; s1.a_kc = 0; s1.a_ones_row = s.K;
+  if (s.K2 > 0) { s1.A2 = x2; s1.lda2 = ld2; s1.a_split = s.K1; }
+  s1.B = w.dz; s1.ldb = s.Hn; s1.b_bf16 = s.bf16; s1.b_nc = 1;
+  s1.ksplit = splitk_len(s1.M, s1.N, s1.K); s1.partial = w.part1;
+  Gemm2Args s2{};
+  s2.M = s.Hn + 1; s2.N = s.Fo; s2.K = s.N;
+  s2.A = act; s2.lda = s.Hn; s2.a_bf16 = s.bf16; s2.a_kc = 0; s2.a_ones_row = s.Hn;
+  s2.B = grad_out; s2.ldb = ldgo; s2.b_bf16 = s.bf16; s2.b_nc = 1;
+  s2.ksplit = splitk_len(s2.M, s2.N, s2.K); s2.partial = w.part2;
+  const int64_t nsplit1 = cdiv(std::max<int64_t>(s.N, 1), s1.ksplit), nsplit2 = cdiv(std::max<int64_t>(s.N, 1), s2.ksplit);
+  if (nsplit1 * s1.M * s1.N > w.part1_elems || nsplit2 * s2.M * s2.N > w.part2_elems) return EGNN_ERR_WORKSPACE;
+  if (s.N > 0) {   // two launches of two independent products each
+    if ((rc = hip_status(launch_gemm2_pair(dz, s2, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_gemm2_pair(gx, s1, s.bf16, st))) != EGNN_OK) return rc;
   }
-  {  // S1 = [x1 | x2 | 1]^T dz
-    Gemm2Args g{};
-    g.M = s.K + 1; g.N = s.Hn; g.K = s.N;
-    const int64_t ksplit = splitk_len(g.M, g.N, g.K);
-    const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
-    g.A = x1; g.lda = ld1; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.K;
-    if (s.K2 > 0) { g.A2 = x2; g.lda2 = ld2; g.a_split = s.K1; }
-    g.B = w.dz; g.ldb = s.Hn; g.b_bf16 = s.bf16; g.b_nc = 1;
-    g.ksplit = ksplit; g.partial = w.part;
-    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
-    if (s.N > 0 && (rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
-    if ((rc = hip_status(launch_sum_rows(w.part, s.N > 0 ? nsplit : 0, g.M * g.N, w.S1, st))) != EGNN_OK) return rc;
-  }
-  {  // S2 = [act | 1]^T dout
-    Gemm2Args g{};
-    g.M = s.Hn + 1; g.N = s.Fo; g.K = s.N;
-    const int64_t ksplit = splitk_len(g.M, g.N, g.K);
-    const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), ksplit);
-    g.A = act; g.lda = s.Hn; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.Hn;
-    g.B = grad_out; g.ldb = ldgo; g.b_bf16 = s.bf16; g.b_nc = 1;
-    g.ksplit = ksplit; g.partial = w.part;
-    if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
-    if (s.N > 0 && (rc = hip_status(launch_gemm2(g, s.bf16, st))) != EGNN_OK) return rc;
-    if ((rc = hip_status(launch_sum_rows(w.part, s.N > 0 ? nsplit : 0, g.M * g.N, w.S2, st))) != EGNN_OK) return rc;
-  }
-  return hip_status(launch_node_finalize(s.bf16, w.S1, w.S2, s.K, s.Hn, s.Fo, grad_w1, grad_b1, grad_w2, grad_b2, st));
+  GradSumArgs q{};
+  q.part0 = w.part1; q.nrows0 = s.N > 0 ? nsplit1 : 0; q.L0 = s1.M * s1.N;
+  q.kind0 = kGradLinT; q.K0 = s.K; q.Nn0 = s.Hn; q.w0 = grad_w1; q.b0 = grad_b1;
+  q.part1 = w.part2; q.nrows1 = s.N > 0 ? nsplit2 : 0; q.L1 = s2.M * s2.N;
+  q.kind1 = kGradLinT; q.K1 = s.Hn; q.Nn1 = s.Fo; q.w1 = grad_w2; q.b1 = grad_b2;
+  // both fixed-order sums, stored as nn.Linear weight and bias gradients
+  return hip_status(launch_grad_sum(s.bf16, q, st));
 }
 
 }  // extern "C"
 
 // ---- dense-layer weight gradient ------------------------------------------------
 namespace {
-struct DenseWs { float* part; float* S; int64_t part_elems; };
+struct DenseWs { float* part; int64_t part_elems; };
 size_t dense_ws_layout(int64_t N, int Kin, int Nout, void* base, DenseWs* w) {
   char* b = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
   w->part_elems = splitk_parts(Kin + 1, Nout, N);
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
-  w->S = (float*)take((size_t)(Kin + 1) * Nout * sizeof(float));
   return off;
 }
 }  // namespace
@@ -627,9 +603,10 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
     g.ksplit = ksplit; g.partial = w.part;
     if ((rc = hip_status(launch_gemm2(g, bf16, st))) != EGNN_OK) return rc;
   }
-  if ((rc = hip_status(launch_sum_rows(w.part, N > 0 ? nsplit : 0, (int64_t)(Kin + 1) * Nout, w.S, st))) != EGNN_OK)
-    return rc;
-  return hip_status(launch_node_finalize(bf16, w.S, nullptr, Kin, Nout, 0, grad_w, grad_b, nullptr, nullptr, st));
+  GradSumArgs q{};   // fixed-order sum stored as the nn.Linear weight and bias gradients
+  q.part0 = w.part; q.nrows0 = N > 0 ? nsplit : 0; q.L0 = (int64_t)(Kin + 1) * Nout;
+  q.kind0 = kGradLinT; q.K0 = Kin; q.Nn0 = Nout; q.w0 = grad_w; q.b0 = grad_b;
+  return hip_status(launch_grad_sum(bf16, q, st));
 }
 
 }  // extern "C"

@@ -31,39 +31,6 @@ namespace {
 using namespace tile;
 
 
-// One thread per edge: delta = x_i - x_j and r^2 (forward record), plus the
-// incoming coordinate gradient of row i (scaled by 1/deg for mean aggregation)
-// and g_phi = delta . grad (backward record).  Gathers and the degree division
-// happen here, off the fused kernels' critical path.
-__global__ __launch_bounds__(256) void edge_geo_kernel(int64_t E, int N, const int32_t* __restrict__ erow,
-                                                       const int32_t* __restrict__ col,
-                                                       const float* __restrict__ coord, int64_t sc,
-                                                       const float* __restrict__ gmov, int64_t sgx,
-                                                       const int32_t* __restrict__ rowptr, int mean,
-                                                       float* __restrict__ out) {
-  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < E; e += (int64_t)gridDim.x * blockDim.x) {
-    const int i = clampi(erow[e], N), j = clampi(col[e], N);
-    const float* xi = coord + (int64_t)i * sc;
-    const float* xj = coord + (int64_t)j * sc;
-    const float dx = xi[0] - xj[0], dy = xi[1] - xj[1], dz = xi[2] - xj[2];
-    const float r2 = dx * dx + dy * dy + dz * dz;
-    if (!gmov) {
-      *reinterpret_cast<f32x4*>(out + e * 4) = f32x4{dx, dy, dz, r2};
-      continue;
-    }
-    float s = 1.0f;
-    if (mean) {
-      const int deg = rowptr[i + 1] - rowptr[i];
-      s = 1.0f / (float)(deg > 1 ? deg : 1);
-    }
-    const float* gx = gmov + (int64_t)i * sgx;
-    const float g0 = gx[0] * s, g1 = gx[1] * s, g2 = gx[2] * s;
-    const float gphi = dx * g0 + dy * g1 + dz * g2;
-    *reinterpret_cast<f32x4*>(out + e * 8) = f32x4{r2, gphi, dx, dy};
-    *reinterpret_cast<f32x4*>(out + e * 8 + 4) = f32x4{dz, g0, g1, g2};
-  }
-}
-
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
@@ -1396,15 +1363,6 @@ int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
 }
 
 }  // namespace
-
-int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* col, const float* coord, int64_t sc,
-                    const float* gmov, int64_t sgx, const int32_t* rowptr, int mean, float* out, hipStream_t st) {
-  if (E <= 0) return 0;
-  const int blocks = (int)std::min<int64_t>(cdiv(E, 256), 8192);
-  hipLaunchKernelGGL(edge_geo_kernel, dim3(blocks), dim3(256), 0, st, E, (int)N, erow, col, coord, sc, gmov, sgx,
-                     rowptr, mean, out);
-  return (int)hipGetLastError();
-}
 
 bool coop_supported(const LayerShape& s) {
   const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);

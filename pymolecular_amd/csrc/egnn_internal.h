@@ -78,9 +78,8 @@ struct BwdWs {
   float* dwd;      // H
   float* dWn;      // (F+1) x 2H  last row = [db1 | sum dQ]
   int64_t part_elems;
-  // workgroup-cooperative path: per-block partials of [dWhl | dW1m | dw2m | dWe | dwd] and their sum
+  // workgroup-cooperative path: per-block partials of [dWhl | dW1m | dw2m | dWe | dwd]
   float* dwpart;
-  float* dwsum;
   int nblk;
   int64_t LW;
   float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
@@ -101,8 +100,20 @@ int launch_schedule(const int32_t* rowptr, const int32_t* col, int64_t N, int64_
                     void* tmp, size_t tmp_bytes, hipStream_t st);
 size_t schedule_tmp_bytes(int64_t N, int64_t E);
 
+// Per-edge geometry records of the cooperative and wide kernels, built by the prep launch:
+// forward [E][4] = (delta, r^2); backward [E][8] = (r^2, g_phi, delta, grad x_i / deg).
+struct GeoArgs {
+  int64_t E; int N;
+  const int32_t* erow; const int32_t* col;
+  const float* coord; int64_t sc;
+  const float* gmov; int64_t sgx;   // null: forward records
+  const int32_t* rowptr; int mean;
+  float* out;                        // null: no records
+};
+// Weight fragments, [W_n1 | W_n2], fp32 vectors and (geo != null) the per-edge records, in one launch.
 int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
-                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st);
+                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, const GeoArgs* geo,
+                hipStream_t st);
 
 // Node-level GEMM with 16-byte loads along the contiguous dimension of each
 // operand.  A is (M x K) row-major ("k contiguous") or given as its transpose
@@ -127,6 +138,8 @@ struct Gemm2Args {
   const int32_t* b_kidx;   // n-contiguous B only: row k of B is row b_kidx[k] of the array
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
+// Two independent products, in one launch when both take the 32 x 64 bf16 tiles (else one after the other).
+int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf16, hipStream_t st);
 // Weight-gradient GEMM over edges with k-contiguous bf16 operands (feature-major
 // per-edge factors): partial[z][m][n] = sum_{k in split z} A[m][k] B[n][k];
 // b_colsum adds row M = sum_k B[n][k].  ksplit is a multiple of 64.
@@ -140,8 +153,6 @@ struct WgradArgs {
 };
 int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st);
 int64_t wgrad_ksplit(int64_t K);   // k per split of the edge-factor GEMMs (multiple of 64)
-int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,
-                         void* gw2, void* gb2, hipStream_t st);
 
 struct FwdArgs {
   int64_t N, E, ntiles;
@@ -196,8 +207,6 @@ int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 // Per-edge geometry records for the cooperative kernels (one thread per edge):
 // forward [E][4] = (delta, r^2); backward [E][8] = (r^2, g_phi, delta, grad x_i / deg).
-int launch_edge_geo(int64_t E, int64_t N, const int32_t* erow, const int32_t* col, const float* coord, int64_t sc,
-                    const float* gmov, int64_t sgx, const int32_t* rowptr, int mean, float* out, hipStream_t st);
 int bwd_tile_edges(const LayerShape& s);
 
 // dPQ[n] = [sum_row Gh | sum_csc Gh] (summed in fp32, stored in the activation dtype);
@@ -214,5 +223,18 @@ struct FinalizeArgs {
   int lin;   // write the weight gradients in torch.nn.Linear (out, in) layout
 };
 int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st);
+
+// Fixed-order sums of up to two sets of weight-gradient partials part_j[nrows_j][L_j], each sum stored in the
+// caller's gradient layout (grad_sum_kernel).  Kinds: kGradLinT, an (K + 1) x Nn [W^T ; b] stored as w[n][k], b[n];
+// kGradCoop, the cooperative backward's partial layout (coop_dw_len); kGradWn, [dW_n1 | dW_n2 ; db1].
+enum { kGradLinT = 0, kGradCoop = 1, kGradWn = 2 };
+struct GradSumArgs {
+  const float* part0; int64_t nrows0, L0; int kind0, K0, Nn0; void* w0; void* b0;
+  const float* part1; int64_t nrows1, L1; int kind1, K1, Nn1; void* w1; void* b1;
+  int64_t nb0;               // blocks of the first job (set by launch_grad_sum)
+  FinalizeArgs f;            // destinations of kGradCoop / kGradWn
+  int F, FE, H, O, M, g;     // layer shape of kGradCoop / kGradWn (g = 1 for the equivariant layer)
+};
+int launch_grad_sum(bool bf16_out, GradSumArgs a, hipStream_t st);
 
 }  // namespace egnn

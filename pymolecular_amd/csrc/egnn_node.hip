@@ -105,7 +105,6 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->nblk = coop ? coop_bwd_blocks(s) : 0;
   w->LW = coop ? coop_dw_len(s) : 0;
   w->dwpart = coop ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
-  w->dwsum = coop ? (float*)take((size_t)w->LW * sizeof(float)) : nullptr;
   w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
   w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N);
@@ -148,6 +147,9 @@ struct PrepArgs {
   float *b2f, *bx1f, *w2mf, *wdf;
   int F, FE, H, O, M, eq;
   int kw;                                   // 0: w1_msg is (K, H) packed; else its row length K (nn.Linear layout)
+  int bx;                                   // blocks per job
+  GeoArgs geo;                              // per-edge records, on geo_blocks blocks after the jobs
+  int geo_blocks;
 };
 
 // w1_msg element (input row k, hidden unit h): packed (K, H), or (H, K) with kw = K
@@ -157,11 +159,11 @@ __device__ __forceinline__ float w1_at(const T* w1, int64_t k, int64_t h, int H,
 }
 
 template <typename T>
-__device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq, int kw) {
+__device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq, int kw, int bid, int nb) {
   const int64_t total = (int64_t)(d.R / 16) * d.nkc * kFragElems;
   const T* src = (const T*)d.src;
   T* dst = (T*)d.dst;
-  for (int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)gridDim.x * blockDim.x) {
+  for (int64_t idx = bid * (int64_t)blockDim.x + threadIdx.x; idx < total; idx += (int64_t)nb * blockDim.x) {
     int s = (int)(idx & 7);
     int lane = (int)((idx >> 3) & 63);
     int64_t f = idx >> 9;
@@ -189,29 +191,61 @@ __device__ void frag_build(const FragDesc& d, int F, int FE, int H, int eq, int 
   }
 }
 
+// One thread per edge: delta = x_i - x_j and r^2 (forward record), plus the
+// incoming coordinate gradient of row i (scaled by 1/deg for mean aggregation)
+// and g_phi = delta . grad (backward record).  Gathers and the degree division
+// happen here, off the fused kernels' critical path.
+__device__ void edge_geo(const GeoArgs& a, int bid, int nb) {
+  for (int64_t e = bid * (int64_t)blockDim.x + threadIdx.x; e < a.E; e += (int64_t)nb * blockDim.x) {
+    const int i = clampi(a.erow[e], a.N), j = clampi(a.col[e], a.N);
+    const float* xi = a.coord + (int64_t)i * a.sc;
+    const float* xj = a.coord + (int64_t)j * a.sc;
+    const float dx = xi[0] - xj[0], dy = xi[1] - xj[1], dz = xi[2] - xj[2];
+    const float r2 = dx * dx + dy * dy + dz * dz;
+    if (!a.gmov) {
+      *reinterpret_cast<f32x4*>(a.out + e * 4) = f32x4{dx, dy, dz, r2};
+      continue;
+    }
+    float s = 1.0f;
+    if (a.mean) {
+      const int deg = a.rowptr[i + 1] - a.rowptr[i];
+      s = 1.0f / (float)(deg > 1 ? deg : 1);
+    }
+    const float* gx = a.gmov + (int64_t)i * a.sgx;
+    const float g0 = gx[0] * s, g1 = gx[1] * s, g2 = gx[2] * s;
+    const float gphi = dx * g0 + dy * g1 + dz * g2;
+    *reinterpret_cast<f32x4*>(a.out + e * 8) = f32x4{r2, gphi, dx, dy};
+    *reinterpret_cast<f32x4*>(a.out + e * 8 + 4) = f32x4{dz, g0, g1, g2};
+  }
+}
+
+// Block b < bx * (nfrag + 2) runs job b / bx with index b % bx; the blocks
+// after those build the per-edge records.
 template <typename T>
 __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
-  const int job = blockIdx.y;
-  if (job < p.nfrag) {
+  const int job = (int)(blockIdx.x / (unsigned)p.bx), bid = (int)(blockIdx.x % (unsigned)p.bx), nb = p.bx;
+  if (job > p.nfrag + 1) {
+    edge_geo(p.geo, (int)(blockIdx.x - (unsigned)(p.bx * (p.nfrag + 2))), p.geo_blocks);
+  } else if (job < p.nfrag) {
     switch (job) {
-      case 0: frag_build<T>(p.f0, p.F, p.FE, p.H, p.eq, p.kw); break;
-      case 1: frag_build<T>(p.f1, p.F, p.FE, p.H, p.eq, p.kw); break;
-      case 2: frag_build<T>(p.f2, p.F, p.FE, p.H, p.eq, p.kw); break;
-      case 3: frag_build<T>(p.f3, p.F, p.FE, p.H, p.eq, p.kw); break;
-      case 4: frag_build<T>(p.f4, p.F, p.FE, p.H, p.eq, p.kw); break;
-      default: frag_build<T>(p.f5, p.F, p.FE, p.H, p.eq, p.kw); break;
+      case 0: frag_build<T>(p.f0, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
+      case 1: frag_build<T>(p.f1, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
+      case 2: frag_build<T>(p.f2, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
+      case 3: frag_build<T>(p.f3, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
+      case 4: frag_build<T>(p.f4, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
+      default: frag_build<T>(p.f5, p.F, p.FE, p.H, p.eq, p.kw, bid, nb); break;
     }
   } else if (job == p.nfrag) {
     const T* w1 = (const T*)p.w1;
     T* wn = (T*)p.wn;
     const int64_t total = (int64_t)p.F * 2 * p.H;
-    for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
+    for (int64_t t = bid * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)nb * blockDim.x) {
       const int64_t f = t / (2 * p.H), n = t % (2 * p.H);
       wn[t] = from_f32<T>(n < p.H ? w1_at(w1, f, n, p.H, p.kw) : w1_at(w1, p.F + f, n - p.H, p.H, p.kw));
     }
   } else {
     const int n = p.O > p.M + 4 ? (p.O > p.H ? p.O : p.H) : (p.M + 4 > p.H ? p.M + 4 : p.H);
-    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < n; t += gridDim.x * blockDim.x) {
+    for (int t = bid * blockDim.x + threadIdx.x; t < n; t += nb * blockDim.x) {
       if (t < p.O) p.b2f[t] = p.b2 ? to_f32(((const T*)p.b2)[t]) : 0.0f;
       if (t < p.H) p.wdf[t] = p.wd ? w1_at((const T*)p.w1, 2 * p.F, t, p.H, p.kw) : 0.0f;
       if (t < p.M + 4) {
@@ -224,7 +258,8 @@ __global__ __launch_bounds__(256) void prep_kernel(PrepArgs p) {
 
 template <typename T>
 static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
-                     const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st) {
+                     const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, const GeoArgs* geo,
+                     hipStream_t st) {
   PrepArgs p{};
   FragDesc* slots[6] = {&p.f0, &p.f1, &p.f2, &p.f3, &p.f4, &p.f5};
   int64_t most = 0;
@@ -250,15 +285,21 @@ static int prep_impl(const LayerShape& s, const void* w1, const void* w2, const 
   p.kw = s.lin ? 2 * s.F + (s.eq ? 1 : 0) + s.FE : 0;
   p.b2f = fr.b2f; p.bx1f = fr.bx1f; p.w2mf = fr.w2mf; p.wdf = fr.wdf;
   p.F = s.F; p.FE = s.FE; p.H = s.H; p.O = s.O; p.M = s.M; p.eq = s.eq ? 1 : 0;
-  const unsigned bx = (unsigned)std::max<int64_t>(1, std::min<int64_t>(cdiv(most, 256), 1024));
-  hipLaunchKernelGGL(prep_kernel<T>, dim3(bx, (unsigned)(p.nfrag + 2)), dim3(256), 0, st, p);
+  p.bx = (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(most, 256), 1024));
+  if (geo && geo->out && geo->E > 0) {
+    p.geo = *geo;
+    p.geo_blocks = (int)std::min<int64_t>(cdiv(geo->E, 256), 8192);
+  }
+  const unsigned blocks = (unsigned)(p.bx * (p.nfrag + 2) + p.geo_blocks);
+  hipLaunchKernelGGL(prep_kernel<T>, dim3(blocks), dim3(256), 0, st, p);
   return (int)hipGetLastError();
 }
 
 int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void* w1m, const void* w2m,
-                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, hipStream_t st) {
-  return s.bf16 ? prep_impl<bf16>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, st)
-                : prep_impl<float>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, st);
+                const void* b2, const void* bx1, const FragSet& fr, bool with_bwd, const GeoArgs* geo,
+                hipStream_t st) {
+  return s.bf16 ? prep_impl<bf16>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, geo, st)
+                : prep_impl<float>(s, w1, w2, w1m, w2m, b2, bx1, fr, with_bwd, geo, st);
 }
 
 // ---------------------------------------------------------------------------
@@ -459,28 +500,36 @@ __device__ __forceinline__ bf16x8 join_tr(const bf16x4v& lo, const bf16x4v& hi) 
 // staged through NBUF LDS buffers (2: the next slice is loaded into registers
 // while the current one is multiplied; 1: one buffer, refilled after each slice).
 template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
+struct GemmBf16Smem {
+  static constexpr int PK = BK + 8, PA = BM + 16, PB = BN + 16, CP = BN + 4;
+  static constexpr int TA_ = A_KC ? BM * PK : BK * PA;
+  static constexpr int TB_ = B_NC ? BK * PB : BN * PK;
+  static constexpr int MAIN = NBUF * (TA_ + TB_);       // bf16 elements of the operand buffers
+  static constexpr int OUTB = BM * CP * 2;              // bf16-element size of the fp32 output tile
+  static constexpr int n = MAIN > OUTB ? MAIN : OUTB;
+};
+
+// One output tile (bx, by) of split bz; smem holds GemmBf16Smem<...>::n elements.
+template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
+__device__ __forceinline__ void gemm_bf16_tile(const Gemm2Args& g, int bx, int by, int bz, bf16* smem) {
+  using SM = GemmBf16Smem<A_KC, B_NC, BM, BN, BK, NBUF>;
   constexpr int WM = BM / 2, MI = WM / 16;              // rows per wave, MFMA row blocks per wave
   constexpr int WN = BN / 2, NJ = WN / 16;              // columns per wave, MFMA column blocks per wave
-  constexpr int PK = BK + 8;                            // row pitch of a k-contiguous tile (bf16)
-  constexpr int PA = BM + 16, PB = BN + 16;             // row pitches of m- / n-contiguous tiles
+  constexpr int PK = SM::PK;                            // row pitch of a k-contiguous tile (bf16)
+  constexpr int PA = SM::PA, PB = SM::PB;               // row pitches of m- / n-contiguous tiles
   constexpr int NLA = BM * BK / 8 / 256;                // 16-byte A vectors per thread per slice
   constexpr int NLB = BN * BK / 8 / 256;                // 16-byte B vectors per thread per slice
-  constexpr int TA_ = A_KC ? BM * PK : BK * PA;
-  constexpr int TB_ = B_NC ? BK * PB : BN * PK;
-  constexpr int CP = BN + 4;                            // row pitch of the fp32 output tile
-  constexpr int MAIN = NBUF * (TA_ + TB_);              // bf16 elements of the operand buffers
-  constexpr int OUTB = BM * CP * 2;                     // bf16-element size of the fp32 output tile
+  constexpr int TA_ = SM::TA_, TB_ = SM::TB_;
+  constexpr int CP = SM::CP;                            // row pitch of the fp32 output tile
   static_assert(NLA >= 1 && NLB >= 1 && BM * BK % 2048 == 0 && BN * BK % 2048 == 0, "tile too small");
-  __shared__ __attribute__((aligned(16))) bf16 smem[MAIN > OUTB ? MAIN : OUTB];
   bf16* const As0 = smem;
   bf16* const Bs0 = smem + NBUF * TA_;
   float* const Cs = reinterpret_cast<float*>(smem);
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.x * BM, n0 = (int64_t)blockIdx.y * BN;
+  const int64_t m0 = (int64_t)bx * BM, n0 = (int64_t)by * BN;
   int64_t kbeg = 0, kend = g.K;
-  if (g.ksplit > 0) { kbeg = (int64_t)blockIdx.z * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
+  if (g.ksplit > 0) { kbeg = (int64_t)bz * g.ksplit; kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit; }
   const bf16* A = (const bf16*)g.A;
   const bf16* A2 = (const bf16*)g.A2;
   const bf16* B = (const bf16*)g.B;
@@ -636,7 +685,7 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
     for (int u = 0; u < 4; ++u) { x[u] = x0[u]; x[4 + u] = x1[u]; }
     const int nv = (int)((g.N - n) < 8 ? (g.N - n) : 8);
     if (g.partial) {
-      float* P = g.partial + ((int64_t)blockIdx.z * g.M + m) * g.N + n;
+      float* P = g.partial + ((int64_t)bz * g.M + m) * g.N + n;
       if (nv == 8 && vec_n) {
         *reinterpret_cast<f32x4*>(P) = x0;
         *reinterpret_cast<f32x4*>(P + 4) = x1;
@@ -705,6 +754,28 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
     } else {
       *reinterpret_cast<bf16x8*>((bf16*)g.C + m * g.ldc + n) = o;
     }
+  }
+}
+
+template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
+__global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[GemmBf16Smem<A_KC, B_NC, BM, BN, BK, NBUF>::n];
+  gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, blockIdx.x, blockIdx.y, blockIdx.z, smem);
+}
+
+// Two independent products on 32 x 64 tiles in one launch: blocks [0, n1) are
+// the tiles of g1 (x fastest, then y, then the split), the rest those of g2.
+template <bool AK1, bool BN1, bool AK2, bool BN2>
+__global__ __launch_bounds__(256) void gemm_bf16_pair_kernel(Gemm2Args g1, Gemm2Args g2, int gx1, int gy1, int n1,
+                                                             int gx2, int gy2) {
+  constexpr int n1s = GemmBf16Smem<AK1, BN1, 32, 64, 64, 2>::n, n2s = GemmBf16Smem<AK2, BN2, 32, 64, 64, 2>::n;
+  __shared__ __attribute__((aligned(16))) bf16 smem[n1s > n2s ? n1s : n2s];
+  int b = (int)blockIdx.x;
+  if (b < n1) {
+    gemm_bf16_tile<AK1, BN1, 32, 64, 64, 2>(g1, b % gx1, (b / gx1) % gy1, b / (gx1 * gy1), smem);
+  } else {
+    b -= n1;
+    gemm_bf16_tile<AK2, BN2, 32, 64, 64, 2>(g2, b % gx2, (b / gx2) % gy2, b / (gx2 * gy2), smem);
   }
 }
 
@@ -962,22 +1033,58 @@ static void gemm2_dispatch(const Gemm2Args& g, dim3 grid, hipStream_t st) {
   else hipLaunchKernelGGL((gemm2_kernel<TA, TB, TC, false, false>), grid, dim3(256), 0, st, g);
 }
 
-int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
-  if (g.M <= 0 || g.N <= 0) return 0;
-  const unsigned gz = g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
-  const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
-  // the tiled bf16 kernel moves 16-byte row segments: every operand row must start 16-byte aligned
+namespace {
+// the tiled bf16 kernel moves 16-byte row segments: every operand row must start 16-byte aligned
+bool bf16_tiled_ok(const Gemm2Args& g, bool compute_bf16) {
   auto al = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 8 == 0); };
-  auto al4 = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 4 == 0); };
   const bool rows16 = al(g.A, g.lda) && al(g.A2, g.lda2) && al(g.B, g.ldb) &&
                       (g.partial ? (((uintptr_t)g.partial) & 15) == 0
                                  : al(g.C, g.ldc) && al(g.Cpre, g.ldpre) && al(g.resid, g.ldr) && al(g.zd, g.ldz));
-  if (compute_bf16 && g.a_bf16 && g.b_bf16 && (g.c_bf16 || g.partial) && rows16) {
-    // 128-row tiles when they fill the device twice over, else 64-row tiles
-    // 128 x 128 tiles for split-K reductions over kSplitKBig rows or more and for
-    // grids of 2048 or more such tiles; else 32 x 64 tiles, whose larger grids
-    // hide the memory latency of the short K loops of the node products
-    const bool big = g.ksplit > 0 ? g.K >= kSplitKBig : cdiv(g.M, 128) * cdiv(g.N, 128) >= 2048;
+  return compute_bf16 && g.a_bf16 && g.b_bf16 && (g.c_bf16 || g.partial) && rows16;
+}
+// 128 x 128 tiles for split-K reductions over kSplitKBig rows or more and for
+// grids of 2048 or more such tiles; else 32 x 64 tiles, whose larger grids
+// hide the memory latency of the short K loops of the node products
+bool bf16_big_tiles(const Gemm2Args& g) {
+  return g.ksplit > 0 ? g.K >= kSplitKBig : cdiv(g.M, 128) * cdiv(g.N, 128) >= 2048;
+}
+unsigned splits_of(const Gemm2Args& g) {
+  return g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
+}
+}  // namespace
+
+int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf16, hipStream_t st) {
+  const bool e1 = g1.M > 0 && g1.N > 0, e2 = g2.M > 0 && g2.N > 0;
+  const bool tiled = e1 && e2 && bf16_tiled_ok(g1, compute_bf16) && bf16_tiled_ok(g2, compute_bf16) &&
+                     !bf16_big_tiles(g1) && !bf16_big_tiles(g2);
+  const int64_t gx1 = cdiv(g1.M, 32), gy1 = cdiv(g1.N, 64), gx2 = cdiv(g2.M, 32), gy2 = cdiv(g2.N, 64);
+  const int64_t n1 = gx1 * gy1 * splits_of(g1), n2 = gx2 * gy2 * splits_of(g2);
+  if (!tiled || n1 + n2 >= (int64_t(1) << 31)) {
+    int r = e1 ? launch_gemm2(g1, compute_bf16, st) : 0;
+    if (r == 0 && e2) r = launch_gemm2(g2, compute_bf16, st);
+    return r;
+  }
+  const dim3 grid((unsigned)(n1 + n2));
+#define GP_LAUNCH(A1, B1, A2, B2) \
+  hipLaunchKernelGGL((gemm_bf16_pair_kernel<A1, B1, A2, B2>), grid, dim3(256), 0, st, g1, g2, (int)gx1, (int)gy1, \
+                     (int)n1, (int)gx2, (int)gy2)
+  if (g1.a_kc && !g1.b_nc && !g2.a_kc && g2.b_nc) GP_LAUNCH(true, false, false, true);        // dh, dW_n
+  else if (g1.a_kc && g1.b_nc && !g2.a_kc && g2.b_nc) GP_LAUNCH(true, true, false, true);     // node backward
+  else {
+    int r = launch_gemm2(g1, compute_bf16, st);
+    return r ? r : launch_gemm2(g2, compute_bf16, st);
+  }
+#undef GP_LAUNCH
+  return (int)hipGetLastError();
+}
+
+int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
+  if (g.M <= 0 || g.N <= 0) return 0;
+  const unsigned gz = splits_of(g);
+  const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
+  auto al4 = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 4 == 0); };
+  if (bf16_tiled_ok(g, compute_bf16)) {
+    const bool big = bf16_big_tiles(g);
     const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
     const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
 #define GB_LAUNCH(AK, BNC)                                                                         \
@@ -1142,25 +1249,35 @@ int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, con
 // ---------------------------------------------------------------------------
 // fixed-order partial sums and gradient scatter
 // ---------------------------------------------------------------------------
+// Sum of part[b][l] over the rows b = r, r + 4, r + 8, ... < nrows, with eight
+// loads in flight: row r + 4u + 32i goes to accumulator u, and the eight
+// accumulators are added in a fixed order, so the result is the same on every run.
+__device__ __forceinline__ float strided_col_sum(const float* __restrict__ part, int64_t nrows, int64_t L, int64_t l,
+                                                 int r) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t b = r;
+  for (; b + 28 < nrows; b += 32) {
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = part[(b + 4 * u) * L + l];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc[u] += v[u];
+  }
+#pragma unroll
+  for (int u = 0; u < 8; ++u)
+    if (b + 4 * u < nrows) acc[u] += part[(b + 4 * u) * L + l];
+  return ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
 // out[l] = sum_b part[b][l].  A block covers 64 columns with 4 row groups;
-// group r sums rows r, r+4, r+8, ... and the 4 group sums are added in order,
-// so the result is the same on every run.
+// group r sums rows r, r+4, r+8, ... and the 4 group sums are added in order.
 __global__ __launch_bounds__(256) void sum_rows_kernel(const float* __restrict__ part, int64_t nrows, int64_t L,
                                                        float* __restrict__ out) {
   __shared__ float red[4][64];
   const int cx = threadIdx.x & 63, r = threadIdx.x >> 6;
   for (int64_t l0 = (int64_t)blockIdx.x * 64; l0 < L; l0 += (int64_t)gridDim.x * 64) {
     const int64_t l = l0 + cx;
-    float a0 = 0.f, a1 = 0.f;
-    if (l < L) {
-      int64_t b = r;
-      for (; b + 4 < nrows; b += 8) {
-        a0 += part[b * L + l];
-        a1 += part[(b + 4) * L + l];
-      }
-      if (b < nrows) a0 += part[b * L + l];
-    }
-    red[r][cx] = a0 + a1;
+    red[r][cx] = l < L ? strided_col_sum(part, nrows, L, l, r) : 0.f;
     __syncthreads();
     if (r == 0 && l < L) out[l] = ((red[0][cx] + red[1][cx]) + red[2][cx]) + red[3][cx];
     __syncthreads();
@@ -1223,43 +1340,82 @@ int launch_finalize(const LayerShape& s, const FinalizeArgs& f, hipStream_t st) 
 
 
 // ---------------------------------------------------------------------------
-// node update: weight-gradient finalize (transpose to nn.Linear layout, cast)
+// fixed-order sums of weight-gradient partials, stored straight into the
+// caller's gradient buffers (one launch instead of sum_rows + finalize)
 // ---------------------------------------------------------------------------
-// S1 = [x1 | x2 | 1]^T dz   ((K + 1) x Hn),  S2 = [a | 1]^T dout   ((Hn + 1) x Fo)
+// Job j sums part_j[0 .. nrows_j)[l] for each of its L_j columns, with the
+// row order of sum_rows_kernel, and stores the sum where its kind sends l:
+//   kGradLinT:  an (K + 1) x Nn matrix [W^T ; b] -> w[n][k] (nn.Linear layout), b[n]
+//   kGradCoop:  the cooperative backward's [dWhl | dW1m | dw2m | dWe | dwd]
+//   kGradWn:    [dW_n1 | dW_n2 ; db1] ((F + 1) x 2H) -> rows 0 .. 2F of w1_msg, b1
+// A block sums 64 consecutive columns of one job.
 template <typename T>
-__global__ void node_finalize_kernel(const float* __restrict__ S1, const float* __restrict__ S2, int K, int Hn,
-                                     int Fo, T* gw1, T* gb1, T* gw2, T* gb2) {
-  const int64_t n1 = (int64_t)Hn * K, n2 = (int64_t)Fo * Hn;
-  const int64_t total = n1 + Hn + n2 + Fo;
-  for (int64_t t = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; t < total; t += (int64_t)gridDim.x * blockDim.x) {
-    if (t < n1) {
-      const int64_t hn = t / K, k = t % K;
-      gw1[t] = from_f32<T>(S1[k * Hn + hn]);
-    } else if (t < n1 + Hn) {
-      const int64_t hn = t - n1;
-      if (gb1) gb1[hn] = from_f32<T>(S1[(int64_t)K * Hn + hn]);
-    } else if (t < n1 + Hn + n2) {
-      const int64_t u = t - n1 - Hn, fo = u / Hn, hn = u % Hn;
-      gw2[u] = from_f32<T>(S2[hn * Fo + fo]);
-    } else {
-      const int64_t fo = t - n1 - Hn - n2;
-      if (gb2) gb2[fo] = from_f32<T>(S2[(int64_t)Hn * Fo + fo]);
-    }
+__device__ __forceinline__ void put_w1_row(const GradSumArgs& a, int64_t row, int64_t h, float v) {
+  const int64_t K1 = 2 * a.F + a.g + a.FE;
+  ((T*)a.f.gw1)[a.f.lin ? h * K1 + row : row * a.H + h] = from_f32<T>(v);
+}
+
+template <typename T>
+__device__ void put_grad(const GradSumArgs& a, int kind, int K, int Nn, void* w, void* b, int64_t l, float v) {
+  if (kind == kGradLinT) {
+    const int64_t k = l / Nn, n = l % Nn;
+    if (k < K) ((T*)w)[n * K + k] = from_f32<T>(v);
+    else if (b) ((T*)b)[n] = from_f32<T>(v);
+    return;
+  }
+  const int64_t H = a.H, O = a.O, M = a.M;
+  const FinalizeArgs& f = a.f;
+  if (kind == kGradWn) {
+    const int64_t r = l / (2 * H), k = l % (2 * H);
+    if (r < a.F) put_w1_row<T>(a, k < H ? r : a.F + r, k < H ? k : k - H, v);
+    else if (k < H && f.gb1) ((T*)f.gb1)[k] = from_f32<T>(v);
+    return;
+  }
+  // kGradCoop: [dW_hl (H x O) ; db2] [dW1_mov (O x M) ; dbx1] [dw2_mov] [dW_e (H x F_E)] [dw_d]
+  if (l < H * O) { ((T*)f.gw2)[f.lin ? (l % O) * H + l / O : l] = from_f32<T>(v); return; }
+  l -= H * O;
+  if (l < O) { if (f.gb2) ((T*)f.gb2)[l] = from_f32<T>(v); return; }
+  l -= O;
+  if (a.g) {
+    if (l < O * M) { ((T*)f.gw1m)[f.lin ? (l % M) * O + l / M : l] = from_f32<T>(v); return; }
+    l -= O * M;
+    if (l < M) { if (f.gbx1) ((T*)f.gbx1)[l] = from_f32<T>(v); return; }
+    l -= M;
+    if (l < M) { ((T*)f.gw2m)[l] = from_f32<T>(v); return; }
+    l -= M;
+  }
+  if (l < H * a.FE) { put_w1_row<T>(a, 2 * a.F + a.g + l % a.FE, l / a.FE, v); return; }
+  l -= H * a.FE;
+  if (a.g && l < H) put_w1_row<T>(a, 2 * a.F, l, v);
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void grad_sum_kernel(GradSumArgs a) {
+  __shared__ float red[4][64];
+  const int cx = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const bool second = (int64_t)blockIdx.x >= a.nb0;
+  const float* part = second ? a.part1 : a.part0;
+  const int64_t nrows = second ? a.nrows1 : a.nrows0;
+  const int64_t L = second ? a.L1 : a.L0;
+  const int64_t l = ((int64_t)blockIdx.x - (second ? a.nb0 : 0)) * 64 + cx;
+  red[r][cx] = l < L ? strided_col_sum(part, nrows, L, l, r) : 0.f;
+  __syncthreads();
+  if (r == 0 && l < L) {
+    const float v = ((red[0][cx] + red[1][cx]) + red[2][cx]) + red[3][cx];
+    if (second) put_grad<T>(a, a.kind1, a.K1, a.Nn1, a.w1, a.b1, l, v);
+    else put_grad<T>(a, a.kind0, a.K0, a.Nn0, a.w0, a.b0, l, v);
   }
 }
 
-int launch_node_finalize(bool bf16_out, const float* S1, const float* S2, int K, int Hn, int Fo, void* gw1, void* gb1,
-                         void* gw2, void* gb2, hipStream_t st) {
-  const int64_t total = (int64_t)Hn * K + Hn + (int64_t)Fo * Hn + Fo;
-  const int blocks = (int)std::min<int64_t>(cdiv(total, 256), 1024);
-  if (bf16_out)
-    hipLaunchKernelGGL(node_finalize_kernel<bf16>, dim3(blocks), dim3(256), 0, st, S1, S2, K, Hn, Fo, (bf16*)gw1,
-                       (bf16*)gb1, (bf16*)gw2, (bf16*)gb2);
-  else
-    hipLaunchKernelGGL(node_finalize_kernel<float>, dim3(blocks), dim3(256), 0, st, S1, S2, K, Hn, Fo, (float*)gw1,
-                       (float*)gb1, (float*)gw2, (float*)gb2);
+int launch_grad_sum(bool bf16_out, GradSumArgs a, hipStream_t st) {
+  a.nb0 = cdiv(a.L0, 64);
+  const int64_t blocks = a.nb0 + (a.part1 || a.L1 > 0 ? cdiv(a.L1, 64) : 0);
+  if (blocks <= 0) return 0;
+  if (bf16_out) hipLaunchKernelGGL(grad_sum_kernel<bf16>, dim3((unsigned)blocks), dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(grad_sum_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, st, a);
   return (int)hipGetLastError();
 }
+
 
 
 // ---------------------------------------------------------------------------

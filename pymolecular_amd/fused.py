@@ -213,7 +213,9 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev, dt = h.device, h.dtype
     N = h.shape[0]
-    gm = grad_out_msg.to(dt).contiguous()
+    gm = grad_out_msg.to(dt)
+    if gm.stride(1) != 1 or (gm.stride(0) * gm.element_size()) % 16 or gm.data_ptr() % 16:
+        gm = gm.contiguous()   # the kernels read 8- and 16-byte pieces of unit-stride rows
     gx = grad_out_mov.to(torch.float32).contiguous() if equivariant else None
     grad_h = torch.empty_like(h)
     grad_coord = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
