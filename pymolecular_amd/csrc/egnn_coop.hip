@@ -775,7 +775,8 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   constexpr int WP = 136;                           // row pitch of the LDS weight matrices (bf16, 272 bytes)
   constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 edge blocks (8 KB)
   // buffers whose live ranges do not overlap share storage:
-  //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5)
+  //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5);
+  // the waves' own m1 and m rows edge-major are transposing reads of the chain buffers
   __shared__ __attribute__((aligned(16))) bf16 s_buf1[CH];
   __shared__ __attribute__((aligned(16))) bf16 s_buf2[CH];
   __shared__ __attribute__((aligned(16))) bf16 s_gq[CH];
@@ -892,7 +893,6 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         *reinterpret_cast<bf16x8*>(s_u + (nb * 16 + c) * FEP + 8 * g) = valid[nb] ? u[nb] : zero_chunk<bf16>();
     }
     bf16x4 s1[2];
-    bf16x8 m1N;
     {
       f32x4 y[2];
 #pragma unroll
@@ -911,13 +911,13 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         s1[nb] = pack4(d);
         put_chain(s_m1, w, nb, l, y[nb]);
       }
-      m1N = edge_major(y[0], y[1], I);
     }
     __syncthreads();
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
     bf16x4 s2[2];
-    bf16x8 mN;
+    // this wave's m1 rows edge-major (dW_hl in S5), read before S4 reuses the buffer
+    const bf16x8 m1N = chain_edge_major(s_m1, w, c, g);
     {
       f32x4 y[2], acc[2];
       acc[0] = acc[1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * w + 4 * g);
@@ -939,12 +939,12 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         s2[nb] = pack4(d);
         put_chain(s_m, w, nb, l, y[nb]);
       }
-      mN = edge_major(y[0], y[1], I);
     }
     __syncthreads();
 
     // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows ----
     float phi[2] = {0.f, 0.f};
+    const bf16x8 mN = chain_edge_major(s_m, w, c, g);   // this wave's m rows edge-major (dW1_mov in S4)
     {
       const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * w + 4 * g);
       f32x4 gq[2], accq[2];

@@ -117,7 +117,8 @@ template <typename T> __device__ __forceinline__ float silu_t(float x) { return 
 struct YD { float y, d; };
 template <typename T> __device__ __forceinline__ YD silu_yd(float x) {
   const float s = sigmoid_t<T>(x);
-  return YD{x * s, s * (1.0f + x * (1.0f - s))};
+  const float y = x * s;
+  return YD{y, __builtin_fmaf(y, 1.0f - s, s)};   // s (1 + x (1 - s)) = s + y (1 - s)
 }
 
 // ---- wave helpers --------------------------------------------------------
@@ -126,6 +127,7 @@ __device__ __forceinline__ float shfl_xor(float v, int m) { return __shfl_xor(v,
 __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, 64); }
 __device__ __forceinline__ int shfl_i(int v, int src) { return __shfl(v, src, 64); }
 
-__device__ __forceinline__ int clampi(int v, int n) { return (unsigned)v < (unsigned)n ? v : (v < 0 ? 0 : n - 1); }
+// an index forced into [0, n) (n >= 1): out-of-range values, negative ones included, become n - 1
+__device__ __forceinline__ int clampi(int v, int n) { return (int)__builtin_elementwise_min((unsigned)v, (unsigned)(n - 1)); }
 
 }  // namespace egnn

@@ -57,6 +57,21 @@ __device__ __forceinline__ f32x4 transpose_block(const f32x4& v, const bf16x8& I
 __device__ __forceinline__ bf16x8 edge_major(const f32x4& nb0, const f32x4& nb1, const bf16x8& I) {
   return pack_chunk<bf16>(transpose_block(nb0, I), transpose_block(nb1, I));
 }
+// The same chunk for 16-row block blk read back from a chain buffer that holds it
+// (put_chain of both edge blocks), by two transposing reads.  Feature
+// 16 (blk & 1) + 4q + i of group blk >> 1 and edge e sit at lane slot 16q + (e & 15)
+// of chunk (blk >> 1, e >> 4), element 4 (blk & 1) + i.  Within a 16-lane group,
+// lane j addresses edge kb + j/4, features 4 (j % 4) .. + 3, and lane c receives
+// feature c of edges kb .. kb + 3: kb = 4g gives elements 0..3, kb = 16 + 4g 4..7.
+__device__ __forceinline__ bf16x8 chain_edge_major(const bf16* buf, int blk, int c, int g) {
+  const bf16* base = buf + (blk >> 1) * 2 * 64 * 8 + 16 * (c & 3) * 8 + 4 * (blk & 1);
+  const int e0 = 4 * g + (c >> 2);         // edges of the first read: 0..15, block 0
+  const bf16* p0 = base + e0 * 8;
+  const bf16* p1 = base + (64 + e0) * 8;   // edge 16 + e0: chunk of edge block 1, lane slot 16q + e0
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p1);
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
 
 __device__ __forceinline__ int rank_of(uint32_t mask, int k) {
   const uint32_t below = (k >= 31) ? 0xffffffffu : ((2u << k) - 1u);
