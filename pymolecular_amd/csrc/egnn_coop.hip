@@ -760,12 +760,15 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward of the equivariant layer, H = O = M = 128, 8 waves per tile
 // ---------------------------------------------------------------------------
-// The stages of coop_bwd_kernel with two changes.  W_hl and W1_mov are held in
-// LDS once each, row-major: the A operands of W_hl m1-type products (rows of
+// The stages of coop_bwd_kernel with three changes.  W_hl and W1_mov are held
+// in LDS once each, row-major: the A operands of W_hl m1-type products (rows of
 // W^T) come from transposing LDS reads, those of W products from plain 8-byte
-// reads, so no transposed copy and no weight registers are needed.  The
-// registers this frees carry the next tile's P_i / Q_j gathers, issued in the
-// middle of the current tile so that they have arrived when its S1 starts.
+// reads, so no transposed copy and no weight registers are needed.  The tiles
+// are software-pipelined: S1 of the next tile (VALU work: SiLU and SiLU' of the
+// first layer) runs in the same barrier interval as S5 of this tile (MFMA work:
+// g_a1 and the dW_hl products), which leaves four barriers per tile.  And the
+// loads run ahead: the indices of tile t + 2 and the P_i / Q_j / edge-feature
+// gathers of tile t + 1 are issued at the top of tile t.
 template <int NU>
 __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, M = 128, W = 8;
@@ -774,22 +777,22 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
   constexpr int WP = 136;                           // row pitch of the LDS weight matrices (bf16, 272 bytes)
   constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 edge blocks (8 KB)
-  // buffers whose live ranges do not overlap share storage:
-  //   m1 (S1 -> S2) with g_a2 (S4 -> S5), m (S2 -> S3) with g_a2 edge-major (S4 -> S5);
-  // the waves' own m1 and m rows edge-major are transposing reads of the chain buffers
-  __shared__ __attribute__((aligned(16))) bf16 s_buf1[CH];
+  // m1 of the next tile is written while this tile's g_a2 is read: separate
+  // buffers; m (S2 -> S3) shares storage with g_a2 edge-major (S4 -> S5).  The
+  // waves' own m1 and m rows edge-major are transposing reads of the chain buffers.
+  __shared__ __attribute__((aligned(16))) bf16 s_m1[CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_ga2[CH];
   __shared__ __attribute__((aligned(16))) bf16 s_buf2[CH];
   __shared__ __attribute__((aligned(16))) bf16 s_gq[CH];
   __shared__ __attribute__((aligned(16))) bf16 s_gqN[NM * 64 * 8];
   __shared__ __attribute__((aligned(16))) bf16 s_Whl[H * WP];    // W_hl[h][o]
   __shared__ __attribute__((aligned(16))) bf16 s_Wmov[O * WP];   // W1_mov[o][m]
-  bf16* const s_m1 = s_buf1;
-  bf16* const s_ga2 = s_buf1;
   bf16* const s_m = s_buf2;
   bf16* const s_ga2N = s_buf2;
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
-  __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];   // [edge][slot] edge features of the tile
+  // [edge][slot] edge features of a tile, by tile parity (the next tile's S1 writes while S5 reads)
+  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NU > 0 ? TE * FEP : 8];
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
   float* const s_b2 = s_vec;
   float* const s_bx1 = s_vec + O;
@@ -804,6 +807,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   const int64_t E = a.E;
   const int N = (int)a.N;
   const int FE = a.FE;
+  const int64_t G = gridDim.x;
 
   for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
   for (int q = threadIdx.x; q < M; q += W * 64) {
@@ -833,90 +837,139 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
   f32x4 vb2 = zero4(), vbx1 = zero4(), vw2m = zero4(), vwd = zero4();
 
-  // indices and geometry of a tile, loaded one tile ahead of their use
-  int ri[2], rj[2], eid[2];
-  float r2[2], gphi[2];
-  auto load_tile = [&](int64_t t, int* pri, int* prj, int* peid, float* pr2, float* pgp) {
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = t * TE + nb * 16 + c;
-      const bool ok = e < E;
-      const int64_t ec = ok ? e : E - 1;
-      pri[nb] = clampi(a.erow[ec], N);
-      prj[nb] = clampi(a.col[ec], N);
-      peid[nb] = (a.eids && FE > 0) ? clampi(a.eids[ec], (int)E) : (int)ec;
-      // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
-      const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
-      pr2[nb] = q.x;
-      pgp[nb] = ok ? q.y : 0.f;
+  // Indices and geometry of the tiles pass through a ring of three LDS slots
+  // (tiles t, t + 1, t + 2), fetched at the top of tile t for tile t + 2 and
+  // stored into the ring by the loader wave in the last barrier interval of
+  // tile t; every wave reads the values it needs from the ring.  No value loaded
+  // from memory is carried in registers from one tile to the next, and every
+  // wave issues the same global loads in the same order, without branches, so
+  // the memory-counter waits stay exact (a load under a branch, or a register
+  // loaded in one tile and read in the next, makes the compiler wait for all
+  // outstanding loads).
+  constexpr int LDW = W - 1;   // loader wave (waves 0 and 1 do S6)
+  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
+  __shared__ float s_r2[3][TE], s_gp[3][TE];
+  const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
+  int ld_ri = 0, ld_rj = 0, ld_eid = 0;
+  float ld_r2 = 0.f, ld_gp = 0.f;
+  auto load_idx = [&](int64_t tt) {   // raw values of edge l % 32 (all waves); nothing reads them before store_idx
+    const int64_t e = tt * TE + (l & 31);
+    const int64_t ec = e < E ? e : E - 1;
+    ld_ri = a.erow[ec];
+    ld_rj = a.col[ec];
+    if constexpr (NU > 0) ld_eid = eidp[ec];
+    const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);   // (r^2, g_phi)
+    ld_r2 = q.x;
+    ld_gp = q.y;
+  };
+  auto store_idx = [&](int slot, int64_t tt) {
+    if (w == LDW && l < TE) {
+      const int64_t e = tt * TE + l;
+      s_ri[slot][l] = clampi(ld_ri, N);
+      s_rj[slot][l] = clampi(ld_rj, N);
+      if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, (int)E) : (int)(e < E ? e : E - 1);
+      s_r2[slot][l] = ld_r2;
+      s_gp[slot][l] = e < E ? ld_gp : 0.f;   // invalid edges contribute nothing through g_phi = 0
     }
   };
-  // P_i and Q_j of the wave's 16 rows, two edge blocks
+  // the gathers of S1 from ring slot `slot`: P_i and Q_j of the wave's 16 rows and
+  // (F_E > 0) the edge features, two edge blocks; the input chunk is put together in S1
   const int poff = 32 * (w >> 1) + 8 * g + 4 * (w & 1);
   bf16x4 pv[2], qv[2];
-  auto load_pq = [&](const int* pri, const int* prj) {
+  bf16x8 ue[2];
+  auto gather = [&](int slot) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      pv[nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)pri[nb] * (4u * H) + 2u * poff));
-      qv[nb] = *reinterpret_cast<const bf16x4*>(PQb + ((uint32_t)prj[nb] * (4u * H) + 2u * (H + poff)));
+      const uint32_t i = (uint32_t)s_ri[slot][nb * 16 + c], j = (uint32_t)s_rj[slot][nb * 16 + c];
+      pv[nb] = *reinterpret_cast<const bf16x4*>(PQb + (i * (4u * H) + 2u * poff));
+      qv[nb] = *reinterpret_cast<const bf16x4*>(PQb + (j * (4u * H) + 2u * (H + poff)));
+      if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
+        ue[nb] = load_chunk(ef + (int64_t)s_eid[slot][nb * 16 + c] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
     }
   };
-  if (blockIdx.x < a.ntiles) {
-    load_tile(blockIdx.x, ri, rj, eid, r2, gphi);
-    load_pq(ri, rj);
-  }
-  __syncthreads();   // weights and vectors in LDS
-
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-    const int64_t base = t * TE;
-    bool valid[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
-    // rows of the incoming message gradient (used in S4), then the next tile's indices
-    bf16x4 gmr[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri[nb] * a.sgm + 16 * w + 4 * g);
-    int n_ri[2], n_rj[2], n_eid[2];
-    float n_r2[2], n_gphi[2];
-    const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
-    load_tile(tn, n_ri, n_rj, n_eid, n_r2, n_gphi);
-
-    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
+  // ---- S1 of tile tt: m1 (to s_m1), s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows
+  auto stage1 = [&](int64_t tt, int slot, int par, bf16x4* s1o) {
     bf16x8 u[2];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) u[nb] = input_chunk(ef, a.se, eid[nb], FE, g, r2[nb], true);
+    for (int nb = 0; nb < 2; ++nb) {
+      u[nb] = (NU > 0 && 8 * g + 8 <= FE) ? ue[nb] : zero_chunk<bf16>();
+      if (8 * g == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
+        const float r2 = s_r2[slot][nb * 16 + c];
+        const bf16 hi = (bf16)r2;
+        u[nb][0] = hi;
+        u[nb][1] = (bf16)(r2 - (float)hi);
+      }
+    }
     // the tile's edge features, [edge][slot], for the dW_e product (zero rows past the end)
     if (NU > 0 && w == 0 && 8 * g < FE) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
-        *reinterpret_cast<bf16x8*>(s_u + (nb * 16 + c) * FEP + 8 * g) = valid[nb] ? u[nb] : zero_chunk<bf16>();
+        *reinterpret_cast<bf16x8*>(s_u[par] + (nb * 16 + c) * FEP + 8 * g) =
+            tt * TE + nb * 16 + c < E ? u[nb] : zero_chunk<bf16>();
     }
-    bf16x4 s1[2];
-    {
-      f32x4 y[2];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        f32x4 acc = zero4();
-        mma(acc, wu, u[nb]);
-        const f32x4 p = unpack4(pv[nb]);
-        const f32x4 q = unpack4(qv[nb]);
-        f32x4 d;
+    for (int nb = 0; nb < 2; ++nb) {
+      f32x4 acc = zero4();
+      mma(acc, wu, u[nb]);
+      const f32x4 p = unpack4(pv[nb]);
+      const f32x4 q = unpack4(qv[nb]);
+      f32x4 y, d;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
-          y[nb][i] = r.y;
-          d[i] = r.d;
-        }
-        s1[nb] = pack4(d);
-        put_chain(s_m1, w, nb, l, y[nb]);
+      for (int i = 0; i < 4; ++i) {
+        const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+        y[i] = r.y;
+        d[i] = r.d;
       }
+      s1o[nb] = pack4(d);
+      put_chain(s_m1, w, nb, l, y);
     }
-    __syncthreads();
+  };
+
+  bf16x4 s1[2];
+  if (blockIdx.x < a.ntiles) {
+    const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
+    load_idx(blockIdx.x);
+    store_idx(0, blockIdx.x);
+    load_idx(t1);
+    store_idx(1, t1);
+  }
+  __syncthreads();   // weights, vectors and the first two ring slots in LDS
+  if (blockIdx.x < a.ntiles) {
+    gather(0);
+    stage1(blockIdx.x, 0, 0, s1);
+  }
+  __syncthreads();   // m1 of the first tile
+
+  int par = 0, sl0 = 0;
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
+    const int64_t base = t * TE;
+    const bool has_next = t + G < a.ntiles;
+    bool valid[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
+    // rows of the incoming message gradient (used in S4), the next tile's gathers
+    // (its S1 runs at the end of this tile), the indices of the tile after it
+    bf16x4 gmr[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
+    gather(sl1);
+    load_idx(t + 2 * G < a.ntiles ? t + 2 * G : t);
+    // S6 (waves 0 and 1): lane (w, l) computes component xc of dL/ddelta of edge xe;
+    // its delta and grad x_i components are loaded here
+    const int xe = l & 31, xc = (w * 64 + l) >> 5;
+    float xdel, xgrd;
+    {
+      const float* q = a.geo + (base + xe < E ? base + xe : E - 1) * 8;   // delta at 2..4, grad x_i at 5..7
+      const int xq = xc < 3 ? xc : 2;
+      xdel = q[2 + xq];
+      xgrd = q[5 + xq];
+    }
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
     bf16x4 s2[2];
-    // this wave's m1 rows edge-major (dW_hl in S5), read before S4 reuses the buffer
+    // this wave's m1 rows edge-major (dW_hl in S5)
     const bf16x8 m1N = chain_edge_major(s_m1, w, c, g);
     {
       f32x4 y[2], acc[2];
@@ -945,6 +998,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows ----
     float phi[2] = {0.f, 0.f};
     const bf16x8 mN = chain_edge_major(s_m, w, c, g);   // this wave's m rows edge-major (dW1_mov in S4)
+    const float gp[2] = {s_gp[sl0][c], s_gp[sl0][16 + c]};
     {
       const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * w + 4 * g);
       f32x4 gq[2], accq[2];
@@ -961,8 +1015,8 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         for (int i = 0; i < 4; ++i) {
           const YD r = silu_yd<bf16>(accq[nb][i]);
           phi[nb] += r.y * w2mv[i];
-          gq[nb][i] = gphi[nb] * w2mv[i] * r.d;
-          vw2m[i] += r.y * gphi[nb];
+          gq[nb][i] = gp[nb] * w2mv[i] * r.d;
+          vw2m[i] += r.y * gp[nb];
           vbx1[i] += gq[nb][i];
         }
         put_chain(s_gq, w, nb, l, gq[nb]);
@@ -976,7 +1030,6 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       }
     }
     __syncthreads();
-    load_pq(n_ri, n_rj);   // the next tile's gathers, consumed by its S1
 
     // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
     {
@@ -1010,6 +1063,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     float gr[2] = {0.f, 0.f};
     {
       const f32x4 wdv = *reinterpret_cast<const f32x4*>(s_wd + 16 * w + 4 * g);
+      const float r2v[2] = {s_r2[sl0][c], s_r2[sl0][16 + c]};
       f32x4 g1[2], acch[2] = {zero4(), zero4()};
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc) {
@@ -1024,10 +1078,10 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         for (int i = 0; i < 4; ++i) {
           g1[nb][i] = acch[nb][i] * d[i];
           gr[nb] += wdv[i] * g1[nb][i];
-          vwd[i] += g1[nb][i] * r2[nb];
+          vwd[i] += g1[nb][i] * r2v[nb];
         }
-        if (valid[nb])
-          *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * w + 4 * g) = pack4(g1[nb]);
+        // Gh has a row for every edge slot of the last tile (rows past E are never read)
+        *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * w + 4 * g) = pack4(g1[nb]);
       }
       const bf16x8 ga1N = edge_major(g1[0], g1[1], I);
       // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e]
@@ -1040,7 +1094,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         const int slot = 16 * ub + c;
         bf16x8 un;
 #pragma unroll
-        for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
+        for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[par][kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
         mma(acc_wu[ub], ga1N, un);
       }
     }
@@ -1050,26 +1104,22 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       gr[nb] += shfl_xor(gr[nb], 32);
       if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
     }
+    // ---- S1 of the next tile, in the same barrier interval; the ring slot of t + 2
+    if (has_next) stage1(t + G, sl1, par ^ 1, s1);
+    store_idx(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);
     __syncthreads();
-    // ---- S6: dL/ddelta = phi gx + 2 g_r delta -------------------------------
-    if (w == 0 && l < TE && base + l < E) {
+    // ---- S6: dL/ddelta = phi gx + 2 g_r delta (component 3 of the record: 0) --
+    if (w < 2) {   // Gx, like Gh, has a row for every edge slot of the last tile
       float grt = 0.f, pht = 0.f;
 #pragma unroll
       for (int ww = 0; ww < W; ++ww) {
-        grt += s_gr[ww][l];
-        pht += s_phi[ww][l];
+        grt += s_gr[ww][xe];
+        pht += s_phi[ww][xe];
       }
-      const float k2 = 2.0f * grt;
-      const float* q = a.geo + (base + l) * 8;   // delta at 2..4, grad x_i at 5..7
-      *reinterpret_cast<f32x4*>(a.Gx + (base + l) * 4) =
-          f32x4{pht * q[5] + k2 * q[2], pht * q[6] + k2 * q[3], pht * q[7] + k2 * q[4], 0.f};
+      a.Gx[(base + xe) * 4 + xc] = xc < 3 ? pht * xgrd + 2.0f * grt * xdel : 0.f;
     }
-    // Every buffer the next tile writes before its first barrier (s_m1 = s_ga2,
-    // s_u) was last read before this tile's g_r barrier: no closing barrier.
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      ri[nb] = n_ri[nb]; rj[nb] = n_rj[nb]; eid[nb] = n_eid[nb]; r2[nb] = n_r2[nb]; gphi[nb] = n_gphi[nb];
-    }
+    // s_phi and s_gr are next written after the next tile's S2 barrier, which
+    // waves 0 and 1 reach after these reads: no closing barrier.
   }
 
   // ---- this block's weight-gradient partial ---------------------------------

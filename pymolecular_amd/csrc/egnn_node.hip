@@ -98,8 +98,10 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Dgq = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
   w->Dga2 = coop ? nullptr : take(E * s.O * s.esz);
   w->Dp = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
-  w->Gh = take(E * s.H * s.esz);
-  w->Gx = (float*)take(E * 4 * sizeof(float));
+  // the cooperative kernels store Gh / Gx rows for every edge slot of the last 32-edge tile
+  const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), kTileEdges) * kTileEdges : E;
+  w->Gh = take(Er * s.H * s.esz);
+  w->Gx = (float*)take(Er * 4 * sizeof(float));
   w->R2 = coop ? nullptr : (float*)take(E * sizeof(float));
   w->geo = ((coop || wide_supported(s)) && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
   w->nblk = coop ? coop_bwd_blocks(s) : 0;
