@@ -34,29 +34,42 @@ using namespace tile;
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
+// Software-pipelined over the block's tiles: S1 of the next tile (its gathers
+// issued at the top of this tile) runs in the last barrier interval of this
+// tile, next to the coordinate sums (EGNN) or the row sums (MPNN).  Tile
+// indices pass through a ring of three LDS slots (tiles t, t + 1, t + 2) that
+// the loader wave fills one tile ahead of the gathers, so no value loaded from
+// memory is carried in registers from one tile to the next and the loads a
+// wave waits on are never followed by loads under a branch (either makes the
+// compiler wait for every outstanding load).
 template <int H, int O, int M, int W, bool EQ>
 __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
   constexpr int KH = H / 32, KO = O / 32;
   constexpr int SEGW = O + (EQ ? 4 : 0);
+  constexpr int LDW = W - 1;   // loader wave
   static_assert(BH >= 1 && BO >= 1 && BM >= 1, "slice smaller than one 16-row block");
-  __shared__ __attribute__((aligned(16))) bf16 s_m1[KH * 2 * 64 * 8];
-  __shared__ __attribute__((aligned(16))) bf16 s_m[KO * 2 * 64 * 8];
+  // m1 by tile parity: S1 of the next tile writes while S2 of this tile may still read
+  __shared__ __attribute__((aligned(16))) bf16 s_m1[2][KH * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_m[EQ ? KO * 2 * 64 * 8 : 8];
   __shared__ __attribute__((aligned(16))) float s_phi[TE][W];   // per-wave partial phi, edge-major
   __shared__ __attribute__((aligned(16))) float s_pht[TE];      // phi of each edge
-  __shared__ float s_d[TE][4];
-  // row and span of each rank, double-buffered by tile parity: the last wave
-  // reads them for the coordinate sums while the next tile's ranks are written
+  // row and span of each rank, by tile parity
   __shared__ int s_rowof[2][TE];
   __shared__ int s_rspan[2][TE];
   __shared__ uint2 s_lut[16];
+  // ring of tile indices: row, source, edge id, rows of the edges before and after the tile, (delta, r^2)
+  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][TE], s_ex[3][2];
+  __shared__ __attribute__((aligned(16))) f32x4 s_geo[3][EQ ? TE : 1];
   seg_lut_init(s_lut, threadIdx.x);
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* ef = (const bf16*)a.ef;
   const int64_t E = a.E;
   const int N = (int)a.N;
-  const bool use_eids = a.eids != nullptr && a.FE > 0;
+  const int FE = a.FE;
+  const int64_t G = gridDim.x;
+  const bool use_eids = a.eids != nullptr && FE > 0;
 
   bf16x8 wu[BH], whlT[BO][KH];
   // W1_mov[o][m] row-major in LDS; the A operands of q = W1_mov^T m are transposing reads
@@ -91,31 +104,78 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   const bf16x8 Ipq = pair_sum_chunk(c, g);
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
 
-  // row ids, sources and edge ids of a tile, loaded one tile ahead; `ex` holds
-  // the rows of the edges just before (lane 0) and just after (lane 1) the tile
-  int er[2], co[2], eid[2], ex;
-  auto load_tile = [&](int64_t t, int* per, int* pco, int* peid, int& pex) {
-    const int64_t base = t * TE;
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      const int64_t ec = e < E ? e : E - 1;
-      per[nb] = a.erow[ec];
-      pco[nb] = a.col[ec];
-      peid[nb] = use_eids ? a.eids[ec] : (int)ec;
-    }
-    const int64_t ee = l == 0 ? base - 1 : base + TE;
-    pex = a.erow[ee < 0 ? 0 : (ee < E ? ee : E - 1)];
+  // ---- ring loads: raw values of tile tt (lanes 0..31: its edges; lanes 32,
+  // 33: the edges just before and after it).  Every wave issues them, and every
+  // wave waits for them in store_idx, where the loader wave writes the slot: a
+  // load whose wait depends on the wave would leave the compiler unsure whether
+  // it is still outstanding at the next tile, and it would then wait for all.
+  const int32_t* eidp = use_eids ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
+  int ld_ri, ld_rj, ld_eid;
+  f32x4 ld_geo = zero4();
+  auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
+    const int eb = (int)(tt * TE);
+    int e = l < TE ? eb + l : (l == TE ? eb - 1 : eb + TE);
+    e = e < 0 ? 0 : (e < (int)E ? e : (int)E - 1);
+    ld_ri = a.erow[e];
+    ld_rj = a.col[e];
+    ld_eid = eidp[e];
+    if constexpr (EQ) ld_geo = *reinterpret_cast<const f32x4*>(a.geo + (int64_t)e * 4);
   };
-  // the tile's P_i / Q_j gathers, r^2 and edge-feature chunks, loaded in the
-  // middle of the previous tile from its (then current) indices
+  auto store_idx = [&](int slot, int64_t tt) {
+    asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_geo));   // the loads are complete in every wave
+    if (w == LDW) {
+      if (l < TE) {
+        const int64_t e = tt * TE + l;
+        s_ri[slot][l] = clampi(ld_ri, N);
+        s_rj[slot][l] = clampi(ld_rj, N);
+        s_eid[slot][l] = use_eids ? clampi(ld_eid, (int)E) : (int)(e < E ? e : E - 1);
+        if constexpr (EQ) s_geo[slot][l] = ld_geo;
+      } else if (l < TE + 2) {
+        s_ex[slot][l - TE] = clampi(ld_ri, N);
+      }
+    }
+  };
+  // ---- ranks of tile tt from its ring slot: edge k starts a rank when it is the
+  // tile's first edge or its row differs from that of edge k - 1; the first
+  // rank's row starts in the tile unless edge base - 1 has the same row, the
+  // last rank's row ends in it unless edge base + TE has the same row
+  struct Ranks { uint32_t mask; int nrank, nvalid; bool start_in, end_in; };
+  auto ranks = [&](int slot, int64_t tt) {
+    Ranks r;
+    const int64_t base = tt * TE;
+    r.nvalid = (int)((E - base) < TE ? (E - base) : TE);
+    const int k = l & 31;
+    const int rk = s_ri[slot][k], rp = s_ri[slot][k > 0 ? k - 1 : 0];
+    const bool nf = l < TE && k < r.nvalid && (k == 0 || rp != rk);
+    r.mask = (uint32_t)(__ballot(nf) & 0xffffffffull);
+    r.nrank = __popc(r.mask);
+    r.start_in = base == 0 || s_ex[slot][0] != s_ri[slot][0];
+    r.end_in = base + TE >= E || s_ex[slot][1] != s_ri[slot][TE - 1];
+    return r;
+  };
+  // rank of each rank-starting edge: its row and the row's edge count in the tile (wave 0)
+  auto rank_tables = [&](int slot, const Ranks& r, int par) {
+    if (w == 0 && l < TE && ((r.mask >> l) & 1u)) {
+      const uint32_t rest = l >= 31 ? 0u : (r.mask & ~((2u << l) - 1u));
+      const int end = rest ? __ffs(rest) - 1 : r.nvalid;
+      const int q = rank_of(r.mask, l);
+      s_rowof[par][q] = s_ri[slot][l];
+      s_rspan[par][q] = rank_span(l, end - l);
+    }
+  };
+  // ---- the gathers of S1 from a ring slot: edge features first (a load under
+  // the F_E > 0 branch must not follow the loads waited on), then P_i, Q_j
   bf16x4 pv[BH][2], qv[BH][2];
-  float r2[2];
   bf16x8 uf[2];
-  auto load_data = [&](int64_t t, const int* per, const int* pco, const int* peid) {
+  auto gather = [&](int slot) {
+    if (FE > 0) {   // slots past F_E read slot 0 and are dropped in S1
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb)
+        uf[nb] = load_chunk(ef + (int64_t)s_eid[slot][nb * 16 + c] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
+    }
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const uint32_t i = (uint32_t)clampi(per[nb], N), j = (uint32_t)clampi(pco[nb], N);
+      const uint32_t i = (uint32_t)s_ri[slot][nb * 16 + c], j = (uint32_t)s_rj[slot][nb * 16 + c];
 #pragma unroll
       for (int jb = 0; jb < BH; ++jb) {
         const int hb = w * BH + jb;
@@ -123,64 +183,21 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         pv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (i * (4u * H) + 2u * poff));
         qv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (j * (4u * H) + 2u * (H + poff)));
       }
-      const int64_t e = t * TE + nb * 16 + c;
-      r2[nb] = EQ ? a.geo[(e < E ? e : E - 1) * 4 + 3] : 0.f;
-      uf[nb] = 8 * g + 8 <= a.FE ? load_chunk(ef + (int64_t)clampi(peid[nb], (int)E) * a.se + 8 * g) : zero_chunk<bf16>();
     }
   };
-  if (blockIdx.x < a.ntiles) {
-    load_tile(blockIdx.x, er, co, eid, ex);
-    load_data(blockIdx.x, er, co, eid);
-  }
-
-  int par = 0;
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x, par ^= 1) {
-    const int64_t base = t * TE;
-    const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
-    int ri[2], rj[2];
-    bool valid[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      ri[nb] = clampi(er[nb], N);
-      rj[nb] = clampi(co[nb], N);
-      valid[nb] = nb * 16 + c < nvalid;
-    }
-    // the input chunk [e | r^2 hi, lo] of the tile's edges
+  // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows, into s_m1[par]
+  auto stage1 = [&](int slot, int par) {
     bf16x8 u[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      u[nb] = uf[nb];
-      if (EQ && 8 * g == a.FE) {
-        const bf16 hi = (bf16)r2[nb];
+      u[nb] = (FE > 0 && 8 * g + 8 <= FE) ? uf[nb] : zero_chunk<bf16>();
+      if (EQ && 8 * g == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
+        const float r2 = s_geo[slot][nb * 16 + c][3];
+        const bf16 hi = (bf16)r2;
         u[nb][0] = hi;
-        u[nb][1] = (bf16)(r2[nb] - (float)hi);
+        u[nb][1] = (bf16)(r2 - (float)hi);
       }
     }
-    f32x4 dgeo = zero4();   // delta of edge l, for the coordinate sums (last wave)
-    if (EQ && w == W - 1) {
-      const int64_t e = base + l;
-      dgeo = *reinterpret_cast<const f32x4*>(a.geo + (e < E ? e : E - 1) * 4);
-    }
-    // edge k starts a rank when it is the tile's first edge or its row differs
-    // from that of edge k - 1 (lane c - 1 of the same 16-lane row, or lane 15
-    // of the first block); the four 16-lane rows hold the same edges
-    const int up0 = __builtin_amdgcn_update_dpp(0, er[0], 0x111, 0xf, 0xf, false);
-    const int up1 = __builtin_amdgcn_update_dpp(0, er[1], 0x111, 0xf, 0xf, false);
-    const int last0 = __builtin_amdgcn_readlane(er[0], 15);
-    const bool nf0 = valid[0] && (c == 0 || up0 != er[0]);
-    const bool nf1 = valid[1] && ((c == 0 ? last0 : up1) != er[1]);
-    const uint32_t mask = lo16(__ballot(nf0)) | (lo16(__ballot(nf1)) << 16);
-    const int nrank = __popc(mask);
-    // the first rank's row starts in this tile unless edge base - 1 has the same
-    // row; the last rank's row ends in it unless edge base + TE has the same row
-    const bool start_in = base == 0 || __builtin_amdgcn_readlane(ex, 0) != __builtin_amdgcn_readlane(er[0], 0);
-    const bool end_in = base + TE >= E || __builtin_amdgcn_readlane(ex, 1) != __builtin_amdgcn_readlane(er[1], 15);
-    // the next tile's indices (consumed by the next iteration), issued after
-    // this tile's loads so that waiting for those does not wait for these
-    const int64_t tn = t + gridDim.x < a.ntiles ? t + gridDim.x : t;
-    load_tile(tn, er, co, eid, ex);
-
-    // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
       const int hb = w * BH + j;
@@ -192,25 +209,35 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         f32x4 x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
-        put_chain(s_m1, hb, nb, l, x);
+        put_chain(s_m1[par], hb, nb, l, x);
       }
     }
-    if (w == 0 && g == 0) {
-      const bool nf[2] = {nf0, nf1};
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const int k = nb * 16 + c;
-        if (nf[nb]) {   // rank of edge k: its row and the row's edge count in this tile
-          const uint32_t rest = k >= 31 ? 0u : (mask & ~((2u << k) - 1u));
-          const int end = rest ? __ffs(rest) - 1 : nvalid;
-          const int r = rank_of(mask, k);
-          s_rowof[par][r] = ri[nb];
-          s_rspan[par][r] = rank_span(k, end - k);
-        }
-      }
-    }
-    if (EQ && w == W - 1 && l < TE) { s_d[l][0] = dgeo[0]; s_d[l][1] = dgeo[1]; s_d[l][2] = dgeo[2]; }
-    __syncthreads();
+  };
+
+  if (blockIdx.x < a.ntiles) {
+    const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
+    load_idx(blockIdx.x);
+    store_idx(0, blockIdx.x);
+    load_idx(t1);
+    store_idx(1, t1);
+  }
+  __syncthreads();   // weights, vectors, the segment table and the first two ring slots
+  if (blockIdx.x < a.ntiles) {
+    gather(0);
+    rank_tables(0, ranks(0, blockIdx.x), 0);
+    stage1(0, 0);
+  }
+  __syncthreads();   // m1 and rank tables of the first tile
+
+  int par = 0, sl0 = 0;
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
+    const int64_t base = t * TE;
+    const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
+    load_idx(t2);    // the loader's loads come first: nothing waits on them before the ring store
+    gather(sl1);     // the next tile's gathers, consumed by its S1 at the end of this tile
+    const Ranks rk = ranks(sl0, t);
+    const int nrank = rk.nrank;
 
     // ---- S2: m = SiLU(W_hl^T m1 + b2) for the wave's O rows; row sums -----
     f32x4 mreg[BO][2];
@@ -222,7 +249,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = b2v;
 #pragma unroll
-        for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1, kc, nb, l));
+        for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1[par], kc, nb, l));
         f32x4 m;
 #pragma unroll
         for (int i = 0; i < 4; ++i) m[i] = silu_t<bf16>(acc[i]);
@@ -231,7 +258,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       }
     }
     // rank r is a whole row when it neither continues from the previous tile nor into the next
-    auto whole = [&](int r) { return (r > 0 || start_in) && (r < nrank - 1 || end_in); };
+    auto whole = [&](int r) { return (r > 0 || rk.start_in) && (r < nrank - 1 || rk.end_in); };
 #pragma unroll
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;
@@ -251,8 +278,6 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         }
       }
     }
-    // the next tile's gathers (P_i, Q_j, r^2, edge features), consumed by its S1
-    load_data(tn, er, co, eid);
     if constexpr (EQ) {
       __syncthreads();
       // ---- S3: phi = SiLU(W1mov^T m + bx1) . w2mov (partial over the wave's M rows)
@@ -293,7 +318,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
 #pragma unroll
             for (int q = 0; q < W; ++q) ph += s_phi[l][q];
           }
-          s_pht[l] = l < nvalid ? ph : 0.f;
+          s_pht[l] = l < rk.nvalid ? ph : 0.f;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
@@ -305,7 +330,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
           const int k = kappa_chain(g, s);
-          const float v = c < 3 ? s_d[k][c < 3 ? c : 0] * (s < 4 ? ph_lo[s] : ph_hi[s - 4]) : 0.f;
+          const float v = c < 3 ? s_geo[sl0][k][c < 3 ? c : 0] * (s < 4 ? ph_lo[s] : ph_hi[s - 4]) : 0.f;
           const bf16 hi = (bf16)v;
           ahi[s] = hi;
           alo[s] = (bf16)(v - (float)hi);
@@ -335,9 +360,13 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         }
       }
     }
-    // With the coordinate stages the S3 barrier orders this tile's reads of
-    // s_m1 before the next tile's writes; the rank tables are double-buffered.
-    if constexpr (!EQ) __syncthreads();
+    // ---- last barrier interval: S1 and the rank tables of the next tile (past the
+    // last tile: of a stand-in tile, never read), the ring slot of t + 2; the
+    // gathers are consumed in every wave on every path, so none is outstanding at the next tile
+    if (w == 0) rank_tables(sl1, ranks(sl1, t + G), par ^ 1);
+    stage1(sl1, par ^ 1);
+    store_idx(sl2, t2);
+    __syncthreads();
   }
 }
 
@@ -863,6 +892,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     ld_gp = q.y;
   };
   auto store_idx = [&](int slot, int64_t tt) {
+    asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_r2), "v"(ld_gp));   // complete in every wave
     if (w == LDW && l < TE) {
       const int64_t e = tt * TE + l;
       s_ri[slot][l] = clampi(ld_ri, N);
@@ -944,7 +974,6 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
     const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
     const int64_t base = t * TE;
-    const bool has_next = t + G < a.ntiles;
     bool valid[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
@@ -1105,7 +1134,9 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
     }
     // ---- S1 of the next tile, in the same barrier interval; the ring slot of t + 2
-    if (has_next) stage1(t + G, sl1, par ^ 1, s1);
+    // (past the last tile: of a stand-in tile, never read; the gathers are consumed
+    // on every path, so none is outstanding at the next tile)
+    stage1(t + G, sl1, par ^ 1, s1);
     store_idx(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);
     __syncthreads();
     // ---- S6: dL/ddelta = phi gx + 2 g_r delta (component 3 of the record: 0) --
@@ -1417,7 +1448,8 @@ int launch_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
 bool coop_supported(const LayerShape& s) {
   const bool dims = (s.H == 128 && s.O == 128 && s.M == 128) || (s.H == 64 && s.O == 32 && s.M == 32);
   // forward: F_E features + r^2 hi/lo in 32 slots; P | Q byte offsets in 32 bits
-  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32 && s.N * 4 * (int64_t)s.H < (int64_t(1) << 32);
+  return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32 && s.N * 4 * (int64_t)s.H < (int64_t(1) << 32) &&
+         s.E + kTileEdges < (int64_t(1) << 31);
 }
 
 int coop_bwd_blocks(const LayerShape& s) {
