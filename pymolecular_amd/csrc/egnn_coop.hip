@@ -1196,6 +1196,10 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
 // of half hf accumulates the columns [64 hf, 64 hf + 64) over all 32 edges.
 // Per-row sums over the edges (db2, dW_e) are per-half partials combined at the
 // end in half order.  Same stages and results as coop_bwd_kernel<..., false>.
+// Two barrier intervals per tile: [S2, S4] (each wave needs only its own s2 for
+// S4) and [S5, S1 of the next tile]; m1 and the edge-feature tile are kept by
+// tile parity.  Indices pass through an LDS ring of three tiles and the next
+// tile's gathers are issued at the top of this tile, as in coop_bwd_eq_kernel.
 template <int NU>
 __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8;
@@ -1204,15 +1208,14 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 halves (8 KB)
   static_assert(CH == NRB * 64 * 8, "chain and edge-major buffers share one size");
   // activation buffers, one array so that the final reduction can use all of it:
-  //   [0] m1 (S1 -> S2), g_a2 (S4 -> S5)   [1] g_a2 edge-major (S4 -> S5)   [2] m1 edge-major (S1 -> S5)
-  __shared__ __attribute__((aligned(16))) bf16 s_act[3 * CH];
+  //   [0] g_a2 (S4 -> S5)  [1] g_a2 edge-major (S4 -> S5)  [2 + p] m1 (S1 -> S2)  [4 + p] m1 edge-major (S1 -> S5)
+  __shared__ __attribute__((aligned(16))) bf16 s_act[6 * CH];
   __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];
-  __shared__ __attribute__((aligned(16))) bf16 s_u[NU > 0 ? TE * FEP : 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NU > 0 ? TE * FEP : 8];
   __shared__ __attribute__((aligned(16))) float s_b2[O];
-  bf16* const s_m1 = s_act;
+  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
   bf16* const s_ga2 = s_act;
   bf16* const s_ga2N = s_act + CH;
-  bf16* const s_m1N = s_act + 2 * CH;
 
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int rb = w & 7, hf = w >> 3;
@@ -1223,6 +1226,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   const int64_t E = a.E;
   const int N = (int)a.N;
   const int FE = a.FE;
+  const int64_t G = gridDim.x;
+  constexpr int LDW = 15;   // loader wave
 
   for (int q = threadIdx.x; q < O; q += 1024) s_b2[q] = a.fr.b2f[q];
   for (int q = threadIdx.x; q < NRB * KO * kFragElems / 8; q += 1024)
@@ -1242,66 +1247,97 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
 #pragma unroll
   for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
 
-  // indices of this wave's 16 edges of a tile, loaded one tile ahead of use
-  int ri, rj, eid;
-  auto load_tile = [&](int64_t t, int& pri, int& prj, int& peid) {
-    const int64_t e = t * TE + hf * 16 + c;
-    const int64_t ec = e < E ? e : E - 1;
-    pri = clampi(a.erow[ec], N);
-    prj = clampi(a.col[ec], N);
-    peid = (a.eids && FE > 0) ? clampi(a.eids[ec], (int)E) : (int)ec;
+  // ring loads (every wave issues and waits for them; the loader wave stores the slot)
+  const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
+  int ld_ri, ld_rj, ld_eid = 0;
+  auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
+    const int e0 = (int)(tt * TE) + (l & 31);
+    const int e = e0 < (int)E ? e0 : (int)E - 1;
+    ld_ri = a.erow[e];
+    ld_rj = a.col[e];
+    if constexpr (NU > 0) ld_eid = eidp[e];
   };
-  if (blockIdx.x < a.ntiles) load_tile(blockIdx.x, ri, rj, eid);
-  __syncthreads();   // weights and vectors in LDS
+  auto store_idx = [&](int slot, int64_t tt) {
+    asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid));
+    if (w == LDW && l < TE) {
+      const int e = (int)(tt * TE) + l;
+      s_ri[slot][l] = clampi(ld_ri, N);
+      s_rj[slot][l] = clampi(ld_rj, N);
+      if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, (int)E) : (e < (int)E ? e : (int)E - 1);
+    }
+  };
+  // the gathers of S1 from a ring slot: the wave's P_i, Q_j and (F_E > 0) edge-feature chunk
+  const int poff = 32 * (rb >> 1) + 8 * g + 4 * (rb & 1);
+  bf16x4 pv, qv;
+  bf16x8 ue;
+  auto gather = [&](int slot) {
+    const int k = hf * 16 + c;
+    if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
+      ue = load_chunk(ef + (int64_t)s_eid[slot][k] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
+    pv = *reinterpret_cast<const bf16x4*>(PQ + (int64_t)s_ri[slot][k] * 2 * H + poff);
+    qv = *reinterpret_cast<const bf16x4*>(PQ + (int64_t)s_rj[slot][k] * 2 * H + H + poff);
+  };
+  // ---- S1 of tile tt: m1 (chain and edge-major, buffers of parity par), s1 = SiLU'(pre1)
+  auto stage1 = [&](int64_t tt, int par, bf16x4& s1o) {
+    const bool v = tt * TE + hf * 16 + c < E;
+    const bf16x8 u = (NU > 0 && 8 * g + 8 <= FE) ? ue : zero_chunk<bf16>();
+    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, [edge][slot], for dW_e
+      *reinterpret_cast<bf16x8*>(s_u[par] + (hf * 16 + c) * FEP + 8 * g) = v ? u : zero_chunk<bf16>();
+    f32x4 acc = zero4();
+    mma(acc, wu, u);
+    const f32x4 p = unpack4(pv);
+    const f32x4 q = unpack4(qv);
+    f32x4 y, d;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+      y[i] = r.y;
+      d[i] = r.d;
+    }
+    s1o = pack4(d);
+    put_chain(s_act + (2 + par) * CH, rb, hf, l, y);
+    *reinterpret_cast<bf16x4*>(s_act + (4 + par) * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(y, I));
+  };
 
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
+  bf16x4 s1;
+  if (blockIdx.x < a.ntiles) {
+    const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
+    load_idx(blockIdx.x);
+    store_idx(0, blockIdx.x);
+    load_idx(t1);
+    store_idx(1, t1);
+  }
+  __syncthreads();   // weights, vectors and the first two ring slots in LDS
+  if (blockIdx.x < a.ntiles) {
+    gather(0);
+    stage1(blockIdx.x, 0, s1);
+  }
+  __syncthreads();   // m1 of the first tile
+
+  int par = 0, sl0 = 0;
+  for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
     const int64_t base = t * TE;
     const bool valid = base + hf * 16 + c < E;
-    // the incoming message gradient of the wave's rows (used in S4), issued early
-    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)ri * a.sgm + 16 * rb + 4 * g);
-
-    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j) -----------------------------
-    const bf16x8 u = input_chunk(ef, a.se, eid, FE, g, 0.f, false);
-    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, [edge][slot], for dW_e
-      *reinterpret_cast<bf16x8*>(s_u + (hf * 16 + c) * FEP + 8 * g) = valid ? u : zero_chunk<bf16>();
-    bf16x4 s1;
-    {
-      const int poff = 32 * (rb >> 1) + 8 * g + 4 * (rb & 1);
-      f32x4 acc = zero4();
-      mma(acc, wu, u);
-      const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri * 2 * H + poff));
-      const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj * 2 * H + H + poff));
-      f32x4 y, d;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
-        y[i] = r.y;
-        d[i] = r.d;
-      }
-      s1 = pack4(d);
-      put_chain(s_m1, rb, hf, l, y);
-      *reinterpret_cast<bf16x4*>(s_m1N + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(y, I));
-    }
-    __syncthreads();
+    // the incoming message gradient of the wave's rows (used in S4), the next tile's
+    // gathers (its S1 runs at the end of this tile), the indices of the tile after it
+    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][hf * 16 + c] * a.sgm + 16 * rb + 4 * g);
+    gather(sl1);
+    const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
+    load_idx(t2);
 
     // ---- S2: s2 = SiLU'(W_hl^T m1 + b2) -------------------------------------------
     bf16x4 s2;
     {
       f32x4 acc = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
 #pragma unroll
-      for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[kc], get_chain(s_m1, kc, hf, l));
+      for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[kc], get_chain(s_act + (2 + par) * CH, kc, hf, l));
       f32x4 d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) d[i] = silu_yd<bf16>(acc[i]).d;
       s2 = pack4(d);
     }
-    __syncthreads();
-
-    // the next tile's indices (consumed by the next iteration)
-    int n_ri, n_rj, n_eid;
-    load_tile(t + gridDim.x < a.ntiles ? t + gridDim.x : t, n_ri, n_rj, n_eid);
-
-    // ---- S4: g_a2 = gm_i SiLU'(pre2) ------------------------------------------------
+    // ---- S4: g_a2 = gm_i SiLU'(pre2), in the same interval (own rows only) --------
     {
       const f32x4 gm = valid ? unpack4(gmr) : zero4();
       const f32x4 d = unpack4(s2);
@@ -1326,9 +1362,10 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       f32x4 g1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) g1[i] = acch[i] * d[i];
-      if (valid) *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(g1);
+      // Gh has a row for every edge slot of the last tile (rows past E are never read)
+      *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(g1);
       // dW_hl rows rb, columns of half hf: sum_e m1[h][e] g_a2[o][e]
-      const bf16x8 m1N = get_norm(s_m1N, rb, l);
+      const bf16x8 m1N = get_norm(s_act + (4 + par) * CH, rb, l);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, 4 * hf + cb, l));
       // dW_e rows rb: sum over this half's edges of g_a1[h][e] e[e][slot] (the other half's slots are zero)
@@ -1343,13 +1380,15 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
           const int slot = 16 * ub + c;
           bf16x8 un;
 #pragma unroll
-          for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
+          for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[par][kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
           mma(acc_wu[ub], ga1N, un);
         }
       }
     }
-    __syncthreads();   // the next tile overwrites s_m1 = s_ga2, s_m1N and s_u
-    ri = n_ri; rj = n_rj; eid = n_eid;
+    // ---- S1 of the next tile (past the last tile: of a stand-in tile, never read), ring slot of t + 2
+    stage1(t + G, par ^ 1, s1);
+    store_idx(sl2, t2);
+    __syncthreads();
   }
 
   // ---- this block's weight-gradient partial ---------------------------------
@@ -1362,7 +1401,7 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int NUR = NU > 0 ? NU : 1;
   float* const red_v = reinterpret_cast<float*>(s_act);          // [rb][16 rows]
   float* const red_u = red_v + NRB * 16;                          // [rb][ub][lane][4]
-  static_assert((NRB * 16 + NRB * NUR * 64 * 4) * 4 <= 3 * CH * 2, "reduction exceeds the LDS buffers");
+  static_assert((NRB * 16 + NRB * NUR * 64 * 4) * 4 <= 6 * CH * 2, "reduction exceeds the LDS buffers");
   if (hf == 1) {
     if (c == 0) {
 #pragma unroll
