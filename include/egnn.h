@@ -73,18 +73,23 @@ typedef struct EgnnDims {
                             transposed, as torch.nn.Linear stores them (egnn_clean.py:24-40): w1_msg
                             (H, 2F+g+F_E), w2_msg (O, H), w1_mov (M, O).  Weight gradients are written
                             in the same layout. */
+  int32_t flags;       /* 0, or EGNN_FLAG_ACCUMULATE_GRAD_H: egnn_bwd adds its grad_h to the values already
+                          in that buffer instead of overwriting them (a layer whose h also feeds the
+                          node update passes the node update's gradient of h there) */
 } EgnnDims;
 
 #define EGNN_WEIGHTS_PACKED 0
 #define EGNN_WEIGHTS_LINEAR 1
+#define EGNN_FLAG_ACCUMULATE_GRAD_H 1
 
 /* Row strides in elements; the inner dimension is always contiguous. */
 typedef struct EgnnStrides {
-  int64_t h;           /* h and grad_h (rows 16-byte aligned)           */
+  int64_t h;           /* h (rows 16-byte aligned)                      */
   int64_t coord;       /* coord and grad_coord (>= 3)                   */
   int64_t edge;        /* edge_feat                                     */
   int64_t msg;         /* out_msg and grad_out_msg                      */
   int64_t mov;         /* out_mov and grad_out_mov (>= 3)               */
+  int64_t grad_h;      /* grad_h; 0: the same as h                      */
 } EgnnStrides;
 
 /* Version of this ABI (bumped on any signature change). */

@@ -31,16 +31,18 @@ K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_redu
 
 
 WEIGHTS_PACKED, WEIGHTS_LINEAR = 0, 1   # include/egnn.h EGNN_WEIGHTS_*
+FLAG_ACCUMULATE_GRAD_H = 1              # include/egnn.h EGNN_FLAG_ACCUMULATE_GRAD_H
 
 
 class EgnnDims(ctypes.Structure):
     _fields_ = [("N", c_int64), ("E", c_int64), ("F", c_int32), ("FE", c_int32), ("H", c_int32),
                 ("O", c_int32), ("M", c_int32), ("equivariant", c_int32), ("mean_agg", c_int32),
-                ("dtype", c_int32), ("weight_layout", c_int32)]
+                ("dtype", c_int32), ("weight_layout", c_int32), ("flags", c_int32)]
 
 
 class EgnnStrides(ctypes.Structure):
-    _fields_ = [("h", c_int64), ("coord", c_int64), ("edge", c_int64), ("msg", c_int64), ("mov", c_int64)]
+    _fields_ = [("h", c_int64), ("coord", c_int64), ("edge", c_int64), ("msg", c_int64), ("mov", c_int64),
+                ("grad_h", c_int64)]
 
 
 class EgnnNodeDims(ctypes.Structure):

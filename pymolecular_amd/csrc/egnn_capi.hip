@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 3;
+constexpr int32_t kAbiVersion = 4;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -59,6 +59,7 @@ int32_t check_strides(const LayerShape& s, const EgnnStrides* st, bool bwd) {
   if (!st) return EGNN_ERR_NULL;
   const int vec = s.bf16 ? 8 : 4;  // elements per 16 bytes
   if (st->h < s.F || (st->h * (int64_t)s.esz) % 16 != 0) return EGNN_ERR_STRIDE;
+  if (st->grad_h != 0 && (st->grad_h < s.F || (st->grad_h * (int64_t)s.esz) % 16 != 0)) return EGNN_ERR_STRIDE;
   if (st->msg < s.O || st->msg % 4 != 0) return EGNN_ERR_STRIDE;
   if (s.FE > 0 && (st->edge < s.FE || st->edge % vec != 0)) return EGNN_ERR_STRIDE;
   if (s.eq && st->coord < 3) return EGNN_ERR_STRIDE;
@@ -335,7 +336,9 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     d.M = s.N; d.N = s.F; d.K = 2 * s.H;
     d.A = w.dPQ; d.lda = 2 * s.H; d.a_bf16 = s.bf16; d.a_kc = 1; d.a_ones_row = -1;
     d.B = w.fr.wn; d.ldb = 2 * s.H; d.b_bf16 = s.bf16; d.b_nc = 0;   // B[k][f] = Wn[f][k]
-    d.C = grad_h; d.ldc = strides->h; d.c_bf16 = s.bf16;
+    const int64_t ldgh = strides->grad_h ? strides->grad_h : strides->h;
+    d.C = grad_h; d.ldc = ldgh; d.c_bf16 = s.bf16;
+    if (s.accum) { d.resid = grad_h; d.ldr = ldgh; d.resid_len = s.F; }   // each element read, then written, by one thread
     Gemm2Args g{};
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
     g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;

@@ -47,6 +47,7 @@ struct LayerShape {
   int F, FE, H, O, M, KU, NUC;   // KU = 32 * NUC (edge-input slots incl. r2 hi/lo)
   bool eq, mean, bf16;
   bool lin;                      // weights in torch.nn.Linear (out, in) layout
+  bool accum;                    // egnn_bwd adds into grad_h
   size_t esz;                    // bytes per activation element
 };
 int make_shape(const EgnnDims* d, LayerShape* s);

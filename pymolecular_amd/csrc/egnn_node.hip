@@ -24,6 +24,8 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
   if (d->weight_layout != EGNN_WEIGHTS_PACKED && d->weight_layout != EGNN_WEIGHTS_LINEAR) return EGNN_ERR_DIMS;
   s->lin = d->weight_layout == EGNN_WEIGHTS_LINEAR;
+  if (d->flags & ~EGNN_FLAG_ACCUMULATE_GRAD_H) return EGNN_ERR_DIMS;
+  s->accum = (d->flags & EGNN_FLAG_ACCUMULATE_GRAD_H) != 0;
   if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
   if (d->F < 1 || d->F > 512 || d->F % 16 != 0) return EGNN_ERR_DIMS;
   if (d->FE < 0 || d->FE > 480 || d->FE % 8 != 0) return EGNN_ERR_DIMS;

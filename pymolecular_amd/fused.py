@@ -199,12 +199,14 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
 def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                         b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
                         equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
-                        linear_weights: bool = False):
+                        linear_weights: bool = False, grad_h_into: Optional[torch.Tensor] = None):
     """Backward by recomputation.  Returns a dict of gradients (None where absent),
     weight gradients in the layout of the weights.
 
     ``node_proj``: the buffer a forward with the same inputs filled (skips the
-    per-node projection GEMM), or None.
+    per-node projection GEMM), or None.  ``grad_h_into``: an (N, F) tensor of h's
+    dtype with unit column stride; the gradient of h is added to it in place
+    (EGNN_FLAG_ACCUMULATE_GRAD_H) and it is returned as the gradient of h.
     """
     w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
@@ -217,7 +219,15 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
     if gm.stride(1) != 1 or (gm.stride(0) * gm.element_size()) % 16 or gm.data_ptr() % 16:
         gm = gm.contiguous()   # the kernels read 8- and 16-byte pieces of unit-stride rows
     gx = grad_out_mov.to(torch.float32).contiguous() if equivariant else None
-    grad_h = torch.empty_like(h)
+    if grad_h_into is not None:
+        gh = grad_h_into
+        if (gh.dtype != dt or tuple(gh.shape) != tuple(h.shape) or gh.stride(1) != 1
+                or (gh.stride(0) * gh.element_size()) % 16 or gh.data_ptr() % 16):
+            raise ValueError("grad_h_into must be an (N, F) tensor of h's dtype with 16-byte aligned unit-stride rows")
+        dims.flags = _capi.FLAG_ACCUMULATE_GRAD_H
+        grad_h = gh
+    else:
+        grad_h = torch.empty_like(h)
     grad_coord = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
     g_w1 = torch.empty_like(w1)
     g_w2 = torch.empty_like(w2)
@@ -232,7 +242,7 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
         raise ValueError(f"unsupported dimensions F={dims.F} FE={dims.FE} H={dims.H} O={dims.O} M={dims.M}")
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     strides = EgnnStrides(h=h.stride(0), coord=3, edge=edge_feat.stride(0) if edge_feat is not None else 0,
-                          msg=gm.stride(0), mov=gx.stride(0) if equivariant else 3)
+                          msg=gm.stride(0), mov=gx.stride(0) if equivariant else 3, grad_h=grad_h.stride(0))
     if equivariant and coord.stride(0) != 3:
         coord = coord[:, :3].contiguous()
     eids = None if edge_ids is None else edge_ids.to(torch.int32).contiguous()

@@ -22,6 +22,7 @@ import torch
 from torch import nn
 
 from ...fused import coo_to_csr, egnn_fused
+from ...layer_fn import GCLLayerFn
 from ...node_update import dense, node_update
 
 __all__ = ["E_GCL", "EGNN", "unsorted_segment_sum", "unsorted_segment_mean", "get_edges", "get_edges_batch"]
@@ -106,6 +107,17 @@ class E_GCL(nn.Module):
         return agg, agg_x
 
     def forward(self, h, edge_index, coord, edge_attr=None, node_attr=None, csr=None):
+        if node_attr is None:   # the whole layer as one autograd node (layer_fn.GCLLayerFn)
+            self._check_supported()
+            row, col = edge_index
+            row_ptrs, col_s, perm = csr if csr is not None else _csr_cache.get(row, col, h.shape[0])
+            e0, e2, c0, c2 = self.edge_mlp[0], self.edge_mlp[2], self.coord_mlp[0], self.coord_mlp[2]
+            n0, n2 = self.node_mlp[0], self.node_mlp[2]
+            ef = edge_attr if (edge_attr is not None and self.edges_in_d > 0) else None
+            h_out, coord = GCLLayerFn.apply(h, coord, ef, row_ptrs, col_s, perm, e0.weight, e0.bias, e2.weight,
+                                            e2.bias, c0.weight, c0.bias, c2.weight, n0.weight, n0.bias, n2.weight,
+                                            n2.bias, self.coords_agg == "mean", self.residual, True)
+            return h_out, coord, edge_attr
         agg, agg_x = self.fused_messages(h, edge_index, coord, edge_attr, csr)
         coord = coord + agg_x.to(coord.dtype)
         # node_model (:60-70): node_mlp(cat([h, agg(, node_attr)])) (+ h), as one fused node update

@@ -16,6 +16,7 @@ import torch
 from torch import nn
 
 from ...fused import egnn_fused
+from ...layer_fn import GCLLayerFn
 from ...node_update import dense, node_update
 from .egnn_clean import _csr_cache
 
@@ -47,6 +48,15 @@ class MPNN_GCL(nn.Module):
         return agg
 
     def forward(self, h, edge_index, edge_attr=None, node_attr=None, csr=None):
+        if node_attr is None:   # the whole layer as one autograd node (layer_fn.GCLLayerFn)
+            row, col = edge_index
+            row_ptrs, col_s, perm = csr if csr is not None else _csr_cache.get(row, col, h.shape[0])
+            e0, e2, n0, n2 = self.edge_mlp[0], self.edge_mlp[2], self.node_mlp[0], self.node_mlp[2]
+            ef = edge_attr if (edge_attr is not None and self.edges_in_d > 0) else None
+            h_out = GCLLayerFn.apply(h, None, ef, row_ptrs, col_s, perm, e0.weight, e0.bias, e2.weight, e2.bias,
+                                     None, None, None, n0.weight, n0.bias, n2.weight, n2.bias, False, self.residual,
+                                     False)
+            return h_out, edge_attr
         agg = self.fused_messages(h, edge_index, edge_attr, csr)
         x2 = agg if node_attr is None else torch.cat([agg, node_attr.to(agg.dtype)], dim=1)
         return node_update(h, x2, self.node_mlp[0], self.node_mlp[2], residual=self.residual), edge_attr

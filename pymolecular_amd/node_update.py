@@ -18,7 +18,7 @@ import torch
 from . import _capi
 from ._capi import EgnnNodeDims, check
 
-__all__ = ["NodeUpdateFn", "node_update", "DenseFn", "dense"]
+__all__ = ["NodeUpdateFn", "node_update", "node_update_forward", "node_update_backward", "DenseFn", "dense"]
 
 
 def _rowmajor(t: torch.Tensor) -> torch.Tensor:
@@ -54,6 +54,57 @@ def _ptr(t: Optional[torch.Tensor]):
     return None if t is None else t.data_ptr()
 
 
+def node_update_forward(x1, x2, w1, b1, w2, b2, residual=True):
+    """``egnn_node_fwd``: returns ``(out, saved)``; ``saved`` is what :func:`node_update_backward` needs."""
+    if not x1.is_cuda:
+        raise RuntimeError("x1 must be a ROCm device tensor: the node update has no CPU path")
+    dt = x1.dtype
+    x1 = _rowmajor(x1)
+    x2 = None if x2 is None else _rowmajor(x2.to(dt))
+    cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
+    w1c, b1c, w2c, b2c = cv(w1), cv(b1), cv(w2), cv(b2)
+    d = _dims(x1, x2, w1c, w2c, residual)
+    N = x1.shape[0]
+    pre = torch.empty((N, d.Hn), dtype=dt, device=x1.device)
+    act = torch.empty_like(pre)
+    out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
+    L = _capi.lib()
+    st = torch.cuda.current_stream(x1.device).cuda_stream
+    rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
+                         w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), act.data_ptr(),
+                         out.data_ptr(), out.stride(0), st)
+    check("egnn_node_fwd", rc)
+    wdt = (w1.dtype, None if b1 is None else b1.dtype, w2.dtype, None if b2 is None else b2.dtype)
+    return out, ((x1, x2, w1c, w2c, pre, act), residual, (b1 is not None, b2 is not None), wdt)
+
+
+def node_update_backward(tensors, residual, has_b, wdt, gout):
+    """``egnn_node_bwd``: returns ``(grad_x, gw1, gb1, gw2, gb2)``, ``grad_x`` the (N, K1 + K2)
+    gradient of ``[x1 | x2]`` (a fresh buffer the caller may add into)."""
+    x1, x2, w1, w2, pre, act = tensors
+    dt = x1.dtype
+    gout = _rowmajor(gout.to(dt))
+    d = _dims(x1, x2, w1, w2, residual)
+    N = x1.shape[0]
+    dev = x1.device
+    grad_x = torch.empty((N, d.K1 + d.K2), dtype=dt, device=dev)
+    gw1, gw2 = torch.empty_like(w1), torch.empty_like(w2)
+    gb1 = torch.empty((d.Hn,), dtype=dt, device=dev) if has_b[0] else None
+    gb2 = torch.empty((d.Fo,), dtype=dt, device=dev) if has_b[1] else None
+    L = _capi.lib()
+    nbytes = L.egnn_node_bwd_workspace_bytes(d)
+    ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    st = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
+                         w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), act.data_ptr(), gout.data_ptr(),
+                         gout.stride(0), grad_x.data_ptr(), gw1.data_ptr(), _ptr(gb1), gw2.data_ptr(),
+                         _ptr(gb2), ws.data_ptr(), nbytes, st)
+    check("egnn_node_bwd", rc)
+    w1dt, b1dt, w2dt, b2dt = wdt
+    return (grad_x, gw1.to(w1dt), None if gb1 is None else gb1.to(b1dt), gw2.to(w2dt),
+            None if gb2 is None else gb2.to(b2dt))
+
+
 class NodeUpdateFn(torch.autograd.Function):
     """``out = NodeUpdateFn.apply(x1, x2, w1, b1, w2, b2, residual)``.
 
@@ -64,55 +115,19 @@ class NodeUpdateFn(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, x1, x2, w1, b1, w2, b2, residual=True):
-        if not x1.is_cuda:
-            raise RuntimeError("x1 must be a ROCm device tensor: the node update has no CPU path")
-        dt = x1.dtype
-        x1 = _rowmajor(x1)
-        x2 = None if x2 is None else _rowmajor(x2.to(dt))
-        cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
-        w1c, b1c, w2c, b2c = cv(w1), cv(b1), cv(w2), cv(b2)
-        d = _dims(x1, x2, w1c, w2c, residual)
-        N = x1.shape[0]
-        pre = torch.empty((N, d.Hn), dtype=dt, device=x1.device)
-        act = torch.empty_like(pre)
-        out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
-        L = _capi.lib()
-        st = torch.cuda.current_stream(x1.device).cuda_stream
-        rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
-                             w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), act.data_ptr(),
-                             out.data_ptr(), out.stride(0), st)
-        check("egnn_node_fwd", rc)
-        ctx.save_for_backward(x1, x2, w1c, w2c, pre, act)
-        ctx.residual = residual
-        ctx.has_b = (b1 is not None, b2 is not None)
-        ctx.wdt = (w1.dtype, None if b1 is None else b1.dtype, w2.dtype, None if b2 is None else b2.dtype)
+        out, (tensors, res, has_b, wdt) = node_update_forward(x1, x2, w1, b1, w2, b2, residual)
+        ctx.save_for_backward(*tensors)
+        ctx.residual, ctx.has_b, ctx.wdt = res, has_b, wdt
+        ctx.has_x2 = x2 is not None
         return out
 
     @staticmethod
     def backward(ctx, gout):
-        x1, x2, w1, w2, pre, act = ctx.saved_tensors
-        dt = x1.dtype
-        gout = _rowmajor(gout.to(dt))
-        d = _dims(x1, x2, w1, w2, ctx.residual)
-        N = x1.shape[0]
-        dev = x1.device
-        grad_x = torch.empty((N, d.K1 + d.K2), dtype=dt, device=dev)
-        gw1, gw2 = torch.empty_like(w1), torch.empty_like(w2)
-        gb1 = torch.empty((d.Hn,), dtype=dt, device=dev) if ctx.has_b[0] else None
-        gb2 = torch.empty((d.Fo,), dtype=dt, device=dev) if ctx.has_b[1] else None
-        L = _capi.lib()
-        nbytes = L.egnn_node_bwd_workspace_bytes(d)
-        ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
-        st = torch.cuda.current_stream(dev).cuda_stream
-        rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
-                             w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), act.data_ptr(), gout.data_ptr(),
-                             gout.stride(0), grad_x.data_ptr(), gw1.data_ptr(), _ptr(gb1), gw2.data_ptr(),
-                             _ptr(gb2), ws.data_ptr(), nbytes, st)
-        check("egnn_node_bwd", rc)
-        w1dt, b1dt, w2dt, b2dt = ctx.wdt
-        g_x2 = None if x2 is None else grad_x[:, d.K1:]
-        return (grad_x[:, :d.K1], g_x2, gw1.to(w1dt), None if gb1 is None else gb1.to(b1dt), gw2.to(w2dt),
-                None if gb2 is None else gb2.to(b2dt), None)
+        tensors = ctx.saved_tensors
+        grad_x, gw1, gb1, gw2, gb2 = node_update_backward(tensors, ctx.residual, ctx.has_b, ctx.wdt, gout)
+        K1 = tensors[0].shape[1]
+        g_x2 = grad_x[:, K1:] if ctx.has_x2 else None
+        return grad_x[:, :K1], g_x2, gw1, gb1, gw2, gb2, None
 
 
 def node_update(x1: torch.Tensor, x2: Optional[torch.Tensor], lin1: torch.nn.Linear, lin2: torch.nn.Linear,

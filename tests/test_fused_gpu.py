@@ -165,3 +165,34 @@ def test_linear_weight_layout(dtype, F, FE, H, O, M, eq):
     for k, v in a["grads"].items():
         if v is not None:
             assert np.array_equal(v, b["grads"][k]), k
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("eq", [True, False])
+def test_accumulate_grad_h(dtype, eq):
+    # grad_h_into (EGNN_FLAG_ACCUMULATE_GRAD_H): the gradient of h is added to the buffer's contents,
+    # here a strided view (row stride 2F) holding random values; everything else is unchanged
+    from pymolecular_amd import fused
+    dt = DT[dtype]
+    case = molecule_case(6, 64, 0 if eq else 16, 128, 128, 128, seed=71, eq=eq, mean_agg=eq)
+    rowptr, col = _dev(case.rowptr), _dev(case.col)
+    h = _dev(case.h, dt)
+    coord = _dev(case.coord) if case.eq else None
+    ef = _dev(case.ef, dt)
+    p = {k: _dev(v, dt) for k, v in case.p.items()}
+    args = (h, coord, ef, rowptr, col, None, p["w1_msg"], p["w2_msg"], p.get("w1_mov"), p.get("w2_mov"),
+            p.get("b1"), p.get("b2"), p.get("bx1"), _dev(case.gm, dt), _dev(case.gx) if case.eq else None)
+    kw = dict(mean_agg=case.mean, equivariant=case.eq)
+    print(f"[accumulate] N={case.N} E={case.E} eq={eq} dtype={dtype}", flush=True)
+    g0 = fused.egnn_fused_backward(*args, **kw)
+    buf = torch.randn((case.N, 2 * case.F), device="cuda").to(dt)
+    base = buf[:, :case.F].float().clone()
+    g1 = fused.egnn_fused_backward(*args, **kw, grad_h_into=buf[:, :case.F])
+    torch.cuda.synchronize()
+    assert g1["h"].data_ptr() == buf.data_ptr()
+    expect = base + g0["h"].float()
+    err = (buf[:, :case.F].float() - expect).abs().max().item() / expect.abs().max().item()
+    assert err <= (1e-6 if dtype == "fp32" else 8e-3), err
+    for k in ("w1_msg", "w2_msg", "coord", "b1"):
+        if g0[k] is not None:
+            assert torch.equal(g0[k], g1[k]), k
