@@ -105,21 +105,25 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
 
   // ---- ring loads: raw values of tile tt (lanes 0..31: its edges; lanes 32,
-  // 33: the edges just before and after it).  Every wave issues them, and every
-  // wave waits for them in store_idx, where the loader wave writes the slot: a
-  // load whose wait depends on the wave would leave the compiler unsure whether
-  // it is still outstanding at the next tile, and it would then wait for all.
+  // 33: the edges just before and after it), first at the top of a tile; every
+  // wave consumes the registers in store_idx (an empty asm use), so none is
+  // still loading at the next tile as far as the compiler's memory-counter
+  // waits can tell.  The equivariant layer leaves the loads to the loader wave,
+  // the MPNN layer (one barrier interval per tile) to every wave: each measured
+  // faster at its workloads.
   const int32_t* eidp = use_eids ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
-  int ld_ri, ld_rj, ld_eid;
+  int ld_ri = 0, ld_rj = 0, ld_eid = 0;
   f32x4 ld_geo = zero4();
   auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
-    const int eb = (int)(tt * TE);
-    int e = l < TE ? eb + l : (l == TE ? eb - 1 : eb + TE);
-    e = e < 0 ? 0 : (e < (int)E ? e : (int)E - 1);
-    ld_ri = a.erow[e];
-    ld_rj = a.col[e];
-    ld_eid = eidp[e];
-    if constexpr (EQ) ld_geo = *reinterpret_cast<const f32x4*>(a.geo + (int64_t)e * 4);
+    if (!EQ || w == LDW) {
+      const int eb = (int)(tt * TE);
+      int e = l < TE ? eb + l : (l == TE ? eb - 1 : eb + TE);
+      e = e < 0 ? 0 : (e < (int)E ? e : (int)E - 1);
+      ld_ri = a.erow[e];
+      ld_rj = a.col[e];
+      ld_eid = eidp[e];
+      if constexpr (EQ) ld_geo = *reinterpret_cast<const f32x4*>(a.geo + (int64_t)e * 4);
+    }
   };
   auto store_idx = [&](int slot, int64_t tt) {
     asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_geo));   // the loads are complete in every wave
@@ -867,29 +871,32 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   f32x4 vb2 = zero4(), vbx1 = zero4(), vw2m = zero4(), vwd = zero4();
 
   // Indices and geometry of the tiles pass through a ring of three LDS slots
-  // (tiles t, t + 1, t + 2), fetched at the top of tile t for tile t + 2 and
-  // stored into the ring by the loader wave in the last barrier interval of
-  // tile t; every wave reads the values it needs from the ring.  No value loaded
-  // from memory is carried in registers from one tile to the next, and every
-  // wave issues the same global loads in the same order, without branches, so
-  // the memory-counter waits stay exact (a load under a branch, or a register
-  // loaded in one tile and read in the next, makes the compiler wait for all
-  // outstanding loads).
+  // (tiles t, t + 1, t + 2), fetched by the loader wave at the top of tile t for
+  // tile t + 2 and stored into the ring in the last barrier interval of tile t;
+  // every wave reads the values it needs from the ring.  No value loaded from
+  // memory is carried in registers from one tile to the next.  The loads that
+  // only some waves issue come first at the top of a tile and every wave
+  // consumes their registers (an empty asm use) in the same tile: then the
+  // compiler's memory-counter waits stay exact (a wave-dependent load followed
+  // by the loads a wave waits on, or a register that may still be loading at
+  // the next tile, makes it wait for all outstanding loads).
   constexpr int LDW = W - 1;   // loader wave (waves 0 and 1 do S6)
   __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
   __shared__ float s_r2[3][TE], s_gp[3][TE];
   const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
   int ld_ri = 0, ld_rj = 0, ld_eid = 0;
   float ld_r2 = 0.f, ld_gp = 0.f;
-  auto load_idx = [&](int64_t tt) {   // raw values of edge l % 32 (all waves); nothing reads them before store_idx
-    const int64_t e = tt * TE + (l & 31);
-    const int64_t ec = e < E ? e : E - 1;
-    ld_ri = a.erow[ec];
-    ld_rj = a.col[ec];
-    if constexpr (NU > 0) ld_eid = eidp[ec];
-    const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);   // (r^2, g_phi)
-    ld_r2 = q.x;
-    ld_gp = q.y;
+  auto load_idx = [&](int64_t tt) {   // raw values of edge l (loader wave); nothing reads them before store_idx
+    if (w == LDW) {
+      const int e0 = (int)(tt * TE) + (l & 31);   // edge ids below 2^31 (coop_supported)
+      const int e = e0 < (int)E ? e0 : (int)E - 1;
+      ld_ri = a.erow[e];
+      ld_rj = a.col[e];
+      if constexpr (NU > 0) ld_eid = eidp[e];
+      const float2 q = *reinterpret_cast<const float2*>(a.geo + (int64_t)e * 8);   // (r^2, g_phi)
+      ld_r2 = q.x;
+      ld_gp = q.y;
+    }
   };
   auto store_idx = [&](int slot, int64_t tt) {
     asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_r2), "v"(ld_gp));   // complete in every wave
@@ -979,22 +986,22 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
     // rows of the incoming message gradient (used in S4), the next tile's gathers
     // (its S1 runs at the end of this tile), the indices of the tile after it
-    bf16x4 gmr[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
-    gather(sl1);
     load_idx(t + 2 * G < a.ntiles ? t + 2 * G : t);
     // S6 (waves 0 and 1): lane (w, l) computes component xc of dL/ddelta of edge xe;
     // its delta and grad x_i components are loaded here
     const int xe = l & 31, xc = (w * 64 + l) >> 5;
-    float xdel, xgrd;
-    {
+    float xdel = 0.f, xgrd = 0.f;
+    if (w < 2) {
       const float* q = a.geo + (base + xe < E ? base + xe : E - 1) * 8;   // delta at 2..4, grad x_i at 5..7
       const int xq = xc < 3 ? xc : 2;
       xdel = q[2 + xq];
       xgrd = q[5 + xq];
     }
+    bf16x4 gmr[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
+    gather(sl1);
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
     bf16x4 s2[2];
@@ -1149,6 +1156,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       }
       a.Gx[(base + xe) * 4 + xc] = xc < 3 ? pht * xgrd + 2.0f * grt * xdel : 0.f;
     }
+    asm volatile("" ::"v"(xdel), "v"(xgrd));   // complete in every wave
     // s_phi and s_gr are next written after the next tile's S2 barrier, which
     // waves 0 and 1 reach after these reads: no closing barrier.
   }
