@@ -42,7 +42,9 @@ void prof_clear() {
 }
 
 // Per-node projection  P | Q = h [W_n1 | W_n2] + [b1 | 0], stored in the
-// activation dtype with each 32-feature group in chain order.
+// activation dtype: in natural feature order for the workgroup-cooperative
+// kernels (a lane gathers 8 consecutive features of one block with one 16-byte
+// load), else with each 32-feature group in chain order.
 int32_t project_nodes(const LayerShape& s, const void* h, int64_t sh, const FragSet& fr, const void* b1, void* PQ,
                       hipStream_t st) {
   Gemm2Args g{};
@@ -51,7 +53,7 @@ int32_t project_nodes(const LayerShape& s, const void* h, int64_t sh, const Frag
   g.B = fr.wn; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 1;     // [W_n1 | W_n2] (F x 2H)
   g.bias = b1; g.bias_bf16 = s.bf16; g.bias_len = b1 ? s.H : 0;
   g.C = PQ; g.ldc = 2 * s.H; g.c_bf16 = s.bf16;
-  g.perm_half = s.H;
+  g.perm_half = coop_supported(s) ? 0 : s.H;
   return hip_status(launch_gemm2(g, s.bf16, st));
 }
 

@@ -101,7 +101,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       whlT[j][kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)(w * BO + j) * KH + kc) * kFragElems + l * 8);
   }
   const bf16x8 I = ident_chunk(c, g);
-  const bf16x8 Ipq = pair_sum_chunk(c, g);
+  const bf16x8 Ipq = pq_sum_chunk(c, g);
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
 
   // ---- ring loads: raw values of tile tt (lanes 0..31: its edges; lanes 32,
@@ -169,7 +169,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   };
   // ---- the gathers of S1 from a ring slot: edge features first (a load under
   // the F_E > 0 branch must not follow the loads waited on), then P_i, Q_j
-  bf16x4 pv[BH][2], qv[BH][2];
+  bf16x8 pq[BH][2];
   bf16x8 uf[2];
   auto gather = [&](int slot) {
     if (FE > 0) {   // slots past F_E read slot 0 and are dropped in S1
@@ -181,12 +181,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     for (int nb = 0; nb < 2; ++nb) {
       const uint32_t i = (uint32_t)s_ri[slot][nb * 16 + c], j = (uint32_t)s_rj[slot][nb * 16 + c];
 #pragma unroll
-      for (int jb = 0; jb < BH; ++jb) {
-        const int hb = w * BH + jb;
-        const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
-        pv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (i * (4u * H) + 2u * poff));
-        qv[jb][nb] = *reinterpret_cast<const bf16x4*>(PQb + (j * (4u * H) + 2u * (H + poff)));
-      }
+      for (int jb = 0; jb < BH; ++jb) pq[jb][nb] = pq_gather(PQb, i, j, w * BH + jb, g, H);
     }
   };
   // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows, into s_m1[par]
@@ -209,7 +204,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
         mma(acc, wu[j], u[nb]);
-        mma(acc, Ipq, __builtin_shufflevector(pv[j][nb], qv[j][nb], 0, 1, 2, 3, 4, 5, 6, 7));   // + P_i + Q_j
+        mma(acc, Ipq, pq[j][nb]);   // + P_i + Q_j
         f32x4 x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
@@ -524,7 +519,7 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
       const int hb = w * BH + j;
-      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+      const int poff = 16 * hb + 4 * g;   // natural-order P | Q rows
       f32x4 y[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -860,6 +855,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   auto a_cols = [&](const bf16* Wl, int blk, int kc) { return lds_cols<WP>(Wl, blk, kc, c, g); };
   const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)w * kFragElems + l * 8);
   const bf16x8 I = ident_chunk(c, g);
+  const bf16x8 Ipq = pq_sum_chunk(c, g);
 
   f32x4 acc_whl[NO], acc_w1m[NM], acc_wu[NU > 0 ? NU : 1];
 #pragma unroll
@@ -911,15 +907,13 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   };
   // the gathers of S1 from ring slot `slot`: P_i and Q_j of the wave's 16 rows and
   // (F_E > 0) the edge features, two edge blocks; the input chunk is put together in S1
-  const int poff = 32 * (w >> 1) + 8 * g + 4 * (w & 1);
-  bf16x4 pv[2], qv[2];
+  bf16x8 pq[2];
   bf16x8 ue[2];
   auto gather = [&](int slot) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
       const uint32_t i = (uint32_t)s_ri[slot][nb * 16 + c], j = (uint32_t)s_rj[slot][nb * 16 + c];
-      pv[nb] = *reinterpret_cast<const bf16x4*>(PQb + (i * (4u * H) + 2u * poff));
-      qv[nb] = *reinterpret_cast<const bf16x4*>(PQb + (j * (4u * H) + 2u * (H + poff)));
+      pq[nb] = pq_gather(PQb, i, j, w, g, H);
       if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
         ue[nb] = load_chunk(ef + (int64_t)s_eid[slot][nb * 16 + c] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
     }
@@ -948,12 +942,11 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     for (int nb = 0; nb < 2; ++nb) {
       f32x4 acc = zero4();
       mma(acc, wu, u[nb]);
-      const f32x4 p = unpack4(pv[nb]);
-      const f32x4 q = unpack4(qv[nb]);
+      mma(acc, Ipq, pq[nb]);   // + P_i + Q_j
       f32x4 y, d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+        const YD r = silu_yd<bf16>(acc[i]);
         y[i] = r.y;
         d[i] = r.d;
       }
@@ -1218,7 +1211,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   // activation buffers, one array so that the final reduction can use all of it:
   //   [0] g_a2 (S4 -> S5)  [1] g_a2 edge-major (S4 -> S5)  [2 + p] m1 (S1 -> S2)  [4 + p] m1 edge-major (S1 -> S5)
   __shared__ __attribute__((aligned(16))) bf16 s_act[6 * CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];
+  __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];    // A fragments of W_hl (S5)
+  __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A fragments of W_hl^T (S2)
   __shared__ __attribute__((aligned(16))) bf16 s_u[2][NU > 0 ? TE * FEP : 8];
   __shared__ __attribute__((aligned(16))) float s_b2[O];
   __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
@@ -1240,11 +1234,9 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   for (int q = threadIdx.x; q < O; q += 1024) s_b2[q] = a.fr.b2f[q];
   for (int q = threadIdx.x; q < NRB * KO * kFragElems / 8; q += 1024)
     reinterpret_cast<bf16x8*>(s_whl)[q] = reinterpret_cast<const bf16x8*>(a.fr.hl)[q];
+  for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 1024)
+    reinterpret_cast<bf16x8*>(s_whlT)[q] = reinterpret_cast<const bf16x8*>(a.fr.hlT)[q];
   const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)rb * kFragElems + l * 8);
-  bf16x8 whlT[KH];
-#pragma unroll
-  for (int kc = 0; kc < KH; ++kc)
-    whlT[kc] = load_chunk((const bf16*)a.fr.hlT + ((int64_t)rb * KH + kc) * kFragElems + l * 8);
   const bf16x8 I = ident_chunk(c, g);
 
   // weight-gradient accumulators: dW_hl columns [64 hf, 64 hf + 64) of the wave's rows
@@ -1275,15 +1267,14 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     }
   };
   // the gathers of S1 from a ring slot: the wave's P_i, Q_j and (F_E > 0) edge-feature chunk
-  const int poff = 32 * (rb >> 1) + 8 * g + 4 * (rb & 1);
-  bf16x4 pv, qv;
+  bf16x8 pq;
   bf16x8 ue;
+  const bf16x8 Ipq = pq_sum_chunk(c, g);
   auto gather = [&](int slot) {
     const int k = hf * 16 + c;
     if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
       ue = load_chunk(ef + (int64_t)s_eid[slot][k] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
-    pv = *reinterpret_cast<const bf16x4*>(PQ + (int64_t)s_ri[slot][k] * 2 * H + poff);
-    qv = *reinterpret_cast<const bf16x4*>(PQ + (int64_t)s_rj[slot][k] * 2 * H + H + poff);
+    pq = pq_gather((const char*)PQ, (uint32_t)s_ri[slot][k], (uint32_t)s_rj[slot][k], rb, g, H);
   };
   // ---- S1 of tile tt: m1 (chain and edge-major, buffers of parity par), s1 = SiLU'(pre1)
   auto stage1 = [&](int64_t tt, int par, bf16x4& s1o) {
@@ -1293,12 +1284,11 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       *reinterpret_cast<bf16x8*>(s_u[par] + (hf * 16 + c) * FEP + 8 * g) = v ? u : zero_chunk<bf16>();
     f32x4 acc = zero4();
     mma(acc, wu, u);
-    const f32x4 p = unpack4(pv);
-    const f32x4 q = unpack4(qv);
+    mma(acc, Ipq, pq);   // + P_i + Q_j
     f32x4 y, d;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const YD r = silu_yd<bf16>(acc[i] + p[i] + q[i]);
+      const YD r = silu_yd<bf16>(acc[i]);
       y[i] = r.y;
       d[i] = r.d;
     }
@@ -1339,7 +1329,9 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     {
       f32x4 acc = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
 #pragma unroll
-      for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[kc], get_chain(s_act + (2 + par) * CH, kc, hf, l));
+      for (int kc = 0; kc < KH; ++kc)
+        mma(acc, *reinterpret_cast<const bf16x8*>(s_whlT + ((rb * KH + kc) * 64 + l) * 8),
+            get_chain(s_act + (2 + par) * CH, kc, hf, l));
       f32x4 d;
 #pragma unroll
       for (int i = 0; i < 4; ++i) d[i] = silu_yd<bf16>(acc[i]).d;

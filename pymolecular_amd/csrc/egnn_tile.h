@@ -97,6 +97,23 @@ __device__ __forceinline__ bf16x8 pair_sum_chunk(int c, int g) {
   return r;
 }
 
+// P_i + Q_j of a 16-feature block from one gathered B chunk: lanes g = 0, 1 of
+// edge column c hold P features 8g .. 8g + 7 of the block, lanes g = 2, 3 Q
+// features 8(g - 2) .. + 7 (pq_gather); A[r][k] = 1 where k is P or Q feature r.
+__device__ __forceinline__ bf16x8 pq_sum_chunk(int c, int g) {
+  bf16x8 r;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) r[s] = ((g & 1) == (c >> 3) && s == (c & 7)) ? (bf16)1.0f : (bf16)0.0f;
+  return r;
+}
+// The B chunk of pq_sum_chunk for feature block blk: one 16-byte load per lane from
+// the natural-order P | Q rows (4H bytes each) of row i (P) or source j (Q).
+__device__ __forceinline__ bf16x8 pq_gather(const char* PQb, uint32_t i, uint32_t j, int blk, int g, int H) {
+  const uint32_t row = g < 2 ? i : j;
+  const uint32_t off = 2u * (uint32_t)((g < 2 ? 0 : H) + 16 * blk + 8 * (g & 1));
+  return *reinterpret_cast<const bf16x8*>(PQb + (row * (4u * (uint32_t)H) + off));
+}
+
 // 16 bf16x4 patterns: element s of entry n is 1.0 when bit s of n is set
 __device__ __forceinline__ void seg_lut_init(uint2* lut, int tid) {
   if (tid < 16) {
