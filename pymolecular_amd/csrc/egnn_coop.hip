@@ -1088,6 +1088,13 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     for (int cb = 0; cb < NM; ++cb) mma(acc_w1m[cb], mN, get_norm(s_gqN, cb, l));
     __syncthreads();
 
+    // ---- S1 of the next tile (past the last tile: of a stand-in tile, never
+    // read; the gathers are consumed on every path, so none is outstanding at
+    // the next tile).  With edge features it goes first in the interval, so
+    // that its SiLU work interleaves with S5's products; without, after S5
+    // (each order measured faster for its case).
+    bf16x4 s1n[2];
+    if constexpr (NU > 0) stage1(t + G, sl1, par ^ 1, s1n);
     // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1), the wave's H rows --------------
     float gr[2] = {0.f, 0.f};
     {
@@ -1133,11 +1140,11 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       gr[nb] += shfl_xor(gr[nb], 32);
       if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
     }
-    // ---- S1 of the next tile, in the same barrier interval; the ring slot of t + 2
-    // (past the last tile: of a stand-in tile, never read; the gathers are consumed
-    // on every path, so none is outstanding at the next tile)
-    stage1(t + G, sl1, par ^ 1, s1);
+    if constexpr (NU == 0) stage1(t + G, sl1, par ^ 1, s1n);
+    // the ring slot of t + 2
     store_idx(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);
+    s1[0] = s1n[0];
+    s1[1] = s1n[1];
     __syncthreads();
     // ---- S6: dL/ddelta = phi gx + 2 g_r delta (component 3 of the record: 0) --
     if (w < 2) {   // Gx, like Gh, has a row for every edge slot of the last tile
