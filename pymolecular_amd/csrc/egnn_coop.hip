@@ -1446,7 +1446,9 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
 template <int H, int O, int M, int W, bool EQ>
 int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (a.ntiles > 0) {
-    const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * 4);
+    // one resident round: 4 waves per SIMD (the launch bound), 16 waves per CU, on 256 CUs; a
+    // second round would repeat the weight prologue of every block
+    const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * (16 / W));
     hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ>), dim3(blocks), dim3(W * 64), 0, st, a);
   }
   return (int)hipGetLastError();

@@ -231,6 +231,10 @@ __global__ __launch_bounds__(256) void fwd_edge_kernel(FwdArgs a) {
 }
 
 // Rows that are empty or cross a tile: sum the tile partials in tile order.
+// One wave per row, 4 columns per lane (SEGW is a multiple of 4, carry rows are
+// 16-byte aligned); the partials of 8 tiles are loaded before they are added,
+// so a row that spans many tiles waits on one load latency per 8 tiles.  The
+// additions run in tile order, element by element.
 template <typename T, bool EQ>
 __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
   const int SEGW = O + (EQ ? 4 : 0);
@@ -240,18 +244,36 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
   for (int64_t f = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); f < nfix; f += nw) {
     const int r = a.fix_rows[f];
     const int rs = a.rowptr[r], re = a.rowptr[r + 1];
-    for (int colx = l; colx < SEGW; colx += 64) {
-      float acc = 0.f;
-      if (re > rs) {
-        const int64_t t0 = rs / kTileEdges, t1 = (re - 1) / kTileEdges;
-        const int slot0 = (a.erow[t0 * kTileEdges] == r) ? 0 : 1;
-        for (int64_t tt = t0; tt <= t1; ++tt) acc += a.carry[(tt * 2 + (tt == t0 ? slot0 : 0)) * SEGW + colx];
+    int64_t t0 = 0, tn = 0;   // tiles t0 .. t0 + tn - 1; tile t0 holds the row in slot 0 or 1, later tiles in slot 0
+    int slot0 = 0;
+    if (re > rs) {
+      t0 = rs / kTileEdges;
+      tn = (re - 1) / kTileEdges - t0 + 1;
+      slot0 = (a.erow[t0 * kTileEdges] == r) ? 0 : 1;
+    }
+    for (int c4 = 4 * l; c4 < SEGW; c4 += 256) {
+      const float* cp = a.carry + t0 * 2 * SEGW + c4;   // tile t0 + k, slot 0: cp + 2 k SEGW
+      f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+      int64_t k = 0;
+      for (; k + 8 <= tn; k += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = load4_f32(cp + ((k + u) * 2 + (k + u == 0 ? slot0 : 0)) * SEGW);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += v[u];
       }
-      if (colx < O) {
-        ((T*)a.out_msg)[(int64_t)r * a.smsg + colx] = from_f32<T>(acc);
-      } else if (EQ && colx < O + 3) {
-        if (a.mean && re > rs) acc /= (float)(re - rs);
-        a.out_mov[(int64_t)r * a.smov + (colx - O)] = acc;
+      for (; k < tn; ++k) acc += load4_f32(cp + (k * 2 + (k == 0 ? slot0 : 0)) * SEGW);
+      if (c4 < O) {
+        T* o = (T*)a.out_msg + (int64_t)r * a.smsg + c4;
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<bf16x4*>(o) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+        } else {
+          *reinterpret_cast<f32x4*>(o) = acc;
+        }
+      } else if (EQ) {   // c4 == O: the three coordinate sums
+        float* o = a.out_mov + (int64_t)r * a.smov;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) o[i] = (a.mean && re > rs) ? acc[i] / (float)(re - rs) : acc[i];
       }
     }
   }
