@@ -73,14 +73,20 @@ typedef struct EgnnDims {
                             transposed, as torch.nn.Linear stores them (egnn_clean.py:24-40): w1_msg
                             (H, 2F+g+F_E), w2_msg (O, H), w1_mov (M, O).  Weight gradients are written
                             in the same layout. */
-  int32_t flags;       /* 0, or EGNN_FLAG_ACCUMULATE_GRAD_H: egnn_bwd adds its grad_h to the values already
-                          in that buffer instead of overwriting them (a layer whose h also feeds the
-                          node update passes the node update's gradient of h there) */
+  int32_t flags;       /* 0, or an OR of:
+                          EGNN_FLAG_ACCUMULATE_GRAD_H: egnn_bwd adds its grad_h to the values already in
+                          that buffer instead of overwriting them (a layer whose h also feeds the node
+                          update passes the node update's gradient of h there);
+                          EGNN_FLAG_COORD_RESIDUAL (equivariant only): the layer's coordinate output is
+                          x' = x + agg_x (egnn_clean.py:97, coord += agg): egnn_fwd writes coord + agg_x
+                          into out_mov, and egnn_bwd writes grad_out_mov + (d agg_x / d coord)^T
+                          grad_out_mov into grad_coord, the whole gradient of x' with respect to x */
 } EgnnDims;
 
 #define EGNN_WEIGHTS_PACKED 0
 #define EGNN_WEIGHTS_LINEAR 1
 #define EGNN_FLAG_ACCUMULATE_GRAD_H 1
+#define EGNN_FLAG_COORD_RESIDUAL 2
 
 /* Row strides in elements; the inner dimension is always contiguous. */
 typedef struct EgnnStrides {

@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 4;
+constexpr int32_t kAbiVersion = 5;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -167,6 +167,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.rowptr = rowptr; a.col = col; a.eids = edge_ids; a.erow = v.erow;
   a.fr = w.fr;
   a.w1m = w1_mov; a.lin = s.lin;
+  a.coord_res = s.coord_res ? 1 : 0;
   a.out_msg = out_msg; a.smsg = strides->msg;
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;
@@ -250,8 +251,9 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   float* gcoord = s.eq ? grad_coord : nullptr;
   {
     ProfScope ps(EGNN_K_NODE_REDUCE, st);
+    const float* gres = s.coord_res ? grad_out_mov : nullptr;
     if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
-                                          strides->coord, st))) != EGNN_OK)
+                                          strides->coord, gres, strides->mov, st))) != EGNN_OK)
       return rc;
   }
 

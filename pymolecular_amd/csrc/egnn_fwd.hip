@@ -235,12 +235,32 @@ __global__ __launch_bounds__(256) void fwd_edge_kernel(FwdArgs a) {
 // 16-byte aligned); the partials of 8 tiles are loaded before they are added,
 // so a row that spans many tiles waits on one load latency per 8 tiles.  The
 // additions run in tile order, element by element.
+// With coord_res the coordinate output is x' = x + agg_x for every row: the
+// rows above get x added to their sums here, and the whole rows (one tile
+// each, the predicate of the schedule's fix-row flags) get x added to the
+// aggregate the edge kernel stored, one thread per row, by the blocks from
+// nfb on; the two sets are disjoint, so no output is touched twice.
 template <typename T, bool EQ>
-__global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
+__global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nfb) {
   const int SEGW = O + (EQ ? 4 : 0);
   const int l = threadIdx.x & 63;
+  if (EQ && (int)blockIdx.x >= nfb) {
+    const int64_t nrb = (int64_t)gridDim.x - nfb;
+    for (int64_t r = (int64_t)(blockIdx.x - nfb) * 256 + threadIdx.x; r < a.N; r += nrb * 256) {
+      const int rs = a.rowptr[r], re = a.rowptr[r + 1];
+      if (re > rs && rs / kTileEdges == (re - 1) / kTileEdges) {
+        float* o = a.out_mov + r * a.smov;
+        const float* x = a.coord + r * a.sc;
+        const float x0 = x[0], x1 = x[1], x2 = x[2], v0 = o[0], v1 = o[1], v2 = o[2];
+        o[0] = x0 + v0;
+        o[1] = x1 + v1;
+        o[2] = x2 + v2;
+      }
+    }
+    return;
+  }
   const int nfix = *a.n_fix;
-  const int64_t nw = (int64_t)gridDim.x * 4;
+  const int64_t nw = (int64_t)nfb * 4;
   for (int64_t f = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); f < nfix; f += nw) {
     const int r = a.fix_rows[f];
     const int rs = a.rowptr[r], re = a.rowptr[r + 1];
@@ -273,7 +293,10 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O) {
       } else if (EQ) {   // c4 == O: the three coordinate sums
         float* o = a.out_mov + (int64_t)r * a.smov;
 #pragma unroll
-        for (int i = 0; i < 3; ++i) o[i] = (a.mean && re > rs) ? acc[i] / (float)(re - rs) : acc[i];
+        for (int i = 0; i < 3; ++i) {
+          const float v = (a.mean && re > rs) ? acc[i] / (float)(re - rs) : acc[i];
+          o[i] = a.coord_res ? a.coord[(int64_t)r * a.sc + i] + v : v;   // x' = x + agg_x
+        }
       }
     }
   }
@@ -290,8 +313,9 @@ static int launch_fwd_t(const FwdArgs& a, int part, hipStream_t st) {
     }
     return (int)hipGetLastError();
   }
-  int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 2048);
-  hipLaunchKernelGGL((fwd_fixup_kernel<T, EQ>), dim3(fb), dim3(256), 0, st, a, O);
+  const int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 2048);
+  const int rb = EQ && a.coord_res ? (int)std::min<int64_t>(cdiv(a.N, 256), 1024) : 0;   // whole-row x + agg_x
+  hipLaunchKernelGGL((fwd_fixup_kernel<T, EQ>), dim3(fb + rb), dim3(256), 0, st, a, O, fb);
   return (int)hipGetLastError();
 }
 

@@ -48,6 +48,7 @@ struct LayerShape {
   bool eq, mean, bf16;
   bool lin;                      // weights in torch.nn.Linear (out, in) layout
   bool accum;                    // egnn_bwd adds into grad_h
+  bool coord_res;                // coordinate output x + agg_x, its gradient includes grad_out_mov
   size_t esz;                    // bytes per activation element
 };
 int make_shape(const EgnnDims* d, LayerShape* s);
@@ -170,6 +171,7 @@ struct FwdArgs {
   const int32_t* fix_rows; const int32_t* n_fix;
   const void* w1m;   // W1_mov: (O x M) row-major, or (M x O) with lin
   int lin;           // weights in torch.nn.Linear (out, in) layout
+  int coord_res;     // out_mov = coord + the aggregated update
 };
 // part 0: edge tiles, part 1: split/empty-row fix-up
 int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
@@ -214,7 +216,7 @@ int bwd_tile_edges(const LayerShape& s);
 // grad_coord = sum_row Gx - sum_csc Gx
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
                        const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord,
-                       int64_t sgc, hipStream_t st);
+                       int64_t sgc, const float* gres, int64_t sgr, hipStream_t st);   // gres: added to gcoord
 // out[l] = sum_b part[b][l] for l < L (fixed order)
 int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st);
 // scatter the fp32 weight-gradient sums into the caller's tensors

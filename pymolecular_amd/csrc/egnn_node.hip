@@ -24,8 +24,10 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
   if (d->weight_layout != EGNN_WEIGHTS_PACKED && d->weight_layout != EGNN_WEIGHTS_LINEAR) return EGNN_ERR_DIMS;
   s->lin = d->weight_layout == EGNN_WEIGHTS_LINEAR;
-  if (d->flags & ~EGNN_FLAG_ACCUMULATE_GRAD_H) return EGNN_ERR_DIMS;
+  if (d->flags & ~(EGNN_FLAG_ACCUMULATE_GRAD_H | EGNN_FLAG_COORD_RESIDUAL)) return EGNN_ERR_DIMS;
   s->accum = (d->flags & EGNN_FLAG_ACCUMULATE_GRAD_H) != 0;
+  s->coord_res = (d->flags & EGNN_FLAG_COORD_RESIDUAL) != 0;
+  if (s->coord_res && !s->eq) return EGNN_ERR_DIMS;   // no coordinates in the MPNN layer
   if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
   if (d->F < 1 || d->F > 512 || d->F % 16 != 0) return EGNN_ERR_DIMS;
   if (d->FE < 0 || d->FE > 480 || d->FE % 8 != 0) return EGNN_ERR_DIMS;
@@ -1161,7 +1163,9 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ rowptr,
                                                           const int32_t* __restrict__ csc_ptr,
                                                           const int32_t* __restrict__ csc_eid, T* __restrict__ dPQ,
-                                                          float* __restrict__ gcoord, int64_t sgc, int64_t N, int eq) {
+                                                          float* __restrict__ gcoord, int64_t sgc,
+                                                          const float* __restrict__ gres, int64_t sgr, int64_t N,
+                                                          int eq) {
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
   constexpr int EPW = 64 / LPE;                // edges per wave-wide load
@@ -1218,7 +1222,7 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
       }
       ax += shfl_xor(ax, off);
     }
-    if (eq && l < 3) gcoord[n * sgc + l] = ax;
+    if (eq && l < 3) gcoord[n * sgc + l] = gres ? gres[n * sgr + l] + ax : ax;   // + the residual path of x'
     if (sub == 0) {   // one 16-byte store per half
       T* out = dPQ + n * 2 * H + q * VPL;
       if constexpr (sizeof(T) == 2) {
@@ -1237,10 +1241,10 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
 
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
                        const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord, int64_t sgc,
-                       hipStream_t st) {
+                       const float* gres, int64_t sgr, hipStream_t st) {
   int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
   int eq = s.eq ? 1 : 0;
-#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, s.N, eq)
+#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq)
   if (s.bf16) {
     if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
   } else {

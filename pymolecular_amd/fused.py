@@ -163,8 +163,11 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
 def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
                        w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
-                       linear_weights: bool = False):
+                       linear_weights: bool = False, coord_residual: bool = False):
     """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``.
+
+    ``coord_residual`` (equivariant only, EGNN_FLAG_COORD_RESIDUAL): ``out_mov`` is
+    the updated coordinate ``coord + agg_x`` instead of ``agg_x``.
 
     ``node_proj`` (uint8 device buffer of ``egnn_node_proj_bytes``): when given,
     receives the per-node projections so that a following backward can reuse them.
@@ -174,6 +177,8 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
     dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
+    if coord_residual and equivariant:
+        dims.flags |= _capi.FLAG_COORD_RESIDUAL
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev = h.device
     N, O = h.shape[0], dims.O
@@ -199,7 +204,8 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
 def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov, w2_mov,
                         b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
                         equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
-                        linear_weights: bool = False, grad_h_into: Optional[torch.Tensor] = None):
+                        linear_weights: bool = False, grad_h_into: Optional[torch.Tensor] = None,
+                        coord_residual: bool = False):
     """Backward by recomputation.  Returns a dict of gradients (None where absent),
     weight gradients in the layout of the weights.
 
@@ -207,6 +213,9 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
     per-node projection GEMM), or None.  ``grad_h_into``: an (N, F) tensor of h's
     dtype with unit column stride; the gradient of h is added to it in place
     (EGNN_FLAG_ACCUMULATE_GRAD_H) and it is returned as the gradient of h.
+    ``coord_residual`` (equivariant only, EGNN_FLAG_COORD_RESIDUAL): the coordinate
+    output was ``coord + agg_x``, so the returned gradient of coord includes
+    ``grad_out_mov`` (the residual path).
     """
     w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
@@ -224,10 +233,12 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
         if (gh.dtype != dt or tuple(gh.shape) != tuple(h.shape) or gh.stride(1) != 1
                 or (gh.stride(0) * gh.element_size()) % 16 or gh.data_ptr() % 16):
             raise ValueError("grad_h_into must be an (N, F) tensor of h's dtype with 16-byte aligned unit-stride rows")
-        dims.flags = _capi.FLAG_ACCUMULATE_GRAD_H
+        dims.flags |= _capi.FLAG_ACCUMULATE_GRAD_H
         grad_h = gh
     else:
         grad_h = torch.empty_like(h)
+    if coord_residual and equivariant:
+        dims.flags |= _capi.FLAG_COORD_RESIDUAL
     grad_coord = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
     g_w1 = torch.empty_like(w1)
     g_w2 = torch.empty_like(w2)

@@ -11,7 +11,9 @@ update, so autograd adds the two gradients of h with an extra elementwise
 kernel.  Here the backward runs the node update's backward first and then the
 fused backward with ``EGNN_FLAG_ACCUMULATE_GRAD_H``, which adds the message
 path's gradient of h into the node update's buffer inside the dh product's
-epilogue.  The MPNN layer (``equivariant = False``) is the same without the
+epilogue.  ``EGNN_FLAG_COORD_RESIDUAL`` does the same for the coordinates: the
+forward writes ``x + agg_x`` and the backward's coordinate gradient includes
+the residual path, so neither needs an elementwise add.  The MPNN layer (``equivariant = False``) is the same without the
 coordinate path.
 """
 from __future__ import annotations
@@ -39,9 +41,9 @@ class GCLLayerFn(torch.autograd.Function):
         hp, coord_p, ef, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
             h, coord, edge_attr, e0w, e2w, c0w, c2w, e0b, e2b, c0b, equivariant)
         pq = _node_proj_buffer(hp, ef, col, w1, w2, w1m, equivariant, mean_agg, True)
-        agg, agg_x = egnn_fused_forward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1,
+        agg, x_new = egnn_fused_forward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1,
                                         mean_agg=mean_agg, equivariant=equivariant, node_proj=pq,
-                                        linear_weights=True)
+                                        linear_weights=True, coord_residual=True)
         out, (nt, res, has_b, wdt) = node_update_forward(hp, agg, n0w, n0b, n2w, n2b, residual)
         ctx.save_for_backward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1, pq, *nt)
         ctx.node = (res, has_b, wdt)
@@ -49,7 +51,7 @@ class GCLLayerFn(torch.autograd.Function):
         ctx.coord_dtype = None if coord is None else coord.dtype
         if not equivariant:
             return out
-        return out, coord + agg_x.to(coord.dtype)
+        return out, x_new.to(coord.dtype)
 
     @staticmethod
     def backward(ctx, g_out, g_coord=None):
@@ -68,10 +70,9 @@ class GCLLayerFn(torch.autograd.Function):
             g_coord = torch.zeros((N, 3), dtype=torch.float32, device=hp.device)
         g = egnn_fused_backward(hp, coord, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1, g_agg,
                                 g_coord.to(torch.float32) if eq else None, mean_agg=ctx.mean_agg,
-                                equivariant=eq, node_proj=pq, linear_weights=True, grad_h_into=g_h)
-        gc = None
-        if eq:
-            gc = (g_coord + g["coord"].to(g_coord.dtype)).to(ctx.coord_dtype)
+                                equivariant=eq, node_proj=pq, linear_weights=True, grad_h_into=g_h,
+                                coord_residual=True)
+        gc = g["coord"].to(ctx.coord_dtype) if eq else None   # includes g_coord (EGNN_FLAG_COORD_RESIDUAL)
         wg = [g[k] for k in ("w1_msg", "w2_msg", "w1_mov", "w2_mov", "b1", "b2", "bx1")]
         e0w_g, e2w_g, c0w_g, c2w_g, e0b_g, e2b_g, c0b_g = [
             None if (t is None or shp is None) else t.reshape(shp) for t, shp in zip(wg, ctx.shapes)]

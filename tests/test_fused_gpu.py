@@ -196,3 +196,36 @@ def test_accumulate_grad_h(dtype, eq):
     for k in ("w1_msg", "w2_msg", "coord", "b1"):
         if g0[k] is not None:
             assert torch.equal(g0[k], g1[k]), k
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("shape", [(0, 128, 128, 128), (16, 128, 128, 128), (32, 256, 256, 256), (8, 64, 32, 32)])
+def test_coord_residual(dtype, shape):
+    # EGNN_FLAG_COORD_RESIDUAL: out_mov = coord + agg_x and grad_coord = grad_out_mov + the message
+    # path's gradient, on every forward path (cooperative, wide, one wave per tile), with mean
+    # aggregation, empty rows and rows across many tiles (rows the fix-up writes)
+    from pymolecular_amd import fused
+    FE, H, O, M = shape
+    dt = DT[dtype]
+    degs = np.array([0, 1, 100, 0, 3, 31, 32, 33, 0, 64, 2, 200, 5, 0, 17] * 4)
+    rowptr_np, col_np = random_csr(len(degs), degs, seed=8)
+    case = Case(rowptr_np, col_np, 64, FE, H, O, M, seed=83, mean_agg=True)
+    rowptr, col = _dev(case.rowptr), _dev(case.col)
+    h, coord, ef = _dev(case.h, dt), _dev(case.coord), _dev(case.ef, dt)
+    p = {k: _dev(v, dt) for k, v in case.p.items()}
+    fa = (h, coord, ef, rowptr, col, None, p["w1_msg"], p["w2_msg"], p["w1_mov"], p["w2_mov"], p.get("b1"),
+          p.get("b2"), p.get("bx1"))
+    kw = dict(mean_agg=True, equivariant=True)
+    print(f"[coord_residual] N={case.N} E={case.E} shape={shape} dtype={dtype}", flush=True)
+    _, mov0 = fused.egnn_fused_forward(*fa, **kw)
+    _, mov1 = fused.egnn_fused_forward(*fa, **kw, coord_residual=True)
+    gx = _dev(case.gx)
+    g0 = fused.egnn_fused_backward(*fa, _dev(case.gm, dt), gx, **kw)
+    g1 = fused.egnn_fused_backward(*fa, _dev(case.gm, dt), gx, **kw, coord_residual=True)
+    torch.cuda.synchronize()
+    # one fp32 add of the same two operands in each direction: equal to the last bit
+    assert torch.equal(mov1, coord + mov0)
+    assert torch.equal(g1["coord"], g0["coord"] + gx)
+    for k in ("h", "w1_msg", "w2_msg", "w1_mov", "b1"):
+        if g0[k] is not None:
+            assert torch.equal(g0[k], g1[k]), k
