@@ -769,6 +769,15 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
   gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
+// 1D grid with the n tiles of one row block adjacent (they share the A rows,
+// read once from memory while they are in L2), then the row blocks, then the split
+template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
+__global__ __launch_bounds__(256) void gemm_bf16_nfirst_kernel(Gemm2Args g, int gx, int gy) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[GemmBf16Smem<A_KC, B_NC, BM, BN, BK, NBUF>::n];
+  const int b = (int)blockIdx.x;
+  gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, (b / gy) % gx, b % gy, b / (gx * gy), smem);
+}
+
 // Two independent products on 32 x 64 tiles in one launch: blocks [0, n1) are
 // the tiles of g1 (x fastest, then y, then the split), the rest those of g2.
 template <bool AK1, bool BN1, bool AK2, bool BN2>
@@ -1092,6 +1101,18 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   if (bf16_tiled_ok(g, compute_bf16)) {
     const bool big = bf16_big_tiles(g);
     const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
+    if (big && !narrow && g.ksplit <= 0 && g.K <= 128 && g.a_kc) {
+      // node products with K <= 128 on large grids: 64 x 128 tiles in 32-deep k stages (a smaller LDS
+      // footprint, more blocks in flight), n tiles of a row block adjacent; measured faster than the
+      // 128 x 128 tiles for these shapes at 2M rows (K = 256 keeps the 128 x 128 tiles)
+      const int64_t gx = cdiv(g.M, 64), gy = cdiv(g.N, 128);
+      if (gx * gy < (int64_t(1) << 31)) {
+        const dim3 g1((unsigned)(gx * gy));
+        if (g.b_nc) hipLaunchKernelGGL((gemm_bf16_nfirst_kernel<true, true, 64, 128, 32, 2>), g1, dim3(256), 0, st, g, (int)gx, (int)gy);
+        else hipLaunchKernelGGL((gemm_bf16_nfirst_kernel<true, false, 64, 128, 32, 2>), g1, dim3(256), 0, st, g, (int)gx, (int)gy);
+        return (int)hipGetLastError();
+      }
+    }
     const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
 #define GB_LAUNCH(AK, BNC)                                                                         \
     do {                                                                                           \

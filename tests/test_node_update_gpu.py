@@ -56,6 +56,12 @@ def test_node_update_matches_reference(dtype, tol, N, K1, K2, Hn, Fo, residual, 
     assert not bad, bad
 
 
+def test_node_update_large_bf16():
+    # 300k nodes: the large-grid tile shapes (128 x 128 for K = 256, 64 x 128 in 32-deep stages for
+    # K = 128, n tiles of a row block adjacent) and long split-K slices
+    test_node_update_matches_reference(torch.bfloat16, 2e-2, 300000, 128, 128, 128, 128, True, True)
+
+
 def test_node_update_deterministic_and_empty():
     from pymolecular_amd.node_update import NodeUpdateFn
     x1, x2, w1, b1, w2, b2, gout = _case(20000, 128, 128, 128, 128, 9)
