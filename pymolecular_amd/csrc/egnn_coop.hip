@@ -47,7 +47,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
   constexpr int KH = H / 32, KO = O / 32;
   constexpr int SEGW = O + (EQ ? 4 : 0);
-  constexpr int LDW = W - 1;   // loader wave
+  constexpr int LDW = EQ && W > 2 ? W - 2 : W - 1;   // loader wave (not the coordinate-sum wave W - 1)
   static_assert(BH >= 1 && BO >= 1 && BM >= 1, "slice smaller than one 16-row block");
   // m1 by tile parity: S1 of the next tile writes while S2 of this tile may still read
   __shared__ __attribute__((aligned(16))) bf16 s_m1[2][KH * 2 * 64 * 8];
