@@ -139,33 +139,10 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       }
     }
   };
-  // ---- ranks of tile tt from its ring slot: edge k starts a rank when it is the
-  // tile's first edge or its row differs from that of edge k - 1; the first
-  // rank's row starts in the tile unless edge base - 1 has the same row, the
-  // last rank's row ends in it unless edge base + TE has the same row
-  struct Ranks { uint32_t mask; int nrank, nvalid; bool start_in, end_in; };
-  auto ranks = [&](int slot, int64_t tt) {
-    Ranks r;
-    const int64_t base = tt * TE;
-    r.nvalid = (int)((E - base) < TE ? (E - base) : TE);
-    const int k = l & 31;
-    const int rk = s_ri[slot][k], rp = s_ri[slot][k > 0 ? k - 1 : 0];
-    const bool nf = l < TE && k < r.nvalid && (k == 0 || rp != rk);
-    r.mask = (uint32_t)(__ballot(nf) & 0xffffffffull);
-    r.nrank = __popc(r.mask);
-    r.start_in = base == 0 || s_ex[slot][0] != s_ri[slot][0];
-    r.end_in = base + TE >= E || s_ex[slot][1] != s_ri[slot][TE - 1];
-    return r;
-  };
-  // rank of each rank-starting edge: its row and the row's edge count in the tile (wave 0)
-  auto rank_tables = [&](int slot, const Ranks& r, int par) {
-    if (w == 0 && l < TE && ((r.mask >> l) & 1u)) {
-      const uint32_t rest = l >= 31 ? 0u : (r.mask & ~((2u << l) - 1u));
-      const int end = rest ? __ffs(rest) - 1 : r.nvalid;
-      const int q = rank_of(r.mask, l);
-      s_rowof[par][q] = s_ri[slot][l];
-      s_rspan[par][q] = rank_span(l, end - l);
-    }
+  // ---- ranks of tile tt from its ring slot (tile_ranks), and the rank tables of one tile (wave 0)
+  auto ranks = [&](int slot, int64_t tt) { return tile_ranks(s_ri[slot], s_ex[slot], tt * TE, E, l); };
+  auto rank_tables = [&](int slot, const TileRanks& r, int par) {
+    if (w == 0) tile_rank_tables(s_ri[slot], r, l, s_rowof[par], s_rspan[par]);
   };
   // ---- the gathers of S1 from a ring slot: edge features first (a load under
   // the F_E > 0 branch must not follow the loads waited on), then P_i, Q_j
@@ -235,7 +212,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
     load_idx(t2);    // the loader's loads come first: nothing waits on them before the ring store
     gather(sl1);     // the next tile's gathers, consumed by its S1 at the end of this tile
-    const Ranks rk = ranks(sl0, t);
+    const TileRanks rk = ranks(sl0, t);
     const int nrank = rk.nrank;
 
     // ---- S2: m = SiLU(W_hl^T m1 + b2) for the wave's O rows; row sums -----
@@ -256,8 +233,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         if (EQ) put_chain(s_m, ob, nb, l, m);
       }
     }
-    // rank r is a whole row when it neither continues from the previous tile nor into the next
-    auto whole = [&](int r) { return (r > 0 || rk.start_in) && (r < nrank - 1 || rk.end_in); };
+    auto whole = [&](int r) { return rank_whole(rk, r); };
 #pragma unroll
     for (int j = 0; j < BO; ++j) {
       const int ob = w * BO + j;

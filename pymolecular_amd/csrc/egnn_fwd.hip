@@ -264,12 +264,19 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nf
   for (int64_t f = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); f < nfix; f += nw) {
     const int r = a.fix_rows[f];
     const int rs = a.rowptr[r], re = a.rowptr[r + 1];
-    int64_t t0 = 0, tn = 0;   // tiles t0 .. t0 + tn - 1; tile t0 holds the row in slot 0 or 1, later tiles in slot 0
+    float x[3] = {0.f, 0.f, 0.f};   // x of the row (x' = x + agg_x), loaded with the row's bounds by
+    if (EQ && a.coord_res && l == (O / 4) % 64) {   // the lane whose columns c4 include c4 = O
+#pragma unroll
+      for (int i = 0; i < 3; ++i) x[i] = a.coord[(int64_t)r * a.sc + i];
+    }
+    // tiles t0 .. t0 + tn - 1; the row is rank 0 (slot 0) of every tile but the first, and of the
+    // first exactly when it starts at that tile's first edge, else its last rank (slot 1)
+    int64_t t0 = 0, tn = 0;
     int slot0 = 0;
     if (re > rs) {
       t0 = rs / kTileEdges;
       tn = (re - 1) / kTileEdges - t0 + 1;
-      slot0 = (a.erow[t0 * kTileEdges] == r) ? 0 : 1;
+      slot0 = rs % kTileEdges == 0 ? 0 : 1;
     }
     for (int c4 = 4 * l; c4 < SEGW; c4 += 256) {
       const float* cp = a.carry + t0 * 2 * SEGW + c4;   // tile t0 + k, slot 0: cp + 2 k SEGW
@@ -295,7 +302,7 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nf
 #pragma unroll
         for (int i = 0; i < 3; ++i) {
           const float v = (a.mean && re > rs) ? acc[i] / (float)(re - rs) : acc[i];
-          o[i] = a.coord_res ? a.coord[(int64_t)r * a.sc + i] + v : v;   // x' = x + agg_x
+          o[i] = a.coord_res ? x[i] + v : v;   // x' = x + agg_x
         }
       }
     }

@@ -137,6 +137,40 @@ __device__ __forceinline__ bf16x8 seg_chunk_span(int span, int g, const uint2* l
   return r;
 }
 
+// Ranks of a 32-edge tile from the rows of its edges (ri[0..TE)) and of the edges
+// just before and after it (ex[0], ex[1]): edge k starts a rank when it is the
+// tile's first edge or its row differs from that of edge k - 1; the first rank's
+// row starts in the tile unless edge base - 1 has the same row, the last rank's
+// row ends in it unless edge base + TE has the same row.  Wave-uniform results.
+struct TileRanks { uint32_t mask; int nrank, nvalid; bool start_in, end_in; };
+__device__ __forceinline__ TileRanks tile_ranks(const int* ri, const int* ex, int64_t base, int64_t E, int l) {
+  TileRanks r;
+  r.nvalid = (int)((E - base) < TE ? (E - base) : TE);
+  const int k = l & 31;
+  const int rk = ri[k], rp = ri[k > 0 ? k - 1 : 0];
+  const bool nf = l < TE && k < r.nvalid && (k == 0 || rp != rk);
+  r.mask = (uint32_t)(__ballot(nf) & 0xffffffffull);
+  r.nrank = __popc(r.mask);
+  r.start_in = base == 0 || ex[0] != ri[0];
+  r.end_in = base + TE >= E || ex[1] != ri[TE - 1];
+  return r;
+}
+// Row and span of each rank (call from one wave): lane l < TE that starts rank q writes
+// rowof[q] and rspan[q].
+__device__ __forceinline__ void tile_rank_tables(const int* ri, const TileRanks& r, int l, int* rowof, int* rspan) {
+  if (l < TE && ((r.mask >> l) & 1u)) {
+    const uint32_t rest = l >= 31 ? 0u : (r.mask & ~((2u << l) - 1u));
+    const int end = rest ? __ffs(rest) - 1 : r.nvalid;
+    const int q = rank_of(r.mask, l);
+    rowof[q] = ri[l];
+    rspan[q] = rank_span(l, end - l);
+  }
+}
+// Rank r of the tile is a whole row: it neither continues from the previous tile nor into the next.
+__device__ __forceinline__ bool rank_whole(const TileRanks& rk, int r) {
+  return (r > 0 || rk.start_in) && (r < rk.nrank - 1 || rk.end_in);
+}
+
 __device__ __forceinline__ bf16x8 input_chunk(const bf16* ef, int64_t se, int eid, int FE, int g, float r2, bool eq) {
   const int slot0 = 8 * g;
   if (slot0 + 8 <= FE) return load_chunk(ef + (int64_t)eid * se + slot0);
