@@ -132,7 +132,7 @@ size_t egnn_bwd_workspace_bytes(const EgnnDims* dims);
 size_t egnn_node_proj_bytes(const EgnnDims* dims);
 
 /* Fused forward.  b1/b2/bx1 may be NULL (no bias); edge_ids may be NULL
- * (identity, datasets_loaders.py:11); edge_feat may be NULL when FE = 0.
+ * (identity, datasets_loaders.py:11); edge_feat may be NULL when FE = 0 or E = 0.
  * For MPNN (equivariant = 0) coord, w1_mov, w2_mov, bx1 and out_mov are
  * ignored and may be NULL.  Writes out_msg (N, O) and out_mov (N, 3). */
 int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides,

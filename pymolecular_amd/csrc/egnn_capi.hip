@@ -137,7 +137,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   if ((rc = check_strides(s, strides, false)) != EGNN_OK) return rc;
   if (!h || !rowptr || !w1_msg || !w2_msg || !out_msg || !sched || !workspace) return EGNN_ERR_NULL;
   if (s.E > 0 && !col) return EGNN_ERR_NULL;
-  if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
+  if (s.FE > 0 && s.E > 0 && !edge_feat) return EGNN_ERR_NULL;   // no edges: nothing reads it
   if (s.eq && (!coord || !w1_mov || !w2_mov || !out_mov)) return EGNN_ERR_NULL;
   if (!aligned16(h) || !aligned16(edge_feat) || !aligned16(out_msg) || !aligned16(workspace)) return EGNN_ERR_ALIGN;
   FwdWs w;
@@ -198,7 +198,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       !workspace)
     return EGNN_ERR_NULL;
   if (s.E > 0 && !col) return EGNN_ERR_NULL;
-  if (s.FE > 0 && !edge_feat) return EGNN_ERR_NULL;
+  if (s.FE > 0 && s.E > 0 && !edge_feat) return EGNN_ERR_NULL;   // no edges: nothing reads it
   if (s.eq && (!coord || !w1_mov || !w2_mov || !grad_out_mov || !grad_coord || !grad_w1_mov || !grad_w2_mov))
     return EGNN_ERR_NULL;
   if (!aligned16(h) || !aligned16(grad_h) || !aligned16(edge_feat) || !aligned16(grad_out_msg) || !aligned16(workspace))

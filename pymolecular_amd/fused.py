@@ -155,6 +155,8 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
         edge_feat = edge_feat.to(dt).contiguous()
         if edge_feat.shape[1] == 0:
             edge_feat = None
+        elif edge_feat.shape[0] == 0:   # no edges: a fresh empty tensor has unit-stride rows of F_E
+            edge_feat = torch.empty((0, edge_feat.shape[1]), dtype=dt, device=edge_feat.device)
     if equivariant:
         coord = coord.to(torch.float32).contiguous()
     return h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1

@@ -229,3 +229,21 @@ def test_coord_residual(dtype, shape):
     for k in ("h", "w1_msg", "w2_msg", "w1_mov", "b1"):
         if g0[k] is not None:
             assert torch.equal(g0[k], g1[k]), k
+
+
+@pytest.mark.parametrize("dtype", ["fp32", "bf16"])
+@pytest.mark.parametrize("eq,FE", [(True, 0), (True, 16), (False, 16)])
+def test_no_edges(dtype, eq, FE):
+    # a graph without edges: zero messages and coordinate updates, zero gradients (the edge kernels
+    # launch nothing, every row is an empty fix-up row; torch hands the empty edge features over
+    # as a NULL pointer)
+    rowptr = np.zeros(41, np.int32)
+    col = np.zeros(0, np.int32)
+    case = Case(rowptr, col, 64, FE, 128, 128, 128, seed=91, eq=eq, mean_agg=eq)
+    r = run_fused(case, dtype)
+    assert not np.any(r["out_msg"])
+    if eq:
+        assert not np.any(r["out_mov"])
+    for k, v in r["grads"].items():
+        if v is not None:
+            assert not np.any(v), k
