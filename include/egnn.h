@@ -234,6 +234,29 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
 int32_t egnn_profile_enable(int32_t on);
 int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches);
 
+/* ---- graph construction (the step before the layer) ------------------------
+ * kNN and radius graphs inside segments (protein chains, catalyst systems) as
+ * CSR: row i lists the sources j of node i's edges in ascending order.  They
+ * replace the host builders of the workload generator (no reference function:
+ * the reference draws random CSR graphs, datasets_loaders.py:3-39).
+ * pos [N][3] fp64 (8-byte aligned); seg_ptr [n_seg + 1] device int32, from 0 to N,
+ * nondecreasing, with no segment larger than max_seg (<= 2048).  The squared
+ * distance is ((dx*dx + dy*dy) + dz*dz) in fp64, d = pos_i - pos_j, each operation
+ * rounded on its own; the candidates of node i are the other nodes of its segment
+ * in (squared distance, index) order.  egnn_knn_graph keeps the first min(k, n - 1)
+ * (k <= 64); egnn_radius_graph the first max_nb (<= 64) with squared distance
+ * <= cutoff * cutoff.  rowptr [N + 1] and col [col_capacity >= N * k (max_nb)] are
+ * written; *n_edges receives E = rowptr[N].  tmp: egnn_graph_tmp_bytes(N) bytes.
+ * Each call synchronises the stream once (for the edge count and the segment check:
+ * EGNN_ERR_DIMS when a segment is malformed or larger than max_seg). */
+size_t egnn_graph_tmp_bytes(int64_t N);
+int32_t egnn_knn_graph(const double* pos, int64_t N, const int32_t* seg_ptr, int32_t n_seg, int32_t max_seg,
+                       int32_t k, int32_t* rowptr, int32_t* col, int64_t col_capacity, void* tmp, size_t tmp_bytes,
+                       int64_t* n_edges, void* stream);
+int32_t egnn_radius_graph(const double* pos, int64_t N, const int32_t* seg_ptr, int32_t n_seg, int32_t max_seg,
+                          double cutoff, int32_t max_nb, int32_t* rowptr, int32_t* col, int64_t col_capacity,
+                          void* tmp, size_t tmp_bytes, int64_t* n_edges, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

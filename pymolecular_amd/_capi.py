@@ -23,6 +23,7 @@ EXPORTED = (
     "egnn_node_bwd_workspace_bytes", "egnn_node_fwd", "egnn_node_bwd",
     "egnn_dense_fwd", "egnn_dense_wgrad_workspace_bytes", "egnn_dense_wgrad",
     "egnn_profile_enable", "egnn_profile_read",
+    "egnn_graph_tmp_bytes", "egnn_knn_graph", "egnn_radius_graph",
 )
 
 # kernel classes of the instrumentation hook
@@ -105,6 +106,14 @@ def lib() -> ctypes.CDLL:
     L.egnn_dense_wgrad_workspace_bytes.argtypes = [c_int64, c_int32, c_int32]
     L.egnn_dense_wgrad.restype = c_int32
     L.egnn_dense_wgrad.argtypes = [c_int32, c_int64, c_int32, c_int32, P, c_int64, P, c_int64, P, P, P, c_size_t, P]
+    L.egnn_graph_tmp_bytes.restype = c_size_t
+    L.egnn_graph_tmp_bytes.argtypes = [c_int64]
+    L.egnn_knn_graph.restype = c_int32
+    L.egnn_knn_graph.argtypes = [P, c_int64, P, c_int32, c_int32, c_int32, P, P, c_int64, P, c_size_t,
+                                 ctypes.POINTER(c_int64), P]
+    L.egnn_radius_graph.restype = c_int32
+    L.egnn_radius_graph.argtypes = [P, c_int64, P, c_int32, c_int32, ctypes.c_double, c_int32, P, P, c_int64, P,
+                                    c_size_t, ctypes.POINTER(c_int64), P]
     L.egnn_profile_enable.restype = c_int32
     L.egnn_profile_enable.argtypes = [c_int32]
     L.egnn_profile_read.restype = c_int32

@@ -29,6 +29,7 @@ from typing import Optional
 import numpy as np
 
 __all__ = ["Graph", "molecule_batch", "protein_chains", "catalyst_slabs", "powerlaw_graph", "rbf",
+           "protein_positions", "knn_rows", "slab_positions", "radius_rows",
            "csr_from_rows", "WORKLOADS", "make_workload", "xavier_uniform"]
 
 
@@ -103,10 +104,9 @@ def molecule_batch(n_graphs: int, seed: int = 1001, feat_seed: int = 2001, lo: i
                  dict(name="molecules", n_graphs=n_graphs, graph_offsets=offs))
 
 
-def protein_chains(n_chains: int = 64, n_res: int = 512, k: int = 30, seed: int = 1003, feat_seed: int = 2003,
-                   step: float = 3.8, min_dist: float = 3.0, n_types: int = 20, n_rbf: int = 16,
-                   rbf_max: float = 15.0, max_tries: int = 200) -> Graph:
-    """Self-avoiding 3-D random-walk chains with an in-chain kNN graph (k = 30)."""
+def protein_positions(n_chains: int = 64, n_res: int = 512, seed: int = 1003, step: float = 3.8,
+                      min_dist: float = 3.0, max_tries: int = 200) -> np.ndarray:
+    """Self-avoiding 3-D random-walk chains, float64 (n_chains, n_res, 3)."""
     r = _rng(seed)
     X = np.zeros((n_chains, n_res, 3))
     for t in range(1, n_res):
@@ -125,18 +125,32 @@ def protein_chains(n_chains: int = 64, n_res: int = 512, k: int = 30, seed: int 
             prop[idx[~ok]] = cand[~ok]     # kept if every try is rejected
             need[idx[ok]] = False
         X[:, t] = prop
+    return X
+
+
+def knn_rows(X: np.ndarray, k: int):
+    """Host kNN inside each segment of X (n_seg, n, 3): (rows, cols) with each node's k nearest
+    others (ties broken by index), sources ascending."""
+    n_seg, n = X.shape[:2]
     rows_l, cols_l = [], []
-    for cidx in range(n_chains):
+    for cidx in range(n_seg):
         P = X[cidx]
         d2 = ((P[:, None, :] - P[None, :, :]) ** 2).sum(-1)
         np.fill_diagonal(d2, np.inf)
         nb = np.argsort(d2, axis=1, kind="stable")[:, :k]      # ties broken by index
         nb = np.sort(nb, axis=1)
-        base = cidx * n_res
-        rows_l.append(np.repeat(np.arange(n_res), k) + base)
+        base = cidx * n
+        rows_l.append(np.repeat(np.arange(n), nb.shape[1]) + base)
         cols_l.append(nb.reshape(-1) + base)
-    rows = np.concatenate(rows_l)
-    cols = np.concatenate(cols_l)
+    return np.concatenate(rows_l), np.concatenate(cols_l)
+
+
+def protein_chains(n_chains: int = 64, n_res: int = 512, k: int = 30, seed: int = 1003, feat_seed: int = 2003,
+                   step: float = 3.8, min_dist: float = 3.0, n_types: int = 20, n_rbf: int = 16,
+                   rbf_max: float = 15.0, max_tries: int = 200) -> Graph:
+    """Self-avoiding 3-D random-walk chains with an in-chain kNN graph (k = 30)."""
+    X = protein_positions(n_chains, n_res, seed, step, min_dist, max_tries)
+    rows, cols = knn_rows(X, k)
     N = n_chains * n_res
     coord = X.reshape(N, 3).astype(np.float32)
     rowptr, col, _ = csr_from_rows(rows, cols, N)
@@ -145,13 +159,16 @@ def protein_chains(n_chains: int = 64, n_res: int = 512, k: int = 30, seed: int 
     return Graph(rowptr, col, coord, _one_hot(types, n_types), rbf(d, n_rbf, rbf_max), dict(name="proteins"))
 
 
-def catalyst_slabs(n_sys: int = 256, n_atoms: int = 80, density: float = 0.08, cutoff: float = 6.0,
-                   max_nb: int = 50, seed: int = 1004, feat_seed: int = 2004, n_types: int = 50,
-                   n_rbf: int = 32) -> Graph:
-    """Uniform atoms in open cubes, radius graph capped at the nearest ``max_nb``."""
-    r = _rng(seed)
+def slab_positions(n_sys: int = 256, n_atoms: int = 80, density: float = 0.08, seed: int = 1004) -> np.ndarray:
+    """Uniform atoms in open cubes of side (n_atoms / density)^(1/3), float64 (n_sys, n_atoms, 3)."""
     side = (n_atoms / density) ** (1.0 / 3.0)
-    X = r.uniform(0.0, side, size=(n_sys, n_atoms, 3))
+    return _rng(seed).uniform(0.0, side, size=(n_sys, n_atoms, 3))
+
+
+def radius_rows(X: np.ndarray, cutoff: float, max_nb: int):
+    """Host radius graph inside each segment of X (n_seg, n, 3): (rows, cols) with each node's
+    nearest max_nb others (ties broken by index) within the cutoff, sources ascending."""
+    n_sys, n_atoms = X.shape[:2]
     rows_l, cols_l = [], []
     for s in range(n_sys):
         P = X[s]
@@ -164,8 +181,15 @@ def catalyst_slabs(n_sys: int = 256, n_atoms: int = 80, density: float = 0.08, c
             cand = np.sort(cand)
             rows_l.append(np.full(cand.size, i + s * n_atoms))
             cols_l.append(cand + s * n_atoms)
-    rows = np.concatenate(rows_l)
-    cols = np.concatenate(cols_l)
+    return np.concatenate(rows_l), np.concatenate(cols_l)
+
+
+def catalyst_slabs(n_sys: int = 256, n_atoms: int = 80, density: float = 0.08, cutoff: float = 6.0,
+                   max_nb: int = 50, seed: int = 1004, feat_seed: int = 2004, n_types: int = 50,
+                   n_rbf: int = 32) -> Graph:
+    """Uniform atoms in open cubes, radius graph capped at the nearest ``max_nb``."""
+    X = slab_positions(n_sys, n_atoms, density, seed)
+    rows, cols = radius_rows(X, cutoff, max_nb)
     N = n_sys * n_atoms
     coord = X.reshape(N, 3).astype(np.float32)
     rowptr, col, _ = csr_from_rows(rows, cols, N)
