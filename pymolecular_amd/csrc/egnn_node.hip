@@ -73,8 +73,11 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
 int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
   K = std::max<int64_t>(K, 1);
   const bool big = K >= kSplitKBig;   // the tile launch_gemm2 picks for this product
-  const int64_t tiles = N == 1 ? 1 : big ? cdiv(M, 128) * cdiv(N, N <= 32 ? 32 : 128) : cdiv(M, 32) * cdiv(N, 64);
-  const int64_t target = N == 1 ? 1024 : 512;   // matrix-vector products: one small block per split
+  const int64_t tiles = N == 1 ? 1 : big ? cdiv(M, 128) * cdiv(N, N <= 32 ? 32 : 128) : cdiv(M, 64) * cdiv(N, 64);
+  // matrix-vector products: one small block per split; 64 x 64 tiles: about 256 rows per split at the
+  // node counts of molecule batches (measured faster than 32 x 64 tiles over 700 rows: fewer re-reads
+  // of the operands from L2 for a few more partials)
+  const int64_t target = N == 1 ? 1024 : big ? 512 : 768;
   const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(target, std::max<int64_t>(tiles, 1)), cdiv(K, 256)));
   return cdiv(cdiv(K, splits), 64) * 64;
 }
@@ -783,14 +786,14 @@ __global__ __launch_bounds__(256) void gemm_bf16_nfirst_kernel(Gemm2Args g, int 
 template <bool AK1, bool BN1, bool AK2, bool BN2>
 __global__ __launch_bounds__(256) void gemm_bf16_pair_kernel(Gemm2Args g1, Gemm2Args g2, int gx1, int gy1, int n1,
                                                              int gx2, int gy2) {
-  constexpr int n1s = GemmBf16Smem<AK1, BN1, 32, 64, 64, 2>::n, n2s = GemmBf16Smem<AK2, BN2, 32, 64, 64, 2>::n;
+  constexpr int n1s = GemmBf16Smem<AK1, BN1, 32, 64, 64, 2>::n, n2s = GemmBf16Smem<AK2, BN2, 64, 64, 64, 2>::n;
   __shared__ __attribute__((aligned(16))) bf16 smem[n1s > n2s ? n1s : n2s];
   int b = (int)blockIdx.x;
   if (b < n1) {
     gemm_bf16_tile<AK1, BN1, 32, 64, 64, 2>(g1, b % gx1, (b / gx1) % gy1, b / (gx1 * gy1), smem);
   } else {
     b -= n1;
-    gemm_bf16_tile<AK2, BN2, 32, 64, 64, 2>(g2, b % gx2, (b / gx2) % gy2, b / (gx2 * gy2), smem);
+    gemm_bf16_tile<AK2, BN2, 64, 64, 64, 2>(g2, b % gx2, (b / gx2) % gy2, b / (gx2 * gy2), smem);
   }
 }
 
@@ -1070,9 +1073,10 @@ unsigned splits_of(const Gemm2Args& g) {
 
 int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf16, hipStream_t st) {
   const bool e1 = g1.M > 0 && g1.N > 0, e2 = g2.M > 0 && g2.N > 0;
+  // the first product on 32 x 64 tiles, the second (a split-K reduction) on 64 x 64 tiles
   const bool tiled = e1 && e2 && bf16_tiled_ok(g1, compute_bf16) && bf16_tiled_ok(g2, compute_bf16) &&
-                     !bf16_big_tiles(g1) && !bf16_big_tiles(g2);
-  const int64_t gx1 = cdiv(g1.M, 32), gy1 = cdiv(g1.N, 64), gx2 = cdiv(g2.M, 32), gy2 = cdiv(g2.N, 64);
+                     !bf16_big_tiles(g1) && !bf16_big_tiles(g2) && g1.ksplit <= 0 && g2.ksplit > 0;
+  const int64_t gx1 = cdiv(g1.M, 32), gy1 = cdiv(g1.N, 64), gx2 = cdiv(g2.M, 64), gy2 = cdiv(g2.N, 64);
   const int64_t n1 = gx1 * gy1 * splits_of(g1), n2 = gx2 * gy2 * splits_of(g2);
   if (!tiled || n1 + n2 >= (int64_t(1) << 31)) {
     int r = e1 ? launch_gemm2(g1, compute_bf16, st) : 0;
@@ -1101,6 +1105,14 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   if (bf16_tiled_ok(g, compute_bf16)) {
     const bool big = bf16_big_tiles(g);
     const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
+    if (!big && g.ksplit > 0) {   // split-K reductions over node-sized K: 64 x 64 tiles
+      const dim3 gs((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
+      if (g.a_kc && g.b_nc) hipLaunchKernelGGL((gemm_bf16_kernel<true, true, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
+      else if (g.a_kc) hipLaunchKernelGGL((gemm_bf16_kernel<true, false, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
+      else if (g.b_nc) hipLaunchKernelGGL((gemm_bf16_kernel<false, true, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
+      else hipLaunchKernelGGL((gemm_bf16_kernel<false, false, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
+      return (int)hipGetLastError();
+    }
     if (big && !narrow && g.ksplit <= 0 && g.K <= 128 && g.a_kc) {
       // node products with K <= 128 on large grids: 64 x 128 tiles in 32-deep k stages (a smaller LDS
       // footprint, more blocks in flight), n tiles of a row block adjacent; measured faster than the
