@@ -255,7 +255,10 @@ def main():
             portions[cls] = dict(mfma_frac=fl / (per / 1e3) / (peak_mfma * 1e12),
                                  hbm_frac=by / (per / 1e3) / (PEAK["hbm_gbs"] * 1e9),
                                  flops=fl, bytes=by)
-    dom = max(kern, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
+    # the dominant kernel class among those with an algorithmic work model (the layer's kernels; the node
+    # update, prep and fix-up classes have none and would report a zero fraction)
+    ranked = [c for c in kern if c in portions] or list(kern)
+    dom = max(ranked, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
     dur_s = kern[dom]["ms_per_launch"] / 1e3
     flops, nbytes = work_per_launch(dom, kern[dom]["launches_per_step"])
     if nbytes / (PEAK["hbm_gbs"] * 1e9) >= flops / (peak_mfma * 1e12):
