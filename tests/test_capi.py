@@ -57,3 +57,35 @@ def test_bad_arguments_return_status_not_crash():
     assert L.egnn_fwd(d, s_bad, *([None] * 18), 0, None) == 3
     assert L.egnn_schedule_build(None, None, 10, 20, None, 0, None, 0, None) == 1
     assert L.egnn_schedule_build(1, 1, 0, 20, 1, 0, 1, 0, None) == 2
+
+
+def test_flags_validated():
+    L = _capi.lib()
+    kw = dict(N=100, E=1000, F=128, FE=16, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=1)
+    for flags in (0, _capi.FLAG_ACCUMULATE_GRAD_H, _capi.FLAG_COORD_RESIDUAL,
+                  _capi.FLAG_ACCUMULATE_GRAD_H | _capi.FLAG_COORD_RESIDUAL):
+        assert L.egnn_bwd_workspace_bytes(_capi.EgnnDims(**kw, flags=flags)) > 0, flags
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**kw, flags=4)) == 0          # unknown flag
+    kw["equivariant"] = 0                                                            # no coordinates in the MPNN layer
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**kw, flags=_capi.FLAG_COORD_RESIDUAL)) == 0
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**kw, flags=_capi.FLAG_ACCUMULATE_GRAD_H)) > 0
+
+
+def test_graph_builder_arguments_checked_on_the_host():
+    # every check below returns before the library touches the device
+    L = _capi.lib()
+    assert L.egnn_graph_tmp_bytes(0) == 0 and L.egnn_graph_tmp_bytes(1000) > 4000
+    ne = ctypes.c_int64(0)
+    buf = 1 << 12   # a non-NULL stand-in address, never dereferenced by these calls
+    call = lambda k, cap, tmpb, pos=buf: L.egnn_knn_graph(pos, 100, buf, 2, 64, k, buf, buf, cap, buf, tmpb,  # noqa: E731
+                                                           ctypes.byref(ne), None)
+    big = L.egnn_graph_tmp_bytes(100)
+    assert call(8, 800, big, pos=None) == 1        # NULL positions
+    assert call(65, 6500, big) == 2                 # k above 64
+    assert call(0, 800, big) == 2                   # k below 1
+    assert call(8, 799, big) == 5                   # col capacity below N * k
+    assert call(8, 800, 16) == 5                    # short tmp
+    assert call(8, 800, big, pos=buf + 4) == 4      # positions not 8-byte aligned
+    assert L.egnn_radius_graph(buf, 100, buf, 2, 64, ctypes.c_double(-1.0), 8, buf, buf, 800, buf, big,
+                               ctypes.byref(ne), None) == 2   # negative cutoff
+    assert L.egnn_knn_graph(buf, 100, buf, 2, 4096, 8, buf, buf, 800, buf, big, ctypes.byref(ne), None) == 2
