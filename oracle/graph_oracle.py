@@ -1,7 +1,7 @@
 """CPU oracle for graph construction inside segments (float64 numpy).
 
-TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, and only as
-the checker; the product path (``pymolecular_amd.graph_build``, the HIP kernels
+TEST INFRASTRUCTURE ONLY.  Only ``tests/`` may import this module, and only to
+check results; the product path (``pymolecular_amd.graph_build``, the HIP kernels
 ``egnn_knn_graph`` / ``egnn_radius_graph``) never imports it.
 
 What it restates

@@ -10,7 +10,7 @@ Reference counterparts
     (models/EGNN/forward_kernel.py:14-43) and
     ``egnn_backward_kernel_node_parallel[grid](...)`` (backward_kernel.py:14-50)
     -> :func:`egnn_fused_forward` / :func:`egnn_fused_backward`;
-  * the reference has no ``autograd.Function`` (SURVEY of the repo: none), so
+  * the reference defines no ``autograd.Function`` for the layer, so
     :class:`EGNNFusedFn` is new; it saves only its inputs and recomputes in the
     backward, like backward_kernel.py:173-180.
 """

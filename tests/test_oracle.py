@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/egnn_oracle.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/egnn_oracle.py) before the GPU tests trust it.
 
 The reference ships no golden vectors, seeds or assertions, so the oracle is
 pinned by what the mathematics fixes:
