@@ -554,7 +554,7 @@ int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
 
 int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st) {
   if (s.eq) return s.NUC == 1 ? launch_wide_bwd_t<256, 8, true, 1>(a, st) : launch_wide_bwd_t<256, 8, true, 2>(a, st);
-  return s.NUC == 1 ? launch_wide_bwd_t<256, 8, false, 1>(a, st) : launch_wide_bwd_t<256, 8, false, 2>(a, st);
+  return s.NUC == 1 ? launch_wide_bwd_t<256, 16, false, 1>(a, st) : launch_wide_bwd_t<256, 16, false, 2>(a, st);
 }
 
 }  // namespace egnn
