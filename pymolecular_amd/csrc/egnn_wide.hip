@@ -276,7 +276,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* PQ = (const bf16*)a.PQ;
   const bf16* ef = (const bf16*)a.ef;
   const bf16* gmsg = (const bf16*)a.gmsg;
@@ -319,6 +319,11 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
 
   for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
     const int64_t base = t * TE;
+    // The lane's fragment offset, made opaque once per tile so that the weight
+    // addresses are formed at each load (SGPR base + this offset) instead of
+    // being hoisted out of the tile loop as one 64-bit VGPR pair per k-slice.
+    int lo8 = l * 8;
+    __asm__ __volatile__("" : "+v"(lo8));
     int ri[2], rj[2], eid[2];
     bool valid[2];
     float r2[2], gphi[2];
@@ -377,7 +382,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
       f32x4 acc[2] = {zero4(), zero4()};
 #pragma unroll
       for (int kc = 0; kc < KH; ++kc) {
-        const bf16x8 A = load_chunk(FhlT + ((int64_t)ob * KH + kc) * kFragElems + l * 8);
+        const bf16x8 A = load_chunk(FhlT + ((int64_t)ob * KH + kc) * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
       }
@@ -407,7 +412,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
         f32x4 acc[2] = {zero4(), zero4()};
 #pragma unroll
         for (int kc = 0; kc < KO; ++kc) {
-          const bf16x8 A = load_chunk(FmovT + ((int64_t)mb * KO + kc) * kFragElems + l * 8);
+          const bf16x8 A = load_chunk(FmovT + ((int64_t)mb * KO + kc) * kFragElems + lo8);
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m, kc, nb, l));
         }
@@ -449,7 +454,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
       if constexpr (EQ) {
 #pragma unroll
         for (int kc = 0; kc < KM; ++kc) {
-          const bf16x8 A = load_chunk(Fmov + ((int64_t)ob * KM + kc) * kFragElems + l * 8);
+          const bf16x8 A = load_chunk(Fmov + ((int64_t)ob * KM + kc) * kFragElems + lo8);
 #pragma unroll
           for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_gq, kc, nb, l));
         }
@@ -475,7 +480,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
       f32x4 acc[2] = {zero4(), zero4()};
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc) {
-        const bf16x8 A = load_chunk(Fhl + ((int64_t)hb * KO + kc) * kFragElems + l * 8);
+        const bf16x8 A = load_chunk(Fhl + ((int64_t)hb * KO + kc) * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_ga2, kc, nb, l));
       }
@@ -553,7 +558,7 @@ int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
 }
 
 int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st) {
-  if (s.eq) return s.NUC == 1 ? launch_wide_bwd_t<256, 8, true, 1>(a, st) : launch_wide_bwd_t<256, 8, true, 2>(a, st);
+  if (s.eq) return s.NUC == 1 ? launch_wide_bwd_t<256, 16, true, 1>(a, st) : launch_wide_bwd_t<256, 16, true, 2>(a, st);
   return s.NUC == 1 ? launch_wide_bwd_t<256, 16, false, 1>(a, st) : launch_wide_bwd_t<256, 16, false, 2>(a, st);
 }
 
