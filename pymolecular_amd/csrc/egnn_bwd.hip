@@ -72,6 +72,10 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
   const int64_t nwt = (int64_t)gridDim.x * 4;
 
   for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < a.ntiles; t += nwt) {
+    // the lane's fragment offset, opaque once per tile: the weight addresses are
+    // formed at each load instead of being hoisted out of the tile loop
+    int lo8 = l * 8;
+    __asm__ __volatile__("" : "+v"(lo8));
     const int64_t base = t * TW;
     int ri[NB], rj[NB], eid[NB];
     int64_t ee[NB];
@@ -116,8 +120,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
       for (int nb = 0; nb < NB; ++nb) lo[nb] = hi[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 1
       for (int uc = 0; uc < NUC; ++uc) {
-        const C ua0 = load_chunk(Fu + ((int64_t)(2 * kc) * NUC + uc) * kFragElems + l * 8);
-        const C ua1 = load_chunk(Fu + ((int64_t)(2 * kc + 1) * NUC + uc) * kFragElems + l * 8);
+        const C ua0 = load_chunk(Fu + ((int64_t)(2 * kc) * NUC + uc) * kFragElems + lo8);
+        const C ua1 = load_chunk(Fu + ((int64_t)(2 * kc + 1) * NUC + uc) * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const C u = edge_input_chunk_b<T, EQ>(ef, a.se, eid[nb], a.FE, uc, g, r2[nb]);
@@ -154,8 +158,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
       for (int nb = 0; nb < NB; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KH; ++kc) {
-        const C a0 = load_chunk(FhlT + ((int64_t)(2 * kp) * KH + kc) * kFragElems + l * 8);
-        const C a1 = load_chunk(FhlT + ((int64_t)(2 * kp + 1) * KH + kc) * kFragElems + l * 8);
+        const C a0 = load_chunk(FhlT + ((int64_t)(2 * kp) * KH + kc) * kFragElems + lo8);
+        const C a1 = load_chunk(FhlT + ((int64_t)(2 * kp + 1) * KH + kc) * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           mma(acc0[nb], a0, m1c[kc][nb]);
@@ -194,8 +198,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
         for (int nb = 0; nb < NB; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kc = 0; kc < KO; ++kc) {
-          const C a0 = load_chunk(FmovT + ((int64_t)(2 * mp) * KO + kc) * kFragElems + l * 8);
-          const C a1 = load_chunk(FmovT + ((int64_t)(2 * mp + 1) * KO + kc) * kFragElems + l * 8);
+          const C a0 = load_chunk(FmovT + ((int64_t)(2 * mp) * KO + kc) * kFragElems + lo8);
+          const C a1 = load_chunk(FmovT + ((int64_t)(2 * mp + 1) * KO + kc) * kFragElems + lo8);
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             mma(acc0[nb], a0, mc[kc][nb]);
@@ -254,8 +258,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
       if constexpr (EQ) {
 #pragma unroll
         for (int kc = 0; kc < KM; ++kc) {
-          const C a0 = load_chunk(Fmov + ((int64_t)(2 * kp) * KM + kc) * kFragElems + l * 8);
-          const C a1 = load_chunk(Fmov + ((int64_t)(2 * kp + 1) * KM + kc) * kFragElems + l * 8);
+          const C a0 = load_chunk(Fmov + ((int64_t)(2 * kp) * KM + kc) * kFragElems + lo8);
+          const C a1 = load_chunk(Fmov + ((int64_t)(2 * kp + 1) * KM + kc) * kFragElems + lo8);
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb) {
             mma(acc0[nb], a0, gqc[kc][nb]);
@@ -289,8 +293,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
       for (int nb = 0; nb < NB; ++nb) acc0[nb] = acc1[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc) {
-        const C a0 = load_chunk(Fhl + ((int64_t)(2 * hc) * KO + kc) * kFragElems + l * 8);
-        const C a1 = load_chunk(Fhl + ((int64_t)(2 * hc + 1) * KO + kc) * kFragElems + l * 8);
+        const C a0 = load_chunk(Fhl + ((int64_t)(2 * hc) * KO + kc) * kFragElems + lo8);
+        const C a1 = load_chunk(Fhl + ((int64_t)(2 * hc + 1) * KO + kc) * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           mma(acc0[nb], a0, ga2c[kc][nb]);
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
       for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kc = 0; kc < KH; ++kc) {
-        const C a0 = load_chunk(FuT + (int64_t)kc * kFragElems + l * 8);
+        const C a0 = load_chunk(FuT + (int64_t)kc * kFragElems + lo8);
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) mma(acc[nb], a0, ga1c[kc][nb]);
       }
