@@ -1477,10 +1477,20 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
   __shared__ __attribute__((aligned(16))) bf16 Bs[2][WG_BN * WG_P];
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
   const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)blockIdx.x * WG_BM, n0 = (int64_t)blockIdx.y * WG_BN;
-  const int64_t kbeg = (int64_t)blockIdx.z * g.ksplit;
+  // 1-D grid, XCD-aware: block b is dispatched to XCD b % 8, and the per = gx * gy
+  // output tiles of k-split z go to consecutive blocks of XCD z % 8, so they share
+  // that XCD's L2 for the split's operand rows.  The grid holds per * roundup(gz, 8)
+  // blocks; those past the last split leave before any barrier.
+  const int gx = (int)((g.M + WG_BM - 1) / WG_BM), per = gx * (int)((g.N + WG_BN - 1) / WG_BN);
+  const int64_t gz = (g.K + g.ksplit - 1) / g.ksplit;
+  const int64_t xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
+  const int64_t bz = (jx / per) * 8 + xcd;
+  if (bz >= gz) return;
+  const int tile = (int)(jx % per), bx = tile % gx, by = tile / gx;
+  const int64_t m0 = (int64_t)bx * WG_BM, n0 = (int64_t)by * WG_BN;
+  const int64_t kbeg = bz * g.ksplit;
   const int64_t kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
-  const bool colsum = g.b_colsum && blockIdx.x == 0;
+  const bool colsum = g.b_colsum && bx == 0;
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -1556,7 +1566,7 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
     buf ^= 1;
   }
 
-  float* P = g.partial + (int64_t)blockIdx.z * (g.M + (g.b_colsum ? 1 : 0)) * g.N;
+  float* P = g.partial + bz * (g.M + (g.b_colsum ? 1 : 0)) * g.N;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -1583,8 +1593,9 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
 
 int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0 || g.K <= 0) return 0;
-  const dim3 grid((unsigned)cdiv(g.M, WG_BM), (unsigned)cdiv(g.N, WG_BN), (unsigned)cdiv(g.K, g.ksplit));
-  hipLaunchKernelGGL(wgrad_gemm_kernel, grid, dim3(256), 0, st, g);
+  const int64_t per = cdiv(g.M, WG_BM) * cdiv(g.N, WG_BN), gz = cdiv(g.K, g.ksplit);
+  const int64_t blocks = per * cdiv(gz, 8) * 8;
+  hipLaunchKernelGGL(wgrad_gemm_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g);
   return (int)hipGetLastError();
 }
 
