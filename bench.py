@@ -1,28 +1,37 @@
 #!/usr/bin/env python
 """Throughput of the fused EGNN/MPNN layer, forward + backward, on one MI355X.
 
-Default workload: 1024 fully connected molecules (9..29 atoms; N = 19,363,
-E = 383,714), an EGNN stack of 4 E_GCL layers at H = 128 (embedding_in 5 ->
-128, embedding_out 128 -> 128), forward + backward of the sum-of-outputs loss
-sum(h_out) + sum(x_out) w.r.t. all parameters.  bf16 activations and weights
-with fp32 accumulation (``--dtype fp32`` for the fp32 run).  ``--workload k``
-selects the other workloads (1 molecules-128 fp32 1 layer, 3 proteins kNN-30
-with 16 RBFs, 4 slabs H = 256 with 32 RBFs, 5 power-law MPNN 2M nodes).
+Default workload: the skewed-degree power-law MPNN, one graph of N = 2,000,000
+nodes and E = 18,566,352 edges (in-degree ~ d^-2.1 on [2, 4096]), 2 MPNN
+layers at H = 128 with 16-dim N(0, 1) edge features, bf16 activations and
+weights with fp32 accumulation -- the largest of the five workloads, all of
+which fit one GPU.  ``--workload k`` (``--dtype``) selects another one:
+1 molecules-128 (1 E_GCL, fp32), 2 molecules-1024 (4 E_GCL, fp32 or bf16),
+3 proteins kNN-30 (4 E_GCL, 16 RBFs), 4 slabs (6 E_GCL, H = 256, 32 RBFs);
+``--all`` prints one line for each workload and dtype.
 
-value = E * layers / t_step: edges per second through the fused layer, whole
-stack timed (fused kernels, per-node GEMMs, node MLPs, autograd glue), inputs
-resident in HBM before the timed region.
+A step is forward + backward of the sum-of-outputs loss of the whole stack
+(embeddings, fused layers, node updates) with respect to all parameters,
+inputs resident in HBM before the timed region.  value = E * layers / t_step:
+edges per second through the fused layer.
 
-roofline: the dominant kernel class of one step, timed with HIP events on
-the stream its kernels run on (the library's instrumentation hook), its
-algorithmic work per launch (MFMA FLOPs of the products it must execute;
-HBM bytes with every gathered row counted once per edge) and the MI355X peak
-of whichever of the two bounds it.  ``traffic`` is the measured HBM bytes per
-launch from the rocprofv3 FETCH_SIZE / WRITE_SIZE summary under profiles/
-when one exists for this workload and dtype, else null.
+roofline: the dominant edge kernel of the step (the fused backward at every
+workload but the one-layer one), its average launch time from HIP events
+recorded on the stream it runs on during the timed steps (the library's
+instrumentation hook), and its algorithmic work per launch from the
+per-edge model of the reference formulation:
+    FLOP_fwd(e) = 2 [(2F + g + F_E) H + H O + g (O M + M)],  FLOP_bwd = 2 FLOP_fwd
+    B_fwd = E (8 + F s + c + F_E s) + N (4 + F s + 2c + O s)
+    B_bwd = E (8 + F s + c + F_E s + 4F + c) + N (4 + F s + 3c + O s + 4F)
+(g = 1 for EGNN, 0 for MPNN; c = 16 g; s = bytes per activation), bounded by
+whichever of HBM (8 TB/s) and MFMA (bf16 2516.6, fp32 157.3 TFLOP/s) takes
+longer for that work.  ``executed`` gives the same kernel's work as this
+build executes it (projections hoisted to the nodes, scratch traffic).
+``traffic`` is the measured HBM bytes per launch from the rocprofv3
+FETCH_SIZE / WRITE_SIZE summary under profiles/ when one exists.
 cpu_baseline: the torch-eager CPU restatement (oracle/torch_ref.py) of the
-same stack in fp32 on a bounded sample of the same workload, on this host's
-cores.
+same stack in fp32 on a deterministic row subset of the same workload (at
+least 10 % of its edges), on this host's cores.
 """
 from __future__ import annotations
 
@@ -48,17 +57,20 @@ DESCR = {
     4: "slabs-256x80: 6 x E_GCL, H=256, radius 6 A capped at 50, F_E=32 RBF",
     5: "powerlaw-2M: 2 x MPNN layer, H=128, power-law in-degree (alpha 2.1, 2..4096), F_E=16",
 }
+ALL = [(1, "fp32"), (2, "fp32"), (2, "bf16"), (3, "bf16"), (4, "bf16"), (5, "bf16")]
 
 
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--workload", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--dtype", choices=["bf16", "fp32"], default=None,
                     help="default: bf16, except fp32 for the one-layer molecules-128 workload")
-    ap.add_argument("--cpu-edges", type=int, default=200_000, help="edge budget of the CPU-baseline sample")
+    ap.add_argument("--all", action="store_true", help="one line per workload and dtype")
+    ap.add_argument("--cpu-frac", type=float, default=0.10, help="least fraction of the edges in the CPU sample")
+    ap.add_argument("--cpu-min-edges", type=int, default=200_000, help="least edges in the CPU sample")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
@@ -66,14 +78,28 @@ def parse():
     return ap.parse_args()
 
 
-def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
-    """Algorithmic (MFMA FLOPs, HBM bytes) of one launch of a kernel class.
+def path_model(cls, N, E, F, H, O, M, FE, g, s):
+    """(FLOPs, bytes) of one launch of an edge kernel under the reference formulation's per-edge model.
 
-    FLOPs count the products the kernel must execute (identity transposes and
-    segment-sum products are overhead, not work).  Bytes count every gathered
-    row once per edge: P_i, Q_j (H each), col and row id (8), edge id and
-    features, x_i and x_j (24); node outputs once per node.
-    """
+    FLOPs: the concat-input MLPs per edge (pytorch_baseline.py:27-35), the backward twice the forward.
+    Bytes: every gathered row counted once per edge, node rows once per node, the dh_j fp32 write
+    once per edge (c = 16 g: a padded fp32 coordinate row)."""
+    c = 16 * g
+    flop_fwd = 2 * ((2 * F + g + FE) * H + H * O + g * (O * M + M))
+    if cls == "fwd_edge":
+        return flop_fwd * E, E * (8 + F * s + c + FE * s) + N * (4 + F * s + 2 * c + O * s)
+    if cls == "bwd_edge":
+        return 2 * flop_fwd * E, E * (8 + F * s + c + FE * s + 4 * F + c) + N * (4 + F * s + 3 * c + O * s + 4 * F)
+    return 0, 0
+
+
+def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
+    """Executed algorithmic (MFMA FLOPs, HBM bytes) of one launch of a kernel class, as this build runs it.
+
+    FLOPs count the products the kernel must execute with the first layer's node projections hoisted
+    out of the edge loop (identity transposes and segment-sum products are overhead, not work).  Bytes
+    count every gathered row once per edge: P_i, Q_j (H each), col and row id (8), edge id and
+    features, the geometry record; scratch stores (Gh, Gx, factors) included; node outputs once."""
     eb = 8 + (4 + FE * s if FE else 0) + 24 * g
     if cls == "fwd_edge":
         flops = 2 * ((g + FE) * H + H * O + g * O * M)
@@ -121,8 +147,19 @@ def read_traffic(name, dtype, cls):
     return None
 
 
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def _closed_prefix(rowptr, col, n_edges):
-    """Largest row prefix [0, r) with at most about n_edges edges whose sources all lie in [0, r)."""
+    """Smallest row prefix [0, r) with at least n_edges edges whose sources all lie in [0, r), or 0."""
     N = rowptr.shape[0] - 1
     deg = np.diff(rowptr)
     rowmax = np.full(N, -1, dtype=np.int64)
@@ -130,30 +167,42 @@ def _closed_prefix(rowptr, col, n_edges):
     rowmax[nz] = np.maximum.reduceat(col.astype(np.int64), rowptr[:-1][nz])
     mx = np.maximum.accumulate(rowmax)
     r_ok = np.nonzero(mx < np.arange(1, N + 1))[0] + 1     # prefixes closed under sources
-    r_ok = r_ok[rowptr[r_ok] <= n_edges]
-    return int(r_ok[-1]) if r_ok.size else 0
+    r_ok = r_ok[rowptr[r_ok] >= n_edges]
+    return int(r_ok[0]) if r_ok.size else 0
 
 
-def cpu_baseline(k, g, H, layers, eq, n_edges, repeats, seed):
+def cpu_sample(g, n_edges):
+    """A deterministic subgraph with at least n_edges edges: (rows, cols, node ids, edge range, description).
+
+    Batched graphs: the smallest prefix of whole graphs.  One connected graph: the first rows holding
+    n_edges edges, with every source they read (relabelled; sources outside the prefix keep no edges)."""
+    r = _closed_prefix(g.rowptr, g.col, n_edges)
+    if r and int(g.rowptr[r]) <= 2 * n_edges:
+        e_end = int(g.rowptr[r])
+        rows = np.repeat(np.arange(r), np.diff(g.rowptr[:r + 1]))
+        return rows, g.col[:e_end].astype(np.int64), np.arange(r), e_end, f"first {r} nodes (whole graphs)"
+    r = int(np.searchsorted(g.rowptr, n_edges, side="left"))
+    e_end = int(g.rowptr[r])
+    rows = np.repeat(np.arange(r), np.diff(g.rowptr[:r + 1]))
+    nodes = np.unique(np.concatenate([np.arange(r), g.col[:e_end]]))
+    cols = np.searchsorted(nodes, g.col[:e_end]).astype(np.int64)
+    return rows, cols, nodes, e_end, (f"first {r} destination rows and the {nodes.size} nodes they read "
+                                      f"(sources relabelled, none folded)")
+
+
+def cpu_baseline(k, g, H, layers, eq, frac, min_edges, repeats, seed):
     import torch
     from oracle.torch_ref import EGNNRef, MPNNRef
     torch.set_num_threads(len(os.sched_getaffinity(0)))
-    r = _closed_prefix(g.rowptr, g.col, n_edges)
-    folded = False
-    if r == 0:        # one connected graph: the first rows, their sources folded into the sample
-        deg_cum = g.rowptr.astype(np.int64)
-        r = int(np.searchsorted(deg_cum, n_edges, side="right") - 1)
-        folded = True
-    e_end = int(g.rowptr[r])
-    rows = np.repeat(np.arange(r), np.diff(g.rowptr[:r + 1]))
-    cols = g.col[:e_end].astype(np.int64) % r if folded else g.col[:e_end].astype(np.int64)
+    target = min(g.E, max(int(np.ceil(frac * g.E)), min_edges))
+    rows, cols, nodes, e_end, how = cpu_sample(g, target)
     edges = (torch.from_numpy(rows.astype(np.int64)), torch.from_numpy(cols))
-    h0 = torch.from_numpy(g.node_feat[:r])
+    h0 = torch.from_numpy(g.node_feat[nodes])
     ea = None if g.edge_attr is None else torch.from_numpy(g.edge_attr[:e_end])
     FE = 0 if ea is None else ea.shape[1]
     torch.manual_seed(seed)
     if eq:
-        x0 = torch.from_numpy(g.coord[:r])
+        x0 = torch.from_numpy(g.coord[nodes])
         model = EGNNRef(h0.shape[1], H, H, FE, n_layers=layers)
         run = lambda: sum(t.sum() for t in model(h0, x0, edges, ea))  # noqa: E731
     else:
@@ -171,29 +220,24 @@ def cpu_baseline(k, g, H, layers, eq, n_edges, repeats, seed):
         step()
         ts.append(time.perf_counter() - t0)
     t = statistics.median(ts)
-    how = "first %d rows, sources folded into them" % r if folded else "first %d nodes (whole graphs)" % r
     return dict(value=e_end * layers / t, unit="edges/s", cores=torch.get_num_threads(), kind="port",
-                sample=f"{how}: N={r}, E={e_end}, {layers} layers fwd+bwd, fp32 torch eager "
-                       f"(oracle/torch_ref.py), median of {repeats} after 1 warm-up; {t * 1e3:.1f} ms per step")
+                cpu_model=cpu_model(),
+                sample=f"{how}: N={nodes.size}, E={e_end} ({100.0 * e_end / g.E:.1f} % of the workload's edges), "
+                       f"{layers} layers fwd+bwd, fp32 torch eager (oracle/torch_ref.py), median of {repeats} "
+                       f"after 1 warm-up; {t * 1e3:.1f} ms per step; value = sample edges x layers / time")
 
 
-def main():
-    a = parse()
-    if a.gpus != 1:
-        print(f"bench.py measures one GPU (asked for --gpus {a.gpus}): the multi-GPU sharding of this layer "
-              "is designed but not built", file=sys.stderr)
-        sys.exit(2)
+def run_workload(k, dtype, a, g=None):
     import torch
     from pymolecular_amd import _capi, graphs
     from pymolecular_amd.models.EGNN import EGNN, MPNN
 
-    k = a.workload
     W = graphs.WORKLOADS[k]
-    dtype = a.dtype or W["dtypes"][-1]
+    dtype = dtype or W["dtypes"][-1]
     dev = torch.device("cuda:0")
     dt = torch.bfloat16 if dtype == "bf16" else torch.float32
     H, L, eq = W["H"], W["layers"], W["eq"]
-    g = graphs.make_workload(k)
+    g = g if g is not None else graphs.make_workload(k)
     N, E = g.N, g.E
     F0 = g.node_feat.shape[1]
     FE = 0 if g.edge_attr is None else g.edge_attr.shape[1]
@@ -213,9 +257,13 @@ def main():
         model.zero_grad(set_to_none=True)
         loss().backward()
 
+    # the library's event hook stays on through warm-up and timed steps: its events are recorded on the
+    # stream each kernel runs on, and the warm-up fills its event pool so the timed steps create none
+    _capi.profile_enable(True)
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
+    _capi.profile_enable(True)    # keep only the timed steps' records
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(a.steps):
@@ -224,13 +272,6 @@ def main():
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / a.steps
     value = E * L / (ms / 1e3)
-
-    # per-kernel device time: HIP events on the launch stream, through the library hook
-    _capi.profile_enable(True)
-    nprof = max(3, min(a.steps, 10))
-    for _ in range(nprof):
-        step()
-    torch.cuda.synchronize()
     prof = _capi.profile_read()
     _capi.profile_enable(False)
 
@@ -238,38 +279,45 @@ def main():
     g1 = 1 if eq else 0
     coop = s == 2 and H == 128 and FE + 2 * g1 <= 32
     peak_mfma = PEAK["bf16_mfma_tflops"] if s == 2 else PEAK["fp32_mfma_tflops"]
-    def work_per_launch(cls, launches_per_step):
+
+    def executed_per_launch(cls, launches_per_step):
         fl, by = kernel_work(cls, coop, N, E, H, H, H, H, FE, g1, s)
         if cls == "wgrad":   # a class of several launches per layer: the average launch
             return fl * L / launches_per_step, by * L / launches_per_step
         return fl, by
+
+    def bound(fl, by, dur_s):
+        t_hbm, t_mfma = by / (PEAK["hbm_gbs"] * 1e9), fl / (peak_mfma * 1e12)
+        if t_hbm >= t_mfma:
+            return dict(bound="hbm", achieved=by / dur_s / 1e9, peak=PEAK["hbm_gbs"], unit="GB/s",
+                        frac=t_hbm / dur_s)
+        return dict(bound="mfma", achieved=fl / dur_s / 1e12, peak=peak_mfma, unit="TFLOP/s", frac=t_mfma / dur_s)
 
     kern, portions = {}, {}
     for cls, (t, n) in prof.items():
         if not n:
             continue
         per = t / n
-        kern[cls] = dict(ms_per_launch=per, launches_per_step=n / nprof, share=(t / nprof) / ms)
-        fl, by = work_per_launch(cls, n / nprof)
+        kern[cls] = dict(ms_per_launch=per, launches_per_step=n / a.steps, share=(t / a.steps) / ms)
+        fl, by = executed_per_launch(cls, n / a.steps)
         if fl or by:
             portions[cls] = dict(mfma_frac=fl / (per / 1e3) / (peak_mfma * 1e12),
-                                 hbm_frac=by / (per / 1e3) / (PEAK["hbm_gbs"] * 1e9),
-                                 flops=fl, bytes=by)
-    # the dominant kernel class among those with an algorithmic work model (the layer's kernels; the node
-    # update, prep and fix-up classes have none and would report a zero fraction)
-    ranked = [c for c in kern if c in portions] or list(kern)
-    dom = max(ranked, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
+                                 hbm_frac=by / (per / 1e3) / (PEAK["hbm_gbs"] * 1e9), flops=fl, bytes=by)
+    edge_cls = [c for c in ("bwd_edge", "fwd_edge") if c in kern]
+    dom = max(edge_cls, key=lambda c: kern[c]["ms_per_launch"] * kern[c]["launches_per_step"])
     dur_s = kern[dom]["ms_per_launch"] / 1e3
-    flops, nbytes = work_per_launch(dom, kern[dom]["launches_per_step"])
-    if nbytes / (PEAK["hbm_gbs"] * 1e9) >= flops / (peak_mfma * 1e12):
-        roof = dict(bound="hbm", achieved=nbytes / dur_s / 1e9, peak=PEAK["hbm_gbs"], unit="GB/s")
-    else:
-        roof = dict(bound="mfma", achieved=flops / dur_s / 1e12, peak=peak_mfma, unit="TFLOP/s")
-    roof["frac"] = roof["achieved"] / roof["peak"]
+    fl, by = path_model(dom, N, E, H, H, H, H, FE, g1, s)
+    roof = bound(fl, by, dur_s)
     name = DESCR[k].split(":")[0]
     roof["traffic"] = read_traffic(name, dtype, dom)
-    roof.update(kernel=dom, ms_per_launch=kern[dom]["ms_per_launch"], algorithmic_flops=flops,
-                algorithmic_bytes=nbytes)
+    xf, xb = executed_per_launch(dom, kern[dom]["launches_per_step"])
+    roof.update(kernel=dom, ms_per_launch=kern[dom]["ms_per_launch"], algorithmic_flops=fl, algorithmic_bytes=by,
+                executed=dict(flops=xf, bytes=xb, **{kk: v for kk, v in bound(xf, xb, dur_s).items()
+                                                     if kk in ("bound", "frac")}))
+    # the whole step against the per-edge model of every layer's forward and backward
+    fwf, fwb = path_model("fwd_edge", N, E, H, H, H, H, FE, g1, s)
+    bwf, bwb = path_model("bwd_edge", N, E, H, H, H, H, FE, g1, s)
+    step_roof = bound((fwf + bwf) * L, (fwb + bwb) * L, ms / 1e3)
     model_mfu = model_flops_per_edge(H, H, H, H, FE, g1) * E * L / (ms / 1e3) / (peak_mfma * 1e12)
 
     out = {
@@ -280,20 +328,36 @@ def main():
         "config": {"workload": DESCR[k] + ", fwd+bwd of the sum-of-outputs loss", "N": N, "E": E, "layers": L,
                    "H": H, "F_E": FE, "dtype": dtype},
         "roofline": roof,
+        "step_roofline": {kk: step_roof[kk] for kk in ("bound", "frac")},
         "portions": portions,
         "model_flops_mfma_frac": model_mfu,
         "kernels": {c: {kk: round(vv, 5) for kk, vv in v.items()} for c, v in kern.items()},
-        "kernel_ms_per_step": sum(t for t, _ in prof.values()) / nprof,
+        "kernel_ms_per_step": sum(t for t, _ in prof.values()) / a.steps,
     }
     if not a.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(k, g, H, L, eq, a.cpu_edges, a.cpu_repeats, 3000 + k)
+        out["cpu_baseline"] = cpu_baseline(k, g, H, L, eq, a.cpu_frac, a.cpu_min_edges, a.cpu_repeats, 3000 + k)
+    del model, edges, h0, ea
+    torch.cuda.empty_cache()
+    return out
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU (asked for --gpus {a.gpus}): every workload fits one MI355X, and the "
+              "multi-GPU sharding of this layer is designed but not built", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    todo = ALL if a.all else [(a.workload, a.dtype)]
+    for k, dtype in todo:
+        out = run_workload(k, dtype, a)
+        print(json.dumps(out), flush=True)
     if a.copy_probe:
-        src = torch.empty(64 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+        src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-    print(json.dumps(out), flush=True)
 
 
 if __name__ == "__main__":

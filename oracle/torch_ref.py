@@ -120,10 +120,14 @@ class EGNNRef(nn.Module):
         self.layers = nn.ModuleList([EGCLRef(hidden_nf, hidden_nf, hidden_nf, edges_in_d=in_edge_nf,
                                              coords_agg=coords_agg) for _ in range(n_layers)])
 
-    def forward(self, h, x, edges, edge_attr=None):
-        h = self.embedding_in(h)
+    def forward(self, h, x, edges, edge_attr=None, act_round=None):
+        """``act_round``: applied to h after the embedding and after every layer (the
+        activations a bf16 stack stores between layers), e.g. :func:`round_bf16_st`."""
+        rd = act_round or (lambda t: t)
+        h = rd(self.embedding_in(h))
         for layer in self.layers:
             h, x, _ = layer(h, edges, x, edge_attr=edge_attr)
+            h = rd(h)
         return self.embedding_out(h), x
 
 
@@ -160,11 +164,18 @@ class MPNNRef(nn.Module):
         self.layers = nn.ModuleList([MPNNGCLRef(hidden_nf, hidden_nf, hidden_nf, edges_in_d=in_edge_nf)
                                      for _ in range(n_layers)])
 
-    def forward(self, h, edges, edge_attr=None):
-        h = self.embedding_in(h)
+    def forward(self, h, edges, edge_attr=None, act_round=None):
+        rd = act_round or (lambda t: t)
+        h = rd(self.embedding_in(h))
         for layer in self.layers:
             h, _ = layer(h, edges, edge_attr=edge_attr)
+            h = rd(h)
         return self.embedding_out(h)
+
+
+def round_bf16_st(t):
+    """Round to bfloat16 values in the forward, identity in the backward (straight through)."""
+    return t + (t.to(torch.bfloat16).to(t.dtype) - t).detach()
 
 
 def egcl_params_packed(layer) -> dict:

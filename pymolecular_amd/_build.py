@@ -3,10 +3,16 @@
 Each ``csrc/*.hip`` file is compiled with ``hipcc --offload-arch=gfx950`` in
 parallel and linked into one shared library next to this file, so that it
 travels with the source tree.  ``python -m pymolecular_amd._build`` runs it.
+
+Next to the library the build writes ``libpymolecular_egnn.so.srchash``: a
+SHA-256 over the sources it was built from (``csrc/``, ``include/egnn.h``)
+and the compiler flags.  ``_capi.lib()`` recomputes it and refuses a library
+built from other sources, so a run always exercises the current tree.
 """
 from __future__ import annotations
 
 import concurrent.futures as cf
+import hashlib
 import os
 import subprocess
 import sys
@@ -14,7 +20,9 @@ from pathlib import Path
 
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
+HEADER = PKG.parent / "include" / "egnn.h"
 LIB = PKG / "libpymolecular_egnn.so"
+STAMP = LIB.with_name(LIB.name + ".srchash")
 OBJ = PKG / "_objs"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -24,6 +32,20 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wno-unused-result",
 ]
+
+
+def source_files() -> list:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [HEADER]
+
+
+def source_hash() -> str:
+    """SHA-256 over the flags and the (relative name, content) of every source file."""
+    h = hashlib.sha256()
+    h.update("\0".join(FLAGS).encode())
+    for p in source_files():
+        h.update(b"\0" + p.name.encode() + b"\0")
+        h.update(p.read_bytes())
+    return h.hexdigest()
 
 
 def _compile(src: Path) -> Path:
@@ -38,6 +60,7 @@ def _compile(src: Path) -> Path:
 
 def build(verbose: bool = True) -> Path:
     OBJ.mkdir(exist_ok=True)
+    digest = source_hash()
     srcs = sorted(CSRC.glob("*.hip"))
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
@@ -47,9 +70,12 @@ def build(verbose: bool = True) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stderr)
+    if STAMP.exists():
+        STAMP.unlink()
     os.replace(tmp, LIB)
+    STAMP.write_text(digest + "\n")
     if verbose:
-        print(f"built {LIB} from {len(srcs)} sources")
+        print(f"built {LIB} from {len(srcs)} sources (sources sha256 {digest[:16]})")
     return LIB
 
 

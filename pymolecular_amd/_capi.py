@@ -54,6 +54,24 @@ class EgnnNodeDims(ctypes.Structure):
 
 _lib = None
 
+ABI_VERSION = 5   # include/egnn.h egnn_abi_version()
+
+
+def _check_stamp() -> None:
+    """Refuse a library that was not built from the sources in this tree.
+
+    The build writes the SHA-256 of its sources next to the library; a missing
+    or different stamp means the library is stale (or foreign)."""
+    from . import _build
+    stamp = _build.STAMP
+    if not stamp.exists():
+        raise RuntimeError(f"{stamp} is missing: rebuild the library with `python -m pymolecular_amd._build`")
+    built = stamp.read_text().strip()
+    now = _build.source_hash()
+    if built != now:
+        raise RuntimeError(f"{LIB_PATH} was built from other sources (sha256 {built[:16]}, tree {now[:16]}): "
+                           "rebuild it with `python -m pymolecular_amd._build`")
+
 
 class EgnnError(RuntimeError):
     """A C-ABI call returned a non-zero status."""
@@ -71,10 +89,14 @@ def lib() -> ctypes.CDLL:
     if not LIB_PATH.exists():
         raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m pymolecular_amd._build` "
                            "(or __graft_entry__.build()); there is no CPU fallback")
+    _check_stamp()
     L = ctypes.CDLL(str(LIB_PATH))
     P = c_void_p
     L.egnn_abi_version.restype = c_int32
     L.egnn_abi_version.argtypes = []
+    if L.egnn_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} implements ABI {L.egnn_abi_version()}, these bindings expect {ABI_VERSION}: "
+                           "rebuild it with `python -m pymolecular_amd._build`")
     L.egnn_status_string.restype = c_char_p
     L.egnn_status_string.argtypes = [c_int32]
     L.egnn_schedule_bytes.restype = c_size_t

@@ -21,12 +21,30 @@ int32_t hip_status(int e) { return e == (int)hipSuccess ? EGNN_OK : EGNN_ERR_HIP
 struct ProfRec { int cls; hipEvent_t a, b; };
 bool g_prof_on = false;
 std::vector<ProfRec> g_prof;
+std::vector<hipEvent_t> g_event_pool;   // events of cleared records, reused (kept until the process ends)
+
+hipEvent_t prof_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e = nullptr;
+  return hipEventCreate(&e) == hipSuccess ? e : nullptr;
+}
 
 struct ProfScope {
   hipStream_t st; int cls; hipEvent_t a = nullptr, b = nullptr;
   ProfScope(int c, hipStream_t s) : st(s), cls(c) {
     if (!g_prof_on) return;
-    if (hipEventCreate(&a) != hipSuccess || hipEventCreate(&b) != hipSuccess) { a = b = nullptr; return; }
+    a = prof_event();
+    b = prof_event();
+    if (!a || !b) {
+      if (a) g_event_pool.push_back(a);
+      if (b) g_event_pool.push_back(b);
+      a = b = nullptr;
+      return;
+    }
     (void)hipEventRecord(a, st);
   }
   ~ProfScope() {
@@ -37,7 +55,7 @@ struct ProfScope {
 };
 
 void prof_clear() {
-  for (auto& r : g_prof) { (void)hipEventDestroy(r.a); (void)hipEventDestroy(r.b); }
+  for (auto& r : g_prof) { g_event_pool.push_back(r.a); g_event_pool.push_back(r.b); }
   g_prof.clear();
 }
 

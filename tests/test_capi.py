@@ -29,7 +29,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_host_only_entry_points():
     L = _capi.lib()
-    assert L.egnn_abi_version() == 5
+    assert L.egnn_abi_version() == _capi.ABI_VERSION
     assert _capi.status_string(0) == "ok"
     assert "CSR" in _capi.status_string(6)
     assert L.egnn_schedule_bytes(100, 1000) > 4 * 1000

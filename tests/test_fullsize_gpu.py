@@ -1,16 +1,20 @@
-"""The fused layer at the workloads' full sizes, checked through properties that hold at any size.
+"""The fused layer at the workloads' full sizes, checked against the oracle and through properties.
 
-The float64 oracle finishes in seconds only on small graphs, so on the full graphs of the
-benchmark workloads (molecules-1024, proteins 64 x 512, the 2M-node power-law graph) these
-tests check, in bf16:
-  * row restriction: out_msg[i] and out_mov[i] depend only on the edges of row i, so the
-    oracle run on the subgraph of a few sampled rows (the heaviest row among them) gives
-    those rows (normwise 2e-2);
-  * E(3) equivariance: rotating and translating the coordinates leaves out_msg unchanged and
-    rotates out_mov;
-  * exact linearity of the backward in the incoming gradients: doubling them doubles every
-    gradient bit for bit (scaling by 2 is exact in bf16 and fp32);
-  * bitwise determinism of the forward and the backward.
+The float64 oracle finishes in seconds only on small graphs.  On the full graphs of the five
+workloads (molecules-128 and -1024, proteins 64 x 512, slabs 256 x 80 at H = 256, the 2M-node
+power-law graph) these tests check:
+  * molecules-128 (E = 45,636, fp32, one layer): the whole graph, forward and backward, against
+    the oracle at 1e-5;
+  * forward row restriction: out_msg[i] and out_mov[i] depend only on the edges of row i, so the
+    oracle on the subgraph of a few sampled rows (the heaviest row among them) gives those rows;
+  * backward row restriction: with the incoming gradients zero outside the sampled rows, every
+    weight gradient depends only on those rows' edges, and so do the gradients of h and x of the
+    nodes they touch; the oracle's backward on the subgraph gives all of them, and every other
+    node's gradient is exactly zero;
+  * E(3) equivariance (rotation and translation of the coordinates);
+  * exact linearity of the backward in the incoming gradients (scaling by 2 is exact) and
+    bitwise determinism of the forward and the backward.
+Bounds: normwise 1e-5 (fp32), 2e-2 (bf16); the bf16 oracle runs in float64 on the bf16 inputs.
 """
 import numpy as np
 import pytest
@@ -22,8 +26,11 @@ from tests.cases import make_params
 
 pytestmark = pytest.mark.gpu
 
-BF = torch.bfloat16
+BF, F32 = torch.bfloat16, torch.float32
+TOL = {BF: 2e-2, F32: 1e-5}
 
+# workload -> (H, equivariant); F = O = M = H, F_E from the workload's own edge inputs
+SHAPE = {1: (128, True), 2: (128, True), 3: (128, True), 4: (256, True), 5: (128, False)}
 
 _GRAPHS = {}
 
@@ -35,18 +42,19 @@ def _graph(k):
     return _GRAPHS[k]
 
 
-def _inputs(k, FE, eq, seed):
+def _inputs(k, dtype, seed):
     g = _graph(k)
-    N, E = g.N, g.E
+    H, eq = SHAPE[k]
+    FE = 0 if g.edge_attr is None else g.edge_attr.shape[1]
     gen = torch.Generator(device="cuda").manual_seed(seed)
-    h = torch.randn((N, 128), generator=gen, device="cuda").to(BF)
-    ef = torch.randn((E, FE), generator=gen, device="cuda").to(BF) if FE else None
+    h = torch.randn((g.N, H), generator=gen, device="cuda").to(dtype)
+    ef = torch.from_numpy(g.edge_attr).cuda().to(dtype) if FE else None
     coord = torch.from_numpy(g.coord).cuda() if eq else None
-    p = make_params(np.random.Generator(np.random.PCG64(seed)), 128, FE, 128, 128, 128, eq=eq)
-    pd = {key: torch.from_numpy(v).cuda().to(BF) for key, v in p.items()}
+    p = make_params(np.random.Generator(np.random.PCG64(seed)), H, FE, H, H, H, eq=eq)
+    pd = {key: torch.from_numpy(v).cuda().to(dtype) for key, v in p.items()}
     rowptr = torch.from_numpy(g.rowptr).cuda()
     col = torch.from_numpy(g.col).cuda()
-    print(f"[fullsize] workload {k} N={N} E={E} FE={FE} eq={eq}", flush=True)
+    print(f"[fullsize] workload {k} N={g.N} E={g.E} H={H} FE={FE} eq={eq} dtype={dtype}", flush=True)
     return g, h, ef, coord, pd, p, rowptr, col
 
 
@@ -64,47 +72,130 @@ def _bwd(h, coord, ef, rowptr, col, pd, gm, gx, eq, mean):
                                      mean_agg=mean, equivariant=eq)
 
 
-@pytest.mark.parametrize("k,FE,eq,mean", [(2, 0, True, False), (3, 16, True, True), (5, 16, False, False)])
-def test_row_restriction_against_oracle(k, FE, eq, mean):
-    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, FE, eq, seed=100 + k)
-    out_msg, out_mov = _fwd(h, coord, ef, rowptr, col, pd, eq, mean)
-    torch.cuda.synchronize()
+def _sample_rows(g, k, n=47):
+    """The heaviest row plus n rows drawn without replacement (seeded), ascending."""
     deg = np.diff(g.rowptr)
     r = np.random.Generator(np.random.PCG64(7 + k))
-    rows = np.unique(np.concatenate([[int(np.argmax(deg))], r.choice(g.N, 47, replace=False)]))
-    # the subgraph of the sampled rows, nodes relabelled: the rows first, then their other sources
-    spans = [np.arange(g.rowptr[i], g.rowptr[i + 1]) for i in rows]
+    return np.unique(np.concatenate([[int(np.argmax(deg))], r.choice(g.N, n, replace=False)]))
+
+
+def _subgraph(g, rows):
+    """CSR of the edges of ``rows`` (ascending) over the nodes they touch, relabelled in ascending order.
+
+    Returns (nodes, sub_rowptr, sub_col, eidx): ``nodes`` are the old ids of the new nodes, ``eidx``
+    the old CSR positions of the subgraph's edges in its CSR order."""
+    spans = [np.arange(g.rowptr[i], g.rowptr[i + 1], dtype=np.int64) for i in rows]
     eidx = np.concatenate(spans)
     nodes = np.unique(np.concatenate([rows, g.col[eidx]]))
-    new = {int(v): q for q, v in enumerate(nodes)}
-    order = np.argsort([new[int(i)] for i in rows], kind="stable")
-    sub_rowptr = np.zeros(len(nodes) + 1, np.int64)
-    for i, s in zip(rows, spans):
-        sub_rowptr[new[int(i)] + 1] = len(s)
-    sub_rowptr = np.cumsum(sub_rowptr)
-    sub_col = np.concatenate([np.array([new[int(v)] for v in g.col[spans[q]]], np.int64) for q in order])
-    sub_eidx = np.concatenate([spans[q] for q in order])
+    deg = np.zeros(len(nodes), np.int64)
+    deg[np.searchsorted(nodes, rows)] = [len(s) for s in spans]
+    sub_rowptr = np.concatenate([[0], np.cumsum(deg)])
+    sub_col = np.searchsorted(nodes, g.col[eidx])
+    return nodes, sub_rowptr, sub_col, eidx
+
+
+def _oracle_inputs(h, coord, ef, p, nodes, eidx, dtype):
+    """The subgraph's inputs in float64 (the device's bf16 values exactly, for bf16)."""
     nodes_t = torch.from_numpy(nodes).cuda()
-    hs = h[nodes_t].float().cpu().numpy()
-    cs = None if coord is None else coord[nodes_t].cpu().numpy()
-    es = None if ef is None else ef[torch.from_numpy(sub_eidx).cuda()].float().cpu().numpy()
-    P = {key: orc.round_bf16(v) for key, v in p.items()}
+    hs = h[nodes_t].double().cpu().numpy()
+    cs = None if coord is None else coord[nodes_t].double().cpu().numpy()
+    es = None if ef is None else ef[torch.from_numpy(eidx).cuda()].double().cpu().numpy()
+    P = {key: (orc.round_bf16(v) if dtype == BF else v.astype(np.float64)) for key, v in p.items()}
+    return nodes_t, hs, cs, es, P
+
+
+ROW_CASES = [(2, BF, False), (2, F32, False), (3, BF, True), (4, BF, True), (5, BF, False)]
+
+
+@pytest.mark.parametrize("k,dtype,mean", ROW_CASES)
+def test_forward_row_restriction(k, dtype, mean, record_error):
+    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, dtype, seed=100 + k)
+    eq = SHAPE[k][1]
+    out_msg, out_mov = _fwd(h, coord, ef, rowptr, col, pd, eq, mean)
+    torch.cuda.synchronize()
+    rows = _sample_rows(g, k)
+    nodes, sub_rowptr, sub_col, eidx = _subgraph(g, rows)
+    _, hs, cs, es, P = _oracle_inputs(h, coord, ef, p, nodes, eidx, dtype)
     ref_msg, ref_mov = orc.fused_forward(hs, cs, es, sub_rowptr, sub_col, None, P, mean_agg=mean, equivariant=eq)
-    rows_new = np.array([new[int(i)] for i in rows])
-    got = out_msg[torch.from_numpy(rows).cuda()].float().cpu().numpy()
-    err = orc.normwise_rel_err(got, ref_msg[rows_new])
-    print(f"[fullsize] rows {len(rows)} (max degree {deg.max()}) out_msg err {err:.2e}", flush=True)
-    assert err <= 2e-2, err
+    rows_new = np.searchsorted(nodes, rows)
+    rows_t = torch.from_numpy(rows).cuda()
+    tol = TOL[dtype]
+    print(f"[fullsize] rows {len(rows)}, subgraph E={len(eidx)} (max degree {np.diff(g.rowptr).max()})", flush=True)
+    err = orc.normwise_rel_err(out_msg[rows_t].double().cpu().numpy(), ref_msg[rows_new])
+    record_error("out_msg", err, tol)
+    assert err <= tol, err
     if eq:
-        gmv = out_mov[torch.from_numpy(rows).cuda()].cpu().numpy()
-        err = orc.normwise_rel_err(gmv, ref_mov[rows_new])
-        print(f"[fullsize] out_mov err {err:.2e}", flush=True)
-        assert err <= 2e-2, err
+        err = orc.normwise_rel_err(out_mov[rows_t].double().cpu().numpy(), ref_mov[rows_new])
+        record_error("out_mov", err, tol)
+        assert err <= tol, err
 
 
-@pytest.mark.parametrize("k,FE,mean", [(2, 0, False), (3, 16, True)])
-def test_equivariance(k, FE, mean):
-    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, FE, True, seed=200 + k)
+@pytest.mark.parametrize("k,dtype,mean", ROW_CASES)
+def test_backward_row_restriction(k, dtype, mean, record_error):
+    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, dtype, seed=400 + k)
+    H, eq = SHAPE[k]
+    rows = _sample_rows(g, k)
+    rows_t = torch.from_numpy(rows).cuda()
+    gen = torch.Generator(device="cuda").manual_seed(9 + k)
+    gm = torch.zeros((g.N, H), dtype=dtype, device="cuda")
+    gm[rows_t] = torch.randn((len(rows), H), generator=gen, device="cuda").to(dtype)
+    gx = None
+    if eq:
+        gx = torch.zeros((g.N, 3), dtype=torch.float32, device="cuda")
+        gx[rows_t] = torch.randn((len(rows), 3), generator=gen, device="cuda")
+    grads = _bwd(h, coord, ef, rowptr, col, pd, gm, gx, eq, mean)
+    torch.cuda.synchronize()
+    nodes, sub_rowptr, sub_col, eidx = _subgraph(g, rows)
+    nodes_t, hs, cs, es, P = _oracle_inputs(h, coord, ef, p, nodes, eidx, dtype)
+    sub_gm = gm[nodes_t].double().cpu().numpy()
+    sub_gx = None if gx is None else gx[nodes_t].double().cpu().numpy()
+    ref = orc.fused_backward(hs, cs, es, sub_rowptr, sub_col, None, P, sub_gm, sub_gx, mean_agg=mean,
+                             equivariant=eq)
+    tol = TOL[dtype]
+    print(f"[fullsize] backward: rows {len(rows)}, subgraph N={len(nodes)} E={len(eidx)}", flush=True)
+    keys = ["w1_msg", "w2_msg", "b1", "b2"] + (["w1_mov", "w2_mov", "bx1"] if eq else [])
+    for key in keys:
+        err = orc.normwise_rel_err(grads[key].double().cpu().numpy().reshape(ref[key].shape), ref[key])
+        record_error("d" + key, err, tol)
+        assert err <= tol, (key, err)
+    outside = torch.ones(g.N, dtype=torch.bool, device="cuda")
+    outside[nodes_t] = False
+    for key in ["h"] + (["coord"] if eq else []):
+        err = orc.normwise_rel_err(grads[key][nodes_t].double().cpu().numpy(), ref[key])
+        record_error("d" + key, err, tol)
+        assert err <= tol, (key, err)
+        nz = int(torch.count_nonzero(grads[key][outside]))
+        assert nz == 0, f"d{key}: {nz} nonzero entries on nodes outside the sampled rows' edges"
+
+
+@pytest.mark.parametrize("mean", [False, True])
+def test_molecules128_whole_graph_fp32(mean, record_error):
+    # the one-layer fp32 workload is small enough for the oracle to run whole
+    g, h, ef, coord, pd, p, rowptr, col = _inputs(1, F32, seed=500 + int(mean))
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    gm = torch.randn((g.N, 128), generator=gen, device="cuda")
+    gx = torch.randn((g.N, 3), generator=gen, device="cuda")
+    out_msg, out_mov = _fwd(h, coord, ef, rowptr, col, pd, True, mean)
+    grads = _bwd(h, coord, ef, rowptr, col, pd, gm, gx, True, mean)
+    torch.cuda.synchronize()
+    P = {key: v.astype(np.float64) for key, v in p.items()}
+    hn, cn = h.double().cpu().numpy(), coord.double().cpu().numpy()
+    ref_msg, ref_mov = orc.fused_forward(hn, cn, None, g.rowptr, g.col, None, P, mean_agg=mean)
+    ref = orc.fused_backward(hn, cn, None, g.rowptr, g.col, None, P, gm.double().cpu().numpy(),
+                             gx.double().cpu().numpy(), mean_agg=mean)
+    errs = {"out_msg": orc.normwise_rel_err(out_msg.double().cpu().numpy(), ref_msg),
+            "out_mov": orc.normwise_rel_err(out_mov.double().cpu().numpy(), ref_mov)}
+    for key in ("h", "coord", "w1_msg", "w2_msg", "w1_mov", "w2_mov", "b1", "b2", "bx1"):
+        errs["d" + key] = orc.normwise_rel_err(grads[key].double().cpu().numpy().reshape(ref[key].shape), ref[key])
+    for key, err in errs.items():
+        record_error(key, err, 1e-5)
+    bad = {key: v for key, v in errs.items() if not v <= 1e-5}
+    assert not bad, bad
+
+
+@pytest.mark.parametrize("k,mean", [(2, False), (3, True), (4, True)])
+def test_equivariance(k, mean, record_error):
+    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, BF, seed=200 + k)
     q, _ = np.linalg.qr(np.random.Generator(np.random.PCG64(k)).standard_normal((3, 3)))
     R = torch.from_numpy(q.astype(np.float32)).cuda()
     t = torch.tensor([3.0, -1.5, 0.25], device="cuda")
@@ -113,15 +204,17 @@ def test_equivariance(k, FE, mean):
     torch.cuda.synchronize()
     e_msg = orc.normwise_rel_err(m1.float().cpu().numpy(), m0.float().cpu().numpy())
     e_mov = orc.normwise_rel_err(x1.cpu().numpy(), (x0 @ R.T).cpu().numpy())
-    print(f"[fullsize] equivariance out_msg {e_msg:.2e} out_mov {e_mov:.2e}", flush=True)
+    record_error("out_msg", e_msg, 2e-2)
+    record_error("out_mov", e_mov, 2e-2)
     assert e_msg <= 2e-2 and e_mov <= 2e-2, (e_msg, e_mov)
 
 
-@pytest.mark.parametrize("k,FE,eq", [(2, 0, True), (5, 16, False)])
-def test_backward_exact_linearity_and_determinism(k, FE, eq):
-    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, FE, eq, seed=300 + k)
+@pytest.mark.parametrize("k", [2, 4, 5])
+def test_backward_exact_linearity_and_determinism(k):
+    g, h, ef, coord, pd, p, rowptr, col = _inputs(k, BF, seed=300 + k)
+    H, eq = SHAPE[k]
     gen = torch.Generator(device="cuda").manual_seed(5)
-    gm = torch.randn((g.N, 128), generator=gen, device="cuda").to(BF)
+    gm = torch.randn((g.N, H), generator=gen, device="cuda").to(BF)
     gx = torch.randn((g.N, 3), generator=gen, device="cuda") if eq else None
     f1 = _fwd(h, coord, ef, rowptr, col, pd, eq, False)
     f2 = _fwd(h, coord, ef, rowptr, col, pd, eq, False)

@@ -128,9 +128,11 @@ def test_hidden_256(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
-@pytest.mark.parametrize("fe,eq,mean", [(16, True, False), (0, True, True), (16, False, False)])
+@pytest.mark.parametrize("fe,eq,mean", [(16, True, False), (0, True, True), (16, False, False), (48, False, False),
+                                        (40, True, True)])
 def test_hidden_256_ragged(dtype, fe, eq, mean):
-    # ragged degrees, a partial last tile, one or two edge-input chunks, EGNN and MPNN
+    # ragged degrees, a partial last tile, one or two 32-slot edge-input chunks (F_E + 2 > 32 for
+    # EGNN, F_E > 32 for MPNN take two), EGNN and MPNN
     rowptr, col = random_csr(701, (np.arange(701) * 11) % 37, seed=33)
     check_case(Case(rowptr, col, 256, fe, 256, 256, 256, seed=19, mean_agg=mean, eq=eq), dtype)
 

@@ -66,11 +66,26 @@ def test_egcl_layer_forward_backward(dtype, tol, edges_in_d):
     assert not bad, bad
 
 
-# Stack-level bound: the per-layer contract (fp32 1e-5, bf16 2e-2) is checked above; through 4
-# layers the bf16 residual stream, bf16 node MLPs and rounded activations compound, and the
-# float64 reference keeps full-precision activations, so the stack check uses a looser bound.
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 1e-1)])
-def test_egnn_stack(dtype, tol):
+def _stack_bounds(errs_fp32_cpu, dtype):
+    """Per-quantity bounds of the stack tests.
+
+    bf16: 2e-2 against a float64 reference whose activations are rounded to bf16 between layers, as
+    the device stores them (so the per-layer contract applies to the stack).  fp32: 1e-5, or twice
+    what the same stack in plain torch fp32 on the CPU reaches against float64 when 4-layer
+    compounding alone exceeds 1e-5."""
+    if dtype == torch.bfloat16:
+        return {k: 2e-2 for k in errs_fp32_cpu}
+    return {k: max(1e-5, 2.0 * v) for k, v in errs_fp32_cpu.items()}
+
+
+def _grads_rel(mod_named, ref_named, rename=lambda n: n):
+    refp = {rename(n): p for n, p in ref_named}
+    return {"d" + n: _rel(p.grad, refp[n].grad) for n, p in mod_named}
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_egnn_stack(dtype, record_error):
+    import copy
     from pymolecular_amd.models.EGNN import EGNN
     torch.manual_seed(1)
     H = 128
@@ -78,34 +93,44 @@ def test_egnn_stack(dtype, tol):
     edges = [torch.from_numpy(g.rows().astype(np.int64)), torch.from_numpy(g.col.astype(np.int64))]
     ref = torch_ref.EGNNRef(5, H, 16, 0, n_layers=4).double()
     mod = EGNN(5, H, 16, 0, n_layers=4).cuda().to(dtype)
+    bf = dtype == torch.bfloat16
     with torch.no_grad():
-        if dtype == torch.bfloat16:
+        if bf:
             for p in ref.parameters():
                 p.copy_(p.to(torch.bfloat16).double())
+    ref32 = copy.deepcopy(ref).float()
     # state dicts map 1:1 except the layer container name
+    ren = lambda n: n.replace("layers.", "gcl_")  # noqa: E731
     pm = dict(mod.named_parameters())
     for n, p in ref.named_parameters():
-        n2 = n.replace("layers.", "gcl_")
         with torch.no_grad():
-            pm[n2].copy_(p.to(dtype))
+            pm[ren(n)].copy_(p.to(dtype))
     h = torch.from_numpy(g.node_feat.astype(np.float64))
     x = torch.from_numpy(g.coord.astype(np.float64))
-    ho, xo = ref(h, x, edges)
+    ho, xo = ref(h, x, edges, act_round=torch_ref.round_bf16_st if bf else None)
     (ho.sum() + xo.sum()).backward()
+    ho32, xo32 = ref32(h.float(), x.float(), edges)
+    (ho32.sum() + xo32.sum()).backward()
     ho2, xo2 = mod(h.to(dtype).cuda(), x.float().cuda(), [e.cuda() for e in edges], None)
     (ho2.float().sum() + xo2.sum()).backward()
-    errs = {"h_out": _rel(ho2, ho), "x_out": _rel(xo2, xo)}
-    refp = {n.replace("layers.", "gcl_"): p for n, p in ref.named_parameters()}
-    for n, p in mod.named_parameters():
-        errs["d" + n] = _rel(p.grad, refp[n].grad)
-    print({k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
-    bad = {k: v for k, v in errs.items() if not v <= tol}
+    errs = {"h_out": _rel(ho2, ho), "x_out": _rel(xo2, xo), **_grads_rel(mod.named_parameters(),
+                                                                        ref.named_parameters(), ren)}
+    e32 = {"h_out": _rel(ho32, ho), "x_out": _rel(xo32, xo), **_grads_rel(ref32.named_parameters(),
+                                                                         ref.named_parameters())}
+    e32 = {k.replace("layers.", "gcl_"): v for k, v in e32.items()}
+    bounds = _stack_bounds(e32, dtype)
+    for k, v in errs.items():
+        record_error(k, v, bounds[k])
+        if not bf:
+            record_error(k + " (torch fp32 cpu)", e32[k], bounds[k])
+    bad = {k: v for k, v in errs.items() if not v <= bounds[k]}
     assert not bad, bad
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 1e-1)])
-def test_mpnn_stack(dtype, tol):
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mpnn_stack(dtype, record_error):
     # non-equivariant stack (2 layers, 16-dim edge features) on a skewed-degree graph
+    import copy
     from pymolecular_amd.models.EGNN import MPNN
     torch.manual_seed(3)
     H, FE = 128, 16
@@ -113,27 +138,35 @@ def test_mpnn_stack(dtype, tol):
     edges = [torch.from_numpy(g.rows().astype(np.int64)), torch.from_numpy(g.col.astype(np.int64))]
     ref = torch_ref.MPNNRef(H, H, 32, FE, n_layers=2).double()
     mod = MPNN(H, H, 32, FE, n_layers=2).cuda().to(dtype)
+    bf = dtype == torch.bfloat16
     with torch.no_grad():
-        if dtype == torch.bfloat16:
+        if bf:
             for p in ref.parameters():
                 p.copy_(p.to(torch.bfloat16).double())
+    ref32 = copy.deepcopy(ref).float()
+    ren = lambda n: n.replace("layers.", "gcl_")  # noqa: E731
     pm = dict(mod.named_parameters())
     for n, p in ref.named_parameters():
         with torch.no_grad():
-            pm[n.replace("layers.", "gcl_")].copy_(p.to(dtype))
-    rd = (lambda t: t.to(torch.bfloat16).double()) if dtype == torch.bfloat16 else (lambda t: t)
+            pm[ren(n)].copy_(p.to(dtype))
+    rd = (lambda t: t.to(torch.bfloat16).double()) if bf else (lambda t: t)
     h = rd(torch.from_numpy(g.node_feat.astype(np.float64)))
     ea = rd(torch.from_numpy(g.edge_attr.astype(np.float64)))
-    ho = ref(h, edges, ea)
+    ho = ref(h, edges, ea, act_round=torch_ref.round_bf16_st if bf else None)
     ho.sum().backward()
+    ho32 = ref32(h.float(), edges, ea.float())
+    ho32.sum().backward()
     ho2 = mod(h.to(dtype).cuda(), [e.cuda() for e in edges], ea.to(dtype).cuda())
     ho2.float().sum().backward()
-    errs = {"h_out": _rel(ho2, ho)}
-    refp = {n.replace("layers.", "gcl_"): p for n, p in ref.named_parameters()}
-    for n, p in mod.named_parameters():
-        errs["d" + n] = _rel(p.grad, refp[n].grad)
-    print({k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
-    bad = {k: v for k, v in errs.items() if not v <= tol}
+    errs = {"h_out": _rel(ho2, ho), **_grads_rel(mod.named_parameters(), ref.named_parameters(), ren)}
+    e32 = {"h_out": _rel(ho32, ho), **_grads_rel(ref32.named_parameters(), ref.named_parameters())}
+    e32 = {k.replace("layers.", "gcl_"): v for k, v in e32.items()}
+    bounds = _stack_bounds(e32, dtype)
+    for k, v in errs.items():
+        record_error(k, v, bounds[k])
+        if not bf:
+            record_error(k + " (torch fp32 cpu)", e32[k], bounds[k])
+    bad = {k: v for k, v in errs.items() if not v <= bounds[k]}
     assert not bad, bad
 
 
