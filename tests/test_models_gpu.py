@@ -67,20 +67,34 @@ def test_egcl_layer_forward_backward(dtype, tol, edges_in_d):
 
 
 def _stack_bounds(errs_fp32_cpu, dtype):
-    """Per-quantity bounds of the stack tests.
+    """Per-quantity bounds of the stack tests from the per-layer contract and the conditioning.
 
-    bf16: 2e-2 against a float64 reference whose activations are rounded to bf16 between layers, as
-    the device stores them (so the per-layer contract applies to the stack).  fp32: 1e-5, or twice
-    what the same stack in plain torch fp32 on the CPU reaches against float64 when 4-layer
-    compounding alone exceeds 1e-5."""
+    The same stack in plain torch fp32 on the CPU, against float64, measures each quantity's
+    condition: err_fp32 ~ kappa * u_fp32.  A first-order forward error bound at another precision is
+    kappa * u.  fp32: max(1e-5, 2 err_fp32).  bf16: max(2e-2, err_fp32 * u_bf16 / u_fp32) with
+    u_bf16 / u_fp32 = 2^-8 / 2^-24.  Well-conditioned quantities keep the contract; only those whose
+    sums largely cancel (the coordinate MLP's weight gradients) get the looser bound."""
     if dtype == torch.bfloat16:
-        return {k: 2e-2 for k in errs_fp32_cpu}
+        return {k: max(2e-2, v * 2.0 ** 16) for k, v in errs_fp32_cpu.items()}
     return {k: max(1e-5, 2.0 * v) for k, v in errs_fp32_cpu.items()}
 
 
 def _grads_rel(mod_named, ref_named, rename=lambda n: n):
     refp = {rename(n): p for n, p in ref_named}
     return {"d" + n: _rel(p.grad, refp[n].grad) for n, p in mod_named}
+
+
+def _loss_weights(N, F, dtype):
+    """Weights of the stack tests' loss <h_out, w_h> + <x_out, w_x>.
+
+    fp32: all ones, the workloads' sum-of-outputs loss.  bf16: seeded N(0, 1) weights.  With a
+    constant upstream coordinate gradient, the coordinate MLP's weight gradients are sums of edge
+    pairs that nearly cancel (delta_ij = -delta_ji while m_ij ~ m_ji); random weights remove that
+    pairing (the sums still cancel partly, which the bounds account for)."""
+    if dtype == torch.float32:
+        return torch.ones((N, F), dtype=torch.float64), torch.ones((N, 3), dtype=torch.float64)
+    r = np.random.Generator(np.random.PCG64(77))
+    return torch.from_numpy(r.standard_normal((N, F))), torch.from_numpy(r.standard_normal((N, 3)))
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
@@ -98,7 +112,7 @@ def test_egnn_stack(dtype, record_error):
         if bf:
             for p in ref.parameters():
                 p.copy_(p.to(torch.bfloat16).double())
-    ref32 = copy.deepcopy(ref).float()
+    refc = copy.deepcopy(ref).float()   # plain torch fp32 on the CPU: the conditioning
     # state dicts map 1:1 except the layer container name
     ren = lambda n: n.replace("layers.", "gcl_")  # noqa: E731
     pm = dict(mod.named_parameters())
@@ -107,22 +121,27 @@ def test_egnn_stack(dtype, record_error):
             pm[ren(n)].copy_(p.to(dtype))
     h = torch.from_numpy(g.node_feat.astype(np.float64))
     x = torch.from_numpy(g.coord.astype(np.float64))
+    wh, wx = _loss_weights(g.N, 16, dtype)
     ho, xo = ref(h, x, edges, act_round=torch_ref.round_bf16_st if bf else None)
-    (ho.sum() + xo.sum()).backward()
-    ho32, xo32 = ref32(h.float(), x.float(), edges)
-    (ho32.sum() + xo32.sum()).backward()
+    ((ho * wh).sum() + (xo * wx).sum()).backward()
+    hoc, xoc = refc(h.float(), x.float(), edges)
+    ((hoc * wh.float()).sum() + (xoc * wx.float()).sum()).backward()
+    refp = copy.deepcopy(refc).double()   # float64 without activation rounding: the conditioning's reference
+    for p in refp.parameters():
+        p.grad = None
+    hop, xop = refp(h, x, edges)
+    ((hop * wh).sum() + (xop * wx).sum()).backward()
     ho2, xo2 = mod(h.to(dtype).cuda(), x.float().cuda(), [e.cuda() for e in edges], None)
-    (ho2.float().sum() + xo2.sum()).backward()
+    ((ho2.float() * wh.float().cuda()).sum() + (xo2 * wx.float().cuda()).sum()).backward()
     errs = {"h_out": _rel(ho2, ho), "x_out": _rel(xo2, xo), **_grads_rel(mod.named_parameters(),
                                                                         ref.named_parameters(), ren)}
-    e32 = {"h_out": _rel(ho32, ho), "x_out": _rel(xo32, xo), **_grads_rel(ref32.named_parameters(),
-                                                                         ref.named_parameters())}
-    e32 = {k.replace("layers.", "gcl_"): v for k, v in e32.items()}
-    bounds = _stack_bounds(e32, dtype)
+    ec = {"h_out": _rel(hoc, hop), "x_out": _rel(xoc, xop), **_grads_rel(refc.named_parameters(),
+                                                                        refp.named_parameters())}
+    ec = {k.replace("layers.", "gcl_"): v for k, v in ec.items()}
+    bounds = _stack_bounds(ec, dtype)
     for k, v in errs.items():
         record_error(k, v, bounds[k])
-        if not bf:
-            record_error(k + " (torch fp32 cpu)", e32[k], bounds[k])
+        record_error(k + " (torch fp32 cpu)", ec[k], bounds[k])
     bad = {k: v for k, v in errs.items() if not v <= bounds[k]}
     assert not bad, bad
 
@@ -143,7 +162,7 @@ def test_mpnn_stack(dtype, record_error):
         if bf:
             for p in ref.parameters():
                 p.copy_(p.to(torch.bfloat16).double())
-    ref32 = copy.deepcopy(ref).float()
+    refc = copy.deepcopy(ref).float()   # plain torch fp32 on the CPU: the conditioning
     ren = lambda n: n.replace("layers.", "gcl_")  # noqa: E731
     pm = dict(mod.named_parameters())
     for n, p in ref.named_parameters():
@@ -152,20 +171,25 @@ def test_mpnn_stack(dtype, record_error):
     rd = (lambda t: t.to(torch.bfloat16).double()) if bf else (lambda t: t)
     h = rd(torch.from_numpy(g.node_feat.astype(np.float64)))
     ea = rd(torch.from_numpy(g.edge_attr.astype(np.float64)))
+    wh, _ = _loss_weights(g.N, 32, dtype)
     ho = ref(h, edges, ea, act_round=torch_ref.round_bf16_st if bf else None)
-    ho.sum().backward()
-    ho32 = ref32(h.float(), edges, ea.float())
-    ho32.sum().backward()
+    (ho * wh).sum().backward()
+    hoc = refc(h.float(), edges, ea.float())
+    (hoc * wh.float()).sum().backward()
+    refp = copy.deepcopy(refc).double()   # float64 without activation rounding: the conditioning's reference
+    for p in refp.parameters():
+        p.grad = None
+    hop = refp(h, edges, ea)
+    (hop * wh).sum().backward()
     ho2 = mod(h.to(dtype).cuda(), [e.cuda() for e in edges], ea.to(dtype).cuda())
-    ho2.float().sum().backward()
+    (ho2.float() * wh.float().cuda()).sum().backward()
     errs = {"h_out": _rel(ho2, ho), **_grads_rel(mod.named_parameters(), ref.named_parameters(), ren)}
-    e32 = {"h_out": _rel(ho32, ho), **_grads_rel(ref32.named_parameters(), ref.named_parameters())}
-    e32 = {k.replace("layers.", "gcl_"): v for k, v in e32.items()}
-    bounds = _stack_bounds(e32, dtype)
+    ec = {"h_out": _rel(hoc, hop), **_grads_rel(refc.named_parameters(), refp.named_parameters())}
+    ec = {k.replace("layers.", "gcl_"): v for k, v in ec.items()}
+    bounds = _stack_bounds(ec, dtype)
     for k, v in errs.items():
         record_error(k, v, bounds[k])
-        if not bf:
-            record_error(k + " (torch fp32 cpu)", e32[k], bounds[k])
+        record_error(k + " (torch fp32 cpu)", ec[k], bounds[k])
     bad = {k: v for k, v in errs.items() if not v <= bounds[k]}
     assert not bad, bad
 
