@@ -51,6 +51,7 @@ extern "C" {
 #define EGNN_ERR_WORKSPACE 5   /* workspace or schedule buffer too small */
 #define EGNN_ERR_CSR 6         /* rowptr not monotone / not [0..E], or a col index out of [0, N) */
 #define EGNN_ERR_HIP 7         /* a HIP runtime call or kernel launch failed */
+#define EGNN_ERR_SCRATCH 8     /* the call needs more than egnn_fwd_static's fixed scratch */
 
 /* activation / weight dtype of h, edge_feat, weights, out_msg and grads
  * (coordinates, out_mov and grad_coord are always fp32) */
@@ -142,6 +143,26 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides,
                  const void* b1, const void* b2, const void* bx1,
                  void* out_msg, float* out_mov, void* node_proj,
                  const void* sched, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Allocation-free forward.  No counterpart in the reference: for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid hipMalloc).  The same computation and kernels as egnn_fwd, with
+ * the workspace in a fixed device array inside the library instead of caller
+ * memory: EGNN_FWD_STATIC_SCRATCH_BYTES per GPU, held from the first call on that
+ * GPU until the process ends.  Calls whose egnn_fwd_workspace_bytes exceed it
+ * return EGNN_ERR_SCRATCH before touching the device.  The caller still provides
+ * inputs, outputs and the schedule (built once, beforehand).  It calls no
+ * allocator.  All calls on one GPU share the array: calls that overlap on one
+ * GPU (several streams or host threads) race.  The stream must belong to the
+ * current device. */
+#define EGNN_FWD_STATIC_SCRATCH_BYTES ((size_t)128 << 20)
+int32_t egnn_fwd_static(const EgnnDims* dims, const EgnnStrides* strides,
+                        const void* h, const float* coord, const void* edge_feat,
+                        const int32_t* rowptr, const int32_t* col, const int32_t* edge_ids,
+                        const void* w1_msg, const void* w2_msg, const void* w1_mov, const void* w2_mov,
+                        const void* b1, const void* b2, const void* bx1,
+                        void* out_msg, float* out_mov, void* node_proj,
+                        const void* sched, void* stream);
 
 /* Fused backward by recomputation.  Takes the forward inputs plus the
  * incoming gradients grad_out_msg (N, O) and grad_out_mov (N, 3), and writes

@@ -12,6 +12,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libpymolecular_egnn.so")
 
 EGNN_OK = 0
+EGNN_ERR_SCRATCH = 8
+FWD_STATIC_SCRATCH_BYTES = 128 << 20   # include/egnn.h EGNN_FWD_STATIC_SCRATCH_BYTES
 EGNN_F32 = 0
 EGNN_BF16 = 1
 
@@ -19,7 +21,7 @@ EGNN_BF16 = 1
 EXPORTED = (
     "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
     "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_node_proj_bytes",
-    "egnn_fwd", "egnn_bwd",
+    "egnn_fwd", "egnn_fwd_static", "egnn_bwd",
     "egnn_node_bwd_workspace_bytes", "egnn_node_fwd", "egnn_node_bwd",
     "egnn_dense_fwd", "egnn_dense_wgrad_workspace_bytes", "egnn_dense_wgrad",
     "egnn_profile_enable", "egnn_profile_read",
@@ -54,7 +56,7 @@ class EgnnNodeDims(ctypes.Structure):
 
 _lib = None
 
-ABI_VERSION = 5   # include/egnn.h egnn_abi_version()
+ABI_VERSION = 6   # include/egnn.h egnn_abi_version()
 
 
 def _check_stamp() -> None:
@@ -113,6 +115,8 @@ def lib() -> ctypes.CDLL:
     L.egnn_node_proj_bytes.argtypes = [ctypes.POINTER(EgnnDims)]
     L.egnn_fwd.restype = c_int32
     L.egnn_fwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 18 + [c_size_t, P]
+    L.egnn_fwd_static.restype = c_int32
+    L.egnn_fwd_static.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 18
     L.egnn_bwd.restype = c_int32
     L.egnn_bwd.argtypes = [ctypes.POINTER(EgnnDims), ctypes.POINTER(EgnnStrides)] + [P] * 27 + [c_size_t, P]
     ND = ctypes.POINTER(EgnnNodeDims)

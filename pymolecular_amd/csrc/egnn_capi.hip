@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 5;
+constexpr int32_t kAbiVersion = 6;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -104,6 +104,7 @@ const char* egnn_status_string(int32_t status) {
     case EGNN_ERR_WORKSPACE: return "workspace or schedule buffer too small";
     case EGNN_ERR_CSR: return "invalid CSR: rowptr not monotone from 0 to E, or col index outside [0, N)";
     case EGNN_ERR_HIP: return "HIP runtime call or kernel launch failed";
+    case EGNN_ERR_SCRATCH: return "the graph needs more workspace than the allocation-free forward's fixed scratch";
     default: return "unknown status";
   }
 }

@@ -89,3 +89,16 @@ def test_graph_builder_arguments_checked_on_the_host():
     assert L.egnn_radius_graph(buf, 100, buf, 2, 64, ctypes.c_double(-1.0), 8, buf, buf, 800, buf, big,
                                ctypes.byref(ne), None) == 2   # negative cutoff
     assert L.egnn_knn_graph(buf, 100, buf, 2, 4096, 8, buf, buf, 800, buf, big, ctypes.byref(ne), None) == 2
+
+
+def test_static_forward_rejects_graphs_beyond_its_scratch():
+    # the size check comes before any device access: a 2M-node layer needs 1 GB of node projections
+    L = _capi.lib()
+    d = _capi.EgnnDims(N=2_000_000, E=18_000_000, F=128, FE=16, H=128, O=128, M=128, equivariant=0, mean_agg=0,
+                       dtype=1)
+    assert L.egnn_fwd_workspace_bytes(d) > _capi.FWD_STATIC_SCRATCH_BYTES
+    s = _capi.EgnnStrides(h=128, coord=4, edge=16, msg=128, mov=3)
+    assert L.egnn_fwd_static(d, s, *([None] * 18)) == _capi.EGNN_ERR_SCRATCH
+    assert "scratch" in _capi.status_string(_capi.EGNN_ERR_SCRATCH)
+    bad = _capi.EgnnDims(N=10, E=20, F=128, FE=0, H=96, O=96, M=96, equivariant=1, mean_agg=0, dtype=1)
+    assert L.egnn_fwd_static(bad, s, *([None] * 18)) == 2
