@@ -1188,7 +1188,7 @@ template <int NU>
 __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8;
   constexpr int KH = H / 32, KO = O / 32;
-  constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
+  constexpr int NUS = NU > 0 ? 16 * NU : 8;         // slot rows of the edge-feature tile
   constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 halves (8 KB)
   static_assert(CH == NRB * 64 * 8, "chain and edge-major buffers share one size");
   // activation buffers, one array so that the final reduction can use all of it:
@@ -1196,13 +1196,13 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_act[6 * CH];
   __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];    // A fragments of W_hl (S5)
   __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A fragments of W_hl^T (S2)
-  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NU > 0 ? TE * FEP : 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NUS * TE];   // edge features, slot-major (put_ut)
   __shared__ __attribute__((aligned(16))) float s_b2[O];
   __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
   bf16* const s_ga2 = s_act;
   bf16* const s_ga2N = s_act + CH;
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const int rb = w & 7, hf = w >> 3;
   const bf16* PQ = (const bf16*)a.PQ;
   const bf16* ef = (const bf16*)a.ef;
@@ -1215,6 +1215,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int LDW = 15;   // loader wave
 
   for (int q = threadIdx.x; q < O; q += 1024) s_b2[q] = a.fr.b2f[q];
+  // slot rows at and past F_E stay zero (the tile loop writes rows below F_E only)
+  for (int q = FE * TE + threadIdx.x; q < NUS * TE; q += 1024) s_u[0][q] = s_u[1][q] = (bf16)0.0f;
   for (int q = threadIdx.x; q < NRB * KO * kFragElems / 8; q += 1024)
     reinterpret_cast<bf16x8*>(s_whl)[q] = reinterpret_cast<const bf16x8*>(a.fr.hl)[q];
   for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 1024)
@@ -1234,8 +1236,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
   int ld_ri, ld_rj, ld_eid = 0;
   auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
-    const int e0 = (int)(tt * TE) + (l & 31);
-    const int e = e0 < (int)E ? e0 : (int)E - 1;
+    const uint32_t e0 = (uint32_t)(tt * TE) + (l & 31);
+    const uint32_t e = e0 < (uint32_t)E ? e0 : (uint32_t)E - 1;
     ld_ri = a.erow[e];
     ld_rj = a.col[e];
     if constexpr (NU > 0) ld_eid = eidp[e];
@@ -1261,10 +1263,11 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   };
   // ---- S1 of tile tt: m1 (chain and edge-major, buffers of parity par), s1 = SiLU'(pre1)
   auto stage1 = [&](int64_t tt, int par, bf16x4& s1o) {
-    const bool v = tt * TE + hf * 16 + c < E;
-    const bf16x8 u = (NU > 0 && 8 * g + 8 <= FE) ? ue : zero_chunk<bf16>();
-    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, [edge][slot], for dW_e
-      *reinterpret_cast<bf16x8*>(s_u[par] + (hf * 16 + c) * FEP + 8 * g) = v ? u : zero_chunk<bf16>();
+    // No masks on the edge features: chunks past F_E (a copy of slot 0's chunk) meet zero columns of
+    // W_u, and the edges past E (indices clamped to real rows) have g_a2 = 0, so they add nothing to dW_e.
+    const bf16x8 u = NU > 0 ? ue : zero_chunk<bf16>();
+    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, slot-major, for dW_e
+      put_ut(s_u[par], hf, c, g, u);
     f32x4 acc = zero4();
     mma(acc, wu, u);
     mma(acc, Ipq, pq);   // + P_i + Q_j
@@ -1299,31 +1302,30 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
     const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
     const int64_t base = t * TE;
-    const bool valid = base + hf * 16 + c < E;
+    const bool valid = (int)base + hf * 16 + c < (int)E;
     // the incoming message gradient of the wave's rows (used in S4), the next tile's
     // gathers (its S1 runs at the end of this tile), the indices of the tile after it
-    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][hf * 16 + c] * a.sgm + 16 * rb + 4 * g);
+    const uint32_t ri = (uint32_t)s_ri[sl0][hf * 16 + c];
+    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (uint64_t)ri * (uint32_t)a.sgm + 16 * rb + 4 * g);
     gather(sl1);
     const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
     load_idx(t2);
 
     // ---- S2: s2 = SiLU'(W_hl^T m1 + b2) -------------------------------------------
-    bf16x4 s2;
+    f32x4 s2;
     {
       f32x4 acc = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
 #pragma unroll
       for (int kc = 0; kc < KH; ++kc)
         mma(acc, *reinterpret_cast<const bf16x8*>(s_whlT + ((rb * KH + kc) * 64 + l) * 8),
             get_chain(s_act + (2 + par) * CH, kc, hf, l));
-      f32x4 d;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) d[i] = silu_yd<bf16>(acc[i]).d;
-      s2 = pack4(d);
+      for (int i = 0; i < 4; ++i) s2[i] = silu_yd<bf16>(acc[i]).d;
     }
     // ---- S4: g_a2 = gm_i SiLU'(pre2), in the same interval (own rows only) --------
     {
-      const f32x4 gm = valid ? unpack4(gmr) : zero4();
-      const f32x4 d = unpack4(s2);
+      const f32x4 gm = valid ? unpack4(gmr) : zero4();   // zero g_a2 on the edges past E
+      const f32x4 d = s2;
       f32x4 ga;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -1353,18 +1355,11 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       for (int cb = 0; cb < 4; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, 4 * hf + cb, l));
       // dW_e rows rb: sum over this half's edges of g_a1[h][e] e[e][slot] (the other half's slots are zero)
       if constexpr (NU > 0) {
-        const f32x4 t1 = transpose_block(g1, I);
-        bf16x8 ga1N = zero_chunk<bf16>();
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ga1N[4 * hf + i] = (bf16)t1[i];
+        const bf16x8 ga1N = half_edge_chunk(transpose_block(g1, I), hf);
 #pragma unroll
         for (int ub = 0; ub < NU; ++ub) {
           if (16 * ub >= FE) continue;   // column block past the edge features
-          const int slot = 16 * ub + c;
-          bf16x8 un;
-#pragma unroll
-          for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[par][kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
-          mma(acc_wu[ub], ga1N, un);
+          mma(acc_wu[ub], ga1N, get_ut(s_u[par], 16 * ub + c, g));   // slots past F_E read zero rows
         }
       }
     }

@@ -73,6 +73,26 @@ __device__ __forceinline__ bf16x8 chain_edge_major(const bf16* buf, int blk, int
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
+// Edge-feature tile stored slot-major for the dW_e products: row `slot` holds the tile's 32
+// edges in kappa_chain order, so the B operand of lane (c, g) (edges kappa_chain(g, s) of one
+// slot) is one 16-byte read.  Edge 16 nb + c sits at position 8 (c >> 2) + 4 nb + (c & 3).
+__device__ __forceinline__ void put_ut(bf16* buf, int nb, int c, int g, const bf16x8& u) {
+  bf16* p = buf + 8 * g * TE + 8 * (c >> 2) + 4 * nb + (c & 3);   // slots 8g .. 8g + 7 of the edge
+#pragma unroll
+  for (int s = 0; s < 8; ++s) p[s * TE] = u[s];
+}
+__device__ __forceinline__ bf16x8 get_ut(const bf16* buf, int slot, int g) {
+  return *reinterpret_cast<const bf16x8*>(buf + slot * TE + 8 * g);
+}
+// The A chunk over the tile's 32 edges (kappa_chain) of a C-block transposed to edge-major
+// (transpose_block) that covers only edge block nb: elements 4 nb .. 4 nb + 3, zeros elsewhere.
+// nb must be wave-uniform (a select of whole registers, no per-element moves).
+__device__ __forceinline__ bf16x8 half_edge_chunk(const f32x4& t, int nb) {
+  const u32x2 v = __builtin_bit_cast(u32x2, pack4(t));
+  const u32x4 q = nb ? u32x4{0u, 0u, v[0], v[1]} : u32x4{v[0], v[1], 0u, 0u};
+  return __builtin_bit_cast(bf16x8, q);
+}
+
 __device__ __forceinline__ int rank_of(uint32_t mask, int k) {
   const uint32_t below = (k >= 31) ? 0xffffffffu : ((2u << k) - 1u);
   return __popc(mask & below) - 1;
