@@ -140,6 +140,12 @@ struct Gemm2Args {
   const int32_t* b_kidx;   // n-contiguous B only: row k of B is row b_kidx[k] of the array
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
+// Streaming node products (egnn_stream.hip): bf16, A k-contiguous with M >= kStreamMinRows rows,
+// K in {128, 256}, N in {128, 256}, K * N <= 32768, no split-K, ones row or B row gather.
+// launch_gemm2 takes them first for the shapes they cover.
+constexpr int64_t kStreamMinRows = 65536;
+bool stream_gemm_ok(const Gemm2Args& g, bool compute_bf16);
+int launch_stream_gemm(const Gemm2Args& g, hipStream_t st);
 // Two independent products, in one launch when both take the 32 x 64 bf16 tiles (else one after the other).
 int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf16, hipStream_t st);
 // Weight-gradient GEMM over edges with k-contiguous bf16 operands (feature-major

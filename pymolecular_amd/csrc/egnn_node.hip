@@ -505,6 +505,15 @@ __device__ __forceinline__ bf16x8 join_tr(const bf16x4v& lo, const bf16x4v& hi) 
 }
 }  // namespace
 
+// The split-K product's ones row is the last row of the result and alone in its row tile of BM rows:
+// the first row tile computes it instead, and the grid has one row tile fewer.
+__host__ __device__ __forceinline__ bool ones_row_folded(const Gemm2Args& g, int BM) {
+  return g.partial != nullptr && g.ksplit > 0 && g.M > 1 && g.a_ones_row == g.M - 1 && (g.M - 1) % BM == 0;
+}
+__host__ __forceinline__ int64_t row_tiles(const Gemm2Args& g, int BM) {
+  return ones_row_folded(g, BM) ? (g.M - 1) / BM : cdiv(g.M, BM);
+}
+
 // BM x BN output tile per 256-thread block (2 x 2 waves), K in slices of BK
 // staged through NBUF LDS buffers (2: the next slice is loaded into registers
 // while the current one is multiplied; 1: one buffer, refilled after each slice).
@@ -548,6 +557,16 @@ __device__ __forceinline__ void gemm_bf16_tile(const Gemm2Args& g, int bx, int b
   for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // a ones row alone past the last full row tile (the bias row of [X | 1]^T dY): tile row 0's first
+  // wave row also sums the B columns (one MFMA against an all-ones A chunk per column block), so
+  // no extra row tile has to read all of B again
+  const bool fold = ones_row_folded(g, BM) && bx == 0 && wm == 0;
+  f32x4 oacc[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) oacc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  bf16x8 ones;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) ones[u] = (bf16)1.0f;
 
   bf16x8 ra[NLA], rb[NLB];
   auto load_stage = [&](int64_t k0) {
@@ -652,6 +671,10 @@ __device__ __forceinline__ void gemm_bf16_tile(const Gemm2Args& g, int bx, int b
       for (int i = 0; i < MI; ++i)
 #pragma unroll
         for (int j = 0; j < NJ; ++j) mma(acc[i][j], a[i], b[j]);
+      if (fold) {
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) mma(oacc[j], ones, b[j]);
+      }
     }
     if (NBUF == 1) {   // refill the one buffer once every wave is done with it
       if (more) {
@@ -666,6 +689,14 @@ __device__ __forceinline__ void gemm_bf16_tile(const Gemm2Args& g, int bx, int b
     __syncthreads();
   }
 
+  if (fold && gq == 0) {   // every row of oacc holds the column sums: row 0 of lane group 0
+    float* P = g.partial + ((int64_t)bz * g.M + g.a_ones_row) * g.N;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int64_t n = n0 + wn * WN + 16 * j + c;
+      if (n < g.N) P[n] = oacc[j][0];
+    }
+  }
   // ---- epilogue: the fp32 tile goes through LDS so that every global access is a 16-byte row segment
 #pragma unroll
   for (int i = 0; i < MI; ++i)
@@ -1076,7 +1107,7 @@ int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf1
   // the first product on 32 x 64 tiles, the second (a split-K reduction) on 64 x 64 tiles
   const bool tiled = e1 && e2 && bf16_tiled_ok(g1, compute_bf16) && bf16_tiled_ok(g2, compute_bf16) &&
                      !bf16_big_tiles(g1) && !bf16_big_tiles(g2) && g1.ksplit <= 0 && g2.ksplit > 0;
-  const int64_t gx1 = cdiv(g1.M, 32), gy1 = cdiv(g1.N, 64), gx2 = cdiv(g2.M, 64), gy2 = cdiv(g2.N, 64);
+  const int64_t gx1 = cdiv(g1.M, 32), gy1 = cdiv(g1.N, 64), gx2 = row_tiles(g2, 64), gy2 = cdiv(g2.N, 64);
   const int64_t n1 = gx1 * gy1 * splits_of(g1), n2 = gx2 * gy2 * splits_of(g2);
   if (!tiled || n1 + n2 >= (int64_t(1) << 31)) {
     int r = e1 ? launch_gemm2(g1, compute_bf16, st) : 0;
@@ -1099,6 +1130,7 @@ int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf1
 
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0) return 0;
+  if (stream_gemm_ok(g, compute_bf16)) return launch_stream_gemm(g, st);
   const unsigned gz = splits_of(g);
   const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
   auto al4 = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 4 == 0); };
@@ -1106,7 +1138,7 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
     const bool big = bf16_big_tiles(g);
     const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
     if (!big && g.ksplit > 0) {   // split-K reductions over node-sized K: 64 x 64 tiles
-      const dim3 gs((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
+      const dim3 gs((unsigned)row_tiles(g, 64), (unsigned)cdiv(g.N, 64), gz);
       if (g.a_kc && g.b_nc) hipLaunchKernelGGL((gemm_bf16_kernel<true, true, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
       else if (g.a_kc) hipLaunchKernelGGL((gemm_bf16_kernel<true, false, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
       else if (g.b_nc) hipLaunchKernelGGL((gemm_bf16_kernel<false, true, 64, 64, 64, 2>), gs, dim3(256), 0, st, g);
@@ -1125,7 +1157,7 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
         return (int)hipGetLastError();
       }
     }
-    const dim3 gb((unsigned)cdiv(g.M, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
+    const dim3 gb((unsigned)row_tiles(g, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
 #define GB_LAUNCH(AK, BNC)                                                                         \
     do {                                                                                           \
       if (narrow) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 32, 64, 2>), gb, dim3(256), 0, st, g); \

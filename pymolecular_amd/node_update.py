@@ -187,17 +187,23 @@ class DenseFn(torch.autograd.Function):
         Np = wp.shape[0]
         gy2 = _rowmajor(_pad_to8(gy.to(dt).reshape(-1, Nout), 1))
         gx = None
-        if ctx.needs_input_grad[0]:
-            gx = (gy2 @ wp)[:, :Kin].reshape(*lead, Kin)
+        L = _capi.lib()
+        code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
+        st = torch.cuda.current_stream(xp.device).cuda_stream
+        if ctx.needs_input_grad[0]:   # gx = gy w, the same product as the forward with w^T as the weight
+            gx = torch.empty((N, Kp), dtype=dt, device=xp.device)
+            if N:
+                check("egnn_dense_fwd", L.egnn_dense_fwd(code, N, Np, Kp, gy2.data_ptr(), gy2.stride(0),
+                                                         wp.t().contiguous().data_ptr(), None, gx.data_ptr(),
+                                                         Kp, st))
+            gx = gx[:, :Kin].reshape(*lead, Kin)
         gw = torch.empty((Np, Kp), dtype=dt, device=xp.device)
         gb = torch.empty((Np,), dtype=dt, device=xp.device) if ctx.has_b else None
-        L = _capi.lib()
         nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kp, Np)
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=xp.device)
-        code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
         rc = L.egnn_dense_wgrad(code, N, Kp, Np, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
                                 gy2.data_ptr() if N else None, gy2.stride(0) if N else Np, gw.data_ptr(), _ptr(gb),
-                                ws.data_ptr(), nbytes, torch.cuda.current_stream(xp.device).cuda_stream)
+                                ws.data_ptr(), nbytes, st)
         check("egnn_dense_wgrad", rc)
         gw = gw[:Nout, :Kin].to(ctx.wdt[0])
         return gx, gw, None if gb is None else gb[:Nout].to(ctx.wdt[1])

@@ -57,9 +57,10 @@ def test_node_update_matches_reference(dtype, tol, N, K1, K2, Hn, Fo, residual, 
 
 
 def test_node_update_large_bf16():
-    # 300k nodes: the large-grid tile shapes (128 x 128 for K = 256, 64 x 128 in 32-deep stages for
-    # K = 128, n tiles of a row block adjacent) and long split-K slices
-    test_node_update_matches_reference(torch.bfloat16, 2e-2, 300000, 128, 128, 128, 128, True, True)
+    # 300,001 nodes (a partial last 16-row tile): the streaming node products (one pass over the rows,
+    # weights in LDS; bias, SiLU with the stored pre-activation, SiLU', residual epilogues) and long
+    # split-K slices
+    test_node_update_matches_reference(torch.bfloat16, 2e-2, 300001, 128, 128, 128, 128, True, True)
 
 
 def test_node_update_deterministic_and_empty():
@@ -84,7 +85,7 @@ def test_node_update_deterministic_and_empty():
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 2e-2)])
 @pytest.mark.parametrize("N,K,Nout,bias", [(19363, 5, 128, True), (3000, 128, 128, False), (500, 20, 36, True),
-                                         (0, 16, 24, True)])
+                                         (0, 16, 24, True), (200003, 128, 128, True)])
 def test_dense_weight_gradient(dtype, tol, N, K, Nout, bias):
     from pymolecular_amd.node_update import DenseFn
     r = np.random.Generator(np.random.PCG64(N + K))
