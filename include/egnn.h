@@ -238,11 +238,14 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
                          size_t workspace_bytes, void* stream);
 
 /* ---- instrumentation (no reference counterpart) ---------------------------
- * When enabled, every kernel launch made by egnn_fwd / egnn_bwd / egnn_node_* is bracketed
- * by HIP events recorded on the caller's stream, grouped by kernel class.
- * egnn_profile_read synchronises on those events and returns the summed
- * device time and the launch count of one class.  Off by default; enabling
- * clears previous records.  Not thread-safe; for benchmarks only. */
+ * egnn_profile_enable(class_mask): the kernel launches of the classes whose bit
+ * (1 << class) is set in class_mask, made by egnn_fwd / egnn_bwd / egnn_node_* /
+ * egnn_dense_*, are bracketed by HIP events recorded on the caller's stream;
+ * 0 turns recording off, EGNN_PROFILE_ALL records every class.  Every call clears
+ * the previous records.  egnn_profile_read synchronises on those events and
+ * returns the summed device time and the launch count of one class.  Off by
+ * default.  Not thread-safe; for benchmarks only. */
+#define EGNN_PROFILE_ALL 0xFF
 #define EGNN_K_FWD_EDGE 0     /* fused forward edge kernel             */
 #define EGNN_K_FWD_FIXUP 1    /* forward split/empty-row fix-up         */
 #define EGNN_K_BWD_EDGE 2     /* fused backward edge kernel            */
@@ -252,7 +255,7 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
 #define EGNN_K_PREP 6         /* weight-fragment preparation           */
 #define EGNN_K_NODE_UPDATE 7  /* node update GEMMs (egnn_node_fwd/bwd) */
 #define EGNN_K_COUNT 8
-int32_t egnn_profile_enable(int32_t on);
+int32_t egnn_profile_enable(int32_t class_mask);
 int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches);
 
 /* ---- graph construction (the step before the layer) ------------------------

@@ -56,7 +56,7 @@ class EgnnNodeDims(ctypes.Structure):
 
 _lib = None
 
-ABI_VERSION = 6   # include/egnn.h egnn_abi_version()
+ABI_VERSION = 7   # include/egnn.h egnn_abi_version()
 
 
 def _check_stamp() -> None:
@@ -148,8 +148,14 @@ def lib() -> ctypes.CDLL:
     return L
 
 
-def profile_enable(on: bool) -> None:
-    check("egnn_profile_enable", lib().egnn_profile_enable(1 if on else 0))
+PROFILE_ALL = 0xFF   # include/egnn.h EGNN_PROFILE_ALL
+
+
+def profile_enable(on: bool, classes=None) -> None:
+    """Record the launches of every kernel class (or of ``classes``, a list of K_* values); clears
+    earlier records.  ``on=False`` stops recording."""
+    mask = 0 if not on else (PROFILE_ALL if classes is None else sum(1 << k for k in classes))
+    check("egnn_profile_enable", lib().egnn_profile_enable(mask))
 
 
 def profile_read() -> dict:

@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
   const int64_t E = a.E;
   const int64_t nwt = (int64_t)gridDim.x * 4;
 
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < a.ntiles; t += nwt) {
+  for (int64_t t = a.tile0 + (int64_t)blockIdx.x * 4 + wave; t < a.ntiles; t += nwt) {
     // the lane's fragment offset, opaque once per tile: the weight addresses are
     // formed at each load instead of being hoisted out of the tile loop
     int lo8 = l * 8;
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
         m1c[kc][nb] = pack_chunk<T>(y0, y1);
         s1c[kc][nb] = pack_chunk<T>(d0, d1);
         if (valid[nb]) {
-          T* dst = Dm1 + ee[nb] * H + 32 * kc + 4 * g;
+          T* dst = Dm1 + (ee[nb] - a.fbase) * H + 32 * kc + 4 * g;
           store4<T>(dst, y0);
           store4<T>(dst + 16, y1);
         }
@@ -179,7 +179,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
         mc[kp][nb] = pack_chunk<T>(y0, y1);
         s2c[kp][nb] = pack_chunk<T>(d0, d1);
         if (valid[nb]) {
-          T* dst = Dm + ee[nb] * O + 32 * kp + 4 * g;
+          T* dst = Dm + (ee[nb] - a.fbase) * O + 32 * kp + 4 * g;
           store4<T>(dst, y0);
           store4<T>(dst + 16, y1);
         }
@@ -227,10 +227,10 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
           }
           gqc[mp][nb] = pack_chunk<T>(g0, g1);
           if (valid[nb]) {
-            T* dq = Dgq + ee[nb] * M + 32 * mp + 4 * g;
+            T* dq = Dgq + (ee[nb] - a.fbase) * M + 32 * mp + 4 * g;
             store4<T>(dq, g0);
             store4<T>(dq + 16, g1);
-            T* dp = Dp + ee[nb] * M + 32 * mp + 4 * g;
+            T* dp = Dp + (ee[nb] - a.fbase) * M + 32 * mp + 4 * g;
             store4<T>(dp, p0);
             store4<T>(dp + 16, p1);
           }
@@ -278,7 +278,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
         }
         ga2c[kp][nb] = pack_chunk<T>(y0, y1);
         if (valid[nb]) {
-          T* dst = Dga2 + ee[nb] * O + 32 * kp + 4 * g;
+          T* dst = Dga2 + (ee[nb] - a.fbase) * O + 32 * kp + 4 * g;
           store4<T>(dst, y0);
           store4<T>(dst + 16, y1);
         }
@@ -347,8 +347,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
 
 template <typename T, int H, int O, int M, int NB, bool EQ>
 static int launch_bwd_t(const BwdArgs& a, hipStream_t st) {
-  if (a.ntiles > 0) {
-    int blocks = (int)std::min<int64_t>(cdiv(a.ntiles, 4), 256 * 4);
+  if (a.ntiles > a.tile0) {
+    int blocks = (int)std::min<int64_t>(cdiv(a.ntiles - a.tile0, 4), 256 * 4);
     hipLaunchKernelGGL((bwd_edge_kernel<T, H, O, M, NB, EQ>), dim3(blocks), dim3(256), 0, st, a);
   }
   return (int)hipGetLastError();

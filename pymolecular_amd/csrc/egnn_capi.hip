@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 6;
+constexpr int32_t kAbiVersion = 7;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -19,7 +19,7 @@ int32_t hip_status(int e) { return e == (int)hipSuccess ? EGNN_OK : EGNN_ERR_HIP
 
 // ---- instrumentation: HIP events around launches, grouped by kernel class ----
 struct ProfRec { int cls; hipEvent_t a, b; };
-bool g_prof_on = false;
+int32_t g_prof_mask = 0;   // bit k: record the launches of kernel class k
 std::vector<ProfRec> g_prof;
 std::vector<hipEvent_t> g_event_pool;   // events of cleared records, reused (kept until the process ends)
 
@@ -36,7 +36,7 @@ hipEvent_t prof_event() {
 struct ProfScope {
   hipStream_t st; int cls; hipEvent_t a = nullptr, b = nullptr;
   ProfScope(int c, hipStream_t s) : st(s), cls(c) {
-    if (!g_prof_on) return;
+    if (!((g_prof_mask >> cls) & 1)) return;
     a = prof_event();
     b = prof_event();
     if (!a || !b) {
@@ -259,23 +259,11 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.ldE = w.ldE;
   a.geo = w.geo;
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
-  {
+  if (coop || wide_supported(s)) {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
-    const int r = coop ? launch_coop_bwd(s, a, w.nblk, st)
-                  : wide_supported(s) ? launch_wide_bwd(s, a, st) : launch_bwd(s, a, st);
+    const int r = coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_wide_bwd(s, a, st);
     if ((rc = hip_status(r)) != EGNN_OK) return rc;
   }
-
-  // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
-  float* gcoord = s.eq ? grad_coord : nullptr;
-  {
-    ProfScope ps(EGNN_K_NODE_REDUCE, st);
-    const float* gres = s.coord_res ? grad_out_mov : nullptr;
-    if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
-                                          strides->coord, gres, strides->mov, st))) != EGNN_OK)
-      return rc;
-  }
-
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
   // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
@@ -322,23 +310,61 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     }
   }
   if (!coop && !wide) {
-    Gemm2Args g{};
-    g.M = s.H + 1; g.N = s.O; g.K = s.E;
-    g.A = w.Dm1; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.H;
-    g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = s.bf16; g.b_nc = 1;
-    if ((rc = splitk2(g, w.dWhl)) != EGNN_OK) return rc;
+    // one-wave-per-tile kernel, one edge chunk at a time: each chunk's factor products right after
+    // its kernel (sums into per-chunk rows, added in chunk order below when there are several)
+    const int TW = bwd_tile_edges(s);
+    const int64_t Lw = (int64_t)(s.H + 1) * s.O, Lm = (int64_t)(s.O + 1) * s.M;
+    for (int ch = 0; ch < w.nchunk; ++ch) {
+      const int64_t e0 = (int64_t)ch * w.chunkE, e1 = std::min<int64_t>(s.E, e0 + w.chunkE);
+      a.tile0 = e0 / TW; a.ntiles = cdiv(e1, TW); a.fbase = e0;
+      {
+        ProfScope ps(EGNN_K_BWD_EDGE, st);
+        if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
+      }
+      const bool one = w.nchunk == 1;
+      Gemm2Args g{};
+      g.M = s.H + 1; g.N = s.O; g.K = e1 - e0;
+      g.A = w.Dm1; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.H;
+      g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = s.bf16; g.b_nc = 1;
+      if ((rc = splitk2(g, one ? w.dWhl : w.chunkres + ch * Lw)) != EGNN_OK) return rc;
+      if (s.eq) {
+        float* res_m = w.chunkres + w.nchunk * Lw;
+        float* res_p = res_m + w.nchunk * Lm;
+        Gemm2Args m{};
+        m.M = s.O + 1; m.N = s.M; m.K = e1 - e0;
+        m.A = w.Dm; m.lda = s.O; m.a_bf16 = s.bf16; m.a_kc = 0; m.a_ones_row = s.O;
+        m.B = w.Dgq; m.ldb = s.M; m.b_bf16 = s.bf16; m.b_nc = 1;
+        if ((rc = splitk2(m, one ? w.dW1m : res_m + ch * Lm)) != EGNN_OK) return rc;
+        Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (g_phi in column 3 of Gx)
+        p.M = s.M; p.N = 1; p.K = e1 - e0;
+        p.A = w.Dp; p.lda = s.M; p.a_bf16 = s.bf16; p.a_kc = 0; p.a_ones_row = -1;
+        p.B = w.Gx + 4 * e0 + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
+        if ((rc = splitk2(p, one ? w.dw2m : res_p + ch * s.M)) != EGNN_OK) return rc;
+      }
+    }
+    if (w.nchunk > 1) {
+      ProfScope ps(EGNN_K_WGRAD, st);
+      if ((rc = hip_status(launch_sum_rows(w.chunkres, w.nchunk, Lw, w.dWhl, st))) != EGNN_OK) return rc;
+      if (s.eq) {
+        const float* res_m = w.chunkres + w.nchunk * Lw;
+        if ((rc = hip_status(launch_sum_rows(res_m, w.nchunk, Lm, w.dW1m, st))) != EGNN_OK) return rc;
+        if ((rc = hip_status(launch_sum_rows(res_m + w.nchunk * Lm, w.nchunk, s.M, w.dw2m, st))) != EGNN_OK)
+          return rc;
+      }
+    }
   }
+  // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
+  float* gcoord = s.eq ? grad_coord : nullptr;
+  {
+    ProfScope ps(EGNN_K_NODE_REDUCE, st);
+    const float* gres = s.coord_res ? grad_out_mov : nullptr;
+    if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
+                                          strides->coord, gres, strides->mov, st))) != EGNN_OK)
+      return rc;
+  }
+
+
   if (s.eq && !coop && !wide) {
-    Gemm2Args g{};
-    g.M = s.O + 1; g.N = s.M; g.K = s.E;
-    g.A = w.Dm; g.lda = s.O; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.O;
-    g.B = w.Dgq; g.ldb = s.M; g.b_bf16 = s.bf16; g.b_nc = 1;
-    if ((rc = splitk2(g, w.dW1m)) != EGNN_OK) return rc;
-    Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (g_phi in column 3 of Gx)
-    p.M = s.M; p.N = 1; p.K = s.E;
-    p.A = w.Dp; p.lda = s.M; p.a_bf16 = s.bf16; p.a_kc = 0; p.a_ones_row = -1;
-    p.B = w.Gx + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
-    if ((rc = splitk2(p, w.dw2m)) != EGNN_OK) return rc;
     Gemm2Args d{};   // dw_d = sum_e g_a1[e] r^2[e]
     d.M = s.H; d.N = 1; d.K = s.E;
     d.A = w.Gh; d.lda = s.H; d.a_bf16 = s.bf16; d.a_kc = 0; d.a_ones_row = -1;
@@ -391,9 +417,9 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   return hip_status(launch_finalize(s, f, st));
 }
 
-int32_t egnn_profile_enable(int32_t on) {
+int32_t egnn_profile_enable(int32_t class_mask) {
   prof_clear();
-  g_prof_on = on != 0;
+  g_prof_mask = class_mask & EGNN_PROFILE_ALL;
   return EGNN_OK;
 }
 

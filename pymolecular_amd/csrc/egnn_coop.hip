@@ -63,7 +63,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) f32x4 s_geo[3][EQ ? TE : 1];
   seg_lut_init(s_lut, threadIdx.x);
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* ef = (const bf16*)a.ef;
   const int64_t E = a.E;
   const int N = (int)a.N;
@@ -166,7 +166,9 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     bf16x8 u[2];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      u[nb] = (FE > 0 && 8 * g + 8 <= FE) ? uf[nb] : zero_chunk<bf16>();
+      // chunks past F_E (copies of slot 0's chunk) meet zero columns of W_u: only F_E = 0 (nothing
+      // loaded) needs a zero chunk, and the r^2 slots are set below
+      u[nb] = FE > 0 ? uf[nb] : zero_chunk<bf16>();
       if (EQ && 8 * g == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
         const float r2 = s_geo[slot][nb * 16 + c][3];
         const bf16 hi = (bf16)r2;

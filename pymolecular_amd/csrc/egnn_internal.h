@@ -86,7 +86,16 @@ struct BwdWs {
   int64_t LW;
   float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
   int64_t ldE;     // row pitch of the factors (feature-major for the wide kernels)
+  // one-wave-per-tile kernel: the factors hold chunkE edges; per-chunk sums of the factor products
+  int64_t chunkE;
+  int nchunk;
+  float* chunkres; // [nchunk][(H + 1) O + (O + 1) M + M]
 };
+// Edges per chunk of the one-wave-per-tile backward: the whole graph when its per-edge factor rows
+// take at most kFactorBudget bytes, else half of it (a multiple of 32 edges) -- half the factor
+// memory for one more kernel and product launch.
+constexpr size_t kFactorBudget = size_t(320) << 20;
+int64_t factor_chunk_edges(const LayerShape& s);
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
 // Split-K products [A | 1]^T B over K rows with an M x N result: rows per
@@ -194,6 +203,8 @@ struct BwdArgs {
   const void* gmsg; int64_t sgm;
   const float* gmov; int64_t sgx;
   void* Dm1; void* Dm; void* Dgq; void* Dga2; void* Dp; void* Gh; float* Gx; float* R2;
+  int64_t tile0;   // one-wave-per-tile kernel: tiles [tile0, ntiles) of this launch (an edge chunk)
+  int64_t fbase;   // first edge of the factor rows Dm1 ... Dp (they hold one chunk; Gh, Gx, R2 hold all edges)
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
   int64_t ldE;     // wide kernels: row pitch of the feature-major factors Dm1 ... Dp

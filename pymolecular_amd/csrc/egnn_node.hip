@@ -91,20 +91,31 @@ int64_t wgrad_ksplit(int64_t K) {
   return cdiv(ks, 64) * 64;
 }
 
+int64_t factor_chunk_edges(const LayerShape& s) {
+  const int64_t E = std::max<int64_t>(s.E, 1);
+  const size_t per_edge = (size_t)(s.H + 2 * s.O + (s.eq ? 2 * s.M : 0)) * s.esz;   // Dm1, Dm, Dga2 (, Dgq, Dp)
+  const int64_t whole = cdiv(E, kTileEdges) * kTileEdges;
+  if ((size_t)E * per_edge <= kFactorBudget) return whole;
+  return cdiv(cdiv(E, 2), kTileEdges) * kTileEdges;
+}
+
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   char* b = (char*)base;
   size_t off = frag_layout(s, b, &w->fr, 0, true);
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
   const bool coop = coop_supported(s), wide = wide_supported(s);
-  // wide kernels store the factors feature-major with a 16-byte aligned row pitch
+  // wide kernels store the factors feature-major with a 16-byte aligned row pitch; the
+  // one-wave-per-tile kernel stores one edge chunk of them at a time
   w->ldE = wide ? (int64_t)align_up((size_t)std::max<int64_t>(s.E, 1), 8) : std::max<int64_t>(s.E, 1);
-  const size_t E = (size_t)w->ldE;
+  w->chunkE = (coop || wide) ? w->ldE : factor_chunk_edges(s);
+  w->nchunk = (coop || wide) ? 1 : (int)cdiv(std::max<int64_t>(s.E, 1), w->chunkE);
+  const size_t E = (size_t)w->ldE, EF = (size_t)w->chunkE;
   w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
-  w->Dm1 = coop ? nullptr : take(E * s.H * s.esz);
-  w->Dm = coop ? nullptr : take(E * s.O * s.esz);
-  w->Dgq = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
-  w->Dga2 = coop ? nullptr : take(E * s.O * s.esz);
-  w->Dp = (s.eq && !coop) ? take(E * s.M * s.esz) : nullptr;
+  w->Dm1 = coop ? nullptr : take(EF * s.H * s.esz);
+  w->Dm = coop ? nullptr : take(EF * s.O * s.esz);
+  w->Dgq = (s.eq && !coop) ? take(EF * s.M * s.esz) : nullptr;
+  w->Dga2 = coop ? nullptr : take(EF * s.O * s.esz);
+  w->Dp = (s.eq && !coop) ? take(EF * s.M * s.esz) : nullptr;
   // the cooperative kernels store Gh / Gx rows for every edge slot of the last 32-edge tile
   const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), kTileEdges) * kTileEdges : E;
   w->Gh = take(Er * s.H * s.esz);
@@ -117,10 +128,18 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
   w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N);
-  if (!coop)
-    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, s.E), splitk_parts(s.O + 1, s.M, s.E),
-                                       splitk_parts(s.M, 1, s.E), splitk_parts(s.H, 1, s.E),
+  if (!coop) {   // the factor products run over one chunk of edges at a time, dw_d and dW_e over all
+    // (the split length is rounded per K: the shorter last chunk may need more partial rows)
+    const int64_t lastE = std::max<int64_t>(s.E, 1) - (int64_t)(w->nchunk - 1) * w->chunkE;
+    for (const int64_t K : {w->chunkE, lastE})
+      w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, K), splitk_parts(s.O + 1, s.M, K),
+                                         splitk_parts(s.M, 1, K)});
+    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H, 1, s.E),
                                        splitk_parts(s.H, std::max(s.FE, 1), s.E)});
+  }
+  w->chunkres = (coop || wide || w->nchunk == 1)
+                    ? nullptr
+                    : (float*)take((size_t)w->nchunk * ((s.H + 1) * s.O + (s.O + 1) * s.M + s.M) * sizeof(float));
   if (wide) {
     const int64_t ks = wgrad_ksplit(s.E);
     const int64_t nw = cdiv(std::max<int64_t>(s.E, 1), ks);

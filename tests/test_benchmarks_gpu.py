@@ -33,7 +33,11 @@ def test_speed_sweep_small():
 
 
 def test_memory_sweep_small():
+    # peak device memory of one backward call, inputs included: the fused layer keeps one E x H
+    # scratch, the eager provider every per-edge activation and its autograd saves
     from pymolecular_amd.benchmarks.test_mem import run_memory_benchmark
     rows = run_memory_benchmark([1000, 20000])
     for n, e, pt, hip in rows:
         assert hip != "OOM" and float(hip) > 0
+        if n == 20000:
+            assert pt == "OOM" or float(hip) < float(pt), (hip, pt)
