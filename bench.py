@@ -73,6 +73,9 @@ def parse():
     ap.add_argument("--cpu-min-edges", type=int, default=200_000, help="least edges in the CPU sample")
     ap.add_argument("--cpu-repeats", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--probe", action="store_true",
+                    help="also time the identity-MLP instrument of the MPNN edge kernels (gather / segment-sum "
+                         "data movement alone) at the power-law workload and print its line")
     ap.add_argument("--copy-probe", action="store_true",
                     help="end with three 256 MiB device copies (scale reference for HBM byte counters)")
     return ap.parse_args()
@@ -354,6 +357,60 @@ def run_workload(k, dtype, a, g=None):
     return out
 
 
+def probe_identity(a, k=5):
+    """Gather / segment-sum data movement of the MPNN layer alone: the edge kernels with the MLP
+    replaced by identity (EGNN_FLAG_PROBE_IDENTITY, an instrument), one layer forward + backward per
+    step, on the full power-law graph.  Bytes per kernel, every gathered row counted once per edge:
+      forward:      E (8 + 2 H s + F_E s) + N O s      (indices, P_i and Q_j, edge features; row sums out)
+      backward:     E (8 + O s + H s)                 (indices, the row's message gradient; dL/dpre1 out)
+      node reduce:  E (2 H s + 4) + N (8 + 2 H s)     (dL/dpre1 by row and by source, CSC ids; dP | dQ out)"""
+    import torch
+    from pymolecular_amd import _capi, fused, graphs
+    g = graphs.make_workload(k)
+    N, E, H, s = g.N, g.E, 128, 2
+    FE = g.edge_attr.shape[1]
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device="cuda").manual_seed(11)
+    h = torch.randn((N, H), generator=gen, device=dev).to(torch.bfloat16)
+    ef = torch.from_numpy(g.edge_attr).to(dev, torch.bfloat16)
+    w1 = (torch.randn((2 * H + FE, H), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+    w2 = (torch.randn((H, H), generator=gen, device=dev) * 0.05).to(torch.bfloat16)
+    gm = torch.randn((N, H), generator=gen, device=dev).to(torch.bfloat16)
+    rowptr, col = torch.from_numpy(g.rowptr).to(dev), torch.from_numpy(g.col).to(dev)
+
+    def step():
+        fused.egnn_fused_forward(h, None, ef, rowptr, col, None, w1, w2, equivariant=False, probe_identity=True)
+        fused.egnn_fused_backward(h, None, ef, rowptr, col, None, w1, w2, None, None, None, None, None, gm, None,
+                                  equivariant=False, probe_identity=True)
+
+    for _ in range(a.warmup):
+        step()
+    torch.cuda.synchronize()
+    _capi.profile_enable(True, [_capi.K_FWD_EDGE, _capi.K_BWD_EDGE, _capi.K_NODE_REDUCE])
+    for _ in range(a.steps):
+        step()
+    torch.cuda.synchronize()
+    prof = _capi.profile_read()
+    _capi.profile_enable(False)
+    model = {"fwd_edge": E * (8 + 2 * H * s + FE * s) + N * H * s,
+             "bwd_edge": E * (8 + H * s + H * s),
+             "node_reduce": E * (2 * H * s + 4) + N * (8 + 2 * H * s)}
+    out = {}
+    tot_b = tot_t = 0.0
+    for cls, nbytes in model.items():
+        t, n = prof[cls]
+        ms = t / max(n, 1)
+        gbs = nbytes / (ms / 1e3) / 1e9
+        out[cls] = dict(ms_per_launch=ms, algorithmic_bytes=nbytes, achieved_gbs=gbs, frac=gbs / PEAK["hbm_gbs"])
+        tot_b += nbytes
+        tot_t += ms
+    gbs = tot_b / (tot_t / 1e3) / 1e9
+    return {"metric": "HBM fraction of the gather / segment-sum portion (identity-MLP instrument of the MPNN "
+                      "edge kernels)", "value": gbs / PEAK["hbm_gbs"], "unit": "fraction of 8 TB/s",
+            "achieved_gbs": gbs, "config": {"workload": DESCR[k], "N": N, "E": E, "steps": a.steps},
+            "kernels": out}
+
+
 def main():
     a = parse()
     if a.gpus != 1:
@@ -365,6 +422,8 @@ def main():
     for k, dtype in todo:
         out = run_workload(k, dtype, a)
         print(json.dumps(out), flush=True)
+    if a.probe:
+        print(json.dumps(probe_identity(a)), flush=True)
     if a.copy_probe:
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)
         dst = torch.empty_like(src)

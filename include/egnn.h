@@ -81,13 +81,20 @@ typedef struct EgnnDims {
                           EGNN_FLAG_COORD_RESIDUAL (equivariant only): the layer's coordinate output is
                           x' = x + agg_x (egnn_clean.py:97, coord += agg): egnn_fwd writes coord + agg_x
                           into out_mov, and egnn_bwd writes grad_out_mov + (d agg_x / d coord)^T
-                          grad_out_mov into grad_coord, the whole gradient of x' with respect to x */
+                          grad_out_mov into grad_coord, the whole gradient of x' with respect to x;
+                          EGNN_FLAG_PROBE_IDENTITY: an instrument, not the layer: egnn_fwd / egnn_bwd
+                          run the edge kernels with the MLP replaced by identity (message P_i + Q_j +
+                          W_u e without SiLU or W_hl; dL/dpre1 = grad_out_msg of the row) and keep their
+                          gathers, tile schedule and row / source sums, so that the data movement of
+                          the gather / segment-sum portion can be timed alone.  bf16 MPNN at H = 128
+                          only; the outputs are not the layer's */
 } EgnnDims;
 
 #define EGNN_WEIGHTS_PACKED 0
 #define EGNN_WEIGHTS_LINEAR 1
 #define EGNN_FLAG_ACCUMULATE_GRAD_H 1
 #define EGNN_FLAG_COORD_RESIDUAL 2
+#define EGNN_FLAG_PROBE_IDENTITY 4
 
 /* Row strides in elements; the inner dimension is always contiguous. */
 typedef struct EgnnStrides {

@@ -36,6 +36,7 @@ K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_redu
 WEIGHTS_PACKED, WEIGHTS_LINEAR = 0, 1   # include/egnn.h EGNN_WEIGHTS_*
 FLAG_ACCUMULATE_GRAD_H = 1              # include/egnn.h EGNN_FLAG_ACCUMULATE_GRAD_H
 FLAG_COORD_RESIDUAL = 2                 # include/egnn.h EGNN_FLAG_COORD_RESIDUAL
+FLAG_PROBE_IDENTITY = 4                 # include/egnn.h EGNN_FLAG_PROBE_IDENTITY (instrument only)
 
 
 class EgnnDims(ctypes.Structure):

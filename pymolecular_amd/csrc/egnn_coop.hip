@@ -42,7 +42,10 @@ using namespace tile;
 // memory is carried in registers from one tile to the next and the loads a
 // wave waits on are never followed by loads under a branch (either makes the
 // compiler wait for every outstanding load).
-template <int H, int O, int M, int W, bool EQ>
+// ID (instrument only, the layer with the MLP replaced by identity: MPNN): the message is
+// P_i + Q_j + W_u e with no SiLU and no W_hl product; the gathers, the tile schedule and the
+// per-row sums are those of the layer.
+template <int H, int O, int M, int W, bool EQ, bool ID = false>
 __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
   constexpr int KH = H / 32, KO = O / 32;
@@ -162,6 +165,7 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     }
   };
   // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows, into s_m1[par]
+  f32x4 m1keep[BH][2];   // ID: the messages of the next tile, kept in registers from S1 to S2
   auto stage1 = [&](int slot, int par) {
     bf16x8 u[2];
 #pragma unroll
@@ -184,10 +188,14 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         f32x4 acc = zero4();
         mma(acc, wu[j], u[nb]);
         mma(acc, Ipq, pq[j][nb]);   // + P_i + Q_j
-        f32x4 x;
+        if constexpr (ID) {
+          m1keep[j][nb] = acc;
+        } else {
+          f32x4 x;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
-        put_chain(s_m1[par], hb, nb, l, x);
+          for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
+          put_chain(s_m1[par], hb, nb, l, x);
+        }
       }
     }
   };
@@ -225,6 +233,10 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       const f32x4 b2v = *reinterpret_cast<const f32x4*>(s_b2 + 16 * ob + 4 * g);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
+        if constexpr (ID) {
+          mreg[j][nb] = m1keep[j][nb];
+          continue;
+        }
         f32x4 acc = b2v;
 #pragma unroll
         for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1[par], kc, nb, l));
@@ -780,7 +792,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, M = 128, W = 8;
   constexpr int KH = H / 32, KO = O / 32, KM = M / 32;
   constexpr int NO = O / 16, NM = M / 16;
-  constexpr int FEP = 40;                           // row pitch of the edge-feature tile (bf16, 80 bytes)
+  constexpr int NUS = NU > 0 ? 16 * NU : 8;         // slot rows of the edge-feature tile
   constexpr int WP = 136;                           // row pitch of the LDS weight matrices (bf16, 272 bytes)
   constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 edge blocks (8 KB)
   // m1 of the next tile is written while this tile's g_a2 is read: separate
@@ -798,14 +810,16 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
   // [edge][slot] edge features of a tile, by tile parity (the next tile's S1 writes while S5 reads)
-  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NU > 0 ? TE * FEP : 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NUS * TE];   // slot-major (put_ut)
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
   float* const s_b2 = s_vec;
   float* const s_bx1 = s_vec + O;
   float* const s_w2m = s_vec + O + M;
   float* const s_wd = s_vec + O + 2 * M;
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  // slot rows at and past F_E stay zero (the tile loop writes rows below F_E only)
+  for (int q = a.FE * TE + (int)threadIdx.x; q < NUS * TE; q += 512) s_u[0][q] = s_u[1][q] = (bf16)0.0f;
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
   const bf16* ef = (const bf16*)a.ef;
   const bf16* gmsg = (const bf16*)a.gmsg;
@@ -909,12 +923,11 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         u[nb][1] = (bf16)(r2 - (float)hi);
       }
     }
-    // the tile's edge features, [edge][slot], for the dW_e product (zero rows past the end)
+    // the tile's edge features, slot-major, for the dW_e product (zero edges past the end)
     if (NU > 0 && w == 0 && 8 * g < FE) {
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb)
-        *reinterpret_cast<bf16x8*>(s_u[par] + (nb * 16 + c) * FEP + 8 * g) =
-            tt * TE + nb * 16 + c < E ? u[nb] : zero_chunk<bf16>();
+        put_ut(s_u[par], nb, c, g, tt * TE + nb * 16 + c < E ? u[nb] : zero_chunk<bf16>());
     }
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -942,7 +955,18 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     store_idx(1, t1);
   }
   __syncthreads();   // weights, vectors and the first two ring slots in LDS
+  // the incoming message gradient of the wave's rows, loaded one tile ahead of its use (the only
+  // value carried from one tile to the next: a tile old at the top of the next tile); with two
+  // edge-input chunks (NU = 2) the registers are short, and it is loaded in its own tile
+  constexpr bool GM_AHEAD = NU < 2;
+  bf16x4 gmr_next[2];
+  auto load_gm = [&](int slot) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb)
+      gmr_next[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[slot][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
+  };
   if (blockIdx.x < a.ntiles) {
+    if (GM_AHEAD) load_gm(0);
     gather(0);
     stage1(blockIdx.x, 0, 0, s1);
   }
@@ -968,10 +992,9 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       xdel = q[2 + xq];
       xgrd = q[5 + xq];
     }
-    bf16x4 gmr[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
-      gmr[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[sl0][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
+    if (!GM_AHEAD) load_gm(sl0);
+    const bf16x4 gmr[2] = {gmr_next[0], gmr_next[1]};
+    if (GM_AHEAD) load_gm(sl1);
     gather(sl1);
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
@@ -1105,11 +1128,7 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
 #pragma unroll
       for (int ub = 0; ub < NU; ++ub) {
         if (16 * ub >= FE) continue;   // column block past the edge features
-        const int slot = 16 * ub + c;
-        bf16x8 un;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) un[s] = slot < FE ? s_u[par][kappa_chain(g, s) * FEP + slot] : (bf16)0.0f;
-        mma(acc_wu[ub], ga1N, un);
+        mma(acc_wu[ub], ga1N, get_ut(s_u[par], 16 * ub + c, g));   // slots past F_E read zero rows
       }
     }
 #pragma unroll
@@ -1186,7 +1205,9 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
 // S4) and [S5, S1 of the next tile]; m1 and the edge-feature tile are kept by
 // tile parity.  Indices pass through an LDS ring of three tiles and the next
 // tile's gathers are issued at the top of this tile, as in coop_bwd_eq_kernel.
-template <int NU>
+// ID (instrument only): the layer with the MLP replaced by identity, g_a1 = the incoming message
+// gradient of row i; the index ring, the gathers of that gradient and the Gh stores are the layer's.
+template <int NU, bool ID = false>
 __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8;
   constexpr int KH = H / 32, KO = O / 32;
@@ -1285,6 +1306,14 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     *reinterpret_cast<bf16x4*>(s_act + (4 + par) * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(y, I));
   };
 
+  // the incoming message gradient of the wave's rows, loaded one tile ahead of its use in S4 (the
+  // only value carried from one tile to the next: at the top of a tile it is a tile old, so the
+  // memory wait there finds it complete)
+  bf16x4 gmr_next;
+  auto load_gm = [&](int slot) {
+    const uint32_t ri = (uint32_t)s_ri[slot][hf * 16 + c];
+    gmr_next = *reinterpret_cast<const bf16x4*>(gmsg + (uint64_t)ri * (uint32_t)a.sgm + 16 * rb + 4 * g);
+  };
   bf16x4 s1;
   if (blockIdx.x < a.ntiles) {
     const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
@@ -1294,7 +1323,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     store_idx(1, t1);
   }
   __syncthreads();   // weights, vectors and the first two ring slots in LDS
-  if (blockIdx.x < a.ntiles) {
+  if (blockIdx.x < a.ntiles) load_gm(0);
+  if (!ID && blockIdx.x < a.ntiles) {
     gather(0);
     stage1(blockIdx.x, 0, s1);
   }
@@ -1307,11 +1337,18 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     const bool valid = (int)base + hf * 16 + c < (int)E;
     // the incoming message gradient of the wave's rows (used in S4), the next tile's
     // gathers (its S1 runs at the end of this tile), the indices of the tile after it
-    const uint32_t ri = (uint32_t)s_ri[sl0][hf * 16 + c];
-    const bf16x4 gmr = *reinterpret_cast<const bf16x4*>(gmsg + (uint64_t)ri * (uint32_t)a.sgm + 16 * rb + 4 * g);
-    gather(sl1);
+    const bf16x4 gmr = gmr_next;
+    load_gm(sl1);
+    if constexpr (!ID) gather(sl1);
     const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
     load_idx(t2);
+    if constexpr (ID) {
+      const f32x4 gm = valid ? unpack4(gmr) : zero4();
+      *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(gm);
+      store_idx(sl2, t2);
+      __syncthreads();
+      continue;
+    }
 
     // ---- S2: s2 = SiLU'(W_hl^T m1 + b2) -------------------------------------------
     f32x4 s2;
@@ -1416,13 +1453,13 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   }
 }
 
-template <int H, int O, int M, int W, bool EQ>
+template <int H, int O, int M, int W, bool EQ, bool ID = false>
 int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (a.ntiles > 0) {
     // one resident round: 4 waves per SIMD (the launch bound), 16 waves per CU, on 256 CUs; a
     // second round would repeat the weight prologue of every block
     const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * (16 / W));
-    hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ>), dim3(blocks), dim3(W * 64), 0, st, a);
+    hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ, ID>), dim3(blocks), dim3(W * 64), 0, st, a);
   }
   return (int)hipGetLastError();
 }
@@ -1439,9 +1476,11 @@ int launch_bwd_eq(const BwdArgs& a, int nblk, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-int launch_mpnn_bwd16(const BwdArgs& a, int nblk, hipStream_t st) {
+int launch_mpnn_bwd16(const BwdArgs& a, int nblk, bool probe, hipStream_t st) {
   if (a.ntiles > 0) {
-    if (a.FE == 0)
+    if (probe)
+      hipLaunchKernelGGL((mpnn_bwd16_kernel<0, true>), dim3(nblk), dim3(1024), 0, st, a);
+    else if (a.FE == 0)
       hipLaunchKernelGGL((mpnn_bwd16_kernel<0>), dim3(nblk), dim3(1024), 0, st, a);
     else if (a.FE <= 16)
       hipLaunchKernelGGL((mpnn_bwd16_kernel<1>), dim3(nblk), dim3(1024), 0, st, a);
@@ -1483,12 +1522,13 @@ int64_t coop_dw_len(const LayerShape& s) {
 }
 
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+  if (s.probe) return launch_fwd_t<128, 128, 128, 8, false, true>(a, st);   // make_shape: MPNN, H = 128
   if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }
 
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
-  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16(a, nblk, st);
+  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16(a, nblk, s.probe, st);
   return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
 }
 

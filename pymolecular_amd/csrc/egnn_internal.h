@@ -49,6 +49,7 @@ struct LayerShape {
   bool lin;                      // weights in torch.nn.Linear (out, in) layout
   bool accum;                    // egnn_bwd adds into grad_h
   bool coord_res;                // coordinate output x + agg_x, its gradient includes grad_out_mov
+  bool probe;                    // EGNN_FLAG_PROBE_IDENTITY: the identity-MLP instrument (MPNN, bf16, H = 128)
   size_t esz;                    // bytes per activation element
 };
 int make_shape(const EgnnDims* d, LayerShape* s);

@@ -24,9 +24,13 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   if (d->dtype != EGNN_F32 && d->dtype != EGNN_BF16) return EGNN_ERR_DIMS;
   if (d->weight_layout != EGNN_WEIGHTS_PACKED && d->weight_layout != EGNN_WEIGHTS_LINEAR) return EGNN_ERR_DIMS;
   s->lin = d->weight_layout == EGNN_WEIGHTS_LINEAR;
-  if (d->flags & ~(EGNN_FLAG_ACCUMULATE_GRAD_H | EGNN_FLAG_COORD_RESIDUAL)) return EGNN_ERR_DIMS;
+  if (d->flags & ~(EGNN_FLAG_ACCUMULATE_GRAD_H | EGNN_FLAG_COORD_RESIDUAL | EGNN_FLAG_PROBE_IDENTITY))
+    return EGNN_ERR_DIMS;
   s->accum = (d->flags & EGNN_FLAG_ACCUMULATE_GRAD_H) != 0;
   s->coord_res = (d->flags & EGNN_FLAG_COORD_RESIDUAL) != 0;
+  s->probe = (d->flags & EGNN_FLAG_PROBE_IDENTITY) != 0;
+  // the identity instrument exists for the bf16 MPNN layer at H = 128 (cooperative kernels)
+  if (s->probe && (d->equivariant || d->dtype != EGNN_BF16 || d->H != 128 || d->FE > 32)) return EGNN_ERR_DIMS;
   if (s->coord_res && !s->eq) return EGNN_ERR_DIMS;   // no coordinates in the MPNN layer
   if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
   if (d->F < 1 || d->F > 512 || d->F % 16 != 0) return EGNN_ERR_DIMS;

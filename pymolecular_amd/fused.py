@@ -165,8 +165,11 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
 def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
                        w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
-                       linear_weights: bool = False, coord_residual: bool = False):
+                       linear_weights: bool = False, coord_residual: bool = False, probe_identity: bool = False):
     """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``.
+
+    ``probe_identity`` (EGNN_FLAG_PROBE_IDENTITY): an instrument, not the layer -- the edge kernels
+    with the MLP replaced by identity, to time the gather / segment-sum data movement alone.
 
     ``coord_residual`` (equivariant only, EGNN_FLAG_COORD_RESIDUAL): ``out_mov`` is
     the updated coordinate ``coord + agg_x`` instead of ``agg_x``.
@@ -181,6 +184,8 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
     if coord_residual and equivariant:
         dims.flags |= _capi.FLAG_COORD_RESIDUAL
+    if probe_identity:
+        dims.flags |= _capi.FLAG_PROBE_IDENTITY
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev = h.device
     N, O = h.shape[0], dims.O
@@ -207,7 +212,7 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
                         b1, b2, bx1, grad_out_msg, grad_out_mov, *, mean_agg: bool = False,
                         equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
                         linear_weights: bool = False, grad_h_into: Optional[torch.Tensor] = None,
-                        coord_residual: bool = False):
+                        coord_residual: bool = False, probe_identity: bool = False):
     """Backward by recomputation.  Returns a dict of gradients (None where absent),
     weight gradients in the layout of the weights.
 
@@ -241,6 +246,8 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
         grad_h = torch.empty_like(h)
     if coord_residual and equivariant:
         dims.flags |= _capi.FLAG_COORD_RESIDUAL
+    if probe_identity:   # the identity-MLP instrument (see egnn_fused_forward)
+        dims.flags |= _capi.FLAG_PROBE_IDENTITY
     grad_coord = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
     g_w1 = torch.empty_like(w1)
     g_w2 = torch.empty_like(w2)

@@ -102,3 +102,15 @@ def test_static_forward_rejects_graphs_beyond_its_scratch():
     assert "scratch" in _capi.status_string(_capi.EGNN_ERR_SCRATCH)
     bad = _capi.EgnnDims(N=10, E=20, F=128, FE=0, H=96, O=96, M=96, equivariant=1, mean_agg=0, dtype=1)
     assert L.egnn_fwd_static(bad, s, *([None] * 18)) == 2
+
+
+def test_identity_probe_flag_only_for_bf16_mpnn_h128():
+    L = _capi.lib()
+    kw = dict(N=100, E=1000, F=128, FE=16, H=128, O=128, M=128, equivariant=0, mean_agg=0, dtype=1,
+              flags=_capi.FLAG_PROBE_IDENTITY)
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**kw)) > 0
+    for field, value in (("equivariant", 1), ("dtype", 0), ("H", 256)):
+        bad = dict(kw, **{field: value})
+        if field == "H":
+            bad.update(O=256, M=256)
+        assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**bad)) == 0, field

@@ -249,3 +249,38 @@ def test_no_edges(dtype, eq, FE):
     for k, v in r["grads"].items():
         if v is not None:
             assert not np.any(v), k
+
+
+def test_identity_probe_instrument_computes_linear_sums():
+    # the instrument of the gather / segment-sum timing: messages P_i + Q_j + e W_e summed per row,
+    # dL/dpre1 = the row's message gradient summed by row and by source into dh
+    from pymolecular_amd import fused
+    rowptr, col = random_csr(900, (np.arange(900) * 5) % 41 + 2, seed=51)
+    case = Case(rowptr, col, 128, 16, 128, 128, 128, seed=52, eq=False, bias=False)
+    bf = torch.bfloat16
+    h, ef = _dev(case.h, bf), _dev(case.ef, bf)
+    w1, w2 = _dev(case.p["w1_msg"], bf), _dev(case.p["w2_msg"], bf)
+    gm = _dev(case.gm, bf)
+    rp, cl = _dev(case.rowptr), _dev(case.col)
+    out, _ = fused.egnn_fused_forward(h, None, ef, rp, cl, None, w1, w2, equivariant=False, probe_identity=True)
+    g = fused.egnn_fused_backward(h, None, ef, rp, cl, None, w1, w2, None, None, None, None, None, gm, None,
+                                  equivariant=False, probe_identity=True)
+    torch.cuda.synchronize()
+    H = 128
+    hd, efd, W = orc.round_bf16(case.h), orc.round_bf16(case.ef), orc.round_bf16(case.p["w1_msg"])
+    Wn1, Wn2, We = W[:H], W[H:2 * H], W[2 * H:]
+    P, Q = orc.round_bf16(hd @ Wn1), orc.round_bf16(hd @ Wn2)   # stored per node in bf16
+    rows = orc.csr_row_of_edge(case.rowptr)
+    msg = P[rows] + Q[case.col] + efd @ We
+    ref = np.zeros((case.N, H))
+    np.add.at(ref, rows, msg)
+    e_fwd = orc.normwise_rel_err(out.float().cpu().numpy(), ref)
+    gmd = orc.round_bf16(case.gm)
+    dP = np.zeros((case.N, H))
+    dQ = np.zeros((case.N, H))
+    np.add.at(dP, rows, gmd[rows])
+    np.add.at(dQ, case.col, gmd[rows])
+    dh = orc.round_bf16(dP) @ Wn1.T + orc.round_bf16(dQ) @ Wn2.T
+    e_bwd = orc.normwise_rel_err(g["h"].float().cpu().numpy(), dh)
+    print(f"probe forward {e_fwd:.2e} backward dh {e_bwd:.2e}", flush=True)
+    assert e_fwd <= 2e-2 and e_bwd <= 2e-2, (e_fwd, e_bwd)
