@@ -261,7 +261,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   if (coop || wide_supported(s)) {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
-    const int r = coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_wide_bwd(s, a, st);
+    const int r = coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_wide_bwd(s, a, wide_bwd_blocks(s), st);
     if ((rc = hip_status(r)) != EGNN_OK) return rc;
   }
 
@@ -297,16 +297,9 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     if ((rc = wgrad(w.Dm1, w.Dga2, s.H, s.O, w.dWhl)) != EGNN_OK) return rc;   // [dW_hl ; db2]
     if (s.eq) {
       if ((rc = wgrad(w.Dm, w.Dgq, s.O, s.M, w.dW1m)) != EGNN_OK) return rc;  // [dW1_mov ; dbx1]
-      Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (p feature-major, g_phi in column 3 of Gx)
-      p.M = s.M; p.N = 1; p.K = s.E;
-      p.A = w.Dp; p.lda = w.ldE; p.a_bf16 = 1; p.a_kc = 1; p.a_ones_row = -1;
-      p.B = w.Gx + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
-      if ((rc = splitk2(p, w.dw2m)) != EGNN_OK) return rc;
-      Gemm2Args d{};   // dw_d = sum_e g_a1[e] r^2[e]
-      d.M = s.H; d.N = 1; d.K = s.E;
-      d.A = w.Gh; d.lda = s.H; d.a_bf16 = 1; d.a_kc = 0; d.a_ones_row = -1;
-      d.B = w.R2; d.ldb = 1; d.b_bf16 = 0; d.b_nc = 1;
-      if ((rc = splitk2(d, w.dwd)) != EGNN_OK) return rc;
+      // dw2_mov | dw_d (adjacent): the kernel's per-block partials, summed in block order
+      ProfScope ps(EGNN_K_WGRAD, st);
+      if ((rc = hip_status(launch_sum_rows(w.dwpart, s.E > 0 ? w.nblk : 0, w.LW, w.dw2m, st))) != EGNN_OK) return rc;
     }
   }
   if (!coop && !wide) {

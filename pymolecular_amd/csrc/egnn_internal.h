@@ -222,10 +222,14 @@ int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
 // Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
-// from L2, backward writes the per-edge weight-gradient factors (Dm1 ... R2).
+// from L2, backward writes the per-edge weight-gradient factors Dm1, Dm, Dgq, Dga2.
 bool wide_supported(const LayerShape& s);
 int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
-int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
+// The backward runs one persistent 16-wave block per CU and writes per-block partials of dw2_mov
+// and dw_d ([nblk][M | H], EGNN) to BwdArgs::dwpart.
+constexpr int kWideBwdBlocks = 256;
+int wide_bwd_blocks(const LayerShape& s);
+int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
 // Per-edge geometry records for the cooperative kernels (one thread per edge):
 // forward [E][4] = (delta, r^2); backward [E][8] = (r^2, g_phi, delta, grad x_i / deg).
 int bwd_tile_edges(const LayerShape& s);

@@ -119,16 +119,17 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Dm = coop ? nullptr : take(EF * s.O * s.esz);
   w->Dgq = (s.eq && !coop) ? take(EF * s.M * s.esz) : nullptr;
   w->Dga2 = coop ? nullptr : take(EF * s.O * s.esz);
-  w->Dp = (s.eq && !coop) ? take(EF * s.M * s.esz) : nullptr;
+  w->Dp = (s.eq && !coop && !wide) ? take(EF * s.M * s.esz) : nullptr;
   // the cooperative kernels store Gh / Gx rows for every edge slot of the last 32-edge tile
   const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), kTileEdges) * kTileEdges : E;
   w->Gh = take(Er * s.H * s.esz);
   w->Gx = (float*)take(Er * 4 * sizeof(float));
-  w->R2 = coop ? nullptr : (float*)take(E * sizeof(float));
+  w->R2 = (coop || wide) ? nullptr : (float*)take(E * sizeof(float));
   w->geo = ((coop || wide_supported(s)) && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
-  w->nblk = coop ? coop_bwd_blocks(s) : 0;
-  w->LW = coop ? coop_dw_len(s) : 0;
-  w->dwpart = coop ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
+  // per-block partials of the cooperative kernels' weight gradients / the wide kernel's dw2_mov | dw_d
+  w->nblk = coop ? coop_bwd_blocks(s) : (wide && s.eq) ? wide_bwd_blocks(s) : 0;
+  w->LW = coop ? coop_dw_len(s) : (wide && s.eq) ? (int64_t)s.M + s.H : 0;
+  w->dwpart = w->nblk > 0 ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
   w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
   w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N);
@@ -152,9 +153,9 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
   w->dW1m = (float*)take((size_t)(s.O + 1) * s.M * sizeof(float));
-  w->dw2m = (float*)take((size_t)s.M * sizeof(float));
+  w->dw2m = (float*)take((size_t)(s.M + s.H) * sizeof(float));   // dw2_mov | dw_d, one fixed-order sum in the wide path
+  w->dwd = w->dw2m + s.M;
   w->dWe = (float*)take((size_t)s.H * std::max(s.FE, 1) * sizeof(float));
-  w->dwd = (float*)take((size_t)s.H * sizeof(float));
   w->dWn = (float*)take((size_t)(s.F + 1) * 2 * s.H * sizeof(float));
   return off;
 }

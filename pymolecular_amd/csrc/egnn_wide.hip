@@ -42,22 +42,23 @@ __device__ __forceinline__ bf16x8 input_chunk_u(const bf16* ef, int64_t se, int 
 __device__ __forceinline__ void store_bf16x4(bf16* p, const f32x4& v) { *reinterpret_cast<bf16x4*>(p) = pack4(v); }
 
 // Feature-major store of one 16-feature block of a tile: v is the edge-major
-// chunk of lane (c = feature 16 b + c, g) over the edges kappa_chain(g, s);
-// DT[f][e] with row pitch ldE (a multiple of 8).  Edges past E are not written.
-__device__ __forceinline__ void store_fmajor(bf16* DT, int64_t ldE, int64_t row, int64_t base, int64_t E, int g,
-                                             const bf16x8& v) {
-  bf16* p = DT + row * ldE + base;
-  if (base + TE <= E) {
+// chunk of lane (c = feature 16 b + c, g) over the edges kappa_chain(g, s).
+// tile = &DT[16 b][base] of DT[f][e] (row pitch ldE, a multiple of 8; the same
+// for every lane), lane_off = c ldE * 2 bytes; edges past the nvalid of the tile
+// are not written.
+__device__ __forceinline__ void store_fmajor(bf16* tile, uint32_t lane_off, int nvalid, int g, const bf16x8& v) {
+  char* p = reinterpret_cast<char*>(tile) + lane_off;
+  if (nvalid >= TE) {
     bf16x4 lo, hi;
     lo[0] = v[0]; lo[1] = v[1]; lo[2] = v[2]; lo[3] = v[3];
     hi[0] = v[4]; hi[1] = v[5]; hi[2] = v[6]; hi[3] = v[7];
-    *reinterpret_cast<bf16x4*>(p + 4 * g) = lo;
-    *reinterpret_cast<bf16x4*>(p + 16 + 4 * g) = hi;
+    *reinterpret_cast<bf16x4*>(p + 8 * g) = lo;
+    *reinterpret_cast<bf16x4*>(p + 32 + 8 * g) = hi;
   } else {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int k = kappa_chain(g, s);
-      if (base + k < E) p[k] = v[s];
+      if (k < nvalid) reinterpret_cast<bf16*>(p)[k] = v[s];
     }
   }
 }
@@ -263,48 +264,69 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward: recompute, chain rule, per-edge weight-gradient factors
 // ---------------------------------------------------------------------------
+// Wave w owns the 16-row blocks BH w .. BH w + BH - 1 of every stage (H = 16 BH W).  One tile is
+//   S2 m = SiLU(W_hl^T m1 + b2) | S3 q, p, g_q | S4 g_a2 | S5 g_a1 | S6 dL/ddelta | S1 of the next tile
+// with a barrier after each stage.  The memory latencies are kept off the stage boundaries:
+//  * the edge records of the tiles (row, source, edge id, r^2, g_phi) pass through a ring of three
+//    LDS slots, fetched by the loader wave two tiles ahead and stored at the end of a tile;
+//  * the gathers of a tile's S1 (P_i, Q_j, edge features) are issued in S4 of the tile before it, and
+//    S1 runs at the end of that tile; the incoming message gradient rows are loaded one tile ahead;
+//  * each stage's weight fragments (the wave's rows over 256 k, from L2) are issued at the end of the
+//    stage before it, into the registers whose MFMAs have just been issued.
+// dw2_mov = sum_e g_phi p and dw_d = sum_e r^2 g_a1 are summed in fp32, each lane's sums in its own
+// LDS slots (read, added to and written back once per tile, in tile order), and written as per-block
+// partials [gridDim.x][M | H]; the other weight gradients go through the feature-major factors m1,
+// m (EGNN), g_q (EGNN) and g_a2.  W_u's fragments are read from LDS in S1: registers are the limit.
 template <int H, int W, bool EQ, int NUC>
 __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
   constexpr int O = H, M = H;
-  constexpr int BH = H / W / 16, KH = H / 32, KO = O / 32, KM = M / 32;
-  // m1 (S1 -> S2) shares storage with g_a2 (S4 -> S5); m (S2 -> S3) with nothing live
-  __shared__ __attribute__((aligned(16))) bf16 s_buf1[KH * 2 * 64 * 8];
-  __shared__ __attribute__((aligned(16))) bf16 s_m[KO * 2 * 64 * 8];
-  __shared__ __attribute__((aligned(16))) bf16 s_gq[(EQ ? KM : 1) * 2 * 64 * 8];
+  constexpr int BH = H / W / 16;   // 16-row blocks per wave
+  static_assert(BH * 16 * W == H && (BH == 1 || BH == 2), "whole 16-row blocks per wave");
+  constexpr int KF = H / 32;       // k-chunks of a row block's fragments (every dimension is H)
+  __shared__ __attribute__((aligned(16))) bf16 s_buf1[KF * 2 * 64 * 8];   // m1 (S1 -> S2), g_a2 (S4 -> S5)
+  __shared__ __attribute__((aligned(16))) bf16 s_m[(EQ ? KF : 1) * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_gq[(EQ ? KF : 1) * 2 * 64 * 8];
   bf16* const s_m1 = s_buf1;
   bf16* const s_ga2 = s_buf1;
   __shared__ float s_phi[W][TE];
   __shared__ float s_gr[W][TE];
-
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  const bf16* PQ = (const bf16*)a.PQ;
-  const bf16* ef = (const bf16*)a.ef;
-  const bf16* gmsg = (const bf16*)a.gmsg;
-  const bf16* FhlT = (const bf16*)a.fr.hlT;
-  const bf16* FmovT = (const bf16*)a.fr.movT;
-  const bf16* Fmov = (const bf16*)a.fr.mov;
-  const bf16* Fhl = (const bf16*)a.fr.hl;
-  bf16* Dm1 = (bf16*)a.Dm1;
-  bf16* Dm = (bf16*)a.Dm;
-  bf16* Dgq = (bf16*)a.Dgq;
-  bf16* Dp = (bf16*)a.Dp;
-  bf16* Dga2 = (bf16*)a.Dga2;
-  bf16* Gh = (bf16*)a.Gh;
-  const int64_t E = a.E;
-  const int N = (int)a.N;
-
-  bf16x8 wu[BH][NUC];
-#pragma unroll
-  for (int j = 0; j < BH; ++j)
-#pragma unroll
-    for (int uc = 0; uc < NUC; ++uc)
-      wu[j][uc] = load_chunk((const bf16*)a.fr.u + ((int64_t)(w * BH + j) * NUC + uc) * kFragElems + l * 8);
-  // per-row vectors, read from LDS where they are used: b2 (O), bx1 (M), w2_mov (M), w_d (H)
+  // per-row vectors, read where they are used: b2 (O), bx1 (M), w2_mov (M), w_d (H)
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
   float* const s_b2 = s_vec;
   float* const s_bx1 = s_vec + O;
   float* const s_w2m = s_vec + O + M;
   float* const s_wd = s_vec + O + 2 * M;
+  // W_u fragments of the wave's row blocks; per-lane sums of dw2_mov and dw_d (EGNN)
+  __shared__ __attribute__((aligned(16))) bf16 s_wu[W * BH * NUC * kFragElems];
+  __shared__ __attribute__((aligned(16))) float s_dacc[EQ ? W * 64 * BH * 8 : 1];
+  // ring of edge records (tiles t, t + G, t + 2G): [slot][row, source, edge id, r^2, g_phi][edge]
+  __shared__ int s_ring[3][5][TE];
+  auto rec_i = [&](int sl, int f, int k) { return s_ring[sl][f][k]; };
+  auto rec_f = [&](int sl, int f, int k) { return __int_as_float(s_ring[sl][f][k]); };
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const bf16* PQ = (const bf16*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const bf16* gmsg = (const bf16*)a.gmsg;
+  bf16* Dm1 = (bf16*)a.Dm1;
+  bf16* Dm = (bf16*)a.Dm;
+  bf16* Dgq = (bf16*)a.Dgq;
+  bf16* Dga2 = (bf16*)a.Dga2;
+  bf16* Gh = (bf16*)a.Gh;
+  const int64_t E = a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+  const int64_t G = gridDim.x;
+  const int rb0 = BH * w;   // the wave's first row block
+
+  for (int q = threadIdx.x; q < W * BH * NUC * 64; q += W * 64)   // the block's rows of W_u: 8-value chunks
+    *reinterpret_cast<bf16x8*>(s_wu + 8 * q) = load_chunk((const bf16*)a.fr.u + 8 * (int64_t)q);
+  // lane slot of the sums: [w][j][half][l][4] with half 0: dw2_mov rows, 1: dw_d rows
+  float* const dacc = s_dacc + (EQ ? (w * BH * 2 * 64 + l) * 4 : 0);
+  if constexpr (EQ) {
+#pragma unroll
+    for (int j = 0; j < 2 * BH; ++j) *reinterpret_cast<f32x4*>(dacc + j * 256) = zero4();
+  }
   for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
   if constexpr (EQ) {
     for (int q = threadIdx.x; q < M; q += W * 64) {
@@ -313,52 +335,110 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
     }
     for (int q = threadIdx.x; q < H; q += W * 64) s_wd[q] = a.fr.wdf[q];
   }
-  __syncthreads();
-
   const bf16x8 I = ident_chunk(c, g);
 
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-    const int64_t base = t * TE;
-    // The lane's fragment offset, made opaque once per tile so that the weight
-    // addresses are formed at each load (SGPR base + this offset) instead of
-    // being hoisted out of the tile loop as one 64-bit VGPR pair per k-slice.
-    int lo8 = l * 8;
-    __asm__ __volatile__("" : "+v"(lo8));
-    int ri[2], rj[2], eid[2];
-    bool valid[2];
-    float r2[2], gphi[2];
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      valid[nb] = e < E;
-      const int64_t ec = valid[nb] ? e : E - 1;
-      ri[nb] = clampi(a.erow[ec], N);
-      rj[nb] = clampi(a.col[ec], N);
-      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
-      r2[nb] = gphi[nb] = 0.f;
-      if constexpr (EQ) {   // (r^2, g_phi); invalid edges contribute nothing through g_phi = 0
-        const float2 q = *reinterpret_cast<const float2*>(a.geo + ec * 8);
-        r2[nb] = q.x;
-        gphi[nb] = valid[nb] ? q.y : 0.f;
+  // ---- the edge-record ring: raw values of edge l & 31 of a tile (loader wave), stored in LDS in
+  // S4 of the tile; every wave consumes the registers there (an empty asm use), so that no load
+  // issued by the loader alone is still counted where the other waves wait for their own loads
+  constexpr int LDW = W - 1;
+  const int32_t* eidp = a.eids ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
+  int ld_ri = 0, ld_rj = 0, ld_eid = 0;
+  float ld_r2 = 0.f, ld_gp = 0.f;
+  auto load_rec = [&](int64_t tt) {
+    if (w == LDW) {
+      const int64_t e0 = tt * TE + (l & 31);
+      const int64_t e = e0 < E ? e0 : E - 1;
+      ld_ri = a.erow[e];
+      ld_rj = a.col[e];
+      ld_eid = eidp[e];
+      if constexpr (EQ) {
+        const float2 q = *reinterpret_cast<const float2*>(a.geo + e * 8);   // (r^2, g_phi)
+        ld_r2 = q.x;
+        ld_gp = q.y;
       }
     }
+  };
+  auto store_rec = [&](int sl, int64_t tt) {
+    asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_r2), "v"(ld_gp));
+    if (w == LDW && l < TE) {
+      const int64_t e = tt * TE + l;
+      s_ring[sl][0][l] = clampi(ld_ri, N);
+      s_ring[sl][1][l] = clampi(ld_rj, N);
+      s_ring[sl][2][l] = a.eids ? clampi(ld_eid, (int)E) : (int)(e < E ? e : E - 1);
+      s_ring[sl][3][l] = __float_as_int(ld_r2);
+      s_ring[sl][4][l] = __float_as_int(e < E ? ld_gp : 0.f);   // edges past E contribute nothing through g_phi = 0
+    }
+  };
 
-    // ---- S1: m1, s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows ------
-    bf16x4 s1[BH][2];
+  // ---- the gathers of S1 from a ring slot: the wave's features of P_i and Q_j (4 per row block and
+  // lane), the edge-feature chunks (F_E > 0; chunks past F_E read slot 0 and are dropped in S1)
+  bf16x4 pg[2][BH], qg[2][BH];
+  bf16x8 ug[2][NUC];
+  // row block rb holds features 32 (rb / 2) + 8 g + 4 (rb % 2) .. + 4 of P | Q
+  auto pq_off = [&](int j) { return 32 * ((rb0 + j) >> 1) + 4 * ((rb0 + j) & 1); };
+  auto gather = [&](int sl) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const int k = nb * 16 + c;
+      const bf16* pr = PQ + (int64_t)rec_i(sl, 0, k) * 2 * H + 8 * g;
+      const bf16* qr = PQ + (int64_t)rec_i(sl, 1, k) * 2 * H + H + 8 * g;
+      if constexpr (BH == 2) {   // both row blocks: 8 consecutive features
+        const bf16x8 p8 = load_chunk(pr + pq_off(0)), q8 = load_chunk(qr + pq_off(0));
+        pg[nb][0] = bf16x4{p8[0], p8[1], p8[2], p8[3]};
+        pg[nb][1] = bf16x4{p8[4], p8[5], p8[6], p8[7]};
+        qg[nb][0] = bf16x4{q8[0], q8[1], q8[2], q8[3]};
+        qg[nb][1] = bf16x4{q8[4], q8[5], q8[6], q8[7]};
+      } else {
+        pg[nb][0] = *reinterpret_cast<const bf16x4*>(pr + pq_off(0));
+        qg[nb][0] = *reinterpret_cast<const bf16x4*>(qr + pq_off(0));
+      }
+      if (FE > 0) {
+        const bf16* er = ef + (int64_t)rec_i(sl, 2, k) * a.se;
+#pragma unroll
+        for (int uc = 0; uc < NUC; ++uc) {
+          const int s0 = 32 * uc + 8 * g;
+          ug[nb][uc] = load_chunk(er + (s0 + 8 <= FE ? s0 : 0));
+        }
+      }
+    }
+  };
+  // feature-major factor rows: row 16 rb + c of [feature][edge] (pitch ldE) at lane byte offset fmo
+  auto fmrow = [&](int j) { return (int64_t)(16 * (rb0 + j)) * a.ldE; };
+  const uint32_t fmo = (uint32_t)(c * a.ldE) * 2u;
+  auto nvalid_of = [&](int64_t tt) { return (int)(E - tt * TE < TE ? E - tt * TE : TE); };
+
+  // ---- S1 of tile tt: m1 = SiLU(W_u U + P_i + Q_j) to s_m1 and Dm1, s1 = SiLU'
+  bf16x4 s1[BH][2];
+  auto stage1 = [&](int64_t tt, int sl) {
+    bf16x8 u[2][NUC];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float r2 = rec_f(sl, 3, nb * 16 + c);
+#pragma unroll
+      for (int uc = 0; uc < NUC; ++uc) {
+        const int s0 = 32 * uc + 8 * g;
+        u[nb][uc] = zero_chunk<bf16>();
+        if (s0 + 8 <= FE) {
+          u[nb][uc] = ug[nb][uc];
+        } else if (EQ && s0 == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
+          const bf16 hi = (bf16)r2;
+          u[nb][uc][0] = hi;
+          u[nb][uc][1] = (bf16)(r2 - (float)hi);
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
-      const int hb = w * BH + j;
-      __asm__ __volatile__("" ::: "memory");   // keep each row block's fragment loads in its own iteration
-      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+      bf16x8 wu[NUC];
+#pragma unroll
+      for (int uc = 0; uc < NUC; ++uc) wu[uc] = get_norm(s_wu, (rb0 + j) * NUC + uc, l);
       f32x4 y[2];
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int uc = 0; uc < NUC; ++uc)
-          mma(acc, wu[j][uc], input_chunk_u(ef, a.se, eid[nb], a.FE, uc, g, r2[nb], EQ));
-        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
-        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        for (int uc = 0; uc < NUC; ++uc) mma(acc, wu[uc], u[nb][uc]);
+        const f32x4 p = unpack4(pg[nb][j]), q = unpack4(qg[nb][j]);
         f32x4 d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -367,70 +447,150 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
           d[i] = r.d;
         }
         s1[j][nb] = pack4(d);
-        put_chain(s_m1, hb, nb, l, y[nb]);
+        put_chain(s_m1, rb0 + j, nb, l, y[nb]);
       }
-      store_fmajor(Dm1, a.ldE, 16 * hb + c, base, E, g, edge_major(y[0], y[1], I));
+      store_fmajor(Dm1 + fmrow(j) + tt * TE, fmo, nvalid_of(tt), g, edge_major(y[0], y[1], I));
     }
-    __syncthreads();
+  };
+  bf16x4 gmr[BH][2];
+  auto load_gm = [&](int sl) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const bf16* gr = gmsg + (int64_t)rec_i(sl, 0, nb * 16 + c) * a.sgm + 4 * g;
+#pragma unroll
+      for (int j = 0; j < BH; ++j) gmr[j][nb] = *reinterpret_cast<const bf16x4*>(gr + 16 * (rb0 + j));
+    }
+  };
+  // The wave's fragments of a stage: BH x 8 chunks of 1 KB from a uniform base, at the lane's byte
+  // offset lo16 + 4 KB q (q = 0 .. 2 BH - 1) plus an immediate.  The offsets are made opaque (lo16 at
+  // the top of each tile, the others at each use) so that they stay single VGPRs instead of becoming
+  // a 64-bit base per chunk.
+  uint32_t lo16 = (uint32_t)l * 16;
+  bf16x8 fr[BH][KF];
+  auto load_frags = [&](const bf16* F, const f32x4 (&after)[BH][2]) {
+    // the loads come after every MFMA of the stage (they write the registers those MFMAs read)
+#pragma unroll
+    for (int j = 0; j < BH; ++j) __asm__ __volatile__("" : "+v"(lo16) : "v"(after[j][0]), "v"(after[j][1]));
+    const char* Fw = (const char*)(F + (int64_t)rb0 * KF * kFragElems);
+    uint32_t off[2 * BH];
+    off[0] = lo16;
+#pragma unroll
+    for (int q = 1; q < 2 * BH; ++q) {
+      off[q] = lo16 + 4096 * q;
+      __asm__ __volatile__("" : "+v"(off[q]));
+    }
+#pragma unroll
+    for (int j = 0; j < BH; ++j)
+#pragma unroll
+      for (int kc = 0; kc < KF; ++kc) {
+        const int ch = j * KF + kc;
+        fr[j][kc] = *reinterpret_cast<const bf16x8*>(Fw + off[ch >> 2] + 1024 * (ch & 3));
+      }
+  };
+  // acc[j][nb] += fragments x the chain buffer's chunks (each chunk read once, used by every row block)
+  auto stage_mma = [&](f32x4 (&acc)[BH][2], const bf16* buf) {
+#pragma unroll
+    for (int kc = 0; kc < KF; ++kc)
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const bf16x8 b = get_chain(buf, kc, nb, l);
+#pragma unroll
+        for (int j = 0; j < BH; ++j) mma(acc[j][nb], fr[j][kc], b);
+      }
+  };
+
+  // ---- prologue: ring slots of the block's first two tiles, S1 of the first
+  const int64_t t0 = blockIdx.x;
+  if (t0 < a.ntiles) {
+    load_rec(t0);
+    store_rec(0, t0);
+    load_rec(t0 + G < a.ntiles ? t0 + G : t0);
+    store_rec(1, t0 + G < a.ntiles ? t0 + G : t0);
+  }
+  __syncthreads();   // vectors and the first two ring slots
+  if (t0 < a.ntiles) {
+    gather(0);
+    const f32x4 none[BH][2] = {};
+    load_frags((const bf16*)a.fr.hlT, none);
+    stage1(t0, 0);
+    load_gm(0);
+  }
+  __syncthreads();   // m1 of the first tile
+
+  int sl0 = 0;
+  for (int64_t t = t0; t < a.ntiles; t += G, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + G, t + 2G
+    const int64_t base = t * TE;
+    const int nvalid = nvalid_of(t);
+    __asm__ __volatile__("" : "+v"(lo16));
+    // loads issued by some waves only come first: the records two tiles ahead (loader wave)
+    load_rec(t + 2 * G < a.ntiles ? t + 2 * G : t);
+    bool valid[2];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) valid[nb] = nb * 16 + c < nvalid;
+    bf16x4 gm_t[BH][2];
+#pragma unroll
+    for (int j = 0; j < BH; ++j) gm_t[j][0] = gmr[j][0], gm_t[j][1] = gmr[j][1];
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
     bf16x4 s2[BH][2];
+    {
+      f32x4 acc[BH][2];
 #pragma unroll
-    for (int j = 0; j < BH; ++j) {
-      const int ob = w * BH + j;
-      __asm__ __volatile__("" ::: "memory");
-      f32x4 acc[2] = {zero4(), zero4()};
-#pragma unroll
-      for (int kc = 0; kc < KH; ++kc) {
-        const bf16x8 A = load_chunk(FhlT + ((int64_t)ob * KH + kc) * kFragElems + lo8);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
-      }
-      f32x4 y[2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        f32x4 d;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const YD r = silu_yd<bf16>(acc[nb][i] + s_b2[16 * ob + 4 * g + i]);
-          y[nb][i] = r.y;
-          d[i] = r.d;
-        }
-        s2[j][nb] = pack4(d);
-        if (EQ) put_chain(s_m, ob, nb, l, y[nb]);
-      }
-      if (EQ) store_fmajor(Dm, a.ldE, 16 * ob + c, base, E, g, edge_major(y[0], y[1], I));
-    }
-    float phi[2] = {0.f, 0.f};
-    if constexpr (EQ) {
-      __syncthreads();
-      // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows --
+      for (int j = 0; j < BH; ++j) acc[j][0] = acc[j][1] = zero4();
+      stage_mma(acc, s_m1);
+      load_frags(EQ ? (const bf16*)a.fr.movT : (const bf16*)a.fr.hl, acc);   // S3 (EGNN) or S5 (MPNN)
 #pragma unroll
       for (int j = 0; j < BH; ++j) {
-        const int mb = w * BH + j;
-      __asm__ __volatile__("" ::: "memory");
-        f32x4 acc[2] = {zero4(), zero4()};
+        const int rb = rb0 + j;
+        f32x4 y[2];
 #pragma unroll
-        for (int kc = 0; kc < KO; ++kc) {
-          const bf16x8 A = load_chunk(FmovT + ((int64_t)mb * KO + kc) * kFragElems + lo8);
+        for (int nb = 0; nb < 2; ++nb) {
+          f32x4 d;
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m, kc, nb, l));
+          for (int i = 0; i < 4; ++i) {
+            const YD r = silu_yd<bf16>(acc[j][nb][i] + s_b2[16 * rb + 4 * g + i]);
+            y[nb][i] = r.y;
+            d[i] = r.d;
+          }
+          s2[j][nb] = pack4(d);
+          if (EQ) put_chain(s_m, rb, nb, l, y[nb]);
         }
-        f32x4 p[2], gq[2];
+        if (EQ) store_fmajor(Dm + fmrow(j) + base, fmo, nvalid, g, edge_major(y[0], y[1], I));
+      }
+    }
+    __syncthreads();
+
+    if constexpr (EQ) {
+      // ---- S3: q -> p = SiLU, g_q = g_phi w2mov SiLU'(q), the wave's M rows
+      f32x4 acc[BH][2];
+#pragma unroll
+      for (int j = 0; j < BH; ++j) acc[j][0] = acc[j][1] = zero4();
+      stage_mma(acc, s_m);
+      load_frags((const bf16*)a.fr.mov, acc);   // S4
+      float phi[2] = {0.f, 0.f};
+      float gphi[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) gphi[nb] = rec_f(sl0, 4, nb * 16 + c);
+#pragma unroll
+      for (int j = 0; j < BH; ++j) {
+        const int rb = rb0 + j;
+        f32x4 gq[2];
+        f32x4 sw = *reinterpret_cast<const f32x4*>(dacc + 2 * j * 256);
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float w2 = s_w2m[16 * mb + 4 * g + i];
-            const YD r = silu_yd<bf16>(acc[nb][i] + s_bx1[16 * mb + 4 * g + i]);
-            p[nb][i] = r.y;
+            const float w2 = s_w2m[16 * rb + 4 * g + i];
+            const YD r = silu_yd<bf16>(acc[j][nb][i] + s_bx1[16 * rb + 4 * g + i]);
             phi[nb] += r.y * w2;
             gq[nb][i] = gphi[nb] * w2 * r.d;
+            sw[i] += gphi[nb] * r.y;
           }
-          put_chain(s_gq, mb, nb, l, gq[nb]);
+          put_chain(s_gq, rb, nb, l, gq[nb]);
         }
-        store_fmajor(Dgq, a.ldE, 16 * mb + c, base, E, g, edge_major(gq[0], gq[1], I));
-        store_fmajor(Dp, a.ldE, 16 * mb + c, base, E, g, edge_major(p[0], p[1], I));
+        *reinterpret_cast<f32x4*>(dacc + 2 * j * 256) = sw;
+        store_fmajor(Dgq + fmrow(j) + base, fmo, nvalid, g, edge_major(gq[0], gq[1], I));
       }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -438,93 +598,120 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
         phi[nb] += shfl_xor(phi[nb], 32);
         if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
       }
+      __syncthreads();
     }
-    __syncthreads();
 
     // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
-    // (m1 is dead -- its last reader was S2, behind at least one barrier -- so g_a2 takes its buffer)
+    // (m1 is dead -- its last reader was S2, behind a barrier -- so g_a2 takes its buffer)
+    gather(sl1);   // S1 of the next tile: S4 and S5 to land
+    {
+      f32x4 acc[BH][2];
 #pragma unroll
-    for (int j = 0; j < BH; ++j) {
-      const int ob = w * BH + j;
-      __asm__ __volatile__("" ::: "memory");
-      f32x4 acc[2];
+      for (int j = 0; j < BH; ++j)
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-        acc[nb] = valid[nb] ? load4_f32(gmsg + (int64_t)ri[nb] * a.sgm + 16 * ob + 4 * g) : zero4();
+        for (int nb = 0; nb < 2; ++nb) acc[j][nb] = valid[nb] ? unpack4(gm_t[j][nb]) : zero4();
       if constexpr (EQ) {
+        stage_mma(acc, s_gq);
+        load_frags((const bf16*)a.fr.hl, acc);   // S5
+      }
 #pragma unroll
-        for (int kc = 0; kc < KM; ++kc) {
-          const bf16x8 A = load_chunk(Fmov + ((int64_t)ob * KM + kc) * kFragElems + lo8);
+      for (int j = 0; j < BH; ++j) {
+        f32x4 ga[2];
 #pragma unroll
-          for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_gq, kc, nb, l));
+        for (int nb = 0; nb < 2; ++nb) {
+          const f32x4 d = unpack4(s2[j][nb]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ga[nb][i] = acc[j][nb][i] * d[i];
+          put_chain(s_ga2, rb0 + j, nb, l, ga[nb]);
         }
+        store_fmajor(Dga2 + fmrow(j) + base, fmo, nvalid, g, edge_major(ga[0], ga[1], I));
       }
-      f32x4 ga[2];
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const f32x4 d = unpack4(s2[j][nb]);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ga[nb][i] = acc[nb][i] * d[i];
-        put_chain(s_ga2, ob, nb, l, ga[nb]);
-      }
-      store_fmajor(Dga2, a.ldE, 16 * ob + c, base, E, g, edge_major(ga[0], ga[1], I));
     }
+    store_rec(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);   // the ring slot two tiles ahead (read after the end of the tile)
     __syncthreads();
 
     // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1), the wave's H rows --------------
-    float gr[2] = {0.f, 0.f};
-#pragma unroll
-    for (int j = 0; j < BH; ++j) {
-      const int hb = w * BH + j;
-      __asm__ __volatile__("" ::: "memory");
-      f32x4 acc[2] = {zero4(), zero4()};
-#pragma unroll
-      for (int kc = 0; kc < KO; ++kc) {
-        const bf16x8 A = load_chunk(Fhl + ((int64_t)hb * KO + kc) * kFragElems + lo8);
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_ga2, kc, nb, l));
-      }
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const f32x4 d = unpack4(s1[j][nb]);
-        f32x4 g1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          g1[i] = acc[nb][i] * d[i];
-          gr[nb] += s_wd[16 * hb + 4 * g + i] * g1[i];
-        }
-        if (valid[nb]) store_bf16x4(Gh + (base + nb * 16 + c) * H + 16 * hb + 4 * g, g1);
-      }
+    // S6's delta and grad x_i components (waves 0 and 1: lane -> component xc of edge xe)
+    const int xe = l & 31, xc = (w * 64 + l) >> 5;
+    float xdel = 0.f, xgrd = 0.f;
+    if (EQ && w < 2) {
+      const float* q = a.geo + (base + xe < E ? base + xe : E - 1) * 8;   // delta at 2..4, grad x_i at 5..7
+      const int xq = xc < 3 ? xc : 2;
+      xdel = q[2 + xq];
+      xgrd = q[5 + xq];
     }
-    if constexpr (EQ) {
+    {
+      f32x4 acc[BH][2];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        gr[nb] += shfl_xor(gr[nb], 16);
-        gr[nb] += shfl_xor(gr[nb], 32);
-        if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
-      }
-      __syncthreads();
-      // ---- S6: dL/ddelta = phi gx + 2 g_r delta; (g_phi, r^2) for the vector gradients
-      if (w == 0 && g == 0) {
+      for (int j = 0; j < BH; ++j) acc[j][0] = acc[j][1] = zero4();
+      stage_mma(acc, s_ga2);
+      load_frags((const bf16*)a.fr.hlT, acc);   // S2 of the next tile
+      float gr[2] = {0.f, 0.f};
+      float r2[2];
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) r2[nb] = valid[nb] ? rec_f(sl0, 3, nb * 16 + c) : 0.f;
+#pragma unroll
+      for (int j = 0; j < BH; ++j) {
+        const int rb = rb0 + j;
+        f32x4 sd = EQ ? *reinterpret_cast<const f32x4*>(dacc + (2 * j + 1) * 256) : zero4();
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb) {
-          if (!valid[nb]) continue;
-          const int k = nb * 16 + c;
-          float grt = 0.f, pht = 0.f;
+          const f32x4 d = unpack4(s1[j][nb]);
+          f32x4 g1;
 #pragma unroll
-          for (int ww = 0; ww < W; ++ww) {
-            grt += s_gr[ww][k];
-            pht += s_phi[ww][k];
+          for (int i = 0; i < 4; ++i) {
+            g1[i] = acc[j][nb][i] * d[i];
+            if constexpr (EQ) {
+              gr[nb] += s_wd[16 * rb + 4 * g + i] * g1[i];
+              sd[i] += r2[nb] * g1[i];
+            }
           }
-          const float k2 = 2.0f * grt;
-          const float* q = a.geo + (base + k) * 8;   // delta at 2..4, grad x_i at 5..7
-          *reinterpret_cast<f32x4*>(a.Gx + (base + k) * 4) =
-              f32x4{pht * q[5] + k2 * q[2], pht * q[6] + k2 * q[3], pht * q[7] + k2 * q[4], gphi[nb]};
-          a.R2[base + k] = r2[nb];
+          if (valid[nb]) store_bf16x4(Gh + (base + nb * 16) * H + 16 * rb + (c * H + 4 * g), g1);
+        }
+        if (EQ) *reinterpret_cast<f32x4*>(dacc + (2 * j + 1) * 256) = sd;
+      }
+      if constexpr (EQ) {
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb) {
+          gr[nb] += shfl_xor(gr[nb], 16);
+          gr[nb] += shfl_xor(gr[nb], 32);
+          if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
         }
       }
     }
+    __syncthreads();   // g_a2 read (its buffer takes the next m1); g_r of every wave for S6
+
+    // ---- S6 (EGNN, waves 0 and 1): dL/ddelta = phi grad x_i + 2 g_r delta, and g_phi
+    if (EQ && w < 2 && xe < nvalid) {
+      float grt = 0.f, pht = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < W; ++ww) {
+        grt += s_gr[ww][xe];
+        pht += s_phi[ww][xe];
+      }
+      a.Gx[(base + xe) * 4 + xc] = xc < 3 ? pht * xgrd + 2.0f * grt * xdel : rec_f(sl0, 4, xe);
+    }
+    // ---- S1 of the next tile and its message-gradient rows
+    if (t + G < a.ntiles) {
+      stage1(t + G, sl1);
+      load_gm(sl1);
+    }
     __syncthreads();
+  }
+
+  if constexpr (EQ) {
+    // per-block partials: dw2_mov and dw_d of the wave's rows, summed over the 16 edge lanes
+#pragma unroll
+    for (int j = 0; j < 2 * BH; ++j) {
+      f32x4 v = *reinterpret_cast<const f32x4*>(dacc + j * 256);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1) v[i] += shfl_xor(v[i], m);
+      }
+      if (c == 0)
+        *reinterpret_cast<f32x4*>(a.dwpart + (int64_t)blockIdx.x * a.LW + (j & 1) * M + 16 * (rb0 + (j >> 1)) + 4 * g) = v;
+    }
   }
 }
 
@@ -538,10 +725,10 @@ int launch_wide_fwd_t(const FwdArgs& a, hipStream_t st) {
 }
 
 template <int H, int W, bool EQ, int NUC>
-int launch_wide_bwd_t(const BwdArgs& a, hipStream_t st) {
+int launch_wide_bwd_t(const BwdArgs& a, int nblk, hipStream_t st) {
   if (a.ntiles > 0) {
-    const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * 2);
-    hipLaunchKernelGGL((wide_bwd_kernel<H, W, EQ, NUC>), dim3(blocks), dim3(W * 64), 0, st, a);
+    if (nblk != (int)std::min<int64_t>(a.ntiles, kWideBwdBlocks)) return (int)hipErrorInvalidValue;   // partial rows
+    hipLaunchKernelGGL((wide_bwd_kernel<H, W, EQ, NUC>), dim3(nblk), dim3(W * 64), 0, st, a);
   }
   return (int)hipGetLastError();
 }
@@ -557,9 +744,14 @@ int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
   return s.NUC == 1 ? launch_wide_fwd_t<256, 16, false, 1>(a, st) : launch_wide_fwd_t<256, 16, false, 2>(a, st);
 }
 
-int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st) {
-  if (s.eq) return s.NUC == 1 ? launch_wide_bwd_t<256, 16, true, 1>(a, st) : launch_wide_bwd_t<256, 16, true, 2>(a, st);
-  return s.NUC == 1 ? launch_wide_bwd_t<256, 16, false, 1>(a, st) : launch_wide_bwd_t<256, 16, false, 2>(a, st);
+int wide_bwd_blocks(const LayerShape& s) {
+  return (int)std::min<int64_t>(cdiv(std::max<int64_t>(s.E, 1), kTileEdges), kWideBwdBlocks);
+}
+
+int launch_wide_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
+  if (s.eq)
+    return s.NUC == 1 ? launch_wide_bwd_t<256, 8, true, 1>(a, nblk, st) : launch_wide_bwd_t<256, 8, true, 2>(a, nblk, st);
+  return s.NUC == 1 ? launch_wide_bwd_t<256, 8, false, 1>(a, nblk, st) : launch_wide_bwd_t<256, 8, false, 2>(a, nblk, st);
 }
 
 }  // namespace egnn
