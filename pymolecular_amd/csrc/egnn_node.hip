@@ -90,9 +90,9 @@ int64_t splitk_parts(int64_t M, int64_t N, int64_t K) {
   return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K)) * M * N;
 }
 
-int64_t wgrad_ksplit(int64_t K) {
+int64_t wgrad_ksplit(int64_t K) {   // whole 128-edge steps of the edge-factor GEMM
   const int64_t ks = std::max<int64_t>(512, cdiv(std::max<int64_t>(K, 1), 128));
-  return cdiv(ks, 64) * 64;
+  return cdiv(ks, 128) * 128;
 }
 
 int64_t factor_chunk_edges(const LayerShape& s) {
@@ -1520,17 +1520,21 @@ int launch_grad_sum(bool bf16_out, GradSumArgs a, hipStream_t st) {
 // ---------------------------------------------------------------------------
 // A (M x K) and B (N x K) are bf16 with k contiguous (feature-major per-edge
 // factors), K = number of edges.  128 x 128 output tile per 4-wave block
-// (each wave 64 x 64 = 4 x 4 MFMA blocks), k step 64, double-buffered LDS,
-// operand rows copied to LDS with 16-byte loads and stores.  With b_colsum,
-// the blocks of the first M tile also write sum_k B[n][k] as row M (the bias
+// (each wave 64 x 64 = 4 x 4 MFMA blocks), k step 128: the next step's operand
+// rows (64 KB) are loaded into registers while the current one is multiplied
+// from LDS and stored to the one LDS buffer after it (two blocks per CU keep
+// 128 KB per CU in flight; a step's loads are issued and consumed in the same
+// loop iteration, so the memory-counter waits are exact).  With b_colsum, the
+// blocks of the first M tile also write sum_k B[n][k] as row M (the bias
 // gradient that rides along with a weight gradient).
 namespace {
-constexpr int WG_BM = 128, WG_BN = 128, WG_BK = 64, WG_P = WG_BK + 8;
+constexpr int WG_BM = 128, WG_BN = 128, WG_BK = 128, WG_P = WG_BK + 8;
+constexpr int WG_SEG = WG_BM * WG_BK / 8 / 256;   // 16-byte segments per thread and operand
 }
 
-__global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
-  __shared__ __attribute__((aligned(16))) bf16 As[2][WG_BM * WG_P];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[2][WG_BN * WG_P];
+__global__ __launch_bounds__(256, 2) void wgrad_gemm_kernel(WgradArgs g) {
+  __shared__ __attribute__((aligned(16))) bf16 As[WG_BM * WG_P];
+  __shared__ __attribute__((aligned(16))) bf16 Bs[WG_BN * WG_P];
   const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
   const int wm = wave >> 1, wn = wave & 1;
   // 1-D grid, XCD-aware: block b is dispatched to XCD b % 8, and the per = gx * gy
@@ -1547,20 +1551,32 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
   const int64_t kbeg = bz * g.ksplit;
   const int64_t kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
   const bool colsum = g.b_colsum && bx == 0;
+  const bool whole_rows = m0 + WG_BM <= g.M && n0 + WG_BN <= g.N;
 
   f32x4 acc[4][4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float bsum[4] = {0.f, 0.f, 0.f, 0.f};
-
-  // thread -> (row, 8-element k segment) of the 128 x 64 operand tiles, 4 per operand
-  bf16x8 ra[4], rb[4];
-  auto load_stage = [&](int64_t k0) {
+  float bsum[WG_SEG];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
+  for (int i = 0; i < WG_SEG; ++i) bsum[i] = 0.f;
+
+  // thread -> (row, 8-element k segment) of the 128 x 128 operand tiles, WG_SEG per operand
+  bf16x8 ra[WG_SEG], rb[WG_SEG];
+  auto load_stage = [&](int64_t k0) {
+    if (whole_rows && k0 + WG_BK <= kend) {   // whole step (block-uniform): no per-lane branch
+#pragma unroll
+      for (int i = 0; i < WG_SEG; ++i) {
+        const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
+        ra[i] = *reinterpret_cast<const bf16x8*>(g.A + (m0 + r) * g.lda + k0 + 8 * q);
+        rb[i] = *reinterpret_cast<const bf16x8*>(g.B + (n0 + r) * g.ldb + k0 + 8 * q);
+      }
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < WG_SEG; ++i) {
+      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
       const int64_t k = k0 + 8 * q;
       const int64_t m = m0 + r, n = n0 + r;
       bf16x8 va = zero_chunk<bf16>(), vb = zero_chunk<bf16>();
@@ -1580,12 +1596,12 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
       rb[i] = vb;
     }
   };
-  auto store_stage = [&](int buf) {
+  auto store_stage = [&]() {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
-      *reinterpret_cast<bf16x8*>(&As[buf][r * WG_P + 8 * q]) = ra[i];
-      *reinterpret_cast<bf16x8*>(&Bs[buf][r * WG_P + 8 * q]) = rb[i];
+    for (int i = 0; i < WG_SEG; ++i) {
+      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
+      *reinterpret_cast<bf16x8*>(&As[r * WG_P + 8 * q]) = ra[i];
+      *reinterpret_cast<bf16x8*>(&Bs[r * WG_P + 8 * q]) = rb[i];
       if (colsum) {
         float t = 0.f;
 #pragma unroll
@@ -1595,10 +1611,9 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
     }
   };
 
-  int buf = 0;
   if (kbeg < kend) {
     load_stage(kbeg);
-    store_stage(0);
+    store_stage();
   }
   __syncthreads();
   for (int64_t k0 = kbeg; k0 < kend; k0 += WG_BK) {
@@ -1609,17 +1624,17 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
       bf16x8 a[4], b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][(wm * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
-        b[i] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(wn * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
+        a[i] = *reinterpret_cast<const bf16x8*>(&As[(wm * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
+        b[i] = *reinterpret_cast<const bf16x8*>(&Bs[(wn * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
     }
-    if (more) store_stage(buf ^ 1);
+    __syncthreads();   // every read of the buffer done
+    if (more) store_stage();
     __syncthreads();
-    buf ^= 1;
   }
 
   float* P = g.partial + bz * (g.M + (g.b_colsum ? 1 : 0)) * g.N;
@@ -1635,12 +1650,13 @@ __global__ __launch_bounds__(256) void wgrad_gemm_kernel(WgradArgs g) {
       }
   if (colsum) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < WG_SEG; ++i) {
       float t = bsum[i];
       t += __shfl_xor(t, 1, 64);
       t += __shfl_xor(t, 2, 64);
       t += __shfl_xor(t, 4, 64);
-      const int idx = tid + 256 * i, r = idx >> 3, q = idx & 7;
+      t += __shfl_xor(t, 8, 64);
+      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
       const int64_t n = n0 + r;
       if (q == 0 && n < g.N) P[g.M * g.N + n] = t;
     }

@@ -66,146 +66,288 @@ __device__ __forceinline__ void store_fmajor(bf16* tile, uint32_t lane_off, int 
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
+// Wave w owns the 16-row blocks BH w .. BH w + BH - 1 of every stage (H = 16 BH W).  One tile is
+//   S2 m = SiLU(W_hl^T m1 + b2) and its per-row sums | S3 phi (EGNN) | coordinate sums (EGNN) |
+//   S1 of the next tile
+// with the backward's latency measures: an edge-record ring filled by the loader wave two tiles ahead,
+// the next tile's gathers in flight during S3, each stage's fragments issued at the end of the stage
+// before.  The loader also derives a tile's row segments from its rows: the first-edge mask, the
+// rank -> row and rank -> length tables, and the rows of edges base - 1 and base + 32, which tell
+// whether the first and last segments continue into the neighbouring tiles.  A segment wholly inside
+// the tile is its row's aggregate, stored to out_msg / out_mov (coordinates scaled by 1 / length with
+// mean aggregation); a continuing one goes to the tile's carry slot (0: the tile's first segment,
+// 1: its last), which the fix-up sums.
 template <int H, int W, bool EQ, int NUC>
 __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
   constexpr int O = H, M = H;
-  constexpr int BH = H / W / 16, KH = H / 32, KO = O / 32;
+  constexpr int BH = H / W / 16;   // 16-row blocks per wave
+  static_assert(BH * 16 * W == H && (BH == 1 || BH == 2), "whole 16-row blocks per wave");
+  constexpr int KF = H / 32;
   constexpr int SEGW = O + (EQ ? 4 : 0);
-  __shared__ __attribute__((aligned(16))) bf16 s_m1[KH * 2 * 64 * 8];
-  __shared__ __attribute__((aligned(16))) bf16 s_m[KO * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_m1[KF * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_m[(EQ ? KF : 1) * 2 * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_wu[W * BH * NUC * kFragElems];
+  __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M];   // b2, bx1, w2_mov
+  float* const s_b2 = s_vec;
+  float* const s_bx1 = s_vec + O;
+  float* const s_w2m = s_vec + O + M;
   __shared__ float s_phi[W][TE];
-  __shared__ float s_d[TE][4];
-  __shared__ int s_rowof[TE];
+  // ring (tiles t, t + G, t + 2G): [slot][row, source, edge id, rank -> row, rank -> length][edge],
+  // (delta, r^2) per edge, and [slot][first-edge mask, row of edge base - 1, row of edge base + 32]
+  __shared__ int s_ring[3][5][TE];
+  __shared__ __attribute__((aligned(16))) float s_geo[3][EQ ? TE : 1][4];
+  __shared__ int s_seg[3][4];
 
-  const int w = threadIdx.x >> 6, l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const bf16* PQ = (const bf16*)a.PQ;
   const bf16* ef = (const bf16*)a.ef;
-  const bf16* FhlT = (const bf16*)a.fr.hlT;
-  const bf16* FmovT = (const bf16*)a.fr.movT;
   const int64_t E = a.E;
   const int N = (int)a.N;
+  const int FE = a.FE;
+  const int64_t G = gridDim.x;
+  const int rb0 = BH * w;
 
-  bf16x8 wu[BH][NUC];
-  f32x4 b2v[BH], bx1v[BH], w2mv[BH];
-#pragma unroll
-  for (int j = 0; j < BH; ++j) {
-    const int rb = w * BH + j;
-#pragma unroll
-    for (int uc = 0; uc < NUC; ++uc)
-      wu[j][uc] = load_chunk((const bf16*)a.fr.u + ((int64_t)rb * NUC + uc) * kFragElems + l * 8);
-    b2v[j] = load4_f32(a.fr.b2f + 16 * rb + 4 * g);
-    bx1v[j] = EQ ? load4_f32(a.fr.bx1f + 16 * rb + 4 * g) : zero4();
-    w2mv[j] = EQ ? load4_f32(a.fr.w2mf + 16 * rb + 4 * g) : zero4();
+  for (int q = threadIdx.x; q < W * BH * NUC * 64; q += W * 64)   // W_u fragments: 8-value chunks
+    *reinterpret_cast<bf16x8*>(s_wu + 8 * q) = load_chunk((const bf16*)a.fr.u + 8 * (int64_t)q);
+  for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
+  if constexpr (EQ) {
+    for (int q = threadIdx.x; q < M; q += W * 64) {
+      s_bx1[q] = a.fr.bx1f[q];
+      s_w2m[q] = a.fr.w2mf[q];
+    }
   }
   const bf16x8 I = ident_chunk(c, g);
 
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += gridDim.x) {
-    const int64_t base = t * TE;
-    const int nvalid = (int)((E - base) < TE ? (E - base) : TE);
-    int ri[2], rj[2], eid[2];
-    float dx[2], dy[2], dz[2], r2[2];
-    bool nf[2];
+  // ---- the edge-record ring (loader wave: lanes 0..31 the tile's edges, lane 32 edge base - 1,
+  // lane 33 edge base + 32); every wave consumes the registers where the loader stores them
+  constexpr int LDW = W - 1;
+  const int32_t* eidp = a.eids ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
+  int ld_r = 0, ld_c = 0, ld_e = 0;
+  f32x4 ld_g = zero4();
+  auto load_rec = [&](int64_t tt) {
+    if (w == LDW) {
+      const int64_t base = tt * TE;
+      const int64_t e0 = l < TE ? base + l : (l == TE ? base - 1 : base + TE);
+      const int64_t e = e0 < 0 ? 0 : (e0 < E ? e0 : E - 1);
+      ld_r = a.erow[e];
+      ld_c = a.col[e];
+      ld_e = eidp[e];
+      if constexpr (EQ) ld_g = *reinterpret_cast<const f32x4*>(a.geo + e * 4);   // (delta, r^2)
+    }
+  };
+  auto store_rec = [&](int sl, int64_t tt) {
+    asm volatile("" ::"v"(ld_r), "v"(ld_c), "v"(ld_e), "v"(ld_g[0]), "v"(ld_g[1]), "v"(ld_g[2]), "v"(ld_g[3]));
+    if (w == LDW) {
+      const int64_t base = tt * TE;
+      const int nv = (int)(E - base < TE ? E - base : TE);
+      const int r = clampi(ld_r, N);
+      const int rprev = __shfl(r, (l + 63) & 63, 64);
+      const bool first = l < nv && (l == 0 || rprev != r);
+      const uint32_t mask = (uint32_t)(__ballot(first) & 0xffffffffull);   // lanes from 32 on are never first
+      if (l < TE) {
+        s_ring[sl][0][l] = r;
+        s_ring[sl][1][l] = clampi(ld_c, N);
+        s_ring[sl][2][l] = a.eids ? clampi(ld_e, (int)E) : (int)(base + l < E ? base + l : E - 1);
+        if (first) {
+          const uint32_t after = l < 31 ? mask >> (l + 1) : 0u;   // first edges past l
+          const int next = after ? l + 1 + __builtin_ctz(after) : nv;
+          s_ring[sl][3][rank_of(mask, l)] = r;
+          s_ring[sl][4][rank_of(mask, l)] = next - l;
+        }
+        if (EQ) *reinterpret_cast<f32x4*>(s_geo[sl][l]) = ld_g;
+      }
+      if (l == 0) s_seg[sl][0] = (int)mask;
+      if (l == TE) s_seg[sl][1] = base > 0 ? r : -1;
+      if (l == TE + 1) s_seg[sl][2] = base + TE < E ? r : -1;
+    }
+  };
+
+  // ---- the gathers of S1 from a ring slot (as in the backward)
+  bf16x4 pg[2][BH], qg[2][BH];
+  bf16x8 ug[2][NUC];
+  auto pq_off = [&](int j) { return 32 * ((rb0 + j) >> 1) + 4 * ((rb0 + j) & 1); };
+  auto gather = [&](int sl) {
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
-      const int64_t e = base + nb * 16 + c;
-      const bool valid = e < E;
-      const int64_t ec = valid ? e : E - 1;
-      ri[nb] = clampi(a.erow[ec], N);
-      rj[nb] = clampi(a.col[ec], N);
-      eid[nb] = a.eids ? clampi(a.eids[ec], (int)E) : (int)ec;
-      nf[nb] = valid && (e == base || a.erow[e - 1] != a.erow[e]);
-      dx[nb] = dy[nb] = dz[nb] = r2[nb] = 0.f;
-      if constexpr (EQ) {
-        const f32x4 q = *reinterpret_cast<const f32x4*>(a.geo + ec * 4);
-        dx[nb] = q[0]; dy[nb] = q[1]; dz[nb] = q[2]; r2[nb] = q[3];
+      const int k = nb * 16 + c;
+      const bf16* pr = PQ + (int64_t)s_ring[sl][0][k] * 2 * H + 8 * g;
+      const bf16* qr = PQ + (int64_t)s_ring[sl][1][k] * 2 * H + H + 8 * g;
+      if constexpr (BH == 2) {
+        const bf16x8 p8 = load_chunk(pr + pq_off(0)), q8 = load_chunk(qr + pq_off(0));
+        pg[nb][0] = bf16x4{p8[0], p8[1], p8[2], p8[3]};
+        pg[nb][1] = bf16x4{p8[4], p8[5], p8[6], p8[7]};
+        qg[nb][0] = bf16x4{q8[0], q8[1], q8[2], q8[3]};
+        qg[nb][1] = bf16x4{q8[4], q8[5], q8[6], q8[7]};
+      } else {
+        pg[nb][0] = *reinterpret_cast<const bf16x4*>(pr + pq_off(0));
+        qg[nb][0] = *reinterpret_cast<const bf16x4*>(qr + pq_off(0));
+      }
+      if (FE > 0) {
+        const bf16* er = ef + (int64_t)s_ring[sl][2][k] * a.se;
+#pragma unroll
+        for (int uc = 0; uc < NUC; ++uc) {
+          const int s0 = 32 * uc + 8 * g;
+          ug[nb][uc] = load_chunk(er + (s0 + 8 <= FE ? s0 : 0));
+        }
       }
     }
-    const uint32_t mask = lo16(__ballot(nf[0])) | (lo16(__ballot(nf[1])) << 16);
-    const int nrank = __popc(mask);
-
-    // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows -------------
+  };
+  // ---- S1 of the tile in ring slot sl: m1 = SiLU(W_u U + P_i + Q_j) to s_m1
+  auto stage1 = [&](int sl) {
+    bf16x8 u[2][NUC];
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const float r2 = EQ ? s_geo[sl][EQ ? nb * 16 + c : 0][3] : 0.f;
+#pragma unroll
+      for (int uc = 0; uc < NUC; ++uc) {
+        const int s0 = 32 * uc + 8 * g;
+        u[nb][uc] = zero_chunk<bf16>();
+        if (s0 + 8 <= FE) {
+          u[nb][uc] = ug[nb][uc];
+        } else if (EQ && s0 == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
+          const bf16 hi = (bf16)r2;
+          u[nb][uc][0] = hi;
+          u[nb][uc][1] = (bf16)(r2 - (float)hi);
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < BH; ++j) {
-      const int hb = w * BH + j;
-      const int poff = 32 * (hb >> 1) + 8 * g + 4 * (hb & 1);
+      bf16x8 wu[NUC];
+#pragma unroll
+      for (int uc = 0; uc < NUC; ++uc) wu[uc] = get_norm(s_wu, (rb0 + j) * NUC + uc, l);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int uc = 0; uc < NUC; ++uc)
-          mma(acc, wu[j][uc], input_chunk_u(ef, a.se, eid[nb], a.FE, uc, g, r2[nb], EQ));
-        const f32x4 p = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)ri[nb] * 2 * H + poff));
-        const f32x4 q = unpack4(*reinterpret_cast<const bf16x4*>(PQ + (int64_t)rj[nb] * 2 * H + H + poff));
+        for (int uc = 0; uc < NUC; ++uc) mma(acc, wu[uc], u[nb][uc]);
+        const f32x4 p = unpack4(pg[nb][j]), q = unpack4(qg[nb][j]);
         f32x4 x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i] + p[i] + q[i]);
-        put_chain(s_m1, hb, nb, l, x);
+        put_chain(s_m1, rb0 + j, nb, l, x);
       }
     }
-    if (w == 0 && g == 0) {
+  };
+  // fragments of a stage, issued after every MFMA of the stage before (see the backward)
+  uint32_t lane16 = (uint32_t)l * 16;
+  bf16x8 fr[BH][KF];
+  auto load_frags = [&](const bf16* F, const f32x4 (&after)[BH][2]) {
+#pragma unroll
+    for (int j = 0; j < BH; ++j) __asm__ __volatile__("" : "+v"(lane16) : "v"(after[j][0]), "v"(after[j][1]));
+    const char* Fw = (const char*)(F + (int64_t)rb0 * KF * kFragElems);
+    uint32_t off[2 * BH];
+    off[0] = lane16;
+#pragma unroll
+    for (int q = 1; q < 2 * BH; ++q) {
+      off[q] = lane16 + 4096 * q;
+      __asm__ __volatile__("" : "+v"(off[q]));
+    }
+#pragma unroll
+    for (int j = 0; j < BH; ++j)
+#pragma unroll
+      for (int kc = 0; kc < KF; ++kc) {
+        const int ch = j * KF + kc;
+        fr[j][kc] = *reinterpret_cast<const bf16x8*>(Fw + off[ch >> 2] + 1024 * (ch & 3));
+      }
+  };
+  auto stage_mma = [&](f32x4 (&acc)[BH][2], const bf16* buf) {
+#pragma unroll
+    for (int kc = 0; kc < KF; ++kc)
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        const int k = nb * 16 + c;
-        if (nf[nb]) s_rowof[rank_of(mask, k)] = ri[nb];
-        if (EQ) { s_d[k][0] = dx[nb]; s_d[k][1] = dy[nb]; s_d[k][2] = dz[nb]; }
+        const bf16x8 b = get_chain(buf, kc, nb, l);
+#pragma unroll
+        for (int j = 0; j < BH; ++j) mma(acc[j][nb], fr[j][kc], b);
       }
-    }
-    __syncthreads();
+  };
+
+  // ---- prologue: ring slots of the block's first two tiles, S1 of the first
+  const int64_t t0 = blockIdx.x;
+  if (t0 < a.ntiles) {
+    load_rec(t0);
+    store_rec(0, t0);
+    load_rec(t0 + G < a.ntiles ? t0 + G : t0);
+    store_rec(1, t0 + G < a.ntiles ? t0 + G : t0);
+  }
+  __syncthreads();   // W_u, vectors and the first two ring slots
+  if (t0 < a.ntiles) {
+    gather(0);
+    const f32x4 none[BH][2] = {};
+    load_frags((const bf16*)a.fr.hlT, none);
+    stage1(0);
+  }
+  __syncthreads();   // m1 of the first tile
+
+  int sl0 = 0;
+  for (int64_t t = t0; t < a.ntiles; t += G, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + G, t + 2G
+    const int64_t base = t * TE;
+    const int nvalid = (int)(E - base < TE ? E - base : TE);
+    __asm__ __volatile__("" : "+v"(lane16));
+    load_rec(t + 2 * G < a.ntiles ? t + 2 * G : t);   // issued by the loader only: first
+    const uint32_t mask = (uint32_t)s_seg[sl0][0];
+    const int nrank = __popc(mask);
+    const int rprev = s_seg[sl0][1], rnext = s_seg[sl0][2];
+    // row of rank r and whether its segment continues into a neighbouring tile
+    auto seg_row = [&](int r, bool& split) {
+      const int R = s_ring[sl0][3][r];
+      split = (r == 0 && R == rprev) || (r == nrank - 1 && R == rnext);
+      return R;
+    };
 
     // ---- S2: m = SiLU(W_hl^T m1 + b2) for the wave's O rows; row sums -----
-    const int rfirst = s_rowof[0];
+    {
+      f32x4 acc[BH][2];
 #pragma unroll
-    for (int j = 0; j < BH; ++j) {
-      const int ob = w * BH + j;
-      f32x4 acc[2] = {zero4(), zero4()};
+      for (int j = 0; j < BH; ++j) acc[j][0] = acc[j][1] = zero4();
+      stage_mma(acc, s_m1);
+      load_frags((const bf16*)(EQ ? a.fr.movT : a.fr.hlT), acc);   // S3 (EGNN) or S2 of the next tile
 #pragma unroll
-      for (int kc = 0; kc < KH; ++kc) {
-        const bf16x8 A = load_chunk(FhlT + ((int64_t)ob * KH + kc) * kFragElems + l * 8);
+      for (int j = 0; j < BH; ++j) {
+        const int ob = rb0 + j;
+        f32x4 m[2];
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
-      }
-      f32x4 m[2];
+        for (int nb = 0; nb < 2; ++nb) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) m[nb][i] = silu_t<bf16>(acc[nb][i] + b2v[j][i]);
-        if (EQ) put_chain(s_m, ob, nb, l, m[nb]);
-      }
-      const bf16x8 Am = edge_major(m[0], m[1], I);
-      for (int rb = 0; rb * 16 < nrank; ++rb) {
-        f32x4 D = zero4();
-        mma(D, Am, seg_chunk(mask, nvalid, rb, c, g));
-        const int r = rb * 16 + c;
-        if (r < nrank) {
-          const int R = s_rowof[r];
-          const int rs = a.rowptr[R], re = a.rowptr[R + 1];
-          if (rs >= base && re <= base + TE) {
-            *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)R * a.smsg + 16 * ob + 4 * g) = pack4(D);
-          } else {
-            const int slot = (R == rfirst) ? 0 : 1;
-            *reinterpret_cast<f32x4*>(a.carry + ((int64_t)t * 2 + slot) * SEGW + 16 * ob + 4 * g) = D;
+          for (int i = 0; i < 4; ++i) m[nb][i] = silu_t<bf16>(acc[j][nb][i] + s_b2[16 * ob + 4 * g + i]);
+          if (EQ) put_chain(s_m, ob, nb, l, m[nb]);
+        }
+        const bf16x8 Am = edge_major(m[0], m[1], I);
+        for (int rb = 0; rb * 16 < nrank; ++rb) {
+          f32x4 D = zero4();
+          mma(D, Am, seg_chunk(mask, nvalid, rb, c, g));
+          const int r = rb * 16 + c;
+          if (r < nrank) {
+            bool split;
+            const int R = seg_row(r, split);
+            if (!split)
+              *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)R * a.smsg + 16 * ob + 4 * g) = pack4(D);
+            else
+              *reinterpret_cast<f32x4*>(a.carry + ((int64_t)t * 2 + (r == 0 ? 0 : 1)) * SEGW + 16 * ob + 4 * g) = D;
           }
         }
       }
     }
+    __syncthreads();   // m (EGNN); every read of m1 done (S1 of the next tile rewrites it)
+    gather(sl1);       // S1 of the next tile: S3 and the coordinate sums to land
+
     if constexpr (EQ) {
-      __syncthreads();
       // ---- S3: phi = SiLU(W1mov^T m + bx1) . w2mov (partial over the wave's M rows)
+      f32x4 acc[BH][2];
+#pragma unroll
+      for (int j = 0; j < BH; ++j) acc[j][0] = acc[j][1] = zero4();
+      stage_mma(acc, s_m);
+      load_frags((const bf16*)a.fr.hlT, acc);   // S2 of the next tile
       float phi[2] = {0.f, 0.f};
 #pragma unroll
       for (int j = 0; j < BH; ++j) {
-        const int mb = w * BH + j;
-        f32x4 acc[2] = {zero4(), zero4()};
-#pragma unroll
-        for (int kc = 0; kc < KO; ++kc) {
-          const bf16x8 A = load_chunk(FmovT + ((int64_t)mb * KO + kc) * kFragElems + l * 8);
-#pragma unroll
-          for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m, kc, nb, l));
-        }
+        const int mb = rb0 + j;
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) phi[nb] += silu_t<bf16>(acc[nb][i] + bx1v[j][i]) * w2mv[j][i];
+          for (int i = 0; i < 4; ++i)
+            phi[nb] += silu_t<bf16>(acc[j][nb][i] + s_bx1[16 * mb + 4 * g + i]) * s_w2m[16 * mb + 4 * g + i];
       }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -214,8 +356,8 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
         if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
       }
       __syncthreads();
-      // ---- coordinate sums: sum_j delta phi per row (hi + lo bf16 split) -----
-      if (w == W - 1) {
+      // ---- coordinate sums (wave 0): sum_j delta phi per row (hi + lo bf16 split)
+      if (w == 0) {
         bf16x8 ahi = zero_chunk<bf16>(), alo = zero_chunk<bf16>();
 #pragma unroll
         for (int s = 0; s < 8; ++s) {
@@ -225,7 +367,7 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
             float ph = 0.f;
 #pragma unroll
             for (int ww = 0; ww < W; ++ww) ph += s_phi[ww][k];
-            v = s_d[k][c] * ph;
+            v = s_geo[sl0][k][c] * ph;
           }
           const bf16 hi = (bf16)v;
           ahi[s] = hi;
@@ -238,17 +380,16 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
           mma(D, alo, S);
           const int r = rb * 16 + c;
           if (g == 0 && r < nrank) {
-            const int R = s_rowof[r];
-            const int rs = a.rowptr[R], re = a.rowptr[R + 1];
-            if (rs >= base && re <= base + TE) {
-              const float sc = a.mean ? 1.0f / (float)(re - rs) : 1.0f;
+            bool split;
+            const int R = seg_row(r, split);
+            if (!split) {
+              const float sc = a.mean ? 1.0f / (float)s_ring[sl0][4][r] : 1.0f;
               float* o = a.out_mov + (int64_t)R * a.smov;
               o[0] = D[0] * sc;
               o[1] = D[1] * sc;
               o[2] = D[2] * sc;
             } else {
-              const int slot = (R == rfirst) ? 0 : 1;
-              float* o = a.carry + ((int64_t)t * 2 + slot) * SEGW + O;
+              float* o = a.carry + ((int64_t)t * 2 + (r == 0 ? 0 : 1)) * SEGW + O;
               o[0] = D[0];
               o[1] = D[1];
               o[2] = D[2];
@@ -257,6 +398,9 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
         }
       }
     }
+    // ---- S1 of the next tile; the ring slot two tiles ahead
+    if (t + G < a.ntiles) stage1(sl1);
+    store_rec(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);
     __syncthreads();
   }
 }
@@ -462,21 +606,21 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
     }
   };
   // The wave's fragments of a stage: BH x 8 chunks of 1 KB from a uniform base, at the lane's byte
-  // offset lo16 + 4 KB q (q = 0 .. 2 BH - 1) plus an immediate.  The offsets are made opaque (lo16 at
+  // offset lane16 + 4 KB q (q = 0 .. 2 BH - 1) plus an immediate.  The offsets are made opaque (lane16 at
   // the top of each tile, the others at each use) so that they stay single VGPRs instead of becoming
   // a 64-bit base per chunk.
-  uint32_t lo16 = (uint32_t)l * 16;
+  uint32_t lane16 = (uint32_t)l * 16;
   bf16x8 fr[BH][KF];
   auto load_frags = [&](const bf16* F, const f32x4 (&after)[BH][2]) {
     // the loads come after every MFMA of the stage (they write the registers those MFMAs read)
 #pragma unroll
-    for (int j = 0; j < BH; ++j) __asm__ __volatile__("" : "+v"(lo16) : "v"(after[j][0]), "v"(after[j][1]));
+    for (int j = 0; j < BH; ++j) __asm__ __volatile__("" : "+v"(lane16) : "v"(after[j][0]), "v"(after[j][1]));
     const char* Fw = (const char*)(F + (int64_t)rb0 * KF * kFragElems);
     uint32_t off[2 * BH];
-    off[0] = lo16;
+    off[0] = lane16;
 #pragma unroll
     for (int q = 1; q < 2 * BH; ++q) {
-      off[q] = lo16 + 4096 * q;
+      off[q] = lane16 + 4096 * q;
       __asm__ __volatile__("" : "+v"(off[q]));
     }
 #pragma unroll
@@ -522,7 +666,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
     const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + G, t + 2G
     const int64_t base = t * TE;
     const int nvalid = nvalid_of(t);
-    __asm__ __volatile__("" : "+v"(lo16));
+    __asm__ __volatile__("" : "+v"(lane16));
     // loads issued by some waves only come first: the records two tiles ahead (loader wave)
     load_rec(t + 2 * G < a.ntiles ? t + 2 * G : t);
     bool valid[2];
@@ -718,7 +862,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
 template <int H, int W, bool EQ, int NUC>
 int launch_wide_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (a.ntiles > 0) {
-    const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * 2);
+    const int blocks = (int)std::min<int64_t>(a.ntiles, kWideBwdBlocks);   // one persistent block per CU
     hipLaunchKernelGGL((wide_fwd_kernel<H, W, EQ, NUC>), dim3(blocks), dim3(W * 64), 0, st, a);
   }
   return (int)hipGetLastError();
@@ -740,8 +884,8 @@ bool wide_supported(const LayerShape& s) {
 }
 
 int launch_wide_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
-  if (s.eq) return s.NUC == 1 ? launch_wide_fwd_t<256, 16, true, 1>(a, st) : launch_wide_fwd_t<256, 16, true, 2>(a, st);
-  return s.NUC == 1 ? launch_wide_fwd_t<256, 16, false, 1>(a, st) : launch_wide_fwd_t<256, 16, false, 2>(a, st);
+  if (s.eq) return s.NUC == 1 ? launch_wide_fwd_t<256, 8, true, 1>(a, st) : launch_wide_fwd_t<256, 8, true, 2>(a, st);
+  return s.NUC == 1 ? launch_wide_fwd_t<256, 8, false, 1>(a, st) : launch_wide_fwd_t<256, 8, false, 2>(a, st);
 }
 
 int wide_bwd_blocks(const LayerShape& s) {
