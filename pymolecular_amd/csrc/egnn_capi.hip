@@ -256,7 +256,6 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.Dm1 = w.Dm1; a.Dm = w.Dm; a.Dgq = w.Dgq; a.Dga2 = w.Dga2; a.Dp = w.Dp; a.Gh = w.Gh; a.Gx = w.Gx; a.R2 = w.R2;
   const bool coop = coop_supported(s);
   a.dwpart = w.dwpart; a.LW = w.LW;
-  a.ldE = w.ldE;
   a.geo = w.geo;
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   if (coop || wide_supported(s)) {
@@ -278,25 +277,18 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     return hip_status(launch_sum_rows(w.part, s.E > 0 ? nsplit : 0, g.M * g.N, dst, st));
   };
   const bool wide = wide_supported(s);
-  // wide kernels: feature-major bf16 factors, [A | bias row]^T B by the edge-factor GEMM
-  auto wgrad = [&](const void* A, const void* B, int64_t M, int64_t N, float* dst) -> int32_t {
-    WgradArgs g{};
-    g.M = M; g.N = N; g.K = s.E;
-    g.A = (const bf16*)A; g.lda = w.ldE;
-    g.B = (const bf16*)B; g.ldb = w.ldE;
-    g.ksplit = wgrad_ksplit(s.E);
-    g.partial = w.part; g.b_colsum = 1;
-    const int64_t nsplit = cdiv(std::max<int64_t>(s.E, 1), g.ksplit);
-    if (nsplit * (M + 1) * N > w.part_elems) return EGNN_ERR_WORKSPACE;
-    ProfScope ps(EGNN_K_WGRAD, st);
-    int32_t r = s.E > 0 ? hip_status(launch_wgrad_gemm(g, st)) : EGNN_OK;
-    if (r != EGNN_OK) return r;
-    return hip_status(launch_sum_rows(w.part, s.E > 0 ? nsplit : 0, (M + 1) * N, dst, st));
-  };
-  if (wide) {
-    if ((rc = wgrad(w.Dm1, w.Dga2, s.H, s.O, w.dWhl)) != EGNN_OK) return rc;   // [dW_hl ; db2]
+  if (wide) {   // edge-major bf16 factors of every edge: [A | 1]^T B over the edges
+    Gemm2Args g{};
+    g.M = s.H + 1; g.N = s.O; g.K = s.E;
+    g.A = w.Dm1; g.lda = s.H; g.a_bf16 = 1; g.a_kc = 0; g.a_ones_row = s.H;
+    g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = 1; g.b_nc = 1;
+    if ((rc = splitk2(g, w.dWhl)) != EGNN_OK) return rc;   // [dW_hl ; db2]
     if (s.eq) {
-      if ((rc = wgrad(w.Dm, w.Dgq, s.O, s.M, w.dW1m)) != EGNN_OK) return rc;  // [dW1_mov ; dbx1]
+      Gemm2Args m{};
+      m.M = s.O + 1; m.N = s.M; m.K = s.E;
+      m.A = w.Dm; m.lda = s.O; m.a_bf16 = 1; m.a_kc = 0; m.a_ones_row = s.O;
+      m.B = w.Dgq; m.ldb = s.M; m.b_bf16 = 1; m.b_nc = 1;
+      if ((rc = splitk2(m, w.dW1m)) != EGNN_OK) return rc;   // [dW1_mov ; dbx1]
       // dw2_mov | dw_d (adjacent): the kernel's per-block partials, summed in block order
       ProfScope ps(EGNN_K_WGRAD, st);
       if ((rc = hip_status(launch_sum_rows(w.dwpart, s.E > 0 ? w.nblk : 0, w.LW, w.dw2m, st))) != EGNN_OK) return rc;

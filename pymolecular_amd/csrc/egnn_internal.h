@@ -81,12 +81,11 @@ struct BwdWs {
   float* dwd;      // H
   float* dWn;      // (F+1) x 2H  last row = [db1 | sum dQ]
   int64_t part_elems;
-  // workgroup-cooperative path: per-block partials of [dWhl | dW1m | dw2m | dWe | dwd]
+  // per-block partials: the cooperative path's [dWhl | dW1m | dw2m | dWe | dwd], the wide path's [dw2m | dwd]
   float* dwpart;
   int nblk;
   int64_t LW;
   float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
-  int64_t ldE;     // row pitch of the factors (feature-major for the wide kernels)
   // one-wave-per-tile kernel: the factors hold chunkE edges; per-chunk sums of the factor products
   int64_t chunkE;
   int nchunk;
@@ -158,19 +157,6 @@ bool stream_gemm_ok(const Gemm2Args& g, bool compute_bf16);
 int launch_stream_gemm(const Gemm2Args& g, hipStream_t st);
 // Two independent products, in one launch when both take the 32 x 64 bf16 tiles (else one after the other).
 int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf16, hipStream_t st);
-// Weight-gradient GEMM over edges with k-contiguous bf16 operands (feature-major
-// per-edge factors): partial[z][m][n] = sum_{k in split z} A[m][k] B[n][k];
-// b_colsum adds row M = sum_k B[n][k].  ksplit is a multiple of 64.
-struct WgradArgs {
-  int64_t M, N, K;
-  const bf16* A; int64_t lda;
-  const bf16* B; int64_t ldb;
-  int64_t ksplit;
-  float* partial;    // [nsplit][M (+1)][N]
-  int b_colsum;
-};
-int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st);
-int64_t wgrad_ksplit(int64_t K);   // k per split of the edge-factor GEMMs (multiple of 64)
 
 struct FwdArgs {
   int64_t N, E, ntiles;
@@ -208,7 +194,6 @@ struct BwdArgs {
   int64_t fbase;   // first edge of the factor rows Dm1 ... Dp (they hold one chunk; Gh, Gx, R2 hold all edges)
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
-  int64_t ldE;     // wide kernels: row pitch of the feature-major factors Dm1 ... Dp
   const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype;
   const void* w1m; // (O x H) and (M x O) with lin
   int lin;         // weights in torch.nn.Linear (out, in) layout

@@ -77,7 +77,10 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
 int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
   K = std::max<int64_t>(K, 1);
   const bool big = K >= kSplitKBig;   // the tile launch_gemm2 picks for this product
-  const int64_t tiles = N == 1 ? 1 : big ? cdiv(M, 128) * cdiv(N, N <= 32 ? 32 : 128) : cdiv(M, 64) * cdiv(N, 64);
+  // row tiles: M = R + 1 with R a multiple of the tile is taken as rows plus the ones row (a bias
+  // gradient), which the first row tile folds in
+  auto rt = [&](int64_t bm) { return (M > 1 && (M - 1) % bm == 0) ? (M - 1) / bm : cdiv(M, bm); };
+  const int64_t tiles = N == 1 ? 1 : big ? rt(128) * cdiv(N, N <= 32 ? 32 : 128) : rt(64) * cdiv(N, 64);
   // matrix-vector products: one small block per split; 64 x 64 tiles: about 256 rows per split at the
   // node counts of molecule batches (measured faster than 32 x 64 tiles over 700 rows: fewer re-reads
   // of the operands from L2 for a few more partials)
@@ -88,11 +91,6 @@ int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
 
 int64_t splitk_parts(int64_t M, int64_t N, int64_t K) {
   return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K)) * M * N;
-}
-
-int64_t wgrad_ksplit(int64_t K) {   // whole 128-edge steps of the edge-factor GEMM
-  const int64_t ks = std::max<int64_t>(512, cdiv(std::max<int64_t>(K, 1), 128));
-  return cdiv(ks, 128) * 128;
 }
 
 int64_t factor_chunk_edges(const LayerShape& s) {
@@ -108,12 +106,11 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   size_t off = frag_layout(s, b, &w->fr, 0, true);
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
   const bool coop = coop_supported(s), wide = wide_supported(s);
-  // wide kernels store the factors feature-major with a 16-byte aligned row pitch; the
-  // one-wave-per-tile kernel stores one edge chunk of them at a time
-  w->ldE = wide ? (int64_t)align_up((size_t)std::max<int64_t>(s.E, 1), 8) : std::max<int64_t>(s.E, 1);
-  w->chunkE = (coop || wide) ? w->ldE : factor_chunk_edges(s);
-  w->nchunk = (coop || wide) ? 1 : (int)cdiv(std::max<int64_t>(s.E, 1), w->chunkE);
-  const size_t E = (size_t)w->ldE, EF = (size_t)w->chunkE;
+  // edge-major factors; the one-wave-per-tile kernel stores one edge chunk of them at a time
+  const int64_t E1 = std::max<int64_t>(s.E, 1);
+  w->chunkE = (coop || wide) ? E1 : factor_chunk_edges(s);
+  w->nchunk = (coop || wide) ? 1 : (int)cdiv(E1, w->chunkE);
+  const size_t E = (size_t)E1, EF = (size_t)w->chunkE;
   w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
   w->Dm1 = coop ? nullptr : take(EF * s.H * s.esz);
   w->Dm = coop ? nullptr : take(EF * s.O * s.esz);
@@ -145,11 +142,6 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->chunkres = (coop || wide || w->nchunk == 1)
                     ? nullptr
                     : (float*)take((size_t)w->nchunk * ((s.H + 1) * s.O + (s.O + 1) * s.M + s.M) * sizeof(float));
-  if (wide) {
-    const int64_t ks = wgrad_ksplit(s.E);
-    const int64_t nw = cdiv(std::max<int64_t>(s.E, 1), ks);
-    w->part_elems = std::max<int64_t>(w->part_elems, nw * (int64_t)(std::max(s.H, s.O) + 1) * std::max(s.O, s.M));
-  }
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
   w->dW1m = (float*)take((size_t)(s.O + 1) * s.M * sizeof(float));
@@ -1514,161 +1506,5 @@ int launch_grad_sum(bool bf16_out, GradSumArgs a, hipStream_t st) {
 }
 
 
-
-// ---------------------------------------------------------------------------
-// weight-gradient GEMM over edges: partial[z][m][n] = sum_{k in split z} A[m][k] B[n][k]
-// ---------------------------------------------------------------------------
-// A (M x K) and B (N x K) are bf16 with k contiguous (feature-major per-edge
-// factors), K = number of edges.  128 x 128 output tile per 4-wave block
-// (each wave 64 x 64 = 4 x 4 MFMA blocks), k step 128: the next step's operand
-// rows (64 KB) are loaded into registers while the current one is multiplied
-// from LDS and stored to the one LDS buffer after it (two blocks per CU keep
-// 128 KB per CU in flight; a step's loads are issued and consumed in the same
-// loop iteration, so the memory-counter waits are exact).  With b_colsum, the
-// blocks of the first M tile also write sum_k B[n][k] as row M (the bias
-// gradient that rides along with a weight gradient).
-namespace {
-constexpr int WG_BM = 128, WG_BN = 128, WG_BK = 128, WG_P = WG_BK + 8;
-constexpr int WG_SEG = WG_BM * WG_BK / 8 / 256;   // 16-byte segments per thread and operand
-}
-
-__global__ __launch_bounds__(256, 2) void wgrad_gemm_kernel(WgradArgs g) {
-  __shared__ __attribute__((aligned(16))) bf16 As[WG_BM * WG_P];
-  __shared__ __attribute__((aligned(16))) bf16 Bs[WG_BN * WG_P];
-  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
-  const int wm = wave >> 1, wn = wave & 1;
-  // 1-D grid, XCD-aware: block b is dispatched to XCD b % 8, and the per = gx * gy
-  // output tiles of k-split z go to consecutive blocks of XCD z % 8, so they share
-  // that XCD's L2 for the split's operand rows.  The grid holds per * roundup(gz, 8)
-  // blocks; those past the last split leave before any barrier.
-  const int gx = (int)((g.M + WG_BM - 1) / WG_BM), per = gx * (int)((g.N + WG_BN - 1) / WG_BN);
-  const int64_t gz = (g.K + g.ksplit - 1) / g.ksplit;
-  const int64_t xcd = blockIdx.x % 8, jx = blockIdx.x / 8;
-  const int64_t bz = (jx / per) * 8 + xcd;
-  if (bz >= gz) return;
-  const int tile = (int)(jx % per), bx = tile % gx, by = tile / gx;
-  const int64_t m0 = (int64_t)bx * WG_BM, n0 = (int64_t)by * WG_BN;
-  const int64_t kbeg = bz * g.ksplit;
-  const int64_t kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
-  const bool colsum = g.b_colsum && bx == 0;
-  const bool whole_rows = m0 + WG_BM <= g.M && n0 + WG_BN <= g.N;
-
-  f32x4 acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float bsum[WG_SEG];
-#pragma unroll
-  for (int i = 0; i < WG_SEG; ++i) bsum[i] = 0.f;
-
-  // thread -> (row, 8-element k segment) of the 128 x 128 operand tiles, WG_SEG per operand
-  bf16x8 ra[WG_SEG], rb[WG_SEG];
-  auto load_stage = [&](int64_t k0) {
-    if (whole_rows && k0 + WG_BK <= kend) {   // whole step (block-uniform): no per-lane branch
-#pragma unroll
-      for (int i = 0; i < WG_SEG; ++i) {
-        const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
-        ra[i] = *reinterpret_cast<const bf16x8*>(g.A + (m0 + r) * g.lda + k0 + 8 * q);
-        rb[i] = *reinterpret_cast<const bf16x8*>(g.B + (n0 + r) * g.ldb + k0 + 8 * q);
-      }
-      return;
-    }
-#pragma unroll
-    for (int i = 0; i < WG_SEG; ++i) {
-      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
-      const int64_t k = k0 + 8 * q;
-      const int64_t m = m0 + r, n = n0 + r;
-      bf16x8 va = zero_chunk<bf16>(), vb = zero_chunk<bf16>();
-      if (k + 8 <= kend) {
-        if (m < g.M) va = *reinterpret_cast<const bf16x8*>(g.A + m * g.lda + k);
-        if (n < g.N) vb = *reinterpret_cast<const bf16x8*>(g.B + n * g.ldb + k);
-      } else {
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-          if (k + u < kend) {
-            if (m < g.M) va[u] = g.A[m * g.lda + k + u];
-            if (n < g.N) vb[u] = g.B[n * g.ldb + k + u];
-          }
-        }
-      }
-      ra[i] = va;
-      rb[i] = vb;
-    }
-  };
-  auto store_stage = [&]() {
-#pragma unroll
-    for (int i = 0; i < WG_SEG; ++i) {
-      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
-      *reinterpret_cast<bf16x8*>(&As[r * WG_P + 8 * q]) = ra[i];
-      *reinterpret_cast<bf16x8*>(&Bs[r * WG_P + 8 * q]) = rb[i];
-      if (colsum) {
-        float t = 0.f;
-#pragma unroll
-        for (int u = 0; u < 8; ++u) t += (float)rb[i][u];
-        bsum[i] += t;
-      }
-    }
-  };
-
-  if (kbeg < kend) {
-    load_stage(kbeg);
-    store_stage();
-  }
-  __syncthreads();
-  for (int64_t k0 = kbeg; k0 < kend; k0 += WG_BK) {
-    const bool more = k0 + WG_BK < kend;
-    if (more) load_stage(k0 + WG_BK);
-#pragma unroll
-    for (int ks = 0; ks < WG_BK / 32; ++ks) {
-      bf16x8 a[4], b[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        a[i] = *reinterpret_cast<const bf16x8*>(&As[(wm * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
-        b[i] = *reinterpret_cast<const bf16x8*>(&Bs[(wn * 64 + i * 16 + c) * WG_P + 32 * ks + 8 * gq]);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) mma(acc[i][j], a[i], b[j]);
-    }
-    __syncthreads();   // every read of the buffer done
-    if (more) store_stage();
-    __syncthreads();
-  }
-
-  float* P = g.partial + bz * (g.M + (g.b_colsum ? 1 : 0)) * g.N;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t m = m0 + wm * 64 + i * 16 + 4 * gq + r;
-        const int64_t n = n0 + wn * 64 + j * 16 + c;
-        if (m < g.M && n < g.N) P[m * g.N + n] = acc[i][j][r];
-      }
-  if (colsum) {
-#pragma unroll
-    for (int i = 0; i < WG_SEG; ++i) {
-      float t = bsum[i];
-      t += __shfl_xor(t, 1, 64);
-      t += __shfl_xor(t, 2, 64);
-      t += __shfl_xor(t, 4, 64);
-      t += __shfl_xor(t, 8, 64);
-      const int idx = tid + 256 * i, r = idx >> 4, q = idx & 15;
-      const int64_t n = n0 + r;
-      if (q == 0 && n < g.N) P[g.M * g.N + n] = t;
-    }
-  }
-}
-
-int launch_wgrad_gemm(const WgradArgs& g, hipStream_t st) {
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0) return 0;
-  const int64_t per = cdiv(g.M, WG_BM) * cdiv(g.N, WG_BN), gz = cdiv(g.K, g.ksplit);
-  const int64_t blocks = per * cdiv(gz, 8) * 8;
-  hipLaunchKernelGGL(wgrad_gemm_kernel, dim3((unsigned)blocks), dim3(256), 0, st, g);
-  return (int)hipGetLastError();
-}
 
 }  // namespace egnn

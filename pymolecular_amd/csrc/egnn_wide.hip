@@ -1,18 +1,18 @@
 // Workgroup-cooperative fused forward and backward for wide layers
 // (bf16, H = O = M = 256, gfx950).
 //
-// Same tile organisation as the H = 128 kernels (all W = 8 waves on one
-// 32-edge tile, wave w owning rows [32 w, 32 w + 32) of every feature
-// dimension, stages handing C-blocks to each other through chain-ordered LDS
-// buffers), with two differences forced by the size of the weights:
+// Same tile organisation as the H = 128 kernels: all W = 8 waves of a block
+// on one 32-edge tile, wave w owning the 16-row blocks 2w and 2w + 1 of every
+// feature dimension, stages handing C-blocks to each other through
+// chain-ordered LDS buffers.  Two differences are forced by the size of the
+// weights:
 //  * a 256 x 256 weight matrix is 128 KB in bf16, so the A-operand fragments
 //    are not kept resident: each wave streams the fragments of its rows from
-//    global memory (L2) in the stage that uses them;
+//    global memory (L2), issued one stage ahead;
 //  * register-resident weight-gradient accumulators would need 256 KB per
-//    matrix per workgroup, so the backward writes the per-edge factors of the
-//    weight gradients (m1, m, g_q, p, g_a2) feature-major ([feature][edge],
-//    turned edge-major in registers by identity MFMAs) and fixed-order
-//    split-K GEMMs with k-contiguous operands reduce them.
+//    matrix per workgroup, so the backward writes the per-edge factors of
+//    the weight gradients (m1, m, g_q, g_a2) edge-major and the split-K node
+//    products reduce them over the edges.
 // Edge inputs of up to NUC x 32 slots ([e | r^2 hi | r^2 lo]) are supported.
 // Reference: forward_kernel.py:89-153 and backward_kernel.py:143-257 compute
 // the same quantities one program per CSR row.
@@ -40,28 +40,6 @@ __device__ __forceinline__ bf16x8 input_chunk_u(const bf16* ef, int64_t se, int 
 }
 
 __device__ __forceinline__ void store_bf16x4(bf16* p, const f32x4& v) { *reinterpret_cast<bf16x4*>(p) = pack4(v); }
-
-// Feature-major store of one 16-feature block of a tile: v is the edge-major
-// chunk of lane (c = feature 16 b + c, g) over the edges kappa_chain(g, s).
-// tile = &DT[16 b][base] of DT[f][e] (row pitch ldE, a multiple of 8; the same
-// for every lane), lane_off = c ldE * 2 bytes; edges past the nvalid of the tile
-// are not written.
-__device__ __forceinline__ void store_fmajor(bf16* tile, uint32_t lane_off, int nvalid, int g, const bf16x8& v) {
-  char* p = reinterpret_cast<char*>(tile) + lane_off;
-  if (nvalid >= TE) {
-    bf16x4 lo, hi;
-    lo[0] = v[0]; lo[1] = v[1]; lo[2] = v[2]; lo[3] = v[3];
-    hi[0] = v[4]; hi[1] = v[5]; hi[2] = v[6]; hi[3] = v[7];
-    *reinterpret_cast<bf16x4*>(p + 8 * g) = lo;
-    *reinterpret_cast<bf16x4*>(p + 32 + 8 * g) = hi;
-  } else {
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int k = kappa_chain(g, s);
-      if (k < nvalid) reinterpret_cast<bf16*>(p)[k] = v[s];
-    }
-  }
-}
 
 // ---------------------------------------------------------------------------
 // forward
@@ -419,8 +397,10 @@ __global__ __launch_bounds__(W * 64) void wide_fwd_kernel(FwdArgs a) {
 //    stage before it, into the registers whose MFMAs have just been issued.
 // dw2_mov = sum_e g_phi p and dw_d = sum_e r^2 g_a1 are summed in fp32, each lane's sums in its own
 // LDS slots (read, added to and written back once per tile, in tile order), and written as per-block
-// partials [gridDim.x][M | H]; the other weight gradients go through the feature-major factors m1,
-// m (EGNN), g_q (EGNN) and g_a2.  W_u's fragments are read from LDS in S1: registers are the limit.
+// partials [gridDim.x][M | H]; the other weight gradients go through the edge-major factors m1,
+// m (EGNN), g_q (EGNN) and g_a2 ([E][256] bf16, each lane storing its C-block's 4 features of one
+// edge, as Gh), reduced by the split-K products.  W_u's fragments are read from LDS in S1:
+// registers are the limit.
 template <int H, int W, bool EQ, int NUC>
 __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
   constexpr int O = H, M = H;
@@ -479,7 +459,6 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
     }
     for (int q = threadIdx.x; q < H; q += W * 64) s_wd[q] = a.fr.wdf[q];
   }
-  const bf16x8 I = ident_chunk(c, g);
 
   // ---- the edge-record ring: raw values of edge l & 31 of a tile (loader wave), stored in LDS in
   // S4 of the tile; every wave consumes the registers there (an empty asm use), so that no load
@@ -546,14 +525,16 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
       }
     }
   };
-  // feature-major factor rows: row 16 rb + c of [feature][edge] (pitch ldE) at lane byte offset fmo
-  auto fmrow = [&](int j) { return (int64_t)(16 * (rb0 + j)) * a.ldE; };
-  const uint32_t fmo = (uint32_t)(c * a.ldE) * 2u;
+  // edge-major rows [E][H] (factors, Gh): the lane's 4 features of row block rb for edge b + 16 nb + c
+  auto store_row4 = [&](bf16* D, int64_t b, int rb, int nb, const f32x4& v) {
+    store_bf16x4(D + (b + nb * 16) * H + 16 * rb + (c * H + 4 * g), v);
+  };
   auto nvalid_of = [&](int64_t tt) { return (int)(E - tt * TE < TE ? E - tt * TE : TE); };
 
   // ---- S1 of tile tt: m1 = SiLU(W_u U + P_i + Q_j) to s_m1 and Dm1, s1 = SiLU'
   bf16x4 s1[BH][2];
   auto stage1 = [&](int64_t tt, int sl) {
+    const int nv = nvalid_of(tt);
     bf16x8 u[2][NUC];
 #pragma unroll
     for (int nb = 0; nb < 2; ++nb) {
@@ -592,8 +573,8 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
         }
         s1[j][nb] = pack4(d);
         put_chain(s_m1, rb0 + j, nb, l, y[nb]);
+        if (nb * 16 + c < nv) store_row4(Dm1, tt * TE, rb0 + j, nb, y[nb]);
       }
-      store_fmajor(Dm1 + fmrow(j) + tt * TE, fmo, nvalid_of(tt), g, edge_major(y[0], y[1], I));
     }
   };
   bf16x4 gmr[BH][2];
@@ -698,9 +679,11 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
             d[i] = r.d;
           }
           s2[j][nb] = pack4(d);
-          if (EQ) put_chain(s_m, rb, nb, l, y[nb]);
+          if (EQ) {
+            put_chain(s_m, rb, nb, l, y[nb]);
+            if (valid[nb]) store_row4(Dm, base, rb, nb, y[nb]);
+          }
         }
-        if (EQ) store_fmajor(Dm + fmrow(j) + base, fmo, nvalid, g, edge_major(y[0], y[1], I));
       }
     }
     __syncthreads();
@@ -732,9 +715,9 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
             sw[i] += gphi[nb] * r.y;
           }
           put_chain(s_gq, rb, nb, l, gq[nb]);
+          if (valid[nb]) store_row4(Dgq, base, rb, nb, gq[nb]);
         }
         *reinterpret_cast<f32x4*>(dacc + 2 * j * 256) = sw;
-        store_fmajor(Dgq + fmrow(j) + base, fmo, nvalid, g, edge_major(gq[0], gq[1], I));
       }
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
@@ -767,8 +750,8 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) ga[nb][i] = acc[j][nb][i] * d[i];
           put_chain(s_ga2, rb0 + j, nb, l, ga[nb]);
+          if (valid[nb]) store_row4(Dga2, base, rb0 + j, nb, ga[nb]);
         }
-        store_fmajor(Dga2 + fmrow(j) + base, fmo, nvalid, g, edge_major(ga[0], ga[1], I));
       }
     }
     store_rec(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);   // the ring slot two tiles ahead (read after the end of the tile)
@@ -810,7 +793,7 @@ __global__ __launch_bounds__(W * 64) void wide_bwd_kernel(BwdArgs a) {
               sd[i] += r2[nb] * g1[i];
             }
           }
-          if (valid[nb]) store_bf16x4(Gh + (base + nb * 16) * H + 16 * rb + (c * H + 4 * g), g1);
+          if (valid[nb]) store_row4(Gh, base, rb, nb, g1);
         }
         if (EQ) *reinterpret_cast<f32x4*>(dacc + (2 * j + 1) * 256) = sd;
       }
