@@ -819,6 +819,21 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(Gemm2Args g) {
   gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, blockIdx.x, blockIdx.y, blockIdx.z, smem);
 }
 
+// Split-K launches, 1D grid, XCD-aware: block b is dispatched to XCD b % 8, and the gx x gy output
+// tiles of split z go to consecutive blocks of XCD z % 8, so the tiles that share a split's operand
+// rows read them through one L2 (a 3-D grid puts them on different XCDs: each operand fetched once
+// per tile row or column).  The grid holds gx gy roundup(gz, 8) blocks; those past the last split
+// leave before any barrier.
+template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
+__global__ __launch_bounds__(256) void gemm_bf16_xcd_kernel(Gemm2Args g, int gx, int gy, int gz) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[GemmBf16Smem<A_KC, B_NC, BM, BN, BK, NBUF>::n];
+  const int b = (int)blockIdx.x, per = gx * gy, jx = b / 8;
+  const int bz = (jx / per) * 8 + b % 8;
+  if (bz >= gz) return;
+  const int tile = jx % per;
+  gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, tile % gx, tile / gx, bz, smem);
+}
+
 // 1D grid with the n tiles of one row block adjacent (they share the A rows,
 // read once from memory while they are in L2), then the row blocks, then the split
 template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
@@ -1174,6 +1189,20 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
       }
     }
     const dim3 gb((unsigned)row_tiles(g, big ? 128 : 32), (unsigned)cdiv(g.N, narrow ? 32 : big ? 128 : 64), gz);
+    if (big && !narrow && g.ksplit > 0 && gz > 1 && gb.x * gb.y > 1) {   // split-K over many rows, shared operands
+      const int64_t nb = (int64_t)gb.x * gb.y * cdiv(gz, 8) * 8;
+      if (nb < (int64_t(1) << 31)) {
+        const dim3 gxd((unsigned)nb);
+#define GX_LAUNCH(AK, BNC) \
+        hipLaunchKernelGGL((gemm_bf16_xcd_kernel<AK, BNC, 128, 128, 64, 2>), gxd, dim3(256), 0, st, g, (int)gb.x, (int)gb.y, (int)gz)
+        if (g.a_kc && g.b_nc) GX_LAUNCH(true, true);
+        else if (g.a_kc) GX_LAUNCH(true, false);
+        else if (g.b_nc) GX_LAUNCH(false, true);
+        else GX_LAUNCH(false, false);
+#undef GX_LAUNCH
+        return (int)hipGetLastError();
+      }
+    }
 #define GB_LAUNCH(AK, BNC)                                                                         \
     do {                                                                                           \
       if (narrow) hipLaunchKernelGGL((gemm_bf16_kernel<AK, BNC, 128, 32, 64, 2>), gb, dim3(256), 0, st, g); \
