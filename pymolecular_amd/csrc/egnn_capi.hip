@@ -267,7 +267,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
   // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
   auto splitk2 = [&](Gemm2Args g, float* dst) -> int32_t {
-    g.ksplit = splitk_len(g.M, g.N, g.K);
+    g.ksplit = splitk_len(g.M, g.N, g.K, s.bf16);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
     ProfScope ps(EGNN_K_WGRAD, st);
@@ -377,7 +377,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
     g.M = s.F + 1; g.N = 2 * s.H; g.K = s.N;
     g.A = h; g.lda = strides->h; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.F;
     g.B = w.dPQ; g.ldb = 2 * s.H; g.b_bf16 = s.bf16; g.b_nc = 1;
-    g.ksplit = splitk_len(g.M, g.N, g.K);
+    g.ksplit = splitk_len(g.M, g.N, g.K, s.bf16);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(s.N, 1), g.ksplit);
     if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
@@ -550,12 +550,12 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   s1.A = x1; s1.lda = ld1; s1.a_bf16 = s.bf16; s1.a_kc = 0; s1.a_ones_row = s.K;
   if (s.K2 > 0) { s1.A2 = x2; s1.lda2 = ld2; s1.a_split = s.K1; }
   s1.B = w.dz; s1.ldb = s.Hn; s1.b_bf16 = s.bf16; s1.b_nc = 1;
-  s1.ksplit = splitk_len(s1.M, s1.N, s1.K); s1.partial = w.part1;
+  s1.ksplit = splitk_len(s1.M, s1.N, s1.K, s.bf16); s1.partial = w.part1;
   Gemm2Args s2{};
   s2.M = s.Hn + 1; s2.N = s.Fo; s2.K = s.N;
   s2.A = act; s2.lda = s.Hn; s2.a_bf16 = s.bf16; s2.a_kc = 0; s2.a_ones_row = s.Hn;
   s2.B = grad_out; s2.ldb = ldgo; s2.b_bf16 = s.bf16; s2.b_nc = 1;
-  s2.ksplit = splitk_len(s2.M, s2.N, s2.K); s2.partial = w.part2;
+  s2.ksplit = splitk_len(s2.M, s2.N, s2.K, s.bf16); s2.partial = w.part2;
   const int64_t nsplit1 = cdiv(std::max<int64_t>(s.N, 1), s1.ksplit), nsplit2 = cdiv(std::max<int64_t>(s.N, 1), s2.ksplit);
   if (nsplit1 * s1.M * s1.N > w.part1_elems || nsplit2 * s2.M * s2.N > w.part2_elems) return EGNN_ERR_WORKSPACE;
   if (s.N > 0) {   // two launches of two independent products each
@@ -629,7 +629,7 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
   dense_ws_layout(N, Kin, Nout, workspace, &w);
   hipStream_t st = (hipStream_t)stream;
   ProfScope ps(EGNN_K_NODE_UPDATE, st);
-  const int64_t ksplit = splitk_len(Kin + 1, Nout, N);
+  const int64_t ksplit = splitk_len(Kin + 1, Nout, N, bf16);
   const int64_t nsplit = cdiv(std::max<int64_t>(N, 1), ksplit);
   int32_t rc;
   if (N > 0) {   // S = [x | 1]^T dy, split over the nodes

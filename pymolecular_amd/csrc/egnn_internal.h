@@ -103,7 +103,7 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
 // and the fp32 partial elements that need.  Reductions over kSplitKBig rows or
 // more use 128 x 128 tiles.
 constexpr int64_t kSplitKBig = 65536;
-int64_t splitk_len(int64_t M, int64_t N, int64_t K);
+int64_t splitk_len(int64_t M, int64_t N, int64_t K, bool fold);   // fold: bf16 products (ones row folded)
 int64_t splitk_parts(int64_t M, int64_t N, int64_t K);
 
 // ---- launchers (return hipError_t as int) --------------------------------

@@ -74,12 +74,13 @@ size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w) {
   return off;
 }
 
-int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
+int64_t splitk_len(int64_t M, int64_t N, int64_t K, bool fold) {
   K = std::max<int64_t>(K, 1);
   const bool big = K >= kSplitKBig;   // the tile launch_gemm2 picks for this product
-  // row tiles: M = R + 1 with R a multiple of the tile is taken as rows plus the ones row (a bias
-  // gradient), which the first row tile folds in
-  auto rt = [&](int64_t bm) { return (M > 1 && (M - 1) % bm == 0) ? (M - 1) / bm : cdiv(M, bm); };
+  // row tiles: with fold (the bf16 products), M = R + 1 with R a multiple of the tile is taken as rows
+  // plus the ones row of a bias gradient, which the first row tile folds in.  Folding only adds
+  // splits, so the workspace is sized with it.
+  auto rt = [&](int64_t bm) { return (fold && M > 1 && (M - 1) % bm == 0) ? (M - 1) / bm : cdiv(M, bm); };
   const int64_t tiles = N == 1 ? 1 : big ? rt(128) * cdiv(N, N <= 32 ? 32 : 128) : rt(64) * cdiv(N, 64);
   // matrix-vector products: one small block per split; 64 x 64 tiles: about 256 rows per split at the
   // node counts of molecule batches (measured faster than 32 x 64 tiles over 700 rows: fewer re-reads
@@ -90,7 +91,7 @@ int64_t splitk_len(int64_t M, int64_t N, int64_t K) {
 }
 
 int64_t splitk_parts(int64_t M, int64_t N, int64_t K) {
-  return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K)) * M * N;
+  return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K, true)) * M * N;
 }
 
 int64_t factor_chunk_edges(const LayerShape& s) {
