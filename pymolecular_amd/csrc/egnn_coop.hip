@@ -1328,6 +1328,7 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     gather(0);
     stage1(blockIdx.x, 0, s1);
   }
+  asm volatile("" ::"v"(gmr_next));   // complete on entry to the tile loop, as at its back edge
   __syncthreads();   // m1 of the first tile
 
   int par = 0, sl0 = 0;
@@ -1405,6 +1406,9 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     // ---- S1 of the next tile (past the last tile: of a stand-in tile, never read), ring slot of t + 2
     stage1(t + G, par ^ 1, s1);
     store_idx(sl2, t2);
+    // the next tile's message-gradient rows, waited for here (a tile after their load) and not at
+    // the top of the next tile, where the wait would also cover this tile's Gh store
+    asm volatile("" ::"v"(gmr_next));
     __syncthreads();
   }
 
