@@ -96,7 +96,7 @@ def path_model(cls, N, E, F, H, O, M, FE, g, s):
     return 0, 0
 
 
-def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
+def kernel_work(cls, path, N, E, F, H, O, M, FE, g, s):
     """Executed algorithmic (MFMA FLOPs, HBM bytes) of one launch of a kernel class, as this build runs it.
 
     FLOPs count the products the kernel must execute with the first layer's node projections hoisted
@@ -109,9 +109,12 @@ def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
         return flops * E, E * (2 * H * s + eb) + N * (O * s + 12 * g)
     if cls == "bwd_edge":
         per_edge = 2 * H * s + eb + O * s + 12 * g + H * s + 16 * g      # + grad rows of i, Gh and Gx stores
-        if coop:      # weight gradients accumulated in registers
+        if path == "coop":   # weight gradients accumulated in registers
             flops = 4 * (g + FE) * H + 6 * H * O + 6 * g * O * M
-        else:         # weight-gradient factors m1, m, g_q, p, g_a2 stored for the split-K GEMMs
+        elif path == "wide":  # factors m1, m, g_q, g_a2 stored for the split-K products (dw2_mov, dw_d in the kernel)
+            flops = 2 * (g + FE) * H + 4 * H * O + 4 * g * O * M
+            per_edge += (H + O + g * M + O) * s
+        else:         # one wave per tile: factors m1, m, g_q, p, g_a2 and r^2 stored for the split-K products
             flops = 2 * (g + FE) * H + 4 * H * O + 4 * g * O * M
             per_edge += (H + O + 2 * g * M + O) * s + 4 * g
         return flops * E, E * per_edge
@@ -121,7 +124,10 @@ def kernel_work(cls, coop, N, E, F, H, O, M, FE, g, s):
         return 2 * N * F * 2 * H, N * (F + 2 * H) * s
     if cls == "wgrad":   # whole layer: dh and [dW_n1 | dW_n2; db1] over the nodes, plus the edge-factor products
         flops, nbytes = 2 * N * (F + 1) * 2 * H + 2 * N * 2 * H * F, N * (F + 2 * H) * s + N * (2 * H + F) * s
-        if not coop:
+        if path == "wide":     # [dW_hl; db2], [dW1_mov; dbx1] over the edge factors; dW_e over Gh
+            flops += 2 * E * ((H + 1) * O + g * (O + 1) * M + H * FE)
+            nbytes += E * ((H + O) * s + g * (O + M) * s + (H * s + FE * s + 4 if FE else 0))
+        elif path == "one":    # the same, plus the dw2_mov and dw_d matrix-vector products over p, Gh and r^2
             flops += 2 * E * ((H + 1) * O + g * ((O + 1) * M + M + H) + H * FE)
             nbytes += E * ((H + O) * s + g * ((O + M) * s + M * s + 4 + H * s + 4) + (H * s + FE * s + 4 if FE else 0))
         return flops, nbytes
@@ -290,11 +296,11 @@ def run_workload(k, dtype, a, g=None):
 
     s = 2 if dt == torch.bfloat16 else 4
     g1 = 1 if eq else 0
-    coop = s == 2 and H == 128 and FE + 2 * g1 <= 32
+    path = "coop" if s == 2 and H == 128 and FE + 2 * g1 <= 32 else "wide" if s == 2 and H == 256 else "one"
     peak_mfma = PEAK["bf16_mfma_tflops"] if s == 2 else PEAK["fp32_mfma_tflops"]
 
     def executed_per_launch(cls, launches_per_step):
-        fl, by = kernel_work(cls, coop, N, E, H, H, H, H, FE, g1, s)
+        fl, by = kernel_work(cls, path, N, E, H, H, H, H, FE, g1, s)
         if cls == "wgrad":   # a class of several launches per layer: the average launch
             return fl * L / launches_per_step, by * L / launches_per_step
         return fl, by

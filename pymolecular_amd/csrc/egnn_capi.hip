@@ -454,8 +454,8 @@ size_t node_ws_layout(const NodeShape& s, void* base, NodeWs* w) {
   char* b = (char*)base;
   size_t off = 0;
   auto take = [&](size_t bytes) { void* p = b ? b + off : nullptr; off = align_up(off + bytes); return p; };
-  w->part1_elems = splitk_parts(s.K + 1, s.Hn, s.N);
-  w->part2_elems = splitk_parts(s.Hn + 1, s.Fo, s.N);
+  w->part1_elems = splitk_parts(s.K + 1, s.Hn, s.N, s.bf16);
+  w->part2_elems = splitk_parts(s.Hn + 1, s.Fo, s.N, s.bf16);
   w->dz = take((size_t)s.N * s.Hn * s.esz);
   w->part1 = (float*)take((size_t)w->part1_elems * sizeof(float));
   w->part2 = (float*)take((size_t)w->part2_elems * sizeof(float));

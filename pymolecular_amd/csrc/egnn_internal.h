@@ -104,7 +104,8 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
 // more use 128 x 128 tiles.
 constexpr int64_t kSplitKBig = 65536;
 int64_t splitk_len(int64_t M, int64_t N, int64_t K, bool fold);   // fold: bf16 products (ones row folded)
-int64_t splitk_parts(int64_t M, int64_t N, int64_t K);
+// split-K partial elements of an M x N product over K (fold as for splitk_len; true is the larger)
+int64_t splitk_parts(int64_t M, int64_t N, int64_t K, bool fold = true);
 
 // ---- launchers (return hipError_t as int) --------------------------------
 int launch_schedule(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E, const SchedView& v,

@@ -90,8 +90,8 @@ int64_t splitk_len(int64_t M, int64_t N, int64_t K, bool fold) {
   return cdiv(cdiv(K, splits), 64) * 64;
 }
 
-int64_t splitk_parts(int64_t M, int64_t N, int64_t K) {
-  return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K, true)) * M * N;
+int64_t splitk_parts(int64_t M, int64_t N, int64_t K, bool fold) {
+  return cdiv(std::max<int64_t>(K, 1), splitk_len(M, N, K, fold)) * M * N;
 }
 
 int64_t factor_chunk_edges(const LayerShape& s) {
@@ -130,15 +130,15 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->dwpart = w->nblk > 0 ? (float*)take((size_t)w->nblk * w->LW * sizeof(float)) : nullptr;
   w->dPQ = take((size_t)s.N * 2 * s.H * s.esz);
   // split-K partials: largest (splits x M x N) over the weight-gradient GEMMs
-  w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N);
+  w->part_elems = splitk_parts(s.F + 1, 2 * s.H, s.N, s.bf16);
   if (!coop) {   // the factor products run over one chunk of edges at a time, dw_d and dW_e over all
     // (the split length is rounded per K: the shorter last chunk may need more partial rows)
     const int64_t lastE = std::max<int64_t>(s.E, 1) - (int64_t)(w->nchunk - 1) * w->chunkE;
     for (const int64_t K : {w->chunkE, lastE})
-      w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, K), splitk_parts(s.O + 1, s.M, K),
-                                         splitk_parts(s.M, 1, K)});
-    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H, 1, s.E),
-                                       splitk_parts(s.H, std::max(s.FE, 1), s.E)});
+      w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, K, s.bf16), splitk_parts(s.O + 1, s.M, K, s.bf16),
+                                         splitk_parts(s.M, 1, K, s.bf16)});
+    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H, 1, s.E, s.bf16),
+                                       splitk_parts(s.H, std::max(s.FE, 1), s.E, s.bf16)});
   }
   w->chunkres = (coop || wide || w->nchunk == 1)
                     ? nullptr
