@@ -776,58 +776,60 @@ __global__ __launch_bounds__(W * 64) void coop_bwd_kernel(BwdArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// backward of the equivariant layer, H = O = M = 128, 8 waves per tile
+// backward of the equivariant layer, H = O = M = 128, 8 waves, 64-edge tiles
 // ---------------------------------------------------------------------------
-// The stages of coop_bwd_kernel with three changes.  W_hl and W1_mov are held
-// in LDS once each, row-major: the A operands of W_hl m1-type products (rows of
-// W^T) come from transposing LDS reads, those of W products from plain 8-byte
-// reads, so no transposed copy and no weight registers are needed.  The tiles
-// are software-pipelined: S1 of the next tile (VALU work: SiLU and SiLU' of the
-// first layer) runs in the same barrier interval as S5 of this tile (MFMA work:
-// g_a1 and the dW_hl products), which leaves four barriers per tile.  And the
-// loads run ahead: the indices of tile t + 2 and the P_i / Q_j / edge-feature
-// gathers of tile t + 1 are issued at the top of tile t.
+// The stages of coop_bwd_kernel on tiles of 64 edges (two schedule tiles, four
+// 16-edge blocks per wave): every weight fragment read from LDS feeds four
+// products, and each barrier interval holds four independent product chains.
+// W_hl and W1_mov are held in LDS once each, row-major: the A operands of
+// W_hl^T-type products (S2, S3) come from transposing LDS reads, those of W
+// products (S4, S5) from plain 8-byte reads.  Every stage output passes through
+// a chain buffer, and the edge-major operands of the weight-gradient products
+// are transposing reads of those buffers.  The tiles are software-pipelined: S1
+// of the next tile runs in the same barrier interval as S5 of this tile, which
+// leaves four barriers per tile, and the loads run ahead: the indices of tile
+// t + 2 and the P_i / Q_j / edge-feature gathers of tile t + 1 are issued at the
+// top of tile t.
 template <int NU>
 __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
-  constexpr int H = 128, O = 128, M = 128, W = 8;
+  constexpr int H = 128, O = 128, M = 128, W = 8, NB = 4, TP = 16 * NB;
   constexpr int KH = H / 32, KO = O / 32, KM = M / 32;
   constexpr int NO = O / 16, NM = M / 16;
-  constexpr int NUS = NU > 0 ? 16 * NU : 8;         // slot rows of the edge-feature tile
+  constexpr int PU = 40;                            // row pitch of the edge-input tiles (bf16, 80 bytes)
   constexpr int WP = 136;                           // row pitch of the LDS weight matrices (bf16, 272 bytes)
-  constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 edge blocks (8 KB)
-  // m1 of the next tile is written while this tile's g_a2 is read: separate
-  // buffers; m (S2 -> S3) shares storage with g_a2 edge-major (S4 -> S5).  The
-  // waves' own m1 and m rows edge-major are transposing reads of the chain buffers.
+  constexpr int CH = KH * NB * 64 * 8;              // chain buffer: 4 chunks x 4 edge blocks (16 KB)
+  // m1 (S1 -> S2, S5) is written for the next tile in S5 of this tile, by each wave for its own rows
   __shared__ __attribute__((aligned(16))) bf16 s_m1[CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_ga2[CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_buf2[CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_gq[CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_gqN[NM * 64 * 8];
+  __shared__ __attribute__((aligned(16))) bf16 s_m[CH];     // S2 -> S3, S4
+  __shared__ __attribute__((aligned(16))) bf16 s_gq[CH];    // S3 -> S4
+  __shared__ __attribute__((aligned(16))) bf16 s_ga2[CH];   // S4 -> S5
   __shared__ __attribute__((aligned(16))) bf16 s_Whl[H * WP];    // W_hl[h][o]
   __shared__ __attribute__((aligned(16))) bf16 s_Wmov[O * WP];   // W1_mov[o][m]
-  bf16* const s_m = s_buf2;
-  bf16* const s_ga2N = s_buf2;
-  __shared__ float s_phi[W][TE];
-  __shared__ float s_gr[W][TE];
-  // [edge][slot] edge features of a tile, by tile parity (the next tile's S1 writes while S5 reads)
-  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NUS * TE];   // slot-major (put_ut)
+  __shared__ float s_phi[W][TP];
+  __shared__ float s_gr[W][TP];
+  // the edge inputs of a tile by tile parity, [edge][slot]: F_E features, r^2 as a bf16 hi + lo
+  // pair in slots F_E, F_E + 1, zeros up to 32 (the B operands of S1, and by transposing reads
+  // those of the dW_e product); the tile t + 1 inputs are stored in S4 of tile t
+  __shared__ __attribute__((aligned(16))) bf16 s_ub[2][TP * PU];
   __shared__ __attribute__((aligned(16))) float s_vec[O + 2 * M + H];
   float* const s_b2 = s_vec;
   float* const s_bx1 = s_vec + O;
   float* const s_w2m = s_vec + O + M;
   float* const s_wd = s_vec + O + 2 * M;
 
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  // slot rows at and past F_E stay zero (the tile loop writes rows below F_E only)
-  for (int q = a.FE * TE + (int)threadIdx.x; q < NUS * TE; q += 512) s_u[0][q] = s_u[1][q] = (bf16)0.0f;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // lane index and its parts; made opaque again at the top of every tile, so that the compiler
+  // recomputes the lane-dependent LDS and memory offsets where they are used instead of keeping
+  // them all in registers across the tile loop
+  int l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   const char* PQb = (const char*)a.PQ;   // P | Q rows are 4H bytes; N * 4H < 2^32 (coop_supported)
   const bf16* ef = (const bf16*)a.ef;
   const bf16* gmsg = (const bf16*)a.gmsg;
   bf16* Gh = (bf16*)a.Gh;
-  const int64_t E = a.E;
+  const int E = (int)a.E;   // edge indices below 2^31 (coop_supported)
   const int N = (int)a.N;
   const int FE = a.FE;
-  const int64_t G = gridDim.x;
+  const int G = (int)gridDim.x, ntp = (int)((a.E + TP - 1) / TP);   // 64-edge tiles
 
   for (int q = threadIdx.x; q < O; q += W * 64) s_b2[q] = a.fr.b2f[q];
   for (int q = threadIdx.x; q < M; q += W * 64) {
@@ -843,11 +845,9 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
     fill_weight_lds<H, O, WP, W * 64>(s_Whl, (const bf16*)a.w2);
     fill_weight_lds<O, M, WP, W * 64>(s_Wmov, (const bf16*)a.w1m);
   }
-  auto a_rows = [&](const bf16* Wl, int blk, int kc) { return lds_rows<WP>(Wl, blk, kc, c, g); };
-  auto a_cols = [&](const bf16* Wl, int blk, int kc) { return lds_cols<WP>(Wl, blk, kc, c, g); };
+  auto a_rows = [&](const bf16* Wl, int kc) { return lds_rows<WP>(Wl, w, kc, c, g); };
+  auto a_cols = [&](const bf16* Wl, int kc) { return lds_cols<WP>(Wl, w, kc, c, g); };
   const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)w * kFragElems + l * 8);
-  const bf16x8 I = ident_chunk(c, g);
-  const bf16x8 Ipq = pq_sum_chunk(c, g);
 
   f32x4 acc_whl[NO], acc_w1m[NM], acc_wu[NU > 0 ? NU : 1];
 #pragma unroll
@@ -859,25 +859,26 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   f32x4 vb2 = zero4(), vbx1 = zero4(), vw2m = zero4(), vwd = zero4();
 
   // Indices and geometry of the tiles pass through a ring of three LDS slots
-  // (tiles t, t + 1, t + 2), fetched by the loader wave at the top of tile t for
-  // tile t + 2 and stored into the ring in the last barrier interval of tile t;
-  // every wave reads the values it needs from the ring.  No value loaded from
-  // memory is carried in registers from one tile to the next.  The loads that
+  // (tiles t, t + 1, t + 2), fetched by the loader wave (lane l: edge l of the
+  // tile) at the top of tile t for tile t + 2 and stored into the ring in the
+  // last barrier interval of tile t; every wave reads the values it needs from
+  // the ring.  No value loaded from memory is carried in registers from one
+  // tile to the next except the message-gradient rows (below).  The loads that
   // only some waves issue come first at the top of a tile and every wave
   // consumes their registers (an empty asm use) in the same tile: then the
   // compiler's memory-counter waits stay exact (a wave-dependent load followed
   // by the loads a wave waits on, or a register that may still be loading at
   // the next tile, makes it wait for all outstanding loads).
-  constexpr int LDW = W - 1;   // loader wave (waves 0 and 1 do S6)
-  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
-  __shared__ float s_r2[3][TE], s_gp[3][TE];
+  constexpr int LDW = W - 1;   // loader wave (waves 0..3 do S6)
+  __shared__ int s_ri[3][TP], s_rj[3][TP], s_eid[3][NU > 0 ? TP : 1];
+  __shared__ float s_r2[3][TP], s_gp[3][TP];
   const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
   int ld_ri = 0, ld_rj = 0, ld_eid = 0;
   float ld_r2 = 0.f, ld_gp = 0.f;
-  auto load_idx = [&](int64_t tt) {   // raw values of edge l (loader wave); nothing reads them before store_idx
+  auto load_idx = [&](int tt) {   // raw values of edge l (loader wave); nothing reads them before store_idx
     if (w == LDW) {
-      const int e0 = (int)(tt * TE) + (l & 31);   // edge ids below 2^31 (coop_supported)
-      const int e = e0 < (int)E ? e0 : (int)E - 1;
+      const int e0 = tt * TP + l;
+      const int e = e0 < E ? e0 : E - 1;
       ld_ri = a.erow[e];
       ld_rj = a.col[e];
       if constexpr (NU > 0) ld_eid = eidp[e];
@@ -886,53 +887,54 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
       ld_gp = q.y;
     }
   };
-  auto store_idx = [&](int slot, int64_t tt) {
+  auto store_idx = [&](int slot, int tt) {
     asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid), "v"(ld_r2), "v"(ld_gp));   // complete in every wave
-    if (w == LDW && l < TE) {
-      const int64_t e = tt * TE + l;
+    if (w == LDW) {
+      const int e = tt * TP + l;
       s_ri[slot][l] = clampi(ld_ri, N);
       s_rj[slot][l] = clampi(ld_rj, N);
-      if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, (int)E) : (int)(e < E ? e : E - 1);
+      if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, E) : (e < E ? e : E - 1);
       s_r2[slot][l] = ld_r2;
       s_gp[slot][l] = e < E ? ld_gp : 0.f;   // invalid edges contribute nothing through g_phi = 0
     }
   };
-  // the gathers of S1 from ring slot `slot`: P_i and Q_j of the wave's 16 rows and
-  // (F_E > 0) the edge features, two edge blocks; the input chunk is put together in S1
-  bf16x8 pq[2];
-  bf16x8 ue[2];
+  // the gathers of S1 from ring slot `slot`: P_i and Q_j of the wave's 16 rows, four edge blocks
+  bf16x8 pq[NB];
   auto gather = [&](int slot) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       const uint32_t i = (uint32_t)s_ri[slot][nb * 16 + c], j = (uint32_t)s_rj[slot][nb * 16 + c];
       pq[nb] = pq_gather(PQb, i, j, w, g, H);
-      if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
-        ue[nb] = load_chunk(ef + (int64_t)s_eid[slot][nb * 16 + c] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
     }
   };
+  // the edge inputs of a tile from ring slot `slot`: lane (w, l) loads and stores slots
+  // 4 uh .. 4 uh + 3 of edge ue (512 lanes: 64 edges x 32 slots)
+  bf16x4 uld;
+  auto load_u = [&](int slot) {
+    const int q = w * 64 + l, ue = q >> 3, uh = q & 7;
+    if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in store_u
+      uld = *reinterpret_cast<const bf16x4*>(ef + (int64_t)s_eid[slot][ue] * a.se + (4 * uh + 4 <= FE ? 4 * uh : 0));
+  };
+  auto store_u = [&](int slot, int tt, int par) {
+    const int q = w * 64 + l, ue = q >> 3, uh = q & 7;
+    bf16x4 v = {};
+    if (NU > 0 && 4 * uh + 4 <= FE) v = uld;
+    if (4 * uh == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
+      const float r2 = s_r2[slot][ue];
+      const bf16 hi = (bf16)r2;
+      v[0] = hi;
+      v[1] = (bf16)(r2 - (float)hi);
+    }
+    if (tt * TP + ue >= E) v = bf16x4{};   // edges past the end: zero inputs
+    *reinterpret_cast<bf16x4*>(s_ub[par] + ue * PU + 4 * uh) = v;
+  };
   // ---- S1 of tile tt: m1 (to s_m1), s1 = SiLU/SiLU'(W_u U + P_i + Q_j), the wave's H rows
-  auto stage1 = [&](int64_t tt, int slot, int par, bf16x4* s1o) {
-    bf16x8 u[2];
+  auto stage1 = [&](int par, bf16x4* s1o) {
+    const bf16x8 Ipq = pq_sum_chunk(c, g);
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      u[nb] = (NU > 0 && 8 * g + 8 <= FE) ? ue[nb] : zero_chunk<bf16>();
-      if (8 * g == FE) {   // r^2 as a bf16 hi + lo pair in slots F_E, F_E + 1
-        const float r2 = s_r2[slot][nb * 16 + c];
-        const bf16 hi = (bf16)r2;
-        u[nb][0] = hi;
-        u[nb][1] = (bf16)(r2 - (float)hi);
-      }
-    }
-    // the tile's edge features, slot-major, for the dW_e product (zero edges past the end)
-    if (NU > 0 && w == 0 && 8 * g < FE) {
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb)
-        put_ut(s_u[par], nb, c, g, tt * TE + nb * 16 + c < E ? u[nb] : zero_chunk<bf16>());
-    }
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       f32x4 acc = zero4();
-      mma(acc, wu, u[nb]);
+      mma(acc, wu, *reinterpret_cast<const bf16x8*>(s_ub[par] + (nb * 16 + c) * PU + 8 * g));
       mma(acc, Ipq, pq[nb]);   // + P_i + Q_j
       f32x4 y, d;
 #pragma unroll
@@ -942,220 +944,245 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
         d[i] = r.d;
       }
       s1o[nb] = pack4(d);
-      put_chain(s_m1, w, nb, l, y);
+      put_chain<NB, true>(s_m1, w, nb, l, y);
     }
   };
 
-  bf16x4 s1[2];
-  if (blockIdx.x < a.ntiles) {
-    const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
-    load_idx(blockIdx.x);
-    store_idx(0, blockIdx.x);
+  bf16x4 s1[NB];
+  const int b0 = (int)blockIdx.x;
+  if (b0 < ntp) {
+    const int t1 = b0 + G < ntp ? b0 + G : b0;
+    load_idx(b0);
+    store_idx(0, b0);
     load_idx(t1);
     store_idx(1, t1);
   }
   __syncthreads();   // weights, vectors and the first two ring slots in LDS
-  // the incoming message gradient of the wave's rows, loaded one tile ahead of its use (the only
-  // value carried from one tile to the next: a tile old at the top of the next tile); with two
-  // edge-input chunks (NU = 2) the registers are short, and it is loaded in its own tile
-  constexpr bool GM_AHEAD = NU < 2;
-  bf16x4 gmr_next[2];
+  // the incoming message gradient of the wave's rows, loaded one tile ahead of its use in S4 and
+  // waited for at the end of the tile it was loaded in; with edge features the registers are short,
+  // and it is loaded at the top of its own tile
+  constexpr bool GM_AHEAD = NU == 0;
+  bf16x4 gmr_next[NB];
   auto load_gm = [&](int slot) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb)
+    for (int nb = 0; nb < NB; ++nb)
       gmr_next[nb] = *reinterpret_cast<const bf16x4*>(gmsg + (int64_t)s_ri[slot][nb * 16 + c] * a.sgm + 16 * w + 4 * g);
   };
-  if (blockIdx.x < a.ntiles) {
+  if (b0 < ntp) {
+    load_u(0);
+    store_u(0, b0, 0);
+  }
+  __syncthreads();   // the edge inputs of the first tile
+  if (b0 < ntp) {
     if (GM_AHEAD) load_gm(0);
     gather(0);
-    stage1(blockIdx.x, 0, 0, s1);
+    stage1(0, s1);
   }
+  asm volatile("" ::"v"(gmr_next[0]), "v"(gmr_next[1]), "v"(gmr_next[2]), "v"(gmr_next[3]));
   __syncthreads();   // m1 of the first tile
 
   int par = 0, sl0 = 0;
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+  for (int t = b0; t < ntp; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+    asm volatile("" : "+v"(l));
+    c = l & 15;
+    g = l >> 4;
     const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
-    const int64_t base = t * TE;
-    bool valid[2];
+    const int base = t * TP;
+    bool valid[NB];
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) valid[nb] = base + nb * 16 + c < E;
-    // rows of the incoming message gradient (used in S4), the next tile's gathers
-    // (its S1 runs at the end of this tile), the indices of the tile after it
-    load_idx(t + 2 * G < a.ntiles ? t + 2 * G : t);
-    // S6 (waves 0 and 1): lane (w, l) computes component xc of dL/ddelta of edge xe;
+    for (int nb = 0; nb < NB; ++nb) valid[nb] = base + nb * 16 + c < E;
+    const int t2 = t + 2 * G < ntp ? t + 2 * G : t;
+    load_idx(t2);
+    // S6 (waves 0..3): lane (w, l) computes component w of dL/ddelta of edge l;
     // its delta and grad x_i components are loaded here
-    const int xe = l & 31, xc = (w * 64 + l) >> 5;
     float xdel = 0.f, xgrd = 0.f;
-    if (w < 2) {
-      const float* q = a.geo + (base + xe < E ? base + xe : E - 1) * 8;   // delta at 2..4, grad x_i at 5..7
-      const int xq = xc < 3 ? xc : 2;
+    if (w < 4) {
+      const float* q = a.geo + (int64_t)(base + l < E ? base + l : E - 1) * 8;   // delta at 2..4, grad x_i at 5..7
+      const int xq = w < 3 ? w : 2;
       xdel = q[2 + xq];
       xgrd = q[5 + xq];
     }
+    // the message-gradient rows of this tile (used in S4), the next tile's edge inputs (stored in
+    // S4), gathers (its S1 runs at the end of this tile) and message-gradient rows
+    bf16x4 gmr[NB];
+    load_u(sl1);
     if (!GM_AHEAD) load_gm(sl0);
-    const bf16x4 gmr[2] = {gmr_next[0], gmr_next[1]};
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) gmr[nb] = gmr_next[nb];
     if (GM_AHEAD) load_gm(sl1);
     gather(sl1);
 
     // ---- S2: m, s2 = SiLU/SiLU'(W_hl^T m1 + b2), the wave's O rows ---------
-    bf16x4 s2[2];
-    // this wave's m1 rows edge-major (dW_hl in S5)
-    const bf16x8 m1N = chain_edge_major(s_m1, w, c, g);
+    bf16x4 s2[NB];
     {
-      f32x4 y[2], acc[2];
-      acc[0] = acc[1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * w + 4 * g);
+      f32x4 acc[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[nb] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * w + 4 * g);
 #pragma unroll
       for (int kc = 0; kc < KH; ++kc) {
-        const bf16x8 A = a_cols(s_Whl, w, kc);
+        const bf16x8 A = a_cols(s_Whl, kc);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acc[nb], A, get_chain(s_m1, kc, nb, l));
+        for (int nb = 0; nb < NB; ++nb) mma(acc[nb], A, get_chain<NB, true>(s_m1, kc, nb, l));
       }
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        f32x4 d;
+      for (int nb = 0; nb < NB; ++nb) {
+        f32x4 y, d;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const YD r = silu_yd<bf16>(acc[nb][i]);
-          y[nb][i] = r.y;
+          y[i] = r.y;
           d[i] = r.d;
         }
         s2[nb] = pack4(d);
-        put_chain(s_m, w, nb, l, y[nb]);
+        put_chain<NB, true>(s_m, w, nb, l, y);
       }
     }
     __syncthreads();
 
     // ---- S3: q -> p = SiLU, g_q = gphi w2mov SiLU'(q), the wave's M rows ----
-    float phi[2] = {0.f, 0.f};
-    const bf16x8 mN = chain_edge_major(s_m, w, c, g);   // this wave's m rows edge-major (dW1_mov in S4)
-    const float gp[2] = {s_gp[sl0][c], s_gp[sl0][16 + c]};
     {
       const f32x4 w2mv = *reinterpret_cast<const f32x4*>(s_w2m + 16 * w + 4 * g);
-      f32x4 gq[2], accq[2];
-      accq[0] = accq[1] = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * w + 4 * g);
+      f32x4 accq[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) accq[nb] = *reinterpret_cast<const f32x4*>(s_bx1 + 16 * w + 4 * g);
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc) {
-        const bf16x8 A = a_cols(s_Wmov, w, kc);
+        const bf16x8 A = a_cols(s_Wmov, kc);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(accq[nb], A, get_chain(s_m, kc, nb, l));
+        for (int nb = 0; nb < NB; ++nb) mma(accq[nb], A, get_chain<NB, true>(s_m, kc, nb, l));
       }
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NB; ++nb) {
+        const float gp = s_gp[sl0][nb * 16 + c];
+        float phi = 0.f;
+        f32x4 gq;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const YD r = silu_yd<bf16>(accq[nb][i]);
-          phi[nb] += r.y * w2mv[i];
-          gq[nb][i] = gp[nb] * w2mv[i] * r.d;
-          vw2m[i] += r.y * gp[nb];
-          vbx1[i] += gq[nb][i];
+          phi += r.y * w2mv[i];
+          gq[i] = gp * w2mv[i] * r.d;
+          vw2m[i] += r.y * gp;
+          vbx1[i] += gq[i];
         }
-        put_chain(s_gq, w, nb, l, gq[nb]);
-      }
-      put_norm(s_gqN, w, l, edge_major(gq[0], gq[1], I));
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        phi[nb] += shfl_xor(phi[nb], 16);
-        phi[nb] += shfl_xor(phi[nb], 32);
-        if (g == 0) s_phi[w][nb * 16 + c] = phi[nb];
+        put_chain<NB, true>(s_gq, w, nb, l, gq);
+        phi += shfl_xor(phi, 16);
+        phi += shfl_xor(phi, 32);
+        if (g == 0) s_phi[w][nb * 16 + c] = phi;
       }
     }
     __syncthreads();
 
     // ---- S4: g_a2 = (gm_i + W1mov g_q) SiLU'(pre2), the wave's O rows ------
     {
-      f32x4 ga[2], acca[2];
+      f32x4 acca[NB];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) acca[nb] = valid[nb] ? unpack4(gmr[nb]) : zero4();
+      for (int nb = 0; nb < NB; ++nb) acca[nb] = valid[nb] ? unpack4(gmr[nb]) : zero4();
 #pragma unroll
       for (int kc = 0; kc < KM; ++kc) {
-        const bf16x8 A = a_rows(s_Wmov, w, kc);
+        const bf16x8 A = a_rows(s_Wmov, kc);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acca[nb], A, get_chain(s_gq, kc, nb, l));
+        for (int nb = 0; nb < NB; ++nb) mma(acca[nb], A, get_chain<NB, true>(s_gq, kc, nb, l));
       }
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NB; ++nb) {
         const f32x4 d = unpack4(s2[nb]);
+        f32x4 ga;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          ga[nb][i] = acca[nb][i] * d[i];
-          vb2[i] += ga[nb][i];
+          ga[i] = acca[nb][i] * d[i];
+          vb2[i] += ga[i];
         }
-        put_chain(s_ga2, w, nb, l, ga[nb]);
+        put_chain<NB, true>(s_ga2, w, nb, l, ga);
       }
-      put_norm(s_ga2N, w, l, edge_major(ga[0], ga[1], I));
-    }
-    // dW1_mov rows of this wave: sum_e m[o][e] g_q[m][e]
+      // the next tile's edge inputs (its S1 reads them after the next barrier)
+      store_u(sl1, t + G, par ^ 1);
+      // dW1_mov rows of this wave: sum_e m[o][e] g_q[m][e]
 #pragma unroll
-    for (int cb = 0; cb < NM; ++cb) mma(acc_w1m[cb], mN, get_norm(s_gqN, cb, l));
+      for (int eh = 0; eh < 2; ++eh) {
+        const bf16x8 mN = chain_edge_major<NB, true>(s_m, w, c, g, eh);
+#pragma unroll
+        for (int cb = 0; cb < NM; ++cb) mma(acc_w1m[cb], mN, chain_edge_major<NB, true>(s_gq, cb, c, g, eh));
+      }
+    }
     __syncthreads();
 
-    // ---- S1 of the next tile (past the last tile: of a stand-in tile, never
-    // read; the gathers are consumed on every path, so none is outstanding at
-    // the next tile).  With edge features it goes first in the interval, so
-    // that its SiLU work interleaves with S5's products; without, after S5
-    // (each order measured faster for its case).
-    bf16x4 s1n[2];
-    if constexpr (NU > 0) stage1(t + G, sl1, par ^ 1, s1n);
     // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1), the wave's H rows --------------
-    float gr[2] = {0.f, 0.f};
+    float gr[NB];
     {
       const f32x4 wdv = *reinterpret_cast<const f32x4*>(s_wd + 16 * w + 4 * g);
-      const float r2v[2] = {s_r2[sl0][c], s_r2[sl0][16 + c]};
-      f32x4 g1[2], acch[2] = {zero4(), zero4()};
+      f32x4 acch[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acch[nb] = zero4();
 #pragma unroll
       for (int kc = 0; kc < KO; ++kc) {
-        const bf16x8 A = a_rows(s_Whl, w, kc);
+        const bf16x8 A = a_rows(s_Whl, kc);
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) mma(acch[nb], A, get_chain(s_ga2, kc, nb, l));
+        for (int nb = 0; nb < NB; ++nb) mma(acch[nb], A, get_chain<NB, true>(s_ga2, kc, nb, l));
       }
+      f32x4 g1[NB];
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
+      for (int nb = 0; nb < NB; ++nb) {
         const f32x4 d = unpack4(s1[nb]);
+        const float r2v = s_r2[sl0][nb * 16 + c];
+        gr[nb] = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           g1[nb][i] = acch[nb][i] * d[i];
           gr[nb] += wdv[i] * g1[nb][i];
-          vwd[i] += g1[nb][i] * r2v[nb];
+          vwd[i] += g1[nb][i] * r2v;
         }
         // Gh has a row for every edge slot of the last tile (rows past E are never read)
-        *reinterpret_cast<bf16x4*>(Gh + (base + nb * 16 + c) * H + 16 * w + 4 * g) = pack4(g1[nb]);
+        *reinterpret_cast<bf16x4*>(Gh + (int64_t)(base + nb * 16 + c) * H + 16 * w + 4 * g) = pack4(g1[nb]);
       }
-      const bf16x8 ga1N = edge_major(g1[0], g1[1], I);
-      // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e]
+      // dW_hl rows of this wave: sum_e m1[h][e] g_a2[o][e].  The wave's own m1 rows are read
+      // before its S1 of the next tile overwrites them below (each wave reads and writes only its
+      // own rows of s_m1 in this interval; all reads of other rows ended with S2)
 #pragma unroll
-      for (int cb = 0; cb < NO; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, cb, l));
+      for (int eh = 0; eh < 2; ++eh) {
+        const bf16x8 m1N = chain_edge_major<NB, true>(s_m1, w, c, g, eh);
+#pragma unroll
+        for (int cb = 0; cb < NO; ++cb) mma(acc_whl[cb], m1N, chain_edge_major<NB, true>(s_ga2, cb, c, g, eh));
+      }
       // dW_e rows of this wave: sum_e g_a1[h][e] e[e][slot] (the r^2 column is accumulated above)
+      if constexpr (NU > 0) {
+        const bf16x8 I = ident_chunk(c, g);
 #pragma unroll
-      for (int ub = 0; ub < NU; ++ub) {
-        if (16 * ub >= FE) continue;   // column block past the edge features
-        mma(acc_wu[ub], ga1N, get_ut(s_u[par], 16 * ub + c, g));   // slots past F_E read zero rows
+        for (int eh = 0; eh < 2; ++eh) {
+          const bf16x8 ga1N = edge_major(g1[2 * eh], g1[2 * eh + 1], I);
+#pragma unroll
+          for (int ub = 0; ub < NU; ++ub) {
+            if (16 * ub >= FE) continue;   // column block past the edge features
+            mma(acc_wu[ub], ga1N, lds_cols<PU>(s_ub[par], ub, eh, c, g));   // slots past F_E: not stored
+          }
+        }
       }
     }
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       gr[nb] += shfl_xor(gr[nb], 16);
       gr[nb] += shfl_xor(gr[nb], 32);
       if (g == 0) s_gr[w][nb * 16 + c] = gr[nb];
     }
-    if constexpr (NU == 0) stage1(t + G, sl1, par ^ 1, s1n);
-    // the ring slot of t + 2
-    store_idx(sl2, t + 2 * G < a.ntiles ? t + 2 * G : t);
-    s1[0] = s1n[0];
-    s1[1] = s1n[1];
+    // ---- S1 of the next tile (past the last tile: of a stand-in tile, never read), ring slot of t + 2
+    stage1(par ^ 1, s1);
+    store_idx(sl2, t2);
+    // the next tile's message-gradient rows, waited for here (a tile after their load) and not at
+    // the top of the next tile
+    if (GM_AHEAD) asm volatile("" ::"v"(gmr_next[0]), "v"(gmr_next[1]), "v"(gmr_next[2]), "v"(gmr_next[3]));
     __syncthreads();
     // ---- S6: dL/ddelta = phi gx + 2 g_r delta (component 3 of the record: 0) --
-    if (w < 2) {   // Gx, like Gh, has a row for every edge slot of the last tile
+    if (w < 4) {   // Gx, like Gh, has a row for every edge slot of the last tile
       float grt = 0.f, pht = 0.f;
 #pragma unroll
       for (int ww = 0; ww < W; ++ww) {
-        grt += s_gr[ww][xe];
-        pht += s_phi[ww][xe];
+        grt += s_gr[ww][l];
+        pht += s_phi[ww][l];
       }
-      a.Gx[(base + xe) * 4 + xc] = xc < 3 ? pht * xgrd + 2.0f * grt * xdel : 0.f;
+      a.Gx[(int64_t)(base + l) * 4 + w] = w < 3 ? pht * xgrd + 2.0f * grt * xdel : 0.f;
     }
     asm volatile("" ::"v"(xdel), "v"(xgrd));   // complete in every wave
     // s_phi and s_gr are next written after the next tile's S2 barrier, which
-    // waves 0 and 1 reach after these reads: no closing barrier.
+    // waves 0..3 reach after these reads: no closing barrier.
   }
 
   // ---- this block's weight-gradient partial ---------------------------------
@@ -1517,7 +1544,8 @@ bool coop_supported(const LayerShape& s) {
 }
 
 int coop_bwd_blocks(const LayerShape& s) {
-  return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(s.E, TE), 256));
+  const int64_t tile = (s.eq && s.H == 128) ? 2 * TE : TE;   // coop_bwd_eq_kernel: 64-edge tiles
+  return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(s.E, tile), 256));
 }
 
 int64_t coop_dw_len(const LayerShape& s) {

@@ -22,12 +22,21 @@ __device__ __forceinline__ f32x4 unpack4(const bf16x4& v) {
 }
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
-// chain buffer: chunk (kc, nb) = 64 lanes x 8 bf16; 16-row block blk fills half (blk & 1) of chunk blk >> 1
+// chain buffer over NB 16-edge blocks: chunk (kc, nb) = 64 lanes x 8 bf16 at index kc NB + nb;
+// 16-row block blk fills half (blk & 1) of chunk blk >> 1.  With SW the 16-byte lane slot s of a
+// chunk is stored at s ^ 4 ((s >> 4) & 3) (within its aligned group of 16 slots): the 8-byte
+// transposing reads of chain_edge_major (lanes of g = 0, 1 read slots 16 q + 4 g + b, q = c & 3,
+// b = c >> 2) then fall on 16 different slots mod 16, two lanes each, instead of 8 slots, four
+// lanes each; the lane-order reads and writes keep their bank spread.
+template <bool SW>
+__device__ __forceinline__ int chain_slot(int s) { return SW ? s ^ (((s >> 4) & 3) << 2) : s; }
+template <int NB = 2, bool SW = false>
 __device__ __forceinline__ void put_chain(bf16* buf, int blk, int nb, int l, const f32x4& v) {
-  *reinterpret_cast<bf16x4*>(buf + (((blk >> 1) * 2 + nb) * 64 + l) * 8 + 4 * (blk & 1)) = pack4(v);
+  *reinterpret_cast<bf16x4*>(buf + (((blk >> 1) * NB + nb) * 64 + chain_slot<SW>(l)) * 8 + 4 * (blk & 1)) = pack4(v);
 }
+template <int NB = 2, bool SW = false>
 __device__ __forceinline__ bf16x8 get_chain(const bf16* buf, int kc, int nb, int l) {
-  return *reinterpret_cast<const bf16x8*>(buf + ((kc * 2 + nb) * 64 + l) * 8);
+  return *reinterpret_cast<const bf16x8*>(buf + ((kc * NB + nb) * 64 + chain_slot<SW>(l)) * 8);
 }
 // edge-major buffer: feature block blk, lane (c = feature, g) holds 8 edges in kappa_chain order
 __device__ __forceinline__ void put_norm(bf16* buf, int blk, int l, const bf16x8& v) {
@@ -58,16 +67,18 @@ __device__ __forceinline__ bf16x8 edge_major(const f32x4& nb0, const f32x4& nb1,
   return pack_chunk<bf16>(transpose_block(nb0, I), transpose_block(nb1, I));
 }
 // The same chunk for 16-row block blk read back from a chain buffer that holds it
-// (put_chain of both edge blocks), by two transposing reads.  Feature
-// 16 (blk & 1) + 4q + i of group blk >> 1 and edge e sit at lane slot 16q + (e & 15)
-// of chunk (blk >> 1, e >> 4), element 4 (blk & 1) + i.  Within a 16-lane group,
+// (put_chain of the edge blocks 2 eh, 2 eh + 1: edges 32 eh .. 32 eh + 31), by two transposing
+// reads.  Feature 16 (blk & 1) + 4q + i of group blk >> 1 and edge e sit at lane slot
+// 16q + (e & 15) of chunk (blk >> 1, e >> 4), element 4 (blk & 1) + i.  Within a 16-lane group,
 // lane j addresses edge kb + j/4, features 4 (j % 4) .. + 3, and lane c receives
 // feature c of edges kb .. kb + 3: kb = 4g gives elements 0..3, kb = 16 + 4g 4..7.
-__device__ __forceinline__ bf16x8 chain_edge_major(const bf16* buf, int blk, int c, int g) {
-  const bf16* base = buf + (blk >> 1) * 2 * 64 * 8 + 16 * (c & 3) * 8 + 4 * (blk & 1);
+template <int NB = 2, bool SW = false>
+__device__ __forceinline__ bf16x8 chain_edge_major(const bf16* buf, int blk, int c, int g, int eh = 0) {
+  const bf16* base = buf + ((blk >> 1) * NB + 2 * eh) * 64 * 8 + 4 * (blk & 1);
   const int e0 = 4 * g + (c >> 2);         // edges of the first read: 0..15, block 0
-  const bf16* p0 = base + e0 * 8;
-  const bf16* p1 = base + (64 + e0) * 8;   // edge 16 + e0: chunk of edge block 1, lane slot 16q + e0
+  const int sl = chain_slot<SW>(16 * (c & 3) + e0);
+  const bf16* p0 = base + sl * 8;
+  const bf16* p1 = base + (64 + sl) * 8;   // edge 16 + e0: chunk of edge block 1, lane slot 16q + e0
   const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p0);
   const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p1);
   return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
