@@ -104,6 +104,10 @@ def kernel_work(cls, path, N, E, F, H, O, M, FE, g, s):
     count every gathered row once per edge: P_i, Q_j (H each), col and row id (8), edge id and
     features, the geometry record; scratch stores (Gh, Gx, factors) included; node outputs once."""
     eb = 8 + (4 + FE * s if FE else 0) + 24 * g
+    # the cooperative MPNN backward (H = 128) sums dL/dpre1 over each row itself: dP rows and, for the
+    # rows split over tiles, fp32 carries (about two per 32-edge tile) out; the node reduction then
+    # reads Gh once, by source
+    dst = path == "coop" and g == 0 and H == 128
     if cls == "fwd_edge":
         flops = 2 * ((g + FE) * H + H * O + g * O * M)
         return flops * E, E * (2 * H * s + eb) + N * (O * s + 12 * g)
@@ -117,8 +121,12 @@ def kernel_work(cls, path, N, E, F, H, O, M, FE, g, s):
         else:         # one wave per tile: factors m1, m, g_q, p, g_a2 and r^2 stored for the split-K products
             flops = 2 * (g + FE) * H + 4 * H * O + 4 * g * O * M
             per_edge += (H + O + 2 * g * M + O) * s + 4 * g
+        if dst:
+            return flops * E, E * (per_edge + H / 4) + N * H * s
         return flops * E, E * per_edge
     if cls == "node_reduce":
+        if dst:
+            return 0, E * (H * s + 4) + N * (H * s + 8)
         return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
     if cls == "node_gemm":
         return 2 * N * F * 2 * H, N * (F + 2 * H) * s
@@ -368,8 +376,10 @@ def probe_identity(a, k=5):
     replaced by identity (EGNN_FLAG_PROBE_IDENTITY, an instrument), one layer forward + backward per
     step, on the full power-law graph.  Bytes per kernel, every gathered row counted once per edge:
       forward:      E (8 + 2 H s + F_E s) + N O s      (indices, P_i and Q_j, edge features; row sums out)
-      backward:     E (8 + O s + H s)                 (indices, the row's message gradient; dL/dpre1 out)
-      node reduce:  E (2 H s + 4) + N (8 + 2 H s)     (dL/dpre1 by row and by source, CSC ids; dP | dQ out)"""
+      backward:     E (8 + O s + H s + H / 4) + N H s (indices, the row's message gradient; dL/dpre1 out,
+                                                    its row sums: dP rows, fp32 carries of the split rows)
+      node reduce:  E (H s + 4) + N (8 + H s)         (dL/dpre1 by source, CSC ids; dQ out)
+      fix-ups:      E H / 4 each                      (the carries of the split rows, forward and backward)"""
     import torch
     from pymolecular_amd import _capi, fused, graphs
     g = graphs.make_workload(k)
@@ -392,15 +402,16 @@ def probe_identity(a, k=5):
     for _ in range(a.warmup):
         step()
     torch.cuda.synchronize()
-    _capi.profile_enable(True, [_capi.K_FWD_EDGE, _capi.K_BWD_EDGE, _capi.K_NODE_REDUCE])
+    _capi.profile_enable(True, [_capi.K_FWD_EDGE, _capi.K_FWD_FIXUP, _capi.K_BWD_EDGE, _capi.K_NODE_REDUCE])
     for _ in range(a.steps):
         step()
     torch.cuda.synchronize()
     prof = _capi.profile_read()
     _capi.profile_enable(False)
     model = {"fwd_edge": E * (8 + 2 * H * s + FE * s) + N * H * s,
-             "bwd_edge": E * (8 + H * s + H * s),
-             "node_reduce": E * (2 * H * s + 4) + N * (8 + 2 * H * s)}
+             "fwd_fixup": E * H / 4,
+             "bwd_edge": E * (8 + H * s + H * s + H / 4) + N * H * s,
+             "node_reduce": E * (H * s + 4) + N * (8 + H * s)}
     out = {}
     tot_b = tot_t = 0.0
     for cls, nbytes in model.items():

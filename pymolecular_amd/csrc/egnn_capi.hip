@@ -257,11 +257,20 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   const bool coop = coop_supported(s);
   a.dwpart = w.dwpart; a.LW = w.LW;
   a.geo = w.geo;
+  a.dP = w.dPQ; a.sdp = 2 * s.H; a.carry = w.carry;
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   if (coop || wide_supported(s)) {
     ProfScope ps(EGNN_K_BWD_EDGE, st);
     const int r = coop ? launch_coop_bwd(s, a, w.nblk, st) : launch_wide_bwd(s, a, wide_bwd_blocks(s), st);
     if ((rc = hip_status(r)) != EGNN_OK) return rc;
+  }
+  if (coop_dst_sums(s)) {   // destination sums of the rows split over tiles (and zero for empty rows)
+    FwdArgs f{};
+    f.N = s.N; f.E = s.E;
+    f.rowptr = rowptr; f.carry = w.carry; f.fix_rows = v.fix_rows; f.n_fix = v.n_fix;
+    f.out_msg = w.dPQ; f.smsg = 2 * s.H;
+    ProfScope ps(EGNN_K_FWD_FIXUP, st);
+    if ((rc = hip_status(launch_fwd(s, f, 1, st))) != EGNN_OK) return rc;
   }
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums

@@ -1248,7 +1248,17 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A fragments of W_hl^T (S2)
   __shared__ __attribute__((aligned(16))) bf16 s_u[2][NUS * TE];   // edge features, slot-major (put_ut)
   __shared__ __attribute__((aligned(16))) float s_b2[O];
-  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1];
+  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1], s_ex[3][2];
+  // destination sums, by tile parity: g_a1 edge-major (written in S5, summed in the next tile), the
+  // B operands S[edge][rank] of the two rank blocks, the target of each rank (a row >= 0, carry
+  // slot 0 / 1 as -1 / -2, none -3) and the rank count; the row and span of each rank and the 0/1
+  // patterns of the segment matrix are the table wave's scratch
+  __shared__ __attribute__((aligned(16))) bf16 s_g1N[2 * CH];
+  __shared__ __attribute__((aligned(16))) bf16 s_segB[2][2][64 * 8];
+  __shared__ int s_tgt[2][TE], s_nrk[2];
+  __shared__ int s_rowof[TE], s_rspan[TE];
+  __shared__ uint2 s_lut[16];
+  seg_lut_init(s_lut, threadIdx.x);
   bf16* const s_ga2 = s_act;
   bf16* const s_ga2N = s_act + CH;
 
@@ -1282,11 +1292,13 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
 #pragma unroll
   for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
 
-  // ring loads (every wave issues and waits for them; the loader wave stores the slot)
+  // ring loads (every wave issues and waits for them; the loader wave stores the slot): lanes
+  // 0..31 the tile's edges, lanes 32 and 33 the edges just before and after it (their rows)
   const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
   int ld_ri, ld_rj, ld_eid = 0;
   auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
-    const uint32_t e0 = (uint32_t)(tt * TE) + (l & 31);
+    const uint32_t eb = (uint32_t)(tt * TE);
+    const uint32_t e0 = l < TE ? eb + l : (l == TE ? eb - 1u : eb + TE);   // eb - 1 at eb = 0: clamped
     const uint32_t e = e0 < (uint32_t)E ? e0 : (uint32_t)E - 1;
     ld_ri = a.erow[e];
     ld_rj = a.col[e];
@@ -1299,7 +1311,45 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       s_ri[slot][l] = clampi(ld_ri, N);
       s_rj[slot][l] = clampi(ld_rj, N);
       if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, (int)E) : (e < (int)E ? e : (int)E - 1);
+    } else if (w == LDW && l < TE + 2) {
+      s_ex[slot][l - TE] = clampi(ld_ri, N);
     }
+  };
+  // ---- destination sums of tile tt (parity p), by the waves of half 0, row block rb: per-rank
+  // sums D = g_a1 S against the tile's 0/1 segment matrix; a rank that is a whole row is stored to
+  // dP, the partial first / last ranks to the tile's carry slots 0 / 1 (summed in tile order by
+  // the fix-up)
+  auto dst_sums = [&](int64_t tt, int p) {
+    const int nrk = __builtin_amdgcn_readfirstlane(s_nrk[p]);
+    const bf16x8 A = get_norm(s_g1N + p * CH, rb, l);
+    auto block = [&](int q) {
+      f32x4 D = zero4();
+      mma(D, A, get_norm(s_segB[p][q], 0, l));
+      const int tg = s_tgt[p][16 * q + c];
+      if (tg >= 0)
+        *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * rb + 4 * g) = pack4(D);
+      else if (tg > -3)
+        *reinterpret_cast<f32x4*>(a.carry + ((int64_t)tt * 2 - 1 - tg) * O + 16 * rb + 4 * g) = D;
+    };
+    block(0);
+    if (nrk > 16) block(1);
+  };
+  // rank tables of tile tt from ring slot sl into parity p (one wave): the segment-matrix operands
+  // and the targets of its ranks
+  auto rank_tables = [&](int64_t tt, int sl, int p) {
+    const TileRanks rk = tile_ranks(s_ri[sl], s_ex[sl], tt * TE, E, l);
+    tile_rank_tables(s_ri[sl], rk, l, s_rowof, s_rspan);
+    // the lanes read what other lanes of this wave wrote: LDS accesses of one wave complete in
+    // order, so only the compiler must keep the order (no memory wait, which would also wait for
+    // the next tile's gathers)
+    asm volatile("" ::: "memory");
+    for (int q = 0; q < (rk.nrank > 16 ? 2 : 1); ++q) {
+      const int r = 16 * q + c;
+      const bool has = r < rk.nrank;
+      put_norm(s_segB[p][q], 0, l, seg_chunk_span(has ? s_rspan[r] : 0, g, s_lut));
+      if (g == 0) s_tgt[p][r] = !has ? -3 : rank_whole(rk, r) ? s_rowof[r] : (r == 0 ? -1 : -2);
+    }
+    if (l == 0) s_nrk[p] = rk.nrank;
   };
   // the gathers of S1 from a ring slot: the wave's P_i, Q_j and (F_E > 0) edge-feature chunk
   bf16x8 pq;
@@ -1359,7 +1409,8 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
   __syncthreads();   // m1 of the first tile
 
   int par = 0, sl0 = 0;
-  for (int64_t t = blockIdx.x; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
+  int64_t t = blockIdx.x;
+  for (; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
     const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
     const int64_t base = t * TE;
     const bool valid = (int)base + hf * 16 + c < (int)E;
@@ -1371,8 +1422,11 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
     load_idx(t2);
     if constexpr (ID) {
+      if (hf == 0 && t != (int64_t)blockIdx.x) dst_sums(t - G, par ^ 1);
       const f32x4 gm = valid ? unpack4(gmr) : zero4();
       *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(gm);
+      *reinterpret_cast<bf16x4*>(s_g1N + par * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(gm, I));
+      if (w == 8) rank_tables(t, sl0, par);
       store_idx(sl2, t2);
       __syncthreads();
       continue;
@@ -1402,6 +1456,10 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       put_chain(s_ga2, rb, hf, l, ga);
       *reinterpret_cast<bf16x4*>(s_ga2N + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(ga, I));
     }
+    // the destination sums of the previous tile (half 0) and the rank tables of this one (a wave of
+    // half 1)
+    if (hf == 0 && t != (int64_t)blockIdx.x) dst_sums(t - G, par ^ 1);
+    if (w == 8) rank_tables(t, sl0, par);
     __syncthreads();
 
     // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1) ------------------------------------------
@@ -1416,13 +1474,16 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
       for (int i = 0; i < 4; ++i) g1[i] = acch[i] * d[i];
       // Gh has a row for every edge slot of the last tile (rows past E are never read)
       *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(g1);
+      // g_a1 edge-major (zero on the edges past E) for the destination sums in the next tile
+      const f32x4 g1T = transpose_block(g1, I);
+      *reinterpret_cast<bf16x4*>(s_g1N + par * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(g1T);
       // dW_hl rows rb, columns of half hf: sum_e m1[h][e] g_a2[o][e]
       const bf16x8 m1N = get_norm(s_act + (4 + par) * CH, rb, l);
 #pragma unroll
       for (int cb = 0; cb < 4; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, 4 * hf + cb, l));
       // dW_e rows rb: sum over this half's edges of g_a1[h][e] e[e][slot] (the other half's slots are zero)
       if constexpr (NU > 0) {
-        const bf16x8 ga1N = half_edge_chunk(transpose_block(g1, I), hf);
+        const bf16x8 ga1N = half_edge_chunk(g1T, hf);
 #pragma unroll
         for (int ub = 0; ub < NU; ++ub) {
           if (16 * ub >= FE) continue;   // column block past the edge features
@@ -1438,6 +1499,9 @@ __global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
     asm volatile("" ::"v"(gmr_next));
     __syncthreads();
   }
+
+  // the destination sums of the block's last tile (parity par ^ 1)
+  if (hf == 0 && (int64_t)blockIdx.x < a.ntiles) dst_sums(t - G, par ^ 1);
 
   // ---- this block's weight-gradient partial ---------------------------------
   // db2 is first summed over the wave's 16 edge lanes; half 1 then leaves its
@@ -1542,6 +1606,8 @@ bool coop_supported(const LayerShape& s) {
   return s.bf16 && dims && s.FE + (s.eq ? 2 : 0) <= 32 && s.N * 4 * (int64_t)s.H < (int64_t(1) << 32) &&
          s.E + kTileEdges < (int64_t(1) << 31);
 }
+
+bool coop_dst_sums(const LayerShape& s) { return coop_supported(s) && !s.eq && s.H == 128; }
 
 int coop_bwd_blocks(const LayerShape& s) {
   const int64_t tile = (s.eq && s.H == 128) ? 2 * TE : TE;   // coop_bwd_eq_kernel: 64-edge tiles

@@ -86,6 +86,7 @@ struct BwdWs {
   int nblk;
   int64_t LW;
   float* geo;      // cooperative EGNN kernel: [E][8] per-edge record
+  float* carry;    // cooperative MPNN kernel: [ntiles][2][O] partial destination sums (BwdArgs::carry)
   // one-wave-per-tile kernel: the factors hold chunkE edges; per-chunk sums of the factor products
   int64_t chunkE;
   int nchunk;
@@ -195,6 +196,10 @@ struct BwdArgs {
   int64_t fbase;   // first edge of the factor rows Dm1 ... Dp (they hold one chunk; Gh, Gx, R2 hold all edges)
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
+  // cooperative MPNN kernel: destination sums of dL/dpre1, the rows whole in a 32-edge tile
+  // stored to dP (row stride sdp), the partial first / last rows of tile t to carry[t][2][O]
+  void* dP; int64_t sdp;
+  float* carry;
   const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype;
   const void* w1m; // (O x H) and (M x O) with lin
   int lin;         // weights in torch.nn.Linear (out, in) layout
@@ -204,6 +209,10 @@ int launch_bwd(const LayerShape& s, const BwdArgs& a, hipStream_t st);
 // Workgroup-cooperative fused kernels (bf16, H = 128 or H = 64 / O = M = 32, NUC = 1).
 bool coop_supported(const LayerShape& s);
 int coop_bwd_blocks(const LayerShape& s);
+// The cooperative MPNN backward (H = O = 128) sums dL/dpre1 over each row's edges itself
+// (BwdArgs::dP, carry; the split rows are completed by the forward's carry fix-up), and the node
+// reduction then sums the source side only.
+bool coop_dst_sums(const LayerShape& s);
 int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);

@@ -124,6 +124,7 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Gx = (float*)take(Er * 4 * sizeof(float));
   w->R2 = (coop || wide) ? nullptr : (float*)take(E * sizeof(float));
   w->geo = ((coop || wide_supported(s)) && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
+  w->carry = coop_dst_sums(s) ? (float*)take((size_t)cdiv(E1, kTileEdges) * 2 * s.O * sizeof(float)) : nullptr;
   // per-block partials of the cooperative kernels' weight gradients / the wide kernel's dw2_mov | dw_d
   w->nblk = coop ? coop_bwd_blocks(s) : (wide && s.eq) ? wide_bwd_blocks(s) : 0;
   w->LW = coop ? coop_dw_len(s) : (wide && s.eq) ? (int64_t)s.M + s.H : 0;
@@ -1276,7 +1277,7 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ csc_eid, T* __restrict__ dPQ,
                                                           float* __restrict__ gcoord, int64_t sgc,
                                                           const float* __restrict__ gres, int64_t sgr, int64_t N,
-                                                          int eq) {
+                                                          int eq, int dst) {
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
   constexpr int EPW = 64 / LPE;                // edges per wave-wide load
@@ -1313,9 +1314,11 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
 #pragma unroll
     for (int u = 0; u < VPL; ++u) ap[u] = aq[u] = 0.f;
     float ax = 0.f;
-    // destination sums: the row's edges are contiguous
-    const int rs = rowptr[n], re = rowptr[n + 1];
-    gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+    // destination sums (unless the edge kernel made them): the row's edges are contiguous
+    if (dst) {
+      const int rs = rowptr[n], re = rowptr[n + 1];
+      gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+    }
     // source sums: the edges listed for n by the stable CSC, edge ids 64 at a time, one per lane
     const int cs = csc_ptr[n], ce = csc_ptr[n + 1];
     for (int k0 = cs; k0 < ce; k0 += 64) {
@@ -1340,10 +1343,10 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
         bf16x8 vp, vq;
 #pragma unroll
         for (int u = 0; u < VPL; ++u) { vp[u] = (bf16)ap[u]; vq[u] = (bf16)aq[u]; }
-        *reinterpret_cast<bf16x8*>(out) = vp;
+        if (dst) *reinterpret_cast<bf16x8*>(out) = vp;
         *reinterpret_cast<bf16x8*>(out + H) = vq;
       } else {
-        *reinterpret_cast<f32x4*>(out) = f32x4{ap[0], ap[1], ap[2], ap[3]};
+        if (dst) *reinterpret_cast<f32x4*>(out) = f32x4{ap[0], ap[1], ap[2], ap[3]};
         *reinterpret_cast<f32x4*>(out + H) = f32x4{aq[0], aq[1], aq[2], aq[3]};
       }
     }
@@ -1355,7 +1358,8 @@ int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, con
                        const float* gres, int64_t sgr, hipStream_t st) {
   int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
   int eq = s.eq ? 1 : 0;
-#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq)
+  int dst = coop_dst_sums(s) ? 0 : 1;   // the cooperative MPNN kernel stores the destination sums
+#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, dst)
   if (s.bf16) {
     if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
   } else {
