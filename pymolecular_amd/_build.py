@@ -34,6 +34,13 @@ FLAGS = [
 ]
 
 
+# per-file flags: the edge-parallel MPNN backward keeps its MFMA accumulators in VGPRs (the VALU reads
+# every product's result; the AGPR form would copy each one back)
+FILE_FLAGS = {
+    "egnn_mpnn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def source_files() -> list:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [HEADER]
 
@@ -42,6 +49,8 @@ def source_hash() -> str:
     """SHA-256 over the flags and the (relative name, content) of every source file."""
     h = hashlib.sha256()
     h.update("\0".join(FLAGS).encode())
+    for name in sorted(FILE_FLAGS):
+        h.update(("\0" + name + "\0" + "\0".join(FILE_FLAGS[name])).encode())
     for p in source_files():
         h.update(b"\0" + p.name.encode() + b"\0")
         h.update(p.read_bytes())
@@ -50,7 +59,7 @@ def source_hash() -> str:
 
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         msg = "\n".join(l for l in r.stderr.splitlines() if "not a recognized feature" not in l)

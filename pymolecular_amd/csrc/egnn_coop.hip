@@ -1220,7 +1220,8 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // backward of the non-equivariant layer (MPNN), H = O = 128, 16 waves per tile
 // ---------------------------------------------------------------------------
-// Wave w owns feature rows [16 rb, 16 rb + 16), rb = w & 7, of every stage for
+// Launched only as the identity-MLP instrument (ID); the layer's backward is the
+// edge-parallel kernel of egnn_mpnn.hip.  Wave w owns feature rows [16 rb, 16 rb + 16), rb = w & 7, of every stage for
 // the 16 edges of half hf = w >> 3 of the tile.  Compared with one wave per row
 // block over both halves, each wave holds half the per-edge state, so 16 waves
 // (4 per SIMD) fit one CU and hide each other's latencies.  The edge-major
@@ -1571,17 +1572,8 @@ int launch_bwd_eq(const BwdArgs& a, int nblk, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
-int launch_mpnn_bwd16(const BwdArgs& a, int nblk, bool probe, hipStream_t st) {
-  if (a.ntiles > 0) {
-    if (probe)
-      hipLaunchKernelGGL((mpnn_bwd16_kernel<0, true>), dim3(nblk), dim3(1024), 0, st, a);
-    else if (a.FE == 0)
-      hipLaunchKernelGGL((mpnn_bwd16_kernel<0>), dim3(nblk), dim3(1024), 0, st, a);
-    else if (a.FE <= 16)
-      hipLaunchKernelGGL((mpnn_bwd16_kernel<1>), dim3(nblk), dim3(1024), 0, st, a);
-    else
-      hipLaunchKernelGGL((mpnn_bwd16_kernel<2>), dim3(nblk), dim3(1024), 0, st, a);
-  }
+int launch_mpnn_bwd16_probe(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.ntiles > 0) hipLaunchKernelGGL((mpnn_bwd16_kernel<0, true>), dim3(nblk), dim3(1024), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -1607,10 +1599,15 @@ bool coop_supported(const LayerShape& s) {
          s.E + kTileEdges < (int64_t(1) << 31);
 }
 
+// The MPNN H = 128 backward runs the edge-parallel kernel (egnn_mpnn.hip); the 16-wave kernel
+// remains as the identity-MLP instrument (EGNN_FLAG_PROBE_IDENTITY).
+static bool mpnn_ep(const LayerShape& s) { return !s.eq && s.H == 128 && !s.probe; }
+
 bool coop_dst_sums(const LayerShape& s) { return coop_supported(s) && !s.eq && s.H == 128; }
 
 int coop_bwd_blocks(const LayerShape& s) {
-  const int64_t tile = (s.eq && s.H == 128) ? 2 * TE : TE;   // coop_bwd_eq_kernel: 64-edge tiles
+  // coop_bwd_eq_kernel: 64-edge tiles, the edge-parallel MPNN kernel: 128-edge tiles
+  const int64_t tile = (s.H == 128 && mpnn_ep(s)) ? 4 * TE : (s.H == 128 && s.eq) ? 2 * TE : TE;
   return (int)std::max<int64_t>(1, std::min<int64_t>(cdiv(s.E, tile), 256));
 }
 
@@ -1626,7 +1623,8 @@ int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
 }
 
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
-  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16(a, nblk, s.probe, st);
+  if (s.H == 128 && mpnn_ep(s)) return launch_mpnn_bwd_ep(a, nblk, st);
+  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16_probe(a, nblk, st);
   return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
 }
 

@@ -216,6 +216,10 @@ bool coop_dst_sums(const LayerShape& s);
 int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
+// Edge-parallel MPNN backward (bf16, H = O = 128): 128-edge block tiles, per-block partials of
+// [dW_hl ; db2 | dW_e] (coop_dw_len), Gh per edge, the destination sums of Gh (dP, carries) as the
+// 16-wave kernel makes them.
+int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st);
 // Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
 // from L2, backward writes the per-edge weight-gradient factors Dm1, Dm, Dgq, Dga2.
 bool wide_supported(const LayerShape& s);

@@ -1,0 +1,435 @@
+// Edge-parallel backward of the non-equivariant layer (MPNN), bf16, H = O = 128 (gfx950).
+//
+// One block of eight waves per CU, two waves per SIMD (a single wave per SIMD
+// issues vector-ALU instructions at about half the rate).  Each wave runs the
+// message chain of its own 16-edge sub-tile from end to end in registers:
+//   S1  pre1 = W_u e + P_i + Q_j            (the P_i + Q_j sum is an MFMA against a 0/1 operand)
+//       m1 = SiLU(pre1), s1 = SiLU'(pre1)
+//   S2  pre2 = W_hl^T m1 + b2, s2 = SiLU'(pre2)
+//   S4  g_a2 = g_m,i * s2                   (g_m,i: the incoming message gradient of row i)
+//   S5  g_a1 = (W_hl g_a2) * s1             stored per edge as Gh (dL/dpre1)
+// with every stage's two 16-row C-blocks forming the next stage's B operand
+// (kappa_chain order), so no activation leaves the wave.  The weights are A
+// operands read from one row-major copy of W_hl in LDS (transposing reads for
+// W_hl^T).
+//
+// The weight gradients contract over edges, which needs edge-major operands.
+// After its chain each wave writes its m1, g_a2 and g_a1 (and the edge
+// features) into chain-ordered LDS buffers of the 128-edge block tile; after a
+// barrier wave w reads them back edge-major with transposing LDS reads and
+// accumulates, over all 128 edges, the rows [16 w, 16 w + 16) of dW_hl and dW_e
+// and the columns [16 w, 16 w + 16) of db2 in its registers.  Each block writes
+// one partial of [dW_hl ; db2 | dW_e] that a fixed-order sum reduces.  The same
+// edge-major g_a1 gives the destination sums of Gh (dP) per 32-edge tile, by an
+// MFMA against the tile's 0/1 segment matrix: rows whole in the tile are stored,
+// the partial first and last rows go to carry slots that the fix-up sums in tile
+// order.  The source sums (dQ) are made by the node reduction.
+// Reference: backward_kernel.py:143-257 computes the same quantities one
+// program per CSR row.
+#include "egnn_device.h"
+#include "egnn_internal.h"
+#include "egnn_tile.h"
+
+namespace egnn {
+namespace {
+
+using namespace tile;
+
+// W_hl[h][o] in LDS as rows of 144 bf16 (288 bytes), the 8-byte unit u of row R stored at unit
+// u ^ ((R >> 2) & 3).  Both operand reads then hit 16 different 8-byte bank groups per 16 lanes: the
+// W_hl rows of S5 (lanes c read rows 16 blk + c at one unit) and the transposing W_hl^T reads of S2
+// (lanes read rows kb + c / 4 at units 4 blk + c % 4).  The swizzle changes only the two low bits
+// of a unit, so every fragment's address is a per-lane base plus a constant.
+constexpr int kWP = 144;
+__device__ __forceinline__ const bf16* wunit(const bf16* W, int R, int u) { return W + R * kWP + 4 * (u ^ ((R >> 2) & 3)); }
+// A[r][k] = W[16 blk + r][32 kc + kappa_chain(g, s)]  (S5: A = W_hl); Wr = the lane's base, wrow_base
+__device__ __forceinline__ const bf16* wrow_base(const bf16* W, int c, int g) { return W + c * kWP + 4 * (g ^ ((c >> 2) & 3)); }
+__device__ __forceinline__ bf16x8 w_rows(const bf16* Wr, int blk, int kc) {
+  const bf16* p = Wr + 16 * blk * kWP + 32 * kc;
+  return __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16),
+                                 0, 1, 2, 3, 4, 5, 6, 7);
+}
+// A[r][k] = W[32 kc + kappa_chain(g, s)][16 blk + r]  (S2: A = W_hl^T), two transposing reads: lane c
+// addresses row kb + c / 4, columns 16 blk + 4 (c % 4) .. + 3, and receives column 16 blk + c of rows
+// kb .. kb + 3; Wc = the lane's base, wcol_base
+__device__ __forceinline__ const bf16* wcol_base(const bf16* W, int c, int g) {
+  return W + (4 * g + (c >> 2)) * kWP + 4 * ((c & 3) ^ (g & 3));
+}
+__device__ __forceinline__ bf16x8 w_cols(const bf16* Wc, int blk, int kc) {
+  const bf16* p = Wc + 32 * kc * kWP + 16 * blk;
+  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p);
+  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p + 16 * kWP));
+  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+constexpr int kEpWaves = 8;                   // waves per block, two per SIMD
+constexpr int kEpSub = 16;                    // edges per wave sub-tile
+constexpr int kEpTile = kEpWaves * kEpSub;    // edges per block tile
+
+// Indices of the lane's edge (column c of the wave's sub-tile); values clamped when used.
+struct EpIdx { int ri, rj, eid; };
+// The gathers of one sub-tile: P_i | Q_j chunks of the eight 16-feature blocks (pq_gather), the
+// incoming message gradient of row i for the lane's four features of each block, the edge features.
+struct EpGat { bf16x8 pq[8]; bf16x4 gm[8]; bf16x8 u; };
+
+template <int NU>
+__global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
+  constexpr int H = 128, O = 128, NRB = 8, KH = H / 32, KO = O / 32;
+  constexpr int NB = kEpWaves;                  // 16-edge blocks of a block tile
+  constexpr int NK = kEpTile / 32;              // 32-edge K chunks of a block tile
+  constexpr int CHB = KH * NB * 64 * 8;         // one chain buffer: 4 chunks x 8 edge blocks (32 KB)
+  constexpr int NUS = NU > 0 ? 16 * NU : 1;     // slot rows of the edge-feature buffer
+  constexpr bool SW = true;                     // swizzled lane slots (2-way transposing reads)
+  __shared__ __attribute__((aligned(16))) bf16 s_whl[H * kWP];                    // W_hl[h][o], swizzled units
+  __shared__ __attribute__((aligned(16))) bf16 s_wu[NU > 0 ? NRB * kFragElems : 8];   // A = W_u, S1
+  __shared__ __attribute__((aligned(16))) float s_b2[O];
+  __shared__ __attribute__((aligned(16))) bf16 s_m1[CHB];
+  __shared__ __attribute__((aligned(16))) bf16 s_ga2[CHB];
+  __shared__ __attribute__((aligned(16))) bf16 s_g1[CHB];
+  // destination sums: the 32-edge tiles of the block tile, built by waves 0..3 (one each): the rows of
+  // edges base - 1 .. base + 32, the row and span of each rank, the target of each rank (a row >= 0,
+  // carry slot 0 / 1 as -1 / -2, none -3) and the rank count
+  __shared__ int s_rows[kEpTile / 32][34], s_rowof[kEpTile / 32][32], s_rspan[kEpTile / 32][32];
+  __shared__ int s_tgt[kEpTile / 32][32], s_nrk[kEpTile / 32];
+  __shared__ uint2 s_lut[16];
+  __shared__ __attribute__((aligned(16))) bf16 s_u[NUS * kEpTile];              // [slot][128 edges, kappa order]
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  seg_lut_init(s_lut, threadIdx.x);
+  const char* PQ = (const char*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const bf16* gmsg = (const bf16*)a.gmsg;
+  bf16* Gh = (bf16*)a.Gh;
+  const uint32_t E = (uint32_t)a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+  const int64_t NT = (a.E + kEpTile - 1) / kEpTile;
+  const int64_t G = gridDim.x;
+
+  // W_hl[h][o] from the packed (in, out) layout or its nn.Linear transpose, one 8-byte unit per step
+  for (int q = threadIdx.x; q < H * O / 4; q += 512) {
+    const int h = q / (O / 4), u = q % (O / 4);
+    const bf16* src = (const bf16*)a.w2;
+    bf16x4 v;
+    if (a.lin) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) v[t] = src[(int64_t)(4 * u + t) * H + h];
+    } else {
+      v = *reinterpret_cast<const bf16x4*>(src + (int64_t)h * O + 4 * u);
+    }
+    *reinterpret_cast<bf16x4*>(const_cast<bf16*>(wunit(s_whl, h, u))) = v;
+  }
+  if constexpr (NU > 0)
+    for (int q = threadIdx.x; q < NRB * kFragElems / 8; q += 512)
+      reinterpret_cast<bf16x8*>(s_wu)[q] = reinterpret_cast<const bf16x8*>(a.fr.u)[q];
+  for (int q = threadIdx.x; q < O; q += 512) s_b2[q] = a.fr.b2f[q];
+  // slot rows at and past F_E stay zero (the tiles write rows below F_E only)
+  if constexpr (NU > 0)
+    for (int q = FE * kEpTile + (int)threadIdx.x; q < NUS * kEpTile; q += 512) s_u[q] = (bf16)0.0f;
+  const bf16* const Wr = wrow_base(s_whl, c, g);
+  const bf16* const Wc = wcol_base(s_whl, c, g);
+  const bf16x8 Ipq = pq_sum_chunk(c, g);
+  bf16x8 ones;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) ones[s] = (bf16)1.0f;
+
+  // weight gradients of the wave's rows: dW_hl rows 16 w + 4g + i x columns 16 ob + c; db2
+  // columns 16 w + c (every row of the block holds the same sum); dW_e rows 16 w + 4g + i x slots 16 ub + c
+  f32x4 acc_hl[NRB], acc_b2, acc_we[NU > 0 ? NU : 1];
+#pragma unroll
+  for (int ob = 0; ob < NRB; ++ob) acc_hl[ob] = zero4();
+  acc_b2 = zero4();
+#pragma unroll
+  for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_we[ub] = zero4();
+
+  auto load_idx = [&](int64_t T, EpIdx& x) {   // E < 2^31 (coop_supported)
+    const uint32_t e0 = (uint32_t)T * kEpTile + 16 * w + c;
+    const uint32_t e = e0 < E ? e0 : E - 1;
+    x.ri = a.erow[e];
+    x.rj = a.col[e];
+    x.eid = NU > 0 ? (a.eids ? a.eids[e] : (int)e) : 0;
+  };
+  // the gathers of a sub-tile, in two parts: P_i | Q_j and the edge features (read by S1), and the
+  // message gradient of row i (read by S4); each part is issued into the registers of the current
+  // tile right after the stage that reads them, so one set of registers serves two tiles
+  auto gather_pq = [&](const EpIdx& x, EpGat& d) {
+    const uint32_t ri = (uint32_t)clampi(x.ri, N), rj = (uint32_t)clampi(x.rj, N);
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) d.pq[rb] = pq_gather(PQ, ri, rj, rb, g, H);
+  };
+  auto gather_u = [&](const EpIdx& x, EpGat& d) {
+    if constexpr (NU > 0) {   // slots past F_E read slot 0 and meet zero columns of W_u
+      const int eid = clampi(x.eid, (int)E);
+      d.u = load_chunk(ef + (int64_t)eid * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
+    }
+  };
+  auto gather_gm = [&](const EpIdx& x, EpGat& d) {
+    const uint32_t ri = (uint32_t)clampi(x.ri, N);
+    const bf16* gr = gmsg + (uint64_t)ri * (uint32_t)a.sgm + 4 * g;
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) d.gm[rb] = *reinterpret_cast<const bf16x4*>(gr + 16 * rb);
+  };
+  // the compiler waits for a loaded value where it is used; an empty asm that names every value of
+  // the next sub-tile makes that wait happen at the end of a tile, so that no load is carried into
+  // the loop header incomplete (which would make it wait for every outstanding store as well)
+  auto complete = [&](const EpGat& d, const EpIdx& x) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) asm volatile("" ::"v"(d.pq[rb]), "v"(d.gm[rb]));
+    asm volatile("" ::"v"(d.u), "v"(x.ri), "v"(x.rj), "v"(x.eid));
+  };
+
+  // the wave's chain for block tile T from its gathers, then the block's weight-gradient products
+  auto tile = [&](int64_t T, EpGat& cur, const EpIdx& xn) {
+    const uint32_t e = (uint32_t)T * kEpTile + 16 * w + c;
+    // waves 0..3: the rows of edges base - 1 .. base + 32 of 32-edge tile w (lanes 0..33), for its
+    // rank tables (issued first: only these waves load them)
+    int rowv = 0;
+    if (w < NK) {
+      const int64_t ee = T * kEpTile + 32 * w - 1 + l;
+      rowv = a.erow[ee < 0 ? 0 : (ee >= (int64_t)E ? (int64_t)E - 1 : ee)];
+    }
+    if ((uint32_t)T * kEpTile + kEpTile > E) {   // last tile: zero g_m on the edges past E (block-uniform)
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb)
+        if (e >= E) cur.gm[rb] = bf16x4{(bf16)0.0f, (bf16)0.0f, (bf16)0.0f, (bf16)0.0f};
+    }
+    // Each stage is software-pipelined over its eight 16-row blocks: the LDS operands of block
+    // rb + 1 are requested before the products of block rb, and the elementwise work of block
+    // rb - 1 follows them, so neither the LDS latency nor the product latency is waited for in
+    // line.  Scheduling barriers keep that order.
+    // ---- S1: pre1 = W_u e + P_i + Q_j; m1 = SiLU(pre1), s1 = SiLU'(pre1) (bf16)
+    bf16x4 s1[NRB];
+    bf16x8 m1c[KH];
+    {
+      bf16x8 fw[2];
+      f32x4 acc[2], y[2];
+      if constexpr (NU > 0) fw[0] = *reinterpret_cast<const bf16x8*>(s_wu + l * 8);
+#pragma unroll
+      for (int rb = 0; rb <= NRB; ++rb) {
+        if (rb < NRB) {
+          if constexpr (NU > 0)
+            if (rb + 1 < NRB) fw[(rb + 1) & 1] = *reinterpret_cast<const bf16x8*>(s_wu + ((rb + 1) * 64 + l) * 8);
+          __builtin_amdgcn_sched_barrier(0);
+          acc[rb & 1] = zero4();
+          if constexpr (NU > 0) mma(acc[rb & 1], fw[rb & 1], cur.u);
+          mma(acc[rb & 1], Ipq, cur.pq[rb]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (rb >= 1) {
+          const int r = rb - 1;
+          f32x4 d;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const YD v = silu_yd<bf16>(acc[r & 1][i]);
+            y[r & 1][i] = v.y;
+            d[i] = v.d;
+          }
+          s1[r] = pack4(d);
+          if (r & 1) m1c[r >> 1] = pack_chunk<bf16>(y[0], y[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    gather_pq(xn, cur);   // the next tile's
+    // ---- S2, S4: s2 = SiLU'(W_hl^T m1 + b2), g_a2 = g_m,i s2
+    bf16x8 ga2c[KO];
+    {
+      bf16x8 fr[2][KH];
+      f32x4 acc[2], ga[2];
+#pragma unroll
+      for (int k = 0; k < KH; ++k) fr[0][k] = w_cols(Wc, 0, k);
+#pragma unroll
+      for (int rb = 0; rb <= NRB; ++rb) {
+        if (rb < NRB) {
+          if (rb + 1 < NRB) {
+#pragma unroll
+            for (int k = 0; k < KH; ++k) fr[(rb + 1) & 1][k] = w_cols(Wc, rb + 1, k);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          acc[rb & 1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
+#pragma unroll
+          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], fr[rb & 1][k], m1c[k]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (rb >= 1) {
+          const int r = rb - 1;
+          const f32x4 gm = unpack4(cur.gm[r]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ga[r & 1][i] = gm[i] * silu_yd<bf16>(acc[r & 1][i]).d;
+          if (r & 1) ga2c[r >> 1] = pack_chunk<bf16>(ga[0], ga[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    gather_gm(xn, cur);   // the next tile's
+    // ---- S5: g_a1 = (W_hl g_a2) s1, stored per edge (Gh has a row for every edge of the last tile)
+    bf16x8 g1c[KH];
+    {
+      bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
+      bf16x8 fr[2][KO];
+      f32x4 acc[2], g1[2];
+#pragma unroll
+      for (int k = 0; k < KO; ++k) fr[0][k] = w_rows(Wr, 0, k);
+#pragma unroll
+      for (int rb = 0; rb <= NRB; ++rb) {
+        if (rb < NRB) {
+          if (rb + 1 < NRB) {
+#pragma unroll
+            for (int k = 0; k < KO; ++k) fr[(rb + 1) & 1][k] = w_rows(Wr, rb + 1, k);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          acc[rb & 1] = zero4();
+#pragma unroll
+          for (int k = 0; k < KO; ++k) mma(acc[rb & 1], fr[rb & 1][k], ga2c[k]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (rb >= 1) {
+          const int r = rb - 1;
+          const f32x4 d = unpack4(s1[r]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) g1[r & 1][i] = acc[r & 1][i] * d[i];
+          *reinterpret_cast<bf16x4*>(ghr + 16 * r) = pack4(g1[r & 1]);
+          if (r & 1) g1c[r >> 1] = pack_chunk<bf16>(g1[0], g1[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+
+    // ---- the block tile's edge-major operands: chain chunk (kc, w) of each buffer
+    __syncthreads();   // every wave has read the previous tile's buffers
+    const int sl = chain_slot<SW>(l);
+#pragma unroll
+    for (int kc = 0; kc < KH; ++kc) {
+      const int o = ((kc * NB + w) * 64 + sl) * 8;
+      *reinterpret_cast<bf16x8*>(s_m1 + o) = m1c[kc];
+      *reinterpret_cast<bf16x8*>(s_ga2 + o) = ga2c[kc];
+      *reinterpret_cast<bf16x8*>(s_g1 + o) = g1c[kc];
+    }
+    if constexpr (NU > 0) {
+      if (8 * g < FE) {   // edge 16 (w & 1) + c of K-chunk w >> 1 at position 8 (c >> 2) + 4 (w & 1) + (c & 3)
+        bf16* p = s_u + 8 * g * kEpTile + 32 * (w >> 1) + 8 * (c >> 2) + 4 * (w & 1) + (c & 3);
+#pragma unroll
+        for (int s = 0; s < 8; ++s) p[s * kEpTile] = cur.u[s];
+      }
+    }
+    gather_u(xn, cur);   // the next tile's
+    if (w < NK) {   // rank tables of 32-edge tile w (this wave's lanes read what its other lanes wrote:
+                    // LDS accesses of one wave complete in order, only the compiler must keep the order)
+      int* rows = s_rows[w];
+      if (l < 34) rows[l] = clampi(rowv, N);
+      asm volatile("" ::: "memory");
+      const int64_t base = T * kEpTile + 32 * w;
+      TileRanks rk;
+      rk.nvalid = (int)((int64_t)E - base < 32 ? (int64_t)E - base : 32);
+      const int k = l & 31;
+      const bool nf = l < 32 && k < rk.nvalid && (k == 0 || rows[k] != rows[k + 1]);
+      rk.mask = (uint32_t)(__ballot(nf) & 0xffffffffull);
+      rk.nrank = __popc(rk.mask);
+      rk.start_in = base == 0 || rows[0] != rows[1];
+      rk.end_in = base + 32 >= (int64_t)E || rows[33] != rows[32];
+      tile_rank_tables(rows + 1, rk, l, s_rowof[w], s_rspan[w]);
+      asm volatile("" ::: "memory");
+      if (l < 32) s_tgt[w][l] = l >= rk.nrank ? -3 : rank_whole(rk, l) ? s_rowof[w][l] : (l == 0 ? -1 : -2);
+      if (l == 0) s_nrk[w] = rk.nrank;
+    }
+    __syncthreads();
+    // ---- weight gradients over the 128 edges (four 32-edge K chunks), the edge-major chunk of the
+    // next column block requested before the products of this one
+    {
+      bf16x8 Am[NK], Bg[2];
+#pragma unroll
+      for (int eh = 0; eh < NK; ++eh) Am[eh] = chain_edge_major<NB, SW>(s_m1, w, c, g, eh);
+      Bg[0] = chain_edge_major<NB, SW>(s_ga2, 0, c, g, 0);
+#pragma unroll
+      for (int st = 0; st < NK * NRB; ++st) {
+        const int eh = st / NRB, ob = st % NRB;
+        if (st + 1 < NK * NRB)
+          Bg[(st + 1) & 1] = chain_edge_major<NB, SW>(s_ga2, (st + 1) % NRB, c, g, (st + 1) / NRB);
+        __builtin_amdgcn_sched_barrier(0);
+        mma(acc_hl[ob], Am[eh], Bg[st & 1]);
+        if (ob == w) mma(acc_b2, ones, Bg[st & 1]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int eh = 0; eh < NK; ++eh) {
+        const bf16x8 Ag = chain_edge_major<NB, SW>(s_g1, w, c, g, eh);   // g_a1 rows 16 w .. + 15, 32 edges
+        if constexpr (NU > 0) {
+#pragma unroll
+          for (int ub = 0; ub < NU; ++ub) {
+            if (16 * ub >= FE) continue;   // column block past the edge features
+            mma(acc_we[ub], Ag, *reinterpret_cast<const bf16x8*>(s_u + (16 * ub + c) * kEpTile + 32 * eh + 8 * g));
+          }
+        }
+        // destination sums of 32-edge tile eh: D = g_a1 S against its 0/1 segment matrix; a rank that
+        // is a whole row is stored to dP, the partial first / last ranks to the tile's carry slots
+        // 0 / 1 (summed in tile order by the fix-up)
+        const int nrk = __builtin_amdgcn_readfirstlane(s_nrk[eh]);
+        const int64_t tt = T * (kEpTile / 32) + eh;
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          if (16 * q >= nrk) break;
+          const int r = 16 * q + c;
+          f32x4 D = zero4();
+          mma(D, Ag, seg_chunk_span(r < nrk ? s_rspan[eh][r] : 0, g, s_lut));
+          const int tg = s_tgt[eh][r];
+          if (tg >= 0)
+            *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * w + 4 * g) = pack4(D);
+          else if (tg > -3)
+            *reinterpret_cast<f32x4*>(a.carry + (tt * 2 - 1 - tg) * O + 16 * w + 4 * g) = D;
+        }
+      }
+    }
+  };
+
+  EpIdx ix0, ix1;
+  EpGat cur;
+  const int64_t T0 = blockIdx.x;
+  load_idx(T0, ix0);
+  load_idx(T0 + G < NT ? T0 + G : T0, ix1);
+  gather_pq(ix0, cur);
+  gather_u(ix0, cur);
+  gather_gm(ix0, cur);
+  complete(cur, ix1);
+  __syncthreads();   // weights in LDS
+  // tile T from cur (whose registers receive the gathers of tile T + G, indices ix1) while the
+  // indices of tile T + 2G load into ix0
+  for (int64_t T = T0; T < NT; T += G) {
+    load_idx(T + 2 * G < NT ? T + 2 * G : T, ix0);
+    tile(T, cur, ix1);
+    complete(cur, ix0);
+    ix1 = ix0;
+  }
+
+  // ---- this block's weight-gradient partial [dW_hl ; db2 | dW_e]
+  float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
+#pragma unroll
+  for (int ob = 0; ob < NRB; ++ob)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) P[(int64_t)(16 * w + 4 * g + i) * O + 16 * ob + c] = acc_hl[ob][i];
+  if (g == 0) P[(int64_t)H * O + 16 * w + c] = acc_b2[0];
+  if constexpr (NU > 0) {
+#pragma unroll
+    for (int ub = 0; ub < NU; ++ub) {
+      const int slot = 16 * ub + c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (slot < FE) P[(int64_t)(H + 1) * O + (int64_t)(16 * w + 4 * g + i) * FE + slot] = acc_we[ub][i];
+    }
+  }
+}
+
+}  // namespace
+
+int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.E > 0) {
+    if (a.FE == 0)
+      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
+    else if (a.FE <= 16)
+      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<1>), dim3(nblk), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<2>), dim3(nblk), dim3(512), 0, st, a);
+  }
+  return (int)hipGetLastError();
+}
+
+}  // namespace egnn

@@ -118,8 +118,8 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Dgq = (s.eq && !coop) ? take(EF * s.M * s.esz) : nullptr;
   w->Dga2 = coop ? nullptr : take(EF * s.O * s.esz);
   w->Dp = (s.eq && !coop && !wide) ? take(EF * s.M * s.esz) : nullptr;
-  // the cooperative kernels store Gh / Gx rows for every edge slot of their last tile (32 or 64 edges)
-  const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), 2 * kTileEdges) * 2 * kTileEdges : E;
+  // the cooperative kernels store Gh / Gx rows for every edge slot of their last tile (32, 64 or 128 edges)
+  const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), 4 * kTileEdges) * 4 * kTileEdges : E;
   w->Gh = take(Er * s.H * s.esz);
   w->Gx = (float*)take(Er * 4 * sizeof(float));
   w->R2 = (coop || wide) ? nullptr : (float*)take(E * sizeof(float));
