@@ -17,8 +17,8 @@
 // After its chain each wave writes its m1, g_a2 and g_a1 (and the edge
 // features) into chain-ordered LDS buffers of the 128-edge block tile; after a
 // barrier wave w reads them back edge-major with transposing LDS reads and
-// accumulates, over all 128 edges, the rows [16 w, 16 w + 16) of dW_hl and dW_e
-// and the columns [16 w, 16 w + 16) of db2 in its registers.  Each block writes
+// accumulates, over all 128 edges, a 64 x 32 block of dW_hl, the rows
+// [16 w, 16 w + 16) of dW_e and 16 columns of db2 in its registers.  Each block writes
 // one partial of [dW_hl ; db2 | dW_e] that a fixed-order sum reduces.  The same
 // edge-major g_a1 gives the destination sums of Gh (dP) per 32-edge tile, by an
 // MFMA against the tile's 0/1 segment matrix: rows whole in the tile are stored,
@@ -133,8 +133,9 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 #pragma unroll
   for (int s = 0; s < 8; ++s) ones[s] = (bf16)1.0f;
 
-  // weight gradients of the wave's rows: dW_hl rows 16 w + 4g + i x columns 16 ob + c; db2
-  // columns 16 w + c (every row of the block holds the same sum); dW_e rows 16 w + 4g + i x slots 16 ub + c
+  // weight gradients: dW_hl block (4 (w >> 2) + a, 2 (w & 3) + b) in acc_hl[2a + b], rows 4g + i x columns c
+  // of the block; db2 columns 16 (2 (w & 3) + (w >> 2)) + c (every row of the block holds the same sum);
+  // dW_e rows 16 w + 4g + i x slots 16 ub + c
   f32x4 acc_hl[NRB], acc_b2, acc_we[NU > 0 ? NU : 1];
 #pragma unroll
   for (int ob = 0; ob < NRB; ++ob) acc_hl[ob] = zero4();
@@ -333,21 +334,29 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
       if (l == 0) s_nrk[w] = rk.nrank;
     }
     __syncthreads();
-    // ---- weight gradients over the 128 edges (four 32-edge K chunks), the edge-major chunk of the
-    // next column block requested before the products of this one
+    // ---- weight gradients over the 128 edges (four 32-edge K chunks): wave w takes the 4 x 2 blocks
+    // h-blocks 4 (w >> 2) .. + 3 x o-blocks 2 (w & 3), + 1 of dW_hl (six edge-major operand chunks per K
+    // chunk), the next K chunk's operands requested before the products of this one
     {
-      bf16x8 Am[NK], Bg[2];
+      const int hq = w >> 2, oq = w & 3;
+      bf16x8 Am[2][4], Bg[2][2];
+      auto load_ops = [&](int eh, int p) {
 #pragma unroll
-      for (int eh = 0; eh < NK; ++eh) Am[eh] = chain_edge_major<NB, SW>(s_m1, w, c, g, eh);
-      Bg[0] = chain_edge_major<NB, SW>(s_ga2, 0, c, g, 0);
+        for (int a4 = 0; a4 < 4; ++a4) Am[p][a4] = chain_edge_major<NB, SW>(s_m1, 4 * hq + a4, c, g, eh);
 #pragma unroll
-      for (int st = 0; st < NK * NRB; ++st) {
-        const int eh = st / NRB, ob = st % NRB;
-        if (st + 1 < NK * NRB)
-          Bg[(st + 1) & 1] = chain_edge_major<NB, SW>(s_ga2, (st + 1) % NRB, c, g, (st + 1) / NRB);
+        for (int b2 = 0; b2 < 2; ++b2) Bg[p][b2] = chain_edge_major<NB, SW>(s_ga2, 2 * oq + b2, c, g, eh);
+      };
+      load_ops(0, 0);
+#pragma unroll
+      for (int eh = 0; eh < NK; ++eh) {
+        if (eh + 1 < NK) load_ops(eh + 1, (eh + 1) & 1);
         __builtin_amdgcn_sched_barrier(0);
-        mma(acc_hl[ob], Am[eh], Bg[st & 1]);
-        if (ob == w) mma(acc_b2, ones, Bg[st & 1]);
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4)
+#pragma unroll
+          for (int b2 = 0; b2 < 2; ++b2) mma(acc_hl[2 * a4 + b2], Am[eh & 1][a4], Bg[eh & 1][b2]);
+        if (hq) mma(acc_b2, ones, Bg[eh & 1][1]);   // db2 columns of o-block 2 oq + hq
+        else mma(acc_b2, ones, Bg[eh & 1][0]);
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -403,10 +412,13 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   // ---- this block's weight-gradient partial [dW_hl ; db2 | dW_e]
   float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
 #pragma unroll
-  for (int ob = 0; ob < NRB; ++ob)
+  for (int a4 = 0; a4 < 4; ++a4)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) P[(int64_t)(16 * w + 4 * g + i) * O + 16 * ob + c] = acc_hl[ob][i];
-  if (g == 0) P[(int64_t)H * O + 16 * w + c] = acc_b2[0];
+    for (int b2 = 0; b2 < 2; ++b2)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        P[(int64_t)(16 * (4 * (w >> 2) + a4) + 4 * g + i) * O + 16 * (2 * (w & 3) + b2) + c] = acc_hl[2 * a4 + b2][i];
+  if (g == 0) P[(int64_t)H * O + 16 * (2 * (w & 3) + (w >> 2)) + c] = acc_b2[0];
   if constexpr (NU > 0) {
 #pragma unroll
     for (int ub = 0; ub < NU; ++ub) {
