@@ -57,7 +57,7 @@ class EgnnNodeDims(ctypes.Structure):
 
 _lib = None
 
-ABI_VERSION = 7   # include/egnn.h egnn_abi_version()
+ABI_VERSION = 8   # include/egnn.h egnn_abi_version()
 
 
 def _check_stamp() -> None:

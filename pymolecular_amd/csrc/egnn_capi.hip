@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 7;
+constexpr int32_t kAbiVersion = 8;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -257,7 +257,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   const bool coop = coop_supported(s);
   a.dwpart = w.dwpart; a.LW = w.LW;
   a.geo = w.geo;
-  a.dP = w.dPQ; a.sdp = 2 * s.H; a.carry = w.carry;
+  a.dP = w.dPQ; a.sdp = 2 * s.H; a.carry = w.carry; a.tile_tab = v.tile_tab;
   if (coop || wide_supported(s)) a.ntiles = cdiv(s.E, kTileEdges);
   if (coop || wide_supported(s)) {
     ProfScope ps(EGNN_K_BWD_EDGE, st);

@@ -22,7 +22,14 @@ struct SchedView {
   int32_t* csc_ptr;   // [N+1] source-sorted offsets
   int32_t* csc_eid;   // [E]   CSR edge positions sorted by col (stable)
   int32_t* err;       // [1]   CSR validation flag
+  int32_t* tile_tab;  // [ceil(E/32)][64] ranks of each 32-edge tile (kTab* offsets)
 };
+// Ranks of a 32-edge tile (the maximal runs of edges of one row inside it), one 64-int row per tile:
+// [kTabTgt + r] target of rank r: its row when the rank is the whole row, -1 / -2 when it is the
+// partial first / last rank of a row that crosses the tile (carry slot 0 / 1), -3 past the last rank;
+// [kTabSpan ...] the ranks' spans as 16-bit values (first edge | count << 8), two per int;
+// [kTabNrank] the rank count.
+constexpr int kTabTgt = 0, kTabSpan = 32, kTabNrank = 48, kTabInts = 64;
 size_t sched_layout(int64_t N, int64_t E, void* base, SchedView* v);
 
 // ---- weight fragments ------------------------------------------------------
@@ -200,6 +207,7 @@ struct BwdArgs {
   // stored to dP (row stride sdp), the partial first / last rows of tile t to carry[t][2][O]
   void* dP; int64_t sdp;
   float* carry;
+  const int32_t* tile_tab;   // the schedule's per-32-edge-tile rank tables (SchedView::tile_tab)
   const void* w2;  // W_hl (H x O) and W1_mov (O x M), row-major, activation dtype;
   const void* w1m; // (O x H) and (M x O) with lin
   int lin;         // weights in torch.nn.Linear (out, in) layout

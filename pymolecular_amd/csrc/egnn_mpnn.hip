@@ -86,11 +86,9 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_m1[CHB];
   __shared__ __attribute__((aligned(16))) bf16 s_ga2[CHB];
   __shared__ __attribute__((aligned(16))) bf16 s_g1[CHB];
-  // destination sums: the 32-edge tiles of the block tile, built by waves 0..3 (one each): the rows of
-  // edges base - 1 .. base + 32, the row and span of each rank, the target of each rank (a row >= 0,
-  // carry slot 0 / 1 as -1 / -2, none -3) and the rank count
-  __shared__ int s_rows[kEpTile / 32][34], s_rowof[kEpTile / 32][32], s_rspan[kEpTile / 32][32];
-  __shared__ int s_tgt[kEpTile / 32][32], s_nrk[kEpTile / 32];
+  // destination sums: the rank tables of the block tile's 32-edge tiles (from the schedule, one per
+  // wave 0..3), and the 0/1 patterns of the segment matrix
+  __shared__ int s_tab[kEpTile / 32][kTabInts];
   __shared__ uint2 s_lut[16];
   __shared__ __attribute__((aligned(16))) bf16 s_u[NUS * kEpTile];              // [slot][128 edges, kappa order]
 
@@ -182,13 +180,11 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   // the wave's chain for block tile T from its gathers, then the block's weight-gradient products
   auto tile = [&](int64_t T, EpGat& cur, const EpIdx& xn) {
     const uint32_t e = (uint32_t)T * kEpTile + 16 * w + c;
-    // waves 0..3: the rows of edges base - 1 .. base + 32 of 32-edge tile w (lanes 0..33), for its
-    // rank tables (issued first: only these waves load them)
-    int rowv = 0;
-    if (w < NK) {
-      const int64_t ee = T * kEpTile + 32 * w - 1 + l;
-      rowv = a.erow[ee < 0 ? 0 : (ee >= (int64_t)E ? (int64_t)E - 1 : ee)];
-    }
+    // waves 0..3: the rank table of 32-edge tile w (one int per lane; issued first: only these waves
+    // load it); a tile past the last edge has no ranks
+    const int64_t ntt = ((int64_t)E + 31) / 32, tw = T * (kEpTile / 32) + w;
+    int tabv = 0;
+    if (w < NK) tabv = a.tile_tab[(tw < ntt ? tw : ntt - 1) * kTabInts + l];
     if ((uint32_t)T * kEpTile + kEpTile > E) {   // last tile: zero g_m on the edges past E (block-uniform)
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)
@@ -314,25 +310,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
       }
     }
     gather_u(xn, cur);   // the next tile's
-    if (w < NK) {   // rank tables of 32-edge tile w (this wave's lanes read what its other lanes wrote:
-                    // LDS accesses of one wave complete in order, only the compiler must keep the order)
-      int* rows = s_rows[w];
-      if (l < 34) rows[l] = clampi(rowv, N);
-      asm volatile("" ::: "memory");
-      const int64_t base = T * kEpTile + 32 * w;
-      TileRanks rk;
-      rk.nvalid = (int)((int64_t)E - base < 32 ? (int64_t)E - base : 32);
-      const int k = l & 31;
-      const bool nf = l < 32 && k < rk.nvalid && (k == 0 || rows[k] != rows[k + 1]);
-      rk.mask = (uint32_t)(__ballot(nf) & 0xffffffffull);
-      rk.nrank = __popc(rk.mask);
-      rk.start_in = base == 0 || rows[0] != rows[1];
-      rk.end_in = base + 32 >= (int64_t)E || rows[33] != rows[32];
-      tile_rank_tables(rows + 1, rk, l, s_rowof[w], s_rspan[w]);
-      asm volatile("" ::: "memory");
-      if (l < 32) s_tgt[w][l] = l >= rk.nrank ? -3 : rank_whole(rk, l) ? s_rowof[w][l] : (l == 0 ? -1 : -2);
-      if (l == 0) s_nrk[w] = rk.nrank;
-    }
+    if (w < NK) s_tab[w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
     __syncthreads();
     // ---- weight gradients over the 128 edges (four 32-edge K chunks): wave w takes the 4 x 2 blocks
     // h-blocks 4 (w >> 2) .. + 3 x o-blocks 2 (w & 3), + 1 of dW_hl (six edge-major operand chunks per K
@@ -372,15 +350,16 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         // destination sums of 32-edge tile eh: D = g_a1 S against its 0/1 segment matrix; a rank that
         // is a whole row is stored to dP, the partial first / last ranks to the tile's carry slots
         // 0 / 1 (summed in tile order by the fix-up)
-        const int nrk = __builtin_amdgcn_readfirstlane(s_nrk[eh]);
+        const int nrk = __builtin_amdgcn_readfirstlane(s_tab[eh][kTabNrank]);
         const int64_t tt = T * (kEpTile / 32) + eh;
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
           if (16 * q >= nrk) break;
           const int r = 16 * q + c;
           f32x4 D = zero4();
-          mma(D, Ag, seg_chunk_span(r < nrk ? s_rspan[eh][r] : 0, g, s_lut));
-          const int tg = s_tgt[eh][r];
+          mma(D, Ag, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[eh] + kTabSpan)[r] : 0,
+                                    g, s_lut));
+          const int tg = s_tab[eh][kTabTgt + r];
           if (tg >= 0)
             *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * w + 4 * g) = pack4(D);
           else if (tg > -3)

@@ -10,6 +10,8 @@
 //                 their partial sums are combined by a fixed-order fix-up
 //   csc_ptr/eid   the edges sorted by source (stable), for the deterministic
 //                 source-side gradient sum of the backward pass
+//   tile_tab[]    per 32-edge tile: the row runs (ranks) inside it, with the
+//                 span and destination of each, for the per-tile row sums
 // Built once per graph and cached by the caller.
 #include <hipcub/hipcub.hpp>
 #include "egnn_device.h"
@@ -27,6 +29,7 @@ size_t sched_layout(int64_t N, int64_t E, void* base, SchedView* v) {
   v->csc_ptr = (int32_t*)take(sizeof(int32_t) * (size_t)(N + 1));
   v->csc_eid = (int32_t*)take(sizeof(int32_t) * (size_t)std::max<int64_t>(E, 1));
   v->err = (int32_t*)take(sizeof(int32_t));
+  v->tile_tab = (int32_t*)take(sizeof(int32_t) * kTabInts * (size_t)std::max<int64_t>(cdiv(E, kTileEdges), 1));
   return off;
 }
 
@@ -115,6 +118,47 @@ __global__ void fix_flag_kernel(const int32_t* __restrict__ rowptr, int64_t N, u
   }
 }
 
+// One wave per 32-edge tile t: lanes 0..33 hold the rows of edges 32 t - 1 .. 32 t + 32 (clamped);
+// edge k of the tile starts a rank when k = 0 or its row differs from that of edge k - 1.  The lane
+// that starts rank q sends its span and row to lane q, which writes entry q of the table.
+__global__ __launch_bounds__(256) void tile_tab_kernel(const int32_t* __restrict__ erow, int64_t E, int64_t ntiles,
+                                                       int32_t* __restrict__ tab) {
+  const int l = threadIdx.x & 63;
+  const int64_t t = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= ntiles) return;   // whole waves
+  const int64_t base = t * kTileEdges;
+  const int64_t e = base - 1 + l;
+  const int row = erow[e < 0 ? 0 : (e >= E ? E - 1 : e)];
+  const int nvalid = (int)(E - base < kTileEdges ? E - base : kTileEdges);
+  const int rk = __shfl(row, l + 1 < 64 ? l + 1 : 63, 64), rprev = row;   // edge l and edge l - 1
+  const bool starts = l < nvalid && (l == 0 || rk != rprev);
+  const uint32_t mask = (uint32_t)(__ballot(starts) & 0xffffffffull);
+  const int nrank = __popc(mask);
+  const bool start_in = base == 0 || __shfl(row, 0, 64) != __shfl(row, 1, 64);
+  const bool end_in = base + kTileEdges >= E || __shfl(row, 33, 64) != __shfl(row, 32, 64);
+  // the lane that starts rank q: its span (first edge | count << 8) and row, sent to lane q
+  int q = 63, span = 0;
+  if (starts) {
+    const uint32_t rest = l >= 31 ? 0u : (mask & ~((2u << l) - 1u));
+    const int end = rest ? __ffs(rest) - 1 : nvalid;
+    q = __popc(mask & ((2u << l) - 1u)) - 1;
+    span = l | ((end - l) << 8);
+  }
+  const int rspan = __builtin_amdgcn_ds_permute(q * 4, span);
+  const int rrow = __builtin_amdgcn_ds_permute(q * 4, rk);
+  int32_t* tt = tab + t * kTabInts;
+  if (l < kTileEdges) {
+    const bool has = l < nrank;
+    const bool whole = (l > 0 || start_in) && (l < nrank - 1 || end_in);
+    tt[kTabTgt + l] = !has ? -3 : whole ? rrow : (l == 0 ? -1 : -2);
+    reinterpret_cast<uint16_t*>(tt + kTabSpan)[l] = (uint16_t)(has ? rspan : 0);
+  } else if (l == kTileEdges) {
+    tt[kTabNrank] = nrank;
+  } else if (l > kTileEdges && l < kTileEdges + 16) {
+    tt[kTabNrank + l - kTileEdges] = 0;   // padding
+  }
+}
+
 __global__ void iota_kernel(int32_t* __restrict__ v, int64_t E) {
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < E; e += (int64_t)gridDim.x * blockDim.x)
     v[e] = (int32_t)e;
@@ -145,7 +189,11 @@ int launch_schedule(const int32_t* rowptr, const int32_t* col, int64_t N, int64_
   if (hipStreamSynchronize(st) != hipSuccess) return EGNN_ERR_HIP;
   if (herr) return EGNN_ERR_CSR;
 
-  if (E > 0) hipLaunchKernelGGL(erow_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, rowptr, N, v.erow);
+  if (E > 0) {
+    hipLaunchKernelGGL(erow_kernel, dim3((unsigned)cdiv(N, 256)), dim3(256), 0, st, rowptr, N, v.erow);
+    const int64_t nt = cdiv(E, kTileEdges);
+    hipLaunchKernelGGL(tile_tab_kernel, dim3((unsigned)cdiv(nt, 4)), dim3(256), 0, st, v.erow, E, nt, v.tile_tab);
+  }
   int fb = (int)std::min<int64_t>(cdiv(N, 256), 4096);
   hipLaunchKernelGGL(fix_flag_kernel, dim3(fb), dim3(256), 0, st, rowptr, N, t.flags);
   size_t cb = t.cub_bytes;

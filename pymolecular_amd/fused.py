@@ -52,13 +52,18 @@ class Schedule:
 
 def schedule_arrays(sched: Schedule) -> dict:
     """int32 views of a schedule buffer, in the layout egnn_schedule_build writes:
-    erow [E], fix_rows [n_fix], csc_ptr [N+1], csc_eid [E] (each 256-byte aligned)."""
+    erow [E], fix_rows [n_fix], csc_ptr [N+1], csc_eid [E], and the per-32-edge-tile rank tables
+    tile_tab [ceil(E/32)][64] (each 256-byte aligned)."""
     N, E = sched.N, sched.E
+    ntiles = max((E + 31) // 32, 1)
     off = 0
     out = {}
-    for name, n in (("erow", max(E, 1)), ("fix_rows", N), ("n_fix", 1), ("csc_ptr", N + 1), ("csc_eid", max(E, 1))):
+    for name, n in (("erow", max(E, 1)), ("fix_rows", N), ("n_fix", 1), ("csc_ptr", N + 1), ("csc_eid", max(E, 1)),
+                    ("err", 1), ("tile_tab", ntiles * 64)):
         out[name] = sched.buf[off:off + 4 * n].view(torch.int32)
         off = (off + 4 * n + 255) // 256 * 256
+    out.pop("err")
+    out["tile_tab"] = out["tile_tab"].view(ntiles, 64)[:(E + 31) // 32]
     nf = int(out.pop("n_fix")[0])
     out["fix_rows"] = out["fix_rows"][:nf]
     out["erow"] = out["erow"][:E]

@@ -9,8 +9,35 @@ from tests.cases import random_csr
 TILE = 32
 
 
+def tile_tab_ref(erow):
+    """Rank tables of the 32-edge tiles (one int32 row of 64 per tile), from the per-edge rows: a rank
+    starts at the tile's first edge and wherever the row changes; targets are the row of a rank that
+    is a whole row, -1 / -2 for a partial first / last rank, -3 past the last rank; spans are
+    first | count << 8 as 16-bit values in ints 32..47; the rank count in int 48."""
+    erow = np.asarray(erow, np.int64)
+    E = len(erow)
+    nt = (E + TILE - 1) // TILE
+    tab = np.zeros((nt, 64), np.int64)
+    for t in range(nt):
+        base = t * TILE
+        nv = min(E - base, TILE)
+        rows = erow[base:base + nv]
+        starts = [k for k in range(nv) if k == 0 or rows[k] != rows[k - 1]]
+        nr = len(starts)
+        start_in = base == 0 or erow[base - 1] != erow[base]
+        end_in = base + TILE >= E or erow[base + TILE] != erow[base + TILE - 1]
+        tab[t, :TILE] = -3
+        for q, k in enumerate(starts):
+            end = starts[q + 1] if q + 1 < nr else nv
+            whole = (q > 0 or start_in) and (q < nr - 1 or end_in)
+            tab[t, q] = rows[k] if whole else (-1 if q == 0 else -2)
+            tab[t, 32 + q // 2] |= (k | ((end - k) << 8)) << (16 * (q % 2))
+        tab[t, 48] = nr
+    return tab.astype(np.uint32).view(np.int32)
+
+
 def schedule_ref(rowptr, col):
-    """numpy restatement of the schedule: per-edge rows, split/empty rows, stable CSC."""
+    """numpy restatement of the schedule: per-edge rows, split/empty rows, stable CSC, tile rank tables."""
     rowptr = np.asarray(rowptr, np.int64)
     N = len(rowptr) - 1
     deg = np.diff(rowptr)
@@ -20,7 +47,35 @@ def schedule_ref(rowptr, col):
     fix = np.flatnonzero((deg == 0) | (first_tile != last_tile))
     csc_eid = np.argsort(np.asarray(col), kind="stable")
     csc_ptr = np.searchsorted(np.asarray(col)[csc_eid], np.arange(N + 1), side="left")
-    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid)
+    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid, tile_tab=tile_tab_ref(erow))
+
+
+def brute_force_tile_tab(rowptr, E):
+    """The same tables from the rows' edge ranges: the ranks of tile t are the rows whose range
+    [rowptr[r], rowptr[r + 1]) meets [32 t, 32 t + 32), in order; a rank is a whole row when the
+    range lies inside the tile."""
+    N = len(rowptr) - 1
+    nt = (E + TILE - 1) // TILE
+    out = []
+    for t in range(nt):
+        lo, hi = t * TILE, min(t * TILE + TILE, E)
+        tgt, spans = [], []
+        for r in range(N):
+            a, b = int(rowptr[r]), int(rowptr[r + 1])
+            s0, s1 = max(a, lo), min(b, hi)
+            if s0 >= s1:
+                continue
+            spans.append((s0 - lo) + ((s1 - s0) << 8))
+            tgt.append(r if (a >= lo and b <= lo + TILE) else (-1 if not tgt else -2))
+        row = [-3] * 64
+        row[:len(tgt)] = tgt
+        for i in range(32, 64):
+            row[i] = 0
+        for q, sp in enumerate(spans):
+            row[32 + q // 2] |= sp << (16 * (q % 2))
+        row[48] = len(tgt)
+        out.append([v - (1 << 32) if v >= (1 << 31) else v for v in row])
+    return np.asarray(out, np.int64).reshape(nt, 64)
 
 
 def brute_force_schedule(rowptr, col):
@@ -39,11 +94,13 @@ def brute_force_schedule(rowptr, col):
     csc_ptr = [0]
     for bkt in buckets:
         csc_ptr.append(csc_ptr[-1] + len(bkt))
-    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid)
+    return dict(erow=erow, fix_rows=fix, csc_ptr=csc_ptr, csc_eid=csc_eid,
+                tile_tab=brute_force_tile_tab(rowptr, len(col)))
 
 
 def test_schedule_ref_matches_brute_force():
     for seed in range(5):
+        # degrees from 0 to 69: empty rows, rows inside one tile, rows across several tiles
         degs = np.random.Generator(np.random.PCG64(seed)).integers(0, 70, size=37)
         rowptr, col = random_csr(37, degs, seed)
         a, b = schedule_ref(rowptr, col), brute_force_schedule(rowptr, col)
