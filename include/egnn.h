@@ -119,8 +119,10 @@ size_t egnn_schedule_tmp_bytes(int64_t N, int64_t E);
 
 /* Validate the CSR (rowptr[0]=0, non-decreasing, rowptr[N]=E, 0<=col<N) and
  * build the schedule into `sched` (egnn_schedule_bytes bytes): the per-edge
- * row ids, the list of rows that cross a 32-edge tile or are empty, and the
- * stable source-sorted permutation of the edges.  Bit-exact and deterministic.
+ * row ids, the list of rows that cross a 32-edge tile or are empty, the
+ * stable source-sorted permutation of the edges, and for every 32-edge tile
+ * the runs of one row inside it (span and destination of each, for the
+ * per-tile row sums).  Bit-exact and deterministic.
  * Synchronises `stream` once to read the validation flag. */
 int32_t egnn_schedule_build(const int32_t* rowptr, const int32_t* col, int64_t N, int64_t E,
                             void* sched, size_t sched_bytes, void* tmp, size_t tmp_bytes,

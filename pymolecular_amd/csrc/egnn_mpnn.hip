@@ -264,7 +264,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
     {
       bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
       bf16x8 fr[2][KO];
-      f32x4 acc[2], g1[2];
+      f32x4 acc[2];
+      bf16x4 g1p[2];
 #pragma unroll
       for (int k = 0; k < KO; ++k) fr[0][k] = w_rows(Wr, 0, k);
 #pragma unroll
@@ -283,10 +284,12 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         if (rb >= 1) {
           const int r = rb - 1;
           const f32x4 d = unpack4(s1[r]);
+          f32x4 g1;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) g1[r & 1][i] = acc[r & 1][i] * d[i];
-          *reinterpret_cast<bf16x4*>(ghr + 16 * r) = pack4(g1[r & 1]);
-          if (r & 1) g1c[r >> 1] = pack_chunk<bf16>(g1[0], g1[1]);
+          for (int i = 0; i < 4; ++i) g1[i] = acc[r & 1][i] * d[i];
+          g1p[r & 1] = pack4(g1);
+          *reinterpret_cast<bf16x4*>(ghr + 16 * r) = g1p[r & 1];
+          if (r & 1) g1c[r >> 1] = __builtin_shufflevector(g1p[0], g1p[1], 0, 1, 2, 3, 4, 5, 6, 7);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
