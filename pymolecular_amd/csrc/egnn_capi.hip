@@ -190,7 +190,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.out_msg = out_msg; a.smsg = strides->msg;
   a.out_mov = out_mov; a.smov = strides->mov;
   a.carry = w.carry;
-  a.fix_rows = v.fix_rows; a.n_fix = v.n_fix;
+  a.fix_rows = v.fix_rows; a.n_fix = v.n_fix; a.tile_tab = v.tile_tab;
   a.geo = w.geo;
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);

@@ -1599,8 +1599,8 @@ bool coop_supported(const LayerShape& s) {
          s.E + kTileEdges < (int64_t(1) << 31);
 }
 
-// The MPNN H = 128 backward runs the edge-parallel kernel (egnn_mpnn.hip); the 16-wave kernel
-// remains as the identity-MLP instrument (EGNN_FLAG_PROBE_IDENTITY).
+// The MPNN H = 128 layer runs the edge-parallel kernels (egnn_mpnn.hip); the cooperative MPNN kernels
+// remain as the identity-MLP instrument (EGNN_FLAG_PROBE_IDENTITY).
 static bool mpnn_ep(const LayerShape& s) { return !s.eq && s.H == 128 && !s.probe; }
 
 bool coop_dst_sums(const LayerShape& s) { return coop_supported(s) && !s.eq && s.H == 128; }
@@ -1618,6 +1618,7 @@ int64_t coop_dw_len(const LayerShape& s) {
 
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
   if (s.probe) return launch_fwd_t<128, 128, 128, 8, false, true>(a, st);   // make_shape: MPNN, H = 128
+  if (mpnn_ep(s)) return launch_mpnn_fwd_ep(a, st);
   if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }

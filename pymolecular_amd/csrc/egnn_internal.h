@@ -183,6 +183,7 @@ struct FwdArgs {
   const void* w1m;   // W1_mov: (O x M) row-major, or (M x O) with lin
   int lin;           // weights in torch.nn.Linear (out, in) layout
   int coord_res;     // out_mov = coord + the aggregated update
+  const int32_t* tile_tab;   // the schedule's per-32-edge-tile rank tables (SchedView::tile_tab)
 };
 // part 0: edge tiles, part 1: split/empty-row fix-up
 int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
@@ -228,6 +229,10 @@ int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t
 // [dW_hl ; db2 | dW_e] (coop_dw_len), Gh per edge, the destination sums of Gh (dP, carries) as the
 // 16-wave kernel makes them.
 int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st);
+// Edge-parallel MPNN forward (bf16, H = O = 128): the per-row sums as whole rows and carries, completed
+// by the fix-up launch; mpnn_ep_blocks: its (and the backward's) grid.
+int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st);
+int mpnn_ep_blocks(int64_t E);
 // Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
 // from L2, backward writes the per-edge weight-gradient factors Dm1, Dm, Dgq, Dga2.
 bool wide_supported(const LayerShape& s);

@@ -412,7 +412,199 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// forward of the MPNN layer, edge-parallel (bf16, H = O = 128)
+// ---------------------------------------------------------------------------
+// The same organisation as the backward: eight waves per CU, each runs S1 (pre1 = W_u e + P_i +
+// Q_j, m1 = SiLU(pre1)) and S2 (m = SiLU(W_hl^T m1 + b2)) for its own 16 edges in registers, the W_u
+// and W_hl^T fragments read from LDS as whole 16-byte fragments, each stage software-pipelined over
+// its row blocks.  The messages m go chain-ordered into an LDS buffer of the 128-edge block tile (by
+// tile parity, so one barrier per tile); after the barrier wave w sums the rows 16 w .. 16 w + 15 of
+// m over each row run of the four 32-edge tiles: one MFMA per 16 ranks against the 0/1 segment
+// matrix from the schedule's rank tables, a run that is a whole row stored to out_msg, a partial
+// first / last run to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).
+// Reference: forward_kernel.py:89-153 computes the same per-row sums one program per CSR row.
+template <int NU>
+__global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
+  constexpr int H = 128, O = 128, NRB = 8, KH = H / 32, KO = O / 32;
+  constexpr int NB = kEpWaves;                  // 16-edge blocks of a block tile
+  constexpr int NK = kEpTile / 32;              // 32-edge tiles of a block tile
+  constexpr int CHB = KO * NB * 64 * 8;         // one chain buffer: 4 chunks x 8 edge blocks (32 KB)
+  constexpr bool SW = true;
+  __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A = W_hl^T, S2
+  __shared__ __attribute__((aligned(16))) bf16 s_wu[NU > 0 ? NRB * kFragElems : 8];   // A = W_u, S1
+  __shared__ __attribute__((aligned(16))) float s_b2[O];
+  __shared__ __attribute__((aligned(16))) bf16 s_m[2][CHB];                     // messages, by tile parity
+  __shared__ int s_tab[2][NK][kTabInts];                                      // rank tables, by tile parity
+  __shared__ uint2 s_lut[16];
+
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
+  seg_lut_init(s_lut, threadIdx.x);
+  const char* PQ = (const char*)a.PQ;
+  const bf16* ef = (const bf16*)a.ef;
+  const uint32_t E = (uint32_t)a.E;
+  const int N = (int)a.N;
+  const int FE = a.FE;
+  const int64_t NT = (a.E + kEpTile - 1) / kEpTile;
+  const int64_t ntt = (a.E + 31) / 32;
+  const int64_t G = gridDim.x;
+  const bool use_eids = a.eids != nullptr;
+
+  for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 512)
+    reinterpret_cast<bf16x8*>(s_whlT)[q] = reinterpret_cast<const bf16x8*>(a.fr.hlT)[q];
+  if constexpr (NU > 0)
+    for (int q = threadIdx.x; q < NRB * kFragElems / 8; q += 512)
+      reinterpret_cast<bf16x8*>(s_wu)[q] = reinterpret_cast<const bf16x8*>(a.fr.u)[q];
+  for (int q = threadIdx.x; q < O; q += 512) s_b2[q] = a.fr.b2f[q];
+  const bf16x8 Ipq = pq_sum_chunk(c, g);
+
+  auto load_idx = [&](int64_t T, EpIdx& x) {   // E < 2^31 (coop_supported)
+    const uint32_t e0 = (uint32_t)T * kEpTile + 16 * w + c;
+    const uint32_t e = e0 < E ? e0 : E - 1;
+    x.ri = a.erow[e];
+    x.rj = a.col[e];
+    x.eid = NU > 0 ? (use_eids ? a.eids[e] : (int)e) : 0;
+  };
+  auto gather = [&](const EpIdx& x, EpGat& d) {
+    const uint32_t ri = (uint32_t)clampi(x.ri, N), rj = (uint32_t)clampi(x.rj, N);
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) d.pq[rb] = pq_gather(PQ, ri, rj, rb, g, H);
+    if constexpr (NU > 0) {   // slots past F_E read slot 0 and meet zero columns of W_u
+      const int eid = clampi(x.eid, (int)E);
+      d.u = load_chunk(ef + (int64_t)eid * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
+    }
+  };
+  // an empty asm that names every value of the next sub-tile: the wait for them happens at the end of
+  // a tile, so no load is carried into the loop header incomplete
+  auto complete = [&](const EpGat& d, const EpIdx& x) {
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) asm volatile("" ::"v"(d.pq[rb]));
+    asm volatile("" ::"v"(d.u), "v"(x.ri), "v"(x.rj), "v"(x.eid));
+  };
+
+  auto tile = [&](int64_t T, int par, EpGat& cur, const EpIdx& xn) {
+    // waves 0..3: the rank table of 32-edge tile w (issued first: only these waves load it)
+    const int64_t tw = T * NK + w;
+    int tabv = 0;
+    if (w < NK) tabv = a.tile_tab[(tw < ntt ? tw : ntt - 1) * kTabInts + l];
+    // ---- S1: m1 = SiLU(W_u e + P_i + Q_j), software-pipelined over the row blocks
+    bf16x8 m1c[KH];
+    {
+      bf16x8 fw[2];
+      f32x4 acc[2], y[2];
+      if constexpr (NU > 0) fw[0] = *reinterpret_cast<const bf16x8*>(s_wu + l * 8);
+#pragma unroll
+      for (int rb = 0; rb <= NRB; ++rb) {
+        if (rb < NRB) {
+          if constexpr (NU > 0)
+            if (rb + 1 < NRB) fw[(rb + 1) & 1] = *reinterpret_cast<const bf16x8*>(s_wu + ((rb + 1) * 64 + l) * 8);
+          __builtin_amdgcn_sched_barrier(0);
+          acc[rb & 1] = zero4();
+          if constexpr (NU > 0) mma(acc[rb & 1], fw[rb & 1], cur.u);
+          mma(acc[rb & 1], Ipq, cur.pq[rb]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (rb >= 1) {
+          const int r = rb - 1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[r & 1][i] = silu_t<bf16>(acc[r & 1][i]);
+          if (r & 1) m1c[r >> 1] = pack_chunk<bf16>(y[0], y[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    gather(xn, cur);   // the next tile's
+    // ---- S2: m = SiLU(W_hl^T m1 + b2)
+    bf16x8 mc[KO];
+    {
+      bf16x8 fr[2][KH];
+      f32x4 acc[2], y[2];
+#pragma unroll
+      for (int k = 0; k < KH; ++k) fr[0][k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
+#pragma unroll
+      for (int rb = 0; rb <= NRB; ++rb) {
+        if (rb < NRB) {
+          if (rb + 1 < NRB) {
+#pragma unroll
+            for (int k = 0; k < KH; ++k)
+              fr[(rb + 1) & 1][k] = *reinterpret_cast<const bf16x8*>(s_whlT + (((rb + 1) * KH + k) * 64 + l) * 8);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+          acc[rb & 1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
+#pragma unroll
+          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], fr[rb & 1][k], m1c[k]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if (rb >= 1) {
+          const int r = rb - 1;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) y[r & 1][i] = silu_t<bf16>(acc[r & 1][i]);
+          if (r & 1) mc[r >> 1] = pack_chunk<bf16>(y[0], y[1]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    // ---- the messages, chain chunk (kc, w), and the rank tables, into the buffers of parity par
+    bf16* const sm = s_m[par];
+    const int sl = chain_slot<SW>(l);
+#pragma unroll
+    for (int kc = 0; kc < KO; ++kc) *reinterpret_cast<bf16x8*>(sm + ((kc * NB + w) * 64 + sl) * 8) = mc[kc];
+    if (w < NK) s_tab[par][w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
+    __syncthreads();
+    // ---- per-row sums of rows 16 w .. 16 w + 15 of m over each rank of the four 32-edge tiles
+#pragma unroll
+    for (int eh = 0; eh < NK; ++eh) {
+      const int nrk = __builtin_amdgcn_readfirstlane(s_tab[par][eh][kTabNrank]);
+      if (nrk == 0) continue;
+      const bf16x8 Am = chain_edge_major<NB, SW>(sm, w, c, g, eh);
+      const int64_t tt = T * NK + eh;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        if (16 * q >= nrk) break;
+        const int r = 16 * q + c;
+        f32x4 D = zero4();
+        mma(D, Am, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[par][eh] + kTabSpan)[r] : 0,
+                                  g, s_lut));
+        const int tg = s_tab[par][eh][kTabTgt + r];
+        if (tg >= 0)
+          *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)tg * a.smsg + 16 * w + 4 * g) = pack4(D);
+        else if (tg > -3)
+          *reinterpret_cast<f32x4*>(a.carry + (tt * 2 - 1 - tg) * O + 16 * w + 4 * g) = D;
+      }
+    }
+  };
+
+  EpIdx ix0, ix1;
+  EpGat cur;
+  const int64_t T0 = blockIdx.x;
+  load_idx(T0, ix0);
+  load_idx(T0 + G < NT ? T0 + G : T0, ix1);
+  gather(ix0, cur);
+  complete(cur, ix1);
+  __syncthreads();   // weights in LDS
+  int par = 0;
+  for (int64_t T = T0; T < NT; T += G, par ^= 1) {
+    load_idx(T + 2 * G < NT ? T + 2 * G : T, ix0);
+    tile(T, par, cur, ix1);
+    complete(cur, ix0);
+    ix1 = ix0;
+  }
+}
+
 }  // namespace
+
+int mpnn_ep_blocks(int64_t E) { return (int)std::max<int64_t>(1, std::min<int64_t>((E + kEpTile - 1) / kEpTile, 256)); }
+
+int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st) {
+  if (a.E > 0) {
+    const int nblk = mpnn_ep_blocks(a.E);
+    if (a.FE == 0)
+      hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
+    else
+      hipLaunchKernelGGL((mpnn_fwd_ep_kernel<1>), dim3(nblk), dim3(512), 0, st, a);
+  }
+  return (int)hipGetLastError();
+}
 
 int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st) {
   if (a.E > 0) {
