@@ -121,6 +121,22 @@ def test_mpnn_variant(dtype):
     check_case(Case(rowptr, col, 128, 16, 128, 128, 128, seed=16, eq=False), dtype)
 
 
+@pytest.mark.parametrize("fe,skewed,eids", [(0, True, False), (8, False, True), (16, True, True), (24, True, False),
+                                            (32, False, False)])
+def test_mpnn_edge_parallel_cases(fe, skewed, eids):
+    """The edge-parallel MPNN kernels (bf16, H = 128): every edge-feature width they instantiate (none, one and
+    two 16-slot blocks of the dW_e product), rows across many 128-edge block tiles and 32-edge rank tables,
+    empty rows, a partial last block tile, and edge ids that permute the feature rows."""
+    if skewed:
+        degs = np.array([0, 300, 1, 2, 0, 129, 3, 31, 33, 0, 64, 127, 128, 5, 2, 2, 2, 0, 17] * 6)
+    else:
+        degs = (np.arange(517) * 11) % 37
+    rowptr, col = random_csr(len(degs), degs, seed=61 + fe)
+    perm = np.random.Generator(np.random.PCG64(5)).permutation(len(col)) if eids else None
+    print(f"[mpnn-ep] N={len(degs)} E={len(col)} fe={fe} skewed={skewed} eids={eids}", flush=True)
+    check_case(Case(rowptr, col, 128, fe, 128, 128, 128, seed=22 + fe, eq=False, edge_ids=perm), "bf16")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
 def test_hidden_256(dtype):
     rowptr, col = random_csr(160, np.full(160, 40), seed=31)
@@ -150,7 +166,7 @@ def test_determinism_bitwise():
 
 @pytest.mark.parametrize("dtype,F,FE,H,O,M,eq", [
     ("bf16", 128, 0, 128, 128, 128, True),     # cooperative kernels
-    ("bf16", 128, 16, 128, 128, 128, False),   # MPNN backward with 16 waves
+    ("bf16", 128, 16, 128, 128, 128, False),   # edge-parallel MPNN kernels
     ("bf16", 64, 8, 64, 32, 32, True),         # cooperative kernels, H = 64
     ("bf16", 256, 32, 256, 256, 256, True),    # wide kernels
     ("fp32", 128, 16, 128, 128, 128, True),    # one wave per tile
