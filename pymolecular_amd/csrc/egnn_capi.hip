@@ -496,6 +496,14 @@ int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
     if (!aligned16(p)) return EGNN_ERR_ALIGN;
   hipStream_t st = (hipStream_t)stream;
   ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  if (stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16)) {   // both products in one pass over the rows
+    NodeMlpArgs a{};
+    a.N = s.N; a.K2 = s.K2; a.residual = s.residual;
+    a.x1 = x1; a.ld1 = ld1; a.x2 = x2; a.ld2 = ld2;
+    a.w1 = w1; a.b1 = b1; a.w2 = w2; a.b2 = b2;
+    a.pre = pre; a.act = act; a.out = out; a.ldo = ldo;
+    return hip_status(launch_stream_node_fwd(a, st));
+  }
   {  // pre = [x1 | x2] W1^T + b1 ; act = SiLU(pre)
     Gemm2Args g{};
     g.M = s.N; g.N = s.Hn; g.K = s.K;
@@ -567,7 +575,16 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   s2.ksplit = splitk_len(s2.M, s2.N, s2.K, s.bf16); s2.partial = w.part2;
   const int64_t nsplit1 = cdiv(std::max<int64_t>(s.N, 1), s1.ksplit), nsplit2 = cdiv(std::max<int64_t>(s.N, 1), s2.ksplit);
   if (nsplit1 * s1.M * s1.N > w.part1_elems || nsplit2 * s2.M * s2.N > w.part2_elems) return EGNN_ERR_WORKSPACE;
-  if (s.N > 0) {   // two launches of two independent products each
+  if (s.N > 0 && stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16)) {
+    // dz and grad_x in one pass over the rows, then the two weight-gradient products
+    NodeMlpArgs a{};
+    a.N = s.N; a.K2 = s.K2; a.residual = s.residual;
+    a.w1 = w1; a.w2 = w2; a.pre = const_cast<void*>(pre);
+    a.gout = grad_out; a.ldgo = ldgo; a.dz = w.dz; a.gx = grad_x;
+    if ((rc = hip_status(launch_stream_node_bwd(a, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_gemm2(s2, s.bf16, st))) != EGNN_OK) return rc;
+    if ((rc = hip_status(launch_gemm2(s1, s.bf16, st))) != EGNN_OK) return rc;
+  } else if (s.N > 0) {   // two launches of two independent products each
     if ((rc = hip_status(launch_gemm2_pair(dz, s2, s.bf16, st))) != EGNN_OK) return rc;
     if ((rc = hip_status(launch_gemm2_pair(gx, s1, s.bf16, st))) != EGNN_OK) return rc;
   }

@@ -175,7 +175,235 @@ int launch_stream_t(const Gemm2Args& g, hipStream_t st) {
   return (int)hipGetLastError();
 }
 
+// ---- the node update's MLP in one pass ------------------------------------------------------
+// The first product's epilogue leaves, per 32 hidden features, 8 consecutive features of the lane's row
+// in the lane's registers: exactly the lane's part of the second product's B operand for that k slice.
+// So the second product reads its operand from registers, and the hidden activation is stored once
+// (forward: pre and act, which the backward's weight gradient reads; backward: dz) and never re-read.
+
+// rows of a (R x C) row-major matrix into LDS rows of pitch P
+template <int R, int C, int P, int NT>
+__device__ __forceinline__ void lds_rows(bf16* s, const bf16* g, int64_t ld, int tid) {
+  for (int v = tid; v < R * (C / 8); v += NT) {
+    const int r = v / (C / 8), k = 8 * (v % (C / 8));
+    *reinterpret_cast<bf16x8*>(s + r * P + k) = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + k);
+  }
+}
+// the transpose of a (R x C) row-major matrix into LDS rows of pitch P: s[c][r] = g[r][c]
+template <int R, int C, int P, int NT>
+__device__ __forceinline__ void lds_cols(bf16* s, const bf16* g, int64_t ld, int tid) {
+  for (int v = tid; v < R * (C / 8); v += NT) {
+    const int r = v / (C / 8), c = 8 * (v % (C / 8));
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + c);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s[(c + u) * P + r] = x[u];
+  }
+}
+// acc[nb] += W[stream_feat(nb, c)][32 kc + 8 gq ..] . b[kc] over the KC k slices (W in LDS, k-contiguous,
+// pitch P; wl = stream_feat(0, c) P + 8 gq)
+template <int NB, int KC, int P>
+__device__ __forceinline__ void stream_mm(f32x4 (&acc)[NB], const bf16* s_w, int wl, const bf16x8 (&b)[KC]) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const bf16* wr = s_w + wl + (32 * (nb >> 1) + 4 * (nb & 1)) * P;
+#pragma unroll
+    for (int kc = 0; kc < KC; ++kc) mma(acc[nb], *reinterpret_cast<const bf16x8*>(wr + 32 * kc), b[kc]);
+  }
+}
+// LDS offset of the lane's weight fragments, hidden from the compiler so that it reads them at their use
+// instead of hoisting every fragment of the loop into registers
+template <int P>
+__device__ __forceinline__ int stream_wl(int c, int gq) {
+  int wl = stream_feat(0, c) * P + 8 * gq;
+  asm volatile("" : "+v"(wl));
+  return wl;
+}
+
+constexpr int kNodeHn = 128, kNodeK1 = 128, kNodeWaves = 8;
+
+// forward: pre = [x1 | x2] W1^T + b1, act = SiLU(pre) (of pre's bf16 value), out = act W2^T + b2 (+ x1);
+// one 16-row tile per wave and step, the next tile's rows in flight
+template <int K, bool RES>
+__global__ __launch_bounds__(64 * kNodeWaves, 1) void stream_node_fwd_kernel(NodeMlpArgs a) {
+  constexpr int HN = kNodeHn, FO = kNodeHn, K1 = kNodeK1;
+  constexpr int KC1 = K / 32, NB1 = HN / 16, NQ1 = HN / 32, KC2 = HN / 32, NB2 = FO / 16, NQ2 = FO / 32;
+  constexpr int P1 = K + 8, P2 = HN + 8, NT = 64 * kNodeWaves;
+  __shared__ __attribute__((aligned(16))) bf16 s_w1[HN * P1];   // W1 (Hn x K) as given: k-contiguous
+  __shared__ __attribute__((aligned(16))) bf16 s_w2[FO * P2];   // W2 (Fo x Hn)
+  __shared__ __attribute__((aligned(16))) float s_b1[HN];
+  __shared__ __attribute__((aligned(16))) float s_b2[FO];
+  const int tid = threadIdx.x, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  lds_rows<HN, K, P1, NT>(s_w1, (const bf16*)a.w1, K, tid);
+  lds_rows<FO, HN, P2, NT>(s_w2, (const bf16*)a.w2, HN, tid);
+  for (int n = tid; n < HN; n += NT) s_b1[n] = a.b1 ? (float)((const bf16*)a.b1)[n] : 0.f;
+  for (int n = tid; n < FO; n += NT) s_b2[n] = a.b2 ? (float)((const bf16*)a.b2)[n] : 0.f;
+  __syncthreads();
+
+  const bf16* X1 = (const bf16*)a.x1;
+  const bf16* X2 = (const bf16*)a.x2;
+  const int64_t M = a.N, ntile = (M + 15) / 16, stride = (int64_t)gridDim.x * kNodeWaves;
+  bf16x8 xa[KC1];
+  auto load = [&](int64_t t) {
+    const int64_t m0 = t * 16 + c;
+    const int64_t m = m0 < M ? m0 : M - 1;   // rows past M read the last row and are not stored
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) {
+      const int k = 32 * kc + 8 * gq;
+      const bf16* p = 32 * kc < K1 ? X1 + m * a.ld1 + k : X2 + m * a.ld2 + (k - K1);
+      xa[kc] = *reinterpret_cast<const bf16x8*>(p);
+    }
+  };
+  int64_t t = (int64_t)blockIdx.x * kNodeWaves + wave;
+  if (t < ntile) load(t);
+  for (; t < ntile; t += stride) {
+    bf16x8 x[KC1];
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) x[kc] = xa[kc];
+    if (t + stride < ntile) load(t + stride);
+
+    f32x4 acc[NB1];
+#pragma unroll
+    for (int nb = 0; nb < NB1; ++nb) acc[nb] = *reinterpret_cast<const f32x4*>(s_b1 + stream_feat(nb, 4 * gq));
+    stream_mm<NB1, KC1, P1>(acc, s_w1, stream_wl<P1>(c, gq), x);
+
+    const int64_t m = t * 16 + c;
+    const bool live = m < M;
+    bf16x8 h[NQ1];   // act of hidden features 32 q + 8 gq .. + 7 of row m: the B operand of slice q
+#pragma unroll
+    for (int q = 0; q < NQ1; ++q) {
+      bf16x8 p;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) { p[i] = (bf16)acc[2 * q][i]; p[4 + i] = (bf16)acc[2 * q + 1][i]; }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) h[q][u] = (bf16)silu_t<bf16>((float)p[u]);
+      if (live) {
+        const int64_t o = m * HN + 32 * q + 8 * gq;
+        *reinterpret_cast<bf16x8*>((bf16*)a.pre + o) = p;
+        *reinterpret_cast<bf16x8*>((bf16*)a.act + o) = h[q];
+      }
+    }
+
+    f32x4 acc2[NB2];
+#pragma unroll
+    for (int nb = 0; nb < NB2; ++nb) acc2[nb] = *reinterpret_cast<const f32x4*>(s_b2 + stream_feat(nb, 4 * gq));
+    stream_mm<NB2, KC2, P2>(acc2, s_w2, stream_wl<P2>(c, gq), h);
+    if (!live) continue;
+#pragma unroll
+    for (int q = 0; q < NQ2; ++q) {
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo = acc2[2 * q][i], hi = acc2[2 * q + 1][i];
+        if constexpr (RES) { lo += (float)x[q][i]; hi += (float)x[q][4 + i]; }   // x1 = the first K1 features
+        o[i] = (bf16)lo; o[4 + i] = (bf16)hi;
+      }
+      *reinterpret_cast<bf16x8*>((bf16*)a.out + m * a.ldo + 32 * q + 8 * gq) = o;
+    }
+  }
+}
+
+// backward data gradients: dz = (gout W2) * SiLU'(pre), gx = dz W1 (+ gout on the first K1 columns)
+template <int K, bool RES>
+__global__ __launch_bounds__(64 * kNodeWaves, 1) void stream_node_bwd_kernel(NodeMlpArgs a) {
+  constexpr int HN = kNodeHn, FO = kNodeHn, K1 = kNodeK1;
+  constexpr int KC1 = FO / 32, NB1 = HN / 16, NQ1 = HN / 32, KC2 = HN / 32, NB2 = K / 16, NQ2 = K / 32;
+  constexpr int P1 = FO + 8, P2 = HN + 8, NT = 64 * kNodeWaves;
+  __shared__ __attribute__((aligned(16))) bf16 s_w2t[HN * P1];   // s_w2t[n][k] = W2[k][n]
+  __shared__ __attribute__((aligned(16))) bf16 s_w1t[K * P2];    // s_w1t[n][k] = W1[k][n]
+  const int tid = threadIdx.x, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  lds_cols<FO, HN, P1, NT>(s_w2t, (const bf16*)a.w2, HN, tid);
+  lds_cols<HN, K, P2, NT>(s_w1t, (const bf16*)a.w1, K, tid);
+  __syncthreads();
+
+  const bf16* G = (const bf16*)a.gout;
+  const bf16* Z = (const bf16*)a.pre;
+  const int64_t M = a.N, ntile = (M + 15) / 16, stride = (int64_t)gridDim.x * kNodeWaves;
+  bf16x8 ga[KC1], za[NQ1];
+  auto load = [&](int64_t t) {
+    const int64_t m0 = t * 16 + c;
+    const int64_t m = m0 < M ? m0 : M - 1;
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) ga[kc] = *reinterpret_cast<const bf16x8*>(G + m * a.ldgo + 32 * kc + 8 * gq);
+#pragma unroll
+    for (int q = 0; q < NQ1; ++q) za[q] = *reinterpret_cast<const bf16x8*>(Z + m * HN + 32 * q + 8 * gq);
+  };
+  int64_t t = (int64_t)blockIdx.x * kNodeWaves + wave;
+  if (t < ntile) load(t);
+  for (; t < ntile; t += stride) {
+    bf16x8 g[KC1], z[NQ1];
+#pragma unroll
+    for (int kc = 0; kc < KC1; ++kc) g[kc] = ga[kc];
+#pragma unroll
+    for (int q = 0; q < NQ1; ++q) z[q] = za[q];
+    if (t + stride < ntile) load(t + stride);
+
+    f32x4 acc[NB1];
+#pragma unroll
+    for (int nb = 0; nb < NB1; ++nb) acc[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    stream_mm<NB1, KC1, P1>(acc, s_w2t, stream_wl<P1>(c, gq), g);
+
+    const int64_t m = t * 16 + c;
+    const bool live = m < M;
+    bf16x8 h[NQ1];   // dz of hidden features 32 q + 8 gq .. + 7 of row m
+#pragma unroll
+    for (int q = 0; q < NQ1; ++q) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h[q][i] = (bf16)(acc[2 * q][i] * silu_yd<bf16>((float)z[q][i]).d);
+        h[q][4 + i] = (bf16)(acc[2 * q + 1][i] * silu_yd<bf16>((float)z[q][4 + i]).d);
+      }
+      if (live) *reinterpret_cast<bf16x8*>((bf16*)a.dz + m * HN + 32 * q + 8 * gq) = h[q];
+    }
+
+    f32x4 acc2[NB2];
+#pragma unroll
+    for (int nb = 0; nb < NB2; ++nb) acc2[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    stream_mm<NB2, KC2, P2>(acc2, s_w1t, stream_wl<P2>(c, gq), h);
+    if (!live) continue;
+#pragma unroll
+    for (int q = 0; q < NQ2; ++q) {
+      bf16x8 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float lo = acc2[2 * q][i], hi = acc2[2 * q + 1][i];
+        if (RES && 32 * q < K1) { lo += (float)g[q % KC1][i]; hi += (float)g[q % KC1][4 + i]; }
+        o[i] = (bf16)lo; o[4 + i] = (bf16)hi;
+      }
+      *reinterpret_cast<bf16x8*>((bf16*)a.gx + m * K + 32 * q + 8 * gq) = o;
+    }
+  }
+}
+
+template <int K>
+int launch_node_fwd_t(const NodeMlpArgs& a, hipStream_t st) {
+  const int blocks = (int)std::min<int64_t>(cdiv(cdiv(a.N, 16), kNodeWaves), 256);   // one block per CU, persistent
+  if (a.residual) hipLaunchKernelGGL((stream_node_fwd_kernel<K, true>), dim3(blocks), dim3(64 * kNodeWaves), 0, st, a);
+  else hipLaunchKernelGGL((stream_node_fwd_kernel<K, false>), dim3(blocks), dim3(64 * kNodeWaves), 0, st, a);
+  return (int)hipGetLastError();
+}
+template <int K>
+int launch_node_bwd_t(const NodeMlpArgs& a, hipStream_t st) {
+  const int blocks = (int)std::min<int64_t>(cdiv(cdiv(a.N, 16), kNodeWaves), 256);
+  if (a.residual) hipLaunchKernelGGL((stream_node_bwd_kernel<K, true>), dim3(blocks), dim3(64 * kNodeWaves), 0, st, a);
+  else hipLaunchKernelGGL((stream_node_bwd_kernel<K, false>), dim3(blocks), dim3(64 * kNodeWaves), 0, st, a);
+  return (int)hipGetLastError();
+}
+
 }  // namespace
+
+bool stream_node_ok(int64_t N, int K1, int K2, int Hn, int Fo, bool bf16) {
+  return bf16 && N >= kStreamMinRows && K1 == kNodeK1 && (K2 == 0 || K2 == kNodeK1) && Hn == kNodeHn && Fo == kNodeHn;
+}
+
+int launch_stream_node_fwd(const NodeMlpArgs& a, hipStream_t st) {
+  return a.K2 ? launch_node_fwd_t<kNodeK1 + kNodeK1>(a, st) : launch_node_fwd_t<kNodeK1>(a, st);
+}
+
+int launch_stream_node_bwd(const NodeMlpArgs& a, hipStream_t st) {
+  return a.K2 ? launch_node_bwd_t<kNodeK1 + kNodeK1>(a, st) : launch_node_bwd_t<kNodeK1>(a, st);
+}
 
 bool stream_gemm_ok(const Gemm2Args& g, bool compute_bf16) {
   auto al = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 8 == 0); };

@@ -56,11 +56,16 @@ def test_node_update_matches_reference(dtype, tol, N, K1, K2, Hn, Fo, residual, 
     assert not bad, bad
 
 
-def test_node_update_large_bf16():
-    # 300,001 nodes (a partial last 16-row tile): the streaming node products (one pass over the rows,
-    # weights in LDS; bias, SiLU with the stored pre-activation, SiLU', residual epilogues) and long
-    # split-K slices
-    test_node_update_matches_reference(torch.bfloat16, 2e-2, 300001, 128, 128, 128, 128, True, True)
+@pytest.mark.parametrize("N,K2,residual,bias", [
+    (300001, 128, True, True),    # the power-law layer's node update, a partial last 16-row tile
+    (70001, 0, False, False),     # one input, no residual, no bias
+    (65541, 128, False, True),    # just above the streaming threshold, no residual
+])
+def test_node_update_large_bf16(N, K2, residual, bias):
+    # at 65,536 rows or more with K1 = Hn = Fo = 128 both products of each direction run in one streaming
+    # pass (weights in LDS, the hidden activation handed from the first product to the second in
+    # registers), followed by long split-K slices for the weight gradients
+    test_node_update_matches_reference(torch.bfloat16, 2e-2, N, 128, K2, 128, 128, residual, bias)
 
 
 def test_node_update_deterministic_and_empty():
