@@ -415,17 +415,18 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // forward of the MPNN layer, edge-parallel (bf16, H = O = 128)
 // ---------------------------------------------------------------------------
-// The same organisation as the backward: eight waves per CU, each runs S1 (pre1 = W_u e + P_i +
+// The same organisation as the backward: blocks of eight waves, each runs S1 (pre1 = W_u e + P_i +
 // Q_j, m1 = SiLU(pre1)) and S2 (m = SiLU(W_hl^T m1 + b2)) for its own 16 edges in registers, the W_u
 // and W_hl^T fragments read from LDS as whole 16-byte fragments, each stage software-pipelined over
-// its row blocks.  The messages m go chain-ordered into an LDS buffer of the 128-edge block tile (by
-// tile parity, so one barrier per tile); after the barrier wave w sums the rows 16 w .. 16 w + 15 of
+// its row blocks.  Two blocks share a CU (77 KB of LDS each, 96 VGPRs per wave), so that while one
+// block waits at a barrier the other's gathers and products go on.  The messages m go chain-ordered
+// into an LDS buffer of the 128-edge block tile; after a barrier wave w sums the rows 16 w .. 16 w + 15 of
 // m over each row run of the four 32-edge tiles: one MFMA per 16 ranks against the 0/1 segment
 // matrix from the schedule's rank tables, a run that is a whole row stored to out_msg, a partial
 // first / last run to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).
 // Reference: forward_kernel.py:89-153 computes the same per-row sums one program per CSR row.
 template <int NU>
-__global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
+__global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8, KH = H / 32, KO = O / 32;
   constexpr int NB = kEpWaves;                  // 16-edge blocks of a block tile
   constexpr int NK = kEpTile / 32;              // 32-edge tiles of a block tile
@@ -434,8 +435,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A = W_hl^T, S2
   __shared__ __attribute__((aligned(16))) bf16 s_wu[NU > 0 ? NRB * kFragElems : 8];   // A = W_u, S1
   __shared__ __attribute__((aligned(16))) float s_b2[O];
-  __shared__ __attribute__((aligned(16))) bf16 s_m[2][CHB];                     // messages, by tile parity
-  __shared__ int s_tab[2][NK][kTabInts];                                      // rank tables, by tile parity
+  __shared__ __attribute__((aligned(16))) bf16 s_m[CHB];                        // messages of the block tile
+  __shared__ int s_tab[NK][kTabInts];                                         // rank tables of the block tile
   __shared__ uint2 s_lut[16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
@@ -482,7 +483,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
     asm volatile("" ::"v"(d.u), "v"(x.ri), "v"(x.rj), "v"(x.eid));
   };
 
-  auto tile = [&](int64_t T, int par, EpGat& cur, const EpIdx& xn) {
+  auto tile = [&](int64_t T, EpGat& cur, const EpIdx& xn) {
     // waves 0..3: the rank table of 32-edge tile w (issued first: only these waves load it)
     const int64_t tw = T * NK + w;
     int tabv = 0;
@@ -517,22 +518,24 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
     // ---- S2: m = SiLU(W_hl^T m1 + b2)
     bf16x8 mc[KO];
     {
-      bf16x8 fr[2][KH];
+      // one set of fragment registers: those of row block rb + 1 are requested once the products of rb
+      // have read theirs, and arrive during the elementwise work of rb - 1
+      bf16x8 fr[KH];
       f32x4 acc[2], y[2];
 #pragma unroll
-      for (int k = 0; k < KH; ++k) fr[0][k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
+      for (int k = 0; k < KH; ++k) fr[k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
 #pragma unroll
       for (int rb = 0; rb <= NRB; ++rb) {
         if (rb < NRB) {
+          acc[rb & 1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
+#pragma unroll
+          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], fr[k], m1c[k]);
+          __builtin_amdgcn_sched_barrier(0);
           if (rb + 1 < NRB) {
 #pragma unroll
             for (int k = 0; k < KH; ++k)
-              fr[(rb + 1) & 1][k] = *reinterpret_cast<const bf16x8*>(s_whlT + (((rb + 1) * KH + k) * 64 + l) * 8);
+              fr[k] = *reinterpret_cast<const bf16x8*>(s_whlT + (((rb + 1) * KH + k) * 64 + l) * 8);
           }
-          __builtin_amdgcn_sched_barrier(0);
-          acc[rb & 1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
-#pragma unroll
-          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], fr[rb & 1][k], m1c[k]);
           __builtin_amdgcn_sched_barrier(0);
         }
         if (rb >= 1) {
@@ -544,17 +547,19 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
         }
       }
     }
-    // ---- the messages, chain chunk (kc, w), and the rank tables, into the buffers of parity par
-    bf16* const sm = s_m[par];
+    // ---- the messages, chain chunk (kc, w), and the rank tables, into the block tile's buffers once every
+    // wave has read the previous tile's
+    __syncthreads();
+    bf16* const sm = s_m;
     const int sl = chain_slot<SW>(l);
 #pragma unroll
     for (int kc = 0; kc < KO; ++kc) *reinterpret_cast<bf16x8*>(sm + ((kc * NB + w) * 64 + sl) * 8) = mc[kc];
-    if (w < NK) s_tab[par][w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
+    if (w < NK) s_tab[w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
     __syncthreads();
     // ---- per-row sums of rows 16 w .. 16 w + 15 of m over each rank of the four 32-edge tiles
 #pragma unroll
     for (int eh = 0; eh < NK; ++eh) {
-      const int nrk = __builtin_amdgcn_readfirstlane(s_tab[par][eh][kTabNrank]);
+      const int nrk = __builtin_amdgcn_readfirstlane(s_tab[eh][kTabNrank]);
       if (nrk == 0) continue;
       const bf16x8 Am = chain_edge_major<NB, SW>(sm, w, c, g, eh);
       const int64_t tt = T * NK + eh;
@@ -563,9 +568,9 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
         if (16 * q >= nrk) break;
         const int r = 16 * q + c;
         f32x4 D = zero4();
-        mma(D, Am, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[par][eh] + kTabSpan)[r] : 0,
+        mma(D, Am, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[eh] + kTabSpan)[r] : 0,
                                   g, s_lut));
-        const int tg = s_tab[par][eh][kTabTgt + r];
+        const int tg = s_tab[eh][kTabTgt + r];
         if (tg >= 0)
           *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)tg * a.smsg + 16 * w + 4 * g) = pack4(D);
         else if (tg > -3)
@@ -582,10 +587,9 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
   gather(ix0, cur);
   complete(cur, ix1);
   __syncthreads();   // weights in LDS
-  int par = 0;
-  for (int64_t T = T0; T < NT; T += G, par ^= 1) {
+  for (int64_t T = T0; T < NT; T += G) {
     load_idx(T + 2 * G < NT ? T + 2 * G : T, ix0);
-    tile(T, par, cur, ix1);
+    tile(T, cur, ix1);
     complete(cur, ix0);
     ix1 = ix0;
   }
@@ -596,8 +600,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_fwd_ep_kernel(FwdArgs a) {
 int mpnn_ep_blocks(int64_t E) { return (int)std::max<int64_t>(1, std::min<int64_t>((E + kEpTile - 1) / kEpTile, 256)); }
 
 int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st) {
-  if (a.E > 0) {
-    const int nblk = mpnn_ep_blocks(a.E);
+  if (a.E > 0) {   // two blocks per CU
+    const int nblk = (int)std::max<int64_t>(1, std::min<int64_t>((a.E + kEpTile - 1) / kEpTile, 2 * 256));
     if (a.FE == 0)
       hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
     else
