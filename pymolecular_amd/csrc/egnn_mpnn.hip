@@ -415,28 +415,24 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // forward of the MPNN layer, edge-parallel (bf16, H = O = 128)
 // ---------------------------------------------------------------------------
-// The same organisation as the backward: blocks of eight waves, each runs S1 (pre1 = W_u e + P_i +
-// Q_j, m1 = SiLU(pre1)) and S2 (m = SiLU(W_hl^T m1 + b2)) for its own 16 edges in registers, the W_u
-// and W_hl^T fragments read from LDS as whole 16-byte fragments, each stage software-pipelined over
-// its row blocks.  Two blocks share a CU (77 KB of LDS each, 96 VGPRs per wave), so that while one
-// block waits at a barrier the other's gathers and products go on.  The messages m go chain-ordered
-// into an LDS buffer of the 128-edge block tile; after a barrier wave w sums the rows 16 w .. 16 w + 15 of
-// m over each row run of the four 32-edge tiles: one MFMA per 16 ranks against the 0/1 segment
-// matrix from the schedule's rank tables, a run that is a whole row stored to out_msg, a partial
-// first / last run to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).
+// Each wave takes whole 32-edge schedule tiles, one 16-edge half at a time.  S1 (pre1 = W_u e + P_i
+// + Q_j, m1 = SiLU(pre1)) is computed with the features on the MFMA rows, so that its C-blocks are
+// S2's operand; S2 (m = SiLU(m1 W_hl + b2)) with the edges on the rows, so that a lane's C-block of
+// feature block rb holds four edges of one feature.  The first half's messages wait in registers
+// (bf16); with the second half's they form, per feature block, the A operand (16 features x the
+// tile's 32 edges) of the per-row sums: one MFMA per 16 ranks against the 0/1 segment matrix from
+// the schedule's rank table, a rank that is a whole row stored to out_msg, a partial first / last
+// rank to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).  No LDS exchange
+// and no barrier after the weight copy: the waves run independently, two blocks of eight per CU.
 // Reference: forward_kernel.py:89-153 computes the same per-row sums one program per CSR row.
 template <int NU>
 __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
-  constexpr int H = 128, O = 128, NRB = 8, KH = H / 32, KO = O / 32;
-  constexpr int NB = kEpWaves;                  // 16-edge blocks of a block tile
-  constexpr int NK = kEpTile / 32;              // 32-edge tiles of a block tile
-  constexpr int CHB = KO * NB * 64 * 8;         // one chain buffer: 4 chunks x 8 edge blocks (32 KB)
-  constexpr bool SW = true;
-  __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A = W_hl^T, S2
+  constexpr int H = 128, O = 128, NRB = 8, KH = H / 32;
+  __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // W_hl fragments, S2
   __shared__ __attribute__((aligned(16))) bf16 s_wu[NU > 0 ? NRB * kFragElems : 8];   // A = W_u, S1
   __shared__ __attribute__((aligned(16))) float s_b2[O];
-  __shared__ __attribute__((aligned(16))) bf16 s_m[CHB];                        // messages of the block tile
-  __shared__ int s_tab[NK][kTabInts];                                         // rank tables of the block tile
+  __shared__ __attribute__((aligned(16))) bf16x4 s_m0[kEpWaves][NRB][64];   // each wave's first-half messages
+  __shared__ __attribute__((aligned(16))) bf16x8 s_ipq[64];   // pq_sum_chunk of each lane
   __shared__ uint2 s_lut[16];
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
@@ -446,9 +442,8 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   const uint32_t E = (uint32_t)a.E;
   const int N = (int)a.N;
   const int FE = a.FE;
-  const int64_t NT = (a.E + kEpTile - 1) / kEpTile;
   const int64_t ntt = (a.E + 31) / 32;
-  const int64_t G = gridDim.x;
+  const int64_t GW = (int64_t)gridDim.x * kEpWaves;   // waves of the grid: the tile stride
   const bool use_eids = a.eids != nullptr;
 
   for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 512)
@@ -457,10 +452,10 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     for (int q = threadIdx.x; q < NRB * kFragElems / 8; q += 512)
       reinterpret_cast<bf16x8*>(s_wu)[q] = reinterpret_cast<const bf16x8*>(a.fr.u)[q];
   for (int q = threadIdx.x; q < O; q += 512) s_b2[q] = a.fr.b2f[q];
-  const bf16x8 Ipq = pq_sum_chunk(c, g);
+  if (threadIdx.x < 64) s_ipq[l] = pq_sum_chunk(c, g);
 
-  auto load_idx = [&](int64_t T, EpIdx& x) {   // E < 2^31 (coop_supported)
-    const uint32_t e0 = (uint32_t)T * kEpTile + 16 * w + c;
+  auto load_idx = [&](int64_t T, int h, EpIdx& x) {   // E < 2^31 (coop_supported)
+    const uint32_t e0 = (uint32_t)T * 32 + 16 * h + c;
     const uint32_t e = e0 < E ? e0 : E - 1;
     x.ri = a.erow[e];
     x.rj = a.col[e];
@@ -475,22 +470,24 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       d.u = load_chunk(ef + (int64_t)eid * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
     }
   };
-  // an empty asm that names every value of the next sub-tile: the wait for them happens at the end of
-  // a tile, so no load is carried into the loop header incomplete
+  // an empty asm that names every value of the next half: the wait for them happens at the end of a
+  // half, so no load is carried into the next one incomplete
   auto complete = [&](const EpGat& d, const EpIdx& x) {
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) asm volatile("" ::"v"(d.pq[rb]));
     asm volatile("" ::"v"(d.u), "v"(x.ri), "v"(x.rj), "v"(x.eid));
   };
 
-  auto tile = [&](int64_t T, EpGat& cur, const EpIdx& xn) {
-    // waves 0..3: the rank table of 32-edge tile w (issued first: only these waves load it)
-    const int64_t tw = T * NK + w;
-    int tabv = 0;
-    if (w < NK) tabv = a.tile_tab[(tw < ntt ? tw : ntt - 1) * kTabInts + l];
-    // ---- S1: m1 = SiLU(W_u e + P_i + Q_j), software-pipelined over the row blocks
+  // One 16-edge half HC of tile T: S1 on cur, then the gathers of the half after next into cur, then S2.
+  // The first half leaves its messages in the wave's LDS slots; the second half sums both over the
+  // tile's ranks (a wave reads only what it wrote: no barrier).
+  bf16x4* const m0 = &s_m0[w][0][l];
+  auto half = [&](auto hc, int64_t T, EpGat& cur, const EpIdx& xn, int tabv) {
+    constexpr int HC = decltype(hc)::value;
+    // ---- S1: m1 = SiLU(W_u e + P_i + Q_j) (features on the rows), software-pipelined over the row blocks
     bf16x8 m1c[KH];
     {
+      const bf16x8 Ipq = s_ipq[l];
       bf16x8 fw[2];
       f32x4 acc[2], y[2];
       if constexpr (NU > 0) fw[0] = *reinterpret_cast<const bf16x8*>(s_wu + l * 8);
@@ -514,22 +511,36 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
         }
       }
     }
-    gather(xn, cur);   // the next tile's
-    // ---- S2: m = SiLU(W_hl^T m1 + b2)
-    bf16x8 mc[KO];
+    gather(xn, cur);
+    // ---- the tile's rank table (second half): lane (g, c) handles ranks c and 16 + c; the segment
+    // operand of ranks 16 .. 31 (tiles of more than 16 rows) is rebuilt where it is used
+    int nrk = 0, tg[2] = {-3, -3}, span[2] = {0, 0};
+    bf16x8 sq0;
+    if constexpr (HC == 1) {
+      nrk = __builtin_amdgcn_readlane(tabv, kTabNrank);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int r = 16 * q + c;
+        tg[q] = __shfl(tabv, kTabTgt + r, 64);
+        const int sp = __shfl(tabv, kTabSpan + (r >> 1), 64);
+        span[q] = r < nrk ? (sp >> (16 * (r & 1))) & 0xffff : 0;
+      }
+      sq0 = seg_chunk_span(span[0], g, s_lut);
+    }
+    // ---- S2: m = SiLU(m1 W_hl + b2) (edges on the rows); W_hl fragments of block rb + 1 requested once the
+    // products of rb have read theirs
     {
-      // one set of fragment registers: those of row block rb + 1 are requested once the products of rb
-      // have read theirs, and arrive during the elementwise work of rb - 1
       bf16x8 fr[KH];
-      f32x4 acc[2], y[2];
+      f32x4 acc[2];
 #pragma unroll
       for (int k = 0; k < KH; ++k) fr[k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
 #pragma unroll
       for (int rb = 0; rb <= NRB; ++rb) {
         if (rb < NRB) {
-          acc[rb & 1] = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
+          const float b = s_b2[16 * rb + c];
+          acc[rb & 1] = f32x4{b, b, b, b};
 #pragma unroll
-          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], fr[k], m1c[k]);
+          for (int k = 0; k < KH; ++k) mma(acc[rb & 1], m1c[k], fr[k]);
           __builtin_amdgcn_sched_barrier(0);
           if (rb + 1 < NRB) {
 #pragma unroll
@@ -540,58 +551,53 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
         }
         if (rb >= 1) {
           const int r = rb - 1;
+          f32x4 y;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) y[r & 1][i] = silu_t<bf16>(acc[r & 1][i]);
-          if (r & 1) mc[r >> 1] = pack_chunk<bf16>(y[0], y[1]);
+          for (int i = 0; i < 4; ++i) y[i] = silu_t<bf16>(acc[r & 1][i]);
+          const bf16x4 mr = pack4(y);   // edges 4g .. 4g + 3 of this half, feature 16 r + c
+          if constexpr (HC == 0) {
+            m0[64 * r] = mr;
+          } else {
+            // rows 16 r .. 16 r + 15 of m over the tile's 32 edges in kappa_chain order
+            const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mr, 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+              if (16 * q >= nrk) break;
+              f32x4 D = zero4();
+              mma(D, Am, q == 0 ? sq0 : seg_chunk_span(span[1], g, s_lut));
+              if (tg[q] >= 0)
+                *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)tg[q] * a.smsg + 16 * r + 4 * g) = pack4(D);
+              else if (tg[q] > -3)
+                *reinterpret_cast<f32x4*>(a.carry + (T * 2 - 1 - tg[q]) * O + 16 * r + 4 * g) = D;
+            }
+          }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
-    // ---- the messages, chain chunk (kc, w), and the rank tables, into the block tile's buffers once every
-    // wave has read the previous tile's
-    __syncthreads();
-    bf16* const sm = s_m;
-    const int sl = chain_slot<SW>(l);
-#pragma unroll
-    for (int kc = 0; kc < KO; ++kc) *reinterpret_cast<bf16x8*>(sm + ((kc * NB + w) * 64 + sl) * 8) = mc[kc];
-    if (w < NK) s_tab[w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
-    __syncthreads();
-    // ---- per-row sums of rows 16 w .. 16 w + 15 of m over each rank of the four 32-edge tiles
-#pragma unroll
-    for (int eh = 0; eh < NK; ++eh) {
-      const int nrk = __builtin_amdgcn_readfirstlane(s_tab[eh][kTabNrank]);
-      if (nrk == 0) continue;
-      const bf16x8 Am = chain_edge_major<NB, SW>(sm, w, c, g, eh);
-      const int64_t tt = T * NK + eh;
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        if (16 * q >= nrk) break;
-        const int r = 16 * q + c;
-        f32x4 D = zero4();
-        mma(D, Am, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[eh] + kTabSpan)[r] : 0,
-                                  g, s_lut));
-        const int tg = s_tab[eh][kTabTgt + r];
-        if (tg >= 0)
-          *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)tg * a.smsg + 16 * w + 4 * g) = pack4(D);
-        else if (tg > -3)
-          *reinterpret_cast<f32x4*>(a.carry + (tt * 2 - 1 - tg) * O + 16 * w + 4 * g) = D;
-      }
-    }
   };
 
-  EpIdx ix0, ix1;
+  const int64_t T0 = (int64_t)blockIdx.x * kEpWaves + w;
+  const bool active = T0 < ntt;
+  EpIdx ixa, ixb;
   EpGat cur;
-  const int64_t T0 = blockIdx.x;
-  load_idx(T0, ix0);
-  load_idx(T0 + G < NT ? T0 + G : T0, ix1);
-  gather(ix0, cur);
-  complete(cur, ix1);
+  if (active) {
+    load_idx(T0, 0, ixa);
+    gather(ixa, cur);
+    load_idx(T0, 1, ixa);
+    complete(cur, ixa);
+  }
   __syncthreads();   // weights in LDS
-  for (int64_t T = T0; T < NT; T += G) {
-    load_idx(T + 2 * G < NT ? T + 2 * G : T, ix0);
-    tile(T, cur, ix1);
-    complete(cur, ix0);
-    ix1 = ix0;
+  if (!active) return;
+  for (int64_t T = T0; T < ntt; T += GW) {
+    const int64_t Tn = T + GW < ntt ? T + GW : T;
+    const int tabv = a.tile_tab[T * kTabInts + l];
+    load_idx(Tn, 0, ixb);
+    half(std::integral_constant<int, 0>{}, T, cur, ixa, tabv);   // gathers (T, 1)
+    complete(cur, ixb);
+    load_idx(Tn, 1, ixa);
+    half(std::integral_constant<int, 1>{}, T, cur, ixb, tabv);   // gathers (Tn, 0)
+    complete(cur, ixa);
   }
 }
 
@@ -600,8 +606,8 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
 int mpnn_ep_blocks(int64_t E) { return (int)std::max<int64_t>(1, std::min<int64_t>((E + kEpTile - 1) / kEpTile, 256)); }
 
 int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st) {
-  if (a.E > 0) {   // two blocks per CU
-    const int nblk = (int)std::max<int64_t>(1, std::min<int64_t>((a.E + kEpTile - 1) / kEpTile, 2 * 256));
+  if (a.E > 0) {   // eight 32-edge tiles per block at a time, two blocks per CU
+    const int nblk = (int)std::max<int64_t>(1, std::min<int64_t>((a.E + 8 * 32 - 1) / (8 * 32), 2 * 256));
     if (a.FE == 0)
       hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
     else
