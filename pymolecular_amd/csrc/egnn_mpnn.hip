@@ -90,7 +90,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   // wave 0..3), and the 0/1 patterns of the segment matrix
   __shared__ int s_tab[kEpTile / 32][kTabInts];
   __shared__ uint2 s_lut[16];
-  __shared__ __attribute__((aligned(16))) bf16 s_u[NUS * kEpTile];              // [slot][128 edges, kappa order]
+  constexpr int UP = kEpTile + 8;               // row pitch of s_u: 16-byte row offsets spread the dW_e reads over the banks
+  __shared__ __attribute__((aligned(16))) bf16 s_u[NUS * UP];                   // [slot][128 edges, kappa order]
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   seg_lut_init(s_lut, threadIdx.x);
@@ -123,7 +124,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   for (int q = threadIdx.x; q < O; q += 512) s_b2[q] = a.fr.b2f[q];
   // slot rows at and past F_E stay zero (the tiles write rows below F_E only)
   if constexpr (NU > 0)
-    for (int q = FE * kEpTile + (int)threadIdx.x; q < NUS * kEpTile; q += 512) s_u[q] = (bf16)0.0f;
+    for (int q = FE * UP + (int)threadIdx.x; q < NUS * UP; q += 512) s_u[q] = (bf16)0.0f;
   const bf16* const Wr = wrow_base(s_whl, c, g);
   const bf16* const Wc = wcol_base(s_whl, c, g);
   const bf16x8 Ipq = pq_sum_chunk(c, g);
@@ -307,9 +308,9 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
     }
     if constexpr (NU > 0) {
       if (8 * g < FE) {   // edge 16 (w & 1) + c of K-chunk w >> 1 at position 8 (c >> 2) + 4 (w & 1) + (c & 3)
-        bf16* p = s_u + 8 * g * kEpTile + 32 * (w >> 1) + 8 * (c >> 2) + 4 * (w & 1) + (c & 3);
+        bf16* p = s_u + 8 * g * UP + 32 * (w >> 1) + 8 * (c >> 2) + 4 * (w & 1) + (c & 3);
 #pragma unroll
-        for (int s = 0; s < 8; ++s) p[s * kEpTile] = cur.u[s];
+        for (int s = 0; s < 8; ++s) p[s * UP] = cur.u[s];
       }
     }
     gather_u(xn, cur);   // the next tile's
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 #pragma unroll
           for (int ub = 0; ub < NU; ++ub) {
             if (16 * ub >= FE) continue;   // column block past the edge features
-            mma(acc_we[ub], Ag, *reinterpret_cast<const bf16x8*>(s_u + (16 * ub + c) * kEpTile + 32 * eh + 8 * g));
+            mma(acc_we[ub], Ag, *reinterpret_cast<const bf16x8*>(s_u + (16 * ub + c) * UP + 32 * eh + 8 * g));
           }
         }
         // destination sums of 32-edge tile eh: D = g_a1 S against its 0/1 segment matrix; a rank that
