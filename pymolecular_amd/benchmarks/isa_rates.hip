@@ -32,7 +32,9 @@ __global__ __launch_bounds__(256) void valu_kernel(float* out, float seed) {
   if (OP == 3) asm volatile("v_cvt_pk_bf16_f32 %0, %0, %0" : "+v"(a));                         \
   if (OP == 4) asm volatile("v_pk_add_f16 %0, %0, %0" : "+v"(a));                              \
   if (OP == 5) asm volatile("v_dot2_f32_bf16 %0, %0, %0, %0" : "+v"(a));                       \
-  if (OP == 6) asm volatile("v_fma_mix_f32 %0, %0, %0, %0 op_sel_hi:[1,1,0]" : "+v"(a));
+  if (OP == 6) asm volatile("v_fma_mix_f32 %0, %0, %0, %0 op_sel_hi:[1,1,0]" : "+v"(a));        \
+  if (OP == 7) asm volatile("v_exp_f16 %0, %0" : "+v"(a));                                     \
+  if (OP == 8) asm volatile("v_rcp_f16 %0, %0" : "+v"(a));
     VOP(a0) VOP(a1) VOP(a2) VOP(a3) VOP(a4) VOP(a5) VOP(a6) VOP(a7)
 #undef VOP
   }
@@ -130,9 +132,9 @@ int main() {
   auto per_simd = [&](double ms, int wps, double instr_per_wave) { return ms * 1e-3 * clk / (wps * instr_per_wave); };
   printf("{\"test\": \"clock\", \"ghz\": %.1f}\n", clk / 1e9);
   const char* vname[] = {"v_add_f32", "v_exp_f32", "v_rcp_f32", "v_cvt_pk_bf16_f32", "v_pk_add_f16", "v_dot2_f32_bf16",
-                         "v_fma_mix_f32"};
+                         "v_fma_mix_f32", "v_exp_f16", "v_rcp_f16"};
   for (int wps : {1, 2, 4}) {
-    for (int op = 0; op < 7; ++op) {
+    for (int op = 0; op < 9; ++op) {
       const int blocks = 256 * wps;
       double ms = -1.0;
       switch (op) {
@@ -142,7 +144,9 @@ int main() {
         case 3: ms = time_ms([&] { valu_kernel<3><<<blocks, 256>>>(out, 0.5f); }); break;
         case 4: ms = time_ms([&] { valu_kernel<4><<<blocks, 256>>>(out, 0.5f); }); break;
         case 5: ms = time_ms([&] { valu_kernel<5><<<blocks, 256>>>(out, 0.5f); }); break;
-        default: ms = time_ms([&] { valu_kernel<6><<<blocks, 256>>>(out, 0.5f); }); break;
+        case 6: ms = time_ms([&] { valu_kernel<6><<<blocks, 256>>>(out, 0.5f); }); break;
+        case 7: ms = time_ms([&] { valu_kernel<7><<<blocks, 256>>>(out, 0.5f); }); break;
+        default: ms = time_ms([&] { valu_kernel<8><<<blocks, 256>>>(out, 0.5f); }); break;
       }
       printf("{\"test\": \"valu\", \"op\": \"%s\", \"waves_per_simd\": %d, \"cycles_per_instr\": %.2f}\n", vname[op], wps,
              per_simd(ms, wps, 8.0 * IT));
