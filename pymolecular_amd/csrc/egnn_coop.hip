@@ -1618,7 +1618,8 @@ int64_t coop_dw_len(const LayerShape& s) {
 
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
   if (s.probe) return launch_fwd_t<128, 128, 128, 8, false, true>(a, st);   // make_shape: MPNN, H = 128
-  if (mpnn_ep(s)) return launch_mpnn_fwd_ep(a, st);
+  // the edge-parallel forward addresses the message rows by 32-bit byte offsets
+  if (mpnn_ep(s) && s.N * a.smsg * 2 < (int64_t(1) << 31)) return launch_mpnn_fwd_ep(a, st);
   if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }

@@ -431,7 +431,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8, KH = H / 32;
   __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // W_hl fragments, S2
   __shared__ __attribute__((aligned(16))) bf16 s_wu[NU > 0 ? NRB * kFragElems : 8];   // A = W_u, S1
-  __shared__ __attribute__((aligned(16))) float s_b2[O];
+  __shared__ __attribute__((aligned(16))) f32x4 s_b2[O];                          // b2[o] in all four entries
   __shared__ __attribute__((aligned(16))) bf16x4 s_m0[kEpWaves][NRB][64];   // each wave's first-half messages
   __shared__ __attribute__((aligned(16))) bf16x8 s_ipq[64];   // pq_sum_chunk of each lane
   __shared__ uint2 s_lut[16];
@@ -452,7 +452,10 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   if constexpr (NU > 0)
     for (int q = threadIdx.x; q < NRB * kFragElems / 8; q += 512)
       reinterpret_cast<bf16x8*>(s_wu)[q] = reinterpret_cast<const bf16x8*>(a.fr.u)[q];
-  for (int q = threadIdx.x; q < O; q += 512) s_b2[q] = a.fr.b2f[q];
+  for (int q = threadIdx.x; q < O; q += 512) {
+    const float b = a.fr.b2f[q];
+    s_b2[q] = f32x4{b, b, b, b};
+  }
   if (threadIdx.x < 64) s_ipq[l] = pq_sum_chunk(c, g);
 
   auto load_idx = [&](int64_t T, int h, EpIdx& x) {   // E < 2^31 (coop_supported)
@@ -514,17 +517,23 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     }
     gather(xn, cur);
     // ---- the tile's rank table (second half): lane (g, c) handles ranks c and 16 + c; the segment
-    // operand of ranks 16 .. 31 (tiles of more than 16 rows) is rebuilt where it is used
-    int nrk = 0, tg[2] = {-3, -3}, span[2] = {0, 0};
+    // operand of ranks 16 .. 31 (tiles of more than 16 rows) is rebuilt where it is used.  Each rank's
+    // destination is a 32-bit byte offset from out_msg (bit 31 clear; the host keeps out_msg under 2 GB) or
+    // from the tile's carry slots (bit 31 set; none: ~0), so that the stores of the feature blocks differ
+    // only in their immediate offsets.
+    int nrk = 0, span[2] = {0, 0};
+    uint32_t dst[2] = {~0u, ~0u};
     bf16x8 sq0;
     if constexpr (HC == 1) {
       nrk = __builtin_amdgcn_readlane(tabv, kTabNrank);
 #pragma unroll
       for (int q = 0; q < 2; ++q) {
         const int r = 16 * q + c;
-        tg[q] = __shfl(tabv, kTabTgt + r, 64);
+        const int tg = __shfl(tabv, kTabTgt + r, 64);
         const int sp = __shfl(tabv, kTabSpan + (r >> 1), 64);
         span[q] = r < nrk ? (sp >> (16 * (r & 1))) & 0xffff : 0;
+        if (tg >= 0) dst[q] = (uint32_t)(((int64_t)tg * a.smsg + 4 * g) * 2);
+        else if (tg > -3) dst[q] = 0x80000000u | (uint32_t)(((-1 - tg) * O + 4 * g) * 4);
       }
       sq0 = seg_chunk_span(span[0], g, s_lut);
     }
@@ -538,8 +547,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
 #pragma unroll
       for (int rb = 0; rb <= NRB; ++rb) {
         if (rb < NRB) {
-          const float b = s_b2[16 * rb + c];
-          acc[rb & 1] = f32x4{b, b, b, b};
+          acc[rb & 1] = s_b2[16 * rb + c];
 #pragma unroll
           for (int k = 0; k < KH; ++k) mma(acc[rb & 1], m1c[k], fr[k]);
           __builtin_amdgcn_sched_barrier(0);
@@ -566,10 +574,10 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
               if (16 * q >= nrk) break;
               f32x4 D = zero4();
               mma(D, Am, q == 0 ? sq0 : seg_chunk_span(span[1], g, s_lut));
-              if (tg[q] >= 0)
-                *reinterpret_cast<bf16x4*>((bf16*)a.out_msg + (int64_t)tg[q] * a.smsg + 16 * r + 4 * g) = pack4(D);
-              else if (tg[q] > -3)
-                *reinterpret_cast<f32x4*>(a.carry + (T * 2 - 1 - tg[q]) * O + 16 * r + 4 * g) = D;
+              if (dst[q] < 0x80000000u)
+                *reinterpret_cast<bf16x4*>((char*)a.out_msg + dst[q] + 32 * r) = pack4(D);
+              else if (dst[q] != ~0u)
+                *reinterpret_cast<f32x4*>((char*)(a.carry + T * 2 * O) + (dst[q] & 0x7fffffffu) + 64 * r) = D;
             }
           }
           __builtin_amdgcn_sched_barrier(0);
