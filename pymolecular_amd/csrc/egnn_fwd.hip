@@ -265,7 +265,11 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nf
   }
   const int nfix = *a.n_fix;
   const int64_t nw = (int64_t)nfb * 4;
-  for (int64_t f = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6); f < nfix; f += nw) {
+  // rows of at most 128 message columns: two rows per wave, one per half, so that every lane works
+  const int rpw = (!EQ && O <= 128) ? 2 : 1, lpr = 64 / rpw, lr = l % lpr;
+  for (int64_t f0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * rpw; f0 < nfix; f0 += nw * rpw) {
+    const int64_t f = f0 + l / lpr;
+    if (f >= nfix) continue;
     const int r = a.fix_rows[f];
     const int rs = a.rowptr[r], re = a.rowptr[r + 1];
     float x[3] = {0.f, 0.f, 0.f};   // x of the row (x' = x + agg_x), loaded with the row's bounds by
@@ -282,7 +286,7 @@ __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nf
       tn = (re - 1) / kTileEdges - t0 + 1;
       slot0 = rs % kTileEdges == 0 ? 0 : 1;
     }
-    for (int c4 = 4 * l; c4 < SEGW; c4 += 256) {
+    for (int c4 = 4 * lr; c4 < SEGW; c4 += 4 * lpr) {
       const float* cp = a.carry + t0 * 2 * SEGW + c4;   // tile t0 + k, slot 0: cp + 2 k SEGW
       f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
       int64_t k = 0;
@@ -324,7 +328,7 @@ static int launch_fwd_t(const FwdArgs& a, int part, hipStream_t st) {
     }
     return (int)hipGetLastError();
   }
-  const int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 2048);
+  const int fb = (int)std::min<int64_t>(cdiv(a.N, 4), 4096);
   const int rb = EQ && a.coord_res ? (int)std::min<int64_t>(cdiv(a.N, 256), 1024) : 0;   // whole-row x + agg_x
   hipLaunchKernelGGL((fwd_fixup_kernel<T, EQ>), dim3(fb + rb), dim3(256), 0, st, a, O, fb);
   return (int)hipGetLastError();
