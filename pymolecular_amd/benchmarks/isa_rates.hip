@@ -107,6 +107,16 @@ __global__ __launch_bounds__(256) void lds_kernel(float* out, float seed) {
   out[blockIdx.x * 256 + threadIdx.x] = a0[0] + a1[1] + a2[2] + a3[3];
 }
 
+// ---- HBM: a 1 GiB stream read, and copied, 16 bytes per lane per access (the node products' pattern)
+__global__ __launch_bounds__(256) void hbm_copy_kernel(const f32x4* __restrict__ a, f32x4* __restrict__ b, long n) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) b[i] = a[i];
+}
+__global__ __launch_bounds__(256) void hbm_read_kernel(const f32x4* __restrict__ a, float* out, long n) {
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) s += a[i];
+  if (s[0] + s[1] + s[2] + s[3] == 12345.f) out[0] = 1.f;   // keeps the loads
+}
+
 template <typename F>
 static double time_ms(F launch) {
   hipEvent_t a, b;
@@ -186,6 +196,22 @@ int main() {
     printf("{\"test\": \"lds\", \"op\": \"%s\", \"bytes_per_cycle_per_cu\": %.1f}\n", lname[k],
            bytes_per_cu / (ms * 1e-3 * clk));
     fflush(stdout);
+  }
+  {
+    const long bytes = 1L << 30, n = bytes / 16;
+    f32x4 *ha = nullptr, *hb = nullptr;
+    if (hipMalloc(&ha, bytes) == hipSuccess && hipMalloc(&hb, bytes) == hipSuccess &&
+        hipMemset(ha, 0, bytes) == hipSuccess && hipMemset(hb, 0, bytes) == hipSuccess) {
+      for (int grid : {1024, 4096}) {
+        const double mc = time_ms([&] { hbm_copy_kernel<<<grid, 256>>>(ha, hb, n); });
+        const double mr = time_ms([&] { hbm_read_kernel<<<grid, 256>>>(ha, out, n); });
+        printf("{\"test\": \"hbm\", \"blocks\": %d, \"copy_tb_per_s\": %.2f, \"read_tb_per_s\": %.2f}\n", grid,
+               2.0 * bytes / (mc * 1e-3) / 1e12, bytes / (mr * 1e-3) / 1e12);
+        fflush(stdout);
+      }
+    }
+    hipFree(ha);
+    hipFree(hb);
   }
   hipFree(out);
   return 0;
