@@ -496,7 +496,7 @@ int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
     if (!aligned16(p)) return EGNN_ERR_ALIGN;
   hipStream_t st = (hipStream_t)stream;
   ProfScope ps(EGNN_K_NODE_UPDATE, st);
-  if (stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16)) {   // both products in one pass over the rows
+  if (stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16, true)) {   // both products in one pass over the rows
     NodeMlpArgs a{};
     a.N = s.N; a.K2 = s.K2; a.residual = s.residual;
     a.x1 = x1; a.ld1 = ld1; a.x2 = x2; a.ld2 = ld2;
@@ -575,7 +575,7 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   s2.ksplit = splitk_len(s2.M, s2.N, s2.K, s.bf16); s2.partial = w.part2;
   const int64_t nsplit1 = cdiv(std::max<int64_t>(s.N, 1), s1.ksplit), nsplit2 = cdiv(std::max<int64_t>(s.N, 1), s2.ksplit);
   if (nsplit1 * s1.M * s1.N > w.part1_elems || nsplit2 * s2.M * s2.N > w.part2_elems) return EGNN_ERR_WORKSPACE;
-  if (s.N > 0 && stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16)) {
+  if (s.N > 0 && stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16, false)) {
     // dz and grad_x in one pass over the rows, then the two weight-gradient products
     NodeMlpArgs a{};
     a.N = s.N; a.K2 = s.K2; a.residual = s.residual;

@@ -164,8 +164,8 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
 constexpr int64_t kStreamMinRows = 65536;
 bool stream_gemm_ok(const Gemm2Args& g, bool compute_bf16);
 int launch_stream_gemm(const Gemm2Args& g, hipStream_t st);
-// The node update's MLP in one streaming pass (egnn_stream.hip): bf16, N >= kStreamMinRows rows,
-// K1 = Hn = Fo = 128, K2 in {0, 128}.  Forward: pre = [x1 | x2] W1^T + b1, act = SiLU(pre),
+// The node update's MLP in one streaming pass (egnn_stream.hip): bf16, K1 = Hn = Fo = 128, K2 in {0, 128},
+// N >= kNodeFuseFwdMinRows rows (forward) or kStreamMinRows rows (backward).  Forward: pre = [x1 | x2] W1^T + b1, act = SiLU(pre),
 // out = act W2^T + b2 (+ x1).  Backward: dz = (gout W2) * SiLU'(pre), gx = dz W1 (+ gout on the
 // first K1 columns).  Weights in nn.Linear (out, in) layout; row strides are multiples of 8.
 struct NodeMlpArgs {
@@ -175,7 +175,8 @@ struct NodeMlpArgs {
   void* pre; void* act; void* out; int64_t ldo;          // forward outputs (pre, act: N x Hn)
   const void* gout; int64_t ldgo; void* dz; void* gx;    // backward (reads pre; dz: N x Hn, gx: N x K)
 };
-bool stream_node_ok(int64_t N, int K1, int K2, int Hn, int Fo, bool bf16);
+constexpr int64_t kNodeFuseFwdMinRows = 1024;
+bool stream_node_ok(int64_t N, int K1, int K2, int Hn, int Fo, bool bf16, bool fwd);
 int launch_stream_node_fwd(const NodeMlpArgs& a, hipStream_t st);
 int launch_stream_node_bwd(const NodeMlpArgs& a, hipStream_t st);
 // Two independent products, in one launch when both take the 32 x 64 bf16 tiles (else one after the other).

@@ -189,14 +189,17 @@ __device__ __forceinline__ void lds_rows(bf16* s, const bf16* g, int64_t ld, int
     *reinterpret_cast<bf16x8*>(s + r * P + k) = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + k);
   }
 }
-// the transpose of a (R x C) row-major matrix into LDS rows of pitch P: s[c][r] = g[r][c]
+// the transpose of a (R x C) row-major matrix into LDS rows of pitch P: s[c][r] = g[r][c]; a thread gathers 8
+// consecutive r of one column c (each load coalesced over the wave's consecutive c) and stores them as one
+// 16-byte LDS write (rows P apart, so the wave's writes spread over the banks)
 template <int R, int C, int P, int NT>
 __device__ __forceinline__ void lds_cols(bf16* s, const bf16* g, int64_t ld, int tid) {
-  for (int v = tid; v < R * (C / 8); v += NT) {
-    const int r = v / (C / 8), c = 8 * (v % (C / 8));
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(g + (int64_t)r * ld + c);
+  for (int v = tid; v < C * (R / 8); v += NT) {
+    const int c = v % C, r = 8 * (v / C);
+    bf16x8 x;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) s[(c + u) * P + r] = x[u];
+    for (int u = 0; u < 8; ++u) x[u] = g[(int64_t)(r + u) * ld + c];
+    *reinterpret_cast<bf16x8*>(s + c * P + r) = x;
   }
 }
 // acc[nb] += W[stream_feat(nb, c)][32 kc + 8 gq ..] . b[kc] over the KC k slices (W in LDS, k-contiguous,
@@ -393,8 +396,11 @@ int launch_node_bwd_t(const NodeMlpArgs& a, hipStream_t st) {
 
 }  // namespace
 
-bool stream_node_ok(int64_t N, int K1, int K2, int Hn, int Fo, bool bf16) {
-  return bf16 && N >= kStreamMinRows && K1 == kNodeK1 && (K2 == 0 || K2 == kNodeK1) && Hn == kNodeHn && Fo == kNodeHn;
+bool stream_node_ok(int64_t N, int K1, int K2, int Hn, int Fo, bool bf16, bool fwd) {
+  // the forward pass replaces two product launches at any node count; the backward pass replaces two paired
+  // launches by one pass and two split-K launches, which pays only at stream sizes
+  return bf16 && N >= (fwd ? kNodeFuseFwdMinRows : kStreamMinRows) && K1 == kNodeK1 && (K2 == 0 || K2 == kNodeK1) &&
+         Hn == kNodeHn && Fo == kNodeHn;
 }
 
 int launch_stream_node_fwd(const NodeMlpArgs& a, hipStream_t st) {
