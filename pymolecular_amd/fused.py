@@ -170,8 +170,12 @@ def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant
 def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_msg, w2_msg, w1_mov=None,
                        w2_mov=None, b1=None, b2=None, bx1=None, *, mean_agg: bool = False,
                        equivariant: bool = True, node_proj: Optional[torch.Tensor] = None,
-                       linear_weights: bool = False, coord_residual: bool = False, probe_identity: bool = False):
+                       linear_weights: bool = False, coord_residual: bool = False, probe_identity: bool = False,
+                       out_msg: Optional[torch.Tensor] = None):
     """One fused layer forward.  Returns ``(out_msg (N, O), out_mov (N, 3) or None)``.
+
+    ``out_msg``: when given, an (N, O) tensor of h's dtype on h's device with unit column stride (its rows
+    may lie further apart, e.g. a column slice of a wider buffer); the message sums are written into it.
 
     ``probe_identity`` (EGNN_FLAG_PROBE_IDENTITY): an instrument, not the layer -- the edge kernels
     with the MLP replaced by identity, to time the gather / segment-sum data movement alone.
@@ -194,7 +198,11 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev = h.device
     N, O = h.shape[0], dims.O
-    out_msg = torch.empty((N, O), dtype=h.dtype, device=dev)
+    if out_msg is None:
+        out_msg = torch.empty((N, O), dtype=h.dtype, device=dev)
+    elif (tuple(out_msg.shape) != (N, O) or out_msg.dtype != h.dtype or out_msg.device != dev or
+          (N > 0 and out_msg.stride(1) != 1)):
+        raise ValueError("out_msg must be an (N, O) tensor of h's dtype and device with unit column stride")
     out_mov = torch.empty((N, 3), dtype=torch.float32, device=dev) if equivariant else None
     L = _capi.lib()
     ws_bytes = L.egnn_fwd_workspace_bytes(dims)

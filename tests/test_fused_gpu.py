@@ -137,6 +137,32 @@ def test_mpnn_edge_parallel_cases(fe, skewed, eids):
     check_case(Case(rowptr, col, 128, fe, 128, 128, 128, seed=22 + fe, eq=False, edge_ids=perm), "bf16")
 
 
+def test_mpnn_forward_wide_message_rows():
+    """Message rows 2 MiB apart (an output of more than 2 GB in all): the MPNN forward leaves the edge-parallel
+    kernel, whose stores use 32-bit offsets, for the cooperative kernel; both against the oracle."""
+    from pymolecular_amd import fused
+    degs = (np.arange(1100) * 7) % 29
+    rowptr, col = random_csr(len(degs), degs, seed=71)
+    case = Case(rowptr, col, 128, 16, 128, 128, 128, seed=23, eq=False)
+    dt = DT["bf16"]
+    p = {k: _dev(v, dt) for k, v in case.p.items()}
+    row_elems = (1 << 20) + 128
+    print(f"[wide-msg] N={case.N} E={case.E} row stride {row_elems}", flush=True)
+    big = torch.zeros((case.N, row_elems), dtype=dt, device="cuda")
+    outs = []
+    for out in (None, big[:, :128]):
+        o, _ = fused.egnn_fused_forward(_dev(case.h, dt), None, _dev(case.ef, dt), _dev(case.rowptr), _dev(case.col),
+                                        None, p["w1_msg"], p["w2_msg"], None, None, p.get("b1"), p.get("b2"), None,
+                                        equivariant=False, out_msg=out)
+        outs.append(o.float().cpu().numpy())
+    del big
+    ref_msg, _ = case.forward_ref(True)
+    for o in outs:
+        err = orc.normwise_rel_err(o, ref_msg)
+        print(f"[wide-msg] out_msg err {err:.1e}", flush=True)
+        assert err <= TOL["bf16"]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "fp32"])
 def test_hidden_256(dtype):
     rowptr, col = random_csr(160, np.full(160, 40), seed=31)
