@@ -16,6 +16,9 @@
 //  * each wave owns its 16-row tiles: no barrier after the weight copy.
 // Same arguments and results as the tiled node products (Gemm2Args); the host
 // picks this kernel for the shapes it covers.
+// The node update's MLP runs the same way with both weight matrices in LDS:
+// one pass per direction (stream_node_fwd_kernel, stream_node_bwd_kernel), the
+// first product's registers being the second product's operand.
 #include "egnn_device.h"
 #include "egnn_internal.h"
 
