@@ -111,6 +111,13 @@ __global__ __launch_bounds__(256) void lds_kernel(float* out, float seed) {
 __global__ __launch_bounds__(256) void hbm_copy_kernel(const f32x4* __restrict__ a, f32x4* __restrict__ b, long n) {
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) b[i] = a[i];
 }
+__global__ __launch_bounds__(256) void hbm_widen_kernel(const f32x4* __restrict__ a, f32x4* __restrict__ b, long n) {
+  for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) {   // 1 read : 2 writes
+    const f32x4 v = a[i];
+    b[2 * i] = v;
+    b[2 * i + 1] = v + 1.0f;
+  }
+}
 __global__ __launch_bounds__(256) void hbm_read_kernel(const f32x4* __restrict__ a, float* out, long n) {
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   for (long i = blockIdx.x * 256L + threadIdx.x; i < n; i += (long)gridDim.x * 256) s += a[i];
@@ -205,8 +212,10 @@ int main() {
       for (int grid : {1024, 4096}) {
         const double mc = time_ms([&] { hbm_copy_kernel<<<grid, 256>>>(ha, hb, n); });
         const double mr = time_ms([&] { hbm_read_kernel<<<grid, 256>>>(ha, out, n); });
-        printf("{\"test\": \"hbm\", \"blocks\": %d, \"copy_tb_per_s\": %.2f, \"read_tb_per_s\": %.2f}\n", grid,
-               2.0 * bytes / (mc * 1e-3) / 1e12, bytes / (mr * 1e-3) / 1e12);
+        const double mw = time_ms([&] { hbm_widen_kernel<<<grid, 256>>>(ha, hb, n / 2); });
+        printf("{\"test\": \"hbm\", \"blocks\": %d, \"copy_tb_per_s\": %.2f, \"read_tb_per_s\": %.2f, "
+               "\"read1_write2_tb_per_s\": %.2f}\n", grid, 2.0 * bytes / (mc * 1e-3) / 1e12, bytes / (mr * 1e-3) / 1e12,
+               1.5 * bytes / (mw * 1e-3) / 1e12);
         fflush(stdout);
       }
     }
