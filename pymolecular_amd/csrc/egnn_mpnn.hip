@@ -35,33 +35,6 @@ namespace {
 
 using namespace tile;
 
-// W_hl[h][o] in LDS as rows of 144 bf16 (288 bytes), the 8-byte unit u of row R stored at unit
-// u ^ ((R >> 2) & 3).  Both operand reads then hit 16 different 8-byte bank groups per 16 lanes: the
-// W_hl rows of S5 (lanes c read rows 16 blk + c at one unit) and the transposing W_hl^T reads of S2
-// (lanes read rows kb + c / 4 at units 4 blk + c % 4).  The swizzle changes only the two low bits
-// of a unit, so every fragment's address is a per-lane base plus a constant.
-constexpr int kWP = 144;
-__device__ __forceinline__ const bf16* wunit(const bf16* W, int R, int u) { return W + R * kWP + 4 * (u ^ ((R >> 2) & 3)); }
-// A[r][k] = W[16 blk + r][32 kc + kappa_chain(g, s)]  (S5: A = W_hl); Wr = the lane's base, wrow_base
-__device__ __forceinline__ const bf16* wrow_base(const bf16* W, int c, int g) { return W + c * kWP + 4 * (g ^ ((c >> 2) & 3)); }
-__device__ __forceinline__ bf16x8 w_rows(const bf16* Wr, int blk, int kc) {
-  const bf16* p = Wr + 16 * blk * kWP + 32 * kc;
-  return __builtin_shufflevector(*reinterpret_cast<const bf16x4*>(p), *reinterpret_cast<const bf16x4*>(p + 16),
-                                 0, 1, 2, 3, 4, 5, 6, 7);
-}
-// A[r][k] = W[32 kc + kappa_chain(g, s)][16 blk + r]  (S2: A = W_hl^T), two transposing reads: lane c
-// addresses row kb + c / 4, columns 16 blk + 4 (c % 4) .. + 3, and receives column 16 blk + c of rows
-// kb .. kb + 3; Wc = the lane's base, wcol_base
-__device__ __forceinline__ const bf16* wcol_base(const bf16* W, int c, int g) {
-  return W + (4 * g + (c >> 2)) * kWP + 4 * ((c & 3) ^ (g & 3));
-}
-__device__ __forceinline__ bf16x8 w_cols(const bf16* Wc, int blk, int kc) {
-  const bf16* p = Wc + 32 * kc * kWP + 16 * blk;
-  const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)p);
-  const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((__attribute__((address_space(3))) bf16x4*)(p + 16 * kWP));
-  return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-}
-
 constexpr int kEpWaves = 8;                   // waves per block, two per SIMD
 constexpr int kEpSub = 16;                    // edges per wave sub-tile
 constexpr int kEpTile = kEpWaves * kEpSub;    // edges per block tile
@@ -105,19 +78,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   const int64_t NT = (a.E + kEpTile - 1) / kEpTile;
   const int64_t G = gridDim.x;
 
-  // W_hl[h][o] from the packed (in, out) layout or its nn.Linear transpose, one 8-byte unit per step
-  for (int q = threadIdx.x; q < H * O / 4; q += 512) {
-    const int h = q / (O / 4), u = q % (O / 4);
-    const bf16* src = (const bf16*)a.w2;
-    bf16x4 v;
-    if (a.lin) {
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = src[(int64_t)(4 * u + t) * H + h];
-    } else {
-      v = *reinterpret_cast<const bf16x4*>(src + (int64_t)h * O + 4 * u);
-    }
-    *reinterpret_cast<bf16x4*>(const_cast<bf16*>(wunit(s_whl, h, u))) = v;
-  }
+  // W_hl[h][o] from the packed (in, out) layout or its nn.Linear transpose
+  fill_weight_swizzled<H, O, 512>(s_whl, (const bf16*)a.w2, a.lin != 0);
   if constexpr (NU > 0)
     for (int q = threadIdx.x; q < NRB * kFragElems / 8; q += 512)
       reinterpret_cast<bf16x8*>(s_wu)[q] = reinterpret_cast<const bf16x8*>(a.fr.u)[q];
