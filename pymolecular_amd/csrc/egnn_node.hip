@@ -86,6 +86,8 @@ int64_t splitk_len(int64_t M, int64_t N, int64_t K, bool fold) {
   // node counts of molecule batches (measured faster than 32 x 64 tiles over 700 rows: fewer re-reads
   // of the operands from L2 for a few more partials)
   const int64_t target = N == 1 ? 1024 : big ? 512 : 768;
+  if (fold && big && N == 256 && (M == 256 || M == 257))   // gemm_atb256_kernel: one split per CU
+    return cdiv(cdiv(K, std::min<int64_t>(256, cdiv(K, 256))), 64) * 64;
   const int64_t splits = std::max<int64_t>(1, std::min<int64_t>(cdiv(target, std::max<int64_t>(tiles, 1)), cdiv(K, 256)));
   return cdiv(cdiv(K, splits), 64) * 64;
 }
@@ -836,6 +838,104 @@ __global__ __launch_bounds__(256) void gemm_bf16_xcd_kernel(Gemm2Args g, int gx,
   gemm_bf16_tile<A_KC, B_NC, BM, BN, BK, NBUF>(g, tile % gx, tile / gx, bz, smem);
 }
 
+// Split-K [A | 1]^T B over the edges for 256 x 256 results, A[k][m] and B[k][n] edge-major (the wide
+// path's factor products; the ones row 256 optional): one block of 8 waves computes the whole result
+// of its split, so every operand row is read from memory once (128 x 128 tiles read each twice).
+// Wave (wm, wn) = (w >> 1, w & 1) owns rows [64 wm, 64 wm + 64) and columns [128 wn, 128 wn + 128);
+// slices of BK edges pass through two LDS buffers as in gemm_bf16_tile.  The ones row (the column
+// sums of B) is summed by the loading threads in fp32, 8 columns each, and combined in thread order.
+constexpr int kAtbSlice = 64;   // edges per LDS slice
+template <int BK>
+__global__ __launch_bounds__(512) void gemm_atb256_kernel(Gemm2Args g) {
+  constexpr int P = 256 + 16, T = BK * P;           // row pitch and size (bf16) of one operand slice
+  constexpr int MI = 4, NJ = 8, NL = BK * 256 / 8 / 512;
+  static_assert(BK % 32 == 0 && NL >= 1, "slice depth");
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * T];
+  const int tid = threadIdx.x, wave = tid >> 6, l = tid & 63, c = l & 15, gq = l >> 4;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int bz = (int)blockIdx.x;
+  const int64_t kbeg = (int64_t)bz * g.ksplit, kend = g.K < kbeg + g.ksplit ? g.K : kbeg + g.ksplit;
+  const bf16* A = (const bf16*)g.A;
+  const bf16* B = (const bf16*)g.B;
+  const bool ones_row = g.M == 257;
+  f32x4 acc[MI][NJ];
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float cs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};   // column sums of B: columns 8 (tid & 31) + u
+  bf16x8 ra[NL], rb[NL];
+  // thread tid loads row (tid >> 5) + 16 i of the slice, columns 8 (tid & 31) .. + 7, of A and of B
+  auto load = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int64_t k = k0 + (tid >> 5) + 16 * i;
+      const int q = tid & 31;
+      ra[i] = k < kend ? *reinterpret_cast<const bf16x8*>(A + k * g.lda + 8 * q) : zero_chunk<bf16>();
+      rb[i] = k < kend ? *reinterpret_cast<const bf16x8*>(B + k * g.ldb + 8 * q) : zero_chunk<bf16>();
+    }
+  };
+  auto store = [&](int buf) {
+    bf16* At = smem + buf * 2 * T;
+    bf16* Bt = At + T;
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+      const int r = (tid >> 5) + 16 * i, q = tid & 31;
+      *reinterpret_cast<bf16x8*>(&At[r * P + 8 * q]) = ra[i];
+      *reinterpret_cast<bf16x8*>(&Bt[r * P + 8 * q]) = rb[i];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cs[u] += (float)rb[i][u];
+    }
+  };
+  int buf = 0;
+  if (kbeg < kend) {
+    load(kbeg);
+    store(0);
+  }
+  __syncthreads();
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) load(k0 + BK);
+    const bf16* At = smem + buf * 2 * T;
+    const bf16* Bt = At + T;
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8 a[MI], b[NJ];
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+        a[i] = join_tr(ld_tr4<P>(At, 32 * ks + 8 * gq, wm * 64 + 16 * i, c), ld_tr4<P>(At, 32 * ks + 8 * gq + 4, wm * 64 + 16 * i, c));
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        b[j] = join_tr(ld_tr4<P>(Bt, 32 * ks + 8 * gq, wn * 128 + 16 * j, c), ld_tr4<P>(Bt, 32 * ks + 8 * gq + 4, wn * 128 + 16 * j, c));
+#pragma unroll
+      for (int i = 0; i < MI; ++i)
+#pragma unroll
+        for (int j = 0; j < NJ; ++j) mma(acc[i][j], a[i], b[j]);
+    }
+    if (more) store(buf ^ 1);
+    buf ^= 1;
+    __syncthreads();
+  }
+  float* Pz = g.partial + (int64_t)bz * g.M * 256;
+#pragma unroll
+  for (int i = 0; i < MI; ++i)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Pz[(int64_t)(wm * 64 + 16 * i + 4 * gq + r) * 256 + wn * 128 + 16 * j + c] = acc[i][j][r];
+  if (ones_row) {   // the 16 threads of each column group, in order (the loop's last barrier freed smem)
+    float* s_cs = reinterpret_cast<float*>(smem);   // [16][256]
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s_cs[(tid >> 5) * 256 + 8 * (tid & 31) + u] = cs[u];
+    __syncthreads();
+    if (tid < 256) {
+      float t = 0.f;
+      for (int r = 0; r < 16; ++r) t += s_cs[r * 256 + tid];
+      Pz[256 * 256 + tid] = t;
+    }
+  }
+}
+
 // 1D grid with the n tiles of one row block adjacent (they share the A rows,
 // read once from memory while they are in L2), then the row blocks, then the split
 template <bool A_KC, bool B_NC, int BM, int BN, int BK, int NBUF>
@@ -1130,6 +1230,12 @@ bool bf16_tiled_ok(const Gemm2Args& g, bool compute_bf16) {
 bool bf16_big_tiles(const Gemm2Args& g) {
   return g.ksplit > 0 ? g.K >= kSplitKBig : cdiv(g.M, 128) * cdiv(g.N, 128) >= 2048;
 }
+// the edge-sized split-K products that gemm_atb256_kernel takes: A[k][m], B[k][n] with 256 columns
+// each, 16-byte aligned rows, optionally the ones row 256 (sized for one split per CU by splitk_len)
+bool atb256_ok(const Gemm2Args& g) {
+  return g.ksplit > 0 && g.K >= kSplitKBig && g.partial && !g.a_kc && g.b_nc && !g.A2 && !g.b_kidx &&
+         g.N == 256 && (g.M == 256 || (g.M == 257 && g.a_ones_row == 256)) && g.lda >= 256 && g.ldb >= 256;
+}
 unsigned splits_of(const Gemm2Args& g) {
   return g.ksplit > 0 ? (unsigned)std::max<int64_t>(1, cdiv(g.K, g.ksplit)) : 1u;
 }
@@ -1168,6 +1274,10 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);
   auto al4 = [](const void* p, int64_t ld) { return p == nullptr || ((((uintptr_t)p) & 15) == 0 && ld % 4 == 0); };
   if (bf16_tiled_ok(g, compute_bf16)) {
+    if (atb256_ok(g)) {   // one block per split computes the whole 256 x 256 (+ ones row) result
+      hipLaunchKernelGGL((gemm_atb256_kernel<kAtbSlice>), dim3(gz), dim3(512), 0, st, g);
+      return (int)hipGetLastError();
+    }
     const bool big = bf16_big_tiles(g);
     const bool narrow = big && g.N <= 32;   // e.g. dW_e over the edges: 128 x 32 tiles
     if (!big && g.ksplit > 0) {   // split-K reductions over node-sized K: 64 x 64 tiles
