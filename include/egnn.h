@@ -157,8 +157,10 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides,
  * cannot allocate device memory (code under HIP graph capture, serving loops
  * that forbid hipMalloc).  The same computation and kernels as egnn_fwd, with
  * the workspace in a fixed device array inside the library instead of caller
- * memory: EGNN_FWD_STATIC_SCRATCH_BYTES per GPU, held from the first call on that
- * GPU until the process ends.  Calls whose egnn_fwd_workspace_bytes exceed it
+ * memory: EGNN_FWD_STATIC_SCRATCH_BYTES per GPU, part of the library's device
+ * code object: resident from when that object is loaded on a GPU (the library's
+ * first kernel launch or symbol lookup there, whichever entry point makes it)
+ * until the process ends.  Calls whose egnn_fwd_workspace_bytes exceed it
  * return EGNN_ERR_SCRATCH before touching the device.  The caller still provides
  * inputs, outputs and the schedule (built once, beforehand).  It calls no
  * allocator.  All calls on one GPU share the array: calls that overlap on one

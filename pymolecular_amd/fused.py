@@ -25,7 +25,7 @@ import torch
 from . import _capi
 from ._capi import EgnnDims, EgnnStrides, check
 
-__all__ = ["Schedule", "get_schedule", "egnn_fused_forward", "egnn_fused_backward", "EGNNFusedFn",
+__all__ = ["Schedule", "TensorCache", "get_schedule", "egnn_fused_forward", "egnn_fused_backward", "EGNNFusedFn",
            "egnn_fused", "coo_to_csr"]
 
 
@@ -71,28 +71,77 @@ def schedule_arrays(sched: Schedule) -> dict:
     return out
 
 
-_SCHED_CACHE: "dict[tuple, tuple[weakref.ref, weakref.ref, Schedule]]" = {}
+class TensorCache:
+    """Values derived from tensors, kept while those very tensors live unmodified.
+
+    An entry holds weak references to the root tensors (the ``_base`` of a view)
+    of its keys plus each key's device, dtype, shape, strides, storage offset and
+    in-place version counter.  A lookup hits only when every key's root *is* the
+    remembered object: a freed tensor whose memory (same data pointer, version 0)
+    is handed to a new tensor of the same size therefore never matches, and a
+    tensor edited in place has a new version.  Fresh views of a live tensor (the
+    ``row, col = edge_index`` unpacking of a (2, E) tensor) share its root and hit.
+    """
+
+    def __init__(self, maxsize: int = 8):
+        self.maxsize = maxsize
+        self._entries: list = []
+
+    @staticmethod
+    def _root(t: torch.Tensor) -> torch.Tensor:
+        return t if t._base is None else t._base
+
+    @staticmethod
+    def _meta(t: torch.Tensor) -> tuple:
+        return (t.device, t.dtype, tuple(t.shape), tuple(t.stride()), t.storage_offset(), t._version)
+
+    def get(self, tensors, extra, make):
+        """The value for ``tensors`` (and the hashable ``extra``), computed by ``make()`` on a miss."""
+        roots = [self._root(t) for t in tensors]
+        meta = (tuple(self._meta(t) for t in tensors), extra)
+        live = []
+        hit = None
+        for refs, m, val in self._entries:
+            objs = [r() for r in refs]
+            if any(o is None for o in objs):
+                continue   # a key tensor died: its memory may belong to another tensor now
+            live.append((refs, m, val))
+            if hit is None and m == meta and all(o is r for o, r in zip(objs, roots)):
+                hit = val
+        self._entries = live
+        if hit is not None:
+            return hit
+        val = make()
+        self._entries.append(([weakref.ref(r) for r in roots], meta, val))
+        del self._entries[:-self.maxsize]
+        return val
+
+    def clear(self):
+        self._entries = []
+
+
+_SCHED_CACHE = TensorCache(maxsize=16)
 
 
 def get_schedule(row_ptrs: torch.Tensor, col_indices: torch.Tensor, num_nodes: int) -> Schedule:
     """Build (or fetch from the cache) the schedule of a dst-sorted int32 CSR graph.
 
-    Keyed by the storage pointers and in-place version counters of ``row_ptrs``
-    and ``col_indices``, so an edited graph gets a new schedule.
+    Cached per (``row_ptrs``, ``col_indices``) tensor pair by :class:`TensorCache`:
+    a different or edited graph gets a new schedule.
     """
     _require_device(row_ptrs, "row_ptrs")
     if row_ptrs.dtype != torch.int32 or col_indices.dtype != torch.int32:
         raise TypeError("row_ptrs and col_indices must be int32 (datasets_loaders.py CSR contract)")
     if row_ptrs.numel() != num_nodes + 1:
         raise ValueError(f"row_ptrs has {row_ptrs.numel()} entries, expected num_nodes + 1 = {num_nodes + 1}")
+    return _SCHED_CACHE.get((row_ptrs, col_indices), int(num_nodes),
+                            lambda: _build_schedule(row_ptrs, col_indices, int(num_nodes)))
+
+
+def _build_schedule(row_ptrs: torch.Tensor, col_indices: torch.Tensor, N: int) -> Schedule:
     row_ptrs = row_ptrs.contiguous()
     col_indices = col_indices.contiguous()
-    N, E = int(num_nodes), int(col_indices.numel())
-    key = (row_ptrs.data_ptr(), col_indices.data_ptr(), N, E, row_ptrs._version, col_indices._version,
-           row_ptrs.device.index)
-    hit = _SCHED_CACHE.get(key)
-    if hit is not None and hit[0]() is row_ptrs and hit[1]() is col_indices:
-        return hit[2]
+    E = int(col_indices.numel())
     L = _capi.lib()
     nbytes = L.egnn_schedule_bytes(N, E)
     tbytes = L.egnn_schedule_tmp_bytes(N, E)
@@ -101,11 +150,7 @@ def get_schedule(row_ptrs: torch.Tensor, col_indices: torch.Tensor, num_nodes: i
     rc = L.egnn_schedule_build(row_ptrs.data_ptr(), col_indices.data_ptr() if E else None, N, E, buf.data_ptr(),
                                nbytes, tmp.data_ptr(), tbytes, _stream(row_ptrs.device))
     check("egnn_schedule_build", rc)
-    sched = Schedule(buf, N, E)
-    if len(_SCHED_CACHE) > 64:
-        _SCHED_CACHE.clear()
-    _SCHED_CACHE[key] = (weakref.ref(row_ptrs), weakref.ref(col_indices), sched)
-    return sched
+    return Schedule(buf, N, E)
 
 
 def coo_to_csr(row: torch.Tensor, col: torch.Tensor, num_nodes: int):

@@ -21,7 +21,7 @@ from __future__ import annotations
 import torch
 from torch import nn
 
-from ...fused import coo_to_csr, egnn_fused
+from ...fused import TensorCache, coo_to_csr, egnn_fused
 from ...layer_fn import GCLLayerFn
 from ...node_update import dense, node_update
 
@@ -29,18 +29,14 @@ __all__ = ["E_GCL", "EGNN", "unsorted_segment_sum", "unsorted_segment_mean", "ge
 
 
 class _CSRCache:
-    """dst-sorted CSR of an edge_index, cached by tensor identity and version."""
+    """dst-sorted CSR of an edge_index, cached per edge tensor by :class:`~pymolecular_amd.fused.TensorCache`
+    (identity of the live tensors, not their addresses, so a new graph at a reused address is rebuilt)."""
 
     def __init__(self):
-        self.key = None
-        self.val = None
+        self._cache = TensorCache(maxsize=8)
 
     def get(self, row: torch.Tensor, col: torch.Tensor, n: int):
-        key = (row.data_ptr(), col.data_ptr(), row._version, col._version, n, row.numel())
-        if key != self.key:
-            self.val = coo_to_csr(row, col, n)
-            self.key = key
-        return self.val
+        return self._cache.get((row, col), int(n), lambda: coo_to_csr(row, col, n))
 
 
 _csr_cache = _CSRCache()

@@ -18,7 +18,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from ...fused import coo_to_csr, egnn_fused
+from ...fused import TensorCache, coo_to_csr, egnn_fused
 from ...node_update import node_update
 
 
@@ -38,22 +38,22 @@ class EGNN_HIP_Layer(nn.Module):
         node_mlp_in = f_node + msg_out_feat
         self.node_mlp = nn.Sequential(nn.Linear(node_mlp_in, node_hidden_dim), nn.SiLU(),
                                       nn.Linear(node_hidden_dim, f_node))
-        self._csr_key = None
-        self._csr = None
+        # CSR of the symmetrised edge list, per live edge_index tensor (not per address)
+        self._csr = TensorCache(maxsize=4)
 
     def _both_ways(self, edge_index, num_nodes):
-        key = (edge_index.data_ptr(), edge_index._version, edge_index.shape[1], num_nodes)
-        if key != self._csr_key:
-            src, dst = edge_index[0].to(torch.int64), edge_index[1].to(torch.int64)
-            E = src.numel()
-            rows = torch.cat([dst, src])          # destination of each directed message
-            cols = torch.cat([src, dst])
-            row_ptrs, col_s, perm = coo_to_csr(rows, cols, num_nodes)
-            eids = (perm.to(torch.int64) % max(E, 1)).to(torch.int32)   # both directions read edge e's features
-            deg = torch.diff(row_ptrs).to(torch.float32).clamp(min=1.0)
-            self._csr = (row_ptrs, col_s, eids, deg)
-            self._csr_key = key
-        return self._csr
+        return self._csr.get((edge_index,), int(num_nodes), lambda: self._build_both_ways(edge_index, num_nodes))
+
+    @staticmethod
+    def _build_both_ways(edge_index, num_nodes):
+        src, dst = edge_index[0].to(torch.int64), edge_index[1].to(torch.int64)
+        E = src.numel()
+        rows = torch.cat([dst, src])          # destination of each directed message
+        cols = torch.cat([src, dst])
+        row_ptrs, col_s, perm = coo_to_csr(rows, cols, num_nodes)
+        eids = (perm.to(torch.int64) % max(E, 1)).to(torch.int32)   # both directions read edge e's features
+        deg = torch.diff(row_ptrs).to(torch.float32).clamp(min=1.0)
+        return row_ptrs, col_s, eids, deg
 
     def forward(self, node_feat, coord, edge_index, edge_feat):
         N = node_feat.shape[0]

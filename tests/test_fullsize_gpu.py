@@ -13,7 +13,9 @@ power-law graph) these tests check:
     node's gradient is exactly zero;
   * E(3) equivariance (rotation and translation of the coordinates);
   * exact linearity of the backward in the incoming gradients (scaling by 2 is exact) and
-    bitwise determinism of the forward and the backward.
+    bitwise determinism of the forward and the backward;
+  * the schedule of the 2M-node power-law graph (per-edge rows, split rows, CSC, the rank tables of
+    its ~580k 32-edge tiles) bit-exact against the numpy restatement.
 Bounds: normwise 1e-5 (fp32), 2e-2 (bf16); the bf16 oracle runs in float64 on the bf16 inputs.
 """
 import numpy as np
@@ -73,10 +75,21 @@ def _bwd(h, coord, ef, rowptr, col, pd, gm, gx, eq, mean):
 
 
 def _sample_rows(g, k, n=47):
-    """The heaviest row plus n rows drawn without replacement (seeded), ascending."""
+    """Rows checked by the row-restriction tests (ascending): n rows drawn without replacement
+    (seeded), the 16 highest-degree rows, and the rows where the 32-edge tiling is hardest (where
+    they exist): 16 drawn among the rows spread over three or more tiles, and up to 4 each of the
+    rows whose first edge is the last of a tile and whose last edge is the first of a tile."""
     deg = np.diff(g.rowptr)
     r = np.random.Generator(np.random.PCG64(7 + k))
-    return np.unique(np.concatenate([[int(np.argmax(deg))], r.choice(g.N, n, replace=False)]))
+    first_t = g.rowptr[:-1] // 32
+    last_t = (g.rowptr[1:] - 1) // 32
+    straddle = np.flatnonzero((deg > 0) & (last_t - first_t >= 2))
+    starts_late = np.flatnonzero((deg > 1) & (g.rowptr[:-1] % 32 == 31))
+    ends_early = np.flatnonzero((deg > 1) & (g.rowptr[1:] % 32 == 1))
+    pick = lambda a, m: r.choice(a, min(m, len(a)), replace=False) if len(a) else np.zeros(0, np.int64)  # noqa: E731
+    parts = [r.choice(g.N, n, replace=False), np.argsort(deg, kind="stable")[-16:], pick(straddle, 16),
+             pick(starts_late, 4), pick(ends_early, 4)]
+    return np.unique(np.concatenate(parts).astype(np.int64))
 
 
 def _subgraph(g, rows):
@@ -228,3 +241,17 @@ def test_backward_exact_linearity_and_determinism(k):
             continue
         assert torch.equal(v, b[key]), key
         assert torch.equal(c[key], v * 2), key
+
+
+def test_powerlaw_schedule_bit_exact():
+    # the degree-binning schedule at the size that needs it: 2M rows of degree 2..4096, ~18.6M edges
+    from pymolecular_amd import fused
+    from tests.test_schedule import schedule_ref
+    g = _graph(5)
+    print(f"[fullsize] schedule N={g.N} E={g.E} max degree {np.diff(g.rowptr).max()}", flush=True)
+    rp = torch.from_numpy(g.rowptr).cuda()
+    cl = torch.from_numpy(g.col).cuda()
+    got = fused.schedule_arrays(fused.get_schedule(rp, cl, g.N))
+    ref = schedule_ref(g.rowptr, g.col)
+    for key, v in ref.items():
+        np.testing.assert_array_equal(got[key].cpu().numpy(), v, err_msg=key)

@@ -137,6 +137,20 @@ def test_mpnn_edge_parallel_cases(fe, skewed, eids):
     check_case(Case(rowptr, col, 128, fe, 128, 128, 128, seed=22 + fe, eq=False, edge_ids=perm), "bf16")
 
 
+@pytest.mark.parametrize("mean", [False, True])
+def test_egnn_h128_edge_features_24(mean):
+    """The cooperative EGNN kernels (bf16, H = 128) at F_E = 24: the forward's edge-input chunk of 24 features
+    plus r^2, and the backward's second 16-slot dW_e block, which also holds the r^2 slots.  Skewed rows that
+    cross many 64-edge tiles, empty rows, a partial last 64-edge tile (E % 64 != 0) and edge ids that permute
+    the feature rows."""
+    degs = np.array([0, 300, 1, 2, 0, 129, 3, 31, 33, 0, 64, 127, 128, 5, 2, 2, 2, 0, 17] * 5 + [7])
+    rowptr, col = random_csr(len(degs), degs, seed=81)
+    assert len(col) % 64 != 0
+    perm = np.random.Generator(np.random.PCG64(9)).permutation(len(col))
+    print(f"[egnn-fe24] N={len(degs)} E={len(col)} mean={mean}", flush=True)
+    check_case(Case(rowptr, col, 128, 24, 128, 128, 128, seed=83, eq=True, mean_agg=mean, edge_ids=perm), "bf16")
+
+
 def test_mpnn_forward_wide_message_rows():
     """Message rows 2 MiB apart (an output of more than 2 GB in all): the MPNN forward leaves the edge-parallel
     kernel, whose stores use 32-bit offsets, for the cooperative kernel; both against the oracle."""

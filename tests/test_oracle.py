@@ -282,3 +282,77 @@ def test_round_bf16_matches_torch():
 def test_normwise_error():
     assert orc.normwise_rel_err(np.array([1.0, 2.0]), np.array([1.0, 2.0])) == 0.0
     assert abs(orc.normwise_rel_err(np.array([1.0, 2.1]), np.array([1.0, 2.0])) - 0.05) < 1e-12
+
+
+def test_hoisted_first_layer_equals_concat_form():
+    # the per-node products P[row] + Q[col] + W_x [r2, e] are the concat-form Linear in exact arithmetic:
+    # outputs and every gradient agree to float64 roundoff, for the EGNN and the MPNN layer
+    torch.manual_seed(5)
+    c = small_case(18, N=13, eq=True)
+    rows = torch.tensor(orc.csr_row_of_edge(c["rowptr"]))
+    col = torch.tensor(c["col"], dtype=torch.int64)
+    for layer in (torch_ref.EGCLRef(8, 8, 8, edges_in_d=3).double(), torch_ref.MPNNGCLRef(8, 8, 8, edges_in_d=3).double()):
+        res = []
+        for hoist in (False, True):
+            layer.hoist_first_layer = hoist
+            layer.zero_grad()
+            h = torch.tensor(rng(3).standard_normal((13, 8)), requires_grad=True)
+            x = torch.tensor(rng(4).standard_normal((13, 3)), requires_grad=True)
+            ea = torch.tensor(rng(5).standard_normal((len(col), 3)))
+            out = layer(h, (rows, col), x, ea) if isinstance(layer, torch_ref.EGCLRef) else layer(h, (rows, col), ea)
+            loss = out[0].pow(2).sum() + (out[1].pow(2).sum() if isinstance(layer, torch_ref.EGCLRef) else 0)
+            loss.backward()
+            res.append([out[0].detach(), h.grad] + [p.grad.clone() for p in layer.parameters()]
+                       + ([x.grad] if isinstance(layer, torch_ref.EGCLRef) else []))
+        for a, b in zip(*res):
+            np.testing.assert_allclose(b.numpy(), a.numpy(), rtol=1e-11, atol=1e-11)
+
+
+def test_hoisted_first_layer_bf16_gradients():
+    # bfloat16 on the CPU: the hoisted form's input gradients agree with float64 to bfloat16 resolution
+    # (guards the contiguous weight slices: torch's CPU bfloat16 linear mishandles a strided weight)
+    torch.manual_seed(6)
+    lin = torch.nn.Linear(2 * 16 + 1, 32).double()
+    rows = torch.tensor(rng(7).integers(0, 20, 200))
+    col = torch.tensor(rng(8).integers(0, 20, 200))
+    r2 = torch.tensor(rng(9).uniform(0, 30, (200, 1)))
+    g = torch.tensor(rng(10).standard_normal((200, 32)))
+    grads = []
+    for dt in (torch.float64, torch.bfloat16):
+        l2 = torch.nn.Linear(33, 32).to(dt)
+        with torch.no_grad():
+            l2.weight.copy_(lin.weight.to(torch.bfloat16))
+            l2.bias.copy_(lin.bias.to(torch.bfloat16))
+        h = torch.tensor(rng(11).standard_normal((20, 16))).to(torch.bfloat16).to(dt).requires_grad_()
+        r = r2.float().requires_grad_()
+        y = torch_ref.first_layer(l2, h, rows, col, [r], hoist=True)
+        y.backward(g.to(y.dtype))
+        grads.append((h.grad.double(), r.grad.double(), l2.weight.grad.double()))
+    for a, b in zip(*grads):
+        assert orc.normwise_rel_err(b.numpy(), a.numpy()) < 2e-2
+
+
+def test_gather_rows_backward_accumulates_in_float32():
+    t = torch.tensor(rng(12).standard_normal((5, 4))).to(torch.bfloat16).requires_grad_()
+    idx = torch.tensor([0, 1, 1, 3] * 500)
+    g = torch.full((len(idx), 4), 1.0 + 2.0 ** -7, dtype=torch.bfloat16)   # exact in bfloat16
+    torch_ref.gather_rows(t, idx).backward(g)
+    exact = torch.bincount(idx, minlength=5).double()[:, None] * (1.0 + 2.0 ** -7)
+    np.testing.assert_array_equal(t.grad.double().numpy(), exact.to(torch.bfloat16).double().expand(5, 4).numpy())
+
+
+def test_bf16_roundoff_realization_bounds():
+    # every rounding point moves a value by at most the unit roundoff, and different seeds differ
+    x = torch.linspace(-3, 3, 1000)
+    a = torch_ref.bf16_roundoff(x, torch.Generator().manual_seed(0))
+    b = torch_ref.bf16_roundoff(x, torch.Generator().manual_seed(1))
+    rel = ((a.double() - x.double()).abs() / x.double().abs().clamp(min=1e-30)).max()
+    assert rel <= torch_ref.BF16_UNIT_ROUNDOFF * (1 + 1e-6)
+    assert not torch.equal(a, b)
+    lin = torch.nn.Linear(4, 4)
+    handles, act = torch_ref.bf16_rounding_realization(lin, torch.Generator().manual_seed(0))
+    y = lin(torch.ones(2, 4))
+    for hd in handles:
+        hd.remove()
+    y0 = lin(torch.ones(2, 4))
+    assert 0 < (y - y0).abs().max() <= torch_ref.BF16_UNIT_ROUNDOFF * y0.abs().max() * 1.01
