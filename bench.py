@@ -18,8 +18,11 @@ edges per second through the fused layer.
 roofline: the dominant edge kernel of the step (the fused backward), its
 time per layer from HIP events recorded on the stream it runs on during the
 timed steps (the library's instrumentation hook; one launch per layer, or
-one per edge chunk of the one-wave-per-tile backward), and its algorithmic
-work per layer from the per-edge model of the reference formulation:
+one per edge chunk of the one-wave-per-tile backward) -- plus, on the paths
+whose backward kernel stores per-edge factors (H = 256, and fp32), the
+weight-gradient products over those factors that finish its work (class
+edge_wgrad) -- and its algorithmic work per layer from the per-edge model of
+the reference formulation:
     FLOP_fwd(e) = 2 [(2F + g + F_E) H + H O + g (O M + M)],  FLOP_bwd = 2 FLOP_fwd
     B_fwd = E (8 + F s + c + F_E s) + N (4 + F s + 2c + O s)
     B_bwd = E (8 + F s + c + F_E s + 4F + c) + N (4 + F s + 3c + O s + 4F)
@@ -76,6 +79,7 @@ def parse():
     ap.add_argument("--probe", action="store_true",
                     help="also time the identity-MLP instrument of the MPNN edge kernels (gather / segment-sum "
                          "data movement alone) at the power-law workload and print its line")
+    ap.add_argument("--probe-only", action="store_true", help="run only the identity-MLP instrument (no workload line)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="end with three 256 MiB device copies (scale reference for HBM byte counters)")
     return ap.parse_args()
@@ -130,14 +134,16 @@ def kernel_work(cls, path, N, E, F, H, O, M, FE, g, s):
         return 0, E * (2 * H * s + 4 + 32 * g) + N * (2 * H * s + 12 * g + 8)
     if cls == "node_gemm":
         return 2 * N * F * 2 * H, N * (F + 2 * H) * s
-    if cls == "wgrad":   # whole layer: dh and [dW_n1 | dW_n2; db1] over the nodes, plus the edge-factor products
-        flops, nbytes = 2 * N * (F + 1) * 2 * H + 2 * N * 2 * H * F, N * (F + 2 * H) * s + N * (2 * H + F) * s
+    if cls == "wgrad":   # whole layer: dh and [dW_n1 | dW_n2; db1] over the nodes
+        return 2 * N * (F + 1) * 2 * H + 2 * N * 2 * H * F, N * (F + 2 * H) * s + N * (2 * H + F) * s
+    if cls == "edge_wgrad":   # whole layer: the weight-gradient products over the factors the edge kernel stored
+        flops = nbytes = 0
         if path == "wide":     # [dW_hl; db2], [dW1_mov; dbx1] over the edge factors; dW_e over Gh
-            flops += 2 * E * ((H + 1) * O + g * (O + 1) * M + H * FE)
-            nbytes += E * ((H + O) * s + g * (O + M) * s + (H * s + FE * s + 4 if FE else 0))
+            flops = 2 * E * ((H + 1) * O + g * (O + 1) * M + H * FE)
+            nbytes = E * ((H + O) * s + g * (O + M) * s + (H * s + FE * s + 4 if FE else 0))
         elif path == "one":    # the same, plus the dw2_mov and dw_d matrix-vector products over p, Gh and r^2
-            flops += 2 * E * ((H + 1) * O + g * ((O + 1) * M + M + H) + H * FE)
-            nbytes += E * ((H + O) * s + g * ((O + M) * s + M * s + 4 + H * s + 4) + (H * s + FE * s + 4 if FE else 0))
+            flops = 2 * E * ((H + 1) * O + g * ((O + 1) * M + M + H) + H * FE)
+            nbytes = E * ((H + O) * s + g * ((O + M) * s + M * s + 4 + H * s + 4) + (H * s + FE * s + 4 if FE else 0))
         return flops, nbytes
     return 0, 0
 
@@ -277,7 +283,7 @@ def run_workload(k, dtype, a, g=None):
     # The library's event hook records the fused edge kernels (the roofline's kernels) through the
     # warm-up and the timed steps, on the stream each kernel runs on; the warm-up fills its event pool so
     # the timed steps create none.  Every kernel class is timed in a separate untimed pass afterwards.
-    edge_classes = [_capi.K_FWD_EDGE, _capi.K_BWD_EDGE]
+    edge_classes = [_capi.K_FWD_EDGE, _capi.K_BWD_EDGE, _capi.K_EDGE_WGRAD]
     _capi.profile_enable(True, edge_classes)
     for _ in range(a.warmup):
         step()
@@ -299,7 +305,7 @@ def run_workload(k, dtype, a, g=None):
     torch.cuda.synchronize()
     prof = _capi.profile_read()
     _capi.profile_enable(False)
-    for cls in ("fwd_edge", "bwd_edge"):   # the roofline's kernels: the timed steps' own records
+    for cls in ("fwd_edge", "bwd_edge", "edge_wgrad"):   # the roofline's kernels: the timed steps' own records
         prof[cls] = (timed[cls][0] * nprof / a.steps, timed[cls][1] * nprof / a.steps)
 
     s = 2 if dt == torch.bfloat16 else 4
@@ -309,7 +315,7 @@ def run_workload(k, dtype, a, g=None):
 
     def executed_per_launch(cls, launches_per_step):
         fl, by = kernel_work(cls, path, N, E, H, H, H, H, FE, g1, s)
-        if cls == "wgrad":   # a class of several launches per layer: the average launch
+        if cls in ("wgrad", "edge_wgrad", "bwd_edge"):   # whole-layer work over the layer's launches
             return fl * L / launches_per_step, by * L / launches_per_step
         return fl, by
 
@@ -335,13 +341,19 @@ def run_workload(k, dtype, a, g=None):
     # one layer's launches of the class (one, or one per edge chunk of the one-wave-per-tile backward)
     per_layer = kern[dom]["launches_per_step"] / L
     dur_s = kern[dom]["ms_per_launch"] * per_layer / 1e3
+    xf, xb = kernel_work(dom, path, N, E, H, H, H, H, FE, g1, s)     # the layer's work
+    handed = dom == "bwd_edge" and "edge_wgrad" in kern
+    if handed:   # the factor products finish the backward kernel's weight gradients: the same layer's work
+        dur_s += kern["edge_wgrad"]["ms_per_launch"] * kern["edge_wgrad"]["launches_per_step"] / L / 1e3
+        ef, eb = kernel_work("edge_wgrad", path, N, E, H, H, H, H, FE, g1, s)
+        xf, xb = xf + ef, xb + eb
     fl, by = path_model(dom, N, E, H, H, H, H, FE, g1, s)
     roof = bound(fl, by, dur_s)
     name = DESCR[k].split(":")[0]
-    roof["traffic"] = read_traffic(name, dtype, dom)
-    xf, xb = executed_per_launch(dom, kern[dom]["launches_per_step"])
-    roof.update(kernel=dom, ms_per_launch=kern[dom]["ms_per_launch"], launches_per_layer=per_layer,
-                algorithmic_flops=fl, algorithmic_bytes=by,
+    traffic = [read_traffic(name, dtype, c) for c in ((dom, "edge_wgrad") if handed else (dom,))]
+    roof["traffic"] = None if None in traffic else sum(traffic)
+    roof.update(kernel=dom + ("+edge_wgrad" if handed else ""), ms_per_launch=kern[dom]["ms_per_launch"],
+                launches_per_layer=per_layer, ms_per_layer=dur_s * 1e3, algorithmic_flops=fl, algorithmic_bytes=by,
                 executed=dict(flops=xf, bytes=xb, **{kk: v for kk, v in bound(xf, xb, dur_s).items()
                                                      if kk in ("bound", "frac")}))
     # the whole step against the per-edge model of every layer's forward and backward
@@ -372,14 +384,18 @@ def run_workload(k, dtype, a, g=None):
 
 
 def probe_identity(a, k=5):
-    """Gather / segment-sum data movement of the MPNN layer alone: the edge kernels with the MLP
-    replaced by identity (EGNN_FLAG_PROBE_IDENTITY, an instrument), one layer forward + backward per
-    step, on the full power-law graph.  Bytes per kernel, every gathered row counted once per edge:
-      forward:      E (8 + 2 H s + F_E s) + N O s      (indices, P_i and Q_j, edge features; row sums out)
-      backward:     E (8 + O s + H s + H / 4) + N H s (indices, the row's message gradient; dL/dpre1 out,
-                                                    its row sums: dP rows, fp32 carries of the split rows)
-      node reduce:  E (H s + 4) + N (8 + H s)         (dL/dpre1 by source, CSC ids; dQ out)
-      fix-ups:      E H / 4 each                      (the carries of the split rows, forward and backward)"""
+    """Gather / segment-sum data movement of the MPNN layer alone: the edge-parallel kernels with the MLP
+    replaced by identity (EGNN_FLAG_PROBE_IDENTITY, an instrument: the same kernels, the same gathers, row
+    sums, stores and carries, without the products and elementwise work of the MLP), one layer forward +
+    backward per step, on the full power-law graph.  Bytes per kernel, every gathered row counted once
+    per edge:
+      forward:      E (8 + 2 H s + F_E s) + N O s        (indices, P_i and Q_j, edge features; row sums out)
+      backward:     E (8 + 2 H s + F_E s + O s + H s + H / 4) + N H s
+                                                        (indices, P_i and Q_j, edge features, the row's
+                                                        message gradient; dL/dpre1 out, its row sums: dP
+                                                        rows and fp32 carries of the split rows)
+      node reduce:  E (H s + 4) + N (8 + H s)           (dL/dpre1 by source, CSC ids; dQ out)
+      fix-ups:      E H / 4 each                        (the carries of the split rows, forward and backward)"""
     import torch
     from pymolecular_amd import _capi, fused, graphs
     g = graphs.make_workload(k)
@@ -410,7 +426,7 @@ def probe_identity(a, k=5):
     _capi.profile_enable(False)
     model = {"fwd_edge": E * (8 + 2 * H * s + FE * s) + N * H * s,
              "fwd_fixup": E * H / 4,
-             "bwd_edge": E * (8 + H * s + H * s + H / 4) + N * H * s,
+             "bwd_edge": E * (8 + 2 * H * s + FE * s + H * s + H * s + H / 4) + N * H * s,
              "node_reduce": E * (H * s + 4) + N * (8 + H * s)}
     out = {}
     tot_b = tot_t = 0.0
@@ -422,8 +438,8 @@ def probe_identity(a, k=5):
         tot_b += nbytes
         tot_t += ms
     gbs = tot_b / (tot_t / 1e3) / 1e9
-    return {"metric": "HBM fraction of the gather / segment-sum portion (identity-MLP instrument of the MPNN "
-                      "edge kernels)", "value": gbs / PEAK["hbm_gbs"], "unit": "fraction of 8 TB/s",
+    return {"metric": "HBM fraction of the gather / segment-sum portion (identity-MLP instrument of the "
+                      "edge-parallel MPNN kernels)", "value": gbs / PEAK["hbm_gbs"], "unit": "fraction of 8 TB/s",
             "achieved_gbs": gbs, "config": {"workload": DESCR[k], "N": N, "E": E, "steps": a.steps},
             "kernels": out}
 
@@ -435,11 +451,11 @@ def main():
               "multi-GPU sharding of this layer is designed but not built", file=sys.stderr)
         sys.exit(2)
     import torch
-    todo = ALL if a.all else [(a.workload, a.dtype)]
+    todo = [] if a.probe_only else ALL if a.all else [(a.workload, a.dtype)]
     for k, dtype in todo:
         out = run_workload(k, dtype, a)
         print(json.dumps(out), flush=True)
-    if a.probe:
+    if a.probe or a.probe_only:
         print(json.dumps(probe_identity(a)), flush=True)
     if a.copy_probe:
         src = torch.empty(64 << 20, dtype=torch.float32, device="cuda:0").fill_(1.0)

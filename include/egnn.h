@@ -83,11 +83,13 @@ typedef struct EgnnDims {
                           into out_mov, and egnn_bwd writes grad_out_mov + (d agg_x / d coord)^T
                           grad_out_mov into grad_coord, the whole gradient of x' with respect to x;
                           EGNN_FLAG_PROBE_IDENTITY: an instrument, not the layer: egnn_fwd / egnn_bwd
-                          run the edge kernels with the MLP replaced by identity (message P_i + Q_j +
-                          W_u e without SiLU or W_hl; dL/dpre1 = grad_out_msg of the row) and keep their
-                          gathers, tile schedule and row / source sums, so that the data movement of
-                          the gather / segment-sum portion can be timed alone.  bf16 MPNN at H = 128
-                          only; the outputs are not the layer's */
+                          run the layer's edge-parallel kernels with the MLP replaced by identity
+                          (message P_i + Q_j + W_u e without SiLU or W_hl; dL/dpre1 = grad_out_msg of
+                          the row) and keep their gathers, tile schedule, Gh stores and row / source
+                          sums, so that the data movement of the gather / segment-sum portion can be
+                          timed alone.  bf16 MPNN at H = 128 within those kernels' limits only
+                          (EGNN_ERR_DIMS otherwise: it never times another kernel); the outputs are
+                          not the layer's */
 } EgnnDims;
 
 #define EGNN_WEIGHTS_PACKED 0
@@ -256,16 +258,19 @@ int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, co
  * the previous records.  egnn_profile_read synchronises on those events and
  * returns the summed device time and the launch count of one class.  Off by
  * default.  Not thread-safe; for benchmarks only. */
-#define EGNN_PROFILE_ALL 0xFF
+#define EGNN_PROFILE_ALL 0x1FF
 #define EGNN_K_FWD_EDGE 0     /* fused forward edge kernel             */
 #define EGNN_K_FWD_FIXUP 1    /* forward split/empty-row fix-up         */
 #define EGNN_K_BWD_EDGE 2     /* fused backward edge kernel            */
 #define EGNN_K_NODE_GEMM 3    /* per-node projection GEMMs (P|Q, dh)   */
-#define EGNN_K_WGRAD 4        /* weight-gradient split-K GEMMs + sums  */
+#define EGNN_K_WGRAD 4        /* node-side weight-gradient GEMMs + sums */
 #define EGNN_K_NODE_REDUCE 5  /* CSR/CSC node gradient reduction       */
 #define EGNN_K_PREP 6         /* weight-fragment preparation           */
 #define EGNN_K_NODE_UPDATE 7  /* node update GEMMs (egnn_node_fwd/bwd) */
-#define EGNN_K_COUNT 8
+#define EGNN_K_EDGE_WGRAD 8   /* weight-gradient products over per-edge
+                                 factors the backward edge kernel stored
+                                 (H = 256 and one-wave-per-tile paths)  */
+#define EGNN_K_COUNT 9
 int32_t egnn_profile_enable(int32_t class_mask);
 int32_t egnn_profile_read(int32_t kernel_class, double* total_ms, int64_t* launches);
 

@@ -29,8 +29,10 @@ EXPORTED = (
 )
 
 # kernel classes of the instrumentation hook
-K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP, K_NODE_UPDATE = range(8)
-K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep", "node_update")
+(K_FWD_EDGE, K_FWD_FIXUP, K_BWD_EDGE, K_NODE_GEMM, K_WGRAD, K_NODE_REDUCE, K_PREP, K_NODE_UPDATE,
+ K_EDGE_WGRAD) = range(9)
+K_NAMES = ("fwd_edge", "fwd_fixup", "bwd_edge", "node_gemm", "wgrad", "node_reduce", "prep", "node_update",
+           "edge_wgrad")
 
 
 WEIGHTS_PACKED, WEIGHTS_LINEAR = 0, 1   # include/egnn.h EGNN_WEIGHTS_*

@@ -192,6 +192,8 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.carry = w.carry;
   a.fix_rows = v.fix_rows; a.n_fix = v.n_fix; a.tile_tab = v.tile_tab;
   a.geo = w.geo;
+  // the edge-parallel MPNN forward addresses message rows by 32-bit byte offsets: the instrument runs it only
+  if (s.probe && s.N * a.smsg * 2 >= (int64_t(1) << 31)) return EGNN_ERR_DIMS;
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
     const int r = coop_supported(s) ? launch_coop_fwd(s, a, st)
@@ -275,11 +277,12 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
 
   // weight gradients: split-K GEMMs over edges / nodes, then fixed-order sums
   // per-edge factor products of the one-wave-per-tile path: [A | 1]^T B over the edges
+  // (instrumented as EGNN_K_EDGE_WGRAD: work the edge kernel handed over, part of the fused backward)
   auto splitk2 = [&](Gemm2Args g, float* dst) -> int32_t {
     g.ksplit = splitk_len(g.M, g.N, g.K, s.bf16);
     g.partial = w.part;
     const int64_t nsplit = cdiv(std::max<int64_t>(g.K, 1), g.ksplit);
-    ProfScope ps(EGNN_K_WGRAD, st);
+    ProfScope ps(EGNN_K_EDGE_WGRAD, st);
     if (nsplit * g.M * g.N > w.part_elems) return EGNN_ERR_WORKSPACE;
     int32_t r = s.E > 0 ? hip_status(launch_gemm2(g, s.bf16, st)) : EGNN_OK;
     if (r != EGNN_OK) return r;
@@ -299,7 +302,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       m.B = w.Dgq; m.ldb = s.M; m.b_bf16 = 1; m.b_nc = 1;
       if ((rc = splitk2(m, w.dW1m)) != EGNN_OK) return rc;   // [dW1_mov ; dbx1]
       // dw2_mov | dw_d (adjacent): the kernel's per-block partials, summed in block order
-      ProfScope ps(EGNN_K_WGRAD, st);
+      ProfScope ps(EGNN_K_EDGE_WGRAD, st);
       if ((rc = hip_status(launch_sum_rows(w.dwpart, s.E > 0 ? w.nblk : 0, w.LW, w.dw2m, st))) != EGNN_OK) return rc;
     }
   }
@@ -337,7 +340,7 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       }
     }
     if (w.nchunk > 1) {
-      ProfScope ps(EGNN_K_WGRAD, st);
+      ProfScope ps(EGNN_K_EDGE_WGRAD, st);
       if ((rc = hip_status(launch_sum_rows(w.chunkres, w.nchunk, Lw, w.dWhl, st))) != EGNN_OK) return rc;
       if (s.eq) {
         const float* res_m = w.chunkres + w.nchunk * Lw;

@@ -42,10 +42,7 @@ using namespace tile;
 // memory is carried in registers from one tile to the next and the loads a
 // wave waits on are never followed by loads under a branch (either makes the
 // compiler wait for every outstanding load).
-// ID (instrument only, the layer with the MLP replaced by identity: MPNN): the message is
-// P_i + Q_j + W_u e with no SiLU and no W_hl product; the gathers, the tile schedule and the
-// per-row sums are those of the layer.
-template <int H, int O, int M, int W, bool EQ, bool ID = false>
+template <int H, int O, int M, int W, bool EQ>
 __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
   constexpr int BH = H / W / 16, BO = O / W / 16, BM = M / W / 16;
   constexpr int KH = H / 32, KO = O / 32;
@@ -165,7 +162,6 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
     }
   };
   // ---- S1: m1 = SiLU(W_u U + P_i + Q_j) for the wave's H rows, into s_m1[par]
-  f32x4 m1keep[BH][2];   // ID: the messages of the next tile, kept in registers from S1 to S2
   auto stage1 = [&](int slot, int par) {
     bf16x8 u[2];
 #pragma unroll
@@ -188,14 +184,10 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
         f32x4 acc = zero4();
         mma(acc, wu[j], u[nb]);
         mma(acc, Ipq, pq[j][nb]);   // + P_i + Q_j
-        if constexpr (ID) {
-          m1keep[j][nb] = acc;
-        } else {
-          f32x4 x;
+        f32x4 x;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
-          put_chain(s_m1[par], hb, nb, l, x);
-        }
+        for (int i = 0; i < 4; ++i) x[i] = silu_t<bf16>(acc[i]);
+        put_chain(s_m1[par], hb, nb, l, x);
       }
     }
   };
@@ -233,10 +225,6 @@ __global__ __launch_bounds__(W * 64, 4) void coop_fwd_kernel(FwdArgs a) {
       const f32x4 b2v = *reinterpret_cast<const f32x4*>(s_b2 + 16 * ob + 4 * g);
 #pragma unroll
       for (int nb = 0; nb < 2; ++nb) {
-        if constexpr (ID) {
-          mreg[j][nb] = m1keep[j][nb];
-          continue;
-        }
         f32x4 acc = b2v;
 #pragma unroll
         for (int kc = 0; kc < KH; ++kc) mma(acc, whlT[j][kc], get_chain(s_m1[par], kc, nb, l));
@@ -1217,345 +1205,13 @@ __global__ __launch_bounds__(512) void coop_bwd_eq_kernel(BwdArgs a) {
   }
 }
 
-// ---------------------------------------------------------------------------
-// backward of the non-equivariant layer (MPNN), H = O = 128, 16 waves per tile
-// ---------------------------------------------------------------------------
-// Launched only as the identity-MLP instrument (ID); the layer's backward is the
-// edge-parallel kernel of egnn_mpnn.hip.  Wave w owns feature rows [16 rb, 16 rb + 16), rb = w & 7, of every stage for
-// the 16 edges of half hf = w >> 3 of the tile.  Compared with one wave per row
-// block over both halves, each wave holds half the per-edge state, so 16 waves
-// (4 per SIMD) fit one CU and hide each other's latencies.  The edge-major
-// operand of dW_hl is assembled in LDS from the two halves; the row-block owner
-// of half hf accumulates the columns [64 hf, 64 hf + 64) over all 32 edges.
-// Per-row sums over the edges (db2, dW_e) are per-half partials combined at the
-// end in half order.  Same stages and results as coop_bwd_kernel<..., false>.
-// Two barrier intervals per tile: [S2, S4] (each wave needs only its own s2 for
-// S4) and [S5, S1 of the next tile]; m1 and the edge-feature tile are kept by
-// tile parity.  Indices pass through an LDS ring of three tiles and the next
-// tile's gathers are issued at the top of this tile, as in coop_bwd_eq_kernel.
-// ID (instrument only): the layer with the MLP replaced by identity, g_a1 = the incoming message
-// gradient of row i; the index ring, the gathers of that gradient and the Gh stores are the layer's.
-template <int NU, bool ID = false>
-__global__ __launch_bounds__(1024) void mpnn_bwd16_kernel(BwdArgs a) {
-  constexpr int H = 128, O = 128, NRB = 8;
-  constexpr int KH = H / 32, KO = O / 32;
-  constexpr int NUS = NU > 0 ? 16 * NU : 8;         // slot rows of the edge-feature tile
-  constexpr int CH = KH * 2 * 64 * 8;               // chain buffer: 4 chunks x 2 halves (8 KB)
-  static_assert(CH == NRB * 64 * 8, "chain and edge-major buffers share one size");
-  // activation buffers, one array so that the final reduction can use all of it:
-  //   [0] g_a2 (S4 -> S5)  [1] g_a2 edge-major (S4 -> S5)  [2 + p] m1 (S1 -> S2)  [4 + p] m1 edge-major (S1 -> S5)
-  __shared__ __attribute__((aligned(16))) bf16 s_act[6 * CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_whl[NRB * KO * kFragElems];    // A fragments of W_hl (S5)
-  __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // A fragments of W_hl^T (S2)
-  __shared__ __attribute__((aligned(16))) bf16 s_u[2][NUS * TE];   // edge features, slot-major (put_ut)
-  __shared__ __attribute__((aligned(16))) float s_b2[O];
-  __shared__ int s_ri[3][TE], s_rj[3][TE], s_eid[3][NU > 0 ? TE : 1], s_ex[3][2];
-  // destination sums, by tile parity: g_a1 edge-major (written in S5, summed in the next tile), the
-  // B operands S[edge][rank] of the two rank blocks, the target of each rank (a row >= 0, carry
-  // slot 0 / 1 as -1 / -2, none -3) and the rank count; the row and span of each rank and the 0/1
-  // patterns of the segment matrix are the table wave's scratch
-  __shared__ __attribute__((aligned(16))) bf16 s_g1N[2 * CH];
-  __shared__ __attribute__((aligned(16))) bf16 s_segB[2][2][64 * 8];
-  __shared__ int s_tgt[2][TE], s_nrk[2];
-  __shared__ int s_rowof[TE], s_rspan[TE];
-  __shared__ uint2 s_lut[16];
-  seg_lut_init(s_lut, threadIdx.x);
-  bf16* const s_ga2 = s_act;
-  bf16* const s_ga2N = s_act + CH;
-
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  const int rb = w & 7, hf = w >> 3;
-  const bf16* PQ = (const bf16*)a.PQ;
-  const bf16* ef = (const bf16*)a.ef;
-  const bf16* gmsg = (const bf16*)a.gmsg;
-  bf16* Gh = (bf16*)a.Gh;
-  const int64_t E = a.E;
-  const int N = (int)a.N;
-  const int FE = a.FE;
-  const int64_t G = gridDim.x;
-  constexpr int LDW = 15;   // loader wave
-
-  for (int q = threadIdx.x; q < O; q += 1024) s_b2[q] = a.fr.b2f[q];
-  // slot rows at and past F_E stay zero (the tile loop writes rows below F_E only)
-  for (int q = FE * TE + threadIdx.x; q < NUS * TE; q += 1024) s_u[0][q] = s_u[1][q] = (bf16)0.0f;
-  for (int q = threadIdx.x; q < NRB * KO * kFragElems / 8; q += 1024)
-    reinterpret_cast<bf16x8*>(s_whl)[q] = reinterpret_cast<const bf16x8*>(a.fr.hl)[q];
-  for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 1024)
-    reinterpret_cast<bf16x8*>(s_whlT)[q] = reinterpret_cast<const bf16x8*>(a.fr.hlT)[q];
-  const bf16x8 wu = load_chunk((const bf16*)a.fr.u + (int64_t)rb * kFragElems + l * 8);
-  const bf16x8 I = ident_chunk(c, g);
-
-  // weight-gradient accumulators: dW_hl columns [64 hf, 64 hf + 64) of the wave's rows
-  f32x4 acc_whl[4], acc_wu[NU > 0 ? NU : 1];
-  f32x4 vb2 = zero4();
-#pragma unroll
-  for (int cb = 0; cb < 4; ++cb) acc_whl[cb] = zero4();
-#pragma unroll
-  for (int ub = 0; ub < (NU > 0 ? NU : 1); ++ub) acc_wu[ub] = zero4();
-
-  // ring loads (every wave issues and waits for them; the loader wave stores the slot): lanes
-  // 0..31 the tile's edges, lanes 32 and 33 the edges just before and after it (their rows)
-  const int32_t* eidp = (NU > 0 && a.eids) ? a.eids : a.erow;   // a.erow: a stand-in read, ignored
-  int ld_ri, ld_rj, ld_eid = 0;
-  auto load_idx = [&](int64_t tt) {   // edge ids below 2^31 (coop_supported)
-    const uint32_t eb = (uint32_t)(tt * TE);
-    const uint32_t e0 = l < TE ? eb + l : (l == TE ? eb - 1u : eb + TE);   // eb - 1 at eb = 0: clamped
-    const uint32_t e = e0 < (uint32_t)E ? e0 : (uint32_t)E - 1;
-    ld_ri = a.erow[e];
-    ld_rj = a.col[e];
-    if constexpr (NU > 0) ld_eid = eidp[e];
-  };
-  auto store_idx = [&](int slot, int64_t tt) {
-    asm volatile("" ::"v"(ld_ri), "v"(ld_rj), "v"(ld_eid));
-    if (w == LDW && l < TE) {
-      const int e = (int)(tt * TE) + l;
-      s_ri[slot][l] = clampi(ld_ri, N);
-      s_rj[slot][l] = clampi(ld_rj, N);
-      if constexpr (NU > 0) s_eid[slot][l] = a.eids ? clampi(ld_eid, (int)E) : (e < (int)E ? e : (int)E - 1);
-    } else if (w == LDW && l < TE + 2) {
-      s_ex[slot][l - TE] = clampi(ld_ri, N);
-    }
-  };
-  // ---- destination sums of tile tt (parity p), by the waves of half 0, row block rb: per-rank
-  // sums D = g_a1 S against the tile's 0/1 segment matrix; a rank that is a whole row is stored to
-  // dP, the partial first / last ranks to the tile's carry slots 0 / 1 (summed in tile order by
-  // the fix-up)
-  auto dst_sums = [&](int64_t tt, int p) {
-    const int nrk = __builtin_amdgcn_readfirstlane(s_nrk[p]);
-    const bf16x8 A = get_norm(s_g1N + p * CH, rb, l);
-    auto block = [&](int q) {
-      f32x4 D = zero4();
-      mma(D, A, get_norm(s_segB[p][q], 0, l));
-      const int tg = s_tgt[p][16 * q + c];
-      if (tg >= 0)
-        *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * rb + 4 * g) = pack4(D);
-      else if (tg > -3)
-        *reinterpret_cast<f32x4*>(a.carry + ((int64_t)tt * 2 - 1 - tg) * O + 16 * rb + 4 * g) = D;
-    };
-    block(0);
-    if (nrk > 16) block(1);
-  };
-  // rank tables of tile tt from ring slot sl into parity p (one wave): the segment-matrix operands
-  // and the targets of its ranks
-  auto rank_tables = [&](int64_t tt, int sl, int p) {
-    const TileRanks rk = tile_ranks(s_ri[sl], s_ex[sl], tt * TE, E, l);
-    tile_rank_tables(s_ri[sl], rk, l, s_rowof, s_rspan);
-    // the lanes read what other lanes of this wave wrote: LDS accesses of one wave complete in
-    // order, so only the compiler must keep the order (no memory wait, which would also wait for
-    // the next tile's gathers)
-    asm volatile("" ::: "memory");
-    for (int q = 0; q < (rk.nrank > 16 ? 2 : 1); ++q) {
-      const int r = 16 * q + c;
-      const bool has = r < rk.nrank;
-      put_norm(s_segB[p][q], 0, l, seg_chunk_span(has ? s_rspan[r] : 0, g, s_lut));
-      if (g == 0) s_tgt[p][r] = !has ? -3 : rank_whole(rk, r) ? s_rowof[r] : (r == 0 ? -1 : -2);
-    }
-    if (l == 0) s_nrk[p] = rk.nrank;
-  };
-  // the gathers of S1 from a ring slot: the wave's P_i, Q_j and (F_E > 0) edge-feature chunk
-  bf16x8 pq;
-  bf16x8 ue;
-  const bf16x8 Ipq = pq_sum_chunk(c, g);
-  auto gather = [&](int slot) {
-    const int k = hf * 16 + c;
-    if constexpr (NU > 0)   // slots past F_E read slot 0 and are dropped in S1
-      ue = load_chunk(ef + (int64_t)s_eid[slot][k] * a.se + (8 * g + 8 <= FE ? 8 * g : 0));
-    pq = pq_gather((const char*)PQ, (uint32_t)s_ri[slot][k], (uint32_t)s_rj[slot][k], rb, g, H);
-  };
-  // ---- S1 of tile tt: m1 (chain and edge-major, buffers of parity par), s1 = SiLU'(pre1)
-  auto stage1 = [&](int64_t tt, int par, bf16x4& s1o) {
-    // No masks on the edge features: chunks past F_E (a copy of slot 0's chunk) meet zero columns of
-    // W_u, and the edges past E (indices clamped to real rows) have g_a2 = 0, so they add nothing to dW_e.
-    const bf16x8 u = NU > 0 ? ue : zero_chunk<bf16>();
-    if (NU > 0 && rb == 0 && 8 * g < FE)   // the tile's edge features, slot-major, for dW_e
-      put_ut(s_u[par], hf, c, g, u);
-    f32x4 acc = zero4();
-    mma(acc, wu, u);
-    mma(acc, Ipq, pq);   // + P_i + Q_j
-    f32x4 y, d;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const YD r = silu_yd<bf16>(acc[i]);
-      y[i] = r.y;
-      d[i] = r.d;
-    }
-    s1o = pack4(d);
-    put_chain(s_act + (2 + par) * CH, rb, hf, l, y);
-    *reinterpret_cast<bf16x4*>(s_act + (4 + par) * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(y, I));
-  };
-
-  // the incoming message gradient of the wave's rows, loaded one tile ahead of its use in S4 (the
-  // only value carried from one tile to the next: at the top of a tile it is a tile old, so the
-  // memory wait there finds it complete)
-  bf16x4 gmr_next;
-  auto load_gm = [&](int slot) {
-    const uint32_t ri = (uint32_t)s_ri[slot][hf * 16 + c];
-    gmr_next = *reinterpret_cast<const bf16x4*>(gmsg + (uint64_t)ri * (uint32_t)a.sgm + 16 * rb + 4 * g);
-  };
-  bf16x4 s1;
-  if (blockIdx.x < a.ntiles) {
-    const int64_t t1 = blockIdx.x + G < a.ntiles ? blockIdx.x + G : blockIdx.x;
-    load_idx(blockIdx.x);
-    store_idx(0, blockIdx.x);
-    load_idx(t1);
-    store_idx(1, t1);
-  }
-  __syncthreads();   // weights, vectors and the first two ring slots in LDS
-  if (blockIdx.x < a.ntiles) load_gm(0);
-  if (!ID && blockIdx.x < a.ntiles) {
-    gather(0);
-    stage1(blockIdx.x, 0, s1);
-  }
-  asm volatile("" ::"v"(gmr_next));   // complete on entry to the tile loop, as at its back edge
-  __syncthreads();   // m1 of the first tile
-
-  int par = 0, sl0 = 0;
-  int64_t t = blockIdx.x;
-  for (; t < a.ntiles; t += G, par ^= 1, sl0 = sl0 == 2 ? 0 : sl0 + 1) {
-    const int sl1 = sl0 == 2 ? 0 : sl0 + 1, sl2 = sl1 == 2 ? 0 : sl1 + 1;   // ring slots of t + 1, t + 2
-    const int64_t base = t * TE;
-    const bool valid = (int)base + hf * 16 + c < (int)E;
-    // the incoming message gradient of the wave's rows (used in S4), the next tile's
-    // gathers (its S1 runs at the end of this tile), the indices of the tile after it
-    const bf16x4 gmr = gmr_next;
-    load_gm(sl1);
-    if constexpr (!ID) gather(sl1);
-    const int64_t t2 = t + 2 * G < a.ntiles ? t + 2 * G : t;
-    load_idx(t2);
-    if constexpr (ID) {
-      if (hf == 0 && t != (int64_t)blockIdx.x) dst_sums(t - G, par ^ 1);
-      const f32x4 gm = valid ? unpack4(gmr) : zero4();
-      *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(gm);
-      *reinterpret_cast<bf16x4*>(s_g1N + par * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(gm, I));
-      if (w == 8) rank_tables(t, sl0, par);
-      store_idx(sl2, t2);
-      __syncthreads();
-      continue;
-    }
-
-    // ---- S2: s2 = SiLU'(W_hl^T m1 + b2) -------------------------------------------
-    f32x4 s2;
-    {
-      f32x4 acc = *reinterpret_cast<const f32x4*>(s_b2 + 16 * rb + 4 * g);
-#pragma unroll
-      for (int kc = 0; kc < KH; ++kc)
-        mma(acc, *reinterpret_cast<const bf16x8*>(s_whlT + ((rb * KH + kc) * 64 + l) * 8),
-            get_chain(s_act + (2 + par) * CH, kc, hf, l));
-#pragma unroll
-      for (int i = 0; i < 4; ++i) s2[i] = silu_yd<bf16>(acc[i]).d;
-    }
-    // ---- S4: g_a2 = gm_i SiLU'(pre2), in the same interval (own rows only) --------
-    {
-      const f32x4 gm = valid ? unpack4(gmr) : zero4();   // zero g_a2 on the edges past E
-      const f32x4 d = s2;
-      f32x4 ga;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        ga[i] = gm[i] * d[i];
-        vb2[i] += ga[i];
-      }
-      put_chain(s_ga2, rb, hf, l, ga);
-      *reinterpret_cast<bf16x4*>(s_ga2N + (rb * 64 + l) * 8 + 4 * hf) = pack4(transpose_block(ga, I));
-    }
-    // the destination sums of the previous tile (half 0) and the rank tables of this one (a wave of
-    // half 1)
-    if (hf == 0 && t != (int64_t)blockIdx.x) dst_sums(t - G, par ^ 1);
-    if (w == 8) rank_tables(t, sl0, par);
-    __syncthreads();
-
-    // ---- S5: g_a1 = (W_hl g_a2) SiLU'(pre1) ------------------------------------------
-    {
-      f32x4 acch = zero4();
-#pragma unroll
-      for (int kc = 0; kc < KO; ++kc)
-        mma(acch, *reinterpret_cast<const bf16x8*>(s_whl + ((rb * KO + kc) * 64 + l) * 8), get_chain(s_ga2, kc, hf, l));
-      const f32x4 d = unpack4(s1);
-      f32x4 g1;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) g1[i] = acch[i] * d[i];
-      // Gh has a row for every edge slot of the last tile (rows past E are never read)
-      *reinterpret_cast<bf16x4*>(Gh + (base + hf * 16 + c) * H + 16 * rb + 4 * g) = pack4(g1);
-      // g_a1 edge-major (zero on the edges past E) for the destination sums in the next tile
-      const f32x4 g1T = transpose_block(g1, I);
-      *reinterpret_cast<bf16x4*>(s_g1N + par * CH + (rb * 64 + l) * 8 + 4 * hf) = pack4(g1T);
-      // dW_hl rows rb, columns of half hf: sum_e m1[h][e] g_a2[o][e]
-      const bf16x8 m1N = get_norm(s_act + (4 + par) * CH, rb, l);
-#pragma unroll
-      for (int cb = 0; cb < 4; ++cb) mma(acc_whl[cb], m1N, get_norm(s_ga2N, 4 * hf + cb, l));
-      // dW_e rows rb: sum over this half's edges of g_a1[h][e] e[e][slot] (the other half's slots are zero)
-      if constexpr (NU > 0) {
-        const bf16x8 ga1N = half_edge_chunk(g1T, hf);
-#pragma unroll
-        for (int ub = 0; ub < NU; ++ub) {
-          if (16 * ub >= FE) continue;   // column block past the edge features
-          mma(acc_wu[ub], ga1N, get_ut(s_u[par], 16 * ub + c, g));   // slots past F_E read zero rows
-        }
-      }
-    }
-    // ---- S1 of the next tile (past the last tile: of a stand-in tile, never read), ring slot of t + 2
-    stage1(t + G, par ^ 1, s1);
-    store_idx(sl2, t2);
-    // the next tile's message-gradient rows, waited for here (a tile after their load) and not at
-    // the top of the next tile, where the wait would also cover this tile's Gh store
-    asm volatile("" ::"v"(gmr_next));
-    __syncthreads();
-  }
-
-  // the destination sums of the block's last tile (parity par ^ 1)
-  if (hf == 0 && (int64_t)blockIdx.x < a.ntiles) dst_sums(t - G, par ^ 1);
-
-  // ---- this block's weight-gradient partial ---------------------------------
-  // db2 is first summed over the wave's 16 edge lanes; half 1 then leaves its
-  // partials in LDS and half 0 adds them after its own (fixed order).
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    vb2[i] += shfl_xor(vb2[i], 1); vb2[i] += shfl_xor(vb2[i], 2); vb2[i] += shfl_xor(vb2[i], 4); vb2[i] += shfl_xor(vb2[i], 8);
-  }
-  constexpr int NUR = NU > 0 ? NU : 1;
-  float* const red_v = reinterpret_cast<float*>(s_act);          // [rb][16 rows]
-  float* const red_u = red_v + NRB * 16;                          // [rb][ub][lane][4]
-  static_assert((NRB * 16 + NRB * NUR * 64 * 4) * 4 <= 6 * CH * 2, "reduction exceeds the LDS buffers");
-  if (hf == 1) {
-    if (c == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) red_v[rb * 16 + 4 * g + i] = vb2[i];
-    }
-#pragma unroll
-    for (int ub = 0; ub < NUR; ++ub)
-      *reinterpret_cast<f32x4*>(red_u + ((rb * NUR + ub) * 64 + l) * 4) = acc_wu[ub];
-  }
-  __syncthreads();
-  float* P = a.dwpart + (int64_t)blockIdx.x * a.LW;
-  const int64_t oWE = (int64_t)(H + 1) * O;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int row = 16 * rb + 4 * g + i;
-#pragma unroll
-    for (int cb = 0; cb < 4; ++cb) P[(int64_t)row * O + 64 * hf + 16 * cb + c] = acc_whl[cb][i];
-  }
-  if (hf == 0) {
-#pragma unroll
-    for (int ub = 0; ub < NU; ++ub) {
-      const f32x4 o = *reinterpret_cast<const f32x4*>(red_u + ((rb * NUR + ub) * 64 + l) * 4);
-      const int slot = 16 * ub + c;
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (slot < FE) P[oWE + (int64_t)(16 * rb + 4 * g + i) * FE + slot] = acc_wu[ub][i] + o[i];
-    }
-    if (c == 0) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) P[(int64_t)H * O + 16 * rb + 4 * g + i] = vb2[i] + red_v[rb * 16 + 4 * g + i];
-    }
-  }
-}
-
-template <int H, int O, int M, int W, bool EQ, bool ID = false>
+template <int H, int O, int M, int W, bool EQ>
 int launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (a.ntiles > 0) {
     // one resident round: 4 waves per SIMD (the launch bound), 16 waves per CU, on 256 CUs; a
     // second round would repeat the weight prologue of every block
     const int blocks = (int)std::min<int64_t>(a.ntiles, 256 * (16 / W));
-    hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ, ID>), dim3(blocks), dim3(W * 64), 0, st, a);
+    hipLaunchKernelGGL((coop_fwd_kernel<H, O, M, W, EQ>), dim3(blocks), dim3(W * 64), 0, st, a);
   }
   return (int)hipGetLastError();
 }
@@ -1569,11 +1225,6 @@ int launch_bwd_eq(const BwdArgs& a, int nblk, hipStream_t st) {
     else
       hipLaunchKernelGGL((coop_bwd_eq_kernel<2>), dim3(nblk), dim3(512), 0, st, a);
   }
-  return (int)hipGetLastError();
-}
-
-int launch_mpnn_bwd16_probe(const BwdArgs& a, int nblk, hipStream_t st) {
-  if (a.ntiles > 0) hipLaunchKernelGGL((mpnn_bwd16_kernel<0, true>), dim3(nblk), dim3(1024), 0, st, a);
   return (int)hipGetLastError();
 }
 
@@ -1599,9 +1250,9 @@ bool coop_supported(const LayerShape& s) {
          s.E + kTileEdges < (int64_t(1) << 31);
 }
 
-// The MPNN H = 128 layer runs the edge-parallel kernels (egnn_mpnn.hip); the cooperative MPNN kernels
-// remain as the identity-MLP instrument (EGNN_FLAG_PROBE_IDENTITY).
-static bool mpnn_ep(const LayerShape& s) { return !s.eq && s.H == 128 && !s.probe; }
+// The MPNN H = 128 layer runs the edge-parallel kernels (egnn_mpnn.hip), and so does its identity-MLP
+// instrument (EGNN_FLAG_PROBE_IDENTITY).
+static bool mpnn_ep(const LayerShape& s) { return !s.eq && s.H == 128; }
 
 bool coop_dst_sums(const LayerShape& s) { return coop_supported(s) && !s.eq && s.H == 128; }
 
@@ -1617,16 +1268,16 @@ int64_t coop_dw_len(const LayerShape& s) {
 }
 
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
-  if (s.probe) return launch_fwd_t<128, 128, 128, 8, false, true>(a, st);   // make_shape: MPNN, H = 128
-  // the edge-parallel forward addresses the message rows by 32-bit byte offsets
-  if (mpnn_ep(s) && s.N * a.smsg * 2 < (int64_t(1) << 31)) return launch_mpnn_fwd_ep(a, st);
+  // the edge-parallel forward addresses the message rows by 32-bit byte offsets (make_shape refuses the
+  // instrument beyond them)
+  if (mpnn_ep(s) && s.N * a.smsg * 2 < (int64_t(1) << 31)) return launch_mpnn_fwd_ep(a, s.probe, st);
   if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }
 
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st) {
-  if (s.H == 128 && mpnn_ep(s)) return launch_mpnn_bwd_ep(a, nblk, st);
-  if (s.H == 128) return s.eq ? launch_bwd_eq(a, nblk, st) : launch_mpnn_bwd16_probe(a, nblk, st);
+  if (mpnn_ep(s)) return launch_mpnn_bwd_ep(a, nblk, s.probe, st);
+  if (s.H == 128) return launch_bwd_eq(a, nblk, st);
   return s.eq ? launch_bwd_t<64, 32, 32, 2, true>(a, nblk, st) : launch_bwd_t<64, 32, 32, 2, false>(a, nblk, st);
 }
 

@@ -241,12 +241,12 @@ int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
 // Edge-parallel MPNN backward (bf16, H = O = 128): 128-edge block tiles, per-block partials of
-// [dW_hl ; db2 | dW_e] (coop_dw_len), Gh per edge, the destination sums of Gh (dP, carries) as the
-// 16-wave kernel makes them.
-int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st);
+// [dW_hl ; db2 | dW_e] (coop_dw_len), Gh per edge, the destination sums of Gh (dP, carries).
+// identity: the EGNN_FLAG_PROBE_IDENTITY instrument (the same kernel with the MLP replaced by identity).
+int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, bool identity, hipStream_t st);
 // Edge-parallel MPNN forward (bf16, H = O = 128): the per-row sums as whole rows and carries, completed
-// by the fix-up launch; mpnn_ep_blocks: its (and the backward's) grid.
-int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st);
+// by the fix-up launch; mpnn_ep_blocks: its (and the backward's) grid.  identity: as above.
+int launch_mpnn_fwd_ep(const FwdArgs& a, bool identity, hipStream_t st);
 int mpnn_ep_blocks(int64_t E);
 // Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
 // from L2, backward writes the per-edge weight-gradient factors Dm1, Dm, Dgq, Dga2.

@@ -24,6 +24,12 @@
 // MFMA against the tile's 0/1 segment matrix: rows whole in the tile are stored,
 // the partial first and last rows go to carry slots that the fix-up sums in tile
 // order.  The source sums (dQ) are made by the node reduction.
+// ID (instrument only, EGNN_FLAG_PROBE_IDENTITY): the layer with the MLP
+// replaced by identity, so g_a1 = the incoming message gradient of row i.  The
+// index loads, the gathers (P_i | Q_j, edge features, message gradient: every
+// one still loaded and waited for), the Gh stores, the LDS exchange of g_a1 and
+// the edge features, dW_e, the destination sums and carries are the layer's; the
+// chain's products and elementwise work and dW_hl are left out.
 // Reference: backward_kernel.py:143-257 computes the same quantities one
 // program per CSR row.
 #include "egnn_device.h"
@@ -45,7 +51,7 @@ struct EpIdx { int ri, rj, eid; };
 // incoming message gradient of row i for the lane's four features of each block, the edge features.
 struct EpGat { bf16x8 pq[8]; bf16x4 gm[8]; bf16x8 u; };
 
-template <int NU>
+template <int NU, bool ID = false>
 __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8, KH = H / 32, KO = O / 32;
   constexpr int NB = kEpWaves;                  // 16-edge blocks of a block tile
@@ -153,13 +159,22 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
       for (int rb = 0; rb < NRB; ++rb)
         if (e >= E) cur.gm[rb] = bf16x4{(bf16)0.0f, (bf16)0.0f, (bf16)0.0f, (bf16)0.0f};
     }
+    bf16x8 m1c[KH], ga2c[KO], g1c[KH];
+    if constexpr (ID) {   // g_a1 = g_m,i: stored as Gh and passed on as the chain of g_a1
+      bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
+#pragma unroll
+      for (int r = 0; r < NRB; ++r) *reinterpret_cast<bf16x4*>(ghr + 16 * r) = cur.gm[r];
+#pragma unroll
+      for (int k = 0; k < KH; ++k) g1c[k] = __builtin_shufflevector(cur.gm[2 * k], cur.gm[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
+      gather_pq(xn, cur);   // the next tile's
+      gather_gm(xn, cur);
+    } else {
     // Each stage is software-pipelined over its eight 16-row blocks: the LDS operands of block
     // rb + 1 are requested before the products of block rb, and the elementwise work of block
     // rb - 1 follows them, so neither the LDS latency nor the product latency is waited for in
     // line.  Scheduling barriers keep that order.
     // ---- S1: pre1 = W_u e + P_i + Q_j; m1 = SiLU(pre1), s1 = SiLU'(pre1) (bf16)
     bf16x4 s1[NRB];
-    bf16x8 m1c[KH];
     {
       bf16x8 fw[2];
       f32x4 acc[2], y[2];
@@ -192,7 +207,6 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
     }
     gather_pq(xn, cur);   // the next tile's
     // ---- S2, S4: s2 = SiLU'(W_hl^T m1 + b2), g_a2 = g_m,i s2
-    bf16x8 ga2c[KO];
     {
       bf16x8 fr[2][KH];
       f32x4 acc[2], ga[2];
@@ -223,7 +237,6 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
     }
     gather_gm(xn, cur);   // the next tile's
     // ---- S5: g_a1 = (W_hl g_a2) s1, stored per edge (Gh has a row for every edge of the last tile)
-    bf16x8 g1c[KH];
     {
       bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
       bf16x8 fr[2][KO];
@@ -257,6 +270,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         }
       }
     }
+    }   // ID
 
     // ---- the block tile's edge-major operands: chain chunk (kc, w) of each buffer
     __syncthreads();   // every wave has read the previous tile's buffers
@@ -264,8 +278,10 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 #pragma unroll
     for (int kc = 0; kc < KH; ++kc) {
       const int o = ((kc * NB + w) * 64 + sl) * 8;
-      *reinterpret_cast<bf16x8*>(s_m1 + o) = m1c[kc];
-      *reinterpret_cast<bf16x8*>(s_ga2 + o) = ga2c[kc];
+      if constexpr (!ID) {
+        *reinterpret_cast<bf16x8*>(s_m1 + o) = m1c[kc];
+        *reinterpret_cast<bf16x8*>(s_ga2 + o) = ga2c[kc];
+      }
       *reinterpret_cast<bf16x8*>(s_g1 + o) = g1c[kc];
     }
     if constexpr (NU > 0) {
@@ -281,7 +297,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
     // ---- weight gradients over the 128 edges (four 32-edge K chunks): wave w takes the 4 x 2 blocks
     // h-blocks 4 (w >> 2) .. + 3 x o-blocks 2 (w & 3), + 1 of dW_hl (six edge-major operand chunks per K
     // chunk), the next K chunk's operands requested before the products of this one
-    {
+    if constexpr (!ID) {
       const int hq = w >> 2, oq = w & 3;
       bf16x8 Am[2][4], Bg[2][2];
       auto load_ops = [&](int eh, int p) {
@@ -303,6 +319,8 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         else mma(acc_b2, ones, Bg[eh & 1][0]);
         __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    {
 #pragma unroll
       for (int eh = 0; eh < NK; ++eh) {
         const bf16x8 Ag = chain_edge_major<NB, SW>(s_g1, w, c, g, eh);   // g_a1 rows 16 w .. + 15, 32 edges
@@ -387,8 +405,12 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 // the schedule's rank table, a rank that is a whole row stored to out_msg, a partial first / last
 // rank to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).  No LDS exchange
 // and no barrier after the weight copy: the waves run independently, two blocks of eight per CU.
+// ID (instrument only, EGNN_FLAG_PROBE_IDENTITY): the layer with the MLP replaced by identity, the
+// message m = W_u e + P_i + Q_j computed with the edges on the MFMA rows (the layout S2 leaves), so
+// that the gathers, the rank tables, the per-row sums, their stores and carries are the layer's and
+// the SiLU and the W_hl product are left out.
 // Reference: forward_kernel.py:89-153 computes the same per-row sums one program per CSR row.
-template <int NU>
+template <int NU, bool ID = false>
 __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   constexpr int H = 128, O = 128, NRB = 8, KH = H / 32;
   __shared__ __attribute__((aligned(16))) bf16 s_whlT[NRB * KH * kFragElems];   // W_hl fragments, S2
@@ -452,7 +474,17 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     constexpr int HC = decltype(hc)::value;
     // ---- S1: m1 = SiLU(W_u e + P_i + Q_j) (features on the rows), software-pipelined over the row blocks
     bf16x8 m1c[KH];
-    {
+    bf16x4 mid[ID ? NRB : 1];   // ID: the message with the edges on the rows, block rb in mid[rb]
+    if constexpr (ID) {
+      const bf16x8 Ipq = s_ipq[l];
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) {
+        f32x4 acc = zero4();
+        if constexpr (NU > 0) mma(acc, cur.u, *reinterpret_cast<const bf16x8*>(s_wu + (rb * 64 + l) * 8));
+        mma(acc, cur.pq[rb], Ipq);
+        mid[rb] = pack4(acc);
+      }
+    } else {
       const bf16x8 Ipq = s_ipq[l];
       bf16x8 fw[2];
       f32x4 acc[2], y[2];
@@ -499,6 +531,26 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       }
       sq0 = seg_chunk_span(span[0], g, s_lut);
     }
+    if constexpr (ID) {   // the messages of feature block r: edges 4g .. 4g + 3 of this half, feature 16 r + c
+#pragma unroll
+      for (int r = 0; r < NRB; ++r) {
+        if constexpr (HC == 0) {
+          m0[64 * r] = mid[r];
+        } else {
+          const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mid[r], 0, 1, 2, 3, 4, 5, 6, 7);
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            if (16 * q >= nrk) break;
+            f32x4 D = zero4();
+            mma(D, Am, q == 0 ? sq0 : seg_chunk_span(span[1], g, s_lut));
+            if (dst[q] < 0x80000000u)
+              *reinterpret_cast<bf16x4*>((char*)a.out_msg + dst[q] + 32 * r) = pack4(D);
+            else if (dst[q] != ~0u)
+              *reinterpret_cast<f32x4*>((char*)(a.carry + T * 2 * O) + (dst[q] & 0x7fffffffu) + 64 * r) = D;
+          }
+        }
+      }
+    } else {
     // ---- S2: m = SiLU(m1 W_hl + b2) (edges on the rows); W_hl fragments of block rb + 1 requested once the
     // products of rb have read theirs
     {
@@ -546,6 +598,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
         }
       }
     }
+    }   // ID
   };
 
   const int64_t T0 = (int64_t)blockIdx.x * kEpWaves + w;
@@ -576,25 +629,37 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
 
 int mpnn_ep_blocks(int64_t E) { return (int)std::max<int64_t>(1, std::min<int64_t>((E + kEpTile - 1) / kEpTile, 256)); }
 
-int launch_mpnn_fwd_ep(const FwdArgs& a, hipStream_t st) {
+int launch_mpnn_fwd_ep(const FwdArgs& a, bool identity, hipStream_t st) {
   if (a.E > 0) {   // eight 32-edge tiles per block at a time, two blocks per CU
     const int nblk = (int)std::max<int64_t>(1, std::min<int64_t>((a.E + 8 * 32 - 1) / (8 * 32), 2 * 256));
-    if (a.FE == 0)
+    if (identity) {
+      if (a.FE == 0)
+        hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0, true>), dim3(nblk), dim3(512), 0, st, a);
+      else
+        hipLaunchKernelGGL((mpnn_fwd_ep_kernel<1, true>), dim3(nblk), dim3(512), 0, st, a);
+    } else if (a.FE == 0) {
       hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
-    else
+    } else {
       hipLaunchKernelGGL((mpnn_fwd_ep_kernel<1>), dim3(nblk), dim3(512), 0, st, a);
+    }
   }
   return (int)hipGetLastError();
 }
 
-int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, hipStream_t st) {
+template <bool ID>
+void launch_mpnn_bwd_ep_t(const BwdArgs& a, int nblk, hipStream_t st) {
+  if (a.FE == 0)
+    hipLaunchKernelGGL((mpnn_bwd_ep_kernel<0, ID>), dim3(nblk), dim3(512), 0, st, a);
+  else if (a.FE <= 16)
+    hipLaunchKernelGGL((mpnn_bwd_ep_kernel<1, ID>), dim3(nblk), dim3(512), 0, st, a);
+  else
+    hipLaunchKernelGGL((mpnn_bwd_ep_kernel<2, ID>), dim3(nblk), dim3(512), 0, st, a);
+}
+
+int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, bool identity, hipStream_t st) {
   if (a.E > 0) {
-    if (a.FE == 0)
-      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<0>), dim3(nblk), dim3(512), 0, st, a);
-    else if (a.FE <= 16)
-      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<1>), dim3(nblk), dim3(512), 0, st, a);
-    else
-      hipLaunchKernelGGL((mpnn_bwd_ep_kernel<2>), dim3(nblk), dim3(512), 0, st, a);
+    if (identity) launch_mpnn_bwd_ep_t<true>(a, nblk, st);
+    else launch_mpnn_bwd_ep_t<false>(a, nblk, st);
   }
   return (int)hipGetLastError();
 }

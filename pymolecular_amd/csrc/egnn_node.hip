@@ -29,7 +29,8 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   s->accum = (d->flags & EGNN_FLAG_ACCUMULATE_GRAD_H) != 0;
   s->coord_res = (d->flags & EGNN_FLAG_COORD_RESIDUAL) != 0;
   s->probe = (d->flags & EGNN_FLAG_PROBE_IDENTITY) != 0;
-  // the identity instrument exists for the bf16 MPNN layer at H = 128 (cooperative kernels)
+  // the identity instrument exists for the bf16 MPNN layer at H = 128 (edge-parallel kernels); the checks
+  // that need the strides (message rows under 2 GB) are egnn_fwd's
   if (s->probe && (d->equivariant || d->dtype != EGNN_BF16 || d->H != 128 || d->FE > 32)) return EGNN_ERR_DIMS;
   if (s->coord_res && !s->eq) return EGNN_ERR_DIMS;   // no coordinates in the MPNN layer
   if (d->N < 1 || d->E < 0 || d->N > (int64_t)INT32_MAX - 1 || d->E > (int64_t)INT32_MAX - 64) return EGNN_ERR_DIMS;
@@ -41,6 +42,8 @@ int make_shape(const EgnnDims* d, LayerShape* s) {
   s->NUC = s->eq ? (int)cdiv(d->FE + 2, 32) : (int)cdiv(d->FE, 32);
   s->KU = 32 * s->NUC;
   s->esz = s->bf16 ? 2 : 4;
+  // the instrument never falls back to another kernel: outside the edge-parallel kernels' limits it is refused
+  if (s->probe && !coop_supported(*s)) return EGNN_ERR_DIMS;
   return EGNN_OK;
 }
 

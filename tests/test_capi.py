@@ -114,3 +114,9 @@ def test_identity_probe_flag_only_for_bf16_mpnn_h128():
         if field == "H":
             bad.update(O=256, M=256)
         assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**bad)) == 0, field
+    # beyond the edge-parallel kernels' 32-bit node-projection offsets (N * 4H >= 2^32) the layer runs other
+    # kernels; the instrument is refused rather than silently timing the real layer
+    big = dict(kw, N=1 << 23)
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**big)) == 0
+    assert L.egnn_bwd_workspace_bytes(_capi.EgnnDims(**big)) == 0
+    assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**dict(big, flags=0))) > 0

@@ -307,11 +307,15 @@ def test_no_edges(dtype, eq, FE):
             assert not np.any(v), k
 
 
-def test_identity_probe_instrument_computes_linear_sums():
-    # the instrument of the gather / segment-sum timing: messages P_i + Q_j + e W_e summed per row,
-    # dL/dpre1 = the row's message gradient summed by row and by source into dh
+@pytest.mark.parametrize("skewed", [False, True])
+def test_identity_probe_instrument_computes_linear_sums(skewed):
+    # the instrument of the gather / segment-sum timing (the edge-parallel kernels with the MLP replaced by
+    # identity): messages P_i + Q_j + e W_e summed per row, dL/dpre1 = the row's message gradient summed by
+    # row and by source into dh, and dW_e = sum_e e g_m,i
     from pymolecular_amd import fused
-    rowptr, col = random_csr(900, (np.arange(900) * 5) % 41 + 2, seed=51)
+    degs = np.array([0, 300, 1, 2, 0, 129, 3, 31, 33, 0, 64, 127, 128, 5, 2, 17] * 8) if skewed else \
+        (np.arange(900) * 5) % 41 + 2
+    rowptr, col = random_csr(len(degs), degs, seed=51)
     case = Case(rowptr, col, 128, 16, 128, 128, 128, seed=52, eq=False, bias=False)
     bf = torch.bfloat16
     h, ef = _dev(case.h, bf), _dev(case.ef, bf)
@@ -338,5 +342,8 @@ def test_identity_probe_instrument_computes_linear_sums():
     np.add.at(dQ, case.col, gmd[rows])
     dh = orc.round_bf16(dP) @ Wn1.T + orc.round_bf16(dQ) @ Wn2.T
     e_bwd = orc.normwise_rel_err(g["h"].float().cpu().numpy(), dh)
-    print(f"probe forward {e_fwd:.2e} backward dh {e_bwd:.2e}", flush=True)
-    assert e_fwd <= 2e-2 and e_bwd <= 2e-2, (e_fwd, e_bwd)
+    dwe = efd.T @ gmd[rows]
+    e_we = orc.normwise_rel_err(g["w1_msg"].float().cpu().numpy()[2 * H:], dwe)
+    print(f"probe forward {e_fwd:.2e} backward dh {e_bwd:.2e} dW_e {e_we:.2e}", flush=True)
+    assert e_fwd <= 2e-2 and e_bwd <= 2e-2 and e_we <= 2e-2, (e_fwd, e_bwd, e_we)
+    assert not torch.any(g["w2_msg"].float()), "the instrument has no W_hl: its gradient is zero"
