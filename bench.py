@@ -108,7 +108,7 @@ def kernel_work(cls, path, N, E, F, H, O, M, FE, g, s):
     count every gathered row once per edge: P_i, Q_j (H each), col and row id (8), edge id and
     features, the geometry record; scratch stores (Gh, Gx, factors) included; node outputs once."""
     eb = 8 + (4 + FE * s if FE else 0) + 24 * g
-    # the cooperative MPNN backward (H = 128) sums dL/dpre1 over each row itself: dP rows and, for the
+    # the edge-parallel MPNN backward (H = 128) sums dL/dpre1 over each row itself: dP rows and, for the
     # rows split over tiles, fp32 carries (about two per 32-edge tile) out; the node reduction then
     # reads Gh once, by source
     dst = path == "coop" and g == 0 and H == 128
