@@ -312,7 +312,7 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
         }
         ga1c[hc][nb] = pack_chunk<T>(y0, y1);
         if (valid[nb]) {
-          T* dst = Gh + ee[nb] * H + 32 * hc + 4 * g;
+          T* dst = Gh + (ee[nb] - a.gbase) * H + 32 * hc + 4 * g;
           store4<T>(dst, y0);
           store4<T>(dst + 16, y1);
         }
@@ -337,8 +337,8 @@ __global__ __launch_bounds__(256) void bwd_edge_kernel(BwdArgs a) {
           const float k2 = 2.0f * gr;
           f32x4 gd = {phi[nb] * gxx[nb] + k2 * dx[nb], phi[nb] * gxy[nb] + k2 * dy[nb],
                       phi[nb] * gxz[nb] + k2 * dz[nb], gphi[nb]};
-          *reinterpret_cast<f32x4*>(a.Gx + ee[nb] * 4) = gd;
-          a.R2[ee[nb]] = r2[nb];
+          *reinterpret_cast<f32x4*>(a.Gx + (ee[nb] - a.gbase) * 4) = gd;
+          a.R2[ee[nb] - a.gbase] = r2[nb];
         }
       }
     }

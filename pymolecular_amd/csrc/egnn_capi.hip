@@ -306,27 +306,66 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
       if ((rc = hip_status(launch_sum_rows(w.dwpart, s.E > 0 ? w.nblk : 0, w.LW, w.dw2m, st))) != EGNN_OK) return rc;
     }
   }
+  // destination/source sums of dL/dpre1 and dL/ddelta (fixed order): node_reduce(e0, e1, accumulate)
+  float* gcoord = s.eq ? grad_coord : nullptr;
+  const float* gres = s.coord_res ? grad_out_mov : nullptr;
+  auto node_reduce = [&](int64_t e0, int64_t e1, bool acc) -> int32_t {
+    ProfScope ps(EGNN_K_NODE_REDUCE, st);
+    return hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
+                                         strides->coord, gres, strides->mov, e0, e1, acc, st));
+  };
+  // dw_d = sum_e g_a1[e] r^2[e] (into dwd, when given) and dW_e = sum_e g_a1[e] e[edge_ids[e]] (into dwe,
+  // when given and F_E > 0) over the edges [e0, e1), whose rows Gh and R2 hold from row e0 - gb
+  auto gh_products = [&](int64_t e0, int64_t e1, int64_t gb, float* dwd, float* dwe) -> int32_t {
+    int32_t r = EGNN_OK;
+    if (s.eq && dwd) {
+      Gemm2Args d{};
+      d.M = s.H; d.N = 1; d.K = e1 - e0;
+      d.A = (const char*)w.Gh + (e0 - gb) * s.H * s.esz; d.lda = s.H; d.a_bf16 = s.bf16; d.a_kc = 0;
+      d.a_ones_row = -1;
+      d.B = w.R2 + (e0 - gb); d.ldb = 1; d.b_bf16 = 0; d.b_nc = 1;
+      if ((r = splitk2(d, dwd)) != EGNN_OK) return r;
+    }
+    if (s.FE > 0 && dwe) {
+      Gemm2Args g{};
+      g.M = s.H; g.N = s.FE; g.K = e1 - e0;
+      g.A = (const char*)w.Gh + (e0 - gb) * s.H * s.esz; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0;
+      g.a_ones_row = -1;
+      g.B = edge_ids ? edge_feat : (const char*)edge_feat + e0 * strides->edge * s.esz; g.ldb = strides->edge;
+      g.b_bf16 = s.bf16; g.b_nc = 1; g.b_kidx = edge_ids ? edge_ids + e0 : nullptr;
+      if ((r = splitk2(g, dwe)) != EGNN_OK) return r;
+    }
+    return r;
+  };
   if (!coop && !wide) {
     // one-wave-per-tile kernel, one edge chunk at a time: each chunk's factor products right after
-    // its kernel (sums into per-chunk rows, added in chunk order below when there are several)
+    // its kernel (sums into per-chunk rows, added in chunk order below when there are several); with
+    // chunk_gh (fp32) also the products over the chunk's Gh and its node sums, added to the earlier
+    // chunks' (so Gh, Gx and r^2 hold one chunk as well)
     const int TW = bwd_tile_edges(s);
     const int64_t Lw = (int64_t)(s.H + 1) * s.O, Lm = (int64_t)(s.O + 1) * s.M;
-    for (int ch = 0; ch < w.nchunk; ++ch) {
+    const int64_t Lwe = (int64_t)s.H * std::max(s.FE, 1);
+    const int nc = w.nchunk;
+    const bool one = nc == 1;
+    float* res_w = w.chunkres;                  // [nc][Lw] | [nc][Lm] | [nc][M] | [nc][H] | [nc][Lwe]
+    float* res_m = res_w + nc * Lw;
+    float* res_p = res_m + nc * Lm;
+    float* res_d = res_p + nc * s.M;
+    float* res_e = res_d + nc * s.H;
+    for (int ch = 0; ch < nc; ++ch) {
       const int64_t e0 = (int64_t)ch * w.chunkE, e1 = std::min<int64_t>(s.E, e0 + w.chunkE);
-      a.tile0 = e0 / TW; a.ntiles = cdiv(e1, TW); a.fbase = e0;
+      const int64_t gb = w.chunk_gh ? e0 : 0;
+      a.tile0 = e0 / TW; a.ntiles = cdiv(e1, TW); a.fbase = e0; a.gbase = gb;
       {
         ProfScope ps(EGNN_K_BWD_EDGE, st);
         if ((rc = hip_status(launch_bwd(s, a, st))) != EGNN_OK) return rc;
       }
-      const bool one = w.nchunk == 1;
       Gemm2Args g{};
       g.M = s.H + 1; g.N = s.O; g.K = e1 - e0;
       g.A = w.Dm1; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = s.H;
       g.B = w.Dga2; g.ldb = s.O; g.b_bf16 = s.bf16; g.b_nc = 1;
-      if ((rc = splitk2(g, one ? w.dWhl : w.chunkres + ch * Lw)) != EGNN_OK) return rc;
+      if ((rc = splitk2(g, one ? w.dWhl : res_w + ch * Lw)) != EGNN_OK) return rc;
       if (s.eq) {
-        float* res_m = w.chunkres + w.nchunk * Lw;
-        float* res_p = res_m + w.nchunk * Lm;
         Gemm2Args m{};
         m.M = s.O + 1; m.N = s.M; m.K = e1 - e0;
         m.A = w.Dm; m.lda = s.O; m.a_bf16 = s.bf16; m.a_kc = 0; m.a_ones_row = s.O;
@@ -335,45 +374,33 @@ int32_t egnn_bwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
         Gemm2Args p{};   // dw2_mov = sum_e p[e] g_phi[e]  (g_phi in column 3 of Gx)
         p.M = s.M; p.N = 1; p.K = e1 - e0;
         p.A = w.Dp; p.lda = s.M; p.a_bf16 = s.bf16; p.a_kc = 0; p.a_ones_row = -1;
-        p.B = w.Gx + 4 * e0 + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
+        p.B = w.Gx + 4 * (e0 - gb) + 3; p.ldb = 4; p.b_bf16 = 0; p.b_nc = 1;
         if ((rc = splitk2(p, one ? w.dw2m : res_p + ch * s.M)) != EGNN_OK) return rc;
       }
-    }
-    if (w.nchunk > 1) {
-      ProfScope ps(EGNN_K_EDGE_WGRAD, st);
-      if ((rc = hip_status(launch_sum_rows(w.chunkres, w.nchunk, Lw, w.dWhl, st))) != EGNN_OK) return rc;
-      if (s.eq) {
-        const float* res_m = w.chunkres + w.nchunk * Lw;
-        if ((rc = hip_status(launch_sum_rows(res_m, w.nchunk, Lm, w.dW1m, st))) != EGNN_OK) return rc;
-        if ((rc = hip_status(launch_sum_rows(res_m + w.nchunk * Lm, w.nchunk, s.M, w.dw2m, st))) != EGNN_OK)
+      if (w.chunk_gh) {
+        if ((rc = gh_products(e0, e1, gb, one ? w.dwd : res_d + ch * s.H, one ? w.dWe : res_e + ch * Lwe)) != EGNN_OK)
           return rc;
+        if ((rc = node_reduce(e0, e1, ch > 0)) != EGNN_OK) return rc;
       }
     }
+    if (!one) {
+      ProfScope ps(EGNN_K_EDGE_WGRAD, st);
+      if ((rc = hip_status(launch_sum_rows(res_w, nc, Lw, w.dWhl, st))) != EGNN_OK) return rc;
+      if (s.eq) {
+        if ((rc = hip_status(launch_sum_rows(res_m, nc, Lm, w.dW1m, st))) != EGNN_OK) return rc;
+        if ((rc = hip_status(launch_sum_rows(res_p, nc, s.M, w.dw2m, st))) != EGNN_OK) return rc;
+        if (w.chunk_gh && (rc = hip_status(launch_sum_rows(res_d, nc, s.H, w.dwd, st))) != EGNN_OK) return rc;
+      }
+      if (w.chunk_gh && s.FE > 0 && (rc = hip_status(launch_sum_rows(res_e, nc, Lwe, w.dWe, st))) != EGNN_OK)
+        return rc;
+    }
   }
-  // destination/source sums of dL/dpre1 and dL/ddelta (fixed order)
-  float* gcoord = s.eq ? grad_coord : nullptr;
-  {
-    ProfScope ps(EGNN_K_NODE_REDUCE, st);
-    const float* gres = s.coord_res ? grad_out_mov : nullptr;
-    if ((rc = hip_status(launch_node_reduce(s, w.Gh, w.Gx, rowptr, v.csc_ptr, v.csc_eid, w.dPQ, gcoord,
-                                          strides->coord, gres, strides->mov, st))) != EGNN_OK)
+  if (!w.chunk_gh) {   // Gh holds every edge: one pass of the node sums and of the products over Gh
+    if ((rc = node_reduce(0, INT64_MAX, false)) != EGNN_OK) return rc;
+    // dw_d: the one-wave path (the wide kernel sums it itself); dW_e: both (the cooperative kernels
+    // accumulate it themselves)
+    if ((rc = gh_products(0, s.E, 0, (!coop && !wide) ? w.dwd : nullptr, coop ? nullptr : w.dWe)) != EGNN_OK)
       return rc;
-  }
-
-
-  if (s.eq && !coop && !wide) {
-    Gemm2Args d{};   // dw_d = sum_e g_a1[e] r^2[e]
-    d.M = s.H; d.N = 1; d.K = s.E;
-    d.A = w.Gh; d.lda = s.H; d.a_bf16 = s.bf16; d.a_kc = 0; d.a_ones_row = -1;
-    d.B = w.R2; d.ldb = 1; d.b_bf16 = 0; d.b_nc = 1;
-    if ((rc = splitk2(d, w.dwd)) != EGNN_OK) return rc;
-  }
-  if (s.FE > 0 && !coop) {   // dW_e = sum_e g_a1[e] e[edge_ids[e]]
-    Gemm2Args g{};
-    g.M = s.H; g.N = s.FE; g.K = s.E;
-    g.A = w.Gh; g.lda = s.H; g.a_bf16 = s.bf16; g.a_kc = 0; g.a_ones_row = -1;
-    g.B = edge_feat; g.ldb = strides->edge; g.b_bf16 = s.bf16; g.b_nc = 1; g.b_kidx = edge_ids;
-    if ((rc = splitk2(g, w.dWe)) != EGNN_OK) return rc;
   }
   {
     // dh = [dP | dQ] [W_n1 | W_n2]^T, and [dW_n1 | dW_n2 ; db1 | .] = [h | 1]^T [dP | dQ] split over the

@@ -97,12 +97,22 @@ struct BwdWs {
   // one-wave-per-tile kernel: the factors hold chunkE edges; per-chunk sums of the factor products
   int64_t chunkE;
   int nchunk;
-  float* chunkres; // [nchunk][(H + 1) O + (O + 1) M + M]
+  bool chunk_gh;   // fp32: Gh, Gx, R2 hold one chunk too, reduced per chunk (node sums accumulated in chunk order)
+  float* chunkres; // [nchunk][chunk_len]: (H + 1) O + (O + 1) M + M (+ H + H F_E with chunk_gh)
+  int64_t chunk_len;
 };
-// Edges per chunk of the one-wave-per-tile backward: the whole graph when its per-edge factor rows
-// take at most kFactorBudget bytes, else half of it (a multiple of 32 edges) -- half the factor
-// memory for one more kernel and product launch.
+// Edges per chunk of the one-wave-per-tile backward.
+//  * fp32: the per-edge rows the chunk needs (factors, Gh, Gx, r^2) take at most kChunkBudget bytes
+//    unless that would make chunks of fewer than kChunkFillEdges edges (6,144 tiles, what fills the
+//    device with the one-wave-per-tile kernel), and a graph of 2 kChunkMinEdges edges or more has at
+//    least two chunks, so the backward's scratch stays a fraction of its per-edge state (the eager
+//    computation holds all of it); the node reduction runs per chunk and accumulates, in chunk order.
+//  * bf16: the whole graph when its factor rows take at most kFactorBudget bytes, else half of it.
+// Chunks are whole 32-edge tiles.
 constexpr size_t kFactorBudget = size_t(320) << 20;
+constexpr size_t kChunkBudget = size_t(256) << 20;
+constexpr int64_t kChunkMinEdges = 4096;
+constexpr int64_t kChunkFillEdges = 6144 * 32;
 int64_t factor_chunk_edges(const LayerShape& s);
 size_t fwd_ws_layout(const LayerShape& s, void* base, FwdWs* w);
 size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w);
@@ -216,7 +226,8 @@ struct BwdArgs {
   const float* gmov; int64_t sgx;
   void* Dm1; void* Dm; void* Dgq; void* Dga2; void* Dp; void* Gh; float* Gx; float* R2;
   int64_t tile0;   // one-wave-per-tile kernel: tiles [tile0, ntiles) of this launch (an edge chunk)
-  int64_t fbase;   // first edge of the factor rows Dm1 ... Dp (they hold one chunk; Gh, Gx, R2 hold all edges)
+  int64_t fbase;   // first edge of the factor rows Dm1 ... Dp (they hold one chunk)
+  int64_t gbase;   // first edge of the rows of Gh, Gx, R2 (0: they hold all edges; fbase: one chunk, fp32)
   float* dwpart;   // cooperative kernel: per-block weight-gradient partials [gridDim.x][LW]
   int64_t LW;
   // cooperative MPNN kernel: destination sums of dL/dpre1, the rows whole in a 32-edge tile
@@ -263,9 +274,12 @@ int bwd_tile_edges(const LayerShape& s);
 
 // dPQ[n] = [sum_row Gh | sum_csc Gh] (summed in fp32, stored in the activation dtype);
 // grad_coord = sum_row Gx - sum_csc Gx
+// e0, e1: the edges [e0, e1) whose rows Gh, Gx hold (Gh row e - e0); accumulate: add the sums to dPQ and
+// gcoord (a later chunk) instead of storing them
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
                        const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord,
-                       int64_t sgc, const float* gres, int64_t sgr, hipStream_t st);   // gres: added to gcoord
+                       int64_t sgc, const float* gres, int64_t sgr, int64_t e0, int64_t e1, bool accumulate,
+                       hipStream_t st);   // gres: added to gcoord (by the storing call)
 // out[l] = sum_b part[b][l] for l < L (fixed order)
 int launch_sum_rows(const float* part, int64_t nrows, int64_t L, float* out, hipStream_t st);
 // scatter the fp32 weight-gradient sums into the caller's tensors

@@ -101,9 +101,16 @@ int64_t splitk_parts(int64_t M, int64_t N, int64_t K, bool fold) {
 
 int64_t factor_chunk_edges(const LayerShape& s) {
   const int64_t E = std::max<int64_t>(s.E, 1);
-  const size_t per_edge = (size_t)(s.H + 2 * s.O + (s.eq ? 2 * s.M : 0)) * s.esz;   // Dm1, Dm, Dga2 (, Dgq, Dp)
+  const size_t factors = (size_t)(s.H + 2 * s.O + (s.eq ? 2 * s.M : 0)) * s.esz;   // Dm1, Dm, Dga2 (, Dgq, Dp)
   const int64_t whole = cdiv(E, kTileEdges) * kTileEdges;
-  if ((size_t)E * per_edge <= kFactorBudget) return whole;
+  if (!s.bf16) {   // fp32: factors, Gh, Gx, r^2 per chunk
+    const size_t per_edge = factors + (size_t)s.H * 4 + 4 * sizeof(float) + sizeof(float);
+    int64_t n = (int64_t)cdiv((int64_t)((size_t)E * per_edge), (int64_t)kChunkBudget);
+    n = std::min<int64_t>(n, std::max<int64_t>(1, E / kChunkFillEdges));   // chunks that fill the device
+    if (E >= 2 * kChunkMinEdges) n = std::max<int64_t>(n, 2);
+    return cdiv(cdiv(E, std::max<int64_t>(n, 1)), kTileEdges) * kTileEdges;
+  }
+  if ((size_t)E * factors <= kFactorBudget) return whole;
   return cdiv(cdiv(E, 2), kTileEdges) * kTileEdges;
 }
 
@@ -116,6 +123,7 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   const int64_t E1 = std::max<int64_t>(s.E, 1);
   w->chunkE = (coop || wide) ? E1 : factor_chunk_edges(s);
   w->nchunk = (coop || wide) ? 1 : (int)cdiv(E1, w->chunkE);
+  w->chunk_gh = !coop && !wide && !s.bf16;   // fp32: Gh, Gx, R2 per chunk as well
   const size_t E = (size_t)E1, EF = (size_t)w->chunkE;
   w->PQ = take((size_t)s.N * 2 * s.H * s.esz);
   w->Dm1 = coop ? nullptr : take(EF * s.H * s.esz);
@@ -124,10 +132,11 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
   w->Dga2 = coop ? nullptr : take(EF * s.O * s.esz);
   w->Dp = (s.eq && !coop && !wide) ? take(EF * s.M * s.esz) : nullptr;
   // the cooperative kernels store Gh / Gx rows for every edge slot of their last tile (32, 64 or 128 edges)
-  const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), 4 * kTileEdges) * 4 * kTileEdges : E;
+  const size_t Er = coop ? (size_t)cdiv(std::max<int64_t>(s.E, 1), 4 * kTileEdges) * 4 * kTileEdges
+                         : w->chunk_gh ? EF : E;
   w->Gh = take(Er * s.H * s.esz);
   w->Gx = (float*)take(Er * 4 * sizeof(float));
-  w->R2 = (coop || wide) ? nullptr : (float*)take(E * sizeof(float));
+  w->R2 = (coop || wide) ? nullptr : (float*)take(Er * sizeof(float));
   w->geo = ((coop || wide_supported(s)) && s.eq) ? (float*)take(E * 8 * sizeof(float)) : nullptr;
   w->carry = coop_dst_sums(s) ? (float*)take((size_t)cdiv(E1, kTileEdges) * 2 * s.O * sizeof(float)) : nullptr;
   // per-block partials of the cooperative kernels' weight gradients / the wide kernel's dw2_mov | dw_d
@@ -143,12 +152,16 @@ size_t bwd_ws_layout(const LayerShape& s, void* base, BwdWs* w) {
     for (const int64_t K : {w->chunkE, lastE})
       w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H + 1, s.O, K, s.bf16), splitk_parts(s.O + 1, s.M, K, s.bf16),
                                          splitk_parts(s.M, 1, K, s.bf16)});
-    w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H, 1, s.E, s.bf16),
-                                       splitk_parts(s.H, std::max(s.FE, 1), s.E, s.bf16)});
+    // dw_d and dW_e over Gh: all edges at once, or (chunk_gh) one chunk at a time
+    const int64_t Ks[2] = {w->chunk_gh ? w->chunkE : s.E, w->chunk_gh ? lastE : s.E};
+    for (const int64_t K : Ks)
+      w->part_elems = std::max<int64_t>({w->part_elems, splitk_parts(s.H, 1, K, s.bf16),
+                                         splitk_parts(s.H, std::max(s.FE, 1), K, s.bf16)});
   }
-  w->chunkres = (coop || wide || w->nchunk == 1)
-                    ? nullptr
-                    : (float*)take((size_t)w->nchunk * ((s.H + 1) * s.O + (s.O + 1) * s.M + s.M) * sizeof(float));
+  w->chunk_len = (int64_t)(s.H + 1) * s.O + (int64_t)(s.O + 1) * s.M + s.M +
+                 (w->chunk_gh ? (int64_t)s.H + (int64_t)s.H * std::max(s.FE, 1) : 0);
+  w->chunkres = (coop || wide || w->nchunk == 1) ? nullptr
+                                                 : (float*)take((size_t)w->nchunk * w->chunk_len * sizeof(float));
   w->part = (float*)take((size_t)w->part_elems * sizeof(float));
   w->dWhl = (float*)take((size_t)(s.H + 1) * s.O * sizeof(float));
   w->dW1m = (float*)take((size_t)(s.O + 1) * s.M * sizeof(float));
@@ -1383,6 +1396,11 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
 // by LPE = H*sizeof(T)/16 lanes, so one wave-wide load covers EPW = 64/LPE
 // edges; the EPW partial sums are combined with lane shuffles at the end, in a
 // fixed order, so the result does not depend on timing.
+// An edge chunk [e0, e1) (Gh, Gx rows e - e0): the row part is the row's edges in
+// the chunk, the source part the sub-range of the node's stable CSC list with
+// edge ids in the chunk (found by binary search: the list ascends); with acc the
+// sums are added to what an earlier chunk stored, element by element, so the
+// chunks add up in chunk order.
 template <typename T, int H>
 __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ Gh, const float* __restrict__ Gx,
                                                           const int32_t* __restrict__ rowptr,
@@ -1390,7 +1408,7 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
                                                           const int32_t* __restrict__ csc_eid, T* __restrict__ dPQ,
                                                           float* __restrict__ gcoord, int64_t sgc,
                                                           const float* __restrict__ gres, int64_t sgr, int64_t N,
-                                                          int eq, int dst) {
+                                                          int eq, int dst, int64_t e0, int64_t e1, int acc) {
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
   constexpr int EPW = 64 / LPE;                // edges per wave-wide load
@@ -1408,9 +1426,9 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int j = j0 + u * EPW + sub;
-        const int e = idx(j < cnt ? j : cnt - 1);
-        v[u] = *reinterpret_cast<const V*>(Gh + (int64_t)e * H + q * VPL);
-        gx[u] = (eq && q < 3) ? Gx[(int64_t)e * 4 + q] : 0.f;
+        const int64_t e = idx(j < cnt ? j : cnt - 1) - e0;
+        v[u] = *reinterpret_cast<const V*>(Gh + e * H + q * VPL);
+        gx[u] = (eq && q < 3) ? Gx[e * 4 + q] : 0.f;
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
@@ -1429,11 +1447,23 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
     float ax = 0.f;
     // destination sums (unless the edge kernel made them): the row's edges are contiguous
     if (dst) {
-      const int rs = rowptr[n], re = rowptr[n + 1];
-      gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+      const int rs = (int)max((int64_t)rowptr[n], e0), re = (int)min((int64_t)rowptr[n + 1], e1);
+      if (re > rs) gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
     }
     // source sums: the edges listed for n by the stable CSC, edge ids 64 at a time, one per lane
-    const int cs = csc_ptr[n], ce = csc_ptr[n + 1];
+    int cs = csc_ptr[n], ce = csc_ptr[n + 1];
+    if (e0 > 0 || e1 < (int64_t)INT32_MAX) {   // the chunk's sub-range: first entries with id >= e0, >= e1
+      auto lower = [&](int lo, int hi, int64_t key) {
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if ((int64_t)csc_eid[mid] < key) lo = mid + 1; else hi = mid;
+        }
+        return lo;
+      };
+      const int a0 = lower(cs, ce, e0);
+      ce = lower(a0, ce, e1);
+      cs = a0;
+    }
     for (int k0 = cs; k0 < ce; k0 += 64) {
       const int cnt = ce - k0 < 64 ? ce - k0 : 64;
       const int my = csc_eid[k0 + (l < cnt ? l : cnt - 1)];
@@ -1449,18 +1479,26 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
       }
       ax += shfl_xor(ax, off);
     }
-    if (eq && l < 3) gcoord[n * sgc + l] = gres ? gres[n * sgr + l] + ax : ax;   // + the residual path of x'
+    if (eq && l < 3) {   // + the residual path of x' (added once, by the storing call)
+      float* o = gcoord + n * sgc + l;
+      *o = acc ? *o + ax : (gres ? gres[n * sgr + l] + ax : ax);
+    }
     if (sub == 0) {   // one 16-byte store per half
       T* out = dPQ + n * 2 * H + q * VPL;
-      if constexpr (sizeof(T) == 2) {
+      if constexpr (sizeof(T) == 2) {   // (no accumulation in bf16: the chunked reduction is fp32 only)
         bf16x8 vp, vq;
 #pragma unroll
         for (int u = 0; u < VPL; ++u) { vp[u] = (bf16)ap[u]; vq[u] = (bf16)aq[u]; }
         if (dst) *reinterpret_cast<bf16x8*>(out) = vp;
         *reinterpret_cast<bf16x8*>(out + H) = vq;
       } else {
-        if (dst) *reinterpret_cast<f32x4*>(out) = f32x4{ap[0], ap[1], ap[2], ap[3]};
-        *reinterpret_cast<f32x4*>(out + H) = f32x4{aq[0], aq[1], aq[2], aq[3]};
+        f32x4 vp = f32x4{ap[0], ap[1], ap[2], ap[3]}, vq = f32x4{aq[0], aq[1], aq[2], aq[3]};
+        if (acc) {
+          if (dst) vp += *reinterpret_cast<const f32x4*>(out);
+          vq += *reinterpret_cast<const f32x4*>(out + H);
+        }
+        if (dst) *reinterpret_cast<f32x4*>(out) = vp;
+        *reinterpret_cast<f32x4*>(out + H) = vq;
       }
     }
   }
@@ -1468,11 +1506,12 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
 
 int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, const int32_t* rowptr,
                        const int32_t* csc_ptr, const int32_t* csc_eid, void* dPQ, float* gcoord, int64_t sgc,
-                       const float* gres, int64_t sgr, hipStream_t st) {
+                       const float* gres, int64_t sgr, int64_t e0, int64_t e1, bool accumulate, hipStream_t st) {
+  if (accumulate && s.bf16) return (int)hipErrorInvalidValue;   // chunk sums add up in fp32 outputs only
   int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
   int eq = s.eq ? 1 : 0;
   int dst = coop_dst_sums(s) ? 0 : 1;   // the cooperative MPNN kernel stores the destination sums
-#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, dst)
+#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, dst, e0, e1, accumulate ? 1 : 0)
   if (s.bf16) {
     if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
   } else {

@@ -33,11 +33,14 @@ def test_speed_sweep_small():
 
 
 def test_memory_sweep_small():
-    # peak device memory of one backward call, inputs included: the fused layer keeps one E x H
-    # scratch, the eager provider every per-edge activation and its autograd saves
+    # peak device memory of one backward call, inputs included: the fused fp32 layer keeps its per-edge
+    # state one edge chunk at a time, the eager provider every per-edge activation and its autograd saves;
+    # at the reference sweep's sizes the fused peak is below the eager one, and at most half of it from
+    # 25k nodes (test_mem.py:42)
     from pymolecular_amd.benchmarks.test_mem import run_memory_benchmark
-    rows = run_memory_benchmark([1000, 20000])
+    rows = run_memory_benchmark([1000, 25000])
     for n, e, pt, hip in rows:
         assert hip != "OOM" and float(hip) > 0
-        if n == 20000:
-            assert pt == "OOM" or float(hip) < float(pt), (hip, pt)
+        assert pt == "OOM" or float(hip) <= float(pt), (n, hip, pt)
+        if n == 25000:
+            assert pt == "OOM" or float(hip) <= 0.5 * float(pt), (hip, pt)

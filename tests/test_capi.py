@@ -120,3 +120,19 @@ def test_identity_probe_flag_only_for_bf16_mpnn_h128():
     assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**big)) == 0
     assert L.egnn_bwd_workspace_bytes(_capi.EgnnDims(**big)) == 0
     assert L.egnn_fwd_workspace_bytes(_capi.EgnnDims(**dict(big, flags=0))) > 0
+
+
+def test_fp32_backward_scratch_is_bounded():
+    # the fp32 backward keeps its per-edge rows (factors, dL/dpre1, dL/ddelta, r^2) one edge chunk at a
+    # time: its workspace grows with the nodes, not with the edges, past the chunk budget
+    L = _capi.lib()
+    kw = dict(F=32, FE=16, H=64, O=32, M=32, equivariant=1, mean_agg=0, dtype=0)
+    small = L.egnn_bwd_workspace_bytes(_capi.EgnnDims(N=250_000, E=8_000_000, **kw))
+    big = L.egnn_bwd_workspace_bytes(_capi.EgnnDims(N=250_000, E=32_000_000, **kw))
+    assert big - small < 32 << 20, (small >> 20, big >> 20)          # 4x the edges, about the same scratch
+    assert small < (256 << 20) + 2 * 250_000 * 2 * 64 * 4 + (32 << 20), small >> 20   # chunk + node rows
+    # graphs of 8,192 edges or more take at least two chunks: the scratch is about half the per-edge state
+    one = L.egnn_bwd_workspace_bytes(_capi.EgnnDims(N=1000, E=8000, **kw))
+    two = L.egnn_bwd_workspace_bytes(_capi.EgnnDims(N=1000, E=32_000, **kw))
+    per_edge = (64 + 2 * 32 + 2 * 32) * 4 + 64 * 4 + 16 + 4
+    assert two < 0.6 * 32_000 * per_edge + one, (one, two)

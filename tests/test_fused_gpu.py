@@ -151,6 +151,24 @@ def test_egnn_h128_edge_features_24(mean):
     check_case(Case(rowptr, col, 128, 24, 128, 128, 128, seed=83, eq=True, mean_agg=mean, edge_ids=perm), "bf16")
 
 
+@pytest.mark.parametrize("dims,eq,mean", [((32, 16, 64, 32, 32), True, False), ((128, 16, 128, 128, 128), True, True),
+                                           ((128, 24, 128, 128, 128), False, False)])
+def test_fp32_edge_chunks(dims, eq, mean):
+    """The fp32 backward in edge chunks (more than 8,192 edges: at least two; Gh, Gx, r^2 and the factors
+    held one chunk at a time, the node sums and weight gradients added in chunk order): rows that straddle
+    the chunk boundaries, empty rows, a degree-1,500 row, edge ids that permute the feature rows."""
+    from pymolecular_amd import _capi
+    F, FE, H, O, M = dims
+    degs = np.array([0, 1500, 3, 61, 0, 7, 33, 2, 90, 1, 31] * 60)
+    rowptr, col = random_csr(len(degs), degs, seed=95)
+    E = len(col)
+    perm = np.random.Generator(np.random.PCG64(96)).permutation(E)
+    d = _capi.EgnnDims(N=len(degs), E=E, F=F, FE=FE, H=H, O=O, M=M, equivariant=int(eq), mean_agg=int(mean), dtype=0)
+    print(f"[fp32-chunks] N={len(degs)} E={E} dims={dims} eq={eq} mean={mean} "
+          f"workspace {_capi.lib().egnn_bwd_workspace_bytes(d) / 2 ** 20:.1f} MB", flush=True)
+    check_case(Case(rowptr, col, F, FE, H, O, M, seed=97, eq=eq, mean_agg=mean, edge_ids=perm), "fp32")
+
+
 def test_mpnn_forward_wide_message_rows():
     """Message rows 2 MiB apart (an output of more than 2 GB in all): the MPNN forward leaves the edge-parallel
     kernel, whose stores use 32-bit offsets, for the cooperative kernel; both against the oracle."""
