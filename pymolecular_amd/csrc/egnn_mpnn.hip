@@ -4,7 +4,7 @@
 // issues vector-ALU instructions at about half the rate).  Each wave runs the
 // message chain of its own 16-edge sub-tile from end to end in registers:
 //   S1  pre1 = W_u e + P_i + Q_j            (the P_i + Q_j sum is an MFMA against a 0/1 operand)
-//       m1 = SiLU(pre1), s1 = SiLU'(pre1)
+//       m1 = SiLU(pre1), s1 = SiLU'(pre1)   (s1 kept in fp32 registers until S5)
 //   S2  pre2 = W_hl^T m1 + b2, s2 = SiLU'(pre2)
 //   S4  g_a2 = g_m,i * s2                   (g_m,i: the incoming message gradient of row i)
 //   S5  g_a1 = (W_hl g_a2) * s1             stored per edge as Gh (dL/dpre1)
@@ -14,8 +14,9 @@
 // W_hl^T).
 //
 // The weight gradients contract over edges, which needs edge-major operands.
-// After its chain each wave writes its m1, g_a2 and g_a1 (and the edge
-// features) into chain-ordered LDS buffers of the 128-edge block tile; after a
+// During its chain each wave writes its edge features (after S1), m1 and g_a2
+// (after S4) and g_a1 (after S5) into chain-ordered LDS buffers of the 128-edge
+// block tile, which the barrier at the top of the tile has freed; after a second
 // barrier wave w reads them back edge-major with transposing LDS reads and
 // accumulates, over all 128 edges, a 64 x 32 block of dW_hl, the rows
 // [16 w, 16 w + 16) of dW_e and 16 columns of db2 in its registers.  Each block writes
@@ -23,7 +24,15 @@
 // edge-major g_a1 gives the destination sums of Gh (dP) per 32-edge tile, by an
 // MFMA against the tile's 0/1 segment matrix: rows whole in the tile are stored,
 // the partial first and last rows go to carry slots that the fix-up sums in tile
-// order.  The source sums (dQ) are made by the node reduction.
+// order.  Every wave holds the four rank tables of its block tile in registers
+// (one int per lane, loaded at the top of the tile) and builds the segment
+// operands with vector instructions.  The source sums (dQ) are made by the node
+// reduction.
+// The two waves of a SIMD run the same chain; issue favours the older one (w < 4),
+// which would finish its chain long before the younger one and wait at the
+// barrier.  The younger wave (w >= 4) raises its priority from the top of the tile
+// to the middle of S4, and again for the dW_hl products, so that both reach the
+// barriers at about the same time.
 // ID (instrument only, EGNN_FLAG_PROBE_IDENTITY): the layer with the MLP
 // replaced by identity, so g_a1 = the incoming message gradient of row i.  The
 // index loads, the gathers (P_i | Q_j, edge features, message gradient: every
@@ -65,15 +74,10 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 s_m1[CHB];
   __shared__ __attribute__((aligned(16))) bf16 s_ga2[CHB];
   __shared__ __attribute__((aligned(16))) bf16 s_g1[CHB];
-  // destination sums: the rank tables of the block tile's 32-edge tiles (from the schedule, one per
-  // wave 0..3), and the 0/1 patterns of the segment matrix
-  __shared__ int s_tab[kEpTile / 32][kTabInts];
-  __shared__ uint2 s_lut[16];
   constexpr int UP = kEpTile + 8;               // row pitch of s_u: 16-byte row offsets spread the dW_e reads over the banks
   __shared__ __attribute__((aligned(16))) bf16 s_u[NUS * UP];                   // [slot][128 edges, kappa order]
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
-  seg_lut_init(s_lut, threadIdx.x);
   const char* PQ = (const char*)a.PQ;
   const bf16* ef = (const bf16*)a.ef;
   const bf16* gmsg = (const bf16*)a.gmsg;
@@ -149,17 +153,38 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
   // the wave's chain for block tile T from its gathers, then the block's weight-gradient products
   auto tile = [&](int64_t T, EpGat& cur, const EpIdx& xn) {
     const uint32_t e = (uint32_t)T * kEpTile + 16 * w + c;
-    // waves 0..3: the rank table of 32-edge tile w (one int per lane; issued first: only these waves
-    // load it); a tile past the last edge has no ranks
-    const int64_t ntt = ((int64_t)E + 31) / 32, tw = T * (kEpTile / 32) + w;
-    int tabv = 0;
-    if (w < NK) tabv = a.tile_tab[(tw < ntt ? tw : ntt - 1) * kTabInts + l];
+    // the rank tables of the block tile's four 32-edge tiles (lane l: int l of table eh), read after
+    // the chain; a tile past the last edge has no ranks
+    const int64_t ntt = ((int64_t)E + 31) / 32;
+    int tabv[NK];
+#pragma unroll
+    for (int eh = 0; eh < NK; ++eh) {
+      const int64_t te = T * NK + eh;
+      tabv[eh] = a.tile_tab[(te < ntt ? te : ntt - 1) * kTabInts + l];
+    }
     if ((uint32_t)T * kEpTile + kEpTile > E) {   // last tile: zero g_m on the edges past E (block-uniform)
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)
         if (e >= E) cur.gm[rb] = bf16x4{(bf16)0.0f, (bf16)0.0f, (bf16)0.0f, (bf16)0.0f};
     }
     bf16x8 m1c[KH], ga2c[KO], g1c[KH];
+    __syncthreads();   // every wave has read the previous tile's buffers
+    if (w >= 4) __builtin_amdgcn_s_setprio(1);   // the younger wave of each SIMD first, to the middle of S4
+    // chain chunk (kc, w) of an LDS buffer of the block tile
+    const int sl = chain_slot<SW>(l);
+    auto put = [&](bf16* buf, const bf16x8* v) {
+#pragma unroll
+      for (int kc = 0; kc < KH; ++kc) *reinterpret_cast<bf16x8*>(buf + ((kc * NB + w) * 64 + sl) * 8) = v[kc];
+    };
+    auto put_u = [&]() {
+      if constexpr (NU > 0) {
+        if (8 * g < FE) {   // edge 16 (w & 1) + c of K-chunk w >> 1 at position 8 (c >> 2) + 4 (w & 1) + (c & 3)
+          bf16* p = s_u + 8 * g * UP + 32 * (w >> 1) + 8 * (c >> 2) + 4 * (w & 1) + (c & 3);
+#pragma unroll
+          for (int s = 0; s < 8; ++s) p[s * UP] = cur.u[s];
+        }
+      }
+    };
     if constexpr (ID) {   // g_a1 = g_m,i: stored as Gh and passed on as the chain of g_a1
       bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
 #pragma unroll
@@ -168,13 +193,16 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
       for (int k = 0; k < KH; ++k) g1c[k] = __builtin_shufflevector(cur.gm[2 * k], cur.gm[2 * k + 1], 0, 1, 2, 3, 4, 5, 6, 7);
       gather_pq(xn, cur);   // the next tile's
       gather_gm(xn, cur);
+      put(s_g1, g1c);
+      put_u();
+      gather_u(xn, cur);
     } else {
     // Each stage is software-pipelined over its eight 16-row blocks: the LDS operands of block
     // rb + 1 are requested before the products of block rb, and the elementwise work of block
     // rb - 1 follows them, so neither the LDS latency nor the product latency is waited for in
     // line.  Scheduling barriers keep that order.
-    // ---- S1: pre1 = W_u e + P_i + Q_j; m1 = SiLU(pre1), s1 = SiLU'(pre1) (bf16)
-    bf16x4 s1[NRB];
+    // ---- S1: pre1 = W_u e + P_i + Q_j; m1 = SiLU(pre1) (bf16), s1 = SiLU'(pre1) (fp32)
+    f32x4 s1[NRB];
     {
       bf16x8 fw[2];
       f32x4 acc[2], y[2];
@@ -199,13 +227,15 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
             y[r & 1][i] = v.y;
             d[i] = v.d;
           }
-          s1[r] = pack4(d);
+          s1[r] = d;
           if (r & 1) m1c[r >> 1] = pack_chunk<bf16>(y[0], y[1]);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
     gather_pq(xn, cur);   // the next tile's
+    put_u();             // the edge features, read by dW_e
+    gather_u(xn, cur);   // the next tile's
     // ---- S2, S4: s2 = SiLU'(W_hl^T m1 + b2), g_a2 = g_m,i s2
     {
       bf16x8 fr[2][KH];
@@ -227,15 +257,22 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         }
         if (rb >= 1) {
           const int r = rb - 1;
+          if (r == 4) __builtin_amdgcn_s_setprio(0);   // back to age order for the rest of the chain
           const f32x4 gm = unpack4(cur.gm[r]);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) ga[r & 1][i] = gm[i] * silu_yd<bf16>(acc[r & 1][i]).d;
+          for (int i = 0; i < 4; ++i) {   // g_m s2 = g_m s (1 + x (1 - s))
+            const float x = acc[r & 1][i], sg = sigmoid_t<bf16>(x);
+            const float t = __builtin_fmaf(-x, sg, x), gs = gm[i] * sg;
+            ga[r & 1][i] = __builtin_fmaf(gs, t, gs);
+          }
           if (r & 1) ga2c[r >> 1] = pack_chunk<bf16>(ga[0], ga[1]);
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
     gather_gm(xn, cur);   // the next tile's
+    put(s_m1, m1c);       // the operands of dW_hl; ga2c is still read by S5
+    put(s_ga2, ga2c);
     // ---- S5: g_a1 = (W_hl g_a2) s1, stored per edge (Gh has a row for every edge of the last tile)
     {
       bf16* ghr = Gh + (uint64_t)e * H + 4 * g;
@@ -259,7 +296,7 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         }
         if (rb >= 1) {
           const int r = rb - 1;
-          const f32x4 d = unpack4(s1[r]);
+          const f32x4 d = s1[r];
           f32x4 g1;
 #pragma unroll
           for (int i = 0; i < 4; ++i) g1[i] = acc[r & 1][i] * d[i];
@@ -270,30 +307,11 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         }
       }
     }
+    put(s_g1, g1c);
     }   // ID
 
-    // ---- the block tile's edge-major operands: chain chunk (kc, w) of each buffer
-    __syncthreads();   // every wave has read the previous tile's buffers
-    const int sl = chain_slot<SW>(l);
-#pragma unroll
-    for (int kc = 0; kc < KH; ++kc) {
-      const int o = ((kc * NB + w) * 64 + sl) * 8;
-      if constexpr (!ID) {
-        *reinterpret_cast<bf16x8*>(s_m1 + o) = m1c[kc];
-        *reinterpret_cast<bf16x8*>(s_ga2 + o) = ga2c[kc];
-      }
-      *reinterpret_cast<bf16x8*>(s_g1 + o) = g1c[kc];
-    }
-    if constexpr (NU > 0) {
-      if (8 * g < FE) {   // edge 16 (w & 1) + c of K-chunk w >> 1 at position 8 (c >> 2) + 4 (w & 1) + (c & 3)
-        bf16* p = s_u + 8 * g * UP + 32 * (w >> 1) + 8 * (c >> 2) + 4 * (w & 1) + (c & 3);
-#pragma unroll
-        for (int s = 0; s < 8; ++s) p[s * UP] = cur.u[s];
-      }
-    }
-    gather_u(xn, cur);   // the next tile's
-    if (w < NK) s_tab[w][l] = (tw < ntt || l != kTabNrank) ? tabv : 0;
-    __syncthreads();
+    __syncthreads();   // the block tile's operands are in LDS
+    if (w >= 4) __builtin_amdgcn_s_setprio(1);   // the younger waves first through the dW_hl products
     // ---- weight gradients over the 128 edges (four 32-edge K chunks): wave w takes the 4 x 2 blocks
     // h-blocks 4 (w >> 2) .. + 3 x o-blocks 2 (w & 3), + 1 of dW_hl (six edge-major operand chunks per K
     // chunk), the next K chunk's operands requested before the products of this one
@@ -320,35 +338,64 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     {
+      // every operand of the four 32-edge tiles requested before the products
+      bf16x8 Ag[NK];   // g_a1 rows 16 w .. + 15, 32 edges
+#pragma unroll
+      for (int eh = 0; eh < NK; ++eh) Ag[eh] = chain_edge_major<NB, SW>(s_g1, w, c, g, eh);
+      bf16x8 Ub[NK][NU > 0 ? NU : 1];
+      if constexpr (NU > 0) {
+#pragma unroll
+        for (int eh = 0; eh < NK; ++eh)
+#pragma unroll
+          for (int ub = 0; ub < NU; ++ub)
+            Ub[eh][ub] = *reinterpret_cast<const bf16x8*>(s_u + (16 * ub + c) * UP + 32 * eh + 8 * g);
+      }
+      // ranks 0..15 of each tile: lane (c, g) takes rank c (span, target); a tile past the last edge has none
+      int nrk[NK], spn[NK], tgv[NK];
 #pragma unroll
       for (int eh = 0; eh < NK; ++eh) {
-        const bf16x8 Ag = chain_edge_major<NB, SW>(s_g1, w, c, g, eh);   // g_a1 rows 16 w .. + 15, 32 edges
-        if constexpr (NU > 0) {
+        nrk[eh] = T * NK + eh < ntt ? __builtin_amdgcn_readlane(tabv[eh], kTabNrank) : 0;
+        tgv[eh] = shfl_i(tabv[eh], kTabTgt + c);
+        const int sp = shfl_i(tabv[eh], kTabSpan + (c >> 1));
+        spn[eh] = c < nrk[eh] ? (sp >> (16 * (c & 1))) & 0xffff : 0;
+      }
+      if constexpr (NU > 0) {
+#pragma unroll
+        for (int eh = 0; eh < NK; ++eh)
 #pragma unroll
           for (int ub = 0; ub < NU; ++ub) {
             if (16 * ub >= FE) continue;   // column block past the edge features
-            mma(acc_we[ub], Ag, *reinterpret_cast<const bf16x8*>(s_u + (16 * ub + c) * UP + 32 * eh + 8 * g));
+            mma(acc_we[ub], Ag[eh], Ub[eh][ub]);
           }
-        }
-        // destination sums of 32-edge tile eh: D = g_a1 S against its 0/1 segment matrix; a rank that
-        // is a whole row is stored to dP, the partial first / last ranks to the tile's carry slots
-        // 0 / 1 (summed in tile order by the fix-up)
-        const int nrk = __builtin_amdgcn_readfirstlane(s_tab[eh][kTabNrank]);
-        const int64_t tt = T * (kEpTile / 32) + eh;
+      }
+      // destination sums of 32-edge tile eh: D = g_a1 S against its 0/1 segment matrix; a rank that
+      // is a whole row is stored to dP, the partial first / last ranks to the tile's carry slots
+      // 0 / 1 (summed in tile order by the fix-up)
+      auto dst_store = [&](int eh, int tg, const f32x4& D) {
+        const int64_t tt = T * NK + eh;
+        if (tg >= 0)
+          *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * w + 4 * g) = pack4(D);
+        else if (tg > -3)
+          *reinterpret_cast<f32x4*>(a.carry + (tt * 2 - 1 - tg) * O + 16 * w + 4 * g) = D;
+      };
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          if (16 * q >= nrk) break;
-          const int r = 16 * q + c;
-          f32x4 D = zero4();
-          mma(D, Ag, seg_chunk_span(r < nrk ? (int)reinterpret_cast<const uint16_t*>(s_tab[eh] + kTabSpan)[r] : 0,
-                                    g, s_lut));
-          const int tg = s_tab[eh][kTabTgt + r];
-          if (tg >= 0)
-            *reinterpret_cast<bf16x4*>((bf16*)a.dP + (int64_t)tg * a.sdp + 16 * w + 4 * g) = pack4(D);
-          else if (tg > -3)
-            *reinterpret_cast<f32x4*>(a.carry + (tt * 2 - 1 - tg) * O + 16 * w + 4 * g) = D;
-        }
+      for (int eh = 0; eh < NK; ++eh) {
+        if (nrk[eh] == 0) continue;
+        f32x4 D = zero4();
+        mma(D, Ag[eh], seg_chunk_valu(spn[eh], g));
+        dst_store(eh, tgv[eh], D);
+      }
+#pragma unroll
+      for (int eh = 0; eh < NK; ++eh) {
+        if (nrk[eh] <= 16) continue;   // ranks 16..31 (a tile of short rows)
+        const int r = 16 + c;
+        const int tg = shfl_i(tabv[eh], kTabTgt + r);
+        const int sp = shfl_i(tabv[eh], kTabSpan + (r >> 1));
+        f32x4 D = zero4();
+        mma(D, Ag[eh], seg_chunk_valu(r < nrk[eh] ? (sp >> (16 * (r & 1))) & 0xffff : 0, g));
+        dst_store(eh, tg, D);
       }
     }
   };

@@ -168,6 +168,19 @@ __device__ __forceinline__ bf16x8 seg_chunk_span(int span, int g, const uint2* l
   return r;
 }
 
+// B operand S[edge][rank] of the rank with this span (0: no rank), made with vector instructions:
+// lane (c, g) covers edges 4g..4g+3 and 16+4g..16+4g+3 (the pattern of seg_chunk_span, without its table)
+__device__ __forceinline__ bf16x8 seg_chunk_valu(int span, int g) {
+  const int start = span & 0xff, cnt = span >> 8;
+  const uint32_t mrow = cnt >= 32 ? 0xffffffffu : (((1u << cnt) - 1u) << start);
+  const uint32_t x = (mrow >> (4 * g)) & 15u, y = (mrow >> (16 + 4 * g)) & 15u;
+  auto pat = [](uint32_t b) { return ((b & 1u) | ((b & 2u) << 15)) * 0x3F80u; };   // 1.0 in the set halves
+  const uint4 v = make_uint4(pat(x), pat(x >> 2), pat(y), pat(y >> 2));
+  bf16x8 r;
+  __builtin_memcpy(&r, &v, 16);
+  return r;
+}
+
 // Ranks of a 32-edge tile from the rows of its edges (ri[0..TE)) and of the edges
 // just before and after it (ex[0], ex[1]): edge k starts a rank when it is the
 // tile's first edge or its row differs from that of edge k - 1; the first rank's
