@@ -50,7 +50,9 @@ namespace {
 
 using namespace tile;
 
-constexpr int kEpWaves = 8;                   // waves per block, two per SIMD
+constexpr int kEpWaves = 8;
+constexpr uint32_t kOob = 0x80000000u;        // a buffer offset past every buffer (the store writes nothing)
+constexpr int kBufFlags = 0x00020000;         // buffer resource word 3 (gfx9 family): raw, range-checked                   // waves per block, two per SIMD
 constexpr int kEpSub = 16;                    // edges per wave sub-tile
 constexpr int kEpTile = kEpWaves * kEpSub;    // edges per block tile
 
@@ -517,6 +519,26 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   // The first half leaves its messages in the wave's LDS slots; the second half sums both over the
   // tile's ranks (a wave reads only what it wrote: no barrier).
   bf16x4* const m0 = &s_m0[w][0][l];
+  // A rank's sum goes to its out_msg row (a whole row) or to the tile's carry slot (a partial row) by two
+  // bounds-checked buffer stores that every lane issues: the one that does not apply has an offset past
+  // its buffer and writes nothing.  The store count is then the same on every path, so the wait for the
+  // next half's gathers at the end of a tile does not also wait for these stores.
+  const __amdgpu_buffer_rsrc_t rs_msg =
+      __builtin_amdgcn_make_buffer_rsrc(a.out_msg, 0, (int)(a.N * a.smsg * 2), kBufFlags);
+  struct RankDst { uint32_t msg, carry; };   // byte offsets into out_msg and the tile's carry slots (or kOob)
+  auto rank_dst = [&](int tabv, int r, int nrk, int& span) {
+    const int tg = __shfl(tabv, kTabTgt + r, 64);
+    const int sp = __shfl(tabv, kTabSpan + (r >> 1), 64);
+    span = r < nrk ? (sp >> (16 * (r & 1))) & 0xffff : 0;
+    RankDst d{kOob, kOob};
+    if (tg >= 0) d.msg = (uint32_t)(((int64_t)tg * a.smsg + 4 * g) * 2);
+    else if (tg > -3) d.carry = (uint32_t)(((-1 - tg) * O + 4 * g) * 4);
+    return d;
+  };
+  auto store_rank = [&](const f32x4& D, const RankDst& d, int r, __amdgpu_buffer_rsrc_t rc) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, pack4(D)), rs_msg, (int)(d.msg + 32 * r), 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, D), rc, (int)(d.carry + 64 * r), 0, 0);
+  };
   auto half = [&](auto hc, int64_t T, EpGat& cur, const EpIdx& xn, int tabv) {
     constexpr int HC = decltype(hc)::value;
     // ---- S1: m1 = SiLU(W_u e + P_i + Q_j) (features on the rows), software-pipelined over the row blocks
@@ -557,26 +579,21 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       }
     }
     gather(xn, cur);
-    // ---- the tile's rank table (second half): lane (g, c) handles ranks c and 16 + c; the segment
-    // operand of ranks 16 .. 31 (tiles of more than 16 rows) is rebuilt where it is used.  Each rank's
-    // destination is a 32-bit byte offset from out_msg (bit 31 clear; the host keeps out_msg under 2 GB) or
-    // from the tile's carry slots (bit 31 set; none: ~0), so that the stores of the feature blocks differ
-    // only in their immediate offsets.
-    int nrk = 0, span[2] = {0, 0};
-    uint32_t dst[2] = {~0u, ~0u};
+    // ---- the tile's rank table (second half): lane (g, c) handles rank c; the destinations and the
+    // segment operand of ranks 16 .. 31 (tiles of more than 16 rows) are rebuilt where they are used.
+    // A rank's destinations are byte offsets into out_msg (the host keeps it under 2 GB) and into the
+    // tile's carry slots, the one that does not apply kOob, so that the stores of the feature blocks
+    // differ only in their immediate offsets.
+    int nrk = 0;
+    RankDst d0;
     bf16x8 sq0;
+    __amdgpu_buffer_rsrc_t rs_carry;
     if constexpr (HC == 1) {
       nrk = __builtin_amdgcn_readlane(tabv, kTabNrank);
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int r = 16 * q + c;
-        const int tg = __shfl(tabv, kTabTgt + r, 64);
-        const int sp = __shfl(tabv, kTabSpan + (r >> 1), 64);
-        span[q] = r < nrk ? (sp >> (16 * (r & 1))) & 0xffff : 0;
-        if (tg >= 0) dst[q] = (uint32_t)(((int64_t)tg * a.smsg + 4 * g) * 2);
-        else if (tg > -3) dst[q] = 0x80000000u | (uint32_t)(((-1 - tg) * O + 4 * g) * 4);
-      }
-      sq0 = seg_chunk_span(span[0], g, s_lut);
+      int span0;
+      d0 = rank_dst(tabv, c, nrk, span0);
+      sq0 = seg_chunk_span(span0, g, s_lut);
+      rs_carry = __builtin_amdgcn_make_buffer_rsrc(a.carry + T * 2 * O, 0, 2 * O * 4, kBufFlags);
     }
     if constexpr (ID) {   // the messages of feature block r: edges 4g .. 4g + 3 of this half, feature 16 r + c
 #pragma unroll
@@ -585,15 +602,15 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
           m0[64 * r] = mid[r];
         } else {
           const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mid[r], 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-          for (int q = 0; q < 2; ++q) {
-            if (16 * q >= nrk) break;
-            f32x4 D = zero4();
-            mma(D, Am, q == 0 ? sq0 : seg_chunk_span(span[1], g, s_lut));
-            if (dst[q] < 0x80000000u)
-              *reinterpret_cast<bf16x4*>((char*)a.out_msg + dst[q] + 32 * r) = pack4(D);
-            else if (dst[q] != ~0u)
-              *reinterpret_cast<f32x4*>((char*)(a.carry + T * 2 * O) + (dst[q] & 0x7fffffffu) + 64 * r) = D;
+          f32x4 D = zero4();
+          mma(D, Am, sq0);
+          store_rank(D, d0, r, rs_carry);
+          if (nrk > 16) {
+            int span1;
+            const RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+            D = zero4();
+            mma(D, Am, seg_chunk_span(span1, g, s_lut));
+            store_rank(D, d1, r, rs_carry);
           }
         }
       }
@@ -630,15 +647,15 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
           } else {
             // rows 16 r .. 16 r + 15 of m over the tile's 32 edges in kappa_chain order
             const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mr, 0, 1, 2, 3, 4, 5, 6, 7);
-#pragma unroll
-            for (int q = 0; q < 2; ++q) {
-              if (16 * q >= nrk) break;
-              f32x4 D = zero4();
-              mma(D, Am, q == 0 ? sq0 : seg_chunk_span(span[1], g, s_lut));
-              if (dst[q] < 0x80000000u)
-                *reinterpret_cast<bf16x4*>((char*)a.out_msg + dst[q] + 32 * r) = pack4(D);
-              else if (dst[q] != ~0u)
-                *reinterpret_cast<f32x4*>((char*)(a.carry + T * 2 * O) + (dst[q] & 0x7fffffffu) + 64 * r) = D;
+            f32x4 D = zero4();
+            mma(D, Am, sq0);
+            store_rank(D, d0, r, rs_carry);
+            if (nrk > 16) {   // ranks 16..31 (a tile of short rows)
+              int span1;
+              const RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+              D = zero4();
+              mma(D, Am, seg_chunk_span(span1, g, s_lut));
+              store_rank(D, d1, r, rs_carry);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
