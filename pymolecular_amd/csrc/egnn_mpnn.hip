@@ -616,14 +616,17 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       }
     } else {
     // ---- S2: m = SiLU(m1 W_hl + b2) (edges on the rows); W_hl fragments of block rb + 1 requested once the
-    // products of rb have read theirs
+    // products of rb have read theirs, and in the second half the first half's messages of block rb - 1
+    // before them
     {
       bf16x8 fr[KH];
       f32x4 acc[2];
+      bf16x4 m0v;
 #pragma unroll
       for (int k = 0; k < KH; ++k) fr[k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
 #pragma unroll
       for (int rb = 0; rb <= NRB; ++rb) {
+        if (HC == 1 && rb >= 1) m0v = m0[64 * (rb - 1)];   // read by this iteration's sums, after the products
         if (rb < NRB) {
           acc[rb & 1] = s_b2[16 * rb + c];
 #pragma unroll
@@ -646,7 +649,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
             m0[64 * r] = mr;
           } else {
             // rows 16 r .. 16 r + 15 of m over the tile's 32 edges in kappa_chain order
-            const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mr, 0, 1, 2, 3, 4, 5, 6, 7);
+            const bf16x8 Am = __builtin_shufflevector(m0v, mr, 0, 1, 2, 3, 4, 5, 6, 7);
             f32x4 D = zero4();
             mma(D, Am, sq0);
             store_rank(D, d0, r, rs_carry);
