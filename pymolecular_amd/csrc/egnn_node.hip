@@ -1401,14 +1401,14 @@ int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
 // edge ids in the chunk (found by binary search: the list ascends); with acc the
 // sums are added to what an earlier chunk stored, element by element, so the
 // chunks add up in chunk order.
-template <typename T, int H>
+template <typename T, int H, bool DST>
 __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ Gh, const float* __restrict__ Gx,
                                                           const int32_t* __restrict__ rowptr,
                                                           const int32_t* __restrict__ csc_ptr,
                                                           const int32_t* __restrict__ csc_eid, T* __restrict__ dPQ,
                                                           float* __restrict__ gcoord, int64_t sgc,
                                                           const float* __restrict__ gres, int64_t sgr, int64_t N,
-                                                          int eq, int dst, int64_t e0, int64_t e1, int acc) {
+                                                          int eq, int64_t e0, int64_t e1, int acc) {
   constexpr int VPL = 16 / sizeof(T);          // values per lane per load
   constexpr int LPE = H / VPL;                 // lanes per edge row
   constexpr int EPW = 64 / LPE;                // edges per wave-wide load
@@ -1445,12 +1445,14 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
 #pragma unroll
     for (int u = 0; u < VPL; ++u) ap[u] = aq[u] = 0.f;
     float ax = 0.f;
-    // destination sums (unless the edge kernel made them): the row's edges are contiguous
-    if (dst) {
-      const int rs = (int)max((int64_t)rowptr[n], e0), re = (int)min((int64_t)rowptr[n + 1], e1);
-      if (re > rs) gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+    // the row's edges [rs, re) (destination sums, unless the edge kernel made them) and the node's
+    // entries [cs, ce) of the stable CSC (source sums): both ranges, and the first 64 CSC edge ids (one
+    // per lane, broadcast by lane shuffles), are requested before the destination rows are summed
+    int rs = 0, re = 0;
+    if constexpr (DST) {
+      rs = (int)max((int64_t)rowptr[n], e0);
+      re = (int)min((int64_t)rowptr[n + 1], e1);
     }
-    // source sums: the edges listed for n by the stable CSC, edge ids 64 at a time, one per lane
     int cs = csc_ptr[n], ce = csc_ptr[n + 1];
     if (e0 > 0 || e1 < (int64_t)INT32_MAX) {   // the chunk's sub-range: first entries with id >= e0, >= e1
       auto lower = [&](int lo, int hi, int64_t key) {
@@ -1464,9 +1466,15 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
       ce = lower(a0, ce, e1);
       cs = a0;
     }
-    for (int k0 = cs; k0 < ce; k0 += 64) {
-      const int cnt = ce - k0 < 64 ? ce - k0 : 64;
-      const int my = csc_eid[k0 + (l < cnt ? l : cnt - 1)];
+    const int ns = ce - cs;
+    int my = 0;
+    if (ns > 0) my = csc_eid[cs + (l < ns ? l : ns - 1)];
+    if constexpr (DST) {   // the row's edges are contiguous
+      if (re > rs) gather(re - rs, [&](int j) { return rs + j; }, ap, ax, 1.0f);
+    }
+    for (int k0 = 0; k0 < ns; k0 += 64) {
+      const int cnt = ns - k0 < 64 ? ns - k0 : 64;
+      if (k0 > 0) my = csc_eid[cs + k0 + (l < cnt ? l : cnt - 1)];
       gather(cnt, [&](int j) { return __shfl(my, j, 64); }, aq, ax, -1.0f);
     }
     // combine the EPW edge groups (lanes q, q + LPE, q + 2 LPE, ...) in a fixed order
@@ -1489,15 +1497,15 @@ __global__ __launch_bounds__(256) void node_reduce_kernel(const T* __restrict__ 
         bf16x8 vp, vq;
 #pragma unroll
         for (int u = 0; u < VPL; ++u) { vp[u] = (bf16)ap[u]; vq[u] = (bf16)aq[u]; }
-        if (dst) *reinterpret_cast<bf16x8*>(out) = vp;
+        if (DST) *reinterpret_cast<bf16x8*>(out) = vp;
         *reinterpret_cast<bf16x8*>(out + H) = vq;
       } else {
         f32x4 vp = f32x4{ap[0], ap[1], ap[2], ap[3]}, vq = f32x4{aq[0], aq[1], aq[2], aq[3]};
         if (acc) {
-          if (dst) vp += *reinterpret_cast<const f32x4*>(out);
+          if (DST) vp += *reinterpret_cast<const f32x4*>(out);
           vq += *reinterpret_cast<const f32x4*>(out + H);
         }
-        if (dst) *reinterpret_cast<f32x4*>(out) = vp;
+        if (DST) *reinterpret_cast<f32x4*>(out) = vp;
         *reinterpret_cast<f32x4*>(out + H) = vq;
       }
     }
@@ -1510,8 +1518,14 @@ int launch_node_reduce(const LayerShape& s, const void* Gh, const float* Gx, con
   if (accumulate && s.bf16) return (int)hipErrorInvalidValue;   // chunk sums add up in fp32 outputs only
   int blocks = (int)std::min<int64_t>(cdiv(s.N, 4), 65535);
   int eq = s.eq ? 1 : 0;
-  int dst = coop_dst_sums(s) ? 0 : 1;   // the cooperative MPNN kernel stores the destination sums
-#define NR_LAUNCH(T, HH) hipLaunchKernelGGL((node_reduce_kernel<T, HH>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, dst, e0, e1, accumulate ? 1 : 0)
+  const bool dst = !coop_dst_sums(s);   // the cooperative MPNN kernel stores the destination sums
+#define NR_LAUNCH(T, HH)                                                                                            \
+  do {                                                                                                             \
+    if (dst) hipLaunchKernelGGL((node_reduce_kernel<T, HH, true>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx, \
+                                rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, e0, e1, accumulate ? 1 : 0); \
+    else hipLaunchKernelGGL((node_reduce_kernel<T, HH, false>), dim3(blocks), dim3(256), 0, st, (const T*)Gh, Gx,    \
+                            rowptr, csc_ptr, csc_eid, (T*)dPQ, gcoord, sgc, gres, sgr, s.N, eq, e0, e1, accumulate ? 1 : 0); \
+  } while (0)
   if (s.bf16) {
     if (s.H == 64) NR_LAUNCH(bf16, 64); else if (s.H == 128) NR_LAUNCH(bf16, 128); else NR_LAUNCH(bf16, 256);
   } else {
