@@ -102,6 +102,14 @@ __device__ __forceinline__ f32x4 load4_f32(const bf16* p) {
   return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
 }
 
+// ---- bounds-checked buffer accesses ----------------------------------------
+// A raw buffer resource over num bytes: loads past the end return 0, stores past
+// the end write nothing.  Every lane can then issue the access on every path (the
+// one that does not apply gets an offset past the buffer), which keeps the
+// memory-wait counts the compiler derives exact.
+constexpr uint32_t kOob = 0x80000000u;   // a buffer offset past every buffer
+constexpr int kBufFlags = 0x00020000;    // buffer resource word 3 (gfx9 family): raw, range-checked
+
 // ---- activations ---------------------------------------------------------
 // SiLU(x) = x / (1 + e^-x), written from the definition; sigma is kept so the
 // backward gets SiLU'(x) = sigma * (1 + x (1 - sigma)) for a few more flops.

@@ -50,9 +50,7 @@ namespace {
 
 using namespace tile;
 
-constexpr int kEpWaves = 8;
-constexpr uint32_t kOob = 0x80000000u;        // a buffer offset past every buffer (the store writes nothing)
-constexpr int kBufFlags = 0x00020000;         // buffer resource word 3 (gfx9 family): raw, range-checked                   // waves per block, two per SIMD
+constexpr int kEpWaves = 8;                   // waves per block, two per SIMD
 constexpr int kEpSub = 16;                    // edges per wave sub-tile
 constexpr int kEpTile = kEpWaves * kEpSub;    // edges per block tile
 
