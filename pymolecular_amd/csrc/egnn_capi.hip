@@ -194,6 +194,7 @@ int32_t egnn_fwd(const EgnnDims* dims, const EgnnStrides* strides, const void* h
   a.geo = w.geo;
   // the edge-parallel MPNN forward addresses message rows by 32-bit byte offsets: the instrument runs it only
   if (s.probe && s.N * a.smsg * 2 >= (int64_t(1) << 31)) return EGNN_ERR_DIMS;
+  a.ranges = coop_supported(s) ? coop_fwd_ranges(s, a) : 0;   // read by the edge kernel and the fix-up
   {
     ProfScope ps(EGNN_K_FWD_EDGE, st);
     const int r = coop_supported(s) ? launch_coop_fwd(s, a, st)

@@ -1267,10 +1267,14 @@ int64_t coop_dw_len(const LayerShape& s) {
          (s.eq ? s.H : 0);
 }
 
-int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+int64_t coop_fwd_ranges(const LayerShape& s, const FwdArgs& a) {
   // the edge-parallel forward addresses the message rows by 32-bit byte offsets (make_shape refuses the
   // instrument beyond them)
-  if (mpnn_ep(s) && s.N * a.smsg * 2 < (int64_t(1) << 31)) return launch_mpnn_fwd_ep(a, s.probe, st);
+  return mpnn_ep(s) && s.N * a.smsg * 2 < (int64_t(1) << 31) ? mpnn_fwd_ep_waves(s.E) : 0;
+}
+
+int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
+  if (coop_fwd_ranges(s, a) > 0) return launch_mpnn_fwd_ep(a, s.probe, st);
   if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }

@@ -244,8 +244,69 @@ __global__ __launch_bounds__(256) void fwd_edge_kernel(FwdArgs a) {
 // each, the predicate of the schedule's fix-row flags) get x added to the
 // aggregate the edge kernel stored, one thread per row, by the blocks from
 // nfb on; the two sets are disjoint, so no output is touched twice.
+// The fix-up after the edge-parallel MPNN forward (contiguous tile ranges, FwdArgs::ranges > 0): each
+// range's piece of a row is in the carry slot of the piece's last tile, and the edge kernel stored the
+// rows that lie in one range itself.  A wave checks 64 fix rows at once, one per lane; the rows left to
+// do (empty ones: zeros; those that cross a range boundary: the sum of their pieces in tile order) are
+// completed two at a time, one per half wave.
+template <typename T>
+__device__ void fixup_ranges(const FwdArgs& a, int O) {
+  const int l = threadIdx.x & 63, h = l >> 5, lh = l & 31;
+  const int nfix = *a.n_fix;
+  const int R = (int)a.ranges, ntt = (int)((a.E + kTileEdges - 1) / kTileEdges);   // below 2^26
+  const int64_t nwv = (int64_t)gridDim.x * 4;
+  for (int64_t f0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 64; f0 < nfix; f0 += nwv * 64) {
+    const int64_t f = f0 + l;
+    int r = 0, rs = 0, re = 0;
+    bool work = false;
+    if (f < nfix) {
+      r = a.fix_rows[f];
+      rs = a.rowptr[r];
+      re = a.rowptr[r + 1];
+      work = re == rs || ep_range_of(rs / kTileEdges, R, ntt) != ep_range_of((re - 1) / kTileEdges, R, ntt);
+    }
+    uint64_t m = __ballot(work);
+    while (m) {
+      const int l0 = __builtin_ctzll(m);
+      m &= m - 1;
+      const int l1 = m ? __builtin_ctzll(m) : l0;
+      if (m) m &= m - 1;
+      const int src = h ? l1 : l0;
+      const int rr = __shfl(r, src, 64), rrs = __shfl(rs, src, 64), rre = __shfl(re, src, 64);
+      if (h && l1 == l0) continue;   // no second row: the upper half idles
+      int k0 = 0, np = 0, t0 = 0, t1 = 0, slot0 = 0;
+      if (rre > rrs) {
+        t0 = rrs / kTileEdges;
+        t1 = (rre - 1) / kTileEdges;
+        slot0 = rrs % kTileEdges == 0 ? 0 : 1;
+        k0 = (int)ep_range_of(t0, R, ntt);
+        np = (int)ep_range_of(t1, R, ntt) - k0 + 1;
+      }
+      for (int c4 = 4 * lh; c4 < O; c4 += 4 * 32) {
+        f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int k = 0; k < np; ++k) {   // the piece of range k0 + k ends at its last tile or at t1
+          const int te0 = (int)ep_range_begin(k0 + k + 1, R, ntt) - 1, te = te0 < t1 ? te0 : t1;
+          acc += load4_f32(a.carry + ((int64_t)te * 2 + (te == t0 ? slot0 : 0)) * O + c4);
+        }
+        T* o = (T*)a.out_msg + (int64_t)rr * a.smsg + c4;
+        if constexpr (sizeof(T) == 2) {
+          *reinterpret_cast<bf16x4*>(o) = bf16x4{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+        } else {
+          *reinterpret_cast<f32x4*>(o) = acc;
+        }
+      }
+    }
+  }
+}
+
 template <typename T, bool EQ>
 __global__ __launch_bounds__(256) void fwd_fixup_kernel(FwdArgs a, int O, int nfb) {
+  if constexpr (!EQ) {
+    if (a.ranges > 0) {
+      fixup_ranges<T>(a, O);
+      return;
+    }
+  }
   const int SEGW = O + (EQ ? 4 : 0);
   const int l = threadIdx.x & 63;
   if (EQ && (int)blockIdx.x >= nfb) {

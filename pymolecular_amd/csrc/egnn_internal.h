@@ -209,7 +209,24 @@ struct FwdArgs {
   int lin;           // weights in torch.nn.Linear (out, in) layout
   int coord_res;     // out_mov = coord + the aggregated update
   const int32_t* tile_tab;   // the schedule's per-32-edge-tile rank tables (SchedView::tile_tab)
+  // edge-parallel MPNN forward: the number of waves, each taking one contiguous range of the 32-edge
+  // tiles (range k: tiles [ep_range_begin(k), ep_range_begin(k + 1))); a row split over tiles of one
+  // range is summed and stored by its wave, only the pieces of rows that cross a range boundary go to
+  // carry slots.  0: tiles strided over the waves, every split row's pieces in carry slots.
+  int64_t ranges;
 };
+// first tile of range k of R contiguous ranges over ntt tiles (the first ntt % R ranges one tile longer)
+__host__ __device__ inline int64_t ep_range_begin(int64_t k, int64_t R, int64_t ntt) {
+  const int64_t q = ntt / R, rem = ntt % R;
+  return k * q + (k < rem ? k : rem);
+}
+// the range that holds tile t
+__host__ __device__ inline int64_t ep_range_of(int64_t t, int64_t R, int64_t ntt) {
+  const int64_t q = ntt / R, rem = ntt % R, th = rem * (q + 1);
+  return t < th ? t / (q + 1) : rem + (t - th) / q;
+}
+// waves (ranges) of the edge-parallel MPNN forward over E edges: eight per block, up to two blocks per CU
+int64_t mpnn_fwd_ep_waves(int64_t E);
 // part 0: edge tiles, part 1: split/empty-row fix-up
 int launch_fwd(const LayerShape& s, const FwdArgs& a, int part, hipStream_t st);
 
@@ -249,6 +266,8 @@ int coop_bwd_blocks(const LayerShape& s);
 // reduction then sums the source side only.
 bool coop_dst_sums(const LayerShape& s);
 int64_t coop_dw_len(const LayerShape& s);   // [dWhl (H+1)xO | dW1m (O+1)xM | dw2m M | dWe HxFE | dwd H]
+// FwdArgs::ranges for the layer: the edge-parallel MPNN forward's wave count when it runs, else 0
+int64_t coop_fwd_ranges(const LayerShape& s, const FwdArgs& a);
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st);
 int launch_coop_bwd(const LayerShape& s, const BwdArgs& a, int nblk, hipStream_t st);
 // Edge-parallel MPNN backward (bf16, H = O = 128): 128-edge block tiles, per-block partials of

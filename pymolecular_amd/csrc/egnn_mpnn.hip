@@ -443,15 +443,18 @@ __global__ __launch_bounds__(512, 2) void mpnn_bwd_ep_kernel(BwdArgs a) {
 // ---------------------------------------------------------------------------
 // forward of the MPNN layer, edge-parallel (bf16, H = O = 128)
 // ---------------------------------------------------------------------------
-// Each wave takes whole 32-edge schedule tiles, one 16-edge half at a time.  S1 (pre1 = W_u e + P_i
-// + Q_j, m1 = SiLU(pre1)) is computed with the features on the MFMA rows, so that its C-blocks are
-// S2's operand; S2 (m = SiLU(m1 W_hl + b2)) with the edges on the rows, so that a lane's C-block of
-// feature block rb holds four edges of one feature.  The first half's messages wait in registers
-// (bf16); with the second half's they form, per feature block, the A operand (16 features x the
-// tile's 32 edges) of the per-row sums: one MFMA per 16 ranks against the 0/1 segment matrix from
-// the schedule's rank table, a rank that is a whole row stored to out_msg, a partial first / last
-// rank to the tile's carry slot 0 / 1 (summed in tile order by the fix-up launch).  No LDS exchange
-// and no barrier after the weight copy: the waves run independently, two blocks of eight per CU.
+// Each wave takes one contiguous range of whole 32-edge schedule tiles, one 16-edge half at a time.
+// S1 (pre1 = W_u e + P_i + Q_j, m1 = SiLU(pre1)) is computed with the features on the MFMA rows, so
+// that its C-blocks are S2's operand; S2 (m = SiLU(m1 W_hl + b2)) with the edges on the rows, so that
+// a lane's C-block of feature block rb holds four edges of one feature.  The first half's messages
+// wait in LDS (bf16); with the second half's they form, per feature block, the A operand (16 features
+// x the tile's 32 edges) of the per-row sums: one MFMA per 16 ranks against the 0/1 segment matrix
+// from the schedule's rank table, a rank that is a whole row stored to out_msg.  A row that goes on
+// into the next tile of the range stays open: its partial sums wait in the wave's LDS row and are the
+// start of the next tile's rank-0 sums, and the row is stored once it closes.  Only the pieces of rows
+// that cross a range boundary go to the tile's carry slot 0 / 1, which the fix-up launch sums in tile
+// order.  No LDS exchange and no barrier after the weight copy: the waves run independently, two
+// blocks of eight per CU.
 // ID (instrument only, EGNN_FLAG_PROBE_IDENTITY): the layer with the MLP replaced by identity, the
 // message m = W_u e + P_i + Q_j computed with the edges on the MFMA rows (the layout S2 leaves), so
 // that the gathers, the rank tables, the per-row sums, their stores and carries are the layer's and
@@ -466,6 +469,8 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) bf16x4 s_m0[kEpWaves][NRB][64];   // each wave's first-half messages
   __shared__ __attribute__((aligned(16))) bf16x8 s_ipq[64];   // pq_sum_chunk of each lane
   __shared__ uint2 s_lut[16];
+  __shared__ __attribute__((aligned(16))) f32x4 s_open[kEpWaves][NRB][4];   // the open row's partial sums
+  __shared__ __attribute__((aligned(16))) f32x4 s_zero[NRB][4];              // zeros: the other lanes' start
 
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = threadIdx.x & 63, c = l & 15, g = l >> 4;
   seg_lut_init(s_lut, threadIdx.x);
@@ -475,7 +480,6 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
   const int N = (int)a.N;
   const int FE = a.FE;
   const int64_t ntt = (a.E + 31) / 32;
-  const int64_t GW = (int64_t)gridDim.x * kEpWaves;   // waves of the grid: the tile stride
   const bool use_eids = a.eids != nullptr;
 
   for (int q = threadIdx.x; q < NRB * KH * kFragElems / 8; q += 512)
@@ -488,6 +492,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     s_b2[q] = f32x4{b, b, b, b};
   }
   if (threadIdx.x < 64) s_ipq[l] = pq_sum_chunk(c, g);
+  if (threadIdx.x < NRB * 4) (&s_zero[0][0])[threadIdx.x] = zero4();
 
   auto load_idx = [&](int64_t T, int h, EpIdx& x) {   // E < 2^31 (coop_supported)
     const uint32_t e0 = (uint32_t)T * 32 + 16 * h + c;
@@ -525,6 +530,7 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       __builtin_amdgcn_make_buffer_rsrc(a.out_msg, 0, (int)(a.N * a.smsg * 2), kBufFlags);
   struct RankDst { uint32_t msg, carry; };   // byte offsets into out_msg and the tile's carry slots (or kOob)
   auto rank_dst = [&](int tabv, int r, int nrk, int& span) {
+    asm volatile("" : "+v"(r));   // the shuffle addresses computed here, not held across the tile loop
     const int tg = __shfl(tabv, kTabTgt + r, 64);
     const int sp = __shfl(tabv, kTabSpan + (r >> 1), 64);
     span = r < nrk ? (sp >> (16 * (r & 1))) & 0xffff : 0;
@@ -537,7 +543,17 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, pack4(D)), rs_msg, (int)(d.msg + 32 * r), 0, 0);
     __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, D), rc, (int)(d.carry + 64 * r), 0, 0);
   };
-  auto half = [&](auto hc, int64_t T, EpGat& cur, const EpIdx& xn, int tabv) {
+  // The tile's row pieces that continue a row (a) or into the next tile (b): (a) rank 0 of a tile whose
+  // first row was open at the end of the previous tile of the range, its sum started from the wave's
+  // open-row partial; (b) the last rank, when its row goes on in the next tile of the range, kept as
+  // that partial (no store).  A row that closes in the range it started in goes to its out_msg row;
+  // the pieces of a row that crosses a range boundary go to the carry slots the rank table names.
+  struct Open {
+    bool in, out;    // (a) and (b)
+    bool stored;     // rank 0 of (a) closes here and began in this range: to out_msg row `row`
+    int row;
+  };
+  auto half = [&](auto hc, int64_t T, EpGat& cur, const EpIdx& xn, int tabv, const Open& op) {
     constexpr int HC = decltype(hc)::value;
     // ---- S1: m1 = SiLU(W_u e + P_i + Q_j) (features on the rows), software-pipelined over the row blocks
     bf16x8 m1c[KH];
@@ -586,13 +602,22 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     RankDst d0;
     bf16x8 sq0;
     __amdgpu_buffer_rsrc_t rs_carry;
+    bool keep0 = false, keep1 = false;   // lane's rank (c, 16 + c) is the last and stays open
     if constexpr (HC == 1) {
       nrk = __builtin_amdgcn_readlane(tabv, kTabNrank);
       int span0;
       d0 = rank_dst(tabv, c, nrk, span0);
       sq0 = seg_chunk_span(span0, g, s_lut);
       rs_carry = __builtin_amdgcn_make_buffer_rsrc(a.carry + T * 2 * O, 0, 2 * O * 4, kBufFlags);
+      keep0 = op.out && c == nrk - 1;
+      keep1 = op.out && 16 + c == nrk - 1;
+      if (keep0) d0 = RankDst{kOob, kOob};
+      else if (op.stored && c == 0) d0 = RankDst{(uint32_t)(((int64_t)op.row * a.smsg + 4 * g) * 2), kOob};
     }
+    // a rank-0 sum of feature block r starts from the open-row partial (case a), every other sum from
+    // zeros: one LDS read whose row the lane selects once per tile
+    const f32x4* const srow = (HC == 1 && op.in && c == 0) ? &s_open[w][0][g] : &s_zero[0][g];
+    auto start = [&](int r) { return srow[4 * r]; };
     if constexpr (ID) {   // the messages of feature block r: edges 4g .. 4g + 3 of this half, feature 16 r + c
 #pragma unroll
       for (int r = 0; r < NRB; ++r) {
@@ -600,15 +625,18 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
           m0[64 * r] = mid[r];
         } else {
           const bf16x8 Am = __builtin_shufflevector(m0[64 * r], mid[r], 0, 1, 2, 3, 4, 5, 6, 7);
-          f32x4 D = zero4();
+          f32x4 D = start(r);
           mma(D, Am, sq0);
           store_rank(D, d0, r, rs_carry);
+          if (keep0) s_open[w][r][g] = D;
           if (nrk > 16) {
             int span1;
-            const RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+            RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+            if (keep1) d1 = RankDst{kOob, kOob};
             D = zero4();
             mma(D, Am, seg_chunk_span(span1, g, s_lut));
             store_rank(D, d1, r, rs_carry);
+            if (keep1) s_open[w][r][g] = D;
           }
         }
       }
@@ -620,11 +648,15 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
       bf16x8 fr[KH];
       f32x4 acc[2];
       bf16x4 m0v;
+      f32x4 D0;
 #pragma unroll
       for (int k = 0; k < KH; ++k) fr[k] = *reinterpret_cast<const bf16x8*>(s_whlT + (k * 64 + l) * 8);
 #pragma unroll
       for (int rb = 0; rb <= NRB; ++rb) {
-        if (HC == 1 && rb >= 1) m0v = m0[64 * (rb - 1)];   // read by this iteration's sums, after the products
+        if (HC == 1 && rb >= 1) {   // read by this iteration's sums, after the products
+          m0v = m0[64 * (rb - 1)];
+          D0 = start(rb - 1);
+        }
         if (rb < NRB) {
           acc[rb & 1] = s_b2[16 * rb + c];
 #pragma unroll
@@ -648,15 +680,18 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
           } else {
             // rows 16 r .. 16 r + 15 of m over the tile's 32 edges in kappa_chain order
             const bf16x8 Am = __builtin_shufflevector(m0v, mr, 0, 1, 2, 3, 4, 5, 6, 7);
-            f32x4 D = zero4();
+            f32x4 D = D0;
             mma(D, Am, sq0);
             store_rank(D, d0, r, rs_carry);
+            if (keep0) s_open[w][r][g] = D;
             if (nrk > 16) {   // ranks 16..31 (a tile of short rows)
               int span1;
-              const RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+              RankDst d1 = rank_dst(tabv, 16 + c, nrk, span1);
+              if (keep1) d1 = RankDst{kOob, kOob};
               D = zero4();
               mma(D, Am, seg_chunk_span(span1, g, s_lut));
               store_rank(D, d1, r, rs_carry);
+              if (keep1) s_open[w][r][g] = D;
             }
           }
           __builtin_amdgcn_sched_barrier(0);
@@ -666,27 +701,58 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
     }   // ID
   };
 
-  const int64_t T0 = (int64_t)blockIdx.x * kEpWaves + w;
-  const bool active = T0 < ntt;
+  // this wave's tiles [T0, T1)
+  // (tile counts below 2^26: E < 2^31; the bounds wave-uniform, in scalar registers)
+  const int R = (int)a.ranges, kw = (int)blockIdx.x * kEpWaves + w, nt = (int)ntt;
+  const int T0 = __builtin_amdgcn_readfirstlane((int)ep_range_begin(kw, R, nt));
+  const int T1 = __builtin_amdgcn_readfirstlane((int)ep_range_begin(kw + 1, R, nt));
+  const bool active = T0 < T1;
   EpIdx ixa, ixb;
   EpGat cur;
+  // the rows around the range: whether its first tile begins inside a row (that row began in the
+  // previous range) and its last tile ends inside one (the row goes on in the next range)
+  bool open_foreign = false, end_cross = false;
+  int first_row = 0;
   if (active) {
     load_idx(T0, 0, ixa);
+    const uint32_t eb = (uint32_t)T0 * 32, ee = (uint32_t)T1 * 32;
+    const int before = eb > 0 ? a.erow[eb - 1] : -1;
+    const int last = ee < E ? a.erow[ee - 1] : -1, after = ee < E ? a.erow[ee] : -2;
     gather(ixa, cur);
+    first_row = __builtin_amdgcn_readfirstlane(ixa.ri);   // lane 0: the range's first edge
+    open_foreign = before == first_row;
+    end_cross = last == after;
     load_idx(T0, 1, ixa);
     complete(cur, ixa);
   }
   __syncthreads();   // weights in LDS
   if (!active) return;
-  for (int64_t T = T0; T < ntt; T += GW) {
-    const int64_t Tn = T + GW < ntt ? T + GW : T;
+  bool open = false;   // the last row of the previous tile goes on in this one
+  for (int T = T0; T < T1; ++T) {
+    const int Tn = T + 1 < T1 ? T + 1 : T;
     const int tabv = a.tile_tab[T * kTabInts + l];
     load_idx(Tn, 0, ixb);
-    half(std::integral_constant<int, 0>{}, T, cur, ixa, tabv);   // gathers (T, 1)
+    half(std::integral_constant<int, 0>{}, T, cur, ixa, tabv, Open{});   // gathers (T, 1)
     complete(cur, ixb);
+    // the tile's last row (lane 15 of its second half) and the next tile's first row (lane 0)
+    const int last_row = __builtin_amdgcn_readlane(ixa.ri, 15);
+    const int next_row = __builtin_amdgcn_readfirstlane(ixb.ri);
+    const int nrk = __builtin_amdgcn_readlane(tabv, kTabNrank);
+    Open op;
+    op.in = open;
+    op.out = T + 1 < T1 && next_row == last_row;
+    // rank 0's row began before this range: it opened the range (first tile, a row from the previous
+    // range) and has stayed open since
+    const bool foreign0 = T == T0 ? open_foreign : (open && open_foreign);
+    const bool closes = !(nrk == 1 && (op.out || (T + 1 == T1 && end_cross)));
+    op.stored = op.in && !foreign0 && closes;
+    op.row = first_row;
     load_idx(Tn, 1, ixa);
-    half(std::integral_constant<int, 1>{}, T, cur, ixb, tabv);   // gathers (Tn, 0)
+    half(std::integral_constant<int, 1>{}, T, cur, ixb, tabv, op);   // gathers (Tn, 0)
     complete(cur, ixa);
+    open = op.out;
+    open_foreign = nrk == 1 && foreign0;
+    first_row = next_row;
   }
 }
 
@@ -694,9 +760,14 @@ __global__ __launch_bounds__(512, 4) void mpnn_fwd_ep_kernel(FwdArgs a) {
 
 int mpnn_ep_blocks(int64_t E) { return (int)std::max<int64_t>(1, std::min<int64_t>((E + kEpTile - 1) / kEpTile, 256)); }
 
+int64_t mpnn_fwd_ep_waves(int64_t E) {   // a block per eight 32-edge tiles, up to two blocks per CU
+  return kEpWaves * std::max<int64_t>(1, std::min<int64_t>((E + 8 * 32 - 1) / (8 * 32), 2 * 256));
+}
+
 int launch_mpnn_fwd_ep(const FwdArgs& a, bool identity, hipStream_t st) {
-  if (a.E > 0) {   // eight 32-edge tiles per block at a time, two blocks per CU
-    const int nblk = (int)std::max<int64_t>(1, std::min<int64_t>((a.E + 8 * 32 - 1) / (8 * 32), 2 * 256));
+  if (a.E > 0) {   // one contiguous range of 32-edge tiles per wave
+    if (a.ranges != mpnn_fwd_ep_waves(a.E)) return (int)hipErrorInvalidValue;
+    const int nblk = (int)(a.ranges / kEpWaves);
     if (identity) {
       if (a.FE == 0)
         hipLaunchKernelGGL((mpnn_fwd_ep_kernel<0, true>), dim3(nblk), dim3(512), 0, st, a);

@@ -137,6 +137,41 @@ def test_mpnn_edge_parallel_cases(fe, skewed, eids):
     check_case(Case(rowptr, col, 128, fe, 128, 128, 128, seed=22 + fe, eq=False, edge_ids=perm), "bf16")
 
 
+@pytest.mark.parametrize("fe,ndeg", [(16, 14000), (0, 60000)])
+def test_mpnn_forward_tile_ranges(fe, ndeg):
+    """The edge-parallel MPNN forward gives each wave one contiguous range of 32-edge tiles: a row split over
+    tiles of one range is summed by its wave, the pieces of a row that crosses range boundaries are summed
+    by the fix-up.  With ~4,000 waves the 14,000-row graph has one tile per range, so every split row
+    crosses range boundaries (the degree-3,000 row ~95 of them), and the 60,000-row graph three to four
+    tiles per range, so rows also close inside their wave's range; next to short rows, empty rows and a
+    partial last tile.  Every row is checked against the oracle, and the whole output at the usual
+    tolerance."""
+    r = np.random.Generator(np.random.PCG64(401 + fe))
+    degs = r.integers(0, 20, size=ndeg)
+    degs[r.choice(ndeg, 8, replace=False)] = [3000, 1000, 700, 300, 129, 65, 64, 33]
+    degs[r.choice(ndeg, ndeg // 10, replace=False)] = 0
+    rowptr, col = random_csr(len(degs), degs, seed=403 + fe)
+    assert len(col) % 32 != 0
+    case = Case(rowptr, col, 128, fe, 128, 128, 128, seed=405 + fe, eq=False)
+    from pymolecular_amd import _capi
+    ntt = (case.E + 31) // 32
+    waves = 8 * max(1, min((case.E + 255) // 256, 512))
+    print(f"[mpnn-ranges] N={case.N} E={case.E} tiles={ntt} waves={waves} tiles/range={ntt / waves:.2f}", flush=True)
+    res = run_fused(case, "bf16", backward=False)
+    ref_msg, _ = case.forward_ref(True)
+    err = orc.normwise_rel_err(res["out_msg"], ref_msg)
+    deg = np.diff(case.rowptr)
+    num = np.abs(res["out_msg"] - ref_msg).max(axis=1)
+    den = np.abs(ref_msg).max(axis=1)
+    row_err = np.where(deg > 0, num / np.maximum(den, 1e-30), num)
+    worst = int(np.argmax(row_err))
+    print(f"[mpnn-ranges] out_msg err {err:.2e}, worst row {worst} (degree {deg[worst]}) {row_err[worst]:.2e}, "
+          f"empty rows max |out| {np.abs(res['out_msg'][deg == 0]).max():.1e}", flush=True)
+    assert err <= TOL["bf16"]
+    assert row_err.max() <= 3e-2, (worst, deg[worst], row_err[worst])
+    assert not np.any(res["out_msg"][deg == 0])
+
+
 @pytest.mark.parametrize("mean", [False, True])
 def test_egnn_h128_edge_features_24(mean):
     """The cooperative EGNN kernels (bf16, H = 128) at F_E = 24: the forward's edge-input chunk of 24 features
