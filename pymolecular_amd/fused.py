@@ -34,7 +34,8 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw handle of the device's current stream (the library's kernels are enqueued on it)."""
+    return torch._C._cuda_getCurrentRawStream(device.index if device.index is not None else torch.cuda.current_device())
 
 
 def _require_device(t: torch.Tensor, name: str) -> None:
@@ -193,22 +194,30 @@ def _dims(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg, linear=False) -
                     weight_layout=_capi.WEIGHTS_LINEAR if linear else _capi.WEIGHTS_PACKED)
 
 
+def _as(t: Optional[torch.Tensor], dt: torch.dtype) -> Optional[torch.Tensor]:
+    """``t`` in dtype ``dt`` with contiguous storage: ``t`` itself (no torch call) when it already is."""
+    if t is None:
+        return None
+    if t.dtype != dt:
+        t = t.to(dt)
+    return t if t.is_contiguous() else t.contiguous()
+
+
 def _prep_inputs(h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1, equivariant):
     _require_device(h, "h")
     dt = h.dtype
-    h = h.contiguous()
-    cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
-    w1, w2, w1m, b1, b2, bx1 = cv(w1), cv(w2), cv(w1m), cv(b1), cv(b2), cv(bx1)
+    h = h if h.is_contiguous() else h.contiguous()
+    w1, w2, w1m, b1, b2, bx1 = _as(w1, dt), _as(w2, dt), _as(w1m, dt), _as(b1, dt), _as(b2, dt), _as(bx1, dt)
     if w2m is not None:
-        w2m = w2m.reshape(-1).to(dt).contiguous()
+        w2m = _as(w2m.reshape(-1), dt)
     if edge_feat is not None:
-        edge_feat = edge_feat.to(dt).contiguous()
+        edge_feat = _as(edge_feat, dt)
         if edge_feat.shape[1] == 0:
             edge_feat = None
         elif edge_feat.shape[0] == 0:   # no edges: a fresh empty tensor has unit-stride rows of F_E
             edge_feat = torch.empty((0, edge_feat.shape[1]), dtype=dt, device=edge_feat.device)
     if equivariant:
-        coord = coord.to(torch.float32).contiguous()
+        coord = _as(coord, torch.float32)
     return h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1
 
 
@@ -235,12 +244,25 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     """
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
-    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
+    return _fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1,
+                          mean_agg=mean_agg, equivariant=equivariant, node_proj=node_proj,
+                          linear_weights=linear_weights, coord_residual=coord_residual,
+                          probe_identity=probe_identity, out_msg=out_msg)
+
+
+def _fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1, *,
+                   mean_agg, equivariant, node_proj=None, linear_weights=False, coord_residual=False,
+                   probe_identity=False, out_msg=None, dims=None, sched=None):
+    """:func:`egnn_fused_forward` on inputs :func:`_prep_inputs` returned; ``dims`` (without flags) and
+    ``sched`` when the caller has them."""
+    dims = (_dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights) if dims is None
+            else EgnnDims.from_buffer_copy(dims))
     if coord_residual and equivariant:
         dims.flags |= _capi.FLAG_COORD_RESIDUAL
     if probe_identity:
         dims.flags |= _capi.FLAG_PROBE_IDENTITY
-    sched = get_schedule(row_ptrs, col_indices, h.shape[0])
+    if sched is None:
+        sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev = h.device
     N, O = h.shape[0], dims.O
     if out_msg is None:
@@ -256,9 +278,9 @@ def egnn_fused_forward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1_
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     strides = EgnnStrides(h=h.stride(0), coord=coord.stride(0) if equivariant else 4,
                           edge=edge_feat.stride(0) if edge_feat is not None else 0, msg=out_msg.stride(0), mov=3)
-    eids = None if edge_ids is None else edge_ids.to(torch.int32).contiguous()
+    eids = _as(edge_ids, torch.int32)
     rc = L.egnn_fwd(dims, strides, _ptr(h), _ptr(coord) if equivariant else None, _ptr(edge_feat),
-                    _ptr(row_ptrs.contiguous()), _ptr(col_indices.contiguous()), _ptr(eids), _ptr(w1), _ptr(w2),
+                    _ptr(_as(row_ptrs, torch.int32)), _ptr(_as(col_indices, torch.int32)), _ptr(eids), _ptr(w1), _ptr(w2),
                     _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
                     _ptr(bx1) if equivariant else None, _ptr(out_msg), _ptr(out_mov), _ptr(node_proj),
                     sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
@@ -285,14 +307,30 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
     w2m_shape = None if w2_mov is None else tuple(w2_mov.shape)
     h, coord, edge_feat, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
         h, coord, edge_feat, w1_msg, w2_msg, w1_mov, w2_mov, b1, b2, bx1, equivariant)
-    dims = _dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights)
-    sched = get_schedule(row_ptrs, col_indices, h.shape[0])
+    g = _fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1,
+                        grad_out_msg, grad_out_mov, mean_agg=mean_agg, equivariant=equivariant, node_proj=node_proj,
+                        linear_weights=linear_weights, grad_h_into=grad_h_into, coord_residual=coord_residual,
+                        probe_identity=probe_identity)
+    if g["w2_mov"] is not None and w2m_shape is not None:
+        g["w2_mov"] = g["w2_mov"].reshape(w2m_shape)
+    return g
+
+
+def _fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1, w2, w1m, w2m, b1, b2, bx1,
+                    grad_out_msg, grad_out_mov, *, mean_agg, equivariant, node_proj=None, linear_weights=False,
+                    grad_h_into=None, coord_residual=False, probe_identity=False, dims=None, sched=None):
+    """:func:`egnn_fused_backward` on inputs :func:`_prep_inputs` returned (w2_mov's gradient flat);
+    ``dims`` (without flags) and ``sched`` when the caller has them."""
+    dims = (_dims(h, edge_feat, col_indices, w1, w2, w1m, equivariant, mean_agg, linear_weights) if dims is None
+            else EgnnDims.from_buffer_copy(dims))
+    if sched is None:
+        sched = get_schedule(row_ptrs, col_indices, h.shape[0])
     dev, dt = h.device, h.dtype
     N = h.shape[0]
     gm = grad_out_msg.to(dt)
     if gm.stride(1) != 1 or (gm.stride(0) * gm.element_size()) % 16 or gm.data_ptr() % 16:
         gm = gm.contiguous()   # the kernels read 8- and 16-byte pieces of unit-stride rows
-    gx = grad_out_mov.to(torch.float32).contiguous() if equivariant else None
+    gx = _as(grad_out_mov, torch.float32) if equivariant else None
     if grad_h_into is not None:
         gh = grad_h_into
         if (gh.dtype != dt or tuple(gh.shape) != tuple(h.shape) or gh.stride(1) != 1
@@ -323,23 +361,22 @@ def egnn_fused_backward(h, coord, edge_feat, row_ptrs, col_indices, edge_ids, w1
                           msg=gm.stride(0), mov=gx.stride(0) if equivariant else 3, grad_h=grad_h.stride(0))
     if equivariant and coord.stride(0) != 3:
         coord = coord[:, :3].contiguous()
-    eids = None if edge_ids is None else edge_ids.to(torch.int32).contiguous()
+    eids = _as(edge_ids, torch.int32)
     rc = L.egnn_bwd(dims, strides, _ptr(h), _ptr(coord) if equivariant else None, _ptr(edge_feat),
-                    _ptr(row_ptrs.contiguous()), _ptr(col_indices.contiguous()), _ptr(eids), _ptr(w1), _ptr(w2),
+                    _ptr(_as(row_ptrs, torch.int32)), _ptr(_as(col_indices, torch.int32)), _ptr(eids), _ptr(w1), _ptr(w2),
                     _ptr(w1m) if equivariant else None, _ptr(w2m) if equivariant else None, _ptr(b1), _ptr(b2),
                     _ptr(bx1) if equivariant else None, _ptr(gm), _ptr(gx), _ptr(grad_h), _ptr(grad_coord),
                     _ptr(g_w1), _ptr(g_w2), _ptr(g_w1m), _ptr(g_w2m), _ptr(g_b1), _ptr(g_b2), _ptr(g_bx1),
                     _ptr(node_proj), sched.buf.data_ptr(), ws.data_ptr(), ws_bytes, _stream(dev))
     check("egnn_bwd", rc)
-    if g_w2m is not None and w2m_shape is not None:
-        g_w2m = g_w2m.reshape(w2m_shape)
     return dict(h=grad_h, coord=grad_coord, w1_msg=g_w1, w2_msg=g_w2, w1_mov=g_w1m, w2_mov=g_w2m, b1=g_b1,
                 b2=g_b2, bx1=g_bx1)
 
 
-def _node_proj_buffer(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg, linear=False):
-    ef = None if (edge_feat is None or edge_feat.shape[1] == 0) else edge_feat
-    dims = _dims(h, ef, col, w1, w2, w1m, equivariant, mean_agg, linear)
+def _node_proj_buffer(h, edge_feat, col, w1, w2, w1m, equivariant, mean_agg, linear=False, dims=None):
+    if dims is None:
+        ef = None if (edge_feat is None or edge_feat.shape[1] == 0) else edge_feat
+        dims = _dims(h, ef, col, w1, w2, w1m, equivariant, mean_agg, linear)
     n = _capi.lib().egnn_node_proj_bytes(dims)
     return torch.empty(max(n, 16), dtype=torch.uint8, device=h.device)
 

@@ -20,7 +20,7 @@ from __future__ import annotations
 
 import torch
 
-from .fused import _node_proj_buffer, _prep_inputs, egnn_fused_backward, egnn_fused_forward
+from .fused import _dims, _fused_backward, _fused_forward, _node_proj_buffer, _prep_inputs, get_schedule
 from .node_update import node_update_backward, node_update_forward
 
 __all__ = ["GCLLayerFn"]
@@ -40,13 +40,17 @@ class GCLLayerFn(torch.autograd.Function):
         ctx.shapes = [None if t is None else tuple(t.shape) for t in (e0w, e2w, c0w, c2w, e0b, e2b, c0b)]
         hp, coord_p, ef, w1, w2, w1m, w2m, b1, b2, bx1 = _prep_inputs(
             h, coord, edge_attr, e0w, e2w, c0w, c2w, e0b, e2b, c0b, equivariant)
-        pq = _node_proj_buffer(hp, ef, col, w1, w2, w1m, equivariant, mean_agg, True)
-        agg, x_new = egnn_fused_forward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1,
-                                        mean_agg=mean_agg, equivariant=equivariant, node_proj=pq,
-                                        linear_weights=True, coord_residual=True)
+        # the layer's dimensions and the graph's schedule, once for the forward and the backward
+        dims = _dims(hp, ef, col, w1, w2, w1m, equivariant, mean_agg, True)
+        sched = get_schedule(row_ptrs, col, hp.shape[0])
+        pq = _node_proj_buffer(hp, ef, col, w1, w2, w1m, equivariant, mean_agg, True, dims=dims)
+        agg, x_new = _fused_forward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1,
+                                    mean_agg=mean_agg, equivariant=equivariant, node_proj=pq, linear_weights=True,
+                                    coord_residual=True, dims=dims, sched=sched)
         out, (nt, res, has_b, wdt) = node_update_forward(hp, agg, n0w, n0b, n2w, n2b, residual)
         ctx.save_for_backward(hp, coord_p, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1, pq, *nt)
         ctx.node = (res, has_b, wdt)
+        ctx.dims, ctx.sched = dims, sched
         ctx.mean_agg, ctx.equivariant = mean_agg, equivariant
         ctx.coord_dtype = None if coord is None else coord.dtype
         if not equivariant:
@@ -68,10 +72,10 @@ class GCLLayerFn(torch.autograd.Function):
         g_h, g_agg = grad_x[:, :K1], grad_x[:, K1:]
         if eq and g_coord is None:
             g_coord = torch.zeros((N, 3), dtype=torch.float32, device=hp.device)
-        g = egnn_fused_backward(hp, coord, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1, g_agg,
-                                g_coord.to(torch.float32) if eq else None, mean_agg=ctx.mean_agg,
-                                equivariant=eq, node_proj=pq, linear_weights=True, grad_h_into=g_h,
-                                coord_residual=True)
+        g = _fused_backward(hp, coord, ef, row_ptrs, col, perm, w1, w2, w1m, w2m, b1, b2, bx1, g_agg,
+                            g_coord if eq else None, mean_agg=ctx.mean_agg, equivariant=eq, node_proj=pq,
+                            linear_weights=True, grad_h_into=g_h, coord_residual=True, dims=ctx.dims,
+                            sched=ctx.sched)
         gc = g["coord"].to(ctx.coord_dtype) if eq else None   # includes g_coord (EGNN_FLAG_COORD_RESIDUAL)
         wg = [g[k] for k in ("w1_msg", "w2_msg", "w1_mov", "w2_mov", "b1", "b2", "bx1")]
         e0w_g, e2w_g, c0w_g, c2w_g, e0b_g, e2b_g, c0b_g = [

@@ -17,6 +17,7 @@ import torch
 
 from . import _capi
 from ._capi import EgnnNodeDims, check
+from .fused import _as, _stream
 
 __all__ = ["NodeUpdateFn", "node_update", "node_update_forward", "node_update_backward", "DenseFn", "dense"]
 
@@ -60,16 +61,15 @@ def node_update_forward(x1, x2, w1, b1, w2, b2, residual=True):
         raise RuntimeError("x1 must be a ROCm device tensor: the node update has no CPU path")
     dt = x1.dtype
     x1 = _rowmajor(x1)
-    x2 = None if x2 is None else _rowmajor(x2.to(dt))
-    cv = lambda t: None if t is None else t.to(dt).contiguous()  # noqa: E731
-    w1c, b1c, w2c, b2c = cv(w1), cv(b1), cv(w2), cv(b2)
+    x2 = None if x2 is None else _rowmajor(x2 if x2.dtype == dt else x2.to(dt))
+    w1c, b1c, w2c, b2c = _as(w1, dt), _as(b1, dt), _as(w2, dt), _as(b2, dt)
     d = _dims(x1, x2, w1c, w2c, residual)
     N = x1.shape[0]
     pre = torch.empty((N, d.Hn), dtype=dt, device=x1.device)
     act = torch.empty_like(pre)
     out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
     L = _capi.lib()
-    st = torch.cuda.current_stream(x1.device).cuda_stream
+    st = _stream(x1.device)
     rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
                          w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), act.data_ptr(),
                          out.data_ptr(), out.stride(0), st)
@@ -83,7 +83,7 @@ def node_update_backward(tensors, residual, has_b, wdt, gout):
     gradient of ``[x1 | x2]`` (a fresh buffer the caller may add into)."""
     x1, x2, w1, w2, pre, act = tensors
     dt = x1.dtype
-    gout = _rowmajor(gout.to(dt))
+    gout = _rowmajor(gout if gout.dtype == dt else gout.to(dt))
     d = _dims(x1, x2, w1, w2, residual)
     N = x1.shape[0]
     dev = x1.device
@@ -94,15 +94,14 @@ def node_update_backward(tensors, residual, has_b, wdt, gout):
     L = _capi.lib()
     nbytes = L.egnn_node_bwd_workspace_bytes(d)
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
-    st = torch.cuda.current_stream(dev).cuda_stream
+    st = _stream(dev)
     rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
                          w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), act.data_ptr(), gout.data_ptr(),
                          gout.stride(0), grad_x.data_ptr(), gw1.data_ptr(), _ptr(gb1), gw2.data_ptr(),
                          _ptr(gb2), ws.data_ptr(), nbytes, st)
     check("egnn_node_bwd", rc)
     w1dt, b1dt, w2dt, b2dt = wdt
-    return (grad_x, gw1.to(w1dt), None if gb1 is None else gb1.to(b1dt), gw2.to(w2dt),
-            None if gb2 is None else gb2.to(b2dt))
+    return grad_x, _as(gw1, w1dt), _as(gb1, b1dt), _as(gw2, w2dt), _as(gb2, b2dt)
 
 
 class NodeUpdateFn(torch.autograd.Function):
@@ -162,13 +161,13 @@ class DenseFn(torch.autograd.Function):
         Nout, Kin = weight.shape
         lead = x.shape[:-1]
         xp = _rowmajor(_pad_to8(x.reshape(-1, Kin), 1))
-        wp = _pad_to8(_pad_to8(weight.to(dt), 1), 0).contiguous()
-        bp = None if bias is None else _pad_to8(bias.to(dt), 0).contiguous()
+        wp = _as(_pad_to8(_pad_to8(_as(weight, dt), 1), 0), dt)
+        bp = None if bias is None else _as(_pad_to8(_as(bias, dt), 0), dt)
         N, Kp = xp.shape
         Np = wp.shape[0]
         y = torch.empty((N, Np), dtype=dt, device=x.device)
         code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
-        st = torch.cuda.current_stream(x.device).cuda_stream
+        st = _stream(x.device)
         rc = _capi.lib().egnn_dense_fwd(code, N, Kp, Np, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
                                         wp.data_ptr(), _ptr(bp), y.data_ptr() if N else None, Np, st)
         check("egnn_dense_fwd", rc)
@@ -185,11 +184,11 @@ class DenseFn(torch.autograd.Function):
         dt = xp.dtype
         N, Kp = xp.shape
         Np = wp.shape[0]
-        gy2 = _rowmajor(_pad_to8(gy.to(dt).reshape(-1, Nout), 1))
+        gy2 = _rowmajor(_pad_to8((gy if gy.dtype == dt else gy.to(dt)).reshape(-1, Nout), 1))
         gx = None
         L = _capi.lib()
         code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
-        st = torch.cuda.current_stream(xp.device).cuda_stream
+        st = _stream(xp.device)
         if ctx.needs_input_grad[0]:   # gx = gy w, the same product as the forward with w^T as the weight
             gx = torch.empty((N, Kp), dtype=dt, device=xp.device)
             if N:
@@ -205,8 +204,9 @@ class DenseFn(torch.autograd.Function):
                                 gy2.data_ptr() if N else None, gy2.stride(0) if N else Np, gw.data_ptr(), _ptr(gb),
                                 ws.data_ptr(), nbytes, st)
         check("egnn_dense_wgrad", rc)
-        gw = gw[:Nout, :Kin].to(ctx.wdt[0])
-        return gx, gw, None if gb is None else gb[:Nout].to(ctx.wdt[1])
+        gw = gw if (Np, Kp) == (Nout, Kin) else gw[:Nout, :Kin]
+        to = lambda t, d: t if t.dtype == d else t.to(d)  # noqa: E731
+        return gx, to(gw, ctx.wdt[0]), None if gb is None else to(gb[:Nout], ctx.wdt[1])
 
 
 def dense(x: torch.Tensor, lin: torch.nn.Linear) -> torch.Tensor:
