@@ -280,10 +280,13 @@ def run_workload(k, dtype, a, g=None):
         model.zero_grad(set_to_none=True)
         loss().backward()
 
-    # The library's event hook records the fused edge kernels (the roofline's kernels) through the
-    # warm-up and the timed steps, on the stream each kernel runs on; the warm-up fills its event pool so
-    # the timed steps create none.  Every kernel class is timed in a separate untimed pass afterwards.
-    edge_classes = [_capi.K_FWD_EDGE, _capi.K_BWD_EDGE, _capi.K_EDGE_WGRAD]
+    # The library's event hook records the roofline's kernels (the fused backward edge kernel and the
+    # factor products it hands weight-gradient work to) through the warm-up and the timed steps, on the
+    # stream each kernel runs on; the warm-up fills its event pool so the timed steps create none.  Each
+    # recorded event waits for the work before it, so the timed steps record only these classes (at
+    # molecules-1024 recording the forward edge kernels as well cost ~20 us of a ~1.85 ms step).  Every
+    # kernel class is timed in a separate untimed pass afterwards.
+    edge_classes = [_capi.K_BWD_EDGE, _capi.K_EDGE_WGRAD]
     _capi.profile_enable(True, edge_classes)
     for _ in range(a.warmup):
         step()
@@ -305,7 +308,7 @@ def run_workload(k, dtype, a, g=None):
     torch.cuda.synchronize()
     prof = _capi.profile_read()
     _capi.profile_enable(False)
-    for cls in ("fwd_edge", "bwd_edge", "edge_wgrad"):   # the roofline's kernels: the timed steps' own records
+    for cls in ("bwd_edge", "edge_wgrad"):   # the roofline's kernels: the timed steps' own records
         prof[cls] = (timed[cls][0] * nprof / a.steps, timed[cls][1] * nprof / a.steps)
 
     s = 2 if dt == torch.bfloat16 else 4
