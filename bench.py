@@ -398,7 +398,10 @@ def probe_identity(a, k=5):
                                                         message gradient; dL/dpre1 out, its row sums: dP
                                                         rows and fp32 carries of the split rows)
       node reduce:  E (H s + 4) + N (8 + H s)           (dL/dpre1 by source, CSC ids; dQ out)
-      fix-ups:      E H / 4 each                        (the carries of the split rows, forward and backward)"""
+      fix-ups:      E H / 4 per step                    (the fp32 carries of the backward's split rows)
+    The two fix-up launches of a step are timed together: the backward's completes every row split over
+    tiles, the forward's only the rows that cross a wave's range of tiles (a few thousand rows, whose bytes
+    are left out of the count, so its rate is understated)."""
     import torch
     from pymolecular_amd import _capi, fused, graphs
     g = graphs.make_workload(k)
@@ -435,9 +438,15 @@ def probe_identity(a, k=5):
     tot_b = tot_t = 0.0
     for cls, nbytes in model.items():
         t, n = prof[cls]
-        ms = t / max(n, 1)
+        if cls == "fwd_fixup":   # both launches of a step (forward and backward), per step
+            ms = t / max(a.steps, 1)
+            key = "ms_per_step"
+        else:
+            ms = t / max(n, 1)
+            key = "ms_per_launch"
         gbs = nbytes / (ms / 1e3) / 1e9
-        out[cls] = dict(ms_per_launch=ms, algorithmic_bytes=nbytes, achieved_gbs=gbs, frac=gbs / PEAK["hbm_gbs"])
+        out[cls] = {key: ms, "launches": n, "algorithmic_bytes": nbytes, "achieved_gbs": gbs,
+                    "frac": gbs / PEAK["hbm_gbs"]}
         tot_b += nbytes
         tot_t += ms
     gbs = tot_b / (tot_t / 1e3) / 1e9
