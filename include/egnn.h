@@ -214,16 +214,27 @@ typedef struct EgnnNodeDims {
 /* Workspace bytes for egnn_node_bwd. */
 size_t egnn_node_bwd_workspace_bytes(const EgnnNodeDims* dims);
 
+/* 1 if egnn_node_fwd / egnn_node_bwd need the activation buffer `act` for these
+ * dims, 0 if it may be NULL (bf16, K1 = Hn = Fo = 128, K2 in {0, 128}, N >= 65536:
+ * the backward then reads SiLU of the saved `pre` on load, the same bf16 values
+ * the forward would have stored), minus an EGNN_ERR_* code for invalid dims.
+ * No counterpart in the reference, which keeps every activation of its
+ * torch node_mlp for autograd (egnn_clean.py:60-70). */
+int32_t egnn_node_act_required(const EgnnNodeDims* dims);
+
 /* Forward.  Writes out (N, Fo, row stride ldo) and the pre-activation `pre`
- * and activation `act` (both (N, Hn) contiguous) that egnn_node_bwd reads. */
+ * and activation `act` (both (N, Hn) contiguous) that egnn_node_bwd reads;
+ * `act` may be NULL when egnn_node_act_required(dims) is 0 (not written). */
 int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
                       const void* w1, const void* b1, const void* w2, const void* b2,
                       void* pre, void* act, void* out, int64_t ldo, void* stream);
 
 /* Backward.  Writes grad_x (N, K1 + K2) contiguous: columns [0, K1) are dL/dx1
  * (including the residual term), [K1, K1 + K2) dL/dx2; grad_w1 (Hn, K1 + K2),
- * grad_w2 (Fo, Hn), and grad_b1 / grad_b2 when non-NULL.  Weight gradients are
- * split-K partial products summed in a fixed order (deterministic). */
+ * grad_w2 (Fo, Hn), and grad_b1 / grad_b2 when non-NULL.  `act` may be NULL
+ * when egnn_node_act_required(dims) is 0; the results are the same either way.
+ * Weight gradients are split-K partial products summed in a fixed order
+ * (deterministic). */
 int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, const void* x2, int64_t ld2,
                       const void* w1, const void* w2, const void* pre, const void* act,
                       const void* grad_out, int64_t ldgo, void* grad_x,

@@ -12,6 +12,8 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().with_name("libpymolecular_egnn.so")
 
 EGNN_OK = 0
+EGNN_ERR_NULL = 1
+EGNN_ERR_DIMS = 2
 EGNN_ERR_SCRATCH = 8
 FWD_STATIC_SCRATCH_BYTES = 128 << 20   # include/egnn.h EGNN_FWD_STATIC_SCRATCH_BYTES
 EGNN_F32 = 0
@@ -22,7 +24,7 @@ EXPORTED = (
     "egnn_abi_version", "egnn_status_string", "egnn_schedule_bytes", "egnn_schedule_tmp_bytes",
     "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_node_proj_bytes",
     "egnn_fwd", "egnn_fwd_static", "egnn_bwd",
-    "egnn_node_bwd_workspace_bytes", "egnn_node_fwd", "egnn_node_bwd",
+    "egnn_node_bwd_workspace_bytes", "egnn_node_act_required", "egnn_node_fwd", "egnn_node_bwd",
     "egnn_dense_fwd", "egnn_dense_wgrad_workspace_bytes", "egnn_dense_wgrad",
     "egnn_profile_enable", "egnn_profile_read",
     "egnn_graph_tmp_bytes", "egnn_knn_graph", "egnn_radius_graph",
@@ -59,7 +61,7 @@ class EgnnNodeDims(ctypes.Structure):
 
 _lib = None
 
-ABI_VERSION = 8   # include/egnn.h egnn_abi_version()
+ABI_VERSION = 9   # include/egnn.h egnn_abi_version()
 
 
 def _check_stamp() -> None:
@@ -125,6 +127,8 @@ def lib() -> ctypes.CDLL:
     ND = ctypes.POINTER(EgnnNodeDims)
     L.egnn_node_bwd_workspace_bytes.restype = c_size_t
     L.egnn_node_bwd_workspace_bytes.argtypes = [ND]
+    L.egnn_node_act_required.restype = c_int32
+    L.egnn_node_act_required.argtypes = [ND]
     L.egnn_node_fwd.restype = c_int32
     L.egnn_node_fwd.argtypes = [ND, P, c_int64, P, c_int64, P, P, P, P, P, P, P, c_int64, P]
     L.egnn_node_bwd.restype = c_int32

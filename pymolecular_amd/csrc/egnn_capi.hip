@@ -11,7 +11,7 @@ using namespace egnn;
 
 namespace {
 
-constexpr int32_t kAbiVersion = 8;
+constexpr int32_t kAbiVersion = 9;
 
 bool aligned16(const void* p) { return p == nullptr || ((uintptr_t)p & 15u) == 0; }
 
@@ -502,9 +502,19 @@ size_t node_ws_layout(const NodeShape& s, void* base, NodeWs* w) {
   return off;
 }
 
+// the activation buffer is needed unless both passes stream the rows: then the backward's [act | 1]^T dout
+// reads SiLU of the stored pre-activation on load, which is the forward's act value for value
+bool node_act_required(const NodeShape& s) { return !stream_node_ok(s.N, s.K1, s.K2, s.Hn, s.Fo, s.bf16, false); }
+
 }  // namespace
 
 extern "C" {
+
+int32_t egnn_node_act_required(const EgnnNodeDims* dims) {
+  NodeShape s;
+  const int32_t rc = node_shape(dims, &s);
+  return rc != EGNN_OK ? -rc : node_act_required(s) ? 1 : 0;
+}
 
 size_t egnn_node_bwd_workspace_bytes(const EgnnNodeDims* dims) {
   NodeShape s;
@@ -520,7 +530,7 @@ int32_t egnn_node_fwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   int32_t rc = node_shape(dims, &s);
   if (rc != EGNN_OK) return rc;
   if (s.N == 0) return EGNN_OK;
-  if (!x1 || (s.K2 > 0 && !x2) || !w1 || !w2 || !pre || !act || !out) return EGNN_ERR_NULL;
+  if (!x1 || (s.K2 > 0 && !x2) || !w1 || !w2 || !pre || (!act && node_act_required(s)) || !out) return EGNN_ERR_NULL;
   if (!ld_ok(ld1, s.K1, s.esz) || (s.K2 > 0 && !ld_ok(ld2, s.K2, s.esz)) || !ld_ok(ldo, s.Fo, s.esz))
     return EGNN_ERR_STRIDE;
   for (const void* p : std::initializer_list<const void*>{x1, x2, w1, w2, pre, act, out})
@@ -568,7 +578,8 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   int32_t rc = node_shape(dims, &s);
   if (rc != EGNN_OK) return rc;
   if (!w1 || !w2 || !grad_w1 || !grad_w2 || !workspace) return EGNN_ERR_NULL;
-  if (s.N > 0 && (!x1 || (s.K2 > 0 && !x2) || !pre || !act || !grad_out || !grad_x)) return EGNN_ERR_NULL;
+  if (s.N > 0 && (!x1 || (s.K2 > 0 && !x2) || !pre || (!act && node_act_required(s)) || !grad_out || !grad_x))
+    return EGNN_ERR_NULL;
   if (s.N > 0 && (!ld_ok(ld1, s.K1, s.esz) || (s.K2 > 0 && !ld_ok(ld2, s.K2, s.esz)) || !ld_ok(ldgo, s.Fo, s.esz)))
     return EGNN_ERR_STRIDE;
   for (const void* p : std::initializer_list<const void*>{x1, x2, w1, w2, pre, act, grad_out, grad_x, workspace})
@@ -601,7 +612,8 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
   s1.ksplit = splitk_len(s1.M, s1.N, s1.K, s.bf16); s1.partial = w.part1;
   Gemm2Args s2{};
   s2.M = s.Hn + 1; s2.N = s.Fo; s2.K = s.N;
-  s2.A = act; s2.lda = s.Hn; s2.a_bf16 = s.bf16; s2.a_kc = 0; s2.a_ones_row = s.Hn;
+  s2.A = act ? act : pre; s2.lda = s.Hn; s2.a_bf16 = s.bf16; s2.a_kc = 0; s2.a_ones_row = s.Hn;
+  s2.a_silu = act ? 0 : 1;   // no act: SiLU of pre on load (the streaming passes only)
   s2.B = grad_out; s2.ldb = ldgo; s2.b_bf16 = s.bf16; s2.b_nc = 1;
   s2.ksplit = splitk_len(s2.M, s2.N, s2.K, s.bf16); s2.partial = w.part2;
   const int64_t nsplit1 = cdiv(std::max<int64_t>(s.N, 1), s1.ksplit), nsplit2 = cdiv(std::max<int64_t>(s.N, 1), s2.ksplit);

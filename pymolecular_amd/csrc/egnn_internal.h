@@ -153,7 +153,8 @@ int launch_prep(const LayerShape& s, const void* w1, const void* w2, const void*
 // k >= a_split come from A2 (column k - a_split); with an m-contiguous A, rows
 // m >= a_split do.  a_split is a multiple of 8.  Epilogue, in this order:
 // + bias[n]; * SiLU'(zd[m][n]); store the value to Cpre and apply SiLU (act);
-// + resid[m][n] for n < resid_len.  Cpre, resid and zd share C's dtype.
+// + resid[m][n] for n < resid_len.  Cpre, resid and zd share C's dtype.  With a_silu, every element of A
+// but the ones row reads as SiLU of its bf16 value, rounded to bf16 (bf16 tile kernels only).
 struct Gemm2Args {
   int64_t M, N, K;
   const void* A; int64_t lda; int a_bf16; int a_kc; int64_t a_ones_row;
@@ -166,6 +167,7 @@ struct Gemm2Args {
   const void* resid; int64_t ldr; int64_t resid_len;
   const void* zd; int64_t ldz;
   const int32_t* b_kidx;   // n-contiguous B only: row k of B is row b_kidx[k] of the array
+  int a_silu;
 };
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st);
 // Streaming node products (egnn_stream.hip): bf16, A k-contiguous with M >= kStreamMinRows rows,
@@ -182,7 +184,7 @@ struct NodeMlpArgs {
   int64_t N; int K2; int residual;
   const void* x1; int64_t ld1; const void* x2; int64_t ld2;
   const void* w1; const void* b1; const void* w2; const void* b2;
-  void* pre; void* act; void* out; int64_t ldo;          // forward outputs (pre, act: N x Hn)
+  void* pre; void* act; void* out; int64_t ldo;          // forward outputs (pre, act: N x Hn; act may be null)
   const void* gout; int64_t ldgo; void* dz; void* gx;    // backward (reads pre; dz: N x Hn, gx: N x K)
 };
 constexpr int64_t kNodeFuseFwdMinRows = 1024;

@@ -666,6 +666,11 @@ __device__ __forceinline__ void gemm_bf16_tile(const Gemm2Args& g, int bx, int b
 #pragma unroll
     for (int i = 0; i < NLA; ++i) {
       const int idx = tid + 256 * i;
+      if (g.a_silu) {   // here, not at the load, so that the loads stay in flight over the slice's products
+        const int64_t m = A_KC ? m0 + idx / (BK / 8) : m0 + 8 * (idx % (BM / 8));
+        for (int u = 0; u < 8; ++u)   // SiLU(0) = 0 keeps the padding; the ones row stays ones
+          if ((A_KC ? m : m + u) != g.a_ones_row) ra[i][u] = (bf16)silu_t<bf16>((float)ra[i][u]);
+      }
       if constexpr (A_KC) *reinterpret_cast<bf16x8*>(&At[(idx / (BK / 8)) * PK + 8 * (idx % (BK / 8))]) = ra[i];
       else *reinterpret_cast<bf16x8*>(&At[(idx / (BM / 8)) * PA + 8 * (idx % (BM / 8))]) = ra[i];
     }
@@ -1249,7 +1254,7 @@ bool bf16_big_tiles(const Gemm2Args& g) {
 // the edge-sized split-K products that gemm_atb256_kernel takes: A[k][m], B[k][n] with 256 columns
 // each, 16-byte aligned rows, optionally the ones row 256 (sized for one split per CU by splitk_len)
 bool atb256_ok(const Gemm2Args& g) {
-  return g.ksplit > 0 && g.K >= kSplitKBig && g.partial && !g.a_kc && g.b_nc && !g.A2 && !g.b_kidx &&
+  return g.ksplit > 0 && g.K >= kSplitKBig && g.partial && !g.a_kc && g.b_nc && !g.A2 && !g.b_kidx && !g.a_silu &&
          g.N == 256 && (g.M == 256 || (g.M == 257 && g.a_ones_row == 256)) && g.lda >= 256 && g.ldb >= 256;
 }
 unsigned splits_of(const Gemm2Args& g) {
@@ -1285,6 +1290,7 @@ int launch_gemm2_pair(const Gemm2Args& g1, const Gemm2Args& g2, bool compute_bf1
 
 int launch_gemm2(const Gemm2Args& g, bool compute_bf16, hipStream_t st) {
   if (g.M <= 0 || g.N <= 0) return 0;
+  if (g.a_silu && !bf16_tiled_ok(g, compute_bf16)) return (int)hipErrorInvalidValue;   // bf16 tiles only
   if (stream_gemm_ok(g, compute_bf16)) return launch_stream_gemm(g, st);
   const unsigned gz = splits_of(g);
   const dim3 grid((unsigned)cdiv(g.M, 64), (unsigned)cdiv(g.N, 64), gz);

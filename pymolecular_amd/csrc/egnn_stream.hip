@@ -228,6 +228,7 @@ __device__ __forceinline__ int stream_wl(int c, int gq) {
 constexpr int kNodeHn = 128, kNodeK1 = 128, kNodeWaves = 8;
 
 // forward: pre = [x1 | x2] W1^T + b1, act = SiLU(pre) (of pre's bf16 value), out = act W2^T + b2 (+ x1);
+// act is stored only when a.act is set (a product that reads SiLU of pre on load recomputes it exactly);
 // one 16-row tile per wave and step, the next tile's rows in flight
 template <int K, bool RES>
 __global__ __launch_bounds__(64 * kNodeWaves, 1) void stream_node_fwd_kernel(NodeMlpArgs a) {
@@ -286,7 +287,7 @@ __global__ __launch_bounds__(64 * kNodeWaves, 1) void stream_node_fwd_kernel(Nod
       if (live) {
         const int64_t o = m * HN + 32 * q + 8 * gq;
         *reinterpret_cast<bf16x8*>((bf16*)a.pre + o) = p;
-        *reinterpret_cast<bf16x8*>((bf16*)a.act + o) = h[q];
+        if (a.act) *reinterpret_cast<bf16x8*>((bf16*)a.act + o) = h[q];
       }
     }
 
@@ -419,7 +420,8 @@ bool stream_gemm_ok(const Gemm2Args& g, bool compute_bf16) {
   const bool shape = (g.K == 128 || g.K == 256) && (g.N == 128 || g.N == 256) && g.K * g.N <= 32768;
   const bool perm = g.perm_half == 0 || g.perm_half % 32 == 0;
   const bool res_and_zd = g.resid != nullptr && g.resid_len > 0 && g.zd != nullptr;   // not instantiated at N = 256
-  return compute_bf16 && !(res_and_zd && g.N == 256) && g.a_bf16 && g.b_bf16 && g.c_bf16 && !g.partial && g.ksplit <= 0 && g.a_kc &&
+  return compute_bf16 && !g.a_silu && !(res_and_zd && g.N == 256) && g.a_bf16 && g.b_bf16 && g.c_bf16 && !g.partial &&
+         g.ksplit <= 0 && g.a_kc &&
          g.a_ones_row < 0 && !g.b_kidx && g.M >= kStreamMinRows && shape && perm &&
          (g.A2 == nullptr || (g.a_split % 32 == 0 && g.a_split > 0 && g.a_split < g.K)) &&
          (g.bias == nullptr || g.bias_len >= 0) && (g.resid == nullptr || g.resid_len % 8 == 0) &&

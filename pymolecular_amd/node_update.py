@@ -66,12 +66,13 @@ def node_update_forward(x1, x2, w1, b1, w2, b2, residual=True):
     d = _dims(x1, x2, w1c, w2c, residual)
     N = x1.shape[0]
     pre = torch.empty((N, d.Hn), dtype=dt, device=x1.device)
-    act = torch.empty_like(pre)
-    out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
     L = _capi.lib()
+    # the streaming passes recompute act from pre in the backward's weight-gradient product
+    act = torch.empty_like(pre) if L.egnn_node_act_required(d) else None
+    out = torch.empty((N, d.Fo), dtype=dt, device=x1.device)
     st = _stream(x1.device)
     rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
-                         w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), act.data_ptr(),
+                         w1c.data_ptr(), _ptr(b1c), w2c.data_ptr(), _ptr(b2c), pre.data_ptr(), _ptr(act),
                          out.data_ptr(), out.stride(0), st)
     check("egnn_node_fwd", rc)
     wdt = (w1.dtype, None if b1 is None else b1.dtype, w2.dtype, None if b2 is None else b2.dtype)
@@ -96,7 +97,7 @@ def node_update_backward(tensors, residual, has_b, wdt, gout):
     ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     st = _stream(dev)
     rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), _ptr(x2), 0 if x2 is None else x2.stride(0),
-                         w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), act.data_ptr(), gout.data_ptr(),
+                         w1.data_ptr(), w2.data_ptr(), pre.data_ptr(), _ptr(act), gout.data_ptr(),
                          gout.stride(0), grad_x.data_ptr(), gw1.data_ptr(), _ptr(gb1), gw2.data_ptr(),
                          _ptr(gb2), ws.data_ptr(), nbytes, st)
     check("egnn_node_bwd", rc)
@@ -108,8 +109,9 @@ class NodeUpdateFn(torch.autograd.Function):
     """``out = NodeUpdateFn.apply(x1, x2, w1, b1, w2, b2, residual)``.
 
     ``w1`` (Hn, K1 + K2) and ``w2`` (Fo, Hn) in torch.nn.Linear layout; ``b1``
-    and ``b2`` may be None.  Saves the pre-activation and the activation
-    (N x Hn each) for the backward.
+    and ``b2`` may be None.  Saves the pre-activation and, where the library
+    needs it (``egnn_node_act_required``), the activation (N x Hn each) for the
+    backward.
     """
 
     @staticmethod

@@ -59,6 +59,21 @@ def test_bad_arguments_return_status_not_crash():
     assert L.egnn_schedule_build(1, 1, 0, 20, 1, 0, 1, 0, None) == 2
 
 
+def test_node_activation_buffer_requirement():
+    # act may be NULL exactly where both node-update passes stream the rows: bf16, K1 = Hn = Fo = 128,
+    # K2 in {0, 128}, at least 65,536 rows; invalid dims return minus their status code
+    L = _capi.lib()
+    nd = lambda **kw: _capi.EgnnNodeDims(**{**dict(N=65536, K1=128, K2=128, Hn=128, Fo=128, residual=1,  # noqa: E731
+                                                    dtype=_capi.EGNN_BF16), **kw})
+    assert L.egnn_node_act_required(nd()) == 0
+    assert L.egnn_node_act_required(nd(K2=0, residual=0, N=1 << 21)) == 0
+    assert L.egnn_node_act_required(nd(N=65535)) == 1
+    assert L.egnn_node_act_required(nd(dtype=_capi.EGNN_F32)) == 1
+    assert L.egnn_node_act_required(nd(Hn=64)) == 1
+    assert L.egnn_node_act_required(nd(K2=136)) == 1
+    assert L.egnn_node_act_required(nd(K1=12)) == -_capi.EGNN_ERR_DIMS
+
+
 def test_flags_validated():
     L = _capi.lib()
     kw = dict(N=100, E=1000, F=128, FE=16, H=128, O=128, M=128, equivariant=1, mean_agg=0, dtype=1)

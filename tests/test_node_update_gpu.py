@@ -115,3 +115,53 @@ def test_dense_weight_gradient(dtype, tol, N, K, Nout, bias):
     print({k: f"{v:.1e}" for k, v in errs.items()}, flush=True)
     bad = {k: v for k, v in errs.items() if not v <= tol}
     assert not bad, bad
+
+
+@pytest.mark.parametrize("N,K2,residual,bias", [(70001, 128, True, True), (65541, 0, False, False)])
+def test_node_update_without_activation_buffer(N, K2, residual, bias):
+    # streaming sizes: egnn_node_act_required is 0, so act may be NULL; the forward then leaves it unwritten
+    # and the backward's [act | 1]^T dout reads SiLU of pre on load.  Every output must equal the run with
+    # the buffer, bit for bit; below the streaming rows a NULL act is refused.
+    from pymolecular_amd import _capi
+    from pymolecular_amd.node_update import _dims, _stream
+    L = _capi.lib()
+    x1, x2, w1, b1, w2, b2, gout = [None if t is None else t.to(torch.bfloat16).cuda()
+                                    for t in _case(N, 128, K2, 128, 128, 17 + N)]
+    if not bias:
+        b1 = b2 = None
+    d = _dims(x1, x2, w1, w2, residual)
+    assert L.egnn_node_act_required(d) == 0
+    p = lambda t: None if t is None else t.data_ptr()  # noqa: E731
+    st = _stream(x1.device)
+    runs = []
+    for with_act in (True, False):
+        pre = torch.full((N, 128), float("nan"), dtype=torch.bfloat16, device="cuda")
+        act = torch.full_like(pre, float("nan")) if with_act else None
+        out = torch.empty((N, 128), dtype=torch.bfloat16, device="cuda")
+        rc = L.egnn_node_fwd(d, x1.data_ptr(), x1.stride(0), p(x2), 0 if x2 is None else x2.stride(0), w1.data_ptr(),
+                             p(b1), w2.data_ptr(), p(b2), pre.data_ptr(), p(act), out.data_ptr(), out.stride(0), st)
+        assert rc == 0, _capi.lib().egnn_status_string(rc)
+        gx = torch.empty((N, 128 + K2), dtype=torch.bfloat16, device="cuda")
+        gw1, gw2 = torch.empty_like(w1), torch.empty_like(w2)
+        gb1 = torch.empty(128, dtype=torch.bfloat16, device="cuda") if bias else None
+        gb2 = torch.empty(128, dtype=torch.bfloat16, device="cuda") if bias else None
+        nb = L.egnn_node_bwd_workspace_bytes(d)
+        ws = torch.empty(nb, dtype=torch.uint8, device="cuda")
+        rc = L.egnn_node_bwd(d, x1.data_ptr(), x1.stride(0), p(x2), 0 if x2 is None else x2.stride(0), w1.data_ptr(),
+                             w2.data_ptr(), pre.data_ptr(), p(act), gout.data_ptr(), gout.stride(0), gx.data_ptr(),
+                             gw1.data_ptr(), p(gb1), gw2.data_ptr(), p(gb2), ws.data_ptr(), nb, st)
+        assert rc == 0, _capi.lib().egnn_status_string(rc)
+        torch.cuda.synchronize()
+        if with_act:   # the stored act is SiLU of pre's bf16 value, rounded to bf16
+            ref = torch.nn.functional.silu(pre.float()).to(torch.bfloat16)
+            assert (act.float() - ref.float()).abs().max().item() <= 2 ** -8 * ref.float().abs().max().item()
+        runs.append([t for t in (out, pre, gx, gw1, gb1, gw2, gb2) if t is not None])
+    for name, a, b in zip(["out", "pre", "grad_x", "gw1", "gb1", "gw2", "gb2"], *runs):
+        assert torch.equal(a, b), name
+    small = _dims(x1[:1000], None if x2 is None else x2[:1000], w1, w2, residual)
+    assert L.egnn_node_act_required(small) == 1
+    pre = torch.empty((1000, 128), dtype=torch.bfloat16, device="cuda")
+    out = torch.empty((1000, 128), dtype=torch.bfloat16, device="cuda")
+    rc = L.egnn_node_fwd(small, x1.data_ptr(), x1.stride(0), p(x2), 0 if x2 is None else x2.stride(0), w1.data_ptr(),
+                         p(b1), w2.data_ptr(), p(b2), pre.data_ptr(), None, out.data_ptr(), out.stride(0), st)
+    assert rc == _capi.EGNN_ERR_NULL
