@@ -256,6 +256,12 @@ int32_t egnn_node_bwd(const EgnnNodeDims* dims, const void* x1, int64_t ld1, con
  * Python wrapper pads other widths with zero columns), fp32 accumulation. */
 int32_t egnn_dense_fwd(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
                        const void* w, const void* b, void* y, int64_t ldy, void* stream);
+/* Input gradient of the same layer: dx (N, Kin, row stride lddx) = dy w, with
+ * dy (N, Nout, row stride lddy) and w (Nout, Kin) in nn.Linear layout read as
+ * it is (no transposed copy): torch.nn.Linear's grad_input.  Widths and row
+ * strides as for egnn_dense_fwd. */
+int32_t egnn_dense_dgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* dy, int64_t lddy,
+                         const void* w, void* dx, int64_t lddx, void* stream);
 size_t egnn_dense_wgrad_workspace_bytes(int64_t N, int32_t Kin, int32_t Nout);
 int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
                          const void* dy, int64_t lddy, void* grad_w, void* grad_b, void* workspace,

@@ -25,7 +25,7 @@ EXPORTED = (
     "egnn_schedule_build", "egnn_fwd_workspace_bytes", "egnn_bwd_workspace_bytes", "egnn_node_proj_bytes",
     "egnn_fwd", "egnn_fwd_static", "egnn_bwd",
     "egnn_node_bwd_workspace_bytes", "egnn_node_act_required", "egnn_node_fwd", "egnn_node_bwd",
-    "egnn_dense_fwd", "egnn_dense_wgrad_workspace_bytes", "egnn_dense_wgrad",
+    "egnn_dense_fwd", "egnn_dense_dgrad", "egnn_dense_wgrad_workspace_bytes", "egnn_dense_wgrad",
     "egnn_profile_enable", "egnn_profile_read",
     "egnn_graph_tmp_bytes", "egnn_knn_graph", "egnn_radius_graph",
 )
@@ -135,6 +135,8 @@ def lib() -> ctypes.CDLL:
     L.egnn_node_bwd.argtypes = [ND, P, c_int64, P, c_int64, P, P, P, P, P, c_int64, P, P, P, P, P, P, c_size_t, P]
     L.egnn_dense_fwd.restype = c_int32
     L.egnn_dense_fwd.argtypes = [c_int32, c_int64, c_int32, c_int32, P, c_int64, P, P, P, c_int64, P]
+    L.egnn_dense_dgrad.restype = c_int32
+    L.egnn_dense_dgrad.argtypes = [c_int32, c_int64, c_int32, c_int32, P, c_int64, P, P, c_int64, P]
     L.egnn_dense_wgrad_workspace_bytes.restype = c_size_t
     L.egnn_dense_wgrad_workspace_bytes.argtypes = [c_int64, c_int32, c_int32]
     L.egnn_dense_wgrad.restype = c_int32

@@ -684,6 +684,26 @@ int32_t egnn_dense_fwd(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, cons
   return hip_status(launch_gemm2(g, bf16, st));
 }
 
+int32_t egnn_dense_dgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* dy, int64_t lddy,
+                         const void* w, void* dx, int64_t lddx, void* stream) {
+  if (dtype != EGNN_F32 && dtype != EGNN_BF16) return EGNN_ERR_DIMS;
+  if (N < 0 || Kin <= 0 || Nout <= 0 || Kin % 8 || Nout % 8) return EGNN_ERR_DIMS;
+  if (N == 0) return EGNN_OK;
+  if (!dy || !w || !dx) return EGNN_ERR_NULL;
+  if (lddy < Nout || lddx < Kin || lddy % 8 || lddx % 8) return EGNN_ERR_STRIDE;
+  for (const void* p : std::initializer_list<const void*>{dy, w, dx})
+    if (!aligned16(p)) return EGNN_ERR_ALIGN;
+  const bool bf16 = dtype == EGNN_BF16;
+  Gemm2Args g{};
+  g.M = N; g.N = Kin; g.K = Nout;
+  g.A = dy; g.lda = lddy; g.a_bf16 = bf16; g.a_kc = 1; g.a_ones_row = -1;
+  g.B = w; g.ldb = Kin; g.b_bf16 = bf16; g.b_nc = 1;          // B[k][n] = w[k][n]
+  g.C = dx; g.ldc = lddx; g.c_bf16 = bf16;
+  hipStream_t st = (hipStream_t)stream;
+  ProfScope ps(EGNN_K_NODE_UPDATE, st);
+  return hip_status(launch_gemm2(g, bf16, st));
+}
+
 int32_t egnn_dense_wgrad(int32_t dtype, int64_t N, int32_t Kin, int32_t Nout, const void* x, int64_t ldx,
                          const void* dy, int64_t lddy, void* grad_w, void* grad_b, void* workspace,
                          size_t workspace_bytes, void* stream) {

@@ -191,24 +191,24 @@ class DenseFn(torch.autograd.Function):
         L = _capi.lib()
         code = _capi.EGNN_F32 if dt == torch.float32 else _capi.EGNN_BF16
         st = _stream(xp.device)
-        if ctx.needs_input_grad[0]:   # gx = gy w, the same product as the forward with w^T as the weight
+        if ctx.needs_input_grad[0]:   # gx = gy w, the padded weight read as it is
             gx = torch.empty((N, Kp), dtype=dt, device=xp.device)
             if N:
-                check("egnn_dense_fwd", L.egnn_dense_fwd(code, N, Np, Kp, gy2.data_ptr(), gy2.stride(0),
-                                                         wp.t().contiguous().data_ptr(), None, gx.data_ptr(),
-                                                         Kp, st))
+                check("egnn_dense_dgrad", L.egnn_dense_dgrad(code, N, Kp, Np, gy2.data_ptr(), gy2.stride(0),
+                                                             wp.data_ptr(), gx.data_ptr(), Kp, st))
             gx = gx[:, :Kin].reshape(*lead, Kin)
-        gw = torch.empty((Np, Kp), dtype=dt, device=xp.device)
-        gb = torch.empty((Np,), dtype=dt, device=xp.device) if ctx.has_b else None
-        nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kp, Np)
+        # the weight gradient at the layer's own widths (the padded columns of x and gy are not read),
+        # so it is stored in the parameter's shape
+        gw = torch.empty((Nout, Kin), dtype=dt, device=xp.device)
+        gb = torch.empty((Nout,), dtype=dt, device=xp.device) if ctx.has_b else None
+        nbytes = L.egnn_dense_wgrad_workspace_bytes(N, Kin, Nout)
         ws = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=xp.device)
-        rc = L.egnn_dense_wgrad(code, N, Kp, Np, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
+        rc = L.egnn_dense_wgrad(code, N, Kin, Nout, xp.data_ptr() if N else None, xp.stride(0) if N else Kp,
                                 gy2.data_ptr() if N else None, gy2.stride(0) if N else Np, gw.data_ptr(), _ptr(gb),
                                 ws.data_ptr(), nbytes, st)
         check("egnn_dense_wgrad", rc)
-        gw = gw if (Np, Kp) == (Nout, Kin) else gw[:Nout, :Kin]
         to = lambda t, d: t if t.dtype == d else t.to(d)  # noqa: E731
-        return gx, to(gw, ctx.wdt[0]), None if gb is None else to(gb[:Nout], ctx.wdt[1])
+        return gx, to(gw, ctx.wdt[0]), None if gb is None else to(gb, ctx.wdt[1])
 
 
 def dense(x: torch.Tensor, lin: torch.nn.Linear) -> torch.Tensor:
