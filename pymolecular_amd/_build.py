@@ -38,6 +38,7 @@ FLAGS = [
 # every product's result; the AGPR form would copy each one back)
 FILE_FLAGS = {
     "egnn_mpnn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "egnn_eqfwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

@@ -1275,7 +1275,8 @@ int64_t coop_fwd_ranges(const LayerShape& s, const FwdArgs& a) {
 
 int launch_coop_fwd(const LayerShape& s, const FwdArgs& a, hipStream_t st) {
   if (coop_fwd_ranges(s, a) > 0) return launch_mpnn_fwd_ep(a, s.probe, st);
-  if (s.H == 128) return s.eq ? launch_fwd_t<128, 128, 128, 8, true>(a, st) : launch_fwd_t<128, 128, 128, 8, false>(a, st);
+  if (s.H == 128 && s.eq) return launch_egnn_fwd_ep(a, st);
+  if (s.H == 128) return launch_fwd_t<128, 128, 128, 8, false>(a, st);
   return s.eq ? launch_fwd_t<64, 32, 32, 2, true>(a, st) : launch_fwd_t<64, 32, 32, 2, false>(a, st);
 }
 

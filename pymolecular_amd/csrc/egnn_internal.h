@@ -279,6 +279,9 @@ int launch_mpnn_bwd_ep(const BwdArgs& a, int nblk, bool identity, hipStream_t st
 // Edge-parallel MPNN forward (bf16, H = O = 128): the per-row sums as whole rows and carries, completed
 // by the fix-up launch; mpnn_ep_blocks: its (and the backward's) grid.  identity: as above.
 int launch_mpnn_fwd_ep(const FwdArgs& a, bool identity, hipStream_t st);
+// Edge-parallel forward of the equivariant layer (egnn_eqfwd.hip): bf16, H = O = M = 128, coop_supported
+// shapes; whole 32-edge tiles per wave, split rows' pieces in the carry slots for the fix-up.
+int launch_egnn_fwd_ep(const FwdArgs& a, hipStream_t st);
 int mpnn_ep_blocks(int64_t E);
 // Workgroup-cooperative kernels for H = O = M = 256 (bf16): weights streamed
 // from L2, backward writes the per-edge weight-gradient factors Dm1, Dm, Dgq, Dga2.
