@@ -186,6 +186,36 @@ def test_egnn_h128_edge_features_24(mean):
     check_case(Case(rowptr, col, 128, 24, 128, 128, 128, seed=83, eq=True, mean_agg=mean, edge_ids=perm), "bf16")
 
 
+def test_egnn_forward_many_tiles_per_wave():
+    """The edge-parallel EGNN forward (bf16, H = 128) with more 32-edge tiles than the 2048 waves it runs, so
+    each wave walks several tiles with the next tile's gathers and records in flight: skewed rows across
+    tiles, empty rows, edge ids permuting the F_E = 16 features, mean aggregation, and the coordinate
+    residual added to every row (whole rows stored by the kernel, split rows by the fix-up)."""
+    from pymolecular_amd import fused
+    r = np.random.Generator(np.random.PCG64(91))
+    degs = r.integers(0, 48, 7000)
+    degs[::97] = 300
+    degs[::13] = 0
+    rowptr_np, col_np = random_csr(len(degs), degs, seed=92)
+    E = len(col_np)
+    assert (E + 31) // 32 > 2 * 2048 and E % 32 != 0
+    perm = r.permutation(E)
+    case = Case(rowptr_np, col_np, 128, 16, 128, 128, 128, seed=93, eq=True, mean_agg=True, edge_ids=perm)
+    print(f"[egnn-fwd-tiles] N={case.N} E={E} tiles={(E + 31) // 32}", flush=True)
+    check_case(case, "bf16", backward=False)
+    dt = torch.bfloat16
+    h, coord, ef = _dev(case.h, dt), _dev(case.coord), _dev(case.ef, dt)
+    p = {k: _dev(v, dt) for k, v in case.p.items()}
+    fa = (h, coord, ef, _dev(case.rowptr), _dev(case.col), _dev(case.edge_ids), p["w1_msg"], p["w2_msg"],
+          p["w1_mov"], p["w2_mov"], p.get("b1"), p.get("b2"), p.get("bx1"))
+    kw = dict(mean_agg=True, equivariant=True)
+    msg0, mov0 = fused.egnn_fused_forward(*fa, **kw)
+    msg1, mov1 = fused.egnn_fused_forward(*fa, **kw, coord_residual=True)
+    torch.cuda.synchronize()
+    assert torch.equal(msg0, msg1)
+    assert torch.equal(mov1, coord + mov0)   # one fp32 add of the same operands
+
+
 @pytest.mark.parametrize("dims,eq,mean", [((32, 16, 64, 32, 32), True, False), ((128, 16, 128, 128, 128), True, True),
                                            ((128, 24, 128, 128, 128), False, False)])
 def test_fp32_edge_chunks(dims, eq, mean):
