@@ -186,6 +186,16 @@ def test_egnn_h128_edge_features_24(mean):
     check_case(Case(rowptr, col, 128, 24, 128, 128, 128, seed=83, eq=True, mean_agg=mean, edge_ids=perm), "bf16")
 
 
+@pytest.mark.parametrize("dtype", ["bf16", "fp32"])
+@pytest.mark.parametrize("mean", [False, True])
+def test_egnn_graph_smaller_than_a_tile(dtype, mean):
+    """Seven edges: one partial 32-edge tile, so one wave of the edge-parallel forward works and most of its
+    lanes hold edges past E (clamped loads, phi set to zero, outside every rank's span); empty rows too."""
+    rowptr, col = random_csr(6, np.array([0, 3, 1, 0, 3, 0]), seed=95)
+    assert len(col) == 7
+    check_case(Case(rowptr, col, 128, 16, 128, 128, 128, seed=96, eq=True, mean_agg=mean), dtype)
+
+
 def test_egnn_forward_many_tiles_per_wave():
     """The edge-parallel EGNN forward (bf16, H = 128) with more 32-edge tiles than the 2048 waves it runs, so
     each wave walks several tiles with the next tile's gathers and records in flight: skewed rows across
