@@ -197,8 +197,9 @@ def _closed_prefix(rowptr, col, n_edges):
 def cpu_sample(g, n_edges):
     """A deterministic subgraph with at least n_edges edges: (rows, cols, node ids, edge range, description).
 
-    Batched graphs: the smallest prefix of whole graphs.  One connected graph: the first rows holding
-    n_edges edges, with every source they read (relabelled; sources outside the prefix keep no edges)."""
+    Batched graphs: the smallest prefix of whole graphs.  One connected graph: the first r rows holding
+    n_edges edges, each source j read as node j mod r, so the sample has the graph's ratio of nodes to
+    edges (its node-side work per edge) and the same per-edge work."""
     r = _closed_prefix(g.rowptr, g.col, n_edges)
     if r and int(g.rowptr[r]) <= 2 * n_edges:
         e_end = int(g.rowptr[r])
@@ -207,10 +208,8 @@ def cpu_sample(g, n_edges):
     r = int(np.searchsorted(g.rowptr, n_edges, side="left"))
     e_end = int(g.rowptr[r])
     rows = np.repeat(np.arange(r), np.diff(g.rowptr[:r + 1]))
-    nodes = np.unique(np.concatenate([np.arange(r), g.col[:e_end]]))
-    cols = np.searchsorted(nodes, g.col[:e_end]).astype(np.int64)
-    return rows, cols, nodes, e_end, (f"first {r} destination rows and the {nodes.size} nodes they read "
-                                      f"(sources relabelled, none folded)")
+    cols = (g.col[:e_end].astype(np.int64) % r)
+    return rows, cols, np.arange(r), e_end, f"first {r} destination rows, source j read as node j mod {r}"
 
 
 def cpu_baseline(k, g, H, layers, eq, frac, min_edges, repeats, seed):
