@@ -174,10 +174,10 @@ def test_mpnn_forward_tile_ranges(fe, ndeg):
 
 @pytest.mark.parametrize("mean", [False, True])
 def test_egnn_h128_edge_features_24(mean):
-    """The cooperative EGNN kernels (bf16, H = 128) at F_E = 24: the forward's edge-input chunk of 24 features
-    plus r^2, and the backward's second 16-slot dW_e block, which also holds the r^2 slots.  Skewed rows that
-    cross many 64-edge tiles, empty rows, a partial last 64-edge tile (E % 64 != 0) and edge ids that permute
-    the feature rows."""
+    """The bf16 EGNN kernels at H = 128 (edge-parallel forward, cooperative backward) at F_E = 24: the forward's
+    edge-input chunk of 24 features plus r^2 in the fourth 8-slot group, and the backward's second 16-slot dW_e
+    block, which also holds the r^2 slots.  Skewed rows that cross many 32- and 64-edge tiles, empty rows, a
+    partial last 64-edge tile (E % 64 != 0) and edge ids that permute the feature rows."""
     degs = np.array([0, 300, 1, 2, 0, 129, 3, 31, 33, 0, 64, 127, 128, 5, 2, 2, 2, 0, 17] * 5 + [7])
     rowptr, col = random_csr(len(degs), degs, seed=81)
     assert len(col) % 64 != 0
@@ -298,7 +298,7 @@ def test_determinism_bitwise():
 
 
 @pytest.mark.parametrize("dtype,F,FE,H,O,M,eq", [
-    ("bf16", 128, 0, 128, 128, 128, True),     # cooperative kernels
+    ("bf16", 128, 0, 128, 128, 128, True),     # edge-parallel forward, cooperative backward
     ("bf16", 128, 16, 128, 128, 128, False),   # edge-parallel MPNN kernels
     ("bf16", 64, 8, 64, 32, 32, True),         # cooperative kernels, H = 64
     ("bf16", 256, 32, 256, 256, 256, True),    # wide kernels
@@ -353,7 +353,7 @@ def test_accumulate_grad_h(dtype, eq):
 @pytest.mark.parametrize("shape", [(0, 128, 128, 128), (16, 128, 128, 128), (32, 256, 256, 256), (8, 64, 32, 32)])
 def test_coord_residual(dtype, shape):
     # EGNN_FLAG_COORD_RESIDUAL: out_mov = coord + agg_x and grad_coord = grad_out_mov + the message
-    # path's gradient, on every forward path (cooperative, wide, one wave per tile), with mean
+    # path's gradient, on every forward path (edge-parallel, cooperative, wide, one wave per tile), with mean
     # aggregation, empty rows and rows across many tiles (rows the fix-up writes)
     from pymolecular_amd import fused
     FE, H, O, M = shape
